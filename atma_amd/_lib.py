@@ -1,0 +1,101 @@
+"""ctypes binding of libatma_hip.so (the C ABI declared in include/atma_hip.h).
+
+torch is imported first on purpose: the library's HIP runtime dependency
+(libamdhip64.so.7) then resolves to the copy torch already loaded, so device
+pointers and streams are shared with torch.
+"""
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (must precede loading the library; see module docstring)
+
+LIB_PATH = Path(__file__).resolve().parent / "libatma_hip.so"
+HEADER = Path(__file__).resolve().parent.parent / "include" / "atma_hip.h"
+
+ATMA_F32, ATMA_BF16, ATMA_F16 = 0, 1, 2
+DTYPE_CODE = {torch.float32: ATMA_F32, torch.bfloat16: ATMA_BF16, torch.float16: ATMA_F16}
+
+_p, _i64, _i32, _f32, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+
+# name -> (restype, argtypes); must match include/atma_hip.h
+SIGNATURES = {
+    "atma_abi_version": (_i32, []),
+    "atma_last_error": (ctypes.c_char_p, []),
+    "atma_store_kvcache": (_i32, [_p, _i64, _p, _i64, _p, _p, _p, _i64, _i64, _i64, _i32, _p]),
+    "atma_polar_attention_fwd": (_i32, [
+        _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
+        _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
+        _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i64, _f32, _p]),
+    "atma_polar_decode_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64]),
+    "atma_polar_attention_decode": (_i32, [
+        _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _i64, _p,
+        _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i64, _f32, _p, _sz, _p]),
+    "atma_gated_delta_decode_step": (_i32, [
+        _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _p, _p,
+        _i64, _i64, _i64, _i64, _i32, _f32, _p]),
+    "atma_chunk_gated_delta_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64]),
+    "atma_chunk_gated_delta_rule": (_i32, [
+        _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
+        _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _f32, _i32, _i64, _p, _sz, _p]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class HipLibraryMissing(RuntimeError):
+    """libatma_hip.so is not built (or failed to load)."""
+
+
+def load():
+    """Load (once) and return the ctypes handle; raise if the library is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise HipLibraryMissing(
+                    f"{LIB_PATH} is not built; run `python -m atma_amd._build` (hipcc, gfx950)")
+            try:
+                lib = ctypes.CDLL(str(LIB_PATH))
+            except OSError as e:
+                raise HipLibraryMissing(f"failed to load {LIB_PATH}: {e}") from e
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def available() -> bool:
+    try:
+        load()
+        return True
+    except HipLibraryMissing:
+        return False
+
+
+def check(rc: int, what: str):
+    if rc != 0:
+        msg = load().atma_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (code {rc}): {msg}")
+
+
+def ptr(t):
+    """Device address of a tensor (None -> NULL)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_handle(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def dtype_code(dtype) -> int:
+    try:
+        return DTYPE_CODE[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype} (float32, bfloat16, float16)") from None

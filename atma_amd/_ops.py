@@ -1,0 +1,179 @@
+"""torch.library custom ops ``atma_hip::*`` over the C ABI of libatma_hip.so.
+
+Each op launches on torch's current stream of the input's device, allocates its
+outputs / workspace through torch's caching allocator (so it is safe under
+CUDA-graph capture), and never synchronises the host.  Ops that write into
+caller-owned tensors declare them in ``mutates_args``.  There is no CPU
+implementation: a CPU tensor raises, and a missing library raises
+``HipLibraryMissing``.
+"""
+
+from typing import List, Optional
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+
+def _need_cuda(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("atma_hip ops run on the GPU only (got a CPU tensor); "
+                               "this build has no CPU fallback")
+
+
+def _rows16(t: Tensor) -> Tensor:
+    """Return t with unit innermost stride and 16-byte aligned rows/base."""
+    es = t.element_size()
+    ok = t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and all((s * es) % 16 == 0 for s in t.stride()[:-1])
+    return t if ok else t.contiguous()
+
+
+# --------------------------------------------------------------------------- Polar fwd
+@torch.library.custom_op("atma_hip::polar_attention_fwd", mutates_args=())
+def polar_attention_fwd_op(q: Tensor, k: Tensor, v: Tensor, n_keys: Tensor, v_null: Tensor,
+                           null_base: Tensor, null_slope_raw: Tensor, len_gain_raw: Tensor,
+                           mag_beta_raw: Tensor, eps: float, is_causal: bool,
+                           window: int) -> List[Tensor]:
+    _need_cuda(q, k, v, n_keys, v_null)
+    lib = _lib.load()
+    q, k, v = _rows16(q), _rows16(k), _rows16(v)
+    B, Hq, Tq, d = q.shape
+    Hkv, Tk = k.shape[1], k.shape[2]
+    c = torch.empty((B, Hq, Tq, d), device=q.device, dtype=q.dtype)
+    mag = torch.empty((B, Hq, Tq), device=q.device, dtype=q.dtype)
+    rc = lib.atma_polar_attention_fwd(
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
+        k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
+        n_keys.data_ptr(), v_null.data_ptr(), null_base.data_ptr(), null_slope_raw.data_ptr(),
+        len_gain_raw.data_ptr(), mag_beta_raw.data_ptr(), c.data_ptr(), mag.data_ptr(),
+        None, None, None, None, B, Hq, Hkv, Tq, Tk, d, _lib.dtype_code(q.dtype),
+        1 if is_causal else 0, window, eps, _lib.stream_handle(q.device))
+    _lib.check(rc, "polar_attention_fwd")
+    return [c, mag]
+
+
+@polar_attention_fwd_op.register_fake
+def _(q, k, v, n_keys, v_null, null_base, null_slope_raw, len_gain_raw, mag_beta_raw, eps,
+      is_causal, window):
+    B, Hq, Tq, d = q.shape
+    return [q.new_empty((B, Hq, Tq, d)), q.new_empty((B, Hq, Tq))]
+
+
+# --------------------------------------------------------------------------- Polar decode
+@torch.library.custom_op("atma_hip::polar_attention_decode", mutates_args=())
+def polar_attention_decode_op(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_tables: Tensor,
+                              context_lens: Tensor, v_null: Tensor, null_base: Tensor,
+                              null_slope_raw: Tensor, len_gain_raw: Tensor, mag_beta_raw: Tensor,
+                              eps: float, window: int) -> List[Tensor]:
+    _need_cuda(q, k_cache, v_cache, block_tables, context_lens)
+    lib = _lib.load()
+    q = _rows16(q)
+    if not k_cache.is_contiguous() or not v_cache.is_contiguous():
+        raise ValueError("k_cache / v_cache must be contiguous (num_pages, page_size, Hkv, d)")
+    B, Hq, d = q.shape
+    num_pages, page, Hkv, _ = k_cache.shape
+    max_pages = block_tables.shape[1]
+    c = torch.empty((B, Hq, d), device=q.device, dtype=q.dtype)
+    mag = torch.empty((B, Hq), device=q.device, dtype=q.dtype)
+    ws_bytes = lib.atma_polar_decode_workspace_bytes(B, Hq, max_pages, page, d)
+    ws = torch.empty((max(ws_bytes, 4) // 4,), device=q.device, dtype=torch.float32)
+    rc = lib.atma_polar_attention_decode(
+        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
+        num_pages, page, Hkv, block_tables.data_ptr(), block_tables.stride(0), max_pages,
+        context_lens.data_ptr(), v_null.data_ptr(), null_base.data_ptr(), null_slope_raw.data_ptr(),
+        len_gain_raw.data_ptr(), mag_beta_raw.data_ptr(), c.data_ptr(), mag.data_ptr(), B, Hq, d,
+        _lib.dtype_code(q.dtype), window, eps, ws.data_ptr(), ws.numel() * 4,
+        _lib.stream_handle(q.device))
+    _lib.check(rc, "polar_attention_decode")
+    return [c, mag]
+
+
+@polar_attention_decode_op.register_fake
+def _(q, k_cache, v_cache, block_tables, context_lens, v_null, null_base, null_slope_raw,
+      len_gain_raw, mag_beta_raw, eps, window):
+    B, Hq, d = q.shape
+    return [q.new_empty((B, Hq, d)), q.new_empty((B, Hq))]
+
+
+# --------------------------------------------------------------------------- gated delta step
+@torch.library.custom_op("atma_hip::gated_delta_decode_step", mutates_args=("state_table",))
+def gated_delta_decode_step_op(q: Tensor, k: Tensor, v: Tensor, gamma: Tensor, beta: Tensor,
+                               state_table: Tensor, slots: Tensor, eps: float) -> Tensor:
+    _need_cuda(q, k, v, gamma, beta, state_table, slots)
+    lib = _lib.load()
+    if not state_table.is_contiguous() or state_table.dtype != torch.float32:
+        raise ValueError("state_table must be a contiguous float32 (max_seqs, H, dk, dv) tensor")
+    q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+    B, H, dk = q.shape
+    dv = state_table.shape[3]
+    r = torch.empty((B, H, dv), device=q.device, dtype=torch.float32)
+    rc = lib.atma_gated_delta_decode_step(
+        q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
+        v.data_ptr(), v.stride(0), v.stride(1), gamma.data_ptr(), beta.data_ptr(),
+        state_table.data_ptr(), state_table.shape[0], slots.data_ptr(), r.data_ptr(), B, H, dk, dv,
+        _lib.dtype_code(q.dtype), eps, _lib.stream_handle(q.device))
+    _lib.check(rc, "gated_delta_decode_step")
+    return r
+
+
+@gated_delta_decode_step_op.register_fake
+def _(q, k, v, gamma, beta, state_table, slots, eps):
+    B, H, _ = q.shape
+    return q.new_empty((B, H, state_table.shape[3]), dtype=torch.float32)
+
+
+# --------------------------------------------------------------------------- chunked gated delta
+@torch.library.custom_op("atma_hip::chunk_gated_delta_rule", mutates_args=())
+def chunk_gated_delta_rule_op(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,
+                              initial_state: Optional[Tensor], scale: float, use_qk_l2norm: bool,
+                              want_final: bool) -> List[Tensor]:
+    _need_cuda(q, k, v, g, beta, initial_state)
+    lib = _lib.load()
+    q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
+    B, T, H, dk = q.shape
+    dv = v.shape[3]
+    o = torch.empty((B, T, H, dv), device=q.device, dtype=q.dtype)
+    final = torch.empty((B, H, dk, dv), device=q.device, dtype=torch.float32) if want_final else None
+    chunk = 64
+    ws_bytes = lib.atma_chunk_gated_delta_workspace_bytes(B, T, H, dk, dv, chunk)
+    ws = torch.empty((max(ws_bytes, 4) // 4,), device=q.device, dtype=torch.float32)
+    rc = lib.atma_chunk_gated_delta_rule(
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
+        k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
+        g.data_ptr(), beta.data_ptr(), _lib.ptr(initial_state), _lib.ptr(final), o.data_ptr(),
+        B, T, H, dk, dv, _lib.dtype_code(q.dtype), scale, 1 if use_qk_l2norm else 0, chunk,
+        ws.data_ptr(), ws.numel() * 4, _lib.stream_handle(q.device))
+    _lib.check(rc, "chunk_gated_delta_rule")
+    return [o, final] if want_final else [o]
+
+
+@chunk_gated_delta_rule_op.register_fake
+def _(q, k, v, g, beta, initial_state, scale, use_qk_l2norm, want_final):
+    B, T, H, dk = q.shape
+    dv = v.shape[3]
+    o = q.new_empty((B, T, H, dv))
+    return [o, q.new_empty((B, H, dk, dv), dtype=torch.float32)] if want_final else [o]
+
+
+# --------------------------------------------------------------------------- paged KV write
+@torch.library.custom_op("atma_hip::store_kvcache", mutates_args=("k_cache", "v_cache"))
+def store_kvcache_op(key: Tensor, value: Tensor, k_cache: Tensor, v_cache: Tensor,
+                     slot_mapping: Tensor) -> None:
+    _need_cuda(key, value, k_cache, v_cache, slot_mapping)
+    lib = _lib.load()
+    N, hkv, d = key.shape
+    row = hkv * d
+    rc = lib.atma_store_kvcache(
+        key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0), k_cache.data_ptr(),
+        v_cache.data_ptr(), slot_mapping.data_ptr(), N, row, k_cache.numel() // row,
+        _lib.dtype_code(key.dtype), _lib.stream_handle(key.device))
+    _lib.check(rc, "store_kvcache")
+
+
+@store_kvcache_op.register_fake
+def _(key, value, k_cache, v_cache, slot_mapping):
+    return None

@@ -1,0 +1,80 @@
+// Shared device/host helpers for libatma_hip.so (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "atma_hip.h"
+
+namespace atma {
+
+using bf16 = __bf16;
+using f16 = _Float16;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+// Masked logits use this finite sentinel (never -inf * temp) and contribute p = 0.
+constexpr float kSentinel = -1e38f;
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+__device__ __forceinline__ float to_f32(f16 x) { return (float)x; }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x) { return (T)x; }
+
+// softplus with torch's default threshold (x > 20 -> x).
+__device__ __forceinline__ float softplus(float x) {
+  return x > 20.f ? x : log1pf(expf(x));
+}
+
+// 16-byte vector of 8 two-byte elements, reinterpretable for MFMA operands.
+union Pack8 {
+  u32x4 u;
+  bf16x8 b;
+  f16x8 h;
+};
+
+// Wave-local barrier: orders LDS traffic between lanes of one wavefront.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_xor(T x, int mask) {
+  return __shfl_xor(x, mask, 64);
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+  return x;
+}
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m, 64));
+  return x;
+}
+__device__ __forceinline__ float wave_min(float x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x = fminf(x, __shfl_xor(x, m, 64));
+  return x;
+}
+
+// ---------------------------------------------------------------- host side
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+int dtype_size(int dtype);
+
+}  // namespace atma

@@ -1,0 +1,508 @@
+// Polar attention forward (prefill): flash-style, MFMA, one pass over the keys.
+//
+// Reference: _polar_fwd_kernel / _polar_forward / polar_attention_fwd,
+// kernel/polar_triton.py:49-191,505-609 (math: model/blocks.py:171-250).  Per query
+// the kernel streams key blocks keeping (m, l = sum p, q2 = sum p^2, acc = sum p v),
+// folds the null sink once at the end and emits the unit direction c and the
+// bounded magnitude mag = tanh(beta*log1p(L^3/(Q2*Z))).
+//
+// MI355X design (gfx950, wave64, MFMA 32x32):
+//  * A workgroup owns 128 query rows of one query head (4 waves x 32 rows).  The
+//    query tile stays in registers as the MFMA B operand for the whole key loop.
+//  * Each wave computes S^T = K Q^T (rows = keys, columns = its 32 queries) and
+//    O^T = V^T P^T (rows = head dims, columns = queries).  With queries on the
+//    MFMA column axis every per-query quantity (temperature, running max, L, Q2,
+//    the output row) lives in one lane pair (l, l^32): the softmax needs a single
+//    cross-lane exchange per 64-key block and no shuffles of the accumulator.
+//  * K rows are loaded into the S^T A operand in a permuted order so that the
+//    S^T accumulator registers ARE the P^T B operand of the next MFMA: no LDS
+//    round trip for P.
+//  * K and V tiles (64 keys) are staged in LDS once per workgroup; V is stored
+//    transposed ([d][key]) because the PV MFMA contracts over keys.  The next
+//    tile is prefetched into registers while the current one is consumed.
+//  * GQA is resolved in-kernel (kv head = q head / group), and the grid is
+//    ordered so the workgroups of one KV group and neighbouring query tiles land
+//    on the same XCD (shared L2), longest causal tiles first.
+//  * bf16/fp16 use v_mfma_f32_32x32x16_{bf16,f16}; fp32 inputs use
+//    v_mfma_f32_32x32x2f32 (full fp32 products: the 1e-4 mode).
+#include "common.h"
+
+namespace atma {
+
+struct PolarFwdArgs {
+  const void* q;
+  int64_t q_sb, q_sh, q_st;
+  const void* k;
+  int64_t k_sb, k_sh, k_st;
+  const void* v;
+  int64_t v_sb, v_sh, v_st;
+  const float* n_keys;
+  const float* v_null;
+  const float* null_base;
+  const float* null_slope_raw;
+  const float* len_gain_raw;
+  const float* mag_beta_raw;
+  void* c;
+  void* mag;
+  float* stat_m;
+  float* stat_l;
+  float* stat_q2;
+  float* stat_s;
+  int B, Hq, Hkv, Tq, Tk;
+  int is_causal;
+  int window;
+  float eps;
+  int n_qtiles;
+  int xcd_remap;
+};
+
+template <typename T, int D>
+struct FwdCfg {
+  static constexpr bool kHalf = sizeof(T) == 2;
+  static constexpr int BM = 128;                 // query rows per workgroup
+  static constexpr int BN = 64;                  // keys per block
+  static constexpr int VE = 16 / (int)sizeof(T); // elements per 16-byte chunk
+  static constexpr int CPR = D / VE;             // chunks per row
+  static constexpr int KP = D + VE;              // K tile pitch (elements)
+  static constexpr int VP = BN + VE;             // V^T tile pitch (elements)
+  static constexpr int KCH = BN * CPR / 256;     // K chunks per thread
+  static constexpr int VGROUPS = (BN / 4) * CPR; // (4 keys x 1 chunk) groups
+  static constexpr int VG_PT = (VGROUPS + 255) / 256;
+  static constexpr int NT = D / 32;              // O^T tiles (32 dims each)
+  static constexpr int QSTEPS = kHalf ? D / 16 : D / 2;
+};
+
+// Key held by S^T register i (0..15) of 32-key tile j for lane half h.
+__device__ __forceinline__ int st_key(int j, int i, int h) {
+  return 32 * j + 16 * (i >> 3) + 8 * h + (i & 7);
+}
+// Key loaded into S^T A-operand row r (0..31) -- the inverse view of st_key.
+__device__ __forceinline__ int a_row_key(int r) {
+  const int a = r >> 3, hh = (r >> 2) & 1, b = r & 3;
+  return 16 * (a >> 1) + 8 * hh + 4 * (a & 1) + b;
+}
+
+template <typename T>
+__device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f32x16& c) {
+  Pack8 pa, pb;
+  pa.u = a;
+  pb.u = b;
+  if constexpr (__is_same(T, bf16)) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(pa.b, pb.b, c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(pa.h, pb.h, c, 0, 0, 0);
+  }
+}
+
+// Two floats -> one dword of two 16-bit values (element 0 in the low half).
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float x, float y) {
+  T a = (T)x, b = (T)y;
+  uint16_t ua = __builtin_bit_cast(uint16_t, a), ub = __builtin_bit_cast(uint16_t, b);
+  return (uint32_t)ua | ((uint32_t)ub << 16);
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256, 1) polar_fwd_kernel(PolarFwdArgs args) {
+  using Cfg = FwdCfg<T, D>;
+  constexpr int BM = Cfg::BM, BN = Cfg::BN, VE = Cfg::VE, CPR = Cfg::CPR;
+  constexpr int KP = Cfg::KP, VP = Cfg::VP, NT = Cfg::NT;
+  __shared__ __attribute__((aligned(16))) T Ks[BN * KP];
+  __shared__ __attribute__((aligned(16))) T Vt[D * VP];
+  __shared__ float s_bounds[4][2];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int ql = lane & 31, h = lane >> 5;
+
+  // ---- workgroup -> (b, q head, query tile), XCD-aware, longest tile first
+  const int G = args.Hq / args.Hkv;
+  int bid = blockIdx.x;
+  if (args.xcd_remap) {
+    const int x = bid & 7, p = bid >> 3;
+    bid = (x + 8 * (p / G)) * G + p % G;
+  }
+  const int g = bid % G;
+  const int unit = bid / G;
+  const int qt = args.n_qtiles - 1 - unit % args.n_qtiles;
+  const int grp = unit / args.n_qtiles;  // b * Hkv + kv head
+  const int b = grp / args.Hkv, hk = grp % args.Hkv;
+  const int hq = hk * G + g;
+  const int q0 = qt * BM;
+
+  const T* qp = (const T*)args.q + b * args.q_sb + hq * args.q_sh;
+  const T* kp = (const T*)args.k + b * args.k_sb + hk * args.k_sh;
+  const T* vp = (const T*)args.v + b * args.v_sb + hk * args.v_sh;
+
+  // ---- per-query calibration (lane pair owns query row qi)
+  const int qi = q0 + wave * 32 + ql;
+  const bool q_ok = qi < args.Tq;
+  const float n_raw = q_ok ? args.n_keys[qi] : 0.f;
+  float n_cal = n_raw;
+  if (args.window > 0) n_cal = fminf(n_cal, (float)args.window);
+  n_cal = fmaxf(n_cal, 1.f);
+  const float spg = softplus(args.len_gain_raw[hq]);
+  const float sps = softplus(args.null_slope_raw[hq]);
+  const float nb = args.null_base[hq];
+  const float mbeta = softplus(args.mag_beta_raw[hq]);
+  const float temp = 1.f + spg * logf(n_cal);
+  const float nullv = nb + sps * sqrtf(logf(n_cal + 1.f));
+  const float c1 = temp * kLog2e * (1.f / sqrtf((float)D));
+
+  // ---- key-loop bounds from the valid counts of this tile (raw n, window band)
+  {
+    float lo = q_ok ? n_raw : 3.0e38f, hi = q_ok ? n_raw : -1.f;
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    if (lane == 0) {
+      s_bounds[wave][0] = lo;
+      s_bounds[wave][1] = hi;
+    }
+  }
+  __syncthreads();
+  const float w_nlo = s_bounds[wave][0], w_nhi = s_bounds[wave][1];
+  float g_nlo = s_bounds[0][0], g_nhi = s_bounds[0][1];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) {
+    g_nlo = fminf(g_nlo, s_bounds[w][0]);
+    g_nhi = fmaxf(g_nhi, s_bounds[w][1]);
+  }
+  int kend = 0, kbeg = 0;
+  if (g_nhi > 0.f) {
+    float hiF = fminf(g_nhi, (float)args.Tk);
+    kend = (int)ceilf(hiF);
+    if (args.is_causal) kend = min(kend, min(q0 + BM, args.Tk));
+    if (args.window > 0) kbeg = max((int)floorf(g_nlo) - args.window, 0);
+    kbeg = (kbeg / BN) * BN;
+  }
+  const int nblk_beg = kbeg / BN, nblk_end = (kend + BN - 1) / BN;
+
+  // ---- query operand (B of S^T) in registers
+  u32x4 qreg16[Cfg::kHalf ? Cfg::QSTEPS : 1];
+  float qregf[Cfg::kHalf ? 1 : Cfg::QSTEPS];
+  if constexpr (Cfg::kHalf) {
+#pragma unroll
+    for (int s = 0; s < Cfg::QSTEPS; ++s) {
+      qreg16[s] = q_ok ? *(const u32x4*)(qp + (int64_t)qi * args.q_st + 16 * s + 8 * h)
+                       : u32x4{0, 0, 0, 0};
+    }
+  } else {
+#pragma unroll
+    for (int s4 = 0; s4 < Cfg::QSTEPS / 4; ++s4) {
+      f32x4 x = q_ok ? *(const f32x4*)(qp + (int64_t)qi * args.q_st + (D / 2) * h + 4 * s4)
+                     : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) qregf[4 * s4 + e] = x[e];
+    }
+  }
+
+  // ---- running statistics (log2 domain) and O^T accumulators
+  float m_run = kSentinel, l_part = 0.f, q2_part = 0.f;
+  f32x16 oacc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) oacc[t] = f32x16{};
+
+  // ---- global -> register prefetch of one K/V block
+  u32x4 kpre[Cfg::KCH];
+  u32x4 vpre[Cfg::VG_PT][4];
+  auto prefetch = [&](int blk) {
+    const int k0 = blk * BN;
+#pragma unroll
+    for (int r = 0; r < Cfg::KCH; ++r) {
+      const int cidx = tid + 256 * r;
+      const int key = k0 + cidx / CPR, ch = cidx % CPR;
+      kpre[r] = key < args.Tk ? *(const u32x4*)(kp + (int64_t)key * args.k_st + ch * VE)
+                              : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int gi = 0; gi < Cfg::VG_PT; ++gi) {
+      const int grpi = tid + 256 * gi;
+      if (grpi < Cfg::VGROUPS) {
+        const int ch = grpi % CPR, kg = grpi / CPR;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int key = k0 + 4 * kg + r;
+          vpre[gi][r] = key < args.Tk ? *(const u32x4*)(vp + (int64_t)key * args.v_st + ch * VE)
+                                      : u32x4{0, 0, 0, 0};
+        }
+      }
+    }
+  };
+  auto commit = [&]() {
+#pragma unroll
+    for (int r = 0; r < Cfg::KCH; ++r) {
+      const int cidx = tid + 256 * r;
+      const int key = cidx / CPR, ch = cidx % CPR;
+      *(u32x4*)(Ks + key * KP + ch * VE) = kpre[r];
+    }
+#pragma unroll
+    for (int gi = 0; gi < Cfg::VG_PT; ++gi) {
+      const int grpi = tid + 256 * gi;
+      if (grpi < Cfg::VGROUPS) {
+        const int ch = grpi % CPR, kg = grpi / CPR;
+        if constexpr (Cfg::kHalf) {
+          // 4 keys x 8 dims -> 8 rows of V^T, 4 keys (8 bytes) each
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int w = e >> 1, sh = (e & 1) * 16;
+            uint32_t x0 = (vpre[gi][0][w] >> sh) & 0xffffu, x1 = (vpre[gi][1][w] >> sh) & 0xffffu;
+            uint32_t x2 = (vpre[gi][2][w] >> sh) & 0xffffu, x3 = (vpre[gi][3][w] >> sh) & 0xffffu;
+            u32x2 pk = {x0 | (x1 << 16), x2 | (x3 << 16)};
+            *(u32x2*)(Vt + (ch * 8 + e) * VP + 4 * kg) = pk;
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            u32x4 pk = {vpre[gi][0][e], vpre[gi][1][e], vpre[gi][2][e], vpre[gi][3][e]};
+            *(u32x4*)(Vt + (ch * 4 + e) * VP + 4 * kg) = pk;
+          }
+        }
+      }
+    }
+  };
+
+  if (nblk_beg < nblk_end) prefetch(nblk_beg);
+  const int arow = a_row_key(ql);
+
+  for (int blk = nblk_beg; blk < nblk_end; ++blk) {
+    const int k0 = blk * BN;
+    commit();
+    __syncthreads();
+    if (blk + 1 < nblk_end) prefetch(blk + 1);
+
+    // ---- S^T = K Q^T  (two 32-key tiles)
+    f32x16 sacc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      sacc[j] = f32x16{};
+      const T* krow = Ks + (32 * j + arow) * KP;
+      if constexpr (Cfg::kHalf) {
+#pragma unroll
+        for (int s = 0; s < Cfg::QSTEPS; ++s) {
+          u32x4 a = *(const u32x4*)(krow + 16 * s + 8 * h);
+          sacc[j] = mfma32<T>(a, qreg16[s], sacc[j]);
+        }
+      } else {
+#pragma unroll
+        for (int s4 = 0; s4 < Cfg::QSTEPS / 4; ++s4) {
+          f32x4 a = *(const f32x4*)(krow + (D / 2) * h + 4 * s4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            sacc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], qregf[4 * s4 + e], sacc[j], 0, 0, 0);
+        }
+      }
+    }
+
+    // ---- online softmax with the extra sum of p^2
+    const bool full = (k0 + BN <= (int)fminf(w_nlo, (float)args.Tk)) &&
+                      (args.window <= 0 || (float)k0 >= w_nhi - (float)args.window);
+    float mx = kSentinel;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float a = sacc[j][i] * c1;
+        if (!full) {
+          const int key = k0 + st_key(j, i, h);
+          bool ok = (float)key < n_raw && key < args.Tk;
+          if (args.window > 0) ok = ok && (float)key >= n_raw - (float)args.window;
+          a = ok ? a : kSentinel;
+        }
+        sacc[j][i] = a;
+        mx = fmaxf(mx, a);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = exp2f(m_run - m_new);
+    m_run = m_new;
+    float ls = 0.f, qs = 0.f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float a = sacc[j][i];
+        float p = exp2f(a - m_new);
+        if (!full) p = a == kSentinel ? 0.f : p;
+        sacc[j][i] = p;
+        ls += p;
+        qs += p * p;
+      }
+    }
+    l_part = l_part * alpha + ls;
+    q2_part = q2_part * alpha * alpha + qs;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) oacc[t] *= alpha;
+
+    // ---- O^T += V^T P^T
+    if constexpr (Cfg::kHalf) {
+      u32x4 pb[4];
+#pragma unroll
+      for (int ps = 0; ps < 4; ++ps) {
+        const int j = ps >> 1, base = 8 * (ps & 1);
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+          pb[ps][w] = pack2<T>(sacc[j][base + 2 * w], sacc[j][base + 2 * w + 1]);
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const T* vrow = Vt + (32 * t + ql) * VP + 8 * h;
+#pragma unroll
+        for (int ps = 0; ps < 4; ++ps) {
+          u32x4 a = *(const u32x4*)(vrow + 16 * ps);
+          oacc[t] = mfma32<T>(a, pb[ps], oacc[t]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const T* vrow = Vt + (32 * t + ql) * VP + 8 * h;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+              f32x4 a = *(const f32x4*)(vrow + 32 * j + 16 * u + 4 * w);
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                oacc[t] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[e], sacc[j][8 * u + 4 * w + e],
+                                                              oacc[t], 0, 0, 0);
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- fold the null sink, normalise, magnitude
+  float L = l_part + __shfl_xor(l_part, 32, 64);
+  float Q2 = q2_part + __shfl_xor(q2_part, 32, 64);
+  const float an2 = temp * nullv * kLog2e;
+  const float mn = fmaxf(m_run, an2);
+  const float al = exp2f(m_run - mn);
+  L *= al;
+  Q2 *= al * al;
+  const float pn = exp2f(an2 - mn);
+  const float Z = L + pn;
+  const float* vn = args.v_null + (int64_t)hq * D;
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int d = 32 * t + 8 * (i >> 2) + 4 * h + (i & 3);
+      const float s = oacc[t][i] * al + pn * vn[d];
+      oacc[t][i] = s;
+      ss += s * s;
+    }
+  }
+  ss += __shfl_xor(ss, 32, 64);
+  const float inv = 1.f / fmaxf(sqrtf(ss), args.eps);
+  const float n_eff = L * L / fmaxf(Q2, 1e-30f);
+  const float m_eff = n_eff * (L / fmaxf(Z, args.eps));
+  const float magv = tanhf(mbeta * log1pf(m_eff));
+
+  if (q_ok) {
+    const int64_t row = ((int64_t)b * args.Hq + hq) * args.Tq + qi;
+    T* cp = (T*)args.c + row * D;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int d = 32 * t + 8 * gq + 4 * h;
+        if constexpr (Cfg::kHalf) {
+          u32x2 pk = {pack2<T>(oacc[t][4 * gq] * inv, oacc[t][4 * gq + 1] * inv),
+                      pack2<T>(oacc[t][4 * gq + 2] * inv, oacc[t][4 * gq + 3] * inv)};
+          *(u32x2*)(cp + d) = pk;
+        } else {
+          f32x4 x = {oacc[t][4 * gq] * inv, oacc[t][4 * gq + 1] * inv, oacc[t][4 * gq + 2] * inv,
+                     oacc[t][4 * gq + 3] * inv};
+          *(f32x4*)(cp + d) = x;
+        }
+      }
+    }
+    if (h == 0) {
+      ((T*)args.mag)[row] = (T)magv;
+      if (args.stat_m) args.stat_m[row] = mn * kLn2;
+      if (args.stat_l) args.stat_l[row] = L;
+      if (args.stat_q2) args.stat_q2[row] = Q2;
+    }
+    if (args.stat_s) {
+      float* sp = args.stat_s + row * D;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const int d = 32 * t + 8 * gq + 4 * h;
+          f32x4 x = {oacc[t][4 * gq], oacc[t][4 * gq + 1], oacc[t][4 * gq + 2], oacc[t][4 * gq + 3]};
+          *(f32x4*)(sp + d) = x;
+        }
+    }
+  }
+}
+
+template <typename T, int D>
+static int launch_fwd(PolarFwdArgs a, hipStream_t stream) {
+  const int64_t units = (int64_t)a.n_qtiles * a.B * a.Hq;
+  const int G = a.Hq / a.Hkv;
+  a.xcd_remap = (units % (8 * G) == 0) ? 1 : 0;
+  polar_fwd_kernel<T, D><<<dim3((unsigned)units), dim3(256), 0, stream>>>(a);
+  return check_launch("polar_attention_fwd");
+}
+
+}  // namespace atma
+
+extern "C" int atma_polar_attention_fwd(
+    const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb,
+    int64_t k_sh, int64_t k_st, const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+    const float* n_keys, const float* v_null, const float* null_base, const float* null_slope_raw,
+    const float* len_gain_raw, const float* mag_beta_raw, void* c, void* mag, float* stat_m,
+    float* stat_l, float* stat_q2, float* stat_s, int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq,
+    int64_t Tk, int64_t d, int dtype, int is_causal, int64_t window, float eps, void* stream) {
+  using namespace atma;
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || Tq < 0 || Tk < 0)
+    return set_error(ATMA_ERR_INVALID, "polar_attention_fwd: bad sizes");
+  if (Hq % Hkv) return set_error(ATMA_ERR_INVALID, "polar_attention_fwd: Hq %% Hkv != 0");
+  if (is_causal && Tq != Tk)
+    return set_error(ATMA_ERR_INVALID,
+                     "polar_attention_fwd: is_causal=True requires Tq == Tk (got Tq=%lld, Tk=%lld)",
+                     (long long)Tq, (long long)Tk);
+  if (d != 64 && d != 128)
+    return set_error(ATMA_ERR_UNSUPPORTED, "polar_attention_fwd: head_dim %lld (supported: 64, 128)",
+                     (long long)d);
+  if (Tq > (1 << 30) || Tk > (1 << 30) || B * Hq > (1 << 24))
+    return set_error(ATMA_ERR_INVALID, "polar_attention_fwd: sizes too large");
+  if (B == 0 || Tq == 0) return ATMA_OK;
+  if (!q || !k || !v || !n_keys || !v_null || !null_base || !null_slope_raw || !len_gain_raw ||
+      !mag_beta_raw || !c || !mag)
+    return set_error(ATMA_ERR_INVALID, "polar_attention_fwd: null pointer");
+  const int es = dtype_size(dtype);
+  if (!es) return set_error(ATMA_ERR_INVALID, "polar_attention_fwd: unknown dtype %d", dtype);
+  auto al16 = [&](const void* p, int64_t s1, int64_t s2, int64_t s3) {
+    return ((uintptr_t)p % 16 == 0) && ((s1 * es) % 16 == 0) && ((s2 * es) % 16 == 0) &&
+           ((s3 * es) % 16 == 0);
+  };
+  if (!al16(q, q_sb, q_sh, q_st) || !al16(k, k_sb, k_sh, k_st) || !al16(v, v_sb, v_sh, v_st) ||
+      (uintptr_t)c % 16)
+    return set_error(ATMA_ERR_INVALID, "polar_attention_fwd: tensors must be 16-byte aligned rows");
+  PolarFwdArgs a{};
+  a.q = q; a.q_sb = q_sb; a.q_sh = q_sh; a.q_st = q_st;
+  a.k = k; a.k_sb = k_sb; a.k_sh = k_sh; a.k_st = k_st;
+  a.v = v; a.v_sb = v_sb; a.v_sh = v_sh; a.v_st = v_st;
+  a.n_keys = n_keys; a.v_null = v_null; a.null_base = null_base;
+  a.null_slope_raw = null_slope_raw; a.len_gain_raw = len_gain_raw; a.mag_beta_raw = mag_beta_raw;
+  a.c = c; a.mag = mag; a.stat_m = stat_m; a.stat_l = stat_l; a.stat_q2 = stat_q2; a.stat_s = stat_s;
+  a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.Tq = (int)Tq; a.Tk = (int)Tk;
+  a.is_causal = is_causal ? 1 : 0;
+  a.window = window > 0 ? (int)window : 0;
+  a.eps = eps;
+  a.n_qtiles = (int)((Tq + 127) / 128);
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case ATMA_BF16: return d == 128 ? launch_fwd<bf16, 128>(a, s) : launch_fwd<bf16, 64>(a, s);
+    case ATMA_F16: return d == 128 ? launch_fwd<f16, 128>(a, s) : launch_fwd<f16, 64>(a, s);
+    default: return d == 128 ? launch_fwd<float, 128>(a, s) : launch_fwd<float, 64>(a, s);
+  }
+}

@@ -1,0 +1,23 @@
+"""Hot-path ops of ATMA's global-layer mixer under the reference's names
+(``kernel/__init__.py:15-28`` of the reference), backed by libatma_hip.so.
+
+``HAS_HIP`` mirrors the reference's ``HAS_TRITON``: True when the library is
+built and a GPU is visible.  The functions are always importable; calling one
+without the library or on CPU tensors raises (there is no silent fallback).
+"""
+
+import torch
+
+from .. import _lib
+from .gated_delta import chunk_gated_delta_rule, gated_delta_decode_step
+from .polar import polar_attention_decode, polar_attention_fwd
+
+HAS_HIP = _lib.available() and torch.cuda.is_available()
+
+__all__ = [
+    "HAS_HIP",
+    "polar_attention_fwd",
+    "polar_attention_decode",
+    "gated_delta_decode_step",
+    "chunk_gated_delta_rule",
+]

@@ -1,0 +1,83 @@
+"""Gated-delta memory ops backed by libatma_hip.so.
+
+* ``gated_delta_decode_step`` mirrors ``kernel/gated_delta_triton.py:78-117``.
+* ``chunk_gated_delta_rule`` replaces the third-party
+  ``fla.ops.gated_delta_rule.chunk_gated_delta_rule`` with the contract the
+  reference uses (``model/blocks.py:44-49``, ``inference/models/atma.py:285-287``).
+
+Convention (``scripts/titans_proto.py:53-66``): decay first, predict on the decayed
+state, undecayed write, self-inclusive readout ``r_t = M_t q_t``; states are fp32
+in the ``[K, V]`` = (dk, dv) layout.
+"""
+
+import torch
+
+from .. import _ops  # noqa: F401  (registers torch.ops.atma_hip.*)
+
+
+@torch.no_grad()
+def gated_delta_decode_step(q, k, v, gamma, beta, state_table, slots, eps=1e-12, block_v=None):
+    """One batched gated-delta step, IN PLACE on the slot-indexed state table.
+
+    q, k, v: (B, H, d) current-token tensors (KV heads expanded to H).
+    gamma, beta: (B, H) retention / write strength.  state_table: (max_seqs, H, dk, dv)
+    fp32 ``[K, V]``, updated in place.  slots: (B,) int64 rows of the table.
+    ``block_v`` (a Triton tile knob) is accepted and ignored.
+    Returns r (B, H, dv) fp32.  Graph capturable."""
+    if q.dim() != 3 or q.shape != k.shape or q.shape[:2] != v.shape[:2]:
+        raise ValueError("q, k, v must be (B, H, d) with matching shapes")
+    B, H, dk = q.shape
+    if state_table.dim() != 4 or state_table.shape[1] != H or state_table.shape[2] != dk:
+        raise ValueError(f"state_table {tuple(state_table.shape)} incompatible with q {tuple(q.shape)}")
+    if v.shape[2] != state_table.shape[3]:
+        raise ValueError("v's last dim must equal the state's dv")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k, v must share a dtype")
+    gamma = gamma.to(torch.float32).reshape(B, H).contiguous()
+    beta = beta.to(torch.float32).reshape(B, H).contiguous()
+    slots = slots.to(device=q.device, dtype=torch.int64).reshape(B).contiguous()
+    return torch.ops.atma_hip.gated_delta_decode_step(q, k, v, gamma, beta, state_table, slots,
+                                                      float(eps))
+
+
+@torch.no_grad()
+def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
+                           output_final_state=False, use_qk_l2norm_in_kernel=False,
+                           cu_seqlens=None, head_first=False):
+    """Chunked gated-delta prefill with state carry (FLA contract).
+
+    q, k: (B, T, H, dk); v: (B, T, H, dv); g: (B, T, H) log-decay (log gamma);
+    beta: (B, T, H); initial_state: (B, H, dk, dv) fp32 or None.  With
+    ``use_qk_l2norm_in_kernel`` q and k are L2-normalised (x / max(|x|, 1e-12)) before
+    the recurrence; q is then scaled by ``scale`` (default dk**-0.5, FLA's default;
+    the reference passes 1.0).
+    Returns (o (B, T, H, dv) in q's dtype, final_state (B, H, dk, dv) fp32 or None)."""
+    if cu_seqlens is not None or head_first:
+        raise NotImplementedError("cu_seqlens / head_first layouts are not supported")
+    if q.dim() != 4 or k.shape != q.shape or v.shape[:3] != q.shape[:3]:
+        raise ValueError("q, k: (B, T, H, dk) and v: (B, T, H, dv) required")
+    B, T, H, dk = q.shape
+    dv = v.shape[3]
+    if g.shape != (B, T, H) or beta.shape != (B, T, H):
+        raise ValueError("g and beta must be (B, T, H)")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k, v must share a dtype")
+    if initial_state is not None:
+        if initial_state.shape != (B, H, dk, dv):
+            raise ValueError(f"initial_state must be (B, H, dk, dv) = {(B, H, dk, dv)}")
+        initial_state = initial_state.to(torch.float32).contiguous()
+    if scale is None:
+        scale = dk ** -0.5
+    if T == 0:
+        o = q.new_empty((B, 0, H, dv))
+        if not output_final_state:
+            return o, None
+        final = (initial_state.clone() if initial_state is not None
+                 else torch.zeros((B, H, dk, dv), device=q.device, dtype=torch.float32))
+        return o, final
+    g = g.to(torch.float32).contiguous()
+    beta = beta.to(torch.float32).contiguous()
+    outs = torch.ops.atma_hip.chunk_gated_delta_rule(q, k, v, g, beta, initial_state, float(scale),
+                                                     bool(use_qk_l2norm_in_kernel),
+                                                     bool(output_final_state))
+    return outs[0], (outs[1] if output_final_state else None)

@@ -1,0 +1,99 @@
+"""Polar attention ops with the reference's ``kernel/polar_triton.py`` signatures,
+backed by the HIP kernels of libatma_hip.so (``atma_hip::polar_attention_*``).
+
+Polar attention (reference docstring ``kernel/polar_triton.py:10-21``): one
+temperature-sharpened softmax over the causal keys plus a null-sink logit gives a
+unit direction ``c`` and a bounded magnitude ``mag``.
+"""
+
+import torch
+
+from .. import _ops  # noqa: F401  (registers torch.ops.atma_hip.*)
+
+
+def _params(device, v_null, null_base, null_slope_raw, len_gain_raw, mag_beta_raw):
+    f = lambda t: t.detach().to(device=device, dtype=torch.float32).contiguous()  # noqa: E731
+    return (f(v_null), f(null_base), f(null_slope_raw), f(len_gain_raw), f(mag_beta_raw))
+
+
+def _window_arg(window):
+    if window is None:
+        return 0
+    w = int(window)
+    if w <= 0:
+        raise ValueError(f"window must be a positive int or None (got {window})")
+    return w
+
+
+@torch.no_grad()
+def polar_attention_fwd(q, k, v, n_keys, *, v_null, null_base, null_slope_raw, len_gain_raw,
+                        mag_beta_raw, eps=1e-6, is_causal=True, input_precision="ieee",
+                        window=None):
+    """Forward-only Polar attention.  Mirrors ``polar_attention_fwd``
+    (``kernel/polar_triton.py:594-609``, launch checks ``:505-530``).
+
+    q: (B, Hq, Tq, d).  k, v: (B, Hkv, Tk, d) with Hq % Hkv == 0 -- the reference's
+    expanded form (Hkv == Hq) or the unexpanded GQA form (resolved in-kernel).
+    n_keys: (Tq,) valid key count per query.  ``is_causal`` requires Tq == Tk.
+    ``input_precision`` is accepted for signature compatibility: fp32 inputs always
+    use full-fp32 MFMA products.  ``window``: causal sliding window (None = full).
+    Returns (c (B, Hq, Tq, d), mag (B, Hq, Tq)) in q's dtype."""
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be (B, H, T, d)")
+    B, Hq, Tq, dk = q.shape
+    Tk = k.shape[2]
+    if is_causal and Tq != Tk:
+        raise ValueError(
+            f"is_causal=True requires Tq == Tk (standard causal self-attention); got Tq={Tq}, "
+            f"Tk={Tk}. Use is_causal=False with an explicit n_keys for decode / offset-prefill "
+            f"layouts.")
+    if dk & (dk - 1) != 0:
+        raise ValueError(f"head_dim (dk={dk}) must be a power of two.")
+    if k.shape != v.shape or k.shape[0] != B or k.shape[3] != dk:
+        raise ValueError(f"k/v shape {tuple(k.shape)}/{tuple(v.shape)} incompatible with q {tuple(q.shape)}")
+    if Hq % k.shape[1]:
+        raise ValueError(f"query heads ({Hq}) must be a multiple of kv heads ({k.shape[1]})")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k, v must share a dtype")
+    if input_precision not in ("ieee", "tf32", "tf32x3"):
+        raise ValueError(f"unknown input_precision {input_precision!r}")
+    n_keys = n_keys.to(device=q.device, dtype=torch.float32).reshape(-1).contiguous()
+    if n_keys.numel() != Tq:
+        raise ValueError(f"n_keys must have Tq={Tq} entries (got {n_keys.numel()})")
+    p = _params(q.device, v_null, null_base, null_slope_raw, len_gain_raw, mag_beta_raw)
+    c, mag = torch.ops.atma_hip.polar_attention_fwd(q, k, v, n_keys, *p, float(eps), bool(is_causal),
+                                                    _window_arg(window))
+    return c, mag
+
+
+@torch.no_grad()
+def polar_attention_decode(q, k_cache, v_cache, block_tables, context_lens, *, v_null, null_base,
+                           null_slope_raw, len_gain_raw, mag_beta_raw, eps=1e-6, block_n=None,
+                           num_warps=None, num_stages=None, window=None):
+    """Paged Polar decode.  Mirrors ``polar_attention_decode``
+    (``kernel/polar_triton.py:796-858``).
+
+    q: (B, Hq, d) current-token queries (KV heads NOT expanded, GQA in-kernel).
+    k_cache, v_cache: (num_pages, page_size, Hkv, d) contiguous.  block_tables:
+    (B, max_pages) int32 logical->physical page map.  context_lens: (B,) int32 keys
+    per sequence, including the current token.  ``block_n`` / ``num_warps`` /
+    ``num_stages`` are Triton tuning knobs, accepted and ignored.
+    Returns (c (B, Hq, d), mag (B, Hq)) in q's dtype.  Graph capturable."""
+    if q.dim() != 3 or k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
+        raise ValueError("q must be (B, H, d) and k_cache/v_cache (pages, page_size, Hkv, d)")
+    if q.shape[2] != k_cache.shape[3] or q.shape[1] % k_cache.shape[2]:
+        raise ValueError(f"q {tuple(q.shape)} incompatible with cache {tuple(k_cache.shape)}")
+    if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+        raise ValueError("q and the caches must share a dtype")
+    if block_tables.dim() != 2 or block_tables.shape[0] != q.shape[0]:
+        raise ValueError("block_tables must be (B, max_pages)")
+    if block_tables.dtype != torch.int32:
+        block_tables = block_tables.to(torch.int32)
+    if block_tables.stride(1) != 1:
+        block_tables = block_tables.contiguous()
+    context_lens = context_lens.to(device=q.device, dtype=torch.int32).contiguous()
+    p = _params(q.device, v_null, null_base, null_slope_raw, len_gain_raw, mag_beta_raw)
+    c, mag = torch.ops.atma_hip.polar_attention_decode(q, k_cache, v_cache, block_tables,
+                                                       context_lens, *p, float(eps),
+                                                       _window_arg(window))
+    return c, mag

@@ -1,0 +1,163 @@
+/*
+ * atma_hip.h -- C ABI of libatma_hip.so, the MI355X (gfx950) implementation of
+ * ATMA's global-layer mixer: Polar attention prefill and paged decode, the paged
+ * KV write, and the gated-delta memory (chunked prefill + single-token step).
+ *
+ * Conventions (every entry point):
+ *   - plain device pointers, element strides (int64, in elements, not bytes),
+ *     dimensions and float scalars; no framework types;
+ *   - `dtype` selects the element type of the activation tensors (q/k/v, caches,
+ *     outputs c/mag/o): ATMA_F32, ATMA_BF16 or ATMA_F16.  Parameters, n_keys,
+ *     gates and memory states are always fp32;
+ *   - the innermost (head_dim) stride of every activation tensor is 1;
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream);
+ *   - kernels are only enqueued: no host synchronisation, no device allocation
+ *     (scratch comes in through `workspace`), no memset -- every entry point is
+ *     safe under stream / graph capture;
+ *   - return ATMA_OK (0) or an ATMA_ERR_* code; atma_last_error() then returns a
+ *     message (thread-local, valid until the next call on that thread).
+ *
+ * Each declaration cites the reference operation it replaces (paths relative to
+ * the akbar2habibullah/atma repository).
+ */
+#ifndef ATMA_HIP_H
+#define ATMA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { ATMA_F32 = 0, ATMA_BF16 = 1, ATMA_F16 = 2 };
+
+enum {
+  ATMA_OK = 0,
+  ATMA_ERR_INVALID = 1,     /* bad shape / stride / argument            */
+  ATMA_ERR_UNSUPPORTED = 2, /* valid request this build does not cover  */
+  ATMA_ERR_WORKSPACE = 3,   /* workspace missing or too small           */
+  ATMA_ERR_HIP = 4          /* a HIP runtime call or launch failed      */
+};
+
+/* Version of this ABI (bumped on any signature change). */
+int atma_abi_version(void);
+
+/* Message describing the last non-zero return on the calling thread. */
+const char* atma_last_error(void);
+
+/*
+ * Paged KV write.  Replaces store_kvcache (inference/layers/attention.py:30-56).
+ * key/value: (n_tokens, Hkv, d) rows, row stride key_stride / value_stride
+ * elements, each row `row_elems` = Hkv*d contiguous elements.  k_cache/v_cache:
+ * contiguous (num_pages, page_size, Hkv, d) = `total_slots` rows of row_elems.
+ * Token i is copied bit-for-bit into row slot_mapping[i]; slots < 0 are skipped
+ * (reference: -1 = skip) and slots >= total_slots are skipped too.
+ */
+int atma_store_kvcache(const void* key, int64_t key_stride, const void* value,
+                       int64_t value_stride, void* k_cache, void* v_cache,
+                       const int32_t* slot_mapping, int64_t n_tokens, int64_t row_elems,
+                       int64_t total_slots, int dtype, void* stream);
+
+/*
+ * Flash-style Polar attention forward (prefill).  Replaces polar_attention_fwd /
+ * _polar_forward (kernel/polar_triton.py:505-609).
+ * q: (B, Hq, Tq, d) strides (q_sb, q_sh, q_st, 1);  k, v: (B, Hkv, Tk, d) with
+ * Hq % Hkv == 0 (GQA handled in-kernel; Hkv == Hq is the reference's expanded
+ * form).  n_keys: (Tq,) fp32 valid-key count per query (the mask uses it raw,
+ * temp/null use max(min(n, window), 1)).  Raw Polar parameters, fp32, contiguous:
+ * v_null (Hq, d), null_base / null_slope_raw / len_gain_raw / mag_beta_raw (Hq,).
+ * Outputs (dtype, contiguous): c (B, Hq, Tq, d), mag (B, Hq, Tq).  Optional fp32
+ * saved statistics for a backward pass (any may be NULL): stat_m / stat_l /
+ * stat_q2 (B, Hq, Tq) as the natural-log running max, sum p, sum p^2 after the null
+ * fold, and stat_s (B, Hq, Tq, d) the unnormalised direction.
+ * is_causal requires Tq == Tk and bounds each query tile's key loop at the tile's
+ * last row (kernel/polar_triton.py:110-113,522-526).  window <= 0 disables the
+ * sliding window.  d must be 64 or 128.
+ */
+int atma_polar_attention_fwd(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                             const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                             const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                             const float* n_keys, const float* v_null, const float* null_base,
+                             const float* null_slope_raw, const float* len_gain_raw,
+                             const float* mag_beta_raw, void* c, void* mag, float* stat_m,
+                             float* stat_l, float* stat_q2, float* stat_s, int64_t B,
+                             int64_t Hq, int64_t Hkv, int64_t Tq, int64_t Tk, int64_t d,
+                             int dtype, int is_causal, int64_t window, float eps,
+                             void* stream);
+
+/*
+ * Workspace bytes atma_polar_attention_decode needs for this launch shape.
+ */
+size_t atma_polar_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t max_pages,
+                                         int64_t page_size, int64_t d);
+
+/*
+ * Paged Polar GQA decode (split-K over pages + merge).  Replaces
+ * polar_attention_decode / _polar_decode_kernel (kernel/polar_triton.py:682-858).
+ * q: (B, Hq, d) strides (q_sb, q_sh, 1).  k_cache / v_cache: contiguous
+ * (num_pages, page_size, Hkv, d).  block_tables: (B, max_pages) int32 with row
+ * stride bt_sb; context_lens: (B,) int32, keys 0..ctx-1 of sequence b live at
+ * page block_tables[b, pos / page_size], row pos % page_size.  Entries past a
+ * sequence's last page are never read; page ids outside [0, num_pages) are
+ * treated as empty keys.  Outputs (dtype, contiguous): c (B, Hq, d), mag (B, Hq).
+ * The launch shape depends only on (B, Hq, max_pages): graph capturable.
+ */
+int atma_polar_attention_decode(const void* q, int64_t q_sb, int64_t q_sh, const void* k_cache,
+                                const void* v_cache, int64_t num_pages, int64_t page_size,
+                                int64_t Hkv, const int32_t* block_tables, int64_t bt_sb,
+                                int64_t max_pages, const int32_t* context_lens,
+                                const float* v_null, const float* null_base,
+                                const float* null_slope_raw, const float* len_gain_raw,
+                                const float* mag_beta_raw, void* c, void* mag, int64_t B,
+                                int64_t Hq, int64_t d, int dtype, int64_t window, float eps,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * One gated-delta decode step, IN PLACE on the slot-indexed fp32 state table.
+ * Replaces gated_delta_decode_step (kernel/gated_delta_triton.py:78-117).
+ * q, k, v: (B, H, d) strides (x_sb, x_sh, 1) (KV heads already expanded);
+ * gamma, beta: (B, H) fp32 contiguous; state_table: contiguous fp32
+ * (max_seqs, H, dk, dv) in [K, V] layout; slots: (B,) int64 rows of the table
+ * (a slot outside [0, max_seqs) leaves the table untouched and yields NaN r).
+ * Output r: (B, H, dv) fp32 contiguous.  dk = dv = 128 or 64.
+ */
+int atma_gated_delta_decode_step(const void* q, int64_t q_sb, int64_t q_sh, const void* k,
+                                 int64_t k_sb, int64_t k_sh, const void* v, int64_t v_sb,
+                                 int64_t v_sh, const float* gamma, const float* beta,
+                                 float* state_table, int64_t max_seqs, const int64_t* slots,
+                                 float* r, int64_t B, int64_t H, int64_t dk, int64_t dv,
+                                 int dtype, float eps, void* stream);
+
+/*
+ * Workspace bytes atma_chunk_gated_delta_rule needs for this shape.
+ */
+size_t atma_chunk_gated_delta_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t dk,
+                                              int64_t dv, int64_t chunk);
+
+/*
+ * Chunked gated-delta prefill with state carry.  Replaces the third-party
+ * fla.ops.gated_delta_rule.chunk_gated_delta_rule as the reference calls it
+ * (model/blocks.py:44-49, inference/models/atma.py:285-287,318-322), with the
+ * arithmetic of gated_delta_chunked (model/blocks.py:375-423).
+ * q, k: (B, T, H, dk), v: (B, T, H, dv), strides (x_sb, x_st, x_sh, 1);
+ * g (log-decay) and beta: (B, T, H) fp32 contiguous; initial_state (nullable =
+ * zeros) and final_state (nullable = not written): (B, H, dk, dv) fp32 [K, V].
+ * Output o: (B, T, H, dv) dtype contiguous.  q, k are L2-normalised when
+ * use_qk_l2norm != 0, then q is multiplied by `scale`.  chunk must be 64;
+ * dk = dv = 128 or 64.
+ */
+int atma_chunk_gated_delta_rule(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
+                                const void* k, int64_t k_sb, int64_t k_st, int64_t k_sh,
+                                const void* v, int64_t v_sb, int64_t v_st, int64_t v_sh,
+                                const float* g, const float* beta, const float* initial_state,
+                                float* final_state, void* o, int64_t B, int64_t T, int64_t H,
+                                int64_t dk, int64_t dv, int dtype, float scale,
+                                int use_qk_l2norm, int64_t chunk, void* workspace,
+                                size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ATMA_HIP_H */

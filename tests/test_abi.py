@@ -1,0 +1,94 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol declared in
+include/atma_hip.h with the Python binding's signature table, and its host-side
+argument validation rejects bad requests before any launch."""
+
+import ctypes
+import re
+
+import pytest
+import torch
+
+from atma_amd import _lib
+
+
+def _declared():
+    text = _lib.HEADER.read_text()
+    body = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(atma_\w+)\s*\(", body)))
+
+
+def test_header_and_binding_agree():
+    assert _declared() == sorted(_lib.SIGNATURES), "include/atma_hip.h and _lib.SIGNATURES differ"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail("libatma_hip.so missing: run `python -m atma_amd._build` (the driver's build())")
+    return _lib.load()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.atma_abi_version() == 1
+
+
+def test_validation_rejects_without_launch(lib):
+    null = None
+    # is_causal with Tq != Tk
+    rc = lib.atma_polar_attention_fwd(null, 0, 0, 0, null, 0, 0, 0, null, 0, 0, 0, null, null, null,
+                                      null, null, null, null, null, null, null, null, null,
+                                      1, 8, 2, 16, 32, 128, 1, 1, 0, 1e-6, null)
+    assert rc == 1 and b"Tq == Tk" in lib.atma_last_error()
+    # unsupported head dim
+    rc = lib.atma_polar_attention_fwd(null, 0, 0, 0, null, 0, 0, 0, null, 0, 0, 0, null, null, null,
+                                      null, null, null, null, null, null, null, null, null,
+                                      1, 8, 2, 16, 16, 96, 1, 0, 0, 1e-6, null)
+    assert rc == 2
+    # GQA group not dividing
+    rc = lib.atma_polar_attention_decode(null, 0, 0, null, null, 4, 256, 3, null, 0, 2, null, null,
+                                         null, null, null, null, null, null, 2, 8, 128, 1, 0, 1e-6,
+                                         null, 0, null)
+    assert rc == 1
+    # decode workspace too small
+    need = lib.atma_polar_decode_workspace_bytes(2, 8, 4, 256, 128)
+    assert need == 2 * 8 * 4 * (128 + 4) * 4
+    buf = ctypes.create_string_buffer(16)
+    rc = lib.atma_polar_attention_decode(buf, 8, 8, buf, buf, 4, 256, 2, buf, 4, 4, buf, buf, buf,
+                                         buf, buf, buf, buf, buf, 2, 8, 128, 1, 0, 1e-6, buf, 16, null)
+    assert rc == 3
+    # chunked gated delta: chunk must be 64; dk == dv
+    assert lib.atma_chunk_gated_delta_rule(null, 0, 0, 0, null, 0, 0, 0, null, 0, 0, 0, null, null,
+                                           null, null, null, 1, 64, 2, 128, 128, 1, 1.0, 1, 32,
+                                           null, 0, null) == 2
+    assert lib.atma_chunk_gated_delta_workspace_bytes(1, 65, 2, 128, 128, 64) == 2 * 2 * (5 * 64 * 128 + 4) * 4
+    # gated delta step: unsupported dims
+    assert lib.atma_gated_delta_decode_step(null, 0, 0, null, 0, 0, null, 0, 0, null, null, null, 1,
+                                            null, null, 1, 1, 96, 96, 1, 1e-12, null) == 2
+    # store_kvcache: unknown dtype
+    assert lib.atma_store_kvcache(null, 0, null, 0, null, null, null, 1, 256, 8, 9, null) == 1
+    # zero-size requests are no-ops
+    assert lib.atma_store_kvcache(null, 0, null, 0, null, null, null, 0, 256, 8, 1, null) == 0
+
+
+def test_python_wrappers_validate_like_the_reference():
+    from atma_amd.kernel import polar_attention_fwd
+    p = dict(v_null=torch.zeros(2, 128), null_base=torch.zeros(2), null_slope_raw=torch.zeros(2),
+             len_gain_raw=torch.zeros(2), mag_beta_raw=torch.zeros(2))
+    q = torch.zeros(1, 2, 4, 128)
+    k = torch.zeros(1, 2, 6, 128)
+    with pytest.raises(ValueError, match="Tq == Tk"):
+        polar_attention_fwd(q, k, k, torch.arange(1, 5.0), is_causal=True, **p)
+    q3 = torch.zeros(1, 2, 4, 96)
+    with pytest.raises(ValueError, match="power of two"):
+        polar_attention_fwd(q3, q3, q3, torch.arange(1, 5.0), **p)
+
+
+def test_cpu_tensors_fail_loudly():
+    from atma_amd.kernel import polar_attention_fwd
+    p = dict(v_null=torch.zeros(2, 128), null_base=torch.zeros(2), null_slope_raw=torch.zeros(2),
+             len_gain_raw=torch.zeros(2), mag_beta_raw=torch.zeros(2))
+    q = torch.zeros(1, 2, 4, 128)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        polar_attention_fwd(q, q, q, torch.arange(1, 5.0), **p)
