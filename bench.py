@@ -1,0 +1,348 @@
+"""Benchmark of ATMA's global-layer mixer on one MI355X.
+
+Default workload (the `value`): BASELINE.json configs[1] -- bf16 global-layer prefill,
+B=8, T=2048, 8 query / 2 KV heads, d=128: Polar attention forward (GQA in-kernel) plus
+the gated-delta chunked prefill (C=64, fp32 state from zero, memory gate / beta logits
+through the layer's own logsigmoid(z + 3.9) / sigmoid(z)).  One step = both ops over
+the resident batch.  value = (Polar + gated-delta algorithmic FLOPs) / step time.
+
+Also reported in the same JSON line: configs[2] (B=1, T=65,536 and 262,144) and
+configs[3] (paged decode step: 64 sequences, ctx ~ U[1024, 32768], 256-token pages in
+a shuffled pool, store_kvcache + Polar decode + gated-delta step, replayed as a HIP
+graph), each with its roofline fraction, plus the CPU oracle timed on this host.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4] [--no-cpu]
+"""
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+METRIC = "Polar+GDN prefill TFLOP/s & MFMA%; paged decode tok/s & HBM GB/s (1 GPU)"
+HQ, HKV, D, CHUNK = 8, 2, 128, 64
+
+
+def polar_flops(B, T):
+    return float(B) * HQ * 2 * D * T * (T + 1)
+
+
+def gdn_flops(B, T):
+    return float(B) * T * HQ * (6 * D * D + 4 * CHUNK * D)
+
+
+def _params(torch, dev, seed=0):
+    """Polar parameters at the reference priors (model/reference.py:17-20)."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    return dict(v_null=(torch.randn(HQ, D, generator=g) * 0.02).to(dev),
+                null_base=torch.full((HQ,), 2.0, device=dev),
+                null_slope_raw=torch.full((HQ,), 0.5, device=dev),
+                len_gain_raw=torch.full((HQ,), -1.0, device=dev),
+                mag_beta_raw=torch.full((HQ,), -1.5, device=dev))
+
+
+class Prefill:
+    """Resident inputs and one step of the prefill hot path."""
+
+    def __init__(self, torch, dev, B, T, seed=0):
+        from atma_amd.kernel import chunk_gated_delta_rule, polar_attention_fwd
+        self.torch, self.B, self.T = torch, B, T
+        self.fwd, self.gdn = polar_attention_fwd, chunk_gated_delta_rule
+        g = torch.Generator(device=dev).manual_seed(seed)
+        bf = torch.bfloat16
+        self.q = torch.randn(B, HQ, T, D, device=dev, generator=g, dtype=bf)
+        self.k = torch.randn(B, HKV, T, D, device=dev, generator=g, dtype=bf)
+        self.v = torch.randn(B, HKV, T, D, device=dev, generator=g, dtype=bf)
+        # the memory branch sees KV expanded to the query heads, (B, T, H, d) views
+        self.qm = self.q.transpose(1, 2)
+        self.km = self.k.repeat_interleave(HQ // HKV, 1).transpose(1, 2)
+        self.vm = self.v.repeat_interleave(HQ // HKV, 1).transpose(1, 2)
+        self.zg = torch.randn(B, T, HQ, device=dev, generator=g)
+        self.zb = torch.randn(B, T, HQ, device=dev, generator=g)
+        self.s0 = torch.zeros(B, HQ, D, D, device=dev)
+        self.n_keys = torch.arange(1, T + 1, device=dev, dtype=torch.float32)
+        self.p = _params(torch, dev, seed)
+
+    def polar(self):
+        return self.fwd(self.q, self.k, self.v, self.n_keys, **self.p)
+
+    def memory(self):
+        F = self.torch.nn.functional
+        glog = F.logsigmoid(self.zg + 3.9)
+        beta = self.torch.sigmoid(self.zb)
+        return self.gdn(self.qm, self.km, self.vm, glog, beta, scale=1.0, initial_state=self.s0,
+                        output_final_state=True, use_qk_l2norm_in_kernel=True)
+
+    def step(self):
+        self.polar()
+        self.memory()
+
+    def flops(self):
+        return polar_flops(self.B, self.T), gdn_flops(self.B, self.T)
+
+
+def _time(torch, fn, steps, warmup):
+    """Average ms per call of fn over `steps` calls, HIP events on the current stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def bench_prefill(torch, dev, B, T, steps, warmup):
+    w = Prefill(torch, dev, B, T)
+    fp, fg = w.flops()
+    ms_step = _time(torch, w.step, steps, warmup)
+    ms_polar = _time(torch, w.polar, steps, max(1, warmup // 2))
+    ms_gdn = _time(torch, w.memory, steps, max(1, warmup // 2))
+    res = dict(B=B, T=T, ms_per_step=ms_step, tflops=(fp + fg) / (ms_step * 1e-3) / 1e12,
+               polar_ms=ms_polar, polar_tflops=fp / (ms_polar * 1e-3) / 1e12,
+               gdn_ms=ms_gdn, gdn_tflops=fg / (ms_gdn * 1e-3) / 1e12,
+               polar_flops=fp, gdn_flops=fg)
+    res["mfma_frac"] = res["tflops"] / PEAK_BF16_TFLOPS
+    res["polar_mfma_frac"] = res["polar_tflops"] / PEAK_BF16_TFLOPS
+    del w
+    torch.cuda.empty_cache()
+    return res
+
+
+class Decode:
+    """one paged decode step for 64 sequences."""
+
+    def __init__(self, torch, dev, seed=0, B=64, ctx_lo=1024, ctx_hi=32768, page=256, full=False):
+        from atma_amd.kernel import gated_delta_decode_step, polar_attention_decode
+        from atma_amd.layers.attention import store_kvcache
+        self.torch = torch
+        self.dec, self.step_mem, self.store = polar_attention_decode, gated_delta_decode_step, store_kvcache
+        gc = torch.Generator().manual_seed(seed)
+        ctx = (torch.full((B,), ctx_hi) if full else torch.randint(ctx_lo, ctx_hi + 1, (B,), generator=gc))
+        npg = (ctx + page - 1) // page
+        pool = int(npg.sum())
+        perm = torch.randperm(pool, generator=gc).int()
+        maxp = (ctx_hi + page - 1) // page
+        bt = torch.zeros((B, maxp), dtype=torch.int32)
+        used = 0
+        for b in range(B):
+            bt[b, :npg[b]] = perm[used:used + npg[b]]
+            used += int(npg[b])
+        slot_map = torch.tensor([int(bt[b, (int(ctx[b]) - 1) // page]) * page + (int(ctx[b]) - 1) % page
+                                 for b in range(B)], dtype=torch.int32)
+        g = torch.Generator(device=dev).manual_seed(seed)
+        bf = torch.bfloat16
+        self.kc = torch.randn(pool, page, HKV, D, device=dev, generator=g, dtype=bf)
+        self.vc = torch.randn(pool, page, HKV, D, device=dev, generator=g, dtype=bf)
+        self.q = torch.randn(B, HQ, D, device=dev, generator=g, dtype=bf)
+        self.knew = torch.randn(B, HKV, D, device=dev, generator=g, dtype=bf)
+        self.vnew = torch.randn(B, HKV, D, device=dev, generator=g, dtype=bf)
+        self.km = self.knew.repeat_interleave(HQ // HKV, 1)
+        self.vm = self.vnew.repeat_interleave(HQ // HKV, 1)
+        self.gamma = torch.sigmoid(torch.randn(B, HQ, device=dev, generator=g) + 3.9)
+        self.beta = torch.sigmoid(torch.randn(B, HQ, device=dev, generator=g))
+        max_seqs = 2 * B
+        self.table = torch.randn(max_seqs, HQ, D, D, device=dev, generator=g) * 0.1
+        self.slots = torch.randperm(max_seqs, generator=gc)[:B].to(dev)
+        self.bt, self.ctx, self.slot_map = bt.to(dev), ctx.int().to(dev), slot_map.to(dev)
+        self.p = _params(torch, dev, seed)
+        self.B, self.pages = B, pool
+        self.ctx_sum = int(ctx.sum())
+        self.graph = None
+
+    def step(self):
+        self.store(self.knew, self.vnew, self.kc, self.vc, self.slot_map)
+        c, mag = self.dec(self.q, self.kc, self.vc, self.bt, self.ctx, **self.p)
+        r = self.step_mem(self.q, self.km, self.vm, self.gamma, self.beta, self.table, self.slots)
+        return c, mag, r
+
+    def attention(self):
+        return self.dec(self.q, self.kc, self.vc, self.bt, self.ctx, **self.p)
+
+    def capture(self):
+        torch = self.torch
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                self.step()
+        torch.cuda.current_stream().wait_stream(s)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.step()
+
+    def replay(self):
+        self.graph.replay()
+
+    def bytes(self):
+        kv = self.ctx_sum * HKV * D * 2 * 2
+        state = self.B * HQ * D * D * 4 * 2
+        small = (self.B * HQ * D * 2 * 4            # q (attention + memory), km, vm reads
+                 + self.B * HQ * D * 2 + self.B * HQ * 2 + self.B * HQ * D * 4   # c, mag, r
+                 + self.B * HKV * D * 2 * 2 * 2     # new k/v read + written
+                 + 4 * self.pages + 4 * self.B * 3)  # page table, ctx, slots
+        return kv, state, small
+
+
+def bench_decode(torch, dev, steps, warmup, full=False):
+    w = Decode(torch, dev, full=full)
+    w.capture()
+    ms_graph = _time(torch, w.replay, steps, warmup)
+    ms_eager = _time(torch, w.step, steps, warmup)
+    ms_attn = _time(torch, w.attention, steps, warmup)
+    kv, state, small = w.bytes()
+    total = kv + state + small
+    res = dict(B=w.B, ctx_sum=w.ctx_sum, pages=w.pages, ms_per_step=ms_graph, ms_eager=ms_eager,
+               tok_per_s=w.B / (ms_graph * 1e-3), bytes=total, gbs=total / (ms_graph * 1e-3) / 1e9,
+               attn_ms=ms_attn, attn_bytes=kv, attn_gbs=kv / (ms_attn * 1e-3) / 1e9)
+    res["hbm_frac"] = res["gbs"] / PEAK_HBM_GBS
+    res["attn_hbm_frac"] = res["attn_gbs"] / PEAK_HBM_GBS
+    del w
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(torch):
+    """The CPU oracle (oracle/: Polar streaming form + gated-delta chunked UT form, fp32)
+    on a bounded sample of configs[1]: one of the 8 sequences, full T = 2048, all heads."""
+    from oracle import gated_delta as OG
+    from oracle import polar as OP
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    T = 2048
+    q = torch.randn(1, HQ, T, D, generator=g)
+    k = torch.randn(1, HKV, T, D, generator=g)
+    v = torch.randn(1, HKV, T, D, generator=g)
+    zg, zb = torch.randn(1, T, HQ, generator=g), torch.randn(1, T, HQ, generator=g)
+    p = {n: t.cpu() for n, t in _params(torch, "cpu").items()}
+    n = torch.arange(1, T + 1, dtype=torch.float32)
+
+    def run():
+        OP.polar_online(q, k, v, n, params=p, k_block=512)
+        kx, vx = k.repeat_interleave(4, 1), v.repeat_interleave(4, 1)
+        OG.chunk_gated_delta_rule(q.transpose(1, 2), kx.transpose(1, 2), vx.transpose(1, 2),
+                                  torch.nn.functional.logsigmoid(zg + 3.9), torch.sigmoid(zb),
+                                  scale=1.0, output_final_state=True, use_qk_l2norm_in_kernel=True)
+
+    run()
+    times = []
+    t_end = time.perf_counter() + 20.0
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 10):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    sec = statistics.median(times)
+    flops = polar_flops(1, T) + gdn_flops(1, T)
+    model = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"configs[1] sequence 0 of 8 (B=1, T=2048, 8/2 heads, d=128), fp32 torch CPU, "
+                      f"median of {len(times)} runs = {sec:.3f} s",
+            "torch_threads": torch.get_num_threads(), "cpu_model": model}
+
+
+def _traffic():
+    """HBM bytes per Polar prefill launch measured with rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, scaled by a copy-kernel calibration), committed under profiles/."""
+    f = ROOT / "profiles" / "polar_prefill_c2_traffic.json"
+    try:
+        return json.loads(f.read_text()).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", choices=["c2", "c3", "c4"], default=None)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-long", action="store_true", help="skip T=262,144")
+    args = ap.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build targets a single MI355X "
+              "(multi-GPU sharding is design-only); run with --gpus 1", file=sys.stderr)
+        return 2
+    import torch
+    from atma_amd import _lib
+    _lib.load()
+    dev = torch.device("cuda:0")
+    torch.backends.cuda.matmul.allow_tf32 = False
+
+    out = {}
+    if args.only in (None, "c2"):
+        c2 = bench_prefill(torch, dev, 8, 2048, args.steps, args.warmup)
+        print(f"# c2 prefill: {json.dumps(c2)}", file=sys.stderr, flush=True)
+        out["c2"] = c2
+    if args.only in (None, "c3"):
+        c3 = [bench_prefill(torch, dev, 1, 65536, max(2, args.steps // 4), 1)]
+        print(f"# c3 prefill T=65536: {json.dumps(c3[0])}", file=sys.stderr, flush=True)
+        if not args.no_long:
+            c3.append(bench_prefill(torch, dev, 1, 262144, 2, 1))
+            print(f"# c3 prefill T=262144: {json.dumps(c3[1])}", file=sys.stderr, flush=True)
+        out["c3"] = c3
+    if args.only in (None, "c4"):
+        c4 = bench_decode(torch, dev, args.steps, args.warmup)
+        print(f"# c4 decode: {json.dumps(c4)}", file=sys.stderr, flush=True)
+        c4w = bench_decode(torch, dev, max(5, args.steps // 2), 2, full=True)
+        print(f"# c4 decode 64x32768: {json.dumps(c4w)}", file=sys.stderr, flush=True)
+        out["c4"] = [c4, c4w]
+    if args.only is not None:
+        print(json.dumps(out))
+        return 0
+
+    c2 = out["c2"]
+    line = {
+        "metric": METRIC,
+        "value": round(c2["tflops"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c2["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v and gate logits; Polar params at the reference priors)",
+        "config": {"workload": "configs[1]: global-layer prefill, Polar fwd + gated-delta chunked "
+                               "(C=64, fp32 state from 0)", "B": 8, "T": 2048, "q_heads": HQ,
+                   "kv_heads": HKV, "head_dim": D, "mfma_frac_of_bf16_peak": round(c2["mfma_frac"], 4)},
+        "roofline": {"bound": "mfma", "kernel": "polar_fwd_kernel<bf16,128>",
+                     "achieved": round(c2["polar_tflops"], 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(c2["polar_mfma_frac"], 4),
+                     "traffic": _traffic()},
+        "breakdown_c2": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c2.items()},
+        "prefill_long": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+                         for r in out["c3"]],
+        "decode": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+                   for r in out["c4"]],
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(torch)
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -25,7 +25,8 @@ def _inputs(B, T, H, d, dtype, seed):
 
 def _run(dev, *args, **kw):
     from atma_amd.kernel import chunk_gated_delta_rule
-    o, S = chunk_gated_delta_rule(*(a.to(dev) if torch.is_tensor(a) else a for a in args), **kw)
+    mv = lambda a: a.to(dev) if torch.is_tensor(a) else a  # noqa: E731
+    o, S = chunk_gated_delta_rule(*map(mv, args), **{n: mv(a) for n, a in kw.items()})
     torch.cuda.synchronize()
     return o.cpu(), (S.cpu() if S is not None else None)
 
