@@ -24,7 +24,10 @@ ARCH = "gfx950"
 # Packed fp32 VALU ops are disabled for all device code (they have produced wrong
 # results on this hardware pool); hipcc's host pass warns that it does not know
 # the feature, which is harmless.
-DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                # keep MFMA accumulators in VGPRs: the softmax touches them with VALU ops,
+                # and AGPR residency costs a v_accvgpr move per element per key block
+                "-mllvm", "-amdgpu-mfma-vgpr-form"]
 COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-munsafe-fp-atomics",
                 "-Wno-unused-command-line-argument", "-Wno-unknown-warning-option"]
 

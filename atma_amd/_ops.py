@@ -138,7 +138,8 @@ def chunk_gated_delta_rule_op(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: 
     o = torch.empty((B, T, H, dv), device=q.device, dtype=q.dtype)
     final = torch.empty((B, H, dk, dv), device=q.device, dtype=torch.float32) if want_final else None
     chunk = 64
-    ws_bytes = lib.atma_chunk_gated_delta_workspace_bytes(B, T, H, dk, dv, chunk)
+    ws_bytes = lib.atma_chunk_gated_delta_workspace_bytes(B, T, H, dk, dv, chunk,
+                                                          _lib.dtype_code(q.dtype))
     ws = torch.empty((max(ws_bytes, 4) // 4,), device=q.device, dtype=torch.float32)
     rc = lib.atma_chunk_gated_delta_rule(
         q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),

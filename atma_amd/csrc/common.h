@@ -44,6 +44,35 @@ union Pack8 {
   f16x8 h;
 };
 
+// v_mfma_f32_16x16x32_{bf16,f16}: A lane l holds row l%16, k = 8*(l/16)+[0,8);
+// B lane l holds column l%16, same k; C lane l holds rows 4*(l/16)+[0,4), column l%16.
+template <typename T>
+__device__ __forceinline__ f32x4 mfma16x16x32(const u32x4& a, const u32x4& b, const f32x4& c) {
+  Pack8 pa, pb;
+  pa.u = a;
+  pb.u = b;
+  if constexpr (__is_same(T, bf16)) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa.b, pb.b, c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(pa.h, pb.h, c, 0, 0, 0);
+  }
+}
+
+// Two floats -> one dword of two 16-bit values (x in the low half).
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float x, float y) {
+  T a = (T)x, b = (T)y;
+  uint16_t ua = __builtin_bit_cast(uint16_t, a), ub = __builtin_bit_cast(uint16_t, b);
+  return (uint32_t)ua | ((uint32_t)ub << 16);
+}
+
+// 16-bit element e (0..7) of a 16-byte vector, as float.
+template <typename T>
+__device__ __forceinline__ float elem16(const u32x4& x, int e) {
+  const uint16_t u = (uint16_t)(x[e >> 1] >> ((e & 1) * 16));
+  return (float)__builtin_bit_cast(T, u);
+}
+
 // Wave-local barrier: orders LDS traffic between lanes of one wavefront.
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

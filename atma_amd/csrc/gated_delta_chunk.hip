@@ -19,29 +19,9 @@
 // chunks in order, parallel over (sequence, head) x 16-column slabs of S (the
 // state columns are independent), with the slab resident in LDS for the whole
 // sequence.  All arithmetic is fp32.
-#include "common.h"
+#include "gated_delta.h"
 
 namespace atma {
-
-constexpr int kChunk = 64;
-
-struct GdnArgs {
-  const void* q;
-  int64_t q_sb, q_st, q_sh;
-  const void* k;
-  int64_t k_sb, k_st, k_sh;
-  const void* v;
-  int64_t v_sb, v_st, v_sh;
-  const float* g;
-  const float* beta;
-  const float* s0;
-  float* s_out;
-  void* o;
-  int B, T, H, NC;
-  float scale;
-  int l2norm;
-  float* ws;
-};
 
 template <int D>
 __host__ __device__ constexpr int64_t gdn_rec_floats() {
@@ -155,7 +135,7 @@ __global__ void __launch_bounds__(256) gdn_prep_kernel(GdnArgs a) {
   }
   __syncthreads();
 
-  float* rec = a.ws + ((int64_t)bh * a.NC + c) * gdn_rec_floats<D>();
+  float* rec = (float*)a.ws + ((int64_t)bh * a.NC + c) * gdn_rec_floats<D>();
   float* Wg = rec;
   float* U0g = rec + C * D;
   float* Qtg = rec + 2 * C * D;
@@ -257,7 +237,7 @@ __global__ void __launch_bounds__(256) gdn_scan_kernel(GdnArgs a) {
   }
 
   for (int c = 0; c < a.NC; ++c) {
-    const float* rec = a.ws + ((int64_t)bh * a.NC + c) * gdn_rec_floats<D>();
+    const float* rec = (const float*)a.ws + ((int64_t)bh * a.NC + c) * gdn_rec_floats<D>();
     __syncthreads();  // previous chunk finished with the LDS operands
     for (int i = tid; i < C * D / 4; i += 256) {
       const int p = (4 * i) / D, d = (4 * i) % D;
@@ -344,10 +324,12 @@ static int launch_gdn(GdnArgs a, hipStream_t s) {
 }  // namespace atma
 
 extern "C" size_t atma_chunk_gated_delta_workspace_bytes(int64_t B, int64_t T, int64_t H,
-                                                         int64_t dk, int64_t dv, int64_t chunk) {
+                                                         int64_t dk, int64_t dv, int64_t chunk,
+                                                         int dtype) {
   (void)dv;
   if (B <= 0 || T <= 0 || H <= 0 || chunk != atma::kChunk || (dk != 64 && dk != 128)) return 0;
   const int64_t nc = (T + chunk - 1) / chunk;
+  if (dtype == ATMA_BF16 || dtype == ATMA_F16) return (size_t)(B * H * nc) * atma::kGdn16RecBytes;
   const int64_t rec = 5 * chunk * dk + 4;
   return (size_t)(B * H * nc * rec) * sizeof(float);
 }
@@ -377,7 +359,7 @@ extern "C" int atma_chunk_gated_delta_rule(
   }
   if (!q || !k || !v || !g || !beta || !o)
     return set_error(ATMA_ERR_INVALID, "chunk_gated_delta_rule: null pointer");
-  const size_t need = atma_chunk_gated_delta_workspace_bytes(B, T, H, dk, dv, chunk);
+  const size_t need = atma_chunk_gated_delta_workspace_bytes(B, T, H, dk, dv, chunk, dtype);
   if (!workspace || workspace_bytes < need)
     return set_error(ATMA_ERR_WORKSPACE, "chunk_gated_delta_rule: workspace %zu < %zu bytes",
                      workspace_bytes, need);
@@ -387,11 +369,8 @@ extern "C" int atma_chunk_gated_delta_rule(
   a.v = v; a.v_sb = v_sb; a.v_st = v_st; a.v_sh = v_sh;
   a.g = g; a.beta = beta; a.s0 = initial_state; a.s_out = final_state; a.o = o;
   a.B = (int)B; a.T = (int)T; a.H = (int)H; a.NC = (int)((T + chunk - 1) / chunk);
-  a.scale = scale; a.l2norm = use_qk_l2norm ? 1 : 0; a.ws = (float*)workspace;
+  a.scale = scale; a.l2norm = use_qk_l2norm ? 1 : 0; a.ws = workspace;
   hipStream_t s = (hipStream_t)stream;
-  switch (dtype) {
-    case ATMA_BF16: return dk == 128 ? launch_gdn<bf16, 128>(a, s) : launch_gdn<bf16, 64>(a, s);
-    case ATMA_F16: return dk == 128 ? launch_gdn<f16, 128>(a, s) : launch_gdn<f16, 64>(a, s);
-    default: return dk == 128 ? launch_gdn<float, 128>(a, s) : launch_gdn<float, 64>(a, s);
-  }
+  if (dtype == ATMA_BF16 || dtype == ATMA_F16) return launch_gdn16(a, dtype, (int)dk, s);
+  return dk == 128 ? launch_gdn<float, 128>(a, s) : launch_gdn<float, 64>(a, s);
 }

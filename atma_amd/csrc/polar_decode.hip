@@ -57,18 +57,6 @@ __device__ __forceinline__ void span_of(int ctx, int window, int sp, int& t0, in
   t1 = min((sp + 1) * kSplitTokens, ctx);
 }
 
-template <typename T>
-__device__ __forceinline__ f32x4 mfma16(const u32x4& a, const u32x4& b, const f32x4& c) {
-  Pack8 pa, pb;
-  pa.u = a;
-  pb.u = b;
-  if constexpr (__is_same(T, bf16)) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa.b, pb.b, c, 0, 0, 0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(pa.h, pb.h, c, 0, 0, 0);
-  }
-}
-
 __device__ __forceinline__ void unpack8(const u32x4& x, float* out, bf16) {
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
@@ -194,7 +182,7 @@ __global__ void __launch_bounds__(256) polar_decode_split_kernel(DecodeArgs a) {
 #pragma unroll
         for (int s = 0; s < D / 32; ++s) kb[s] = ok ? *(const u32x4*)(kr + 8 * s) : u32x4{0, 0, 0, 0};
 #pragma unroll
-        for (int s = 0; s < D / 32; ++s) sc[j] = mfma16<T>(qa[s], kb[s], sc[j]);
+        for (int s = 0; s < D / 32; ++s) sc[j] = mfma16x16x32<T>(qa[s], kb[s], sc[j]);
       } else {
         f32x4 kb[D / 16];
 #pragma unroll

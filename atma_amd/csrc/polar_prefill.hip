@@ -94,21 +94,13 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f
   }
 }
 
-// Two floats -> one dword of two 16-bit values (element 0 in the low half).
-template <typename T>
-__device__ __forceinline__ uint32_t pack2(float x, float y) {
-  T a = (T)x, b = (T)y;
-  uint16_t ua = __builtin_bit_cast(uint16_t, a), ub = __builtin_bit_cast(uint16_t, b);
-  return (uint32_t)ua | ((uint32_t)ub << 16);
-}
-
 template <typename T, int D>
 __global__ void __launch_bounds__(256, 1) polar_fwd_kernel(PolarFwdArgs args) {
   using Cfg = FwdCfg<T, D>;
   constexpr int BM = Cfg::BM, BN = Cfg::BN, VE = Cfg::VE, CPR = Cfg::CPR;
   constexpr int KP = Cfg::KP, VP = Cfg::VP, NT = Cfg::NT;
-  __shared__ __attribute__((aligned(16))) T Ks[BN * KP];
-  __shared__ __attribute__((aligned(16))) T Vt[D * VP];
+  __shared__ __attribute__((aligned(16))) T Ks[2 * BN * KP];  // double-buffered key tile
+  __shared__ __attribute__((aligned(16))) T Vt[2 * D * VP];   // double-buffered V^T tile
   __shared__ float s_bounds[4][2];
 
   const int tid = threadIdx.x;
@@ -202,80 +194,109 @@ __global__ void __launch_bounds__(256, 1) polar_fwd_kernel(PolarFwdArgs args) {
 #pragma unroll
   for (int t = 0; t < NT; ++t) oacc[t] = f32x16{};
 
-  // ---- global -> register prefetch of one K/V block
+  // ---- per-thread offsets inside a key block.
+  //  K: 16-byte chunk cidx = tid + 256 r -> key cidx / CPR, chunk cidx % CPR (a row per
+  //     CPR consecutive lanes: coalesced loads, contiguous LDS rows).
+  //  V: (4-key, 16-byte) group = tid + 256 gi -> key group kg = group % 16, chunk
+  //     ch = group / 16, so 16 consecutive lanes write one V^T row contiguously.
+  const int kst = (int)args.k_st, vst = (int)args.v_st;
+  int koff[Cfg::KCH], klds[Cfg::KCH];
+#pragma unroll
+  for (int r = 0; r < Cfg::KCH; ++r) {
+    const int cidx = tid + 256 * r;
+    koff[r] = (cidx / CPR) * kst + (cidx % CPR) * VE;
+    klds[r] = (cidx / CPR) * KP + (cidx % CPR) * VE;
+  }
+  int voff[Cfg::VG_PT], vkg[Cfg::VG_PT], vch[Cfg::VG_PT];
+#pragma unroll
+  for (int gi = 0; gi < Cfg::VG_PT; ++gi) {
+    const int grpi = tid + 256 * gi;
+    vkg[gi] = grpi & 15;
+    vch[gi] = grpi >> 4;
+    voff[gi] = 4 * vkg[gi] * vst + vch[gi] * VE;
+  }
+  auto v_active = [&](int gi) { return Cfg::VG_PT * 256 == Cfg::VGROUPS || tid + 256 * gi < Cfg::VGROUPS; };
+
   u32x4 kpre[Cfg::KCH];
   u32x4 vpre[Cfg::VG_PT][4];
   auto prefetch = [&](int blk) {
-    const int k0 = blk * BN;
+    const T* kb = kp + (int64_t)blk * BN * args.k_st;
+    const T* vb = vp + (int64_t)blk * BN * args.v_st;
+    const int lim = args.Tk - blk * BN;  // keys of this block below Tk
+    if (lim >= BN) {
 #pragma unroll
-    for (int r = 0; r < Cfg::KCH; ++r) {
-      const int cidx = tid + 256 * r;
-      const int key = k0 + cidx / CPR, ch = cidx % CPR;
-      kpre[r] = key < args.Tk ? *(const u32x4*)(kp + (int64_t)key * args.k_st + ch * VE)
-                              : u32x4{0, 0, 0, 0};
-    }
+      for (int r = 0; r < Cfg::KCH; ++r) kpre[r] = *(const u32x4*)(kb + koff[r]);
 #pragma unroll
-    for (int gi = 0; gi < Cfg::VG_PT; ++gi) {
-      const int grpi = tid + 256 * gi;
-      if (grpi < Cfg::VGROUPS) {
-        const int ch = grpi % CPR, kg = grpi / CPR;
+      for (int gi = 0; gi < Cfg::VG_PT; ++gi)
+        if (v_active(gi)) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int key = k0 + 4 * kg + r;
-          vpre[gi][r] = key < args.Tk ? *(const u32x4*)(vp + (int64_t)key * args.v_st + ch * VE)
-                                      : u32x4{0, 0, 0, 0};
+          for (int r = 0; r < 4; ++r) vpre[gi][r] = *(const u32x4*)(vb + voff[gi] + r * vst);
         }
-      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < Cfg::KCH; ++r)
+        kpre[r] = (tid + 256 * r) / CPR < lim ? *(const u32x4*)(kb + koff[r]) : u32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int gi = 0; gi < Cfg::VG_PT; ++gi)
+        if (v_active(gi)) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            vpre[gi][r] = 4 * vkg[gi] + r < lim ? *(const u32x4*)(vb + voff[gi] + r * vst)
+                                                : u32x4{0, 0, 0, 0};
+        }
     }
   };
-  auto commit = [&]() {
+  auto commit = [&](int buf) {
+    T* kd = Ks + buf * (BN * KP);
+    T* vd = Vt + buf * (D * VP);
 #pragma unroll
-    for (int r = 0; r < Cfg::KCH; ++r) {
-      const int cidx = tid + 256 * r;
-      const int key = cidx / CPR, ch = cidx % CPR;
-      *(u32x4*)(Ks + key * KP + ch * VE) = kpre[r];
-    }
+    for (int r = 0; r < Cfg::KCH; ++r) *(u32x4*)(kd + klds[r]) = kpre[r];
 #pragma unroll
-    for (int gi = 0; gi < Cfg::VG_PT; ++gi) {
-      const int grpi = tid + 256 * gi;
-      if (grpi < Cfg::VGROUPS) {
-        const int ch = grpi % CPR, kg = grpi / CPR;
+    for (int gi = 0; gi < Cfg::VG_PT; ++gi)
+      if (v_active(gi)) {
+        T* vrow = vd + vch[gi] * VE * VP + 4 * vkg[gi];
         if constexpr (Cfg::kHalf) {
-          // 4 keys x 8 dims -> 8 rows of V^T, 4 keys (8 bytes) each
+          // 4 keys x 8 dims -> 8 rows of V^T holding 4 keys (8 bytes) each
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int w = e >> 1, sh = (e & 1) * 16;
-            uint32_t x0 = (vpre[gi][0][w] >> sh) & 0xffffu, x1 = (vpre[gi][1][w] >> sh) & 0xffffu;
-            uint32_t x2 = (vpre[gi][2][w] >> sh) & 0xffffu, x3 = (vpre[gi][3][w] >> sh) & 0xffffu;
-            u32x2 pk = {x0 | (x1 << 16), x2 | (x3 << 16)};
-            *(u32x2*)(Vt + (ch * 8 + e) * VP + 4 * kg) = pk;
+          for (int w = 0; w < 4; ++w) {
+            const uint32_t lo01 = __builtin_amdgcn_perm(vpre[gi][1][w], vpre[gi][0][w], 0x05040100u);
+            const uint32_t hi01 = __builtin_amdgcn_perm(vpre[gi][1][w], vpre[gi][0][w], 0x07060302u);
+            const uint32_t lo23 = __builtin_amdgcn_perm(vpre[gi][3][w], vpre[gi][2][w], 0x05040100u);
+            const uint32_t hi23 = __builtin_amdgcn_perm(vpre[gi][3][w], vpre[gi][2][w], 0x07060302u);
+            *(u32x2*)(vrow + (2 * w) * VP) = u32x2{lo01, lo23};
+            *(u32x2*)(vrow + (2 * w + 1) * VP) = u32x2{hi01, hi23};
           }
         } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            u32x4 pk = {vpre[gi][0][e], vpre[gi][1][e], vpre[gi][2][e], vpre[gi][3][e]};
-            *(u32x4*)(Vt + (ch * 4 + e) * VP + 4 * kg) = pk;
-          }
+          for (int e = 0; e < 4; ++e)
+            *(u32x4*)(vrow + e * VP) = u32x4{vpre[gi][0][e], vpre[gi][1][e], vpre[gi][2][e], vpre[gi][3][e]};
         }
       }
-    }
   };
 
-  if (nblk_beg < nblk_end) prefetch(nblk_beg);
+  const int nblk = nblk_end - nblk_beg;
+  if (nblk > 0) {
+    prefetch(nblk_beg);
+    commit(0);
+  }
+  __syncthreads();
   const int arow = a_row_key(ql);
+  constexpr float kRescale = 8.f;  // lazy rescale: p <= 2^8 between max updates
 
-  for (int blk = nblk_beg; blk < nblk_end; ++blk) {
+  for (int it = 0; it < nblk; ++it) {
+    const int blk = nblk_beg + it, buf = it & 1;
     const int k0 = blk * BN;
-    commit();
-    __syncthreads();
-    if (blk + 1 < nblk_end) prefetch(blk + 1);
+    const bool more = it + 1 < nblk;
+    if (more) prefetch(blk + 1);
+    const T* Kb = Ks + buf * (BN * KP);
+    const T* Vb = Vt + buf * (D * VP);
 
     // ---- S^T = K Q^T  (two 32-key tiles)
     f32x16 sacc[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       sacc[j] = f32x16{};
-      const T* krow = Ks + (32 * j + arow) * KP;
+      const T* krow = Kb + (32 * j + arow) * KP;
       if constexpr (Cfg::kHalf) {
 #pragma unroll
         for (int s = 0; s < Cfg::QSTEPS; ++s) {
@@ -293,46 +314,51 @@ __global__ void __launch_bounds__(256, 1) polar_fwd_kernel(PolarFwdArgs args) {
       }
     }
 
-    // ---- online softmax with the extra sum of p^2
+    // ---- online softmax (+ sum of p^2); scores scaled inside one FMA per element
     const bool full = (k0 + BN <= (int)fminf(w_nlo, (float)args.Tk)) &&
                       (args.window <= 0 || (float)k0 >= w_nhi - (float)args.window);
-    float mx = kSentinel;
+    float mx = -INFINITY;
+    if (full) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float a = sacc[j][i] * c1;
-        if (!full) {
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[j][i]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
           const int key = k0 + st_key(j, i, h);
           bool ok = (float)key < n_raw && key < args.Tk;
           if (args.window > 0) ok = ok && (float)key >= n_raw - (float)args.window;
-          a = ok ? a : kSentinel;
+          sacc[j][i] = ok ? sacc[j][i] : -INFINITY;
+          mx = fmaxf(mx, sacc[j][i]);
         }
-        sacc[j][i] = a;
-        mx = fmaxf(mx, a);
-      }
     }
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float alpha = exp2f(m_run - m_new);
-    m_run = m_new;
+    const float mxs = mx * c1;
+    if (__ballot(mxs > m_run + kRescale) != 0) {
+      const float m_new = fmaxf(m_run, mxs);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_part *= alpha;
+      q2_part *= alpha * alpha;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) oacc[t] *= alpha;
+    }
+    const float neg_m = -m_run;
     float ls = 0.f, qs = 0.f;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float a = sacc[j][i];
-        float p = exp2f(a - m_new);
-        if (!full) p = a == kSentinel ? 0.f : p;
+        const float p = __builtin_amdgcn_exp2f(fmaf(sacc[j][i], c1, neg_m));
         sacc[j][i] = p;
         ls += p;
-        qs += p * p;
+        qs = fmaf(p, p, qs);
       }
-    }
-    l_part = l_part * alpha + ls;
-    q2_part = q2_part * alpha * alpha + qs;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) oacc[t] *= alpha;
+    l_part += ls;
+    q2_part += qs;
 
     // ---- O^T += V^T P^T
     if constexpr (Cfg::kHalf) {
@@ -346,7 +372,7 @@ __global__ void __launch_bounds__(256, 1) polar_fwd_kernel(PolarFwdArgs args) {
       }
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const T* vrow = Vt + (32 * t + ql) * VP + 8 * h;
+        const T* vrow = Vb + (32 * t + ql) * VP + 8 * h;
 #pragma unroll
         for (int ps = 0; ps < 4; ++ps) {
           u32x4 a = *(const u32x4*)(vrow + 16 * ps);
@@ -356,7 +382,7 @@ __global__ void __launch_bounds__(256, 1) polar_fwd_kernel(PolarFwdArgs args) {
     } else {
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        const T* vrow = Vt + (32 * t + ql) * VP + 8 * h;
+        const T* vrow = Vb + (32 * t + ql) * VP + 8 * h;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
 #pragma unroll
@@ -373,6 +399,7 @@ __global__ void __launch_bounds__(256, 1) polar_fwd_kernel(PolarFwdArgs args) {
         }
       }
     }
+    if (more) commit(buf ^ 1);
     __syncthreads();
   }
 
@@ -487,6 +514,8 @@ extern "C" int atma_polar_attention_fwd(
   if (!al16(q, q_sb, q_sh, q_st) || !al16(k, k_sb, k_sh, k_st) || !al16(v, v_sb, v_sh, v_st) ||
       (uintptr_t)c % 16)
     return set_error(ATMA_ERR_INVALID, "polar_attention_fwd: tensors must be 16-byte aligned rows");
+  if (k_st >= (1 << 24) || v_st >= (1 << 24))
+    return set_error(ATMA_ERR_UNSUPPORTED, "polar_attention_fwd: key/value row stride too large");
   PolarFwdArgs a{};
   a.q = q; a.q_sb = q_sb; a.q_sh = q_sh; a.q_st = q_st;
   a.k = k; a.k_sb = k_sb; a.k_sh = k_sh; a.k_st = k_st;

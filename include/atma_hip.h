@@ -130,10 +130,10 @@ int atma_gated_delta_decode_step(const void* q, int64_t q_sb, int64_t q_sh, cons
                                  int dtype, float eps, void* stream);
 
 /*
- * Workspace bytes atma_chunk_gated_delta_rule needs for this shape.
+ * Workspace bytes atma_chunk_gated_delta_rule needs for this shape and dtype.
  */
 size_t atma_chunk_gated_delta_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t dk,
-                                              int64_t dv, int64_t chunk);
+                                              int64_t dv, int64_t chunk, int dtype);
 
 /*
  * Chunked gated-delta prefill with state carry.  Replaces the third-party
