@@ -73,6 +73,30 @@ __device__ __forceinline__ float elem16(const u32x4& x, int e) {
   return (float)__builtin_bit_cast(T, u);
 }
 
+// Raw buffer access (gfx9 descriptor: no stride, no swizzle, dword format).  The base
+// and size live in scalar registers, a lane contributes a 32-bit byte offset, and
+// reads past `bytes` return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                               uint32_t soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+// Direct global->LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane i's
+// bytes land at lds_wave_base + 16*i.  Issued through inline asm so the compiler does
+// not serialise later LDS reads behind it; completion is tracked by vmcnt, so the
+// caller waits with s_waitcnt vmcnt(N) and a barrier before reading the data.
+__device__ __forceinline__ void dma_load16(const void* gptr, const void* lds_wave_base) {
+  const uint32_t off =
+      (uint32_t)(size_t)((__attribute__((address_space(3))) const void*)lds_wave_base);
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gptr),
+               "{m0}"(__builtin_amdgcn_readfirstlane(off))
+               : "memory");
+}
+
 // Wave-local barrier: orders LDS traffic between lanes of one wavefront.
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

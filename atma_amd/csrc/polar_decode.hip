@@ -8,14 +8,18 @@
 //
 // MI355X design: decode is HBM-bound (4 FLOP per cached byte), and 64 sequences
 // x 2 KV heads is far too few programs for 256 CUs, so:
-//  * pass 1 (split): one workgroup per (sequence, KV head, 256-token span).  Its
-//    4 waves take 64-key sub-blocks; QK^T runs on v_mfma_f32_16x16x32 (query
-//    heads = rows, zero-padded to 16; keys = columns) with K read directly from
-//    the page into the operand registers (each lane one 64-byte run of a row);
-//    p goes through a small LDS tile and PV runs on VALU with each lane owning 8
-//    contiguous head dims, so a wave reads 4 whole 256-byte V rows per load.
-//    Keys past the context, past the window or on an out-of-range page are never
-//    loaded.  The span's (m, L, Q2, acc) goes to the workspace.
+//  * pass 1 (split): one workgroup per (sequence, KV head, 2048-token span); each
+//    of its 4 waves walks a quarter of the span in 32-key sub-blocks.  QK^T runs
+//    on v_mfma_f32_16x16x32 (query heads = rows, zero-padded to 16; keys =
+//    columns) with K read from the page straight into the operand registers; p
+//    goes through a small LDS tile and PV runs on VALU with each lane owning 8
+//    contiguous head dims, so one V load covers 4 whole 256-byte rows.  Pages
+//    whose size is a multiple of 32 are read with buffer loads (page base in
+//    scalar registers, page ids fetched once per wave and picked with
+//    v_readlane), and K of the next sub-block is issued after QK^T, V of the next
+//    after PV, so ~16 KB per wave stay in flight without any full drain.  Keys
+//    past the context, past the window or on an out-of-range page never reach
+//    the sums.  The span's (m, L, Q2, acc) goes to the workspace.
 //  * pass 2 (merge): one workgroup per (sequence, query head) combines the live
 //    spans (m = max, rescale by 2^(m_i - m)), folds the null sink and writes c, mag.
 // The grid depends only on (B, Hq, max_pages): graph capturable.
@@ -23,7 +27,13 @@
 
 namespace atma {
 
-constexpr int kSplitTokens = 256;
+#ifndef ATMA_SPLIT_TOKENS
+#define ATMA_SPLIT_TOKENS 2048
+#endif
+constexpr int kSplitTokens = ATMA_SPLIT_TOKENS;  // tokens per span
+constexpr int kWaveTokens = kSplitTokens / 4;    // a wave's share of a span
+// a wave's sub-blocks have one page id per lane, with lane 63 always left at -1
+static_assert(kWaveTokens % 32 == 0 && kWaveTokens / 32 < 64, "span split");
 
 struct DecodeArgs {
   const void* q;
@@ -71,19 +81,31 @@ __device__ __forceinline__ void unpack8(const u32x4& x, float* out, f16) {
   for (int e = 0; e < 8; ++e) out[e] = (float)p.h[e];
 }
 
-// GP = query-head rows per KV group, padded (4 / 8 / 16).
-template <typename T, int D, int GP>
-__global__ void __launch_bounds__(256) polar_decode_split_kernel(DecodeArgs a) {
+// GP = query-head rows per KV group, padded (4 / 8 / 16).  kAligned: page_size is a
+// multiple of the 32-key sub-block, so a sub-block lies in one page and each wave
+// reads its (at most 8) page ids once, up front; otherwise every key looks its page
+// up on its own.
+template <typename T, int D, int GP, bool kAligned>
+__global__ void __launch_bounds__(256, GP == 4 ? 2 : 1) polar_decode_split_kernel(DecodeArgs a) {
   constexpr bool kHalf = sizeof(T) == 2;
   constexpr int DCH = D / 8;        // lanes per key row in the PV pass (8 dims each)
   constexpr int KPI = 64 / DCH;     // keys per PV step
-  constexpr int QK_E = D / 4;       // elements of a K row per lane (one quarter)
-  __shared__ __attribute__((aligned(16))) float Ps[4][64][GP];
+  constexpr int SUBK = 32;          // keys per sub-block (two 16-key MFMA tiles)
+  constexpr int NT16 = SUBK / 16;   // 16-key tiles per sub-block
+  constexpr int NIT = SUBK / KPI;   // PV steps per sub-block
+  // A lane's 16-byte pieces of a q / K row: piece s of row quarter g holds elements
+  // (4 s + g) * EP ...; the four quarters of one load instruction then cover 64
+  // contiguous bytes of each key row (the dot product is order-free over dims).
+  constexpr int EP = 16 / (int)sizeof(T);
+  constexpr int KV = kHalf ? D / 32 : D / 16;  // 16-byte K loads per lane per 16-key tile
+  constexpr int VV = kHalf ? 1 : 2;            // 16-byte V loads per lane per key
+  __shared__ __attribute__((aligned(16))) float Ps[4][32][GP];
   __shared__ float Alpha[4][GP];
   __shared__ float Wst[4][GP][3];
   __shared__ __attribute__((aligned(16))) float Wacc[4][GP][D];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int bhk = blockIdx.x, sp = blockIdx.y;
   const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
   const int ctx = a.ctx[b];
@@ -92,19 +114,18 @@ __global__ void __launch_bounds__(256) polar_decode_split_kernel(DecodeArgs a) {
   if (t0 >= t1) return;  // uniform across the workgroup
 
   const int col = lane & 15, grp4 = lane >> 4;  // MFMA: key column, K-quarter / row group
-  // per-row (query head) calibration: rows 4*grp4 + i held by this lane
   float n_cal = (float)ctx;
   if (a.window > 0) n_cal = fminf(n_cal, (float)a.window);
   n_cal = fmaxf(n_cal, 1.f);
   const float logn = logf(n_cal);
+  // temperature of query head `col` (one softplus per lane), shuffled to the rows
+  // 4*grp4 + i this lane holds in the MFMA output layout
+  const float c1_col =
+      (1.f + softplus(a.len_gain_raw[hk * a.G + (col < a.G ? col : 0)]) * logn) * kLog2e *
+      (1.f / sqrtf((float)D));
   float c1r[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 4 * grp4 + i;
-    const int hq = hk * a.G + (row < a.G ? row : 0);
-    const float temp = 1.f + softplus(a.len_gain_raw[hq]) * logn;
-    c1r[i] = temp * kLog2e * (1.f / sqrtf((float)D));
-  }
+  for (int i = 0; i < 4; ++i) c1r[i] = __shfl(c1_col, (4 * grp4 + i) & 15, 64);
 
   // q operand (A of QK^T): row = head (lane & 15), quarter = lane >> 4
   u32x4 qa[kHalf ? D / 32 : 1];
@@ -113,14 +134,14 @@ __global__ void __launch_bounds__(256) polar_decode_split_kernel(DecodeArgs a) {
     const int row = col;
     const bool ok = row < a.G;
     const T* qp = (const T*)a.q + b * a.q_sb + (int64_t)(hk * a.G + (ok ? row : 0)) * a.q_sh +
-                  QK_E * grp4;
+                  EP * grp4;
     if constexpr (kHalf) {
 #pragma unroll
-      for (int s = 0; s < D / 32; ++s) qa[s] = ok ? *(const u32x4*)(qp + 8 * s) : u32x4{0, 0, 0, 0};
+      for (int s = 0; s < D / 32; ++s) qa[s] = ok ? *(const u32x4*)(qp + 4 * EP * s) : u32x4{0, 0, 0, 0};
     } else {
 #pragma unroll
       for (int s4 = 0; s4 < D / 16; ++s4) {
-        f32x4 x = ok ? *(const f32x4*)(qp + 4 * s4) : f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 x = ok ? *(const f32x4*)(qp + 4 * EP * s4) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int e = 0; e < 4; ++e) qf[4 * s4 + e] = x[e];
       }
@@ -131,7 +152,8 @@ __global__ void __launch_bounds__(256) polar_decode_split_kernel(DecodeArgs a) {
   const T* vc = (const T*)a.vc;
   const int32_t* btb = a.bt + (int64_t)b * a.bt_sb;
   const int64_t row_elems = (int64_t)a.Hkv * D;
-  // Offset of key `pos` in the cache (elements); ok=false for pages outside the table.
+  // Element offset of key `pos` in the cache.  Pages outside the table are clamped to
+  // page 0 (always a valid address) and reported through `ok`; callers zero them.
   auto key_off = [&](int pos, bool& ok) -> int64_t {
     const int lp = pos / a.page_size;
     int phys = (lp < a.max_pages) ? btb[lp] : -1;
@@ -139,8 +161,6 @@ __global__ void __launch_bounds__(256) polar_decode_split_kernel(DecodeArgs a) {
     if (!ok) phys = 0;
     return ((int64_t)phys * a.page_size + (pos - lp * a.page_size)) * row_elems + (int64_t)hk * D;
   };
-  // With 64-aligned sub-blocks and page_size % 64 == 0 a sub-block lies in one page.
-  const bool page_aligned = (a.page_size % 64) == 0;
 
   float m_run[4], l_part[4], q2_part[4];
 #pragma unroll
@@ -156,68 +176,152 @@ __global__ void __launch_bounds__(256) polar_decode_split_kernel(DecodeArgs a) {
     for (int e = 0; e < 8; ++e) acc[r][e] = 0.f;
 
   const int dch = lane % DCH, kg = lane / DCH;
-  for (int sb = (t0 & ~63) + 64 * wave; sb < t1; sb += 256) {
-    int64_t sb_off = 0;
-    bool sb_page_ok = true;
-    if (page_aligned) sb_off = key_off(sb, sb_page_ok);
-    // ---- S = Q K^T over four 16-key tiles
-    f32x4 sc[4];
-    bool kok[4];
+  // this wave's share of the span, walked in 32-key sub-blocks
+  const int w_lo = sp * kSplitTokens + kWaveTokens * wave;
+  const int sb_beg = max(w_lo, t0 & ~(SUBK - 1));
+  const int sb_end = min(w_lo + kWaveTokens, t1);
+  // Aligned pages: lane j holds the physical page of sub-block w_lo + 32 j (-1 past
+  // the context or the table), read out with v_readlane inside the loop, so no page
+  // lookup there waits on memory (a vector load feeding an address would make the
+  // wave drain every K/V load in flight at each sub-block).
+  int wave_pages = -1;
+  if constexpr (kAligned) {
+    const int pos = w_lo + SUBK * lane;
+    const int lp = pos / a.page_size;
+    if (lane < kWaveTokens / SUBK && pos < t1 && lp < a.max_pages) wave_pages = btb[lp];
+  }
+  // Aligned pages are read with buffer loads: the page is the buffer (base and size
+  // in scalar registers, size 0 for a page outside the pool so nothing is fetched),
+  // a lane keeps one 32-bit offset for its row / columns, and the sub-block's row
+  // within the page is a scalar offset.
+  const uint32_t row_bytes = (uint32_t)row_elems * sizeof(T);
+  const uint32_t page_bytes = (uint32_t)a.page_size * row_bytes;
+  const uint32_t head_b = (uint32_t)(hk * D * sizeof(T));
+  const uint32_t k_voff = col * row_bytes + head_b + (uint32_t)(EP * grp4 * sizeof(T));
+  const uint32_t v_voff = kg * row_bytes + head_b + (uint32_t)(8 * dch * sizeof(T));
+  const int np32 = (int)min(a.num_pages, (int64_t)0x7fffffff);
+  auto sub_page = [&](int sb, bool& ok) -> int64_t {
+    const int phys = __builtin_amdgcn_readlane(wave_pages, min((sb - w_lo) / SUBK, 63));
+    ok = (phys >= 0) & (phys < np32);
+    return ok ? (int64_t)phys * a.page_size * row_elems : 0;
+  };
+
+  // ---- K of one sub-block (16-key tiles: lane = key column x row quarter)
+  bool kok[NT16];
+  u32x4 kb[NT16][KV];
+  auto load_k = [&](int sb) {
+    if constexpr (kAligned) {
+      bool pg;
+      const int64_t pbase = sub_page(sb, pg);
+      const auto rs = buffer_rsrc(kc + pbase, pg ? page_bytes : 0u);
+      const uint32_t soff = (uint32_t)(sb % a.page_size) * row_bytes;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int pos = sb + 16 * j + col;
-      bool ok = pos >= t0 && pos < t1;
-      int64_t off = 0;
-      if (page_aligned) {
-        ok = ok && sb_page_ok;
-        off = sb_off + (int64_t)(16 * j + col) * row_elems;
-      } else if (ok) {
-        off = key_off(pos, ok);
+      for (int j = 0; j < NT16; ++j) {
+        const int pos = sb + 16 * j + col;
+        kok[j] = pg & (pos >= t0) & (pos < t1);
+#pragma unroll
+        for (int s = 0; s < KV; ++s)
+          kb[j][s] = buffer_load16(rs, k_voff + 64u * s, soff + 16u * j * row_bytes);
       }
-      kok[j] = ok;
-      const T* kr = kc + off + QK_E * grp4;
-      sc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if constexpr (kHalf) {
-        u32x4 kb[D / 32];
+    } else {
 #pragma unroll
-        for (int s = 0; s < D / 32; ++s) kb[s] = ok ? *(const u32x4*)(kr + 8 * s) : u32x4{0, 0, 0, 0};
+      for (int j = 0; j < NT16; ++j) {
+        const int pos = sb + 16 * j + col;
+        bool pok;
+        const int64_t off = key_off(pos, pok);
+        kok[j] = pok && pos >= t0 && pos < t1;
+        const T* kr = kc + off + EP * grp4;
 #pragma unroll
-        for (int s = 0; s < D / 32; ++s) sc[j] = mfma16x16x32<T>(qa[s], kb[s], sc[j]);
-      } else {
-        f32x4 kb[D / 16];
-#pragma unroll
-        for (int s4 = 0; s4 < D / 16; ++s4)
-          kb[s4] = ok ? *(const f32x4*)(kr + 4 * s4) : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s4 = 0; s4 < D / 16; ++s4)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            sc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4 + e], kb[s4][e], sc[j], 0, 0, 0);
+        for (int s = 0; s < KV; ++s) kb[j][s] = *(const u32x4*)(kr + 4 * EP * s);
       }
     }
+  };
+  // ---- V of one sub-block (lane = 8 dims x keys kg, kg + KPI, ...)
+  bool vok[NIT];
+  u32x4 vb[NIT][VV];
+  auto load_v = [&](int sb) {
+    if constexpr (kAligned) {
+      bool pg;
+      const int64_t pbase = sub_page(sb, pg);
+      const auto rs = buffer_rsrc(vc + pbase, pg ? page_bytes : 0u);
+      const uint32_t soff = (uint32_t)(sb % a.page_size) * row_bytes;
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        const int pos = sb + it * KPI + kg;
+        vok[it] = pg & (pos >= t0) & (pos < t1);
+#pragma unroll
+        for (int w = 0; w < VV; ++w)
+          vb[it][w] = buffer_load16(rs, v_voff + 16u * w, soff + (uint32_t)(it * KPI) * row_bytes);
+      }
+    } else {
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        const int pos = sb + it * KPI + kg;
+        bool pok;
+        const int64_t off = key_off(pos, pok);
+        vok[it] = pok && pos >= t0 && pos < t1;
+        const T* vr = vc + off + 8 * dch;
+#pragma unroll
+        for (int w = 0; w < VV; ++w) vb[it][w] = *(const u32x4*)(vr + 4 * w);
+      }
+    }
+  };
+
+  // K(sb + 32) is issued right after QK^T(sb) and V(sb + 32) right after PV(sb), so
+  // each has a whole sub-block of work to arrive behind
+  // (On aligned pages the loads are issued unconditionally: past the wave's range the
+  // page id is -1, the buffer is empty and nothing is fetched, and the compiler sees
+  // one fixed order of loads, so its waits stay partial.)
+  if (kAligned || sb_beg < sb_end) {
+    load_k(sb_beg);
+    load_v(sb_beg);
+  }
+  for (int sb = sb_beg; sb < sb_end; sb += SUBK) {
+    // ---- S = Q K^T over four 16-key tiles (rows = heads, columns = keys)
+    f32x4 sc[NT16];
+#pragma unroll
+    for (int j = 0; j < NT16; ++j) {
+      sc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (kHalf) {
+#pragma unroll
+        for (int s = 0; s < KV; ++s) sc[j] = mfma16x16x32<T>(qa[s], kb[j][s], sc[j]);
+      } else {
+#pragma unroll
+        for (int s4 = 0; s4 < KV; ++s4) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            sc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[4 * s4 + e], __uint_as_float(kb[j][s4][e]),
+                                                         sc[j], 0, 0, 0);
+        }
+      }
+    }
+    bool kok_cur[NT16];
+#pragma unroll
+    for (int j = 0; j < NT16; ++j) kok_cur[j] = kok[j];
+    const bool full = sb >= t0 && sb + SUBK <= t1 && vok[0] && vok[NIT - 1];
+    if (kAligned || sb + SUBK < sb_end) load_k(sb + SUBK);  // in flight during the softmax and PV
     // ---- online softmax; rows = heads 4*grp4+i, column key = sb + 16 j + col
     float alpha_r[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float mx = kSentinel;
+      float mx = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float x = kok[j] ? sc[j][i] * c1r[i] : kSentinel;
-        sc[j][i] = x;
-        mx = fmaxf(mx, x);
+      for (int j = 0; j < NT16; ++j) {
+        sc[j][i] = kok_cur[j] ? sc[j][i] : -INFINITY;
+        mx = fmaxf(mx, sc[j][i]);
       }
 #pragma unroll
       for (int m = 8; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
-      const float m_new = fmaxf(m_run[i], mx);
-      const float alpha = exp2f(m_run[i] - m_new);
+      const float m_new = fmaxf(m_run[i], mx * c1r[i]);
+      const float alpha = __builtin_amdgcn_exp2f(m_run[i] - m_new);
       m_run[i] = m_new;
       float ls = 0.f, qs = 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float p = kok[j] ? exp2f(sc[j][i] - m_new) : 0.f;
+      for (int j = 0; j < NT16; ++j) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(sc[j][i], c1r[i], -m_new));
         sc[j][i] = p;
         ls += p;
-        qs += p * p;
+        qs = fmaf(p, p, qs);
       }
       l_part[i] = l_part[i] * alpha + ls;
       q2_part[i] = q2_part[i] * alpha * alpha + qs;
@@ -225,16 +329,14 @@ __global__ void __launch_bounds__(256) polar_decode_split_kernel(DecodeArgs a) {
     }
     if (4 * grp4 < GP) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        *(f32x4*)&Ps[wave][16 * j + col][4 * grp4] = sc[j];
-      }
+      for (int j = 0; j < NT16; ++j) *(f32x4*)&Ps[wave][16 * j + col][4 * grp4] = sc[j];
       if (col == 0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) Alpha[wave][4 * grp4 + i] = alpha_r[i];
       }
     }
     wave_sync();
-    // ---- acc = acc * alpha + P V   (lane: dims 8*dch.., keys kg, kg+KPI, ...)
+    // ---- acc = acc * alpha + P V
     {
       float al[GP];
 #pragma unroll
@@ -244,34 +346,21 @@ __global__ void __launch_bounds__(256) polar_decode_split_kernel(DecodeArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[r][e] *= al[r];
     }
-#pragma unroll 4
-    for (int it = 0; it < 64 / KPI; ++it) {
-      const int kk = it * KPI + kg;
-      const int pos = sb + kk;
-      bool ok = pos >= t0 && pos < t1;
-      int64_t off = 0;
-      if (page_aligned) {
-        ok = ok && sb_page_ok;
-        off = sb_off + (int64_t)kk * row_elems;
-      } else if (ok) {
-        off = key_off(pos, ok);
-      }
-      float vv[8];
-      if (ok) {
-        const T* vr = vc + off + 8 * dch;
-        if constexpr (kHalf) {
-          unpack8(*(const u32x4*)vr, vv, T{});
-        } else {
-          f32x4 x0 = *(const f32x4*)vr, x1 = *(const f32x4*)(vr + 4);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            vv[e] = x0[e];
-            vv[4 + e] = x1[e];
-          }
-        }
+    for (int it = 0; it < NIT; ++it) {
+      const int kk = it * KPI + kg;
+      float vv[8];
+      if constexpr (kHalf) {
+        unpack8(vb[it][0], vv, T{});
       } else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) vv[e] = 0.f;
+        for (int w = 0; w < 2; ++w)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) vv[4 * w + e] = __uint_as_float(vb[it][w][e]);
+      }
+      if (!full) {  // masked rows (even NaN) never enter the sums
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vv[e] = vok[it] ? vv[e] : 0.f;
       }
 #pragma unroll
       for (int r4 = 0; r4 < GP / 4; ++r4) {
@@ -279,9 +368,10 @@ __global__ void __launch_bounds__(256) polar_decode_split_kernel(DecodeArgs a) {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr)
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[4 * r4 + rr][e] += p4[rr] * vv[e];
+          for (int e = 0; e < 8; ++e) acc[4 * r4 + rr][e] = fmaf(p4[rr], vv[e], acc[4 * r4 + rr][e]);
       }
     }
+    if (kAligned || sb + SUBK < sb_end) load_v(sb + SUBK);
     wave_sync();
   }
 
@@ -342,28 +432,62 @@ __global__ void __launch_bounds__(256) polar_decode_split_kernel(DecodeArgs a) {
   }
 }
 
+// One workgroup (256 threads) per (sequence, query head): combine the live spans.
+// Pass 1 finds the common max M over the spans' running maxima (one span per
+// thread, in parallel); pass 2 sums L, Q2 and the direction with factors
+// 2^(m_i - M), D threads per span group so the span records are read in parallel.
 template <typename T, int D>
-__global__ void __launch_bounds__(D) polar_decode_merge_kernel(DecodeArgs a) {
-  __shared__ float red[D / 64];
+__global__ void __launch_bounds__(256) polar_decode_merge_kernel(DecodeArgs a) {
+  constexpr int NG = 256 / D;  // span groups
+  __shared__ float red[4];
+  __shared__ float s_part[NG][D];
+  __shared__ float s_lq[NG][2];
   const int bh = blockIdx.x;
   const int b = bh / a.Hq, hq = bh % a.Hq;
-  const int d = threadIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ctx = a.ctx[b];
   const int lo = a.window > 0 ? max(ctx - a.window, 0) : 0;
   const int sp0 = lo / kSplitTokens;
   const int sp1 = min(ctx > lo ? (ctx + kSplitTokens - 1) / kSplitTokens : sp0, a.max_splits);
   const float* recs = a.ws + ((int64_t)b * a.Hq + hq) * a.max_splits * (D + 4);
-  float M = kSentinel, L = 0.f, Q2 = 0.f, S = 0.f;
-  for (int sp = sp0; sp < sp1; ++sp) {
+
+  float M = kSentinel;
+  for (int sp = sp0 + tid; sp < sp1; sp += 256) M = fmaxf(M, recs[(int64_t)sp * (D + 4)]);
+  M = wave_max(M);
+  if (lane == 0) red[wave] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+
+  const int grp = tid / D, d = tid % D;
+  float S = 0.f, L = 0.f, Q2 = 0.f;
+#pragma unroll 16
+  for (int sp = sp0 + grp; sp < sp1; sp += NG) {
     const float* rec = recs + (int64_t)sp * (D + 4);
-    const float mi = rec[0];
-    const float mn = fmaxf(M, mi);
-    const float fo = exp2f(M - mn), fi = exp2f(mi - mn);
-    L = L * fo + rec[1] * fi;
-    Q2 = Q2 * fo * fo + rec[2] * fi * fi;
-    S = S * fo + rec[4 + d] * fi;
-    M = mn;
+    const float f = exp2f(rec[0] - M);
+    S = fmaf(rec[4 + d], f, S);
+    if (d == 0) {
+      L = fmaf(rec[1], f, L);
+      Q2 = fmaf(rec[2], f * f, Q2);
+    }
   }
+  s_part[grp][d] = S;
+  if (d == 0) {
+    s_lq[grp][0] = L;
+    s_lq[grp][1] = Q2;
+  }
+  __syncthreads();
+  // every thread stays to the last barrier; only the first D (one per head dim) finish
+  const bool act = tid < D;
+  S = 0.f;
+  L = 0.f;
+  Q2 = 0.f;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    S += s_part[g][d];
+    L += s_lq[g][0];
+    Q2 += s_lq[g][1];
+  }
+
   float n_cal = (float)ctx;
   if (a.window > 0) n_cal = fminf(n_cal, (float)a.window);
   n_cal = fmaxf(n_cal, 1.f);
@@ -376,16 +500,17 @@ __global__ void __launch_bounds__(D) polar_decode_merge_kernel(DecodeArgs a) {
   Q2 *= al * al;
   const float pn = exp2f(an2 - mn);
   const float Z = L + pn;
-  const float s = S * al + pn * a.v_null[(int64_t)hq * D + d];
-  float ss = wave_sum(s * s);
-  if ((d & 63) == 0) red[d >> 6] = ss;
+  const float s = act ? S * al + pn * a.v_null[(int64_t)hq * D + d] : 0.f;
+  const float ss_w = wave_sum(s * s);
+  __syncthreads();  // red[] reused
+  if (lane == 0) red[wave] = ss_w;
   __syncthreads();
-  ss = 0.f;
+  float ss = 0.f;
 #pragma unroll
   for (int w = 0; w < D / 64; ++w) ss += red[w];
   const float inv = 1.f / fmaxf(sqrtf(ss), a.eps);
-  ((T*)a.c)[((int64_t)b * a.Hq + hq) * D + d] = (T)(s * inv);
-  if (d == 0) {
+  if (act) ((T*)a.c)[((int64_t)b * a.Hq + hq) * D + d] = (T)(s * inv);
+  if (tid == 0) {
     const float n_eff = L * L / fmaxf(Q2, 1e-30f);
     const float m_eff = n_eff * (L / fmaxf(Z, a.eps));
     const float beta = softplus(a.mag_beta_raw[hq]);
@@ -400,12 +525,15 @@ static int max_splits_for(int64_t max_pages, int64_t page_size) {
 template <typename T, int D, int GP>
 static int launch_decode(DecodeArgs a, hipStream_t s) {
   if (a.max_splits > 0) {
-    polar_decode_split_kernel<T, D, GP>
-        <<<dim3((unsigned)(a.B * a.Hkv), (unsigned)a.max_splits), dim3(256), 0, s>>>(a);
+    const dim3 grid((unsigned)(a.B * a.Hkv), (unsigned)a.max_splits);
+    if (a.page_size % 32 == 0)
+      polar_decode_split_kernel<T, D, GP, true><<<grid, dim3(256), 0, s>>>(a);
+    else
+      polar_decode_split_kernel<T, D, GP, false><<<grid, dim3(256), 0, s>>>(a);
     int rc = check_launch("polar_attention_decode(split)");
     if (rc) return rc;
   }
-  polar_decode_merge_kernel<T, D><<<dim3((unsigned)(a.B * a.Hq)), dim3(D), 0, s>>>(a);
+  polar_decode_merge_kernel<T, D><<<dim3((unsigned)(a.B * a.Hq)), dim3(256), 0, s>>>(a);
   return check_launch("polar_attention_decode(merge)");
 }
 
@@ -445,8 +573,8 @@ extern "C" int atma_polar_attention_decode(
   if (!q || !c || !mag || !context_lens || !v_null || !null_base || !null_slope_raw ||
       !len_gain_raw || !mag_beta_raw)
     return set_error(ATMA_ERR_INVALID, "polar_attention_decode: null pointer");
-  if (max_pages > 0 && (!k_cache || !v_cache || !block_tables))
-    return set_error(ATMA_ERR_INVALID, "polar_attention_decode: null cache pointer");
+  if (max_pages > 0 && (!k_cache || !v_cache || !block_tables || num_pages <= 0))
+    return set_error(ATMA_ERR_INVALID, "polar_attention_decode: empty or null cache");
   const int es = dtype_size(dtype);
   if (!es) return set_error(ATMA_ERR_INVALID, "polar_attention_decode: unknown dtype %d", dtype);
   if ((uintptr_t)q % 16 || (q_sb * es) % 16 || (q_sh * es) % 16 || (uintptr_t)k_cache % 16 ||
