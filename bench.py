@@ -260,6 +260,17 @@ def cpu_baseline(torch):
             "torch_threads": torch.get_num_threads(), "cpu_model": model}
 
 
+def copy_calibration(torch, dev, steps):
+    """A plain copy of known size (512 MiB read + 512 MiB written per launch): what
+    rocprofv3's FETCH_SIZE / WRITE_SIZE report for it, divided by the true byte counts,
+    gives the factors that turn those counters into HBM bytes for the kernels here."""
+    n = 512 << 20
+    src = torch.empty(n, dtype=torch.uint8, device=dev).random_(0, 255)
+    dst = torch.empty_like(src)
+    ms = _time(torch, lambda: dst.copy_(src), max(3, steps), 1)
+    return {"bytes_read": n, "bytes_written": n, "ms": ms, "gbs": 2 * n / (ms * 1e-3) / 1e9}
+
+
 def _traffic():
     """HBM bytes per Polar prefill launch measured with rocprofv3 --pmc (FETCH_SIZE +
     WRITE_SIZE, scaled by a copy-kernel calibration), committed under profiles/."""
@@ -275,7 +286,9 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["c2", "c3", "c4"], default=None)
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "copy"], default=None,
+                    help="one workload; 'copy' runs a plain 512 MiB device copy, the "
+                         "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-long", action="store_true", help="skip T=262,144")
     args = ap.parse_args(argv)
@@ -290,6 +303,10 @@ def main(argv=None):
     torch.backends.cuda.matmul.allow_tf32 = False
 
     out = {}
+    if args.only == "copy":
+        out["copy"] = copy_calibration(torch, dev, args.steps)
+        print(json.dumps(out))
+        return 0
     if args.only in (None, "c2"):
         c2 = bench_prefill(torch, dev, 8, 2048, args.steps, args.warmup)
         print(f"# c2 prefill: {json.dumps(c2)}", file=sys.stderr, flush=True)
