@@ -1,0 +1,340 @@
+"""The global-layer mixer as a PyTorch module: Polar attention + the Titans
+gated-delta memory, with the reference's parameter names and three routes.
+
+* ``forward(x)`` -- the causal full-sequence form of ``PolarAttention.forward``
+  (``model/reference.py:127-195``, memory ``model/blocks.py:463-490``).
+* ``prefill(x, cache, ...)`` -- the engine's dense fresh-prefill route
+  (``inference/models/atma.py:397-437``): writes the paged KV cache, the Canon conv
+  states and the memory state table.
+* ``decode(x, cache, ...)`` -- the engine's decode route
+  (``inference/models/atma.py:546-618``): one token per sequence against the paged
+  cache; conv / memory states advance in place.  Fixed shapes, no host sync:
+  graph capturable.
+
+The Polar and gated-delta arithmetic runs in the HIP kernels (``atma_amd.kernel``);
+projections, RMSNorm and the depthwise Canon conv stay eager, as in the reference.
+Unlike the reference, K/V reach the Polar kernels unexpanded (GQA is resolved
+in-kernel); the memory branch sees them expanded, as it does in the reference.
+With ``overlap=True`` the memory branch runs on a second HIP stream concurrently
+with Polar attention: the two only share their inputs.
+"""
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from ..kernel import (chunk_gated_delta_rule, gated_delta_decode_step, polar_attention_decode,
+                      polar_attention_fwd)
+from .attention import store_kvcache
+
+# Polar structural priors (model/reference.py:17-20)
+LEN_GAIN_INIT = -1.0
+NULL_SLOPE_INIT = 0.5
+NULL_BASE_INIT = 2.0
+MAG_BETA_INIT = -1.5
+
+
+class Linear(nn.Linear):
+    """``F.linear`` with weights cast to the input dtype (``model/reference.py:22-28``)."""
+
+    def forward(self, x):
+        return F.linear(x, self.weight.type_as(x), None if self.bias is None else self.bias.type_as(x))
+
+
+class TitansMemory(nn.Module):
+    """Gated-delta compression memory (``model/blocks.py:426-490``): retention
+    ``gamma = sigmoid(w_gamma x + 3.9)``, write strength ``beta = sigmoid(w_beta x + 0)``,
+    unit-normalised q/k in-kernel, readout RMS-normed per head, output-gated and
+    projected (``proj`` zero-initialised, so the branch starts as a no-op)."""
+
+    def __init__(self, dim, num_heads, head_dim, chunk=64, gamma_bias=3.9, beta_bias=0.0):
+        super().__init__()
+        self.H, self.dk, self.chunk = num_heads, head_dim, chunk
+        self.gamma_bias, self.beta_bias = gamma_bias, beta_bias
+        self.w_gamma = Linear(dim, num_heads)
+        self.w_beta = Linear(dim, num_heads)
+        self.gate = Linear(dim, num_heads * head_dim)
+        self.proj = Linear(num_heads * head_dim, dim)
+        nn.init.zeros_(self.proj.weight)
+        nn.init.zeros_(self.proj.bias)
+
+    def logits(self, x):
+        return (self.w_gamma(x).float() + self.gamma_bias, self.w_beta(x).float() + self.beta_bias)
+
+    def _out(self, x, r):
+        lead = r.shape[:-2]
+        r = F.rms_norm(r, (self.dk,)).reshape(*lead, self.H * self.dk).to(x.dtype)
+        return self.proj(r * torch.sigmoid(self.gate(x)))
+
+    def forward(self, x, q, k, v, initial_state=None, output_final_state=False):
+        """x: (B, T, dim); q, k, v: (B, T, H, dk) (KV expanded).  initial_state:
+        ``[K, V]`` (B, H, dk, dv) fp32 or None.  Returns (out (B, T, dim), final
+        state or None) -- ``_mem_prefill_dense`` (``inference/models/atma.py:305-339``)."""
+        g_logit, b_logit = self.logits(x)
+        r, S = chunk_gated_delta_rule(q, k, v, F.logsigmoid(g_logit), torch.sigmoid(b_logit), scale=1.0,
+                                      initial_state=initial_state,
+                                      output_final_state=output_final_state,
+                                      use_qk_l2norm_in_kernel=True)
+        return self._out(x, r), S
+
+    def step(self, x, q, k, v, state_table, slots):
+        """One decode step, state table advanced in place (``_mem_decode``,
+        ``inference/models/atma.py:341-375``).  x: (B, dim); q, k, v: (B, H, dk)."""
+        g_logit, b_logit = self.logits(x)
+        r = gated_delta_decode_step(q, k, v, torch.sigmoid(g_logit), torch.sigmoid(b_logit),
+                                    state_table, slots)
+        return self._out(x, r)
+
+
+@dataclass
+class GlobalLayerCache:
+    """Per-layer engine state (``inference/engine/model_runner.py:176-193``):
+    paged K/V ``(num_pages, page_size, Hkv, d)``, Canon conv tails
+    ``(max_seqs, channels, kernel_size - 1)`` for q / k / v, and the memory table
+    ``(max_seqs, H, dk, dv)`` fp32 ``[K, V]``."""
+    k_cache: torch.Tensor
+    v_cache: torch.Tensor
+    conv_q: torch.Tensor
+    conv_k: torch.Tensor
+    conv_v: torch.Tensor
+    mem_table: Optional[torch.Tensor] = None
+
+    @staticmethod
+    def allocate(layer, num_pages, page_size, max_seqs, device, dtype):
+        H, Hkv, dk, K = layer.num_heads, layer.num_kv_heads, layer.head_dim, layer.kernel_size
+        z = lambda *s, dt=dtype: torch.zeros(*s, device=device, dtype=dt)  # noqa: E731
+        return GlobalLayerCache(
+            k_cache=z(num_pages, page_size, Hkv, dk), v_cache=z(num_pages, page_size, Hkv, dk),
+            conv_q=z(max_seqs, H * dk, K - 1), conv_k=z(max_seqs, Hkv * dk, K - 1),
+            conv_v=z(max_seqs, Hkv * dk, K - 1),
+            mem_table=z(max_seqs, H, dk, dk, dt=torch.float32) if layer.mem is not None else None)
+
+
+class PolarAttention(nn.Module):
+    """ATMA's global-layer mixer.  Parameters are registered in the reference's order
+    (``model/blocks.py:511-529``, then ``model/reference.py:113-125``) so state dicts
+    line up: q, k, v, canon_q, canon_k, canon_v, proj, mu_proj, v_null, null_base,
+    null_slope_raw, len_gain_raw, mag_beta_raw, mem.*"""
+
+    def __init__(self, dim, head_dim=128, num_kv_heads=None, kernel_size=4, window=None,
+                 mem_enabled=True, mem_chunk=64, mem_gamma_bias=3.9, mem_beta_bias=0.0,
+                 num_heads=None, overlap=True):
+        super().__init__()
+        self.num_heads = num_heads if num_heads is not None else dim // head_dim
+        self.num_kv_heads = num_kv_heads if num_kv_heads is not None else self.num_heads // 4
+        self.head_dim = head_dim
+        self.kernel_size = kernel_size
+        H, Hkv, dk = self.num_heads, self.num_kv_heads, head_dim
+        hd, kvd = H * dk, Hkv * dk
+        self.q = Linear(dim, 2 * hd)
+        self.k = Linear(dim, kvd)
+        self.v = Linear(dim, kvd)
+        self.canon_q = nn.Conv1d(hd, hd, kernel_size, padding=kernel_size - 1, groups=hd, bias=False)
+        self.canon_k = nn.Conv1d(kvd, kvd, kernel_size, padding=kernel_size - 1, groups=kvd, bias=False)
+        self.canon_v = nn.Conv1d(kvd, kvd, kernel_size, padding=kernel_size - 1, groups=kvd, bias=False)
+        self.proj = Linear(hd, dim)
+        self.window = window
+        self.mu_proj = Linear(H, dim)
+        self.v_null = nn.Parameter(torch.zeros(H, dk))
+        self.null_base = nn.Parameter(torch.full((H,), NULL_BASE_INIT))
+        self.null_slope_raw = nn.Parameter(torch.full((H,), NULL_SLOPE_INIT))
+        self.len_gain_raw = nn.Parameter(torch.full((H,), LEN_GAIN_INIT))
+        self.mag_beta_raw = nn.Parameter(torch.full((H,), MAG_BETA_INIT))
+        self.mem = (TitansMemory(dim, H, dk, chunk=mem_chunk, gamma_bias=mem_gamma_bias,
+                                 beta_bias=mem_beta_bias) if mem_enabled else None)
+        self.overlap = overlap
+        self._side = {}
+
+    # ------------------------------------------------------------------ pieces
+    def polar_params(self):
+        return dict(v_null=self.v_null, null_base=self.null_base, null_slope_raw=self.null_slope_raw,
+                    len_gain_raw=self.len_gain_raw, mag_beta_raw=self.mag_beta_raw)
+
+    def _project(self, x):
+        """q/gate, k, v projections and per-head RMSNorm of q, k (``model/reference.py:131-139``).
+        x: (..., dim) -> q (..., H, dk), gate (..., H*dk), k, v (..., Hkv, dk)."""
+        lead = x.shape[:-1]
+        H, Hkv, dk = self.num_heads, self.num_kv_heads, self.head_dim
+        q, gate = torch.chunk(self.q(x).view(*lead, H, 2 * dk), 2, dim=-1)
+        k = self.k(x).view(*lead, Hkv, dk)
+        v = self.v(x).view(*lead, Hkv, dk)
+        return F.rms_norm(q, (dk,)), gate.reshape(*lead, H * dk), F.rms_norm(k, (dk,)), v
+
+    @staticmethod
+    def _conv_prefill(t, conv, tails=None, slots=None):
+        """Residual causal depthwise conv over (B, T, C); optionally stores the last K-1
+        inputs per sequence (``prefill_causal_conv1d_dense``, ``inference/models/atma.py:148-162``)."""
+        w = conv.weight
+        K = w.shape[-1]
+        x_in = t.transpose(1, 2)
+        padded = F.pad(x_in, (K - 1, 0))
+        out = F.conv1d(padded, w.to(t.dtype), groups=x_in.shape[1])
+        if tails is not None:
+            tails[slots] = padded[:, :, padded.shape[2] - (K - 1):].to(tails.dtype)
+        return t + out.transpose(1, 2)
+
+    @staticmethod
+    def _conv_step(t, conv, tails, slots):
+        """Residual conv for one new token per sequence, tails advanced in place
+        (``_gpu_conv_step``, ``inference/models/atma.py:165-192``).  t: (B, C)."""
+        w = conv.weight.squeeze(1).to(t.dtype)           # (C, K)
+        st = tails[slots].to(t.dtype)                    # (B, C, K-1)
+        out = (st * w[:, :-1]).sum(-1) + t * w[:, -1]
+        tails[slots] = torch.cat([st[:, :, 1:], t.unsqueeze(-1)], dim=-1).to(tails.dtype)
+        return t + out
+
+    def _combine(self, c, mag, gate):
+        """``proj(c * sigmoid(gate)) + mu_proj(mag)`` (``inference/models/atma.py:246-252``).
+        c: (..., H, dk), mag: (..., H), gate: (..., H*dk)."""
+        lead = c.shape[:-2]
+        c_flat = c.reshape(*lead, self.num_heads * self.head_dim)
+        return self.proj(c_flat * torch.sigmoid(gate)) + self.mu_proj(mag.to(c.dtype))
+
+    def _side_stream(self, device):
+        s = self._side.get(device)
+        if s is None:
+            s = self._side[device] = torch.cuda.Stream(device=device)  # default priority
+        return s
+
+    def _with_memory(self, polar_fn, mem_fn, inputs):
+        """Run the Polar part on the current stream and the memory branch, concurrently
+        on a side stream when ``overlap`` is set; return (polar result, memory result)."""
+        if self.mem is None:
+            return polar_fn(), None
+        if not self.overlap or not inputs[0].is_cuda or torch.cuda.is_current_stream_capturing():
+            return polar_fn(), mem_fn()
+        main = torch.cuda.current_stream(inputs[0].device)
+        side = self._side_stream(inputs[0].device)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            m = mem_fn()
+        p = polar_fn()
+        main.wait_stream(side)
+        for t in inputs:
+            t.record_stream(side)
+        for t in (m if isinstance(m, tuple) else (m,)):
+            if isinstance(t, torch.Tensor):
+                t.record_stream(main)
+        return p, m
+
+    # ------------------------------------------------------------------ routes
+    def forward(self, x):
+        """Causal full-sequence mixer (``model/reference.py:127-195``): x (B, T, dim)."""
+        B, T, _ = x.shape
+        H, Hkv, dk = self.num_heads, self.num_kv_heads, self.head_dim
+        q, gate, k, v = self._project(x)
+        q = self._conv_prefill(q.reshape(B, T, H * dk), self.canon_q).view(B, T, H, dk)
+        k = self._conv_prefill(k.reshape(B, T, Hkv * dk), self.canon_k).view(B, T, Hkv, dk)
+        v = self._conv_prefill(v.reshape(B, T, Hkv * dk), self.canon_v).view(B, T, Hkv, dk)
+        return self._attend_prefill(x, q, gate, k, v, None, None)
+
+    def _attend_prefill(self, x, q, gate, k, v, S0, final_sink):
+        B, T = q.shape[:2]
+        g = self.num_heads // self.num_kv_heads
+        n_keys = torch.arange(1, T + 1, device=x.device, dtype=torch.float32)
+        qh, kh, vh = (t.transpose(1, 2) for t in (q, k, v))   # (B, heads, T, dk) views
+
+        def polar():
+            c, mag = polar_attention_fwd(qh, kh, vh, n_keys, is_causal=True, window=self.window,
+                                         **self.polar_params())
+            return self._combine(c.transpose(1, 2), mag.transpose(1, 2), gate)
+
+        def memory():
+            km = k.repeat_interleave(g, dim=2)
+            vm = v.repeat_interleave(g, dim=2)
+            return self.mem(x, q, km, vm, initial_state=S0, output_final_state=final_sink is not None)
+
+        out, m = self._with_memory(polar, memory, (x, q, k, v))
+        if m is not None:
+            out = out + m[0]
+            if final_sink is not None:
+                final_sink(m[1])
+        return out
+
+    def prefill(self, x, cache: GlobalLayerCache, slots, slot_mapping):
+        """Dense fresh prefill of B equal-length sequences (``inference/models/atma.py:397-437``).
+
+        x: (B, T, dim); slots: (B,) int64 rows of the conv / memory tables;
+        slot_mapping: (B*T,) int32 cache slots of every token (-1 = skip)."""
+        B, T, _ = x.shape
+        H, Hkv, dk = self.num_heads, self.num_kv_heads, self.head_dim
+        q, gate, k, v = self._project(x)
+        q = self._conv_prefill(q.reshape(B, T, H * dk), self.canon_q, cache.conv_q, slots).view(B, T, H, dk)
+        k = self._conv_prefill(k.reshape(B, T, Hkv * dk), self.canon_k, cache.conv_k, slots).view(B, T, Hkv, dk)
+        v = self._conv_prefill(v.reshape(B, T, Hkv * dk), self.canon_v, cache.conv_v, slots).view(B, T, Hkv, dk)
+        store_kvcache(k.reshape(B * T, Hkv, dk), v.reshape(B * T, Hkv, dk), cache.k_cache, cache.v_cache,
+                      slot_mapping)
+        S0 = cache.mem_table[slots] if self.mem is not None else None
+
+        def sink(S):
+            cache.mem_table[slots] = S
+
+        return self._attend_prefill(x, q, gate, k, v, S0, sink)
+
+    def decode(self, x, cache: GlobalLayerCache, slots, block_tables, context_lens, slot_mapping):
+        """One token per sequence (``inference/models/atma.py:546-618``).
+
+        x: (B, dim); slots: (B,) int64 table rows; block_tables: (B, max_pages) int32;
+        context_lens: (B,) int32 including this token; slot_mapping: (B,) int32."""
+        H, Hkv, dk = self.num_heads, self.num_kv_heads, self.head_dim
+        Bn = x.shape[0]
+        q, gate, k, v = self._project(x)
+        q = self._conv_step(q.reshape(Bn, H * dk), self.canon_q, cache.conv_q, slots).view(Bn, H, dk)
+        k = self._conv_step(k.reshape(Bn, Hkv * dk), self.canon_k, cache.conv_k, slots).view(Bn, Hkv, dk)
+        v = self._conv_step(v.reshape(Bn, Hkv * dk), self.canon_v, cache.conv_v, slots).view(Bn, Hkv, dk)
+        store_kvcache(k, v, cache.k_cache, cache.v_cache, slot_mapping)
+        c, mag = polar_attention_decode(q, cache.k_cache, cache.v_cache, block_tables, context_lens,
+                                        window=self.window, **self.polar_params())
+        out = self._combine(c, mag, gate)
+        if self.mem is not None:
+            g = H // Hkv
+            out = out + self.mem.step(x, q, k.repeat_interleave(g, dim=1), v.repeat_interleave(g, dim=1),
+                                      cache.mem_table, slots)
+        return out
+
+
+class RMSNorm(nn.Module):
+    """``model/layers.py:6-16``."""
+
+    def __init__(self, dim, eps=1e-6):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x):
+        return F.rms_norm(x, (x.size(-1),), weight=self.weight.type_as(x), eps=self.eps)
+
+
+class MLP(nn.Module):
+    """Squared-ReLU gated MLP (``model/layers.py:19-31``)."""
+
+    def __init__(self, dim):
+        super().__init__()
+        self.fc = Linear(dim, 8 * dim)
+        self.proj = Linear(4 * dim, dim)
+
+    def forward(self, x):
+        a, gate = torch.chunk(self.fc(x), 2, dim=-1)
+        return self.proj(gate * a.relu().square())
+
+
+class GlobalBlock(nn.Module):
+    """Pre-norm global block (``model/reference.py:198-229`` with attention=True):
+    ``x + attn(norm1 x)``, then ``x + mlp(norm2 x)``."""
+
+    def __init__(self, dim, head_dim=128, num_kv_heads=None, attn_kernel_size=4, window=None,
+                 mem_enabled=True, mem_chunk=64, overlap=True):
+        super().__init__()
+        self.attn = PolarAttention(dim, head_dim=head_dim, num_kv_heads=num_kv_heads,
+                                   kernel_size=attn_kernel_size, window=window, mem_enabled=mem_enabled,
+                                   mem_chunk=mem_chunk, overlap=overlap)
+        self.mlp = MLP(dim)
+        self.norm1 = RMSNorm(dim)
+        self.norm2 = RMSNorm(dim)
+
+    def forward(self, x):
+        x = x + self.attn(self.norm1(x))
+        return x + self.mlp(self.norm2(x))

@@ -1,0 +1,98 @@
+"""The global-layer module on the GPU (HIP kernels + eager glue) against the CPU
+oracle of ``PolarAttention.forward`` / ``Block.forward``, and the engine routes
+(dense prefill into the paged cache + decode steps) against the full-sequence forward."""
+
+import pytest
+import torch
+
+from oracle import block as OB
+from tests.helpers import max_abs, rel_err
+
+pytestmark = pytest.mark.gpu
+
+DIM, DK = 256, 64          # 4 query heads, 1 KV head (GQA 4:1, as the 1024 / 128 model)
+H, HKV = DIM // DK, DIM // DK // 4
+
+
+def _block(window=None, seed=0, overlap=True):
+    from atma_amd.layers.global_attention import GlobalBlock
+    torch.manual_seed(seed)
+    blk = GlobalBlock(DIM, head_dim=DK, window=window, overlap=overlap)
+    with torch.no_grad():   # every parameter N(0, 0.02), the reference's test convention
+        for n, p in blk.named_parameters():
+            if not n.startswith("norm"):
+                p.normal_(0.0, 0.02)
+            if n in ("attn.null_base", "attn.mag_beta_raw"):
+                p.normal_(0.0, 1.0)
+    return blk
+
+
+def _attn_sd(blk):
+    return {k[5:]: v.detach().cpu().clone() for k, v in blk.state_dict().items() if k.startswith("attn.")}
+
+
+@pytest.mark.parametrize("window", [None, 48])
+def test_mixer_fp32_vs_oracle(dev, window):
+    blk = _block(window=window)
+    x = torch.randn(2, 150, DIM, generator=torch.Generator().manual_seed(1))
+    ref = OB.polar_attention(_attn_sd(blk), x, H=H, Hkv=HKV, dk=DK, window=window)
+    out = blk.attn.to(dev)(x.to(dev))
+    assert max_abs(out, ref) <= 1e-4, max_abs(out, ref)
+
+
+def test_block_fp32_vs_oracle(dev):
+    blk = _block()
+    x = torch.randn(1, 200, DIM, generator=torch.Generator().manual_seed(2))
+    sd = {k: v.detach().cpu().clone() for k, v in blk.state_dict().items()}
+    ref = OB.global_block(sd, x, H=H, Hkv=HKV, dk=DK)
+    out = blk.to(dev)(x.to(dev))
+    assert max_abs(out, ref) <= 1e-4, max_abs(out, ref)
+
+
+def test_mixer_bf16_vs_fp32_oracle(dev):
+    blk = _block()
+    x = torch.randn(2, 130, DIM, generator=torch.Generator().manual_seed(3))
+    ref = OB.polar_attention(_attn_sd(blk), x, H=H, Hkv=HKV, dk=DK)
+    out = blk.attn.to(dev, torch.bfloat16)(x.to(dev, torch.bfloat16))
+    assert rel_err(out.float(), ref) <= 2e-2, rel_err(out.float(), ref)
+
+
+def test_side_stream_overlap_is_bitwise_neutral(dev):
+    a = _block(overlap=True).attn.to(dev)
+    b = _block(overlap=False).attn.to(dev)
+    x = torch.randn(2, 96, DIM, device=dev)
+    assert torch.equal(a(x), b(x))
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+def test_prefill_then_decode_equals_full_forward(dev, dtype, tol):
+    """Dense prefill of T0 tokens (paged KV + conv tails + memory table written), then
+    n decode steps through the paged cache, reproduce rows T0..T0+n-1 of the causal
+    full-sequence forward (inference/models/atma.py:397-437,546-618)."""
+    from atma_amd.layers.global_attention import GlobalLayerCache
+    attn = _block().attn.to(dev, dtype)
+    B, T0, n, page = 3, 70, 6, 16
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(B, T0 + n, DIM, generator=g).to(dev, dtype)
+    full = attn(x)
+
+    max_pages = (T0 + n + page - 1) // page
+    num_pages = B * max_pages + 5
+    cache = GlobalLayerCache.allocate(attn, num_pages, page, max_seqs=B + 2, device=dev, dtype=dtype)
+    perm = torch.randperm(num_pages, generator=g)[:B * max_pages].view(B, max_pages).int()
+    bt = perm.to(dev)
+    slots = torch.tensor([2, 0, 4], device=dev)   # table rows, deliberately not 0..B-1
+
+    def slot_of(b, pos):
+        return int(perm[b, pos // page]) * page + pos % page
+
+    smap = torch.tensor([slot_of(b, t) for b in range(B) for t in range(T0)], dtype=torch.int32, device=dev)
+    pre = attn.prefill(x[:, :T0], cache, slots, smap)
+    assert rel_err(pre.float(), full[:, :T0].float()) <= tol
+    for i in range(n):
+        pos = T0 + i
+        smap1 = torch.tensor([slot_of(b, pos) for b in range(B)], dtype=torch.int32, device=dev)
+        ctx = torch.full((B,), pos + 1, dtype=torch.int32, device=dev)
+        y = attn.decode(x[:, pos], cache, slots, bt, ctx, smap1)
+        err = max_abs(y, full[:, pos]) if dtype == torch.float32 else rel_err(y.float(), full[:, pos].float())
+        assert err <= tol, (i, err)
