@@ -85,6 +85,12 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
+template <typename T>
+__device__ __forceinline__ void buffer_store16b(__amdgpu_buffer_rsrc_t r, uint32_t voff, T x) {
+  static_assert(sizeof(T) == 2, "16-bit element");
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, x), r, voff, 0, 0);
+}
+
 // Direct global->LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane i's
 // bytes land at lds_wave_base + 16*i.  Issued through inline asm so the compiler does
 // not serialise later LDS reads behind it; completion is tracked by vmcnt, so the

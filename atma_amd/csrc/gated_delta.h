@@ -26,9 +26,37 @@ struct GdnArgs {
   void* ws;
 };
 
-// Per-chunk record of the 16-bit path: T*diag(beta) and Rq as 64x64 16-bit matrices
-// (zero above the diagonal), then the 64 inclusive log-decays (fp32).
-constexpr int64_t kGdn16RecBytes = 2 * kChunk * kChunk * 2 + kChunk * 4;
+// Workspace of the 16-bit path: for each of the n = B*H*NC (sequence, head, chunk)
+// records, these fields, each stored as its own array [n][...] so that consecutive
+// chunks of one head are adjacent in memory (element offsets in 16-bit units; C = 64
+// tokens, D = head dim):
+//   w   [C][D]  T diag(beta * ge) Kn      (the state's pull on each row's update)
+//   qn  [C][D]  normalised, scaled queries
+//   kdT [D][C]  (diag(exp(lg_C - lg)) Kn)^T   (write-back operand of the state update)
+//   us  [D/32][4][64][8]  u = T diag(beta) V in the scan's register order: for column
+//               slab s, wave w, lane l = 16 g + c, entries vt*4 + i hold u at token
+//               16 w + 4 g + i, column 32 s + 16 vt + c (one 16-byte load per lane)
+//   unT [D][C]  U^T = (u - w S)^T; written by the scan
+//   rq  [C][C]  exp(lg_p - lg_s) qn_p . kn_s for s <= p, else 0
+//   sT  [D][D]  the state entering the chunk, transposed ([v][k]); written by the scan
+//   lg  [C]     the inclusive log-decays (fp32; lg_byte is a byte offset)
+// T = (I + A)^-1 with A[p,s] = beta_p exp(lg_p - lg_s) kn_p . kn_s (s < p), ge_p = exp(lg_p).
+struct Gdn16Ws {
+  int D;
+  int64_t n;
+  __host__ __device__ constexpr int64_t cd() const { return (int64_t)kChunk * D; }
+  __host__ __device__ constexpr int64_t w(int64_t i) const { return i * cd(); }
+  __host__ __device__ constexpr int64_t qn(int64_t i) const { return (n + i) * cd(); }
+  __host__ __device__ constexpr int64_t kdT(int64_t i) const { return (2 * n + i) * cd(); }
+  __host__ __device__ constexpr int64_t us(int64_t i) const { return (3 * n + i) * cd(); }
+  __host__ __device__ constexpr int64_t unT(int64_t i) const { return (4 * n + i) * cd(); }
+  __host__ __device__ constexpr int64_t rq(int64_t i) const { return 5 * n * cd() + i * kChunk * kChunk; }
+  __host__ __device__ constexpr int64_t sT(int64_t i) const {
+    return 5 * n * cd() + n * kChunk * kChunk + i * (int64_t)D * D;
+  }
+  __host__ __device__ constexpr int64_t lg_byte(int64_t i) const { return sT(n) * 2 + i * kChunk * 4; }
+  __host__ __device__ constexpr int64_t bytes() const { return lg_byte(n); }
+};
 
 int launch_gdn16(const GdnArgs& a, int dtype, int D, hipStream_t stream);
 

@@ -329,7 +329,8 @@ extern "C" size_t atma_chunk_gated_delta_workspace_bytes(int64_t B, int64_t T, i
   (void)dv;
   if (B <= 0 || T <= 0 || H <= 0 || chunk != atma::kChunk || (dk != 64 && dk != 128)) return 0;
   const int64_t nc = (T + chunk - 1) / chunk;
-  if (dtype == ATMA_BF16 || dtype == ATMA_F16) return (size_t)(B * H * nc) * atma::kGdn16RecBytes;
+  if (dtype == ATMA_BF16 || dtype == ATMA_F16)
+    return (size_t)atma::Gdn16Ws{(int)dk, B * H * nc}.bytes();
   const int64_t rec = 5 * chunk * dk + 4;
   return (size_t)(B * H * nc * rec) * sizeof(float);
 }
@@ -359,6 +360,8 @@ extern "C" int atma_chunk_gated_delta_rule(
   }
   if (!q || !k || !v || !g || !beta || !o)
     return set_error(ATMA_ERR_INVALID, "chunk_gated_delta_rule: null pointer");
+  if (es == 2 && T * H * dk * 2 >= (1ll << 32))  // one sequence's output rows form one buffer
+    return set_error(ATMA_ERR_UNSUPPORTED, "chunk_gated_delta_rule: T*H*d too large for one sequence");
   const size_t need = atma_chunk_gated_delta_workspace_bytes(B, T, H, dk, dv, chunk, dtype);
   if (!workspace || workspace_bytes < need)
     return set_error(ATMA_ERR_WORKSPACE, "chunk_gated_delta_rule: workspace %zu < %zu bytes",

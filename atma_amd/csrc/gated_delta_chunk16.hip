@@ -1,90 +1,120 @@
 // Chunked gated-delta prefill for bf16 / fp16 inputs on MFMA (v_mfma_f32_16x16x32).
 //
-// Same algebra as the fp32 path (gated_delta_chunk.hip, after gated_delta_chunked,
-// model/blocks.py:375-423), split so the sequential part is short:
+// Algebra of gated_delta_chunked (model/blocks.py:375-423; FLA convention: decay
+// first, undecayed write, self-inclusive readout).  Inside a 64-token chunk with
+// inclusive log-decays lg_p, ge_p = exp(lg_p), A[p,s] = beta_p exp(lg_p - lg_s)
+// kn_p.kn_s (s < p) and T = (I + A)^-1, the carried state S ([K, V]) gives
+//     U = T diag(beta) V - T diag(beta ge) Kn S  =  u - w S
+//     O = diag(ge) Qn S + Rq U,          Rq[p,s] = exp(lg_p - lg_s) qn_p.kn_s (s <= p)
+//     S <- exp(lg_C) S + (diag(exp(lg_C - lg)) Kn)^T U
+// Everything that does not depend on S is computed chunk-parallel, so the
+// sequential pass only runs two dependent products per chunk:
 //
-//  pass 1, gdn_prep16 -- one workgroup per (sequence, head, chunk), fully parallel:
-//    L2-normalise the chunk's q/k rows, form the Gram blocks K K^T and Q K^T on
-//    MFMA, build A[p,s] = beta_p exp(lg_p - lg_s) k_p.k_s (s < p) and
-//    Rq[p,s] = exp(lg_p - lg_s) q_p.k_s (s <= p), invert the unit lower-triangular
-//    I + A in fp32 by 16x16 blocks (forward substitution on the diagonal blocks,
-//    then three levels of block products), and store T diag(beta) and Rq as 16-bit
-//    64x64 matrices plus the chunk's inclusive log-decays (16.6 KB per chunk).
+//  pass 1, gdn_prep16 -- one workgroup per (sequence, head, chunk): L2-normalise the
+//    rows, Gram blocks Kn Kn^T and Qn Kn^T on MFMA, T by a blocked fp32 inverse
+//    (forward substitution on the 16x16 diagonal blocks, then three levels of block
+//    products), then w = T (beta ge Kn) and u = T (beta V) on MFMA.  Writes the
+//    per-chunk record (w, qn, kdT, u, rq in 16 bits; lg in fp32).
 //
 //  pass 2, gdn_scan16 -- one workgroup per (sequence, head, 32-column slab of the
-//    [K, V] state), chunks in order.  The 128 x 32 fp32 slab lives in MFMA
-//    accumulator registers for the whole sequence (a 16-bit copy in LDS feeds the
-//    B operands).  Per chunk, with ge_p = exp(lg_p), tail_p = exp(lg_C - lg_p):
-//        X = V - diag(ge) K S          (K: normalised keys)
-//        U = (T diag(beta)) X
-//        O = diag(ge) Q S + Rq U       -> output rows
-//        S = exp(lg_C) S + (diag(tail) K)^T U
-//    The products run on 16-bit MFMA with fp32 accumulation (the state itself stays
-//    fp32); the next chunk's rows are prefetched into registers during the math.
+//    [K, V] state), chunks in order.  The 128 x 32 fp32 slab stays in VGPRs; a 16-bit
+//    copy in LDS feeds the B operands.  Per chunk: U = u - w S, U^T to LDS, then
+//    S <- gC S + kdT U: two dependent products and two workgroup barriers.  The
+//    operands of the next three chunks are in flight into registers (A fragments
+//    straight from memory) during the math; the 16-bit state entering each chunk and
+//    U^T go to the record.
+//
+//  pass 3, gdn_out16 -- chunk-parallel again: O = diag(ge) Qn S_c + Rq U_c.
 #include "gated_delta.h"
 
 namespace atma {
 
 __device__ __forceinline__ u32x4 lds16(const void* p) { return *(const u32x4*)p; }
 
+template <typename T>
+__device__ __forceinline__ u32x4 scale8(const u32x4& x, float f) {
+  u32x4 o;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) o[w] = pack2<T>(elem16<T>(x, 2 * w) * f, elem16<T>(x, 2 * w + 1) * f);
+  return o;
+}
+
+// (tp, ts) of the 6 strictly-upper 16x16 blocks of a 64x64 matrix, blk = 0..5
+__device__ __forceinline__ void upper_block(int blk, int& tp, int& ts) {
+  tp = blk < 3 ? 0 : (blk < 5 ? 1 : 2);
+  ts = blk < 3 ? blk + 1 : (blk < 5 ? blk - 1 : 3);
+}
+
 template <typename T, int D>
-__global__ void __launch_bounds__(256) gdn_prep16_kernel(GdnArgs a) {
-  constexpr int C = kChunk, KP = D + 8, FP = C + 1;
-  constexpr int EPT = D / 4, VPT = EPT / 8;  // 4 threads per row
-  __shared__ __attribute__((aligned(16))) T Kn[C * KP];
-  __shared__ __attribute__((aligned(16))) T Qn[C * KP];
-  __shared__ float Af[C * FP], Tf[C * FP], Rf[C * FP];
+__global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
+  constexpr int C = kChunk, KP = D + 8, CP = C + 8, FP = C + 1;
+  constexpr int DC = D / 8;           // 16-byte chunks per row
+  constexpr int NE = (C / 4) * DC;    // (4 tokens x 8 dims) groups
+  constexpr int RB = (C * KP > D * CP) ? C * KP : D * CP;
+  __shared__ __attribute__((aligned(16))) T R1[RB];  // Kn rows, then (beta ge Kn)^T
+  __shared__ __attribute__((aligned(16))) T R2[RB];  // Qn rows, then (beta V)^T
+  __shared__ float Af[C * FP], Tf[C * FP];
   __shared__ float Yf[3 * 256];
-  __shared__ float lg[C], bet[C];
+  __shared__ float lg[C], bet[C], sge[C], stl[C];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, g = lane >> 4;
   const int c = blockIdx.x, bh = blockIdx.y;
   const int b = bh / a.H, h = bh % a.H;
   const int t0 = c * C;
+  const Gdn16Ws W{D, (int64_t)a.B * a.H * a.NC};
+  const int64_t ri = (int64_t)bh * a.NC + c;
+  T* ws16 = (T*)a.ws;
 
-  {  // rows: load, L2-normalise, scale q
-    const int p = tid >> 2, qq = tid & 3;
-    const int t = t0 + p;
-    const bool ok = t < a.T;
-    const T* kr = (const T*)a.k + b * a.k_sb + (int64_t)t * a.k_st + h * a.k_sh + qq * EPT;
-    const T* qr = (const T*)a.q + b * a.q_sb + (int64_t)t * a.q_st + h * a.q_sh + qq * EPT;
-    u32x4 kv[VPT], qv[VPT];
-    float ks = 0.f, qs = 0.f;
+  // ---- rows: thread (p4, dc) holds tokens 4p4..4p4+3, dims 8dc..8dc+7 of k, q, v
+  const bool act = tid < NE;
+  const int p4 = tid / DC, dc = tid % DC;
+  u32x4 kn[4], vr[4];
+  if (act) {
+    u32x4 qv[4];
+    float ks[4], qs[4];
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      kv[i] = ok ? *(const u32x4*)(kr + 8 * i) : u32x4{0, 0, 0, 0};
-      qv[i] = ok ? *(const u32x4*)(qr + 8 * i) : u32x4{0, 0, 0, 0};
+    for (int i = 0; i < 4; ++i) {
+      const int64_t t = t0 + 4 * p4 + i;
+      const bool ok = t < a.T;
+      kn[i] = ok ? *(const u32x4*)((const T*)a.k + b * a.k_sb + t * a.k_st + h * a.k_sh + 8 * dc)
+                 : u32x4{0, 0, 0, 0};
+      qv[i] = ok ? *(const u32x4*)((const T*)a.q + b * a.q_sb + t * a.q_st + h * a.q_sh + 8 * dc)
+                 : u32x4{0, 0, 0, 0};
+      vr[i] = ok ? *(const u32x4*)((const T*)a.v + b * a.v_sb + t * a.v_st + h * a.v_sh + 8 * dc)
+                 : u32x4{0, 0, 0, 0};
+      ks[i] = qs[i] = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float x = elem16<T>(kv[i], e), y = elem16<T>(qv[i], e);
-        ks += x * x;
-        qs += y * y;
+        const float x = elem16<T>(kn[i], e), y = elem16<T>(qv[i], e);
+        ks[i] = fmaf(x, x, ks[i]);
+        qs[i] = fmaf(y, y, qs[i]);
       }
     }
-    ks += __shfl_xor(ks, 1, 64);
-    ks += __shfl_xor(ks, 2, 64);
-    qs += __shfl_xor(qs, 1, 64);
-    qs += __shfl_xor(qs, 2, 64);
-    const float ik = a.l2norm ? 1.f / fmaxf(sqrtf(ks), 1e-12f) : 1.f;
-    const float iq = (a.l2norm ? 1.f / fmaxf(sqrtf(qs), 1e-12f) : 1.f) * a.scale;
 #pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      u32x4 ko, qo;
+    for (int m = 1; m < DC; m <<= 1)
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        ko[w] = pack2<T>(elem16<T>(kv[i], 2 * w) * ik, elem16<T>(kv[i], 2 * w + 1) * ik);
-        qo[w] = pack2<T>(elem16<T>(qv[i], 2 * w) * iq, elem16<T>(qv[i], 2 * w + 1) * iq);
+      for (int i = 0; i < 4; ++i) {
+        ks[i] += __shfl_xor(ks[i], m, 64);
+        qs[i] += __shfl_xor(qs[i], m, 64);
       }
-      *(u32x4*)(Kn + p * KP + qq * EPT + 8 * i) = ko;
-      *(u32x4*)(Qn + p * KP + qq * EPT + 8 * i) = qo;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float ik = a.l2norm ? 1.f / fmaxf(sqrtf(ks[i]), 1e-12f) : 1.f;
+      const float iq = (a.l2norm ? 1.f / fmaxf(sqrtf(qs[i]), 1e-12f) : 1.f) * a.scale;
+      const int p = 4 * p4 + i;
+      kn[i] = scale8<T>(kn[i], ik);
+      const u32x4 qn = scale8<T>(qv[i], iq);
+      *(u32x4*)(R1 + p * KP + 8 * dc) = kn[i];
+      *(u32x4*)(R2 + p * KP + 8 * dc) = qn;
+      *(u32x4*)(ws16 + W.qn(ri) + p * D + 8 * dc) = qn;
     }
-    if (tid < C) {
-      const int tt = t0 + tid;
-      const int64_t gi = ((int64_t)b * a.T + tt) * a.H + h;
-      lg[tid] = tt < a.T ? a.g[gi] : 0.f;
-      bet[tid] = tt < a.T ? a.beta[gi] : 0.f;
-    }
+  }
+  if (tid < C) {
+    const int tt = t0 + tid;
+    const int64_t gi = ((int64_t)b * a.T + tt) * a.H + h;
+    lg[tid] = tt < a.T ? a.g[gi] : 0.f;
+    bet[tid] = tt < a.T ? a.beta[gi] : 0.f;
   }
   __syncthreads();
   if (wave == 0) {  // inclusive prefix sum of the log-decays
@@ -95,33 +125,69 @@ __global__ void __launch_bounds__(256) gdn_prep16_kernel(GdnArgs a) {
       if (lane >= off) x += y;
     }
     lg[lane] = x;
+    sge[lane] = expf(x);
+    const float last = __shfl(x, 63, 64);
+    stl[lane] = expf(last - x);
+    ((float*)((char*)a.ws + W.lg_byte(ri)))[lane] = x;
   }
   __syncthreads();
 
-  // ---- Gram tiles on the lower block triangle: 10 (tp >= ts) for K K^T and Q K^T each
-  {
-    for (int task = wave; task < 20; task += 4) {
-      const int which = task / 10, idx = task % 10;
-      const int tp = (idx >= 1) + (idx >= 3) + (idx >= 6);
-      const int ts = idx - tp * (tp + 1) / 2;
-      const T* arow = (which ? Qn : Kn) + (16 * tp + c16) * KP + 8 * g;
-      const T* brow = Kn + (16 * ts + c16) * KP + 8 * g;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  // ---- Gram tiles: 10 lower-triangle (tp >= ts) tiles of Kn Kn^T and of Qn Kn^T
+  for (int task = wave; task < 20; task += 4) {
+    const int which = task / 10, idx = task % 10;
+    const int tp = (idx >= 1) + (idx >= 3) + (idx >= 6);
+    const int ts = idx - tp * (tp + 1) / 2;
+    const T* arow = (which ? R2 : R1) + (16 * tp + c16) * KP + 8 * g;
+    const T* brow = R1 + (16 * ts + c16) * KP + 8 * g;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < D / 32; ++s) acc = mfma16x16x32<T>(lds16(arow + 32 * s), lds16(brow + 32 * s), acc);
+    for (int s = 0; s < D / 32; ++s) acc = mfma16x16x32<T>(lds16(arow + 32 * s), lds16(brow + 32 * s), acc);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int p = 16 * tp + 4 * g + i, s = 16 * ts + c16;
-        const float dec = s <= p ? expf(lg[p] - lg[s]) : 0.f;
-        if (which == 0)
-          Af[p * FP + s] = s < p ? bet[p] * dec * acc[i] : 0.f;
-        else
-          Rf[p * FP + s] = s <= p ? dec * acc[i] : 0.f;
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int p = 16 * tp + 4 * g + i, s = 16 * ts + c16;
+      const float dec = s <= p ? expf(lg[p] - lg[s]) : 0.f;
+      if (which == 0)
+        Af[p * FP + s] = s < p ? bet[p] * dec * acc[i] : 0.f;
+      else
+        ws16[W.rq(ri) + p * C + s] = (T)(s <= p ? dec * acc[i] : 0.f);
     }
   }
-  __syncthreads();
+  for (int e = tid; e < 6 * 256; e += 256) {  // rq is zero above the block diagonal
+    int tp, ts;
+    upper_block(e >> 8, tp, ts);
+    ws16[W.rq(ri) + (16 * tp + ((e >> 4) & 15)) * C + 16 * ts + (e & 15)] = (T)0.f;
+  }
+  if (act) {  // kdT = (diag(tail) Kn)^T from the row registers
+    float tl[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tl[i] = stl[4 * p4 + i];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      u32x2 pk = {pack2<T>(elem16<T>(kn[0], e) * tl[0], elem16<T>(kn[1], e) * tl[1]),
+                  pack2<T>(elem16<T>(kn[2], e) * tl[2], elem16<T>(kn[3], e) * tl[3])};
+      *(u32x2*)(ws16 + W.kdT(ri) + (8 * dc + e) * C + 4 * p4) = pk;
+    }
+  }
+  __syncthreads();  // Gram done: R1 / R2 are free, A is complete
 
+  // ---- transposed, scaled operands of the w / u products
+  if (act) {
+    float fk[4], fv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fv[i] = bet[4 * p4 + i];
+      fk[i] = fv[i] * sge[4 * p4 + i];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      u32x2 pk = {pack2<T>(elem16<T>(kn[0], e) * fk[0], elem16<T>(kn[1], e) * fk[1]),
+                  pack2<T>(elem16<T>(kn[2], e) * fk[2], elem16<T>(kn[3], e) * fk[3])};
+      *(u32x2*)(R1 + (8 * dc + e) * CP + 4 * p4) = pk;
+      u32x2 pv = {pack2<T>(elem16<T>(vr[0], e) * fv[0], elem16<T>(vr[1], e) * fv[1]),
+                  pack2<T>(elem16<T>(vr[2], e) * fv[2], elem16<T>(vr[3], e) * fv[3])};
+      *(u32x2*)(R2 + (8 * dc + e) * CP + 4 * p4) = pv;
+    }
+  }
   // ---- T = (I + A)^-1: diagonal 16x16 blocks by forward substitution (lane = column)
   if (wave == 0) {
     const int bb = lane >> 4, cc = lane & 15;
@@ -135,6 +201,11 @@ __global__ void __launch_bounds__(256) gdn_prep16_kernel(GdnArgs a) {
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) Tf[(16 * bb + r) * FP + 16 * bb + cc] = col[r];
+  }
+  for (int e = tid; e < 6 * 256; e += 256) {  // T is zero above the block diagonal
+    int tp, ts;
+    upper_block(e >> 8, tp, ts);
+    Tf[(16 * tp + ((e >> 4) & 15)) * FP + 16 * ts + (e & 15)] = 0.f;
   }
   __syncthreads();
   // ---- off-diagonal blocks: T_ij = -T_ii * sum_{k=j}^{i-1} A_ik T_kj, level L = i - j
@@ -161,51 +232,49 @@ __global__ void __launch_bounds__(256) gdn_prep16_kernel(GdnArgs a) {
     __syncthreads();
   }
 
-  // ---- record: T diag(beta), Rq (16-bit, zero above the diagonal), log-decays
-  char* rec = (char*)a.ws + ((int64_t)bh * a.NC + c) * kGdn16RecBytes;
-  T* tb = (T*)rec;
-  T* rq = tb + C * C;
-  float* lgo = (float*)(rq + C * C);
-  for (int e = tid; e < C * C / 8; e += 256) {
-    const int p = e >> 3, s0 = (e & 7) * 8;
-    u32x4 xt, xr;
+  // ---- w = T (beta ge Kn), u = T (beta V): wave = 16-row block of T, all column tiles
+  {
+    const int rb = wave;
+    const int nsteps = rb < 2 ? 1 : 2;  // T is lower triangular: later tokens are 0
+    u32x4 tfrag[2];
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const int s = s0 + 2 * w;
-      const float t0v = s <= p ? Tf[p * FP + s] * bet[s] : 0.f;
-      const float t1v = s + 1 <= p ? Tf[p * FP + s + 1] * bet[s + 1] : 0.f;
-      const float r0v = s <= p ? Rf[p * FP + s] : 0.f;
-      const float r1v = s + 1 <= p ? Rf[p * FP + s + 1] : 0.f;
-      xt[w] = pack2<T>(t0v, t1v);
-      xr[w] = pack2<T>(r0v, r1v);
+    for (int s = 0; s < 2; ++s) {
+      const float* tr = Tf + (16 * rb + c16) * FP + 32 * s + 8 * g;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) tfrag[s][w] = pack2<T>(tr[2 * w], tr[2 * w + 1]);
     }
-    *(u32x4*)(tb + p * C + s0) = xt;
-    *(u32x4*)(rq + p * C + s0) = xr;
+#pragma unroll
+    for (int ct = 0; ct < D / 16; ++ct) {
+      f32x4 aw = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
+      for (int s = 0; s < nsteps; ++s) {
+        aw = mfma16x16x32<T>(tfrag[s], lds16(R1 + (16 * ct + c16) * CP + 32 * s + 8 * g), aw);
+        au = mfma16x16x32<T>(tfrag[s], lds16(R2 + (16 * ct + c16) * CP + 32 * s + 8 * g), au);
+      }
+      // w rows 16rb + 4g + i, column 16ct + c16;  u in the scan's register order
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ws16[W.w(ri) + (16 * rb + 4 * g + i) * D + 16 * ct + c16] = (T)aw[i];
+      u32x2 pk = {pack2<T>(au[0], au[1]), pack2<T>(au[2], au[3])};
+      *(u32x2*)(ws16 + W.us(ri) + (((ct >> 1) * 4 + rb) * 64 + lane) * 8 + (ct & 1) * 4) = pk;
+    }
   }
-  if (tid < C) lgo[tid] = lg[tid];
 }
 
 template <typename T, int D>
-__global__ void __launch_bounds__(256) gdn_scan16_kernel(GdnArgs a) {
+__global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
   constexpr int C = kChunk, VS = 32, KP = D + 8, CP = C + 8;
-  constexpr int EPT = D / 4, VPT = EPT / 8;
+  constexpr int KS = D / 32;   // MFMA k-steps over the head dim
   constexpr int KTW = D / 64;  // 16-row state tiles per wave
-  __shared__ __attribute__((aligned(16))) T Kn[C * KP];
-  __shared__ __attribute__((aligned(16))) T Qn[C * KP];
-  __shared__ __attribute__((aligned(16))) T KdT[D * CP];
-  __shared__ __attribute__((aligned(16))) T Tb[C * CP];
-  __shared__ __attribute__((aligned(16))) T Rq[C * CP];
-  __shared__ __attribute__((aligned(16))) T Sb[VS * KP];
-  __shared__ __attribute__((aligned(16))) T XT[VS * CP];
-  __shared__ __attribute__((aligned(16))) T UT[VS * CP];
-  __shared__ float s_ge[C], s_tail[C];
+  __shared__ __attribute__((aligned(16))) T Sb[VS * KP];  // S^T slab, 16-bit: [v][k]
+  __shared__ __attribute__((aligned(16))) T Ub[VS * CP];  // U^T, 16-bit: [v][token]
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, g = lane >> 4;
   const int bh = blockIdx.x, v0 = blockIdx.y * VS;
-  const int b = bh / a.H, h = bh % a.H;
+  const Gdn16Ws W{D, (int64_t)a.B * a.H * a.NC};
+  const int64_t ri0 = (int64_t)bh * a.NC;
+  T* ws16 = (T*)a.ws;
 
-  // ---- state slab in accumulators: tiles (k-tile wave*KTW + j, v-tile vt)
+  // ---- state slab: tile (k-tile wave*KTW + j, v-tile vt); rows k = 16kt + 4g + i, cols v
   f32x4 S[KTW][2];
 #pragma unroll
   for (int j = 0; j < KTW; ++j)
@@ -217,200 +286,111 @@ __global__ void __launch_bounds__(256) gdn_scan16_kernel(GdnArgs a) {
         const int kx = 16 * kt + 4 * g + i, vx = v0 + 16 * vt + c16;
         S[j][vt][i] = a.s0 ? a.s0[((int64_t)bh * D + kx) * D + vx] : 0.f;
       }
-      u32x2 pk = {pack2<T>(S[j][vt][0], S[j][vt][1]), pack2<T>(S[j][vt][2], S[j][vt][3])};
-      *(u32x2*)(Sb + (16 * vt + c16) * KP + 16 * kt + 4 * g) = pk;
     }
-
-  // ---- register prefetch of one chunk's rows and record
-  const int rp = tid >> 2, rq4 = tid & 3;
-  u32x4 kpre[VPT], qpre[VPT], tpre[2], rpre[2];
-  float vpre[2][4];  // V at rows 16*wave + 4g + i, columns v0 + 16vt + c16
-  float lgpre = 0.f, lgcpre = 0.f;
-  auto prefetch = [&](int c) {
-#pragma unroll
-    for (int vt = 0; vt < 2; ++vt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = c * C + 16 * wave + 4 * g + i;
-        vpre[vt][i] =
-            t < a.T ? to_f32(((const T*)a.v)[b * a.v_sb + (int64_t)t * a.v_st + h * a.v_sh + v0 + 16 * vt + c16])
-                    : 0.f;
-      }
-    const int t = c * C + rp;
-    const bool ok = t < a.T;
-    const T* kr = (const T*)a.k + b * a.k_sb + (int64_t)t * a.k_st + h * a.k_sh + rq4 * EPT;
-    const T* qr = (const T*)a.q + b * a.q_sb + (int64_t)t * a.q_st + h * a.q_sh + rq4 * EPT;
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      kpre[i] = ok ? *(const u32x4*)(kr + 8 * i) : u32x4{0, 0, 0, 0};
-      qpre[i] = ok ? *(const u32x4*)(qr + 8 * i) : u32x4{0, 0, 0, 0};
-    }
-    const T* rec = (const T*)((const char*)a.ws + ((int64_t)bh * a.NC + c) * kGdn16RecBytes);
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const int e = tid + 256 * r;
-      tpre[r] = *(const u32x4*)(rec + 8 * e);
-      rpre[r] = *(const u32x4*)(rec + C * C + 8 * e);
-    }
-    const float* lgr = (const float*)(rec + 2 * C * C);
-    if (tid < C) lgpre = lgr[tid];
-    lgcpre = lgr[C - 1];
-  };
-  prefetch(0);
-
-  for (int c = 0; c < a.NC; ++c) {
-    // ---- phase L: normalised rows, record matrices, decays
-    {
-      float ks = 0.f, qs = 0.f;
-#pragma unroll
-      for (int i = 0; i < VPT; ++i)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float x = elem16<T>(kpre[i], e), y = elem16<T>(qpre[i], e);
-          ks += x * x;
-          qs += y * y;
-        }
-      ks += __shfl_xor(ks, 1, 64);
-      ks += __shfl_xor(ks, 2, 64);
-      qs += __shfl_xor(qs, 1, 64);
-      qs += __shfl_xor(qs, 2, 64);
-      const float ik = a.l2norm ? 1.f / fmaxf(sqrtf(ks), 1e-12f) : 1.f;
-      const float iq = (a.l2norm ? 1.f / fmaxf(sqrtf(qs), 1e-12f) : 1.f) * a.scale;
-#pragma unroll
-      for (int i = 0; i < VPT; ++i) {
-        u32x4 ko, qo;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          ko[w] = pack2<T>(elem16<T>(kpre[i], 2 * w) * ik, elem16<T>(kpre[i], 2 * w + 1) * ik);
-          qo[w] = pack2<T>(elem16<T>(qpre[i], 2 * w) * iq, elem16<T>(qpre[i], 2 * w + 1) * iq);
-        }
-        *(u32x4*)(Kn + rp * KP + rq4 * EPT + 8 * i) = ko;
-        *(u32x4*)(Qn + rp * KP + rq4 * EPT + 8 * i) = qo;
-      }
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int e = tid + 256 * r;
-        const int p = e >> 3, s0 = (e & 7) * 8;
-        *(u32x4*)(Tb + p * CP + s0) = tpre[r];
-        *(u32x4*)(Rq + p * CP + s0) = rpre[r];
-      }
-      if (tid < C) {
-        s_ge[tid] = expf(lgpre);
-        s_tail[tid] = expf(lgcpre - lgpre);
-      }
-    }
-    const float gC = expf(lgcpre);
-    float vcur[2][4];
-#pragma unroll
-    for (int vt = 0; vt < 2; ++vt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) vcur[vt][i] = vpre[vt][i];
-    __syncthreads();
-    if (c + 1 < a.NC) prefetch(c + 1);
-
-    // ---- phase K: KdT[k][p] = tail_p * Kn[p][k]  (4 rows x 8 dims per thread)
-    for (int e = tid; e < (C / 4) * (D / 8); e += 256) {
-      const int p4 = e & 15, kc = e >> 4;
-      u32x4 r[4];
-      float tl[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        r[i] = lds16(Kn + (4 * p4 + i) * KP + 8 * kc);
-        tl[i] = s_tail[4 * p4 + i];
-      }
-#pragma unroll
-      for (int ee = 0; ee < 8; ++ee) {
-        u32x2 pk = {pack2<T>(elem16<T>(r[0], ee) * tl[0], elem16<T>(r[1], ee) * tl[1]),
-                    pack2<T>(elem16<T>(r[2], ee) * tl[2], elem16<T>(r[3], ee) * tl[3])};
-        *(u32x2*)(KdT + (8 * kc + ee) * CP + 4 * p4) = pk;
-      }
-    }
-    // ---- phase X: X = V - diag(ge) K S   (wave: 16 rows, 32 columns)
-    u32x4 sfrag[2][D / 32];  // S (16-bit) B fragments, reused by phase O
-#pragma unroll
-    for (int vt = 0; vt < 2; ++vt)
-#pragma unroll
-      for (int s = 0; s < D / 32; ++s) sfrag[vt][s] = lds16(Sb + (16 * vt + c16) * KP + 8 * g + 32 * s);
-    u32x4 kfrag[D / 32];
-#pragma unroll
-    for (int s = 0; s < D / 32; ++s) kfrag[s] = lds16(Kn + (16 * wave + c16) * KP + 8 * g + 32 * s);
-#pragma unroll
-    for (int vt = 0; vt < 2; ++vt) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < D / 32; ++s) acc = mfma16x16x32<T>(kfrag[s], sfrag[vt][s], acc);
-      float xv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) xv[i] = vcur[vt][i] - s_ge[16 * wave + 4 * g + i] * acc[i];
-      u32x2 pk = {pack2<T>(xv[0], xv[1]), pack2<T>(xv[2], xv[3])};
-      *(u32x2*)(XT + (16 * vt + c16) * CP + 16 * wave + 4 * g) = pk;
-    }
-    __syncthreads();
-
-    // ---- phase U: U = (T diag(beta)) X
-#pragma unroll
-    for (int vt = 0; vt < 2; ++vt) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-      const T* arow = Tb + (16 * wave + c16) * CP + 8 * g;
-      const T* brow = XT + (16 * vt + c16) * CP + 8 * g;
-#pragma unroll
-      for (int s = 0; s < 2; ++s) acc = mfma16x16x32<T>(lds16(arow + 32 * s), lds16(brow + 32 * s), acc);
-      u32x2 pk = {pack2<T>(acc[0], acc[1]), pack2<T>(acc[2], acc[3])};
-      *(u32x2*)(UT + (16 * vt + c16) * CP + 16 * wave + 4 * g) = pk;
-    }
-    __syncthreads();
-
-    // ---- phase O: O = diag(ge) Q S + Rq U
-    u32x4 ufrag[2][2];  // U^T B fragments, reused by phase S
-#pragma unroll
-    for (int vt = 0; vt < 2; ++vt)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) ufrag[vt][s] = lds16(UT + (16 * vt + c16) * CP + 8 * g + 32 * s);
-    u32x4 qfrag[D / 32], rfrag[2];
-#pragma unroll
-    for (int s = 0; s < D / 32; ++s) qfrag[s] = lds16(Qn + (16 * wave + c16) * KP + 8 * g + 32 * s);
-#pragma unroll
-    for (int s = 0; s < 2; ++s) rfrag[s] = lds16(Rq + (16 * wave + c16) * CP + 8 * g + 32 * s);
-#pragma unroll
-    for (int vt = 0; vt < 2; ++vt) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < D / 32; ++s) acc = mfma16x16x32<T>(qfrag[s], sfrag[vt][s], acc);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] *= s_ge[16 * wave + 4 * g + i];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) acc = mfma16x16x32<T>(rfrag[s], ufrag[vt][s], acc);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int t = c * C + 16 * wave + 4 * g + i;
-        if (t < a.T)
-          ((T*)a.o)[(((int64_t)b * a.T + t) * a.H + h) * D + v0 + 16 * vt + c16] = (T)acc[i];
-      }
-    }
-    // ---- phase S: S = gC S + Kd^T U
-#pragma unroll
-    for (int j = 0; j < KTW; ++j) {
-      const int kt = wave * KTW + j;
-      u32x4 kdfrag[2];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) kdfrag[s] = lds16(KdT + (16 * kt + c16) * CP + 8 * g + 32 * s);
-#pragma unroll
-      for (int vt = 0; vt < 2; ++vt) {
-        f32x4 acc = S[j][vt] * gC;
-#pragma unroll
-        for (int s = 0; s < 2; ++s) acc = mfma16x16x32<T>(kdfrag[s], ufrag[vt][s], acc);
-        S[j][vt] = acc;
-      }
-    }
-    __syncthreads();
+  // 16-bit copy of the state entering the next chunk, in LDS (B operands)
+  auto publish_state = [&]() {
 #pragma unroll
     for (int j = 0; j < KTW; ++j)
 #pragma unroll
       for (int vt = 0; vt < 2; ++vt) {
         const int kt = wave * KTW + j;
-        u32x2 pk = {pack2<T>(S[j][vt][0], S[j][vt][1]), pack2<T>(S[j][vt][2], S[j][vt][3])};
+        const u32x2 pk = {pack2<T>(S[j][vt][0], S[j][vt][1]), pack2<T>(S[j][vt][2], S[j][vt][3])};
         *(u32x2*)(Sb + (16 * vt + c16) * KP + 16 * kt + 4 * g) = pk;
       }
+  };
+
+  // ---- one chunk's operands in registers (A fragments straight from memory).  Four
+  // sets rotate: a set is refilled with chunk c + 4 right after chunk c used it, so
+  // each load has three chunk steps to arrive and no set is ever copied.  Per chunk a
+  // wave issues 10 loads and 3 stores, so three chunks in flight stay well inside the
+  // 63 outstanding memory operations a wave can track.
+  struct Frag {
+    u32x4 w[KS], k[KTW][2], u;
+    float lgc;
+  };
+  auto load = [&](Frag& f, int c) {
+    const int64_t ri = ri0 + c;
+    const int row = 16 * wave + c16;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) f.w[s] = *(const u32x4*)(ws16 + W.w(ri) + row * D + 32 * s + 8 * g);
+#pragma unroll
+    for (int j = 0; j < KTW; ++j)
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        f.k[j][s] = *(const u32x4*)(ws16 + W.kdT(ri) + (16 * (wave * KTW + j) + c16) * C + 32 * s + 8 * g);
+    f.u = *(const u32x4*)(ws16 + W.us(ri) + ((blockIdx.y * 4 + wave) * 64 + lane) * 8);
+    f.lgc = ((const float*)((const char*)a.ws + W.lg_byte(ri)))[C - 1];
+  };
+
+  auto body = [&](const Frag& f, int c) {
+    // ---- the state entering this chunk (16-bit, in Sb) to the record, 16 B per store
+    {
+      T* sT = ws16 + W.sT(ri0 + c);
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int e = tid + 256 * r, row = e >> 4, cc = e & 15;  // 32 rows x 16 chunks
+        if (D == 128 || cc < D / 8)
+          *(u32x4*)(sT + (v0 + row) * D + 8 * cc) = lds16(Sb + row * KP + 8 * cc);
+      }
+    }
+    // ---- U = u - w S (rows 16*wave + 4g + i, columns v0 + 16vt + c16)
+#pragma unroll
+    for (int vt = 0; vt < 2; ++vt) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        acc = mfma16x16x32<T>(f.w[s], lds16(Sb + (16 * vt + c16) * KP + 32 * s + 8 * g), acc);
+      float uv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) uv[i] = elem16<T>(f.u, 4 * vt + i) - acc[i];
+      const u32x2 pk = {pack2<T>(uv[0], uv[1]), pack2<T>(uv[2], uv[3])};
+      *(u32x2*)(Ub + (16 * vt + c16) * CP + 16 * wave + 4 * g) = pk;
+    }
+    __syncthreads();
+    // ---- U^T to the record (32 rows x 8 chunks of 16 B)
+    {
+      T* unT = ws16 + W.unT(ri0 + c);
+      const int row = tid >> 3, cc = tid & 7;
+      *(u32x4*)(unT + (v0 + row) * C + 8 * cc) = lds16(Ub + row * CP + 8 * cc);
+    }
+    // ---- S = gC S + kdT U
+    const float gC = expf(f.lgc);
+#pragma unroll
+    for (int vt = 0; vt < 2; ++vt) {
+      u32x4 uf[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) uf[s] = lds16(Ub + (16 * vt + c16) * CP + 32 * s + 8 * g);
+#pragma unroll
+      for (int j = 0; j < KTW; ++j) {
+        f32x4 acc = S[j][vt] * gC;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) acc = mfma16x16x32<T>(f.k[j][s], uf[s], acc);
+        S[j][vt] = acc;
+      }
+    }
+    publish_state();
+    __syncthreads();
+  };
+
+  // (Past the last chunk the loads re-read it: every step issues the same loads in the
+  // same order, so the compiler's waits on them stay partial.)
+  const int last = a.NC - 1;
+  publish_state();
+  Frag f0, f1, f2, f3;
+  load(f0, 0);
+  load(f1, min(1, last));
+  load(f2, min(2, last));
+  load(f3, min(3, last));
+  __syncthreads();
+  for (int c = 0; c < a.NC; c += 4) {
+    body(f0, c);
+    load(f0, min(c + 4, last));
+    if (c + 1 < a.NC) body(f1, c + 1);
+    load(f1, min(c + 5, last));
+    if (c + 2 < a.NC) body(f2, c + 2);
+    load(f2, min(c + 6, last));
+    if (c + 3 < a.NC) body(f3, c + 3);
+    load(f3, min(c + 7, last));
   }
 
   if (a.s_out) {
@@ -428,13 +408,73 @@ __global__ void __launch_bounds__(256) gdn_scan16_kernel(GdnArgs a) {
   }
 }
 
+// Output pass, chunk-parallel: O = diag(ge) Qn S_c + Rq U_c for every chunk from the
+// states and updates the scan published.  One workgroup per (chunk, sequence*head);
+// wave w owns rows 16w..16w+15 and all D columns.
+template <typename T, int D>
+__global__ void __launch_bounds__(256, 2) gdn_out16_kernel(GdnArgs a) {
+  constexpr int C = kChunk, SP = D + 8, UP = C + 8;
+  constexpr int KS = D / 32;
+  __shared__ __attribute__((aligned(16))) T Ss[D * SP];  // S_c^T [v][k]
+  __shared__ __attribute__((aligned(16))) T Us[D * UP];  // U_c^T [v][token]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int c16 = lane & 15, g = lane >> 4;
+  const int c = blockIdx.x, bh = blockIdx.y;
+  const int b = bh / a.H, h = bh % a.H;
+  const Gdn16Ws W{D, (int64_t)a.B * a.H * a.NC};
+  const int64_t ri = (int64_t)bh * a.NC + c;
+  const T* ws16 = (const T*)a.ws;
+
+  for (int e = tid; e < D * D / 8; e += 256) {
+    const int r = e / (D / 8), cc = e % (D / 8);
+    *(u32x4*)(Ss + r * SP + 8 * cc) = *(const u32x4*)(ws16 + W.sT(ri) + r * D + 8 * cc);
+  }
+  for (int e = tid; e < D * C / 8; e += 256) {
+    const int r = e / (C / 8), cc = e % (C / 8);
+    *(u32x4*)(Us + r * UP + 8 * cc) = *(const u32x4*)(ws16 + W.unT(ri) + r * C + 8 * cc);
+  }
+  const int row = 16 * wave + c16;
+  u32x4 qf[KS], rf[2];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) qf[s] = *(const u32x4*)(ws16 + W.qn(ri) + row * D + 32 * s + 8 * g);
+#pragma unroll
+  for (int s = 0; s < 2; ++s) rf[s] = *(const u32x4*)(ws16 + W.rq(ri) + row * C + 32 * s + 8 * g);
+  const float* lgp = (const float*)((const char*)a.ws + W.lg_byte(ri));
+  float ge[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ge[i] = expf(lgp[16 * wave + 4 * g + i]);
+  __syncthreads();
+
+  // this sequence's output rows as one buffer: rows past T are dropped
+  const auto orsrc = buffer_rsrc((const T*)a.o + (int64_t)b * a.T * a.H * D,
+                                 (uint32_t)((int64_t)a.T * a.H * D * 2));
+#pragma unroll
+  for (int ct = 0; ct < D / 16; ++ct) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) acc = mfma16x16x32<T>(qf[s], lds16(Ss + (16 * ct + c16) * SP + 32 * s + 8 * g), acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] *= ge[i];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) acc = mfma16x16x32<T>(rf[s], lds16(Us + (16 * ct + c16) * UP + 32 * s + 8 * g), acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t t = c * C + 16 * wave + 4 * g + i;
+      buffer_store16b<T>(orsrc, ((t * a.H + h) * D + 16 * ct + c16) * 2u, (T)acc[i]);
+    }
+  }
+}
+
 template <typename T, int D>
 static int launch16(const GdnArgs& a, hipStream_t s) {
   gdn_prep16_kernel<T, D><<<dim3((unsigned)a.NC, (unsigned)(a.B * a.H)), dim3(256), 0, s>>>(a);
   int rc = check_launch("chunk_gated_delta_rule(prep16)");
   if (rc) return rc;
   gdn_scan16_kernel<T, D><<<dim3((unsigned)(a.B * a.H), D / 32), dim3(256), 0, s>>>(a);
-  return check_launch("chunk_gated_delta_rule(scan16)");
+  rc = check_launch("chunk_gated_delta_rule(scan16)");
+  if (rc) return rc;
+  gdn_out16_kernel<T, D><<<dim3((unsigned)a.NC, (unsigned)(a.B * a.H)), dim3(256), 0, s>>>(a);
+  return check_launch("chunk_gated_delta_rule(out16)");
 }
 
 int launch_gdn16(const GdnArgs& a, int dtype, int D, hipStream_t s) {
