@@ -66,6 +66,18 @@ __device__ __forceinline__ uint32_t pack2(float x, float y) {
   return (uint32_t)ua | ((uint32_t)ub << 16);
 }
 
+// Dot product of two packed 16-bit pairs accumulated in fp32 (v_dot2_f32_{bf16,f16}).
+template <typename T>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (__is_same(T, bf16)) {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+  } else {
+    typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+  }
+}
+
 // 16-bit element e (0..7) of a 16-byte vector, as float.
 template <typename T>
 __device__ __forceinline__ float elem16(const u32x4& x, int e) {

@@ -23,6 +23,10 @@
 //  * GQA is resolved in-kernel (kv head = q head / group), and the grid is
 //    ordered so the workgroups of one KV group and neighbouring query tiles land
 //    on the same XCD (shared L2), longest causal tiles first.
+//  * 16-bit inputs skip the per-block max: p is formed against the running max as
+//    it stands, and v_dot2 sums p and p^2 from the same 16-bit pairs the PV MFMA
+//    consumes; the max is taken (and the state rescaled) only when a lane's sum
+//    leaves the safe range -- the first block, or a new maximum far above the old.
 //  * bf16/fp16 use v_mfma_f32_32x32x16_{bf16,f16}; fp32 inputs use
 //    v_mfma_f32_32x32x2f32 (full fp32 products: the 1e-4 mode).
 #include "common.h"
@@ -281,7 +285,7 @@ __global__ void __launch_bounds__(256, 1) polar_fwd_kernel(PolarFwdArgs args) {
   }
   __syncthreads();
   const int arow = a_row_key(ql);
-  constexpr float kRescale = 8.f;  // lazy rescale: p <= 2^8 between max updates
+  constexpr float kRescale = 8.f;  // fp32 inputs, lazy rescale: p <= 2^8 between max updates
 
   for (int it = 0; it < nblk; ++it) {
     const int blk = nblk_beg + it, buf = it & 1;
@@ -317,13 +321,7 @@ __global__ void __launch_bounds__(256, 1) polar_fwd_kernel(PolarFwdArgs args) {
     // ---- online softmax (+ sum of p^2); scores scaled inside one FMA per element
     const bool full = (k0 + BN <= (int)fminf(w_nlo, (float)args.Tk)) &&
                       (args.window <= 0 || (float)k0 >= w_nhi - (float)args.window);
-    float mx = -INFINITY;
-    if (full) {
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[j][i]);
-    } else {
+    if (!full) {
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -332,44 +330,60 @@ __global__ void __launch_bounds__(256, 1) polar_fwd_kernel(PolarFwdArgs args) {
           bool ok = (float)key < n_raw && key < args.Tk;
           if (args.window > 0) ok = ok && (float)key >= n_raw - (float)args.window;
           sacc[j][i] = ok ? sacc[j][i] : -INFINITY;
-          mx = fmaxf(mx, sacc[j][i]);
         }
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float mxs = mx * c1;
-    if (__ballot(mxs > m_run + kRescale) != 0) {
-      const float m_new = fmaxf(m_run, mxs);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-      m_run = m_new;
-      l_part *= alpha;
-      q2_part *= alpha * alpha;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) oacc[t] *= alpha;
-    }
-    const float neg_m = -m_run;
-    float ls = 0.f, qs = 0.f;
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(sacc[j][i], c1, neg_m));
-        sacc[j][i] = p;
-        ls += p;
-        qs = fmaf(p, p, qs);
-      }
-    l_part += ls;
-    q2_part += qs;
-
-    // ---- O^T += V^T P^T
     if constexpr (Cfg::kHalf) {
+      // Optimistic pass: p = 2^(s c1 - m_run) against the running max as it stands, the
+      // 16-bit pairs feed the PV MFMA and v_dot2 gives sum p and sum p^2 from the very
+      // same rounded values.  Only when some lane's sum leaves the safe range (a new
+      // maximum far above the old one, or the first block) is the block max taken and
+      // the state rescaled, then p recomputed.
+      constexpr float kSafe = __is_same(T, bf16) ? 1048576.f : 16384.f;
       u32x4 pb[4];
+      float ls = 0.f, qs = 0.f;
+      auto exp_pack = [&]() {
+        const float neg_m = -m_run;
+        ls = qs = 0.f;
 #pragma unroll
-      for (int ps = 0; ps < 4; ++ps) {
-        const int j = ps >> 1, base = 8 * (ps & 1);
+        for (int ps = 0; ps < 4; ++ps) {
+          const int j = ps >> 1, base = 8 * (ps & 1);
 #pragma unroll
-        for (int w = 0; w < 4; ++w)
-          pb[ps][w] = pack2<T>(sacc[j][base + 2 * w], sacc[j][base + 2 * w + 1]);
+          for (int w = 0; w < 4; ++w) {
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[j][base + 2 * w], c1, neg_m));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[j][base + 2 * w + 1], c1, neg_m));
+            pb[ps][w] = pack2<T>(p0, p1);
+          }
+        }
+        const uint32_t one2 = pack2<T>(1.f, 1.f);
+#pragma unroll
+        for (int ps = 0; ps < 4; ++ps)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            ls = dot2<T>(pb[ps][w], one2, ls);
+            qs = dot2<T>(pb[ps][w], pb[ps][w], qs);
+          }
+      };
+      exp_pack();
+      if (__ballot(!(ls <= kSafe)) != 0) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[j][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m_run, mx * c1);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        l_part *= alpha;
+        q2_part *= alpha * alpha;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) oacc[t] *= alpha;
+        exp_pack();
       }
+      l_part += ls;
+      q2_part += qs;
+
+      // ---- O^T += V^T P^T
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const T* vrow = Vb + (32 * t + ql) * VP + 8 * h;
@@ -380,6 +394,37 @@ __global__ void __launch_bounds__(256, 1) polar_fwd_kernel(PolarFwdArgs args) {
         }
       }
     } else {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[j][i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mxs = mx * c1;
+      if (__ballot(mxs > m_run + kRescale) != 0) {
+        const float m_new = fmaxf(m_run, mxs);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+        m_run = m_new;
+        l_part *= alpha;
+        q2_part *= alpha * alpha;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) oacc[t] *= alpha;
+      }
+      const float neg_m = -m_run;
+      float ls = 0.f, qs = 0.f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float p = __builtin_amdgcn_exp2f(fmaf(sacc[j][i], c1, neg_m));
+          sacc[j][i] = p;
+          ls += p;
+          qs = fmaf(p, p, qs);
+        }
+      l_part += ls;
+      q2_part += qs;
+
+      // ---- O^T += V^T P^T (fp32 operands)
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         const T* vrow = Vb + (32 * t + ql) * VP + 8 * h;
