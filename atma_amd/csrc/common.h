@@ -61,9 +61,10 @@ __device__ __forceinline__ f32x4 mfma16x16x32(const u32x4& a, const u32x4& b, co
 // Two floats -> one dword of two 16-bit values (x in the low half).
 template <typename T>
 __device__ __forceinline__ uint32_t pack2(float x, float y) {
-  T a = (T)x, b = (T)y;
-  uint16_t ua = __builtin_bit_cast(uint16_t, a), ub = __builtin_bit_cast(uint16_t, b);
-  return (uint32_t)ua | ((uint32_t)ub << 16);
+  // one v_cvt_pk_{bf16,f16}_f32 (round to nearest even, as the scalar conversions)
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef T t2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2){x, y}, t2));
 }
 
 // Dot product of two packed 16-bit pairs accumulated in fp32 (v_dot2_f32_{bf16,f16}).

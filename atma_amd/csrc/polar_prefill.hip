@@ -182,6 +182,11 @@ __global__ void __launch_bounds__(256, 1) polar_fwd_kernel(PolarFwdArgs args) {
       qreg16[s] = q_ok ? *(const u32x4*)(qp + (int64_t)qi * args.q_st + 16 * s + 8 * h)
                        : u32x4{0, 0, 0, 0};
     }
+    // Consume the query registers here: a first use inside the key loop would make the
+    // compiler drain every load in flight there (the next tile's prefetch included) at
+    // each block.
+#pragma unroll
+    for (int s = 0; s < Cfg::QSTEPS; ++s) asm volatile("" ::"v"(qreg16[s]));
   } else {
 #pragma unroll
     for (int s4 = 0; s4 < Cfg::QSTEPS / 4; ++s4) {
@@ -223,6 +228,9 @@ __global__ void __launch_bounds__(256, 1) polar_fwd_kernel(PolarFwdArgs args) {
 
   u32x4 kpre[Cfg::KCH];
   u32x4 vpre[Cfg::VG_PT][4];
+  // Rows past Tk are read from row Tk - 1 instead (finite values: their scores are
+  // masked and their p is exactly 0), so every block issues the same unconditional
+  // loads and the compiler never has to drain them early.
   auto prefetch = [&](int blk) {
     const T* kb = kp + (int64_t)blk * BN * args.k_st;
     const T* vb = vp + (int64_t)blk * BN * args.v_st;
@@ -238,15 +246,19 @@ __global__ void __launch_bounds__(256, 1) polar_fwd_kernel(PolarFwdArgs args) {
         }
     } else {
 #pragma unroll
-      for (int r = 0; r < Cfg::KCH; ++r)
-        kpre[r] = (tid + 256 * r) / CPR < lim ? *(const u32x4*)(kb + koff[r]) : u32x4{0, 0, 0, 0};
+      for (int r = 0; r < Cfg::KCH; ++r) {
+        const int cidx = tid + 256 * r;
+        const int row = min(cidx / CPR, lim - 1);
+        kpre[r] = *(const u32x4*)(kb + (int64_t)row * kst + (cidx % CPR) * VE);
+      }
 #pragma unroll
       for (int gi = 0; gi < Cfg::VG_PT; ++gi)
         if (v_active(gi)) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            vpre[gi][r] = 4 * vkg[gi] + r < lim ? *(const u32x4*)(vb + voff[gi] + r * vst)
-                                                : u32x4{0, 0, 0, 0};
+          for (int r = 0; r < 4; ++r) {
+            const int row = min(4 * vkg[gi] + r, lim - 1);
+            vpre[gi][r] = *(const u32x4*)(vb + (int64_t)row * vst + vch[gi] * VE);
+          }
         }
     }
   };

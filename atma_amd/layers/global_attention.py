@@ -16,7 +16,8 @@ projections, RMSNorm and the depthwise Canon conv stay eager, as in the referenc
 Unlike the reference, K/V reach the Polar kernels unexpanded (GQA is resolved
 in-kernel); the memory branch sees them expanded, as it does in the reference.
 With ``overlap=True`` the memory branch runs on a second HIP stream concurrently
-with Polar attention: the two only share their inputs.
+with Polar attention (the two only share their inputs); off by default, because
+the prefill kernels each fill the GPU and measured slower side by side.
 """
 
 from dataclasses import dataclass
@@ -121,7 +122,7 @@ class PolarAttention(nn.Module):
 
     def __init__(self, dim, head_dim=128, num_kv_heads=None, kernel_size=4, window=None,
                  mem_enabled=True, mem_chunk=64, mem_gamma_bias=3.9, mem_beta_bias=0.0,
-                 num_heads=None, overlap=True):
+                 num_heads=None, overlap=False):
         super().__init__()
         self.num_heads = num_heads if num_heads is not None else dim // head_dim
         self.num_kv_heads = num_kv_heads if num_kv_heads is not None else self.num_heads // 4
@@ -326,7 +327,7 @@ class GlobalBlock(nn.Module):
     ``x + attn(norm1 x)``, then ``x + mlp(norm2 x)``."""
 
     def __init__(self, dim, head_dim=128, num_kv_heads=None, attn_kernel_size=4, window=None,
-                 mem_enabled=True, mem_chunk=64, overlap=True):
+                 mem_enabled=True, mem_chunk=64, overlap=False):
         super().__init__()
         self.attn = PolarAttention(dim, head_dim=head_dim, num_kv_heads=num_kv_heads,
                                    kernel_size=attn_kernel_size, window=window, mem_enabled=mem_enabled,

@@ -4,8 +4,8 @@ Default workload (the `value`): BASELINE.json configs[1] -- bf16 global-layer pr
 B=8, T=2048, 8 query / 2 KV heads, d=128: Polar attention forward (GQA in-kernel) plus
 the gated-delta chunked prefill (C=64, fp32 state from zero, memory gate / beta logits
 through the layer's own logsigmoid(z + 3.9) / sigmoid(z)).  One step = both ops over
-the resident batch, the memory branch on a second stream concurrently with Polar
-attention as the layer module runs them (the back-to-back time is reported too).
+the resident batch, back to back on one stream (the time with the memory branch on a
+second stream is reported as ms_overlap).
 value = (Polar + gated-delta algorithmic FLOPs) / step time.
 
 Also reported in the same JSON line: configs[2] (B=1, T=65,536 and 262,144) and
@@ -86,8 +86,13 @@ class Prefill:
                         output_final_state=True, use_qk_l2norm_in_kernel=True)
 
     def step(self):
-        """Both ops of the mixer, the memory branch on a second stream concurrently with
-        Polar attention, exactly as ``PolarAttention`` runs them (overlap=True)."""
+        """Both ops of the mixer back to back on one stream."""
+        self.polar()
+        self.memory()
+
+    def step_overlap(self):
+        """The memory branch on a second stream concurrently with Polar attention
+        (``PolarAttention(overlap=True)``); slower today, since Polar fills every CU."""
         torch = self.torch
         main = torch.cuda.current_stream()
         self.side.wait_stream(main)
@@ -95,10 +100,6 @@ class Prefill:
             self.memory()
         self.polar()
         main.wait_stream(self.side)
-
-    def step_sequential(self):
-        self.polar()
-        self.memory()
 
     def flops(self):
         return polar_flops(self.B, self.T), gdn_flops(self.B, self.T)
@@ -122,11 +123,11 @@ def bench_prefill(torch, dev, B, T, steps, warmup):
     w = Prefill(torch, dev, B, T)
     fp, fg = w.flops()
     ms_step = _time(torch, w.step, steps, warmup)
-    ms_seq = _time(torch, w.step_sequential, steps, max(1, warmup // 2))
+    ms_ovl = _time(torch, w.step_overlap, steps, max(1, warmup // 2))
     ms_polar = _time(torch, w.polar, steps, max(1, warmup // 2))
     ms_gdn = _time(torch, w.memory, steps, max(1, warmup // 2))
     res = dict(B=B, T=T, ms_per_step=ms_step, tflops=(fp + fg) / (ms_step * 1e-3) / 1e12,
-               ms_sequential=ms_seq,
+               ms_overlap=ms_ovl,
                polar_ms=ms_polar, polar_tflops=fp / (ms_polar * 1e-3) / 1e12,
                gdn_ms=ms_gdn, gdn_tflops=fg / (ms_gdn * 1e-3) / 1e12,
                polar_flops=fp, gdn_flops=fg)
@@ -307,9 +308,7 @@ def main(argv=None):
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-long", action="store_true", help="skip T=262,144")
-    ap.add_argument("--sequential", action="store_true",
-                    help="run the prefill step's two ops back to back on one stream (for "
-                         "per-kernel profiles without overlap)")
+
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build targets a single MI355X "
@@ -317,8 +316,6 @@ def main(argv=None):
         return 2
     import torch
     from atma_amd import _lib
-    if args.sequential:
-        Prefill.step = Prefill.step_sequential
     _lib.load()
     dev = torch.device("cuda:0")
     torch.backends.cuda.matmul.allow_tf32 = False
