@@ -47,13 +47,14 @@ __device__ __forceinline__ void upper_block(int blk, int& tp, int& ts) {
 
 template <typename T, int D>
 __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
-  constexpr int C = kChunk, KP = D + 8, CP = C + 8, FP = C + 1;
+  constexpr int C = kChunk, KP = D + 8, CP = C + 8, FP = C + 4;
   constexpr int DC = D / 8;           // 16-byte chunks per row
   constexpr int NE = (C / 4) * DC;    // (4 tokens x 8 dims) groups
   constexpr int RB = (C * KP > D * CP) ? C * KP : D * CP;
   __shared__ __attribute__((aligned(16))) T R1[RB];  // Kn rows, then (beta ge Kn)^T
   __shared__ __attribute__((aligned(16))) T R2[RB];  // Qn rows, then (beta V)^T
-  __shared__ float Af[C * FP], Tf[C * FP];
+  __shared__ __attribute__((aligned(16))) float Af[C * FP];
+  __shared__ float Tf[C * FP];
   __shared__ float Yf[3 * 256];
   __shared__ float lg[C], bet[C], sge[C], stl[C];
 
@@ -132,30 +133,38 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
   }
   __syncthreads();
 
-  // ---- Gram tiles: 10 lower-triangle (tp >= ts) tiles of Kn Kn^T and of Qn Kn^T
+  // ---- Gram tiles, transposed: for the 10 lower-triangle block pairs (tp >= ts) the
+  // tile rows are keys s (16 ts + 4g + i) and the columns tokens p (16 tp + c16), so a
+  // lane holds 4 consecutive s of one row p: one 16-byte LDS write of A[p][s..s+3] and
+  // one 8-byte store of rq[p][s..s+3].
   for (int task = wave; task < 20; task += 4) {
     const int which = task / 10, idx = task % 10;
     const int tp = (idx >= 1) + (idx >= 3) + (idx >= 6);
     const int ts = idx - tp * (tp + 1) / 2;
-    const T* arow = (which ? R2 : R1) + (16 * tp + c16) * KP + 8 * g;
-    const T* brow = R1 + (16 * ts + c16) * KP + 8 * g;
+    const T* arow = R1 + (16 * ts + c16) * KP + 8 * g;
+    const T* brow = (which ? R2 : R1) + (16 * tp + c16) * KP + 8 * g;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < D / 32; ++s) acc = mfma16x16x32<T>(lds16(arow + 32 * s), lds16(brow + 32 * s), acc);
+    const int p = 16 * tp + c16, s0 = 16 * ts + 4 * g;
+    float v[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int p = 16 * tp + 4 * g + i, s = 16 * ts + c16;
-      const float dec = s <= p ? expf(lg[p] - lg[s]) : 0.f;
-      if (which == 0)
-        Af[p * FP + s] = s < p ? bet[p] * dec * acc[i] : 0.f;
-      else
-        ws16[W.rq(ri) + p * C + s] = (T)(s <= p ? dec * acc[i] : 0.f);
+      const int s = s0 + i;
+      const float dec = s <= p ? __builtin_amdgcn_exp2f((lg[p] - lg[s]) * kLog2e) : 0.f;
+      v[i] = which == 0 ? (s < p ? bet[p] * dec * acc[i] : 0.f) : dec * acc[i];
+    }
+    if (which == 0) {
+      *(f32x4*)(Af + p * FP + s0) = f32x4{v[0], v[1], v[2], v[3]};
+    } else {
+      *(u32x2*)(ws16 + W.rq(ri) + p * C + s0) = u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
     }
   }
-  for (int e = tid; e < 6 * 256; e += 256) {  // rq is zero above the block diagonal
+  for (int e = tid; e < 6 * 64; e += 256) {  // rq is zero above the block diagonal
     int tp, ts;
-    upper_block(e >> 8, tp, ts);
-    ws16[W.rq(ri) + (16 * tp + ((e >> 4) & 15)) * C + 16 * ts + (e & 15)] = (T)0.f;
+    upper_block(e >> 6, tp, ts);
+    const int r = (e >> 2) & 15, c4 = e & 3;
+    *(u32x2*)(ws16 + W.rq(ri) + (16 * tp + r) * C + 16 * ts + 4 * c4) = u32x2{0u, 0u};
   }
   if (act) {  // kdT = (diag(tail) Kn)^T from the row registers
     float tl[4];
@@ -208,26 +217,28 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
     Tf[(16 * tp + ((e >> 4) & 15)) * FP + 16 * ts + (e & 15)] = 0.f;
   }
   __syncthreads();
-  // ---- off-diagonal blocks: T_ij = -T_ii * sum_{k=j}^{i-1} A_ik T_kj, level L = i - j
+  // ---- off-diagonal blocks: T_ij = -T_ii * sum_{k=j}^{i-1} A_ik T_kj, level L = i - j,
+  // one wave per block, 16x16 products on v_mfma_f32_16x16x4f32 (full fp32)
   for (int L = 1; L < 4; ++L) {
-    const int nblk = 4 - L;
-    for (int e = tid; e < nblk * 256; e += 256) {
-      const int blk = e >> 8, r = (e >> 4) & 15, cc = e & 15;
-      const int i = L + blk, j = blk;
-      float y = 0.f;
+    if (wave < 4 - L) {
+      const int i = L + wave, j = wave;
+      f32x4 y = {0.f, 0.f, 0.f, 0.f};
       for (int kk = j; kk < i; ++kk)
 #pragma unroll
-        for (int m = 0; m < 16; ++m) y += Af[(16 * i + r) * FP + 16 * kk + m] * Tf[(16 * kk + m) * FP + 16 * j + cc];
-      Yf[e] = y;
-    }
-    __syncthreads();
-    for (int e = tid; e < nblk * 256; e += 256) {
-      const int blk = e >> 8, r = (e >> 4) & 15, cc = e & 15;
-      const int i = L + blk, j = blk;
-      float x = 0.f;
+        for (int st = 0; st < 4; ++st)
+          y = __builtin_amdgcn_mfma_f32_16x16x4f32(Af[(16 * i + c16) * FP + 16 * kk + 4 * st + g],
+                                                   Tf[(16 * kk + 4 * st + g) * FP + 16 * j + c16], y, 0, 0, 0);
+      float* yw = Yf + wave * 256;  // this wave's 16x16 scratch, [row][col]
 #pragma unroll
-      for (int m = 0; m < 16; ++m) x -= Tf[(16 * i + r) * FP + 16 * i + m] * Yf[blk * 256 + m * 16 + cc];
-      Tf[(16 * i + r) * FP + 16 * j + cc] = x;
+      for (int r = 0; r < 4; ++r) yw[(4 * g + r) * 16 + c16] = y[r];
+      wave_sync();
+      f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+        t = __builtin_amdgcn_mfma_f32_16x16x4f32(Tf[(16 * i + c16) * FP + 16 * i + 4 * st + g],
+                                                 yw[(4 * st + g) * 16 + c16], t, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Tf[(16 * i + 4 * g + r) * FP + 16 * j + c16] = -t[r];
     }
     __syncthreads();
   }
@@ -247,12 +258,13 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
     for (int ct = 0; ct < D / 16; ++ct) {
       f32x4 aw = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
       for (int s = 0; s < nsteps; ++s) {
-        aw = mfma16x16x32<T>(tfrag[s], lds16(R1 + (16 * ct + c16) * CP + 32 * s + 8 * g), aw);
+        // w^T = (beta ge Kn)^T T^T: the T fragment is the B operand here (same registers)
+        aw = mfma16x16x32<T>(lds16(R1 + (16 * ct + c16) * CP + 32 * s + 8 * g), tfrag[s], aw);
         au = mfma16x16x32<T>(tfrag[s], lds16(R2 + (16 * ct + c16) * CP + 32 * s + 8 * g), au);
       }
-      // w rows 16rb + 4g + i, column 16ct + c16;  u in the scan's register order
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ws16[W.w(ri) + (16 * rb + 4 * g + i) * D + 16 * ct + c16] = (T)aw[i];
+      // w row 16rb + c16, columns 16ct + 4g ..;  u in the scan's register order
+      *(u32x2*)(ws16 + W.w(ri) + (16 * rb + c16) * D + 16 * ct + 4 * g) =
+          u32x2{pack2<T>(aw[0], aw[1]), pack2<T>(aw[2], aw[3])};
       u32x2 pk = {pack2<T>(au[0], au[1]), pack2<T>(au[2], au[3])};
       *(u32x2*)(ws16 + W.us(ri) + (((ct >> 1) * 4 + rb) * 64 + lane) * 8 + (ct & 1) * 4) = pk;
     }

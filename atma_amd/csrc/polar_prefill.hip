@@ -21,8 +21,9 @@
 //    transposed ([d][key]) because the PV MFMA contracts over keys.  The next
 //    tile is prefetched into registers while the current one is consumed.
 //  * GQA is resolved in-kernel (kv head = q head / group), and the grid is
-//    ordered so the workgroups of one KV group and neighbouring query tiles land
-//    on the same XCD (shared L2), longest causal tiles first.
+//    ordered so the workgroups of one KV group land on the same XCD (shared L2).
+//    A workgroup runs two query tiles, the i-th longest and the i-th shortest of
+//    its head, so causal work is the same for every workgroup.
 //  * 16-bit inputs skip the per-block max: p is formed against the running max as
 //    it stands, and v_dot2 sums p and p^2 from the same 16-bit pairs the PV MFMA
 //    consumes; the max is taken (and the state rescaled) only when a lane's sum
@@ -99,7 +100,7 @@ __device__ __forceinline__ f32x16 mfma32(const u32x4& a, const u32x4& b, const f
 }
 
 template <typename T, int D>
-__global__ void __launch_bounds__(256, 1) polar_fwd_kernel(PolarFwdArgs args) {
+__global__ void __launch_bounds__(256, 2) polar_fwd_kernel(PolarFwdArgs args) {
   using Cfg = FwdCfg<T, D>;
   constexpr int BM = Cfg::BM, BN = Cfg::BN, VE = Cfg::VE, CPR = Cfg::CPR;
   constexpr int KP = Cfg::KP, VP = Cfg::VP, NT = Cfg::NT;
@@ -120,10 +121,17 @@ __global__ void __launch_bounds__(256, 1) polar_fwd_kernel(PolarFwdArgs args) {
   }
   const int g = bid % G;
   const int unit = bid / G;
-  const int qt = args.n_qtiles - 1 - unit % args.n_qtiles;
-  const int grp = unit / args.n_qtiles;  // b * Hkv + kv head
+  // A workgroup takes a pair of query tiles, the i-th longest and the i-th shortest
+  // of its head, so under a causal mask every pair costs the same number of key
+  // blocks: the grid has no long tail.
+  const int npairs = (args.n_qtiles + 1) / 2;
+  const int pair = unit % npairs;
+  const int grp = unit / npairs;  // b * Hkv + kv head
   const int b = grp / args.Hkv, hk = grp % args.Hkv;
   const int hq = hk * G + g;
+  const int npass = pair < args.n_qtiles - 1 - pair ? 2 : 1;
+  for (int pass = 0; pass < npass; ++pass) {
+  const int qt = pass == 0 ? args.n_qtiles - 1 - pair : pair;
   const int q0 = qt * BM;
 
   const T* qp = (const T*)args.q + b * args.q_sb + hq * args.q_sh;
@@ -525,11 +533,13 @@ __global__ void __launch_bounds__(256, 1) polar_fwd_kernel(PolarFwdArgs args) {
         }
     }
   }
+  __syncthreads();  // the next pass reuses the LDS tiles and bounds
+  }  // pass
 }
 
 template <typename T, int D>
 static int launch_fwd(PolarFwdArgs a, hipStream_t stream) {
-  const int64_t units = (int64_t)a.n_qtiles * a.B * a.Hq;
+  const int64_t units = (int64_t)((a.n_qtiles + 1) / 2) * a.B * a.Hq;
   const int G = a.Hq / a.Hkv;
   a.xcd_remap = (units % (8 * G) == 0) ? 1 : 0;
   polar_fwd_kernel<T, D><<<dim3((unsigned)units), dim3(256), 0, stream>>>(a);
