@@ -116,6 +116,40 @@ __device__ __forceinline__ void dma_load16(const void* gptr, const void* lds_wav
                : "memory");
 }
 
+// The same copy through a buffer descriptor (buffer_load_dwordx4 ... lds): lane i
+// reads 16 bytes at voff + soff of the buffer (zeros past its size) into
+// lds_wave_base + 16*i.  The address arithmetic stays in one 32-bit offset per lane
+// and one scalar offset, so per-copy cost is a scalar move into m0.
+__device__ __forceinline__ void dma_buf16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                          const void* lds_wave_base) {
+  const uint32_t off =
+      (uint32_t)(size_t)((__attribute__((address_space(3))) const void*)lds_wave_base);
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff),
+               "{m0}"(__builtin_amdgcn_readfirstlane(off))
+               : "memory");
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding (the
+// compiler does not count the inline-asm direct-to-LDS loads above).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+// LDS writes of this wave done, then a workgroup barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives element i % 4
+// of the 64-bit words read by lanes i / 4, i / 4 + 4, i / 4 + 8, i / 4 + 12 (in that
+// order).  With lane s reading row r0 + s / 4, columns c0 + 4 (s % 4) .. + 3 of a
+// row-major 16-bit matrix, lane i gets rows r0 .. r0 + 3 of column c0 + i.
+__device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)p);
+  return __builtin_bit_cast(u32x2, r);
+}
+
 // Wave-local barrier: orders LDS traffic between lanes of one wavefront.
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -537,12 +537,346 @@ __global__ void __launch_bounds__(256, 2) polar_fwd_kernel(PolarFwdArgs args) {
   }  // pass
 }
 
+// 16-bit inputs.  Same math and wave layout as polar_fwd_kernel, with the key / value
+// tiles staged by direct global->LDS copies (global_load_lds_dwordx4, no VGPR
+// staging, no commit pass): K and V both row-major in LDS, unpadded, their 16-byte
+// chunks XOR-swizzled by row (chunk c of row r at c ^ (r % CPR)) so the operand reads
+// below are bank-conflict free.  V^T, the A operand of O^T = V^T P^T, comes out of
+// the row-major V tile through ds_read_b64_tr_b16 (two per operand: keys +0..3 and
+// +4..7).  A wave copies its 16 rows of the next block while the current one is
+// consumed; one barrier per block.
+template <typename T, int D>
+__global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) {
+  constexpr int BM = 128, BN = 64, CPR = D / 8, NT = D / 32, QSTEPS = D / 16;
+  constexpr int RPI = 64 / CPR;            // rows per wave copy instruction (1 KB)
+  constexpr int TILE = BN * D;             // elements of one K or V tile
+  static_assert(BN / 4 % RPI == 0, "a wave copies whole rows");
+  __shared__ __attribute__((aligned(16))) T Ks[2 * TILE];
+  __shared__ __attribute__((aligned(16))) T Vs[2 * TILE];
+  __shared__ float s_bounds[4][2];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ql = lane & 31, h = lane >> 5;
+
+  // ---- workgroup -> (b, q head, pair of query tiles), XCD-aware
+  const int G = args.Hq / args.Hkv;
+  int bid = blockIdx.x;
+  if (args.xcd_remap) {
+    const int x = bid & 7, p = bid >> 3;
+    bid = (x + 8 * (p / G)) * G + p % G;
+  }
+  const int g = bid % G;
+  const int unit = bid / G;
+  const int npairs = (args.n_qtiles + 1) / 2;
+  const int pair = unit % npairs;
+  const int grp = unit / npairs;  // b * Hkv + kv head
+  const int b = grp / args.Hkv, hk = grp % args.Hkv;
+  const int hq = hk * G + g;
+  const int npass = pair < args.n_qtiles - 1 - pair ? 2 : 1;
+  for (int pass = 0; pass < npass; ++pass) {
+  const int qt = pass == 0 ? args.n_qtiles - 1 - pair : pair;
+  const int q0 = qt * BM;
+
+  const T* qp = (const T*)args.q + b * args.q_sb + hq * args.q_sh;
+  const T* kp = (const T*)args.k + b * args.k_sb + hk * args.k_sh;
+  const T* vp = (const T*)args.v + b * args.v_sb + hk * args.v_sh;
+
+  // ---- per-query calibration (lane pair owns query row qi)
+  const int qi = q0 + wave * 32 + ql;
+  const bool q_ok = qi < args.Tq;
+  const float n_raw = q_ok ? args.n_keys[qi] : 0.f;
+  float n_cal = n_raw;
+  if (args.window > 0) n_cal = fminf(n_cal, (float)args.window);
+  n_cal = fmaxf(n_cal, 1.f);
+  const float spg = softplus(args.len_gain_raw[hq]);
+  const float sps = softplus(args.null_slope_raw[hq]);
+  const float nb = args.null_base[hq];
+  const float mbeta = softplus(args.mag_beta_raw[hq]);
+  const float temp = 1.f + spg * logf(n_cal);
+  const float nullv = nb + sps * sqrtf(logf(n_cal + 1.f));
+  const float c1 = temp * kLog2e * (1.f / sqrtf((float)D));
+
+  // ---- key-loop bounds from the valid counts of this tile (raw n, window band)
+  {
+    float lo = q_ok ? n_raw : 3.0e38f, hi = q_ok ? n_raw : -1.f;
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    if (lane == 0) {
+      s_bounds[wave][0] = lo;
+      s_bounds[wave][1] = hi;
+    }
+  }
+  __syncthreads();
+  const float w_nlo = s_bounds[wave][0], w_nhi = s_bounds[wave][1];
+  float g_nlo = s_bounds[0][0], g_nhi = s_bounds[0][1];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) {
+    g_nlo = fminf(g_nlo, s_bounds[w][0]);
+    g_nhi = fmaxf(g_nhi, s_bounds[w][1]);
+  }
+  int kend = 0, kbeg = 0;
+  if (g_nhi > 0.f) {
+    float hiF = fminf(g_nhi, (float)args.Tk);
+    kend = (int)ceilf(hiF);
+    if (args.is_causal) kend = min(kend, min(q0 + BM, args.Tk));
+    if (args.window > 0) kbeg = max((int)floorf(g_nlo) - args.window, 0);
+    kbeg = (kbeg / BN) * BN;
+  }
+  const int nblk_beg = kbeg / BN, nblk_end = (kend + BN - 1) / BN;
+
+  // ---- query operand (B of S^T) in registers, consumed before the key loop
+  u32x4 qreg16[QSTEPS];
+#pragma unroll
+  for (int s = 0; s < QSTEPS; ++s)
+    qreg16[s] = q_ok ? *(const u32x4*)(qp + (int64_t)qi * args.q_st + 16 * s + 8 * h)
+                     : u32x4{0, 0, 0, 0};
+#pragma unroll
+  for (int s = 0; s < QSTEPS; ++s) asm volatile("" ::"v"(qreg16[s]));
+
+  float m_run = kSentinel, l_part = 0.f, q2_part = 0.f;
+  f32x16 oacc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) oacc[t] = f32x16{};
+
+  // ---- direct copies of one key block: this wave's rows 16 wave .. 16 wave + 15 of K
+  // and V, RPI rows per instruction; lane l lands at chunk position l % CPR of row
+  // l / CPR and fetches the logical chunk stored there.  The buffer ends after the
+  // last key row, so rows past Tk read as zeros (finite; their scores are masked and
+  // their p is exactly 0).  Per lane: one byte offset per copy instruction (the swizzle
+  // depends on the row only through RPI r + l / CPR, the same for every wave).
+  const uint32_t kst2 = (uint32_t)args.k_st * 2u, vst2 = (uint32_t)args.v_st * 2u;
+  const uint32_t lrow = (uint32_t)(lane / CPR);
+  constexpr int NCP = BN / 4 / RPI;  // copy instructions per wave and tensor
+  uint32_t coff[NCP];
+#pragma unroll
+  for (int r = 0; r < NCP; ++r) coff[r] = 16u * ((lane % CPR) ^ ((RPI * r + lane / CPR) % CPR));
+  const uint32_t krow_off = lrow * kst2, vrow_off = lrow * vst2;
+  auto copy_block = [&](int blk, int buf) {
+    const int rows = min(args.Tk - blk * BN, BN);
+    const auto krs = buffer_rsrc(kp + (int64_t)blk * BN * args.k_st,
+                                 (uint32_t)((rows - 1) * args.k_st + D) * 2u);
+    const auto vrs = buffer_rsrc(vp + (int64_t)blk * BN * args.v_st,
+                                 (uint32_t)((rows - 1) * args.v_st + D) * 2u);
+#pragma unroll
+    for (int r = 0; r < NCP; ++r) {
+      const uint32_t row0 = 16u * wave + RPI * r;
+      dma_buf16(krs, krow_off + coff[r], row0 * kst2, Ks + buf * TILE + row0 * D);
+      dma_buf16(vrs, vrow_off + coff[r], row0 * vst2, Vs + buf * TILE + row0 * D);
+    }
+  };
+  // element offset of logical chunk c of row r
+  auto swz = [](int r, int c) { return r * D + 8 * (c ^ (r % CPR)); };
+
+  const int nblk = nblk_end - nblk_beg;
+  if (nblk > 0) copy_block(nblk_beg, 0);
+  const int arow = a_row_key(ql);
+  // V^T operand reads: lane group gq = lane / 16 holds d rows 16 (gq % 2) + (lane % 16)
+  // and keys 8 (gq / 2) + 0..7 of a 16-key step; lane s of the group reads key
+  // row + s / 4, columns 4 (s % 4) .. + 3 of its 16-column slice.
+  const int gq = lane >> 4, sl = lane & 15;
+  const int vkey = 8 * (gq >> 1) + (sl >> 2);
+  const int vcol = 16 * (gq & 1) + 4 * (sl & 3);
+
+  for (int it = 0; it < nblk; ++it) {
+    const int blk = nblk_beg + it, buf = it & 1;
+    const int k0 = blk * BN;
+    wait_vmcnt<0>();  // this wave's copies of block blk have landed
+    lds_barrier();    // everyone's have; everyone is done with buf ^ 1
+    if (it + 1 < nblk) copy_block(blk + 1, buf ^ 1);
+    const T* Kb = Ks + buf * TILE;
+    const T* Vb = Vs + buf * TILE;
+
+    // ---- S^T = K Q^T  (two 32-key tiles, their MFMA chains interleaved; the K
+    // fragments of step s + 1 are requested before the MFMAs of step s)
+    f32x16 sacc[2] = {f32x16{}, f32x16{}};
+    {
+      u32x4 kc0 = *(const u32x4*)(Kb + swz(arow, h));
+      u32x4 kc1 = *(const u32x4*)(Kb + swz(32 + arow, h));
+#pragma unroll
+      for (int s = 0; s < QSTEPS; ++s) {
+        u32x4 kn0, kn1;
+        if (s + 1 < QSTEPS) {
+          kn0 = *(const u32x4*)(Kb + swz(arow, 2 * (s + 1) + h));
+          kn1 = *(const u32x4*)(Kb + swz(32 + arow, 2 * (s + 1) + h));
+        }
+        sacc[0] = mfma32<T>(kc0, qreg16[s], sacc[0]);
+        sacc[1] = mfma32<T>(kc1, qreg16[s], sacc[1]);
+        kc0 = kn0;
+        kc1 = kn1;
+      }
+      // keep two fragment pairs in flight: 4 reads, then (2 MFMAs, 2 reads) per step
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+      for (int s = 0; s < QSTEPS - 1; ++s) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
+
+    // ---- online softmax: optimistic pass against the running max (see polar_fwd_kernel)
+    const bool full = (k0 + BN <= (int)fminf(w_nlo, (float)args.Tk)) &&
+                      (args.window <= 0 || (float)k0 >= w_nhi - (float)args.window);
+    if (!full) {
+      // key valid <=> key_lo <= key < key_hi (integer keys: key < n <=> key < ceil n,
+      // key >= x <=> key >= ceil x)
+      const float tkf = (float)args.Tk;
+      const int key_hi = (int)ceilf(fminf(n_raw, tkf)) - k0;
+      const int key_lo =
+          args.window > 0 ? (int)ceilf(fminf(n_raw - (float)args.window, tkf)) - k0 : -(1 << 30);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = st_key(j, i, h);
+          sacc[j][i] = (key < key_hi) & (key >= key_lo) ? sacc[j][i] : -INFINITY;
+        }
+    }
+    constexpr float kSafe = __is_same(T, bf16) ? 1048576.f : 16384.f;
+    u32x4 pb[4];
+    float ls = 0.f, qs = 0.f;
+    auto exp_pack = [&]() {
+      const float neg_m = -m_run;
+      ls = qs = 0.f;
+#pragma unroll
+      for (int ps = 0; ps < 4; ++ps) {
+        const int j = ps >> 1, base = 8 * (ps & 1);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[j][base + 2 * w], c1, neg_m));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[j][base + 2 * w + 1], c1, neg_m));
+          pb[ps][w] = pack2<T>(p0, p1);
+        }
+      }
+      const uint32_t one2 = pack2<T>(1.f, 1.f);
+#pragma unroll
+      for (int ps = 0; ps < 4; ++ps)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          ls = dot2<T>(pb[ps][w], one2, ls);
+          qs = dot2<T>(pb[ps][w], pb[ps][w], qs);
+        }
+    };
+    exp_pack();
+    if (__ballot(!(ls <= kSafe)) != 0) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[j][i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run, mx * c1);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_part *= alpha;
+      q2_part *= alpha * alpha;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) oacc[t] *= alpha;
+      exp_pack();
+    }
+    l_part += ls;
+    q2_part += qs;
+
+    // ---- O^T += V^T P^T, V^T fragments by transposing reads of the row-major V tile,
+    // the next fragment requested before each MFMA
+    {
+      auto vfrag = [&](int t, int ps) {
+        const int kr = 16 * ps + vkey, col = 32 * t + vcol;
+        const u32x2 lo = lds_read_tr16(Vb + swz(kr, col >> 3) + (col & 7));
+        const u32x2 hi = lds_read_tr16(Vb + swz(kr + 4, col >> 3) + (col & 7));
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      };
+      u32x4 vc = vfrag(0, 0);
+#pragma unroll
+      for (int i = 0; i < 4 * NT; ++i) {
+        const int t = i % NT, ps = i / NT;  // alternate the NT accumulator chains
+        u32x4 vn;
+        if (i + 1 < 4 * NT) vn = vfrag((i + 1) % NT, (i + 1) / NT);
+        oacc[t] = mfma32<T>(vc, pb[ps], oacc[t]);
+        vc = vn;
+      }
+    }
+  }
+
+  // ---- fold the null sink, normalise, magnitude
+  float L = l_part + __shfl_xor(l_part, 32, 64);
+  float Q2 = q2_part + __shfl_xor(q2_part, 32, 64);
+  const float an2 = temp * nullv * kLog2e;
+  const float mn = fmaxf(m_run, an2);
+  const float al = exp2f(m_run - mn);
+  L *= al;
+  Q2 *= al * al;
+  const float pn = exp2f(an2 - mn);
+  const float Z = L + pn;
+  const float* vn = args.v_null + (int64_t)hq * D;
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int d = 32 * t + 8 * (i >> 2) + 4 * h + (i & 3);
+      const float s = oacc[t][i] * al + pn * vn[d];
+      oacc[t][i] = s;
+      ss += s * s;
+    }
+  }
+  ss += __shfl_xor(ss, 32, 64);
+  const float inv = 1.f / fmaxf(sqrtf(ss), args.eps);
+  const float n_eff = L * L / fmaxf(Q2, 1e-30f);
+  const float m_eff = n_eff * (L / fmaxf(Z, args.eps));
+  const float magv = tanhf(mbeta * log1pf(m_eff));
+
+  if (q_ok) {
+    const int64_t row = ((int64_t)b * args.Hq + hq) * args.Tq + qi;
+    T* cp = (T*)args.c + row * D;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int d = 32 * t + 8 * gq + 4 * h;
+        if constexpr (true) {
+          u32x2 pk = {pack2<T>(oacc[t][4 * gq] * inv, oacc[t][4 * gq + 1] * inv),
+                      pack2<T>(oacc[t][4 * gq + 2] * inv, oacc[t][4 * gq + 3] * inv)};
+          *(u32x2*)(cp + d) = pk;
+        } else {
+          f32x4 x = {oacc[t][4 * gq] * inv, oacc[t][4 * gq + 1] * inv, oacc[t][4 * gq + 2] * inv,
+                     oacc[t][4 * gq + 3] * inv};
+          *(f32x4*)(cp + d) = x;
+        }
+      }
+    }
+    if (h == 0) {
+      ((T*)args.mag)[row] = (T)magv;
+      if (args.stat_m) args.stat_m[row] = mn * kLn2;
+      if (args.stat_l) args.stat_l[row] = L;
+      if (args.stat_q2) args.stat_q2[row] = Q2;
+    }
+    if (args.stat_s) {
+      float* sp = args.stat_s + row * D;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const int d = 32 * t + 8 * gq + 4 * h;
+          f32x4 x = {oacc[t][4 * gq], oacc[t][4 * gq + 1], oacc[t][4 * gq + 2], oacc[t][4 * gq + 3]};
+          *(f32x4*)(sp + d) = x;
+        }
+    }
+  }
+  __syncthreads();  // the next pass reuses the LDS tiles and bounds
+  }  // pass
+}
+
 template <typename T, int D>
 static int launch_fwd(PolarFwdArgs a, hipStream_t stream) {
   const int64_t units = (int64_t)((a.n_qtiles + 1) / 2) * a.B * a.Hq;
   const int G = a.Hq / a.Hkv;
   a.xcd_remap = (units % (8 * G) == 0) ? 1 : 0;
-  polar_fwd_kernel<T, D><<<dim3((unsigned)units), dim3(256), 0, stream>>>(a);
+  if constexpr (sizeof(T) == 2)
+    polar_fwd16_kernel<T, D><<<dim3((unsigned)units), dim3(256), 0, stream>>>(a);
+  else
+    polar_fwd_kernel<T, D><<<dim3((unsigned)units), dim3(256), 0, stream>>>(a);
   return check_launch("polar_attention_fwd");
 }
 
