@@ -545,6 +545,17 @@ __global__ void __launch_bounds__(256, 2) polar_fwd_kernel(PolarFwdArgs args) {
 // the row-major V tile through ds_read_b64_tr_b16 (two per operand: keys +0..3 and
 // +4..7).  A wave copies its 16 rows of the next block while the current one is
 // consumed; one barrier per block.
+// Chunk swizzle of the 16-bit K / V tiles in LDS: logical 16-byte chunk c of row r is
+// stored at chunk position c ^ f(r).  f is a bijection on r mod CPR, so the QK reads
+// (one chunk of 16 different rows per 16 lanes) hit 16 distinct chunk positions, and
+// f(r) >> 2 differs across any 4 consecutive rows 4k .. 4k + 3, so the transposing V
+// reads (4 rows x 4 adjacent chunks per 32 lanes) hit 16 distinct positions too.
+template <int CPR>
+__device__ __forceinline__ int lds_swizzle(int r) {
+  if constexpr (CPR == 16) return 4 * (r & 3) + ((r >> 2) & 3);
+  else return 2 * (r & 3) + ((r >> 2) & 1);
+}
+
 template <typename T, int D>
 __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) {
   constexpr int BM = 128, BN = 64, CPR = D / 8, NT = D / 32, QSTEPS = D / 16;
@@ -650,7 +661,7 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
   constexpr int NCP = BN / 4 / RPI;  // copy instructions per wave and tensor
   uint32_t coff[NCP];
 #pragma unroll
-  for (int r = 0; r < NCP; ++r) coff[r] = 16u * ((lane % CPR) ^ ((RPI * r + lane / CPR) % CPR));
+  for (int r = 0; r < NCP; ++r) coff[r] = 16u * ((lane % CPR) ^ lds_swizzle<CPR>(RPI * r + lane / CPR));
   const uint32_t krow_off = lrow * kst2, vrow_off = lrow * vst2;
   auto copy_block = [&](int blk, int buf) {
     const int rows = min(args.Tk - blk * BN, BN);
@@ -666,7 +677,7 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
     }
   };
   // element offset of logical chunk c of row r
-  auto swz = [](int r, int c) { return r * D + 8 * (c ^ (r % CPR)); };
+  auto swz = [](int r, int c) { return r * D + 8 * (c ^ lds_swizzle<CPR>(r)); };
 
   const int nblk = nblk_end - nblk_beg;
   if (nblk > 0) copy_block(nblk_beg, 0);
