@@ -129,6 +129,19 @@ __device__ __forceinline__ void dma_buf16(__amdgpu_buffer_rsrc_t r, uint32_t vof
                : "memory");
 }
 
+// 4 bytes per lane (buffer_load_dword ... lds): lane i's dword lands at lds_wave_base + 4*i.
+__device__ __forceinline__ void dma_buf4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                         const void* lds_wave_base) {
+  const uint32_t off =
+      (uint32_t)(size_t)((__attribute__((address_space(3))) const void*)lds_wave_base);
+  asm volatile("buffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff),
+               "{m0}"(__builtin_amdgcn_readfirstlane(off))
+               : "memory");
+}
+__device__ __forceinline__ void buffer_store16(__amdgpu_buffer_rsrc_t r, uint32_t voff, u32x4 x) {
+  __builtin_amdgcn_raw_buffer_store_b128(x, r, voff, 0, 0);
+}
+
 // Wait until at most N vector-memory operations of this wave are outstanding (the
 // compiler does not count the inline-asm direct-to-LDS loads above).
 template <int N>

@@ -36,9 +36,7 @@ struct GdnArgs {
 //   us  [D/32][4][64][8]  u = T diag(beta) V in the scan's register order: for column
 //               slab s, wave w, lane l = 16 g + c, entries vt*4 + i hold u at token
 //               16 w + 4 g + i, column 32 s + 16 vt + c (one 16-byte load per lane)
-//   unT [D][C]  U^T = (u - w S)^T; written by the scan
 //   rq  [C][C]  exp(lg_p - lg_s) qn_p . kn_s for s <= p, else 0
-//   sT  [D][D]  the state entering the chunk, transposed ([v][k]); written by the scan
 //   lg  [C]     the inclusive log-decays (fp32; lg_byte is a byte offset)
 // T = (I + A)^-1 with A[p,s] = beta_p exp(lg_p - lg_s) kn_p . kn_s (s < p), ge_p = exp(lg_p).
 struct Gdn16Ws {
@@ -49,12 +47,8 @@ struct Gdn16Ws {
   __host__ __device__ constexpr int64_t qn(int64_t i) const { return (n + i) * cd(); }
   __host__ __device__ constexpr int64_t kdT(int64_t i) const { return (2 * n + i) * cd(); }
   __host__ __device__ constexpr int64_t us(int64_t i) const { return (3 * n + i) * cd(); }
-  __host__ __device__ constexpr int64_t unT(int64_t i) const { return (4 * n + i) * cd(); }
-  __host__ __device__ constexpr int64_t rq(int64_t i) const { return 5 * n * cd() + i * kChunk * kChunk; }
-  __host__ __device__ constexpr int64_t sT(int64_t i) const {
-    return 5 * n * cd() + n * kChunk * kChunk + i * (int64_t)D * D;
-  }
-  __host__ __device__ constexpr int64_t lg_byte(int64_t i) const { return sT(n) * 2 + i * kChunk * 4; }
+  __host__ __device__ constexpr int64_t rq(int64_t i) const { return 4 * n * cd() + i * kChunk * kChunk; }
+  __host__ __device__ constexpr int64_t lg_byte(int64_t i) const { return rq(n) * 2 + i * kChunk * 4; }
   __host__ __device__ constexpr int64_t bytes() const { return lg_byte(n); }
 };
 

@@ -8,7 +8,8 @@
 //     O = diag(ge) Qn S + Rq U,          Rq[p,s] = exp(lg_p - lg_s) qn_p.kn_s (s <= p)
 //     S <- exp(lg_C) S + (diag(exp(lg_C - lg)) Kn)^T U
 // Everything that does not depend on S is computed chunk-parallel, so the
-// sequential pass only runs two dependent products per chunk:
+// sequential pass only runs two dependent products per chunk (plus two independent
+// ones for the output):
 //
 //  pass 1, gdn_prep16 -- one workgroup per (sequence, head, chunk): L2-normalise the
 //    rows, Gram blocks Kn Kn^T and Qn Kn^T on MFMA, T by a blocked fp32 inverse
@@ -18,13 +19,12 @@
 //
 //  pass 2, gdn_scan16 -- one workgroup per (sequence, head, 32-column slab of the
 //    [K, V] state), chunks in order.  The 128 x 32 fp32 slab stays in VGPRs; a 16-bit
-//    copy in LDS feeds the B operands.  Per chunk: U = u - w S, U^T to LDS, then
-//    S <- gC S + kdT U: two dependent products and two workgroup barriers.  The
-//    operands of the next three chunks are in flight into registers (A fragments
-//    straight from memory) during the math; the 16-bit state entering each chunk and
-//    U^T go to the record.
-//
-//  pass 3, gdn_out16 -- chunk-parallel again: O = diag(ge) Qn S_c + Rq U_c.
+//    copy in LDS feeds the B operands.  Per chunk: U = u - w S and O = diag(ge) Qn S,
+//    U^T to LDS, then S <- gC S + kdT U and O += Rq U: two dependent products and two
+//    workgroup barriers on the recurrence, the output products beside them.  The
+//    recurrence operands of the next three chunks are in flight into registers (A
+//    fragments straight from memory); qn, rq and lg of the next two chunks are copied
+//    straight into LDS.  The output slab leaves through LDS as 16-byte stores.
 #include "gated_delta.h"
 
 namespace atma {
@@ -271,20 +271,38 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
   }
 }
 
+// Swizzle of 16-byte chunks in the LDS copies of the qn / rq records: logical chunk c of
+// row r sits at chunk position c ^ f(r), so the 16 rows an A-fragment read touches (one
+// chunk each) fall in distinct banks: f(r) = r mod 16 for 256-byte rows, (r / 2) mod 8
+// for 128-byte rows (two rows share one 256-byte bank line).
+template <int CPR>
+__device__ __forceinline__ int rec_swizzle(int r) {
+  static_assert(CPR == 8 || CPR == 16, "64- or 128-element rows");
+  return CPR == 16 ? (r & 15) : ((r >> 1) & 7);
+}
+
 template <typename T, int D>
 __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
-  constexpr int C = kChunk, VS = 32, KP = D + 8, CP = C + 8;
+  constexpr int C = kChunk, VS = 32, KP = D + 8, CP = C + 8, OP = VS + 8;
   constexpr int KS = D / 32;   // MFMA k-steps over the head dim
   constexpr int KTW = D / 64;  // 16-row state tiles per wave
+  constexpr int QCPR = D / 8, RCPR = C / 8;  // 16-byte chunks per qn / rq row
+  constexpr int QB = C * D, RB = C * C;      // elements of one qn / rq record
   __shared__ __attribute__((aligned(16))) T Sb[VS * KP];  // S^T slab, 16-bit: [v][k]
   __shared__ __attribute__((aligned(16))) T Ub[VS * CP];  // U^T, 16-bit: [v][token]
+  __shared__ __attribute__((aligned(16))) T Qs[3 * QB];   // qn of chunk j in slot j % 3
+  __shared__ __attribute__((aligned(16))) T Rs[3 * RB];   // rq of chunk j in slot j % 3
+  __shared__ __attribute__((aligned(16))) float Lg[3 * C];
+  __shared__ __attribute__((aligned(16))) T Os[4 * 16 * OP];  // per-wave O tile, [row][v]
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c16 = lane & 15, g = lane >> 4;
   const int bh = blockIdx.x, v0 = blockIdx.y * VS;
+  const int b = bh / a.H, h = bh % a.H;
   const Gdn16Ws W{D, (int64_t)a.B * a.H * a.NC};
   const int64_t ri0 = (int64_t)bh * a.NC;
-  T* ws16 = (T*)a.ws;
+  const T* ws16 = (const T*)a.ws;
 
   // ---- state slab: tile (k-tile wave*KTW + j, v-tile vt); rows k = 16kt + 4g + i, cols v
   f32x4 S[KTW][2];
@@ -311,14 +329,39 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
       }
   };
 
-  // ---- one chunk's operands in registers (A fragments straight from memory).  Four
-  // sets rotate: a set is refilled with chunk c + 4 right after chunk c used it, so
-  // each load has three chunk steps to arrive and no set is ever copied.  Per chunk a
-  // wave issues 10 loads and 3 stores, so three chunks in flight stay well inside the
-  // 63 outstanding memory operations a wave can track.
+  // ---- qn, rq and lg of chunk j copied straight into LDS slot j % 3 (buffer DMA, no
+  // registers): wave w copies rows 16w .. 16w + 15 of qn and rq, wave 0 the 64 lg.
+  // Per wave 16 D / 512 + 2 copy instructions (+1 on wave 0).
+  constexpr int QRPI = 64 / QCPR, RRPI = 64 / RCPR;  // rows per copy instruction
+  constexpr int NQ = 16 / QRPI, NR = 16 / RRPI;
+  constexpr int NDMA = NQ + NR;  // copy instructions of waves 1..3 per chunk
+  constexpr int NLOAD = KS + 2 * KTW + 1;  // register loads per chunk
+  auto copy_rec = [&](int j, int slot) {
+    const int64_t ri = ri0 + j;
+    const auto qrs = buffer_rsrc(ws16 + W.qn(ri), QB * 2);
+    const auto rrs = buffer_rsrc(ws16 + W.rq(ri), RB * 2);
+#pragma unroll
+    for (int r = 0; r < NQ; ++r) {
+      const int row = 16 * wave + QRPI * r + lane / QCPR, pc = lane % QCPR;
+      const int lc = pc ^ rec_swizzle<QCPR>(row);
+      dma_buf16(qrs, (uint32_t)(row * D + 8 * lc) * 2u, 0, Qs + slot * QB + (16 * wave + QRPI * r) * D);
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const int row = 16 * wave + RRPI * r + lane / RCPR, pc = lane % RCPR;
+      const int lc = pc ^ rec_swizzle<RCPR>(row);
+      dma_buf16(rrs, (uint32_t)(row * C + 8 * lc) * 2u, 0, Rs + slot * RB + (16 * wave + RRPI * r) * C);
+    }
+    if (wave == 0)
+      dma_buf4(buffer_rsrc((const char*)a.ws + W.lg_byte(ri), C * 4), (uint32_t)lane * 4u, 0,
+               Lg + slot * C);
+  };
+
+  // ---- one chunk's recurrence operands in registers (A fragments straight from
+  // memory).  Four sets rotate: a set is refilled with chunk c + 4 right after chunk c
+  // used it, so each load has three chunk steps to arrive and no set is ever copied.
   struct Frag {
     u32x4 w[KS], k[KTW][2], u;
-    float lgc;
   };
   auto load = [&](Frag& f, int c) {
     const int64_t ri = ri0 + c;
@@ -331,42 +374,45 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
       for (int s = 0; s < 2; ++s)
         f.k[j][s] = *(const u32x4*)(ws16 + W.kdT(ri) + (16 * (wave * KTW + j) + c16) * C + 32 * s + 8 * g);
     f.u = *(const u32x4*)(ws16 + W.us(ri) + ((blockIdx.y * 4 + wave) * 64 + lane) * 8);
-    f.lgc = ((const float*)((const char*)a.ws + W.lg_byte(ri)))[C - 1];
   };
 
+  // this sequence's output rows as one buffer: rows past T are dropped
+  const auto orsrc = buffer_rsrc((const T*)a.o + (int64_t)b * a.T * a.H * D,
+                                 (uint32_t)((int64_t)a.T * a.H * D * 2));
+  const int last = a.NC - 1;
   auto body = [&](const Frag& f, int c) {
-    // ---- the state entering this chunk (16-bit, in Sb) to the record, 16 B per store
-    {
-      T* sT = ws16 + W.sT(ri0 + c);
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        const int e = tid + 256 * r, row = e >> 4, cc = e & 15;  // 32 rows x 16 chunks
-        if (D == 128 || cc < D / 8)
-          *(u32x4*)(sT + (v0 + row) * D + 8 * cc) = lds16(Sb + row * KP + 8 * cc);
-      }
-    }
-    // ---- U = u - w S (rows 16*wave + 4g + i, columns v0 + 16vt + c16)
+    const int slot = c % 3;
+    copy_rec(min(c + 2, last), (c + 2) % 3);  // the slot chunk c - 1 used
+    const int qrow = 16 * wave + c16;
+    const T* qs = Qs + slot * QB + qrow * D;
+    const T* rs = Rs + slot * RB + qrow * C;
+    const float* lgs = Lg + slot * C;
+    // ---- U = u - w S and O = diag(ge) Qn S (rows 16*wave + 4g + i, columns v0 + 16vt + c16)
+    f32x4 o[2];
 #pragma unroll
     for (int vt = 0; vt < 2; ++vt) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f}, oq = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
-        acc = mfma16x16x32<T>(f.w[s], lds16(Sb + (16 * vt + c16) * KP + 32 * s + 8 * g), acc);
+      for (int s = 0; s < KS; ++s) {
+        const u32x4 sb = lds16(Sb + (16 * vt + c16) * KP + 32 * s + 8 * g);
+        acc = mfma16x16x32<T>(f.w[s], sb, acc);
+        oq = mfma16x16x32<T>(lds16(qs + 8 * ((4 * s + g) ^ rec_swizzle<QCPR>(qrow))), sb, oq);
+      }
+      o[vt] = oq;
       float uv[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) uv[i] = elem16<T>(f.u, 4 * vt + i) - acc[i];
       const u32x2 pk = {pack2<T>(uv[0], uv[1]), pack2<T>(uv[2], uv[3])};
       *(u32x2*)(Ub + (16 * vt + c16) * CP + 16 * wave + 4 * g) = pk;
     }
+    const f32x4 lg4 = *(const f32x4*)(lgs + 16 * wave + 4 * g);
+#pragma unroll
+    for (int vt = 0; vt < 2; ++vt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[vt][i] *= expf(lg4[i]);
+    const float gC = expf(lgs[C - 1]);
     __syncthreads();
-    // ---- U^T to the record (32 rows x 8 chunks of 16 B)
-    {
-      T* unT = ws16 + W.unT(ri0 + c);
-      const int row = tid >> 3, cc = tid & 7;
-      *(u32x4*)(unT + (v0 + row) * C + 8 * cc) = lds16(Ub + row * CP + 8 * cc);
-    }
-    // ---- S = gC S + kdT U
-    const float gC = expf(f.lgc);
+    // ---- S = gC S + kdT U;  O += Rq U
 #pragma unroll
     for (int vt = 0; vt < 2; ++vt) {
       u32x4 uf[2];
@@ -379,20 +425,41 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
         for (int s = 0; s < 2; ++s) acc = mfma16x16x32<T>(f.k[j][s], uf[s], acc);
         S[j][vt] = acc;
       }
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        o[vt] = mfma16x16x32<T>(lds16(rs + 8 * ((4 * s + g) ^ rec_swizzle<RCPR>(qrow))), uf[s], o[vt]);
     }
     publish_state();
+    // ---- O tile (16 tokens x 32 columns) through LDS to one 16-byte store per lane
+    {
+      T* ow = Os + wave * 16 * OP;
+#pragma unroll
+      for (int vt = 0; vt < 2; ++vt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ow[(4 * g + i) * OP + 16 * vt + c16] = (T)o[vt][i];
+      wave_sync();
+      const int r = lane >> 2, q = lane & 3;
+      const uint32_t t = c * C + 16 * wave + r;
+      buffer_store16(orsrc, ((t * a.H + h) * D + v0 + 8 * q) * 2u, lds16(ow + r * OP + 8 * q));
+    }
+    // this wave's copies of chunk c + 1 (issued one chunk earlier) have landed: after
+    // them came the O store and the register loads of step c - 1, this step's copies
+    // and its O store (wave 0 issues one copy more, so the count is the smaller one)
+    wait_vmcnt<NDMA + NLOAD + 2>();
     __syncthreads();
   };
 
-  // (Past the last chunk the loads re-read it: every step issues the same loads in the
-  // same order, so the compiler's waits on them stay partial.)
-  const int last = a.NC - 1;
+  // (Past the last chunk the loads and copies re-read it: every step issues the same
+  // memory operations in the same order, so all waits on them stay partial.)
   publish_state();
+  copy_rec(0, 0);
+  copy_rec(min(1, last), 1);
   Frag f0, f1, f2, f3;
   load(f0, 0);
   load(f1, min(1, last));
   load(f2, min(2, last));
   load(f3, min(3, last));
+  wait_vmcnt<0>();
   __syncthreads();
   for (int c = 0; c < a.NC; c += 4) {
     body(f0, c);
@@ -420,73 +487,13 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
   }
 }
 
-// Output pass, chunk-parallel: O = diag(ge) Qn S_c + Rq U_c for every chunk from the
-// states and updates the scan published.  One workgroup per (chunk, sequence*head);
-// wave w owns rows 16w..16w+15 and all D columns.
-template <typename T, int D>
-__global__ void __launch_bounds__(256, 2) gdn_out16_kernel(GdnArgs a) {
-  constexpr int C = kChunk, SP = D + 8, UP = C + 8;
-  constexpr int KS = D / 32;
-  __shared__ __attribute__((aligned(16))) T Ss[D * SP];  // S_c^T [v][k]
-  __shared__ __attribute__((aligned(16))) T Us[D * UP];  // U_c^T [v][token]
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int c16 = lane & 15, g = lane >> 4;
-  const int c = blockIdx.x, bh = blockIdx.y;
-  const int b = bh / a.H, h = bh % a.H;
-  const Gdn16Ws W{D, (int64_t)a.B * a.H * a.NC};
-  const int64_t ri = (int64_t)bh * a.NC + c;
-  const T* ws16 = (const T*)a.ws;
-
-  for (int e = tid; e < D * D / 8; e += 256) {
-    const int r = e / (D / 8), cc = e % (D / 8);
-    *(u32x4*)(Ss + r * SP + 8 * cc) = *(const u32x4*)(ws16 + W.sT(ri) + r * D + 8 * cc);
-  }
-  for (int e = tid; e < D * C / 8; e += 256) {
-    const int r = e / (C / 8), cc = e % (C / 8);
-    *(u32x4*)(Us + r * UP + 8 * cc) = *(const u32x4*)(ws16 + W.unT(ri) + r * C + 8 * cc);
-  }
-  const int row = 16 * wave + c16;
-  u32x4 qf[KS], rf[2];
-#pragma unroll
-  for (int s = 0; s < KS; ++s) qf[s] = *(const u32x4*)(ws16 + W.qn(ri) + row * D + 32 * s + 8 * g);
-#pragma unroll
-  for (int s = 0; s < 2; ++s) rf[s] = *(const u32x4*)(ws16 + W.rq(ri) + row * C + 32 * s + 8 * g);
-  const float* lgp = (const float*)((const char*)a.ws + W.lg_byte(ri));
-  float ge[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) ge[i] = expf(lgp[16 * wave + 4 * g + i]);
-  __syncthreads();
-
-  // this sequence's output rows as one buffer: rows past T are dropped
-  const auto orsrc = buffer_rsrc((const T*)a.o + (int64_t)b * a.T * a.H * D,
-                                 (uint32_t)((int64_t)a.T * a.H * D * 2));
-#pragma unroll
-  for (int ct = 0; ct < D / 16; ++ct) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < KS; ++s) acc = mfma16x16x32<T>(qf[s], lds16(Ss + (16 * ct + c16) * SP + 32 * s + 8 * g), acc);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] *= ge[i];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) acc = mfma16x16x32<T>(rf[s], lds16(Us + (16 * ct + c16) * UP + 32 * s + 8 * g), acc);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t t = c * C + 16 * wave + 4 * g + i;
-      buffer_store16b<T>(orsrc, ((t * a.H + h) * D + 16 * ct + c16) * 2u, (T)acc[i]);
-    }
-  }
-}
-
 template <typename T, int D>
 static int launch16(const GdnArgs& a, hipStream_t s) {
   gdn_prep16_kernel<T, D><<<dim3((unsigned)a.NC, (unsigned)(a.B * a.H)), dim3(256), 0, s>>>(a);
   int rc = check_launch("chunk_gated_delta_rule(prep16)");
   if (rc) return rc;
   gdn_scan16_kernel<T, D><<<dim3((unsigned)(a.B * a.H), D / 32), dim3(256), 0, s>>>(a);
-  rc = check_launch("chunk_gated_delta_rule(scan16)");
-  if (rc) return rc;
-  gdn_out16_kernel<T, D><<<dim3((unsigned)a.NC, (unsigned)(a.B * a.H)), dim3(256), 0, s>>>(a);
-  return check_launch("chunk_gated_delta_rule(out16)");
+  return check_launch("chunk_gated_delta_rule(scan16)");
 }
 
 int launch_gdn16(const GdnArgs& a, int dtype, int D, hipStream_t s) {
