@@ -47,18 +47,18 @@ __device__ __forceinline__ void upper_block(int blk, int& tp, int& ts) {
 
 template <typename T, int D>
 __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
-  constexpr int C = kChunk, KP = D + 8, CP = C + 8, FP = C + 4;
+  constexpr int C = kChunk, KP = D + 8, FP = C + 4;
   constexpr int DC = D / 8;           // 16-byte chunks per row
   constexpr int NE = (C / 4) * DC;    // (4 tokens x 8 dims) groups
-  constexpr int RB = (C * KP > D * CP) ? C * KP : D * CP;
-  __shared__ __attribute__((aligned(16))) T R1[RB];  // Kn rows, then (beta ge Kn)^T
-  __shared__ __attribute__((aligned(16))) T R2[RB];  // Qn rows, then (beta V)^T
+  __shared__ __attribute__((aligned(16))) T R1[C * KP];  // Kn rows, then beta ge Kn rows
+  __shared__ __attribute__((aligned(16))) T R2[C * KP];  // Qn rows, then beta V rows
   __shared__ __attribute__((aligned(16))) float Af[C * FP];
   __shared__ float Tf[C * FP];
   __shared__ float Yf[3 * 256];
-  __shared__ float lg[C], bet[C], sge[C], stl[C];
+  __shared__ __attribute__((aligned(16))) float lg[C], bet[C], sge[C], stl[C];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
   const int c16 = lane & 15, g = lane >> 4;
   const int c = blockIdx.x, bh = blockIdx.y;
   const int b = bh / a.H, h = bh % a.H;
@@ -147,12 +147,17 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
 #pragma unroll
     for (int s = 0; s < D / 32; ++s) acc = mfma16x16x32<T>(lds16(arow + 32 * s), lds16(brow + 32 * s), acc);
     const int p = 16 * tp + c16, s0 = 16 * ts + 4 * g;
+    // decays and masks without branches (an overflowing exp above the diagonal is
+    // discarded by the select)
+    const float lgp = lg[p], bp = which == 0 ? bet[p] : 1.f;
+    const f32x4 lgs = *(const f32x4*)(lg + s0);
     float v[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int s = s0 + i;
-      const float dec = s <= p ? __builtin_amdgcn_exp2f((lg[p] - lg[s]) * kLog2e) : 0.f;
-      v[i] = which == 0 ? (s < p ? bet[p] * dec * acc[i] : 0.f) : dec * acc[i];
+      const float dec = __builtin_amdgcn_exp2f((lgp - lgs[i]) * kLog2e);
+      const bool keep = which == 0 ? s < p : s <= p;
+      v[i] = keep ? bp * dec * acc[i] : 0.f;
     }
     if (which == 0) {
       *(f32x4*)(Af + p * FP + s0) = f32x4{v[0], v[1], v[2], v[3]};
@@ -179,22 +184,15 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
   }
   __syncthreads();  // Gram done: R1 / R2 are free, A is complete
 
-  // ---- transposed, scaled operands of the w / u products
+  // ---- scaled operands of the w / u products, row-major like Kn (conflict-free writes;
+  // the products read them transposed)
   if (act) {
-    float fk[4], fv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      fv[i] = bet[4 * p4 + i];
-      fk[i] = fv[i] * sge[4 * p4 + i];
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      u32x2 pk = {pack2<T>(elem16<T>(kn[0], e) * fk[0], elem16<T>(kn[1], e) * fk[1]),
-                  pack2<T>(elem16<T>(kn[2], e) * fk[2], elem16<T>(kn[3], e) * fk[3])};
-      *(u32x2*)(R1 + (8 * dc + e) * CP + 4 * p4) = pk;
-      u32x2 pv = {pack2<T>(elem16<T>(vr[0], e) * fv[0], elem16<T>(vr[1], e) * fv[1]),
-                  pack2<T>(elem16<T>(vr[2], e) * fv[2], elem16<T>(vr[3], e) * fv[3])};
-      *(u32x2*)(R2 + (8 * dc + e) * CP + 4 * p4) = pv;
+      const int p = 4 * p4 + i;
+      const float fv = bet[p], fk = fv * sge[p];
+      *(u32x4*)(R1 + p * KP + 8 * dc) = scale8<T>(kn[i], fk);
+      *(u32x4*)(R2 + p * KP + 8 * dc) = scale8<T>(vr[i], fv);
     }
   }
   // ---- T = (I + A)^-1: diagonal 16x16 blocks by forward substitution (lane = column)
@@ -243,7 +241,9 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
     __syncthreads();
   }
 
-  // ---- w = T (beta ge Kn), u = T (beta V): wave = 16-row block of T, all column tiles
+  // ---- w = T (beta ge Kn), u = T (beta V): wave = 16-row block of T, all column tiles.
+  // Both products take 8 consecutive tokens of one head-dim column per lane from the
+  // row-major tiles: two transposing reads (ds_read_b64_tr_b16) of 4 tokens each.
   {
     const int rb = wave;
     const int nsteps = rb < 2 ? 1 : 2;  // T is lower triangular: later tokens are 0
@@ -254,13 +254,19 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
 #pragma unroll
       for (int w = 0; w < 4; ++w) tfrag[s][w] = pack2<T>(tr[2 * w], tr[2 * w + 1]);
     }
+    // lane (g, c16) reads token row 32 s + 8 g + c16 / 4 (+4), columns 16 ct + 4 (c16 % 4)
+    auto colfrag = [&](const T* R, int ct, int s) {
+      const T* p = R + (32 * s + 8 * g + (c16 >> 2)) * KP + 16 * ct + 4 * (c16 & 3);
+      const u32x2 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 4 * KP);
+      return u32x4{lo[0], lo[1], hi[0], hi[1]};
+    };
 #pragma unroll
     for (int ct = 0; ct < D / 16; ++ct) {
       f32x4 aw = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
       for (int s = 0; s < nsteps; ++s) {
         // w^T = (beta ge Kn)^T T^T: the T fragment is the B operand here (same registers)
-        aw = mfma16x16x32<T>(lds16(R1 + (16 * ct + c16) * CP + 32 * s + 8 * g), tfrag[s], aw);
-        au = mfma16x16x32<T>(tfrag[s], lds16(R2 + (16 * ct + c16) * CP + 32 * s + 8 * g), au);
+        aw = mfma16x16x32<T>(colfrag(R1, ct, s), tfrag[s], aw);
+        au = mfma16x16x32<T>(tfrag[s], colfrag(R2, ct, s), au);
       }
       // w row 16rb + c16, columns 16ct + 4g ..;  u in the scan's register order
       *(u32x2*)(ws16 + W.w(ri) + (16 * rb + c16) * D + 16 * ct + 4 * g) =
@@ -387,21 +393,31 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
     const T* qs = Qs + slot * QB + qrow * D;
     const T* rs = Rs + slot * RB + qrow * C;
     const float* lgs = Lg + slot * C;
-    // ---- U = u - w S and O = diag(ge) Qn S (rows 16*wave + 4g + i, columns v0 + 16vt + c16)
-    f32x4 o[2];
+    // ---- U = u - w S and O = diag(ge) Qn S (rows 16*wave + 4g + i, columns v0 + 16vt + c16);
+    // all B fragments of S and A fragments of Qn are requested before the first product
+    u32x4 sbf[2][KS], qf[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      qf[s] = lds16(qs + 8 * ((4 * s + g) ^ rec_swizzle<QCPR>(qrow)));
+#pragma unroll
+      for (int vt = 0; vt < 2; ++vt) sbf[vt][s] = lds16(Sb + (16 * vt + c16) * KP + 32 * s + 8 * g);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 acc[2], o[2];
+#pragma unroll
+    for (int vt = 0; vt < 2; ++vt) acc[vt] = o[vt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int vt = 0; vt < 2; ++vt) {
+        acc[vt] = mfma16x16x32<T>(f.w[s], sbf[vt][s], acc[vt]);
+        o[vt] = mfma16x16x32<T>(qf[s], sbf[vt][s], o[vt]);
+      }
 #pragma unroll
     for (int vt = 0; vt < 2; ++vt) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f}, oq = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const u32x4 sb = lds16(Sb + (16 * vt + c16) * KP + 32 * s + 8 * g);
-        acc = mfma16x16x32<T>(f.w[s], sb, acc);
-        oq = mfma16x16x32<T>(lds16(qs + 8 * ((4 * s + g) ^ rec_swizzle<QCPR>(qrow))), sb, oq);
-      }
-      o[vt] = oq;
       float uv[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) uv[i] = elem16<T>(f.u, 4 * vt + i) - acc[i];
+      for (int i = 0; i < 4; ++i) uv[i] = elem16<T>(f.u, 4 * vt + i) - acc[vt][i];
       const u32x2 pk = {pack2<T>(uv[0], uv[1]), pack2<T>(uv[2], uv[3])};
       *(u32x2*)(Ub + (16 * vt + c16) * CP + 16 * wave + 4 * g) = pk;
     }
@@ -412,23 +428,27 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
       for (int i = 0; i < 4; ++i) o[vt][i] *= expf(lg4[i]);
     const float gC = expf(lgs[C - 1]);
     __syncthreads();
-    // ---- S = gC S + kdT U;  O += Rq U
+    // ---- S = gC S + kdT U;  O += Rq U (fragments requested up front again)
+    u32x4 uf[2][2], rf[2];
 #pragma unroll
-    for (int vt = 0; vt < 2; ++vt) {
-      u32x4 uf[2];
+    for (int s = 0; s < 2; ++s) {
+      rf[s] = lds16(rs + 8 * ((4 * s + g) ^ rec_swizzle<RCPR>(qrow)));
 #pragma unroll
-      for (int s = 0; s < 2; ++s) uf[s] = lds16(Ub + (16 * vt + c16) * CP + 32 * s + 8 * g);
-#pragma unroll
-      for (int j = 0; j < KTW; ++j) {
-        f32x4 acc = S[j][vt] * gC;
-#pragma unroll
-        for (int s = 0; s < 2; ++s) acc = mfma16x16x32<T>(f.k[j][s], uf[s], acc);
-        S[j][vt] = acc;
-      }
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-        o[vt] = mfma16x16x32<T>(lds16(rs + 8 * ((4 * s + g) ^ rec_swizzle<RCPR>(qrow))), uf[s], o[vt]);
+      for (int vt = 0; vt < 2; ++vt) uf[vt][s] = lds16(Ub + (16 * vt + c16) * CP + 32 * s + 8 * g);
     }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int vt = 0; vt < 2; ++vt)
+#pragma unroll
+      for (int j = 0; j < KTW; ++j) S[j][vt] *= gC;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int vt = 0; vt < 2; ++vt) {
+#pragma unroll
+        for (int j = 0; j < KTW; ++j) S[j][vt] = mfma16x16x32<T>(f.k[j][s], uf[vt][s], S[j][vt]);
+        o[vt] = mfma16x16x32<T>(rf[s], uf[vt][s], o[vt]);
+      }
     publish_state();
     // ---- O tile (16 tokens x 32 columns) through LDS to one 16-byte store per lane
     {
