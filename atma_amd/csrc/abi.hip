@@ -22,6 +22,19 @@ int check_launch(const char* what) {
   return ATMA_OK;
 }
 
+int device_cu_count() {
+  static int cached[64];  // 0 = not yet queried; a racing second query writes the same value
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 int dtype_size(int dtype) {
   switch (dtype) {
     case ATMA_F32: return 4;

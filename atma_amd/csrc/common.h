@@ -194,6 +194,8 @@ __device__ __forceinline__ float wave_min(float x) {
 // ---------------------------------------------------------------- host side
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// Compute units of the current device (cached per device; 256 if the query fails).
+int device_cu_count();
 int dtype_size(int dtype);
 
 }  // namespace atma

@@ -25,6 +25,8 @@
 //    recurrence operands of the next three chunks are in flight into registers (A
 //    fragments straight from memory); qn, rq and lg of the next two chunks are copied
 //    straight into LDS.  The output slab leaves through LDS as 16-byte stores.
+#include <algorithm>
+
 #include "gated_delta.h"
 
 namespace atma {
@@ -60,34 +62,55 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
   const int c16 = lane & 15, g = lane >> 4;
-  const int c = blockIdx.x, bh = blockIdx.y;
-  const int b = bh / a.H, h = bh % a.H;
-  const int t0 = c * C;
   const Gdn16Ws W{D, (int64_t)a.B * a.H * a.NC};
-  const int64_t ri = (int64_t)bh * a.NC + c;
   T* ws16 = (T*)a.ws;
-
-  // ---- rows: thread (p4, dc) holds tokens 4p4..4p4+3, dims 8dc..8dc+7 of k, q, v
   const bool act = tid < NE;
   const int p4 = tid / DC, dc = tid % DC;
-  u32x4 kn[4], vr[4];
+
+  // ---- the rows of one (sequence, head, chunk) item: thread (p4, dc) holds tokens
+  // 4p4..4p4+3, dims 8dc..8dc+7 of k, q, v; threads < C one token's g and beta
+  struct Rows {
+    u32x4 k[4], q[4], v[4];
+    float gl, bt;
+  };
+  auto load_rows = [&](Rows& r, int item) {
+    const int bh = item / a.NC, c = item % a.NC;
+    const int b = bh / a.H, h = bh % a.H;
+    if (act) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t t = (int64_t)c * C + 4 * p4 + i;
+        const bool ok = t < a.T;
+        r.k[i] = ok ? *(const u32x4*)((const T*)a.k + b * a.k_sb + t * a.k_st + h * a.k_sh + 8 * dc)
+                    : u32x4{0, 0, 0, 0};
+        r.q[i] = ok ? *(const u32x4*)((const T*)a.q + b * a.q_sb + t * a.q_st + h * a.q_sh + 8 * dc)
+                    : u32x4{0, 0, 0, 0};
+        r.v[i] = ok ? *(const u32x4*)((const T*)a.v + b * a.v_sb + t * a.v_st + h * a.v_sh + 8 * dc)
+                    : u32x4{0, 0, 0, 0};
+      }
+    }
+    if (tid < C) {
+      const int tt = c * C + tid;
+      const int64_t gi = ((int64_t)b * a.T + tt) * a.H + h;
+      r.gl = tt < a.T ? a.g[gi] : 0.f;
+      r.bt = tt < a.T ? a.beta[gi] : 0.f;
+    }
+  };
+
+  auto process = [&](Rows& r, int item) {
+  const int bh = item / a.NC, c = item % a.NC;
+  const int64_t ri = (int64_t)bh * a.NC + c;
+  lds_barrier();  // the previous item is done with every LDS buffer
+  u32x4* kn = r.k;
+  u32x4* vr = r.v;
   if (act) {
-    u32x4 qv[4];
     float ks[4], qs[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int64_t t = t0 + 4 * p4 + i;
-      const bool ok = t < a.T;
-      kn[i] = ok ? *(const u32x4*)((const T*)a.k + b * a.k_sb + t * a.k_st + h * a.k_sh + 8 * dc)
-                 : u32x4{0, 0, 0, 0};
-      qv[i] = ok ? *(const u32x4*)((const T*)a.q + b * a.q_sb + t * a.q_st + h * a.q_sh + 8 * dc)
-                 : u32x4{0, 0, 0, 0};
-      vr[i] = ok ? *(const u32x4*)((const T*)a.v + b * a.v_sb + t * a.v_st + h * a.v_sh + 8 * dc)
-                 : u32x4{0, 0, 0, 0};
       ks[i] = qs[i] = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float x = elem16<T>(kn[i], e), y = elem16<T>(qv[i], e);
+        const float x = elem16<T>(kn[i], e), y = elem16<T>(r.q[i], e);
         ks[i] = fmaf(x, x, ks[i]);
         qs[i] = fmaf(y, y, qs[i]);
       }
@@ -105,17 +128,15 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
       const float iq = (a.l2norm ? 1.f / fmaxf(sqrtf(qs[i]), 1e-12f) : 1.f) * a.scale;
       const int p = 4 * p4 + i;
       kn[i] = scale8<T>(kn[i], ik);
-      const u32x4 qn = scale8<T>(qv[i], iq);
+      const u32x4 qn = scale8<T>(r.q[i], iq);
       *(u32x4*)(R1 + p * KP + 8 * dc) = kn[i];
       *(u32x4*)(R2 + p * KP + 8 * dc) = qn;
       *(u32x4*)(ws16 + W.qn(ri) + p * D + 8 * dc) = qn;
     }
   }
   if (tid < C) {
-    const int tt = t0 + tid;
-    const int64_t gi = ((int64_t)b * a.T + tt) * a.H + h;
-    lg[tid] = tt < a.T ? a.g[gi] : 0.f;
-    bet[tid] = tt < a.T ? a.beta[gi] : 0.f;
+    lg[tid] = r.gl;
+    bet[tid] = r.bt;
   }
   __syncthreads();
   if (wave == 0) {  // inclusive prefix sum of the log-decays
@@ -274,6 +295,21 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
       u32x2 pk = {pack2<T>(au[0], au[1]), pack2<T>(au[2], au[3])};
       *(u32x2*)(ws16 + W.us(ri) + (((ct >> 1) * 4 + rb) * 64 + lane) * 8 + (ct & 1) * 4) = pk;
     }
+  }
+  };
+
+  // ---- persistent: workgroup w takes items w, w + G, w + 2G, ...; the rows of the next
+  // item are in flight into the other register set while this one is processed
+  const int total = a.B * a.H * a.NC, step = gridDim.x;
+  Rows r0, r1;
+  int item = blockIdx.x;
+  if (item < total) load_rows(r0, item);
+  for (; item < total; item += 2 * step) {
+    if (item + step < total) load_rows(r1, item + step);
+    process(r0, item);
+    if (item + step >= total) break;
+    if (item + 2 * step < total) load_rows(r0, item + 2 * step);
+    process(r1, item + step);
   }
 }
 
@@ -509,7 +545,10 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
 
 template <typename T, int D>
 static int launch16(const GdnArgs& a, hipStream_t s) {
-  gdn_prep16_kernel<T, D><<<dim3((unsigned)a.NC, (unsigned)(a.B * a.H)), dim3(256), 0, s>>>(a);
+  // persistent prep: two workgroups per CU (its LDS footprint), each walking items
+  const int64_t items = (int64_t)a.NC * a.B * a.H;
+  const int64_t grid = std::min<int64_t>(items, 2 * (int64_t)device_cu_count());
+  gdn_prep16_kernel<T, D><<<dim3((unsigned)grid), dim3(256), 0, s>>>(a);
   int rc = check_launch("chunk_gated_delta_rule(prep16)");
   if (rc) return rc;
   gdn_scan16_kernel<T, D><<<dim3((unsigned)(a.B * a.H), D / 32), dim3(256), 0, s>>>(a);
