@@ -363,7 +363,7 @@ def main(argv=None):
         "config": {"workload": "configs[1]: global-layer prefill, Polar fwd + gated-delta chunked "
                                "(C=64, fp32 state from 0)", "B": 8, "T": 2048, "q_heads": HQ,
                    "kv_heads": HKV, "head_dim": D, "mfma_frac_of_bf16_peak": round(c2["mfma_frac"], 4)},
-        "roofline": {"bound": "mfma", "kernel": "polar_fwd_kernel<bf16,128>",
+        "roofline": {"bound": "mfma", "kernel": "polar_fwd16_kernel<bf16,128>",
                      "achieved": round(c2["polar_tflops"], 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(c2["polar_mfma_frac"], 4),
                      "traffic": _traffic()},

@@ -69,8 +69,11 @@ int atma_store_kvcache(const void* key, int64_t key_stride, const void* value,
  * v_null (Hq, d), null_base / null_slope_raw / len_gain_raw / mag_beta_raw (Hq,).
  * Outputs (dtype, contiguous): c (B, Hq, Tq, d), mag (B, Hq, Tq).  Optional fp32
  * saved statistics for a backward pass (any may be NULL): stat_m / stat_l /
- * stat_q2 (B, Hq, Tq) as the natural-log running max, sum p, sum p^2 after the null
- * fold, and stat_s (B, Hq, Tq, d) the unnormalised direction.
+ * stat_q2 (B, Hq, Tq) as a natural-log reference m with sum p and sum p^2 taken
+ * relative to it (p = exp(score - m)), after the null fold -- m is the running max
+ * for fp32 inputs and at most it (the kernel's rescaling point) for 16-bit inputs,
+ * so (m, sum p) fix the normaliser either way -- and stat_s (B, Hq, Tq, d) the
+ * unnormalised direction.
  * is_causal requires Tq == Tk and bounds each query tile's key loop at the tile's
  * last row (kernel/polar_triton.py:110-113,522-526).  window <= 0 disables the
  * sliding window.  d must be 64 or 128.
