@@ -97,7 +97,7 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
     }
   };
 
-  auto process = [&](Rows& r, int item) {
+  auto process = [&](Rows& r, int item, int next) {
   const int bh = item / a.NC, c = item % a.NC;
   const int64_t ri = (int64_t)bh * a.NC + c;
   lds_barrier();  // the previous item is done with every LDS buffer
@@ -158,32 +158,48 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
   // tile rows are keys s (16 ts + 4g + i) and the columns tokens p (16 tp + c16), so a
   // lane holds 4 consecutive s of one row p: one 16-byte LDS write of A[p][s..s+3] and
   // one 8-byte store of rq[p][s..s+3].
-  for (int task = wave; task < 20; task += 4) {
-    const int which = task / 10, idx = task % 10;
-    const int tp = (idx >= 1) + (idx >= 3) + (idx >= 6);
-    const int ts = idx - tp * (tp + 1) / 2;
-    const T* arow = R1 + (16 * ts + c16) * KP + 8 * g;
-    const T* brow = (which ? R2 : R1) + (16 * tp + c16) * KP + 8 * g;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  {
+    // this wave's 5 tasks (wave, wave + 4, ..., wave + 16) as independent MFMA chains
+    constexpr int NT = 5;
+    int tp_[NT], ts_[NT];
+    const T* ar[NT];
+    const T* br[NT];
 #pragma unroll
-    for (int s = 0; s < D / 32; ++s) acc = mfma16x16x32<T>(lds16(arow + 32 * s), lds16(brow + 32 * s), acc);
-    const int p = 16 * tp + c16, s0 = 16 * ts + 4 * g;
-    // decays and masks without branches (an overflowing exp above the diagonal is
-    // discarded by the select)
-    const float lgp = lg[p], bp = which == 0 ? bet[p] : 1.f;
-    const f32x4 lgs = *(const f32x4*)(lg + s0);
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int s = s0 + i;
-      const float dec = __builtin_amdgcn_exp2f((lgp - lgs[i]) * kLog2e);
-      const bool keep = which == 0 ? s < p : s <= p;
-      v[i] = keep ? bp * dec * acc[i] : 0.f;
+    for (int k = 0; k < NT; ++k) {
+      const int task = wave + 4 * k, which = task / 10, idx = task % 10;
+      tp_[k] = (idx >= 1) + (idx >= 3) + (idx >= 6);
+      ts_[k] = idx - tp_[k] * (tp_[k] + 1) / 2;
+      ar[k] = R1 + (16 * ts_[k] + c16) * KP + 8 * g;
+      br[k] = (which ? R2 : R1) + (16 * tp_[k] + c16) * KP + 8 * g;
     }
-    if (which == 0) {
-      *(f32x4*)(Af + p * FP + s0) = f32x4{v[0], v[1], v[2], v[3]};
-    } else {
-      *(u32x2*)(ws16 + W.rq(ri) + p * C + s0) = u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
+    f32x4 acc[NT];
+#pragma unroll
+    for (int k = 0; k < NT; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < D / 32; ++s)
+#pragma unroll
+      for (int k = 0; k < NT; ++k) acc[k] = mfma16x16x32<T>(lds16(ar[k] + 32 * s), lds16(br[k] + 32 * s), acc[k]);
+#pragma unroll
+    for (int k = 0; k < NT; ++k) {
+      const int which = (wave + 4 * k) / 10;
+      const int p = 16 * tp_[k] + c16, s0 = 16 * ts_[k] + 4 * g;
+      // decays and masks without branches (an overflowing exp above the diagonal is
+      // discarded by the select)
+      const float lgp = lg[p], bp = which == 0 ? bet[p] : 1.f;
+      const f32x4 lgs = *(const f32x4*)(lg + s0);
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int sx = s0 + i;
+        const float dec = __builtin_amdgcn_exp2f((lgp - lgs[i]) * kLog2e);
+        const bool keep = which == 0 ? sx < p : sx <= p;
+        v[i] = keep ? bp * dec * acc[k][i] : 0.f;
+      }
+      if (which == 0) {
+        *(f32x4*)(Af + p * FP + s0) = f32x4{v[0], v[1], v[2], v[3]};
+      } else {
+        *(u32x2*)(ws16 + W.rq(ri) + p * C + s0) = u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
+      }
     }
   }
   for (int e = tid; e < 6 * 64; e += 256) {  // rq is zero above the block diagonal
@@ -216,6 +232,8 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
       *(u32x4*)(R2 + p * KP + 8 * dc) = scale8<T>(vr[i], fv);
     }
   }
+  // the row registers are free from here: the next item's rows load during the inverse
+  if (next < a.B * a.H * a.NC) load_rows(r, next);
   // ---- T = (I + A)^-1: diagonal 16x16 blocks by forward substitution (lane = column)
   if (wave == 0) {
     const int bb = lane >> 4, cc = lane & 15;
@@ -299,18 +317,11 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
   };
 
   // ---- persistent: workgroup w takes items w, w + G, w + 2G, ...; the rows of the next
-  // item are in flight into the other register set while this one is processed
+  // item load while the current one finishes its inverse and w / u products
   const int total = a.B * a.H * a.NC, step = gridDim.x;
-  Rows r0, r1;
-  int item = blockIdx.x;
-  if (item < total) load_rows(r0, item);
-  for (; item < total; item += 2 * step) {
-    if (item + step < total) load_rows(r1, item + step);
-    process(r0, item);
-    if (item + step >= total) break;
-    if (item + 2 * step < total) load_rows(r0, item + 2 * step);
-    process(r1, item + step);
-  }
+  Rows r;
+  if ((int)blockIdx.x < total) load_rows(r, blockIdx.x);
+  for (int item = blockIdx.x; item < total; item += step) process(r, item, item + step);
 }
 
 // Swizzle of 16-byte chunks in the LDS copies of the qn / rq records: logical chunk c of
