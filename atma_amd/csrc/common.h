@@ -163,6 +163,18 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
   return __builtin_bit_cast(u32x2, r);
 }
 
+// Chunk swizzle of row-major 16-bit tiles in LDS (rows of CPR 16-byte chunks): logical
+// 16-byte chunk c of row r is stored at chunk position c ^ f(r).  f is a bijection on
+// r mod CPR, so row reads (one chunk of 16 different rows per 16 lanes) hit 16 distinct
+// chunk positions, and f(r) >> 2 differs across any 4 consecutive rows 4k .. 4k + 3, so
+// transposing reads (4 rows x 4 adjacent chunks per 32 lanes) hit 16 distinct positions
+// too.
+template <int CPR>
+__device__ __forceinline__ int lds_swizzle(int r) {
+  if constexpr (CPR == 16) return 4 * (r & 3) + ((r >> 2) & 3);
+  else return 2 * (r & 3) + ((r >> 2) & 1);
+}
+
 // Wave-local barrier: orders LDS traffic between lanes of one wavefront.
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -31,25 +31,25 @@ struct GdnArgs {
 // chunks of one head are adjacent in memory (element offsets in 16-bit units; C = 64
 // tokens, D = head dim):
 //   w   [C][D]  T diag(beta * ge) Kn      (the state's pull on each row's update)
-//   qn  [C][D]  normalised, scaled queries
-//   kdT [D][C]  (diag(exp(lg_C - lg)) Kn)^T   (write-back operand of the state update)
 //   us  [D/32][4][64][8]  u = T diag(beta) V in the scan's register order: for column
 //               slab s, wave w, lane l = 16 g + c, entries vt*4 + i hold u at token
 //               16 w + 4 g + i, column 32 s + 16 vt + c (one 16-byte load per lane)
 //   rq  [C][C]  exp(lg_p - lg_s) qn_p . kn_s for s <= p, else 0
-//   lg  [C]     the inclusive log-decays (fp32; lg_byte is a byte offset)
+//   f32 [3][C]  per token (fp32; f32_byte is a byte offset): lg, the inclusive
+//               log-decays; kf = exp(lg_C - lg) / |k| (the write-back weight of the raw
+//               key row, 1 / |k| only with l2norm); qs = scale / |q| (the raw query row's
+//               factor, 1 / |q| only with l2norm)
 // T = (I + A)^-1 with A[p,s] = beta_p exp(lg_p - lg_s) kn_p . kn_s (s < p), ge_p = exp(lg_p).
+// The scan reads q and k rows straight from the inputs and applies qs and kf itself.
 struct Gdn16Ws {
   int D;
   int64_t n;
   __host__ __device__ constexpr int64_t cd() const { return (int64_t)kChunk * D; }
   __host__ __device__ constexpr int64_t w(int64_t i) const { return i * cd(); }
-  __host__ __device__ constexpr int64_t qn(int64_t i) const { return (n + i) * cd(); }
-  __host__ __device__ constexpr int64_t kdT(int64_t i) const { return (2 * n + i) * cd(); }
-  __host__ __device__ constexpr int64_t us(int64_t i) const { return (3 * n + i) * cd(); }
-  __host__ __device__ constexpr int64_t rq(int64_t i) const { return 4 * n * cd() + i * kChunk * kChunk; }
-  __host__ __device__ constexpr int64_t lg_byte(int64_t i) const { return rq(n) * 2 + i * kChunk * 4; }
-  __host__ __device__ constexpr int64_t bytes() const { return lg_byte(n); }
+  __host__ __device__ constexpr int64_t us(int64_t i) const { return (n + i) * cd(); }
+  __host__ __device__ constexpr int64_t rq(int64_t i) const { return 2 * n * cd() + i * kChunk * kChunk; }
+  __host__ __device__ constexpr int64_t f32_byte(int64_t i) const { return rq(n) * 2 + i * 3 * kChunk * 4; }
+  __host__ __device__ constexpr int64_t bytes() const { return f32_byte(n); }
 };
 
 int launch_gdn16(const GdnArgs& a, int dtype, int D, hipStream_t stream);

@@ -362,6 +362,9 @@ extern "C" int atma_chunk_gated_delta_rule(
     return set_error(ATMA_ERR_INVALID, "chunk_gated_delta_rule: null pointer");
   if (es == 2 && T * H * dk * 2 >= (1ll << 32))  // one sequence's output rows form one buffer
     return set_error(ATMA_ERR_UNSUPPORTED, "chunk_gated_delta_rule: T*H*d too large for one sequence");
+  if (es == 2 && (q_st >= (1 << 24) || k_st >= (1 << 24) || q_st < dk || k_st < dk))
+    // the scan copies a chunk's q / k rows through one buffer descriptor each
+    return set_error(ATMA_ERR_UNSUPPORTED, "chunk_gated_delta_rule: q/k token stride out of range");
   const size_t need = atma_chunk_gated_delta_workspace_bytes(B, T, H, dk, dv, chunk, dtype);
   if (!workspace || workspace_bytes < need)
     return set_error(ATMA_ERR_WORKSPACE, "chunk_gated_delta_rule: workspace %zu < %zu bytes",

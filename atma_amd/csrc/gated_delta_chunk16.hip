@@ -57,7 +57,7 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
   __shared__ __attribute__((aligned(16))) float Af[C * FP];
   __shared__ float Tf[C * FP];
   __shared__ float Yf[3 * 256];
-  __shared__ __attribute__((aligned(16))) float lg[C], bet[C], sge[C], stl[C];
+  __shared__ __attribute__((aligned(16))) float lg[C], bet[C], sge[C], ikn[C], iqs[C];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
@@ -128,10 +128,12 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
       const float iq = (a.l2norm ? 1.f / fmaxf(sqrtf(qs[i]), 1e-12f) : 1.f) * a.scale;
       const int p = 4 * p4 + i;
       kn[i] = scale8<T>(kn[i], ik);
-      const u32x4 qn = scale8<T>(r.q[i], iq);
       *(u32x4*)(R1 + p * KP + 8 * dc) = kn[i];
-      *(u32x4*)(R2 + p * KP + 8 * dc) = qn;
-      *(u32x4*)(ws16 + W.qn(ri) + p * D + 8 * dc) = qn;
+      *(u32x4*)(R2 + p * KP + 8 * dc) = scale8<T>(r.q[i], iq);
+      if (dc == 0) {
+        ikn[p] = ik;
+        iqs[p] = iq;
+      }
     }
   }
   if (tid < C) {
@@ -149,8 +151,11 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
     lg[lane] = x;
     sge[lane] = expf(x);
     const float last = __shfl(x, 63, 64);
-    stl[lane] = expf(last - x);
-    ((float*)((char*)a.ws + W.lg_byte(ri)))[lane] = x;
+    const float tail = expf(last - x);
+    float* rec = (float*)((char*)a.ws + W.f32_byte(ri));
+    rec[lane] = x;
+    rec[C + lane] = tail * ikn[lane];
+    rec[2 * C + lane] = iqs[lane];
   }
   __syncthreads();
 
@@ -207,17 +212,6 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
     upper_block(e >> 6, tp, ts);
     const int r = (e >> 2) & 15, c4 = e & 3;
     *(u32x2*)(ws16 + W.rq(ri) + (16 * tp + r) * C + 16 * ts + 4 * c4) = u32x2{0u, 0u};
-  }
-  if (act) {  // kdT = (diag(tail) Kn)^T from the row registers
-    float tl[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) tl[i] = stl[4 * p4 + i];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      u32x2 pk = {pack2<T>(elem16<T>(kn[0], e) * tl[0], elem16<T>(kn[1], e) * tl[1]),
-                  pack2<T>(elem16<T>(kn[2], e) * tl[2], elem16<T>(kn[3], e) * tl[3])};
-      *(u32x2*)(ws16 + W.kdT(ri) + (8 * dc + e) * C + 4 * p4) = pk;
-    }
   }
   __syncthreads();  // Gram done: R1 / R2 are free, A is complete
 
@@ -339,14 +333,16 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
   constexpr int C = kChunk, VS = 32, KP = D + 8, CP = C + 8, OP = VS + 8;
   constexpr int KS = D / 32;   // MFMA k-steps over the head dim
   constexpr int KTW = D / 64;  // 16-row state tiles per wave
-  constexpr int QCPR = D / 8, RCPR = C / 8;  // 16-byte chunks per qn / rq row
-  constexpr int QB = C * D, RB = C * C;      // elements of one qn / rq record
-  __shared__ __attribute__((aligned(16))) T Sb[VS * KP];  // S^T slab, 16-bit: [v][k]
-  __shared__ __attribute__((aligned(16))) T Ub[VS * CP];  // U^T, 16-bit: [v][token]
-  __shared__ __attribute__((aligned(16))) T Qs[3 * QB];   // qn of chunk j in slot j % 3
-  __shared__ __attribute__((aligned(16))) T Rs[3 * RB];   // rq of chunk j in slot j % 3
-  __shared__ __attribute__((aligned(16))) float Lg[3 * C];
-  __shared__ __attribute__((aligned(16))) T Os[4 * 16 * OP];  // per-wave O tile, [row][v]
+  constexpr int QCPR = D / 8, RCPR = C / 8;  // 16-byte chunks per q / k and rq row
+  constexpr int QB = C * D, RB = C * C;      // elements of one q / k block and rq record
+  __shared__ __attribute__((aligned(16))) T Sb[VS * KP];   // S^T slab, 16-bit: [v][k]
+  __shared__ __attribute__((aligned(16))) T Ub[VS * CP];   // U^T, 16-bit: [v][token]
+  __shared__ __attribute__((aligned(16))) T Ubk[VS * CP];  // (diag(kf) U)^T
+  __shared__ __attribute__((aligned(16))) T Qs[3 * QB];    // raw q rows of chunk j in slot j % 3
+  __shared__ __attribute__((aligned(16))) T Kr[3 * QB];    // raw k rows of chunk j in slot j % 3
+  __shared__ __attribute__((aligned(16))) T Rs[3 * RB];    // rq of chunk j in slot j % 3
+  __shared__ __attribute__((aligned(16))) float Fs[3 * 3 * C];  // lg, kf, qs of chunk j
+  __shared__ __attribute__((aligned(16))) T Os[4 * 16 * OP];   // per-wave O tile, [row][v]
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -382,22 +378,29 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
       }
   };
 
-  // ---- qn, rq and lg of chunk j copied straight into LDS slot j % 3 (buffer DMA, no
-  // registers): wave w copies rows 16w .. 16w + 15 of qn and rq, wave 0 the 64 lg.
-  // Per wave 16 D / 512 + 2 copy instructions (+1 on wave 0).
+  // ---- raw q and k rows, rq and the per-token factors of chunk j, copied straight into
+  // LDS slot j % 3 (buffer DMA, no registers): wave w copies token rows 16w .. 16w + 15
+  // of q, k and rq, wave 0 the 3 x 64 factors.  Rows past T read as zeros.  q rows use
+  // the A-fragment swizzle, k rows the transposing-read swizzle (lds_swizzle).
   constexpr int QRPI = 64 / QCPR, RRPI = 64 / RCPR;  // rows per copy instruction
   constexpr int NQ = 16 / QRPI, NR = 16 / RRPI;
-  constexpr int NDMA = NQ + NR;  // copy instructions of waves 1..3 per chunk
-  constexpr int NLOAD = KS + 2 * KTW + 1;  // register loads per chunk
+  constexpr int NDMA = 2 * NQ + NR;  // copy instructions of waves 1..3 per chunk
+  constexpr int NLOAD = KS + 2;      // register loads per chunk (w, u, gC)
+  const uint32_t qst2 = (uint32_t)a.q_st * 2u, kst2 = (uint32_t)a.k_st * 2u;
   auto copy_rec = [&](int j, int slot) {
     const int64_t ri = ri0 + j;
-    const auto qrs = buffer_rsrc(ws16 + W.qn(ri), QB * 2);
+    const int rows = min(a.T - j * C, C);
+    const auto qrs = buffer_rsrc((const T*)a.q + b * a.q_sb + (int64_t)j * C * a.q_st + h * a.q_sh,
+                                 (uint32_t)((rows - 1) * a.q_st + D) * 2u);
+    const auto krs = buffer_rsrc((const T*)a.k + b * a.k_sb + (int64_t)j * C * a.k_st + h * a.k_sh,
+                                 (uint32_t)((rows - 1) * a.k_st + D) * 2u);
     const auto rrs = buffer_rsrc(ws16 + W.rq(ri), RB * 2);
 #pragma unroll
     for (int r = 0; r < NQ; ++r) {
       const int row = 16 * wave + QRPI * r + lane / QCPR, pc = lane % QCPR;
-      const int lc = pc ^ rec_swizzle<QCPR>(row);
-      dma_buf16(qrs, (uint32_t)(row * D + 8 * lc) * 2u, 0, Qs + slot * QB + (16 * wave + QRPI * r) * D);
+      const uint32_t lq = pc ^ rec_swizzle<QCPR>(row), lk = pc ^ lds_swizzle<QCPR>(row);
+      dma_buf16(qrs, row * qst2 + 16u * lq, 0, Qs + slot * QB + (16 * wave + QRPI * r) * D);
+      dma_buf16(krs, row * kst2 + 16u * lk, 0, Kr + slot * QB + (16 * wave + QRPI * r) * D);
     }
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
@@ -405,43 +408,44 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
       const int lc = pc ^ rec_swizzle<RCPR>(row);
       dma_buf16(rrs, (uint32_t)(row * C + 8 * lc) * 2u, 0, Rs + slot * RB + (16 * wave + RRPI * r) * C);
     }
-    if (wave == 0)
-      dma_buf4(buffer_rsrc((const char*)a.ws + W.lg_byte(ri), C * 4), (uint32_t)lane * 4u, 0,
-               Lg + slot * C);
+    if (wave == 0) {
+      const auto frs = buffer_rsrc((const char*)a.ws + W.f32_byte(ri), 3 * C * 4);
+#pragma unroll
+      for (int r = 0; r < 3; ++r)
+        dma_buf4(frs, (uint32_t)(r * C + lane) * 4u, 0, Fs + slot * 3 * C + r * C);
+    }
   };
 
   // ---- one chunk's recurrence operands in registers (A fragments straight from
   // memory).  Four sets rotate: a set is refilled with chunk c + 4 right after chunk c
   // used it, so each load has three chunk steps to arrive and no set is ever copied.
   struct Frag {
-    u32x4 w[KS], k[KTW][2], u;
+    u32x4 w[KS], u;
+    float lgc;
   };
   auto load = [&](Frag& f, int c) {
     const int64_t ri = ri0 + c;
     const int row = 16 * wave + c16;
 #pragma unroll
     for (int s = 0; s < KS; ++s) f.w[s] = *(const u32x4*)(ws16 + W.w(ri) + row * D + 32 * s + 8 * g);
-#pragma unroll
-    for (int j = 0; j < KTW; ++j)
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-        f.k[j][s] = *(const u32x4*)(ws16 + W.kdT(ri) + (16 * (wave * KTW + j) + c16) * C + 32 * s + 8 * g);
     f.u = *(const u32x4*)(ws16 + W.us(ri) + ((blockIdx.y * 4 + wave) * 64 + lane) * 8);
+    f.lgc = ((const float*)((const char*)a.ws + W.f32_byte(ri)))[C - 1];
   };
 
   // this sequence's output rows as one buffer: rows past T are dropped
   const auto orsrc = buffer_rsrc((const T*)a.o + (int64_t)b * a.T * a.H * D,
                                  (uint32_t)((int64_t)a.T * a.H * D * 2));
   const int last = a.NC - 1;
+  const int qrow = 16 * wave + c16;
   auto body = [&](const Frag& f, int c) {
     const int slot = c % 3;
     copy_rec(min(c + 2, last), (c + 2) % 3);  // the slot chunk c - 1 used
-    const int qrow = 16 * wave + c16;
     const T* qs = Qs + slot * QB + qrow * D;
     const T* rs = Rs + slot * RB + qrow * C;
-    const float* lgs = Lg + slot * C;
-    // ---- U = u - w S and O = diag(ge) Qn S (rows 16*wave + 4g + i, columns v0 + 16vt + c16);
-    // all B fragments of S and A fragments of Qn are requested before the first product
+    const T* kr = Kr + slot * QB;
+    const float* fs = Fs + slot * 3 * C;
+    // ---- U = u - w S and O = diag(ge qs) Q S (rows 16*wave + 4g + i, columns v0 + 16vt + c16);
+    // all B fragments of S and A fragments of Q are requested before the first product
     u32x4 sbf[2][KS], qf[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
@@ -460,40 +464,59 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
         acc[vt] = mfma16x16x32<T>(f.w[s], sbf[vt][s], acc[vt]);
         o[vt] = mfma16x16x32<T>(qf[s], sbf[vt][s], o[vt]);
       }
+    const f32x4 lg4 = *(const f32x4*)(fs + 16 * wave + 4 * g);
+    const f32x4 kf4 = *(const f32x4*)(fs + C + 16 * wave + 4 * g);
+    const f32x4 qs4 = *(const f32x4*)(fs + 2 * C + 16 * wave + 4 * g);
 #pragma unroll
     for (int vt = 0; vt < 2; ++vt) {
       float uv[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) uv[i] = elem16<T>(f.u, 4 * vt + i) - acc[vt][i];
       const u32x2 pk = {pack2<T>(uv[0], uv[1]), pack2<T>(uv[2], uv[3])};
+      const u32x2 pkk = {pack2<T>(uv[0] * kf4[0], uv[1] * kf4[1]), pack2<T>(uv[2] * kf4[2], uv[3] * kf4[3])};
       *(u32x2*)(Ub + (16 * vt + c16) * CP + 16 * wave + 4 * g) = pk;
+      *(u32x2*)(Ubk + (16 * vt + c16) * CP + 16 * wave + 4 * g) = pkk;
     }
-    const f32x4 lg4 = *(const f32x4*)(lgs + 16 * wave + 4 * g);
 #pragma unroll
-    for (int vt = 0; vt < 2; ++vt)
+    for (int i = 0; i < 4; ++i) {
+      const float sc = expf(lg4[i]) * qs4[i];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[vt][i] *= expf(lg4[i]);
-    const float gC = expf(lgs[C - 1]);
+      for (int vt = 0; vt < 2; ++vt) o[vt][i] *= sc;
+    }
+    const float gC = expf(f.lgc);
     __syncthreads();
-    // ---- S = gC S + kdT U;  O += Rq U (fragments requested up front again)
-    u32x4 uf[2][2], rf[2];
+    // ---- S = gC S + K^T diag(kf) U  (A fragments: raw k columns by transposing reads);
+    // O += Rq U
+    u32x4 uf[2][2], ukf[2][2], rf[2], kt_[KTW][2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       rf[s] = lds16(rs + 8 * ((4 * s + g) ^ rec_swizzle<RCPR>(qrow)));
 #pragma unroll
-      for (int vt = 0; vt < 2; ++vt) uf[vt][s] = lds16(Ub + (16 * vt + c16) * CP + 32 * s + 8 * g);
+      for (int vt = 0; vt < 2; ++vt) {
+        uf[vt][s] = lds16(Ub + (16 * vt + c16) * CP + 32 * s + 8 * g);
+        ukf[vt][s] = lds16(Ubk + (16 * vt + c16) * CP + 32 * s + 8 * g);
+      }
+      // lane (g, c16) reads token rows 32 s + 8 g + c16 / 4 (+4), columns 16 kt + 4 (c16 % 4)
+#pragma unroll
+      for (int jj = 0; jj < KTW; ++jj) {
+        const int kt = wave * KTW + jj, r0 = 32 * s + 8 * g + (c16 >> 2), col = 16 * kt + 4 * (c16 & 3);
+        const int c8 = col >> 3, e = col & 7;
+        const u32x2 lo = lds_read_tr16(kr + r0 * D + 8 * (c8 ^ lds_swizzle<QCPR>(r0)) + e);
+        const u32x2 hi = lds_read_tr16(kr + (r0 + 4) * D + 8 * (c8 ^ lds_swizzle<QCPR>(r0 + 4)) + e);
+        kt_[jj][s] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int vt = 0; vt < 2; ++vt)
 #pragma unroll
-      for (int j = 0; j < KTW; ++j) S[j][vt] *= gC;
+      for (int jj = 0; jj < KTW; ++jj) S[jj][vt] *= gC;
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
       for (int vt = 0; vt < 2; ++vt) {
 #pragma unroll
-        for (int j = 0; j < KTW; ++j) S[j][vt] = mfma16x16x32<T>(f.k[j][s], uf[vt][s], S[j][vt]);
+        for (int jj = 0; jj < KTW; ++jj) S[jj][vt] = mfma16x16x32<T>(kt_[jj][s], ukf[vt][s], S[jj][vt]);
         o[vt] = mfma16x16x32<T>(rf[s], uf[vt][s], o[vt]);
       }
     publish_state();
@@ -511,7 +534,7 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
     }
     // this wave's copies of chunk c + 1 (issued one chunk earlier) have landed: after
     // them came the O store and the register loads of step c - 1, this step's copies
-    // and its O store (wave 0 issues one copy more, so the count is the smaller one)
+    // and its O store (wave 0 issues more copies, so the count is the smaller one)
     wait_vmcnt<NDMA + NLOAD + 2>();
     __syncthreads();
   };

@@ -545,17 +545,6 @@ __global__ void __launch_bounds__(256, 2) polar_fwd_kernel(PolarFwdArgs args) {
 // the row-major V tile through ds_read_b64_tr_b16 (two per operand: keys +0..3 and
 // +4..7).  A wave copies its 16 rows of the next block while the current one is
 // consumed; one barrier per block.
-// Chunk swizzle of the 16-bit K / V tiles in LDS: logical 16-byte chunk c of row r is
-// stored at chunk position c ^ f(r).  f is a bijection on r mod CPR, so the QK reads
-// (one chunk of 16 different rows per 16 lanes) hit 16 distinct chunk positions, and
-// f(r) >> 2 differs across any 4 consecutive rows 4k .. 4k + 3, so the transposing V
-// reads (4 rows x 4 adjacent chunks per 32 lanes) hit 16 distinct positions too.
-template <int CPR>
-__device__ __forceinline__ int lds_swizzle(int r) {
-  if constexpr (CPR == 16) return 4 * (r & 3) + ((r >> 2) & 3);
-  else return 2 * (r & 3) + ((r >> 2) & 1);
-}
-
 template <typename T, int D>
 __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) {
   constexpr int BM = 128, BN = 64, CPR = D / 8, NT = D / 32, QSTEPS = D / 16;

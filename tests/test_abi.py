@@ -67,10 +67,10 @@ def test_validation_rejects_without_launch(lib):
                                            null, null, null, 1, 64, 2, 128, 128, 1, 1.0, 1, 32,
                                            null, 0, null) == 2
     assert lib.atma_chunk_gated_delta_workspace_bytes(1, 65, 2, 128, 128, 64, 0) == 2 * 2 * (5 * 64 * 128 + 4) * 4
-    # 16-bit path: per (sequence, head, chunk) w, qn, kdT, u (C x d each) and rq (C x C)
-    # in 16 bits, then C fp32 log-decays
+    # 16-bit path: per (sequence, head, chunk) w, u (C x d each) and rq (C x C) in 16
+    # bits, then 3 x C fp32 per-token factors (log-decay, key and query weights)
     assert lib.atma_chunk_gated_delta_workspace_bytes(1, 65, 2, 128, 128, 64, 1) == \
-        2 * 2 * ((4 * 64 * 128 + 64 * 64) * 2 + 64 * 4)
+        2 * 2 * ((2 * 64 * 128 + 64 * 64) * 2 + 3 * 64 * 4)
     # gated delta step: unsupported dims
     assert lib.atma_gated_delta_decode_step(null, 0, 0, null, 0, 0, null, 0, 0, null, null, null, 1,
                                             null, null, 1, 1, 96, 96, 1, 1e-12, null) == 2
