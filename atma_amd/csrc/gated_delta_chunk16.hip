@@ -439,7 +439,6 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
   const int qrow = 16 * wave + c16;
   auto body = [&](const Frag& f, int c) {
     const int slot = c % 3;
-    copy_rec(min(c + 2, last), (c + 2) % 3);  // the slot chunk c - 1 used
     const T* qs = Qs + slot * QB + qrow * D;
     const T* rs = Rs + slot * RB + qrow * C;
     const T* kr = Kr + slot * QB;
@@ -532,10 +531,13 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
       const uint32_t t = c * C + 16 * wave + r;
       buffer_store16(orsrc, ((t * a.H + h) * D + v0 + 8 * q) * 2u, lds16(ow + r * OP + 8 * q));
     }
-    // this wave's copies of chunk c + 1 (issued one chunk earlier) have landed: after
-    // them came the O store and the register loads of step c - 1, this step's copies
-    // and its O store (wave 0 issues more copies, so the count is the smaller one)
-    wait_vmcnt<NDMA + NLOAD + 2>();
+    // copies of chunk c + 2 into the slot chunk c - 1 used (its readers are past the
+    // barrier that began this step)
+    copy_rec(min(c + 2, last), (c + 2) % 3);
+    // this wave's copies of chunk c + 1 (issued one step earlier) have landed: after them
+    // came the register loads of step c - 1, this step's O store and its copies (wave 0
+    // issues more copies, so the count is the smaller one)
+    wait_vmcnt<NDMA + NLOAD + 1>();
     __syncthreads();
   };
 
