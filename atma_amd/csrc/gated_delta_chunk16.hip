@@ -385,7 +385,7 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
   constexpr int QRPI = 64 / QCPR, RRPI = 64 / RCPR;  // rows per copy instruction
   constexpr int NQ = 16 / QRPI, NR = 16 / RRPI;
   constexpr int NDMA = 2 * NQ + NR;  // copy instructions of waves 1..3 per chunk
-  constexpr int NLOAD = KS + 2;      // register loads per chunk (w, u, gC)
+  constexpr int NLOAD = KS + 1;      // register loads per chunk (w, u)
   const uint32_t qst2 = (uint32_t)a.q_st * 2u, kst2 = (uint32_t)a.k_st * 2u;
   auto copy_rec = [&](int j, int slot) {
     const int64_t ri = ri0 + j;
@@ -421,7 +421,6 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
   // used it, so each load has three chunk steps to arrive and no set is ever copied.
   struct Frag {
     u32x4 w[KS], u;
-    float lgc;
   };
   auto load = [&](Frag& f, int c) {
     const int64_t ri = ri0 + c;
@@ -429,7 +428,6 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
 #pragma unroll
     for (int s = 0; s < KS; ++s) f.w[s] = *(const u32x4*)(ws16 + W.w(ri) + row * D + 32 * s + 8 * g);
     f.u = *(const u32x4*)(ws16 + W.us(ri) + ((blockIdx.y * 4 + wave) * 64 + lane) * 8);
-    f.lgc = ((const float*)((const char*)a.ws + W.f32_byte(ri)))[C - 1];
   };
 
   // this sequence's output rows as one buffer: rows past T are dropped
@@ -482,7 +480,7 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
 #pragma unroll
       for (int vt = 0; vt < 2; ++vt) o[vt][i] *= sc;
     }
-    const float gC = expf(f.lgc);
+    const float gC = expf(fs[C - 1]);
     __syncthreads();
     // ---- S = gC S + K^T diag(kf) U  (A fragments: raw k columns by transposing reads);
     // O += Rq U
