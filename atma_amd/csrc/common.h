@@ -104,13 +104,17 @@ __device__ __forceinline__ void buffer_store16b(__amdgpu_buffer_rsrc_t r, uint32
   __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, x), r, voff, 0, 0);
 }
 
+// LDS byte offset of a pointer into __shared__ memory: a flat address in the LDS
+// aperture carries the offset in its low 32 bits (the aperture base is 4 GiB aligned), so
+// a truncation suffices -- no null-pointer select as with an address-space cast.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) { return (uint32_t)(uintptr_t)p; }
+
 // Direct global->LDS copy of 16 bytes per lane (global_load_lds_dwordx4): lane i's
 // bytes land at lds_wave_base + 16*i.  Issued through inline asm so the compiler does
 // not serialise later LDS reads behind it; completion is tracked by vmcnt, so the
 // caller waits with s_waitcnt vmcnt(N) and a barrier before reading the data.
 __device__ __forceinline__ void dma_load16(const void* gptr, const void* lds_wave_base) {
-  const uint32_t off =
-      (uint32_t)(size_t)((__attribute__((address_space(3))) const void*)lds_wave_base);
+  const uint32_t off = lds_offset(lds_wave_base);
   asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gptr),
                "{m0}"(__builtin_amdgcn_readfirstlane(off))
                : "memory");
@@ -122,8 +126,7 @@ __device__ __forceinline__ void dma_load16(const void* gptr, const void* lds_wav
 // and one scalar offset, so per-copy cost is a scalar move into m0.
 __device__ __forceinline__ void dma_buf16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
                                           const void* lds_wave_base) {
-  const uint32_t off =
-      (uint32_t)(size_t)((__attribute__((address_space(3))) const void*)lds_wave_base);
+  const uint32_t off = lds_offset(lds_wave_base);
   asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff),
                "{m0}"(__builtin_amdgcn_readfirstlane(off))
                : "memory");
@@ -132,8 +135,7 @@ __device__ __forceinline__ void dma_buf16(__amdgpu_buffer_rsrc_t r, uint32_t vof
 // 4 bytes per lane (buffer_load_dword ... lds): lane i's dword lands at lds_wave_base + 4*i.
 __device__ __forceinline__ void dma_buf4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
                                          const void* lds_wave_base) {
-  const uint32_t off =
-      (uint32_t)(size_t)((__attribute__((address_space(3))) const void*)lds_wave_base);
+  const uint32_t off = lds_offset(lds_wave_base);
   asm volatile("buffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff),
                "{m0}"(__builtin_amdgcn_readfirstlane(off))
                : "memory");

@@ -476,11 +476,11 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float sc = expf(lg4[i]) * qs4[i];
+      const float sc = __builtin_amdgcn_exp2f(lg4[i] * kLog2e) * qs4[i];
 #pragma unroll
       for (int vt = 0; vt < 2; ++vt) o[vt][i] *= sc;
     }
-    const float gC = expf(fs[C - 1]);
+    const float gC = __builtin_amdgcn_exp2f(fs[C - 1] * kLog2e);
     __syncthreads();
     // ---- S = gC S + K^T diag(kf) U  (A fragments: raw k columns by transposing reads);
     // O += Rq U
