@@ -26,6 +26,7 @@
 //    fragments straight from memory); qn, rq and lg of the next two chunks are copied
 //    straight into LDS.  The output slab leaves through LDS as 16-byte stores.
 #include <algorithm>
+#include <type_traits>
 
 #include "gated_delta.h"
 
@@ -417,8 +418,9 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
   };
 
   // ---- one chunk's recurrence operands in registers (A fragments straight from
-  // memory).  Four sets rotate: a set is refilled with chunk c + 4 right after chunk c
-  // used it, so each load has three chunk steps to arrive and no set is ever copied.
+  // memory).  Three sets rotate with the three LDS slots: a set is refilled with chunk
+  // c + 3 right after chunk c used it, so each load has two chunk steps to arrive, no
+  // set is ever copied, and every slot index is a constant.
   struct Frag {
     u32x4 w[KS], u;
   };
@@ -435,8 +437,8 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
                                  (uint32_t)((int64_t)a.T * a.H * D * 2));
   const int last = a.NC - 1;
   const int qrow = 16 * wave + c16;
-  auto body = [&](const Frag& f, int c) {
-    const int slot = c % 3;
+  auto body = [&](const Frag& f, int c, auto slot_c) {
+    constexpr int slot = decltype(slot_c)::value;  // c % 3, a constant per call site
     const T* qs = Qs + slot * QB + qrow * D;
     const T* rs = Rs + slot * RB + qrow * C;
     const T* kr = Kr + slot * QB;
@@ -531,7 +533,7 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
     }
     // copies of chunk c + 2 into the slot chunk c - 1 used (its readers are past the
     // barrier that began this step)
-    copy_rec(min(c + 2, last), (c + 2) % 3);
+    copy_rec(min(c + 2, last), (slot + 2) % 3);
     // this wave's copies of chunk c + 1 (issued one step earlier) have landed: after them
     // came the register loads of step c - 1, this step's O store and its copies (wave 0
     // issues more copies, so the count is the smaller one)
@@ -544,22 +546,22 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
   publish_state();
   copy_rec(0, 0);
   copy_rec(min(1, last), 1);
-  Frag f0, f1, f2, f3;
+  Frag f0, f1, f2;
   load(f0, 0);
   load(f1, min(1, last));
   load(f2, min(2, last));
-  load(f3, min(3, last));
   wait_vmcnt<0>();
   __syncthreads();
-  for (int c = 0; c < a.NC; c += 4) {
-    body(f0, c);
-    load(f0, min(c + 4, last));
-    if (c + 1 < a.NC) body(f1, c + 1);
-    load(f1, min(c + 5, last));
-    if (c + 2 < a.NC) body(f2, c + 2);
-    load(f2, min(c + 6, last));
-    if (c + 3 < a.NC) body(f3, c + 3);
-    load(f3, min(c + 7, last));
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  for (int c = 0; c < a.NC; c += 3) {
+    body(f0, c, S0{});
+    load(f0, min(c + 3, last));
+    if (c + 1 < a.NC) body(f1, c + 1, S1{});
+    load(f1, min(c + 4, last));
+    if (c + 2 < a.NC) body(f2, c + 2, S2{});
+    load(f2, min(c + 5, last));
   }
 
   if (a.s_out) {
