@@ -125,6 +125,28 @@ def _(q, k, v, gamma, beta, state_table, slots, eps):
     return q.new_empty((B, H, state_table.shape[3]), dtype=torch.float32)
 
 
+# --------------------------------------------------------------------------- memory gates
+@torch.library.custom_op("atma_hip::gated_delta_gates", mutates_args=())
+def gated_delta_gates_op(zg: Tensor, zb: Tensor, g_bias: float, b_bias: float,
+                         decay_as_prob: bool) -> List[Tensor]:
+    _need_cuda(zg, zb)
+    if zg.dtype != torch.float32 or zb.dtype != torch.float32 or zg.shape != zb.shape:
+        raise ValueError("gate logits: two float32 tensors of the same shape")
+    lib = _lib.load()
+    zg, zb = zg.contiguous(), zb.contiguous()
+    g, beta = torch.empty_like(zg), torch.empty_like(zb)
+    rc = lib.atma_gated_delta_gates(zg.data_ptr(), zb.data_ptr(), g_bias, b_bias, g.data_ptr(),
+                                    beta.data_ptr(), zg.numel(), 1 if decay_as_prob else 0,
+                                    _lib.stream_handle(zg.device))
+    _lib.check(rc, "gated_delta_gates")
+    return [g, beta]
+
+
+@gated_delta_gates_op.register_fake
+def _(zg, zb, g_bias, b_bias, decay_as_prob):
+    return [torch.empty_like(zg), torch.empty_like(zb)]
+
+
 # --------------------------------------------------------------------------- chunked gated delta
 @torch.library.custom_op("atma_hip::chunk_gated_delta_rule", mutates_args=())
 def chunk_gated_delta_rule_op(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,

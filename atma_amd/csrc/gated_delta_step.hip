@@ -162,3 +162,35 @@ extern "C" int atma_gated_delta_decode_step(const void* q, int64_t q_sb, int64_t
       return set_error(ATMA_ERR_INVALID, "gated_delta_decode_step: unknown dtype %d", dtype);
   }
 }
+
+// ---------------------------------------------------------------------------------------
+// Gate activations of the memory branch in one pass: g = logsigmoid(zg + g_bias) (the
+// log-decay the chunked rule takes) and beta = sigmoid(zb + b_bias), or with
+// decay_as_prob the decode step's gamma = sigmoid(zg + g_bias).  Replaces the
+// torch add / logsigmoid / sigmoid launches of TitansMemory (model/blocks.py:426-490).
+namespace atma {
+__global__ void gdn_gates_kernel(const float* __restrict__ zg, const float* __restrict__ zb,
+                                 float g_bias, float b_bias, float* __restrict__ g,
+                                 float* __restrict__ beta, int64_t n, int decay_as_prob) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float x = zg[i] + g_bias;
+  // logsigmoid(x) = min(x, 0) - log1p(exp(-|x|)), stable for either sign
+  const float ls = fminf(x, 0.f) - log1pf(expf(-fabsf(x)));
+  g[i] = decay_as_prob ? expf(ls) : ls;
+  const float y = zb[i] + b_bias;
+  beta[i] = 1.f / (1.f + expf(-y));
+}
+}  // namespace atma
+
+extern "C" int atma_gated_delta_gates(const float* zg, const float* zb, float g_bias, float b_bias,
+                                      float* g, float* beta, int64_t n, int decay_as_prob,
+                                      void* stream) {
+  if (n < 0) return atma::set_error(ATMA_ERR_INVALID, "gated_delta_gates: n < 0");
+  if (n == 0) return ATMA_OK;
+  if (!zg || !zb || !g || !beta) return atma::set_error(ATMA_ERR_INVALID, "gated_delta_gates: null pointer");
+  const int64_t blocks = (n + 255) / 256;
+  atma::gdn_gates_kernel<<<dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream>>>(
+      zg, zb, g_bias, b_bias, g, beta, n, decay_as_prob ? 1 : 0);
+  return atma::check_launch("gated_delta_gates");
+}

@@ -9,7 +9,7 @@ without the library or on CPU tensors raises (there is no silent fallback).
 import torch
 
 from .. import _lib
-from .gated_delta import chunk_gated_delta_rule, gated_delta_decode_step
+from .gated_delta import chunk_gated_delta_rule, gated_delta_decode_step, gated_delta_gates
 from .polar import polar_attention_decode, polar_attention_fwd
 
 HAS_HIP = _lib.available() and torch.cuda.is_available()
@@ -20,4 +20,5 @@ __all__ = [
     "polar_attention_decode",
     "gated_delta_decode_step",
     "chunk_gated_delta_rule",
+    "gated_delta_gates",
 ]

@@ -81,3 +81,15 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
                                                      bool(use_qk_l2norm_in_kernel),
                                                      bool(output_final_state))
     return outs[0], (outs[1] if output_final_state else None)
+
+
+@torch.no_grad()
+def gated_delta_gates(g_logit, b_logit, g_bias=0.0, b_bias=0.0, decay_as_prob=False):
+    """The memory branch's gate activations in one launch (TitansMemory,
+    ``model/blocks.py:426-490``): returns ``(logsigmoid(g_logit + g_bias),
+    sigmoid(b_logit + b_bias))`` -- the log-decay and write strength
+    ``chunk_gated_delta_rule`` takes -- or, with ``decay_as_prob``, the decode step's
+    ``(sigmoid(g_logit + g_bias), sigmoid(b_logit + b_bias))``.  fp32 in and out."""
+    g, beta = torch.ops.atma_hip.gated_delta_gates(g_logit.float(), b_logit.float(), float(g_bias),
+                                                   float(b_bias), bool(decay_as_prob))
+    return g, beta

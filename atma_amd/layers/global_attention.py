@@ -27,7 +27,8 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from ..kernel import (chunk_gated_delta_rule, gated_delta_decode_step, polar_attention_decode,
+from ..kernel import (chunk_gated_delta_rule, gated_delta_decode_step, gated_delta_gates,
+                      polar_attention_decode,
                       polar_attention_fwd)
 from .attention import store_kvcache
 
@@ -62,8 +63,10 @@ class TitansMemory(nn.Module):
         nn.init.zeros_(self.proj.weight)
         nn.init.zeros_(self.proj.bias)
 
-    def logits(self, x):
-        return (self.w_gamma(x).float() + self.gamma_bias, self.w_beta(x).float() + self.beta_bias)
+    def raw_logits(self, x):
+        """Gate logits before the biases (fp32); the biases are added by the fused
+        gate kernel together with the activations."""
+        return self.w_gamma(x).float(), self.w_beta(x).float()
 
     def _out(self, x, r):
         lead = r.shape[:-2]
@@ -74,8 +77,8 @@ class TitansMemory(nn.Module):
         """x: (B, T, dim); q, k, v: (B, T, H, dk) (KV expanded).  initial_state:
         ``[K, V]`` (B, H, dk, dv) fp32 or None.  Returns (out (B, T, dim), final
         state or None) -- ``_mem_prefill_dense`` (``inference/models/atma.py:305-339``)."""
-        g_logit, b_logit = self.logits(x)
-        r, S = chunk_gated_delta_rule(q, k, v, F.logsigmoid(g_logit), torch.sigmoid(b_logit), scale=1.0,
+        glog, beta = gated_delta_gates(*self.raw_logits(x), self.gamma_bias, self.beta_bias)
+        r, S = chunk_gated_delta_rule(q, k, v, glog, beta, scale=1.0,
                                       initial_state=initial_state,
                                       output_final_state=output_final_state,
                                       use_qk_l2norm_in_kernel=True)
@@ -84,9 +87,9 @@ class TitansMemory(nn.Module):
     def step(self, x, q, k, v, state_table, slots):
         """One decode step, state table advanced in place (``_mem_decode``,
         ``inference/models/atma.py:341-375``).  x: (B, dim); q, k, v: (B, H, dk)."""
-        g_logit, b_logit = self.logits(x)
-        r = gated_delta_decode_step(q, k, v, torch.sigmoid(g_logit), torch.sigmoid(b_logit),
-                                    state_table, slots)
+        gamma, beta = gated_delta_gates(*self.raw_logits(x), self.gamma_bias, self.beta_bias,
+                                        decay_as_prob=True)
+        r = gated_delta_decode_step(q, k, v, gamma, beta, state_table, slots)
         return self._out(x, r)
 
 

@@ -133,6 +133,17 @@ int atma_gated_delta_decode_step(const void* q, int64_t q_sb, int64_t q_sh, cons
                                  int dtype, float eps, void* stream);
 
 /*
+ * Gate activations of the memory branch in one launch.  Replaces the torch
+ * add / logsigmoid / sigmoid of TitansMemory (model/blocks.py:426-490,
+ * inference/models/atma.py:305-375): g = logsigmoid(zg + g_bias) -- the log-decay
+ * atma_chunk_gated_delta_rule takes -- or, with decay_as_prob != 0, the decode step's
+ * gamma = sigmoid(zg + g_bias); beta = sigmoid(zb + b_bias).  All fp32 contiguous,
+ * n elements each.
+ */
+int atma_gated_delta_gates(const float* zg, const float* zb, float g_bias, float b_bias,
+                           float* g, float* beta, int64_t n, int decay_as_prob, void* stream);
+
+/*
  * Workspace bytes atma_chunk_gated_delta_rule needs for this shape and dtype.
  */
 size_t atma_chunk_gated_delta_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t dk,

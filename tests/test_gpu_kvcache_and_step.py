@@ -72,3 +72,23 @@ def test_gated_delta_step_repeated_calls_track_oracle(dev):
                                     t_dev, slots.to(dev))
         assert rel_err(r, r_ref) < 1e-5
     assert max_abs(t_dev, table) < 1e-5
+
+
+@pytest.mark.parametrize("decay_as_prob", [False, True])
+def test_gate_activations_vs_torch(dev, decay_as_prob):
+    """The fused gate kernel == torch's logsigmoid / sigmoid of the biased logits
+    (TitansMemory, model/blocks.py:426-490), including saturated logits on both sides."""
+    from atma_amd.kernel import gated_delta_gates
+    g = torch.Generator().manual_seed(5)
+    zg = torch.randn(3, 100, 8, generator=g) * 6
+    zb = torch.randn(3, 100, 8, generator=g) * 6
+    zg[0, :4, 0] = torch.tensor([-200.0, 200.0, -3.9, 0.0])
+    zb[0, :4, 0] = torch.tensor([-200.0, 200.0, 0.0, 1e-3])
+    ga, be = gated_delta_gates(zg.to(dev), zb.to(dev), 3.9, 0.5, decay_as_prob=decay_as_prob)
+    ref_g = torch.nn.functional.logsigmoid(zg.double() + 3.9)
+    if decay_as_prob:
+        ref_g = ref_g.exp()
+    ref_b = torch.sigmoid(zb.double() + 0.5)
+    assert ga.dtype == torch.float32 and be.dtype == torch.float32
+    assert torch.allclose(ga.cpu().double(), ref_g, rtol=2e-6, atol=1e-30)
+    assert torch.allclose(be.cpu().double(), ref_b, rtol=2e-6, atol=1e-30)
