@@ -74,3 +74,60 @@ def test_no_l2norm_and_scale(dev):
                                          beta.double(), scale=0.25, initial_state=S0.double(),
                                          use_qk_l2norm_in_kernel=False)
     assert max_abs(o, o_ref) <= 1e-4
+
+
+@pytest.mark.parametrize("T", [1, 63, 65, 200])
+@pytest.mark.parametrize("d", [64, 128])
+def test_half_ragged_with_state(dev, T, d):
+    """16-bit path: ragged chunk tails, both head dims, a carried-in fp32 state."""
+    q, k, v, glog, beta, S0 = _inputs(2, T, 3, d, torch.bfloat16, seed=11 + T + d)
+    o, S = _run(dev, q, k, v, glog, beta, scale=1.0, initial_state=S0, output_final_state=True,
+                use_qk_l2norm_in_kernel=True)
+    o_ref, S_ref = OG.chunk_gated_delta_rule(q.float(), k.float(), v.float(), glog, beta, scale=1.0,
+                                             initial_state=S0, output_final_state=True,
+                                             use_qk_l2norm_in_kernel=True)
+    assert rel_err(o, o_ref) <= 2e-2 and rel_err(S, S_ref) <= 2e-2
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_half_no_l2norm_and_scale(dev, d):
+    """16-bit path without in-kernel normalisation: the raw query rows carry `scale`
+    alone and the raw key rows no norm."""
+    q, k, v, glog, beta, S0 = _inputs(1, 190, 2, d, torch.float32, seed=12)
+    k = F.normalize(k, dim=-1)
+    q, k, v = (t.to(torch.bfloat16) for t in (q, k, v))
+    o, _ = _run(dev, q, k, v, glog, beta, scale=0.25, initial_state=S0, use_qk_l2norm_in_kernel=False)
+    o_ref, _ = OG.chunk_gated_delta_rule(q.float(), k.float(), v.float(), glog, beta, scale=0.25,
+                                         initial_state=S0, use_qk_l2norm_in_kernel=False)
+    assert rel_err(o, o_ref) <= 2e-2
+
+
+def test_half_strided_inputs_bitwise(dev):
+    """q / k / v as (B, T, H, d) views of head-major tensors (the layer's and the
+    bench's layout) give bit-identical results to contiguous copies."""
+    B, T, H, d = 2, 300, 4, 128
+    g = torch.Generator().manual_seed(13)
+    qh, kh, vh = (torch.randn(B, H, T, d, generator=g).to(torch.bfloat16) for _ in range(3))
+    glog = F.logsigmoid(torch.randn(B, T, H, generator=g) + 3.9)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g))
+    kw = dict(scale=1.0, output_final_state=True, use_qk_l2norm_in_kernel=True)
+    views = [t.to(dev).transpose(1, 2) for t in (qh, kh, vh)]
+    o1, S1 = _run(dev, *views, glog, beta, **kw)
+    o2, S2 = _run(dev, *[t.contiguous() for t in views], glog, beta, **kw)
+    assert torch.equal(o1, o2) and torch.equal(S1, S2)
+
+
+def test_half_long_sequence(dev):
+    """configs[2] length, 16-bit: against the fp32 oracle (whole output), and one call ==
+    two calls split at a chunk boundary with the fp32 state carried (bitwise)."""
+    B, T, H, d = 1, 65536, 2, 128
+    q, k, v, glog, beta, _ = _inputs(B, T, H, d, torch.bfloat16, seed=14)
+    kw = dict(scale=1.0, output_final_state=True, use_qk_l2norm_in_kernel=True)
+    o, S = _run(dev, q, k, v, glog, beta, initial_state=None, **kw)
+    h = T // 2
+    o1, S1 = _run(dev, q[:, :h], k[:, :h], v[:, :h], glog[:, :h], beta[:, :h], initial_state=None, **kw)
+    o2, S2 = _run(dev, q[:, h:], k[:, h:], v[:, h:], glog[:, h:], beta[:, h:], initial_state=S1, **kw)
+    assert torch.equal(torch.cat([o1, o2], 1), o) and torch.equal(S2, S)
+    o_ref, S_ref = OG.chunk_gated_delta_rule(q.float(), k.float(), v.float(), glog, beta, scale=1.0,
+                                             output_final_state=True, use_qk_l2norm_in_kernel=True)
+    assert rel_err(o, o_ref) <= 2e-2 and rel_err(S, S_ref) <= 2e-2
