@@ -113,8 +113,8 @@ def gated_delta_decode_step_op(q: Tensor, k: Tensor, v: Tensor, gamma: Tensor, b
     rc = lib.atma_gated_delta_decode_step(
         q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
         v.data_ptr(), v.stride(0), v.stride(1), gamma.data_ptr(), beta.data_ptr(),
-        state_table.data_ptr(), state_table.shape[0], slots.data_ptr(), r.data_ptr(), B, H, dk, dv,
-        _lib.dtype_code(q.dtype), eps, _lib.stream_handle(q.device))
+        state_table.data_ptr(), state_table.shape[0], slots.data_ptr(), r.data_ptr(), B, H,
+        k.shape[1], dk, dv, _lib.dtype_code(q.dtype), eps, _lib.stream_handle(q.device))
     _lib.check(rc, "gated_delta_decode_step")
     return r
 
@@ -168,7 +168,8 @@ def chunk_gated_delta_rule_op(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: 
         k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
         v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
         g.data_ptr(), beta.data_ptr(), _lib.ptr(initial_state), _lib.ptr(final), o.data_ptr(),
-        B, T, H, dk, dv, _lib.dtype_code(q.dtype), scale, 1 if use_qk_l2norm else 0, chunk,
+        B, T, H, k.shape[2], dk, dv, _lib.dtype_code(q.dtype), scale, 1 if use_qk_l2norm else 0,
+        chunk,
         ws.data_ptr(), ws.numel() * 4, _lib.stream_handle(q.device))
     _lib.check(rc, "chunk_gated_delta_rule")
     return [o, final] if want_final else [o]

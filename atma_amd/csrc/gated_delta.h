@@ -21,6 +21,7 @@ struct GdnArgs {
   float* s_out;
   void* o;
   int B, T, H, NC;
+  int G;  // query heads per k / v head (k, v carry H / G heads)
   float scale;
   int l2norm;
   void* ws;

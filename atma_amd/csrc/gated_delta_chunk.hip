@@ -46,8 +46,8 @@ __global__ void __launch_bounds__(256) gdn_prep_kernel(GdnArgs a) {
     const int t = t0 + r;
     const bool ok = t < a.T;
     const T* qr = (const T*)a.q + b * a.q_sb + (int64_t)t * a.q_st + h * a.q_sh;
-    const T* kr = (const T*)a.k + b * a.k_sb + (int64_t)t * a.k_st + h * a.k_sh;
-    const T* vr = (const T*)a.v + b * a.v_sb + (int64_t)t * a.v_st + h * a.v_sh;
+    const T* kr = (const T*)a.k + b * a.k_sb + (int64_t)t * a.k_st + (h / a.G) * a.k_sh;
+    const T* vr = (const T*)a.v + b * a.v_sb + (int64_t)t * a.v_st + (h / a.G) * a.v_sh;
     float qv[D / 64 > 0 ? D / 64 : 1], kv[D / 64 > 0 ? D / 64 : 1];
     float qq = 0.f, kk = 0.f;
 #pragma unroll
@@ -339,7 +339,7 @@ extern "C" int atma_chunk_gated_delta_rule(
     const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh, const void* k, int64_t k_sb,
     int64_t k_st, int64_t k_sh, const void* v, int64_t v_sb, int64_t v_st, int64_t v_sh,
     const float* g, const float* beta, const float* initial_state, float* final_state, void* o,
-    int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int dtype, float scale,
+    int64_t B, int64_t T, int64_t H, int64_t Hkv, int64_t dk, int64_t dv, int dtype, float scale,
     int use_qk_l2norm, int64_t chunk, void* workspace, size_t workspace_bytes, void* stream) {
   using namespace atma;
   if (chunk != kChunk)
@@ -348,6 +348,9 @@ extern "C" int atma_chunk_gated_delta_rule(
     return set_error(ATMA_ERR_UNSUPPORTED, "chunk_gated_delta_rule: dk=dv in {64,128} (got %lld,%lld)",
                      (long long)dk, (long long)dv);
   if (B < 0 || T < 0 || H <= 0) return set_error(ATMA_ERR_INVALID, "chunk_gated_delta_rule: bad sizes");
+  if (Hkv <= 0 || H % Hkv)
+    return set_error(ATMA_ERR_INVALID, "chunk_gated_delta_rule: H=%lld not a multiple of Hkv=%lld",
+                     (long long)H, (long long)Hkv);
   if (B * H > 0x7fffffffll || T > (1ll << 30))
     return set_error(ATMA_ERR_INVALID, "chunk_gated_delta_rule: sizes too large");
   const int es = dtype_size(dtype);
@@ -375,6 +378,7 @@ extern "C" int atma_chunk_gated_delta_rule(
   a.v = v; a.v_sb = v_sb; a.v_st = v_st; a.v_sh = v_sh;
   a.g = g; a.beta = beta; a.s0 = initial_state; a.s_out = final_state; a.o = o;
   a.B = (int)B; a.T = (int)T; a.H = (int)H; a.NC = (int)((T + chunk - 1) / chunk);
+  a.G = (int)(H / Hkv);
   a.scale = scale; a.l2norm = use_qk_l2norm ? 1 : 0; a.ws = workspace;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == ATMA_BF16 || dtype == ATMA_F16) return launch_gdn16(a, dtype, (int)dk, s);

@@ -82,11 +82,11 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
       for (int i = 0; i < 4; ++i) {
         const int64_t t = (int64_t)c * C + 4 * p4 + i;
         const bool ok = t < a.T;
-        r.k[i] = ok ? *(const u32x4*)((const T*)a.k + b * a.k_sb + t * a.k_st + h * a.k_sh + 8 * dc)
+        r.k[i] = ok ? *(const u32x4*)((const T*)a.k + b * a.k_sb + t * a.k_st + (h / a.G) * a.k_sh + 8 * dc)
                     : u32x4{0, 0, 0, 0};
         r.q[i] = ok ? *(const u32x4*)((const T*)a.q + b * a.q_sb + t * a.q_st + h * a.q_sh + 8 * dc)
                     : u32x4{0, 0, 0, 0};
-        r.v[i] = ok ? *(const u32x4*)((const T*)a.v + b * a.v_sb + t * a.v_st + h * a.v_sh + 8 * dc)
+        r.v[i] = ok ? *(const u32x4*)((const T*)a.v + b * a.v_sb + t * a.v_st + (h / a.G) * a.v_sh + 8 * dc)
                     : u32x4{0, 0, 0, 0};
       }
     }
@@ -393,7 +393,7 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
     const int rows = min(a.T - j * C, C);
     const auto qrs = buffer_rsrc((const T*)a.q + b * a.q_sb + (int64_t)j * C * a.q_st + h * a.q_sh,
                                  (uint32_t)((rows - 1) * a.q_st + D) * 2u);
-    const auto krs = buffer_rsrc((const T*)a.k + b * a.k_sb + (int64_t)j * C * a.k_st + h * a.k_sh,
+    const auto krs = buffer_rsrc((const T*)a.k + b * a.k_sb + (int64_t)j * C * a.k_st + (h / a.G) * a.k_sh,
                                  (uint32_t)((rows - 1) * a.k_st + D) * 2u);
     const auto rrs = buffer_rsrc(ws16 + W.rq(ri), RB * 2);
 #pragma unroll

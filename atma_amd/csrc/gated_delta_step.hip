@@ -22,7 +22,7 @@ gated_delta_step_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, con
                         int64_t v_sh, const float* __restrict__ gamma,
                         const float* __restrict__ beta, float* __restrict__ state,
                         int64_t max_seqs, const int64_t* __restrict__ slots, float* __restrict__ r,
-                        int H, float eps) {
+                        int H, int G, float eps) {
   constexpr int VC = 64;            // state columns per workgroup
   constexpr int RPT = D / 16;       // state rows per thread
   __shared__ float s_q[D], s_k[D], s_v[VC], s_u[VC];
@@ -37,9 +37,9 @@ gated_delta_step_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, con
 
   if (tid < D) {
     s_q[tid] = to_f32(q[b * q_sb + h * q_sh + tid]);
-    s_k[tid] = to_f32(k[b * k_sb + h * k_sh + tid]);
+    s_k[tid] = to_f32(k[b * k_sb + (h / G) * k_sh + tid]);
   }
-  if (tid < VC) s_v[tid] = to_f32(v[b * v_sb + h * v_sh + col0 + tid]);
+  if (tid < VC) s_v[tid] = to_f32(v[b * v_sb + (h / G) * v_sh + col0 + tid]);
   __syncthreads();
   if (wave < 2) {  // wave 0: |q|^2, wave 1: |k|^2
     const float* src = wave == 0 ? s_q : s_k;
@@ -106,11 +106,11 @@ template <typename T, int D>
 static int launch_step(const void* q, int64_t q_sb, int64_t q_sh, const void* k, int64_t k_sb,
                        int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sh, const float* gamma,
                        const float* beta, float* state, int64_t max_seqs, const int64_t* slots,
-                       float* r, int64_t B, int64_t H, float eps, hipStream_t stream) {
+                       float* r, int64_t B, int64_t H, int64_t G, float eps, hipStream_t stream) {
   dim3 grid((unsigned)(B * H), D / 64);
   gated_delta_step_kernel<T, D><<<grid, dim3(256), 0, stream>>>(
       (const T*)q, q_sb, q_sh, (const T*)k, k_sb, k_sh, (const T*)v, v_sb, v_sh, gamma, beta,
-      state, max_seqs, slots, r, (int)H, eps);
+      state, max_seqs, slots, r, (int)H, (int)G, eps);
   return check_launch("gated_delta_decode_step");
 }
 
@@ -118,13 +118,13 @@ template <typename T>
 static int dispatch_step(int64_t D, const void* q, int64_t q_sb, int64_t q_sh, const void* k,
                          int64_t k_sb, int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sh,
                          const float* gamma, const float* beta, float* state, int64_t max_seqs,
-                         const int64_t* slots, float* r, int64_t B, int64_t H, float eps,
-                         hipStream_t s) {
+                         const int64_t* slots, float* r, int64_t B, int64_t H, int64_t G,
+                         float eps, hipStream_t s) {
   if (D == 128)
     return launch_step<T, 128>(q, q_sb, q_sh, k, k_sb, k_sh, v, v_sb, v_sh, gamma, beta, state,
-                               max_seqs, slots, r, B, H, eps, s);
+                               max_seqs, slots, r, B, H, G, eps, s);
   return launch_step<T, 64>(q, q_sb, q_sh, k, k_sb, k_sh, v, v_sb, v_sh, gamma, beta, state,
-                            max_seqs, slots, r, B, H, eps, s);
+                            max_seqs, slots, r, B, H, G, eps, s);
 }
 
 }  // namespace atma
@@ -135,14 +135,15 @@ extern "C" int atma_gated_delta_decode_step(const void* q, int64_t q_sb, int64_t
                                             const float* gamma, const float* beta,
                                             float* state_table, int64_t max_seqs,
                                             const int64_t* slots, float* r, int64_t B, int64_t H,
-                                            int64_t dk, int64_t dv, int dtype, float eps,
-                                            void* stream) {
+                                            int64_t Hkv, int64_t dk, int64_t dv, int dtype,
+                                            float eps, void* stream) {
   using namespace atma;
   if (dk != dv || (dk != 128 && dk != 64))
     return set_error(ATMA_ERR_UNSUPPORTED, "gated_delta_decode_step: dk=dv in {64,128} (got %lld,%lld)",
                      (long long)dk, (long long)dv);
-  if (B < 0 || H <= 0 || max_seqs < 0)
-    return set_error(ATMA_ERR_INVALID, "gated_delta_decode_step: bad sizes");
+  if (B < 0 || H <= 0 || max_seqs < 0 || Hkv <= 0 || H % Hkv)
+    return set_error(ATMA_ERR_INVALID, "gated_delta_decode_step: bad sizes (H must be a multiple of Hkv)");
+  const int64_t G = H / Hkv;
   if (B == 0) return ATMA_OK;
   if (!q || !k || !v || !gamma || !beta || !state_table || !slots || !r)
     return set_error(ATMA_ERR_INVALID, "gated_delta_decode_step: null pointer");
@@ -151,13 +152,13 @@ extern "C" int atma_gated_delta_decode_step(const void* q, int64_t q_sb, int64_t
   switch (dtype) {
     case ATMA_F32:
       return dispatch_step<float>(dk, q, q_sb, q_sh, k, k_sb, k_sh, v, v_sb, v_sh, gamma, beta,
-                                  state_table, max_seqs, slots, r, B, H, eps, s);
+                                  state_table, max_seqs, slots, r, B, H, G, eps, s);
     case ATMA_BF16:
       return dispatch_step<bf16>(dk, q, q_sb, q_sh, k, k_sb, k_sh, v, v_sb, v_sh, gamma, beta,
-                                 state_table, max_seqs, slots, r, B, H, eps, s);
+                                 state_table, max_seqs, slots, r, B, H, G, eps, s);
     case ATMA_F16:
       return dispatch_step<f16>(dk, q, q_sb, q_sh, k, k_sb, k_sh, v, v_sb, v_sh, gamma, beta,
-                                state_table, max_seqs, slots, r, B, H, eps, s);
+                                state_table, max_seqs, slots, r, B, H, G, eps, s);
     default:
       return set_error(ATMA_ERR_INVALID, "gated_delta_decode_step: unknown dtype %d", dtype);
   }

@@ -19,14 +19,19 @@ from .. import _ops  # noqa: F401  (registers torch.ops.atma_hip.*)
 def gated_delta_decode_step(q, k, v, gamma, beta, state_table, slots, eps=1e-12, block_v=None):
     """One batched gated-delta step, IN PLACE on the slot-indexed state table.
 
-    q, k, v: (B, H, d) current-token tensors (KV heads expanded to H).
+    q: (B, H, d), k, v: (B, Hkv, d) current-token tensors with H % Hkv == 0: query
+    head h reads key / value head h // (H // Hkv), so grouped KV heads need no
+    expansion (Hkv == H is the reference's expanded call).
     gamma, beta: (B, H) retention / write strength.  state_table: (max_seqs, H, dk, dv)
     fp32 ``[K, V]``, updated in place.  slots: (B,) int64 rows of the table.
     ``block_v`` (a Triton tile knob) is accepted and ignored.
     Returns r (B, H, dv) fp32.  Graph capturable."""
-    if q.dim() != 3 or q.shape != k.shape or q.shape[:2] != v.shape[:2]:
-        raise ValueError("q, k, v must be (B, H, d) with matching shapes")
+    if q.dim() != 3 or k.dim() != 3 or k.shape[0] != q.shape[0] or k.shape[2] != q.shape[2] \
+            or v.dim() != 3 or v.shape[:2] != k.shape[:2]:
+        raise ValueError("q: (B, H, d) and k, v: (B, Hkv, d) required")
     B, H, dk = q.shape
+    if k.shape[1] < 1 or H % k.shape[1]:
+        raise ValueError(f"q heads ({H}) must be a multiple of k/v heads ({k.shape[1]})")
     if state_table.dim() != 4 or state_table.shape[1] != H or state_table.shape[2] != dk:
         raise ValueError(f"state_table {tuple(state_table.shape)} incompatible with q {tuple(q.shape)}")
     if v.shape[2] != state_table.shape[3]:
@@ -46,17 +51,21 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
                            cu_seqlens=None, head_first=False):
     """Chunked gated-delta prefill with state carry (FLA contract).
 
-    q, k: (B, T, H, dk); v: (B, T, H, dv); g: (B, T, H) log-decay (log gamma);
-    beta: (B, T, H); initial_state: (B, H, dk, dv) fp32 or None.  With
+    q: (B, T, H, dk); k: (B, T, Hkv, dk); v: (B, T, Hkv, dv) with H % Hkv == 0 (query
+    head h reads key / value head h // (H // Hkv); Hkv == H is the expanded form FLA
+    takes); g: (B, T, H) log-decay (log gamma); beta: (B, T, H); initial_state: (B, H, dk, dv) fp32 or None.  With
     ``use_qk_l2norm_in_kernel`` q and k are L2-normalised (x / max(|x|, 1e-12)) before
     the recurrence; q is then scaled by ``scale`` (default dk**-0.5, FLA's default;
     the reference passes 1.0).
     Returns (o (B, T, H, dv) in q's dtype, final_state (B, H, dk, dv) fp32 or None)."""
     if cu_seqlens is not None or head_first:
         raise NotImplementedError("cu_seqlens / head_first layouts are not supported")
-    if q.dim() != 4 or k.shape != q.shape or v.shape[:3] != q.shape[:3]:
-        raise ValueError("q, k: (B, T, H, dk) and v: (B, T, H, dv) required")
+    if q.dim() != 4 or k.dim() != 4 or k.shape[:2] != q.shape[:2] or k.shape[3] != q.shape[3] \
+            or v.dim() != 4 or v.shape[:3] != k.shape[:3]:
+        raise ValueError("q: (B, T, H, dk), k: (B, T, Hkv, dk) and v: (B, T, Hkv, dv) required")
     B, T, H, dk = q.shape
+    if k.shape[2] < 1 or H % k.shape[2]:
+        raise ValueError(f"q heads ({H}) must be a multiple of k/v heads ({k.shape[2]})")
     dv = v.shape[3]
     if g.shape != (B, T, H) or beta.shape != (B, T, H):
         raise ValueError("g and beta must be (B, T, H)")

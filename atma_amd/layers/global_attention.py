@@ -74,7 +74,9 @@ class TitansMemory(nn.Module):
         return self.proj(r * torch.sigmoid(self.gate(x)))
 
     def forward(self, x, q, k, v, initial_state=None, output_final_state=False):
-        """x: (B, T, dim); q, k, v: (B, T, H, dk) (KV expanded).  initial_state:
+        """x: (B, T, dim); q: (B, T, H, dk); k, v: (B, T, Hkv, dk) with H % Hkv == 0
+        (the kernel maps query head h to KV head h // (H // Hkv), so the reference's
+        repeat_interleave expansion is not materialised).  initial_state:
         ``[K, V]`` (B, H, dk, dv) fp32 or None.  Returns (out (B, T, dim), final
         state or None) -- ``_mem_prefill_dense`` (``inference/models/atma.py:305-339``)."""
         glog, beta = gated_delta_gates(*self.raw_logits(x), self.gamma_bias, self.beta_bias)
@@ -86,7 +88,8 @@ class TitansMemory(nn.Module):
 
     def step(self, x, q, k, v, state_table, slots):
         """One decode step, state table advanced in place (``_mem_decode``,
-        ``inference/models/atma.py:341-375``).  x: (B, dim); q, k, v: (B, H, dk)."""
+        ``inference/models/atma.py:341-375``).  x: (B, dim); q: (B, H, dk); k, v:
+        (B, Hkv, dk), grouped heads read in-kernel."""
         gamma, beta = gated_delta_gates(*self.raw_logits(x), self.gamma_bias, self.beta_bias,
                                         decay_as_prob=True)
         r = gated_delta_decode_step(q, k, v, gamma, beta, state_table, slots)
@@ -237,7 +240,6 @@ class PolarAttention(nn.Module):
 
     def _attend_prefill(self, x, q, gate, k, v, S0, final_sink):
         B, T = q.shape[:2]
-        g = self.num_heads // self.num_kv_heads
         n_keys = torch.arange(1, T + 1, device=x.device, dtype=torch.float32)
         qh, kh, vh = (t.transpose(1, 2) for t in (q, k, v))   # (B, heads, T, dk) views
 
@@ -247,9 +249,7 @@ class PolarAttention(nn.Module):
             return self._combine(c.transpose(1, 2), mag.transpose(1, 2), gate)
 
         def memory():
-            km = k.repeat_interleave(g, dim=2)
-            vm = v.repeat_interleave(g, dim=2)
-            return self.mem(x, q, km, vm, initial_state=S0, output_final_state=final_sink is not None)
+            return self.mem(x, q, k, v, initial_state=S0, output_final_state=final_sink is not None)
 
         out, m = self._with_memory(polar, memory, (x, q, k, v))
         if m is not None:
@@ -294,9 +294,7 @@ class PolarAttention(nn.Module):
                                         window=self.window, **self.polar_params())
         out = self._combine(c, mag, gate)
         if self.mem is not None:
-            g = H // Hkv
-            out = out + self.mem.step(x, q, k.repeat_interleave(g, dim=1), v.repeat_interleave(g, dim=1),
-                                      cache.mem_table, slots)
+            out = out + self.mem.step(x, q, k, v, cache.mem_table, slots)
         return out
 
 

@@ -64,10 +64,11 @@ class Prefill:
         self.q = torch.randn(B, HQ, T, D, device=dev, generator=g, dtype=bf)
         self.k = torch.randn(B, HKV, T, D, device=dev, generator=g, dtype=bf)
         self.v = torch.randn(B, HKV, T, D, device=dev, generator=g, dtype=bf)
-        # the memory branch sees KV expanded to the query heads, (B, T, H, d) views
+        # the memory branch takes (B, T, heads, d) views of the same tensors; its kernels
+        # map query head h to KV head h // (HQ // HKV), so nothing is expanded
         self.qm = self.q.transpose(1, 2)
-        self.km = self.k.repeat_interleave(HQ // HKV, 1).transpose(1, 2)
-        self.vm = self.v.repeat_interleave(HQ // HKV, 1).transpose(1, 2)
+        self.km = self.k.transpose(1, 2)
+        self.vm = self.v.transpose(1, 2)
         self.zg = torch.randn(B, T, HQ, device=dev, generator=g)
         self.zb = torch.randn(B, T, HQ, device=dev, generator=g)
         self.s0 = torch.zeros(B, HQ, D, D, device=dev)
@@ -164,8 +165,6 @@ class Decode:
         self.q = torch.randn(B, HQ, D, device=dev, generator=g, dtype=bf)
         self.knew = torch.randn(B, HKV, D, device=dev, generator=g, dtype=bf)
         self.vnew = torch.randn(B, HKV, D, device=dev, generator=g, dtype=bf)
-        self.km = self.knew.repeat_interleave(HQ // HKV, 1)
-        self.vm = self.vnew.repeat_interleave(HQ // HKV, 1)
         self.gamma = torch.sigmoid(torch.randn(B, HQ, device=dev, generator=g) + 3.9)
         self.beta = torch.sigmoid(torch.randn(B, HQ, device=dev, generator=g))
         max_seqs = 2 * B
@@ -180,7 +179,7 @@ class Decode:
     def step(self):
         self.store(self.knew, self.vnew, self.kc, self.vc, self.slot_map)
         c, mag = self.dec(self.q, self.kc, self.vc, self.bt, self.ctx, **self.p)
-        r = self.step_mem(self.q, self.km, self.vm, self.gamma, self.beta, self.table, self.slots)
+        r = self.step_mem(self.q, self.knew, self.vnew, self.gamma, self.beta, self.table, self.slots)
         return c, mag, r
 
     def attention(self):
@@ -204,9 +203,9 @@ class Decode:
     def bytes(self):
         kv = self.ctx_sum * HKV * D * 2 * 2
         state = self.B * HQ * D * D * 4 * 2
-        small = (self.B * HQ * D * 2 * 4            # q (attention + memory), km, vm reads
+        small = (self.B * HQ * D * 2 * 2            # q read by attention and memory
                  + self.B * HQ * D * 2 + self.B * HQ * 2 + self.B * HQ * D * 4   # c, mag, r
-                 + self.B * HKV * D * 2 * 2 * 2     # new k/v read + written
+                 + self.B * HKV * D * 2 * 2 * 3     # new k/v: store read + write, memory read
                  + 4 * self.pages + 4 * self.B * 3)  # page table, ctx, slots
         return kv, state, small
 

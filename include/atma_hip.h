@@ -119,7 +119,8 @@ int atma_polar_attention_decode(const void* q, int64_t q_sb, int64_t q_sh, const
 /*
  * One gated-delta decode step, IN PLACE on the slot-indexed fp32 state table.
  * Replaces gated_delta_decode_step (kernel/gated_delta_triton.py:78-117).
- * q, k, v: (B, H, d) strides (x_sb, x_sh, 1) (KV heads already expanded);
+ * q: (B, H, d), k, v: (B, Hkv, d) with H % Hkv == 0, strides (x_sb, x_sh, 1) -- query
+ * head h reads k / v head h / (H / Hkv); Hkv == H is the reference's expanded form;
  * gamma, beta: (B, H) fp32 contiguous; state_table: contiguous fp32
  * (max_seqs, H, dk, dv) in [K, V] layout; slots: (B,) int64 rows of the table
  * (a slot outside [0, max_seqs) leaves the table untouched and yields NaN r).
@@ -129,8 +130,8 @@ int atma_gated_delta_decode_step(const void* q, int64_t q_sb, int64_t q_sh, cons
                                  int64_t k_sb, int64_t k_sh, const void* v, int64_t v_sb,
                                  int64_t v_sh, const float* gamma, const float* beta,
                                  float* state_table, int64_t max_seqs, const int64_t* slots,
-                                 float* r, int64_t B, int64_t H, int64_t dk, int64_t dv,
-                                 int dtype, float eps, void* stream);
+                                 float* r, int64_t B, int64_t H, int64_t Hkv, int64_t dk,
+                                 int64_t dv, int dtype, float eps, void* stream);
 
 /*
  * Gate activations of the memory branch in one launch.  Replaces the torch
@@ -154,7 +155,9 @@ size_t atma_chunk_gated_delta_workspace_bytes(int64_t B, int64_t T, int64_t H, i
  * fla.ops.gated_delta_rule.chunk_gated_delta_rule as the reference calls it
  * (model/blocks.py:44-49, inference/models/atma.py:285-287,318-322), with the
  * arithmetic of gated_delta_chunked (model/blocks.py:375-423).
- * q, k: (B, T, H, dk), v: (B, T, H, dv), strides (x_sb, x_st, x_sh, 1);
+ * q: (B, T, H, dk), k: (B, T, Hkv, dk), v: (B, T, Hkv, dv) with H % Hkv == 0, strides
+ * (x_sb, x_st, x_sh, 1) -- query head h reads k / v head h / (H / Hkv); Hkv == H is
+ * the expanded form FLA and the reference use;
  * g (log-decay) and beta: (B, T, H) fp32 contiguous; initial_state (nullable =
  * zeros) and final_state (nullable = not written): (B, H, dk, dv) fp32 [K, V].
  * Output o: (B, T, H, dv) dtype contiguous.  q, k are L2-normalised when
@@ -166,7 +169,7 @@ int atma_chunk_gated_delta_rule(const void* q, int64_t q_sb, int64_t q_st, int64
                                 const void* v, int64_t v_sb, int64_t v_st, int64_t v_sh,
                                 const float* g, const float* beta, const float* initial_state,
                                 float* final_state, void* o, int64_t B, int64_t T, int64_t H,
-                                int64_t dk, int64_t dv, int dtype, float scale,
+                                int64_t Hkv, int64_t dk, int64_t dv, int dtype, float scale,
                                 int use_qk_l2norm, int64_t chunk, void* workspace,
                                 size_t workspace_bytes, void* stream);
 

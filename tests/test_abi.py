@@ -64,7 +64,7 @@ def test_validation_rejects_without_launch(lib):
     assert rc == 3
     # chunked gated delta: chunk must be 64; dk == dv
     assert lib.atma_chunk_gated_delta_rule(null, 0, 0, 0, null, 0, 0, 0, null, 0, 0, 0, null, null,
-                                           null, null, null, 1, 64, 2, 128, 128, 1, 1.0, 1, 32,
+                                           null, null, null, 1, 64, 2, 2, 128, 128, 1, 1.0, 1, 32,
                                            null, 0, null) == 2
     assert lib.atma_chunk_gated_delta_workspace_bytes(1, 65, 2, 128, 128, 64, 0) == 2 * 2 * (5 * 64 * 128 + 4) * 4
     # 16-bit path: per (sequence, head, chunk) w, u (C x d each) and rq (C x C) in 16
@@ -73,7 +73,7 @@ def test_validation_rejects_without_launch(lib):
         2 * 2 * ((2 * 64 * 128 + 64 * 64) * 2 + 3 * 64 * 4)
     # gated delta step: unsupported dims
     assert lib.atma_gated_delta_decode_step(null, 0, 0, null, 0, 0, null, 0, 0, null, null, null, 1,
-                                            null, null, 1, 1, 96, 96, 1, 1e-12, null) == 2
+                                            null, null, 1, 1, 1, 96, 96, 1, 1e-12, null) == 2
     # store_kvcache: unknown dtype
     assert lib.atma_store_kvcache(null, 0, null, 0, null, null, null, 1, 256, 8, 9, null) == 1
     # zero-size requests are no-ops
@@ -91,6 +91,21 @@ def test_python_wrappers_validate_like_the_reference():
     q3 = torch.zeros(1, 2, 4, 96)
     with pytest.raises(ValueError, match="power of two"):
         polar_attention_fwd(q3, q3, q3, torch.arange(1, 5.0), **p)
+
+
+def test_gated_delta_wrappers_check_head_grouping():
+    """Grouped KV heads must divide the query heads; shapes are checked before any
+    device work, so CPU tensors reach the check."""
+    from atma_amd.kernel import chunk_gated_delta_rule, gated_delta_decode_step
+    q, k = torch.zeros(1, 5, 6, 64), torch.zeros(1, 5, 4, 64)
+    g = torch.zeros(1, 5, 6)
+    with pytest.raises(ValueError, match="multiple of k/v heads"):
+        chunk_gated_delta_rule(q, k, k, g, g)
+    with pytest.raises(ValueError, match="required"):
+        chunk_gated_delta_rule(q, k[:, :4], k, g, g)
+    table = torch.zeros(2, 6, 64, 64)
+    with pytest.raises(ValueError, match="multiple of k/v heads"):
+        gated_delta_decode_step(q[:, 0], k[:, 0], k[:, 0], g[:, 0], g[:, 0], table, torch.zeros(1))
 
 
 def test_cpu_tensors_fail_loudly():

@@ -131,3 +131,24 @@ def test_half_long_sequence(dev):
     o_ref, S_ref = OG.chunk_gated_delta_rule(q.float(), k.float(), v.float(), glog, beta, scale=1.0,
                                              output_final_state=True, use_qk_l2norm_in_kernel=True)
     assert rel_err(o, o_ref) <= 2e-2 and rel_err(S, S_ref) <= 2e-2
+
+
+@pytest.mark.parametrize("dtype,d,T", [(torch.float32, 128, 200), (torch.float32, 64, 65),
+                                       (torch.bfloat16, 128, 300), (torch.float16, 64, 129)])
+def test_grouped_kv_heads_equal_expanded(dev, dtype, d, T):
+    """k / v with Hkv < H heads (query head h reads KV head h // (H // Hkv)) give
+    bit-identical results to the reference's repeat_interleave-expanded call, for
+    head-major views (the layer's layout), with a carried initial state."""
+    B, H, Hkv = 2, 8, 2
+    g = torch.Generator().manual_seed(17 + d + T)
+    qh = torch.randn(B, H, T, d, generator=g).to(dtype)
+    kh, vh = (torch.randn(B, Hkv, T, d, generator=g).to(dtype) for _ in range(2))
+    glog = F.logsigmoid(torch.randn(B, T, H, generator=g) + 3.9)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g))
+    S0 = torch.randn(B, H, d, d, generator=g) * 0.1
+    kw = dict(scale=1.0, initial_state=S0, output_final_state=True, use_qk_l2norm_in_kernel=True)
+    q, k, v = (t.to(dev).transpose(1, 2) for t in (qh, kh, vh))
+    o1, S1 = _run(dev, q, k, v, glog, beta, **kw)
+    kx, vx = (t.repeat_interleave(H // Hkv, 2) for t in (k, v))
+    o2, S2 = _run(dev, q, kx, vx, glog, beta, **kw)
+    assert torch.equal(o1, o2) and torch.equal(S1, S2)

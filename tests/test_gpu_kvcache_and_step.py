@@ -74,6 +74,31 @@ def test_gated_delta_step_repeated_calls_track_oracle(dev):
     assert max_abs(t_dev, table) < 1e-5
 
 
+@pytest.mark.parametrize("dtype,D", [(torch.float32, 128), (torch.bfloat16, 64)])
+def test_gated_delta_step_grouped_kv_heads(dev, dtype, D):
+    """k / v with Hkv < H heads == the expanded call (bitwise, outputs and table), and
+    both track the oracle on the expanded tensors."""
+    from atma_amd.kernel import gated_delta_decode_step
+    B, H, Hkv, max_seqs = 5, 8, 2, 7
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(B, H, D, generator=g).to(dtype)
+    k, v = (torch.randn(B, Hkv, D, generator=g).to(dtype) for _ in range(2))
+    gamma = torch.rand(B, H, generator=g)
+    beta = torch.rand(B, H, generator=g)
+    table = torch.randn(max_seqs, H, D, D, generator=g) * 0.1
+    slots = torch.randperm(max_seqs, generator=g)[:B]
+    kx, vx = (t.repeat_interleave(H // Hkv, 1) for t in (k, v))
+    t1, t2 = table.to(dev), table.to(dev)
+    args = (gamma.to(dev), beta.to(dev))
+    r1 = gated_delta_decode_step(q.to(dev), k.to(dev), v.to(dev), *args, t1, slots.to(dev))
+    r2 = gated_delta_decode_step(q.to(dev), kx.to(dev), vx.to(dev), *args, t2, slots.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(r1, r2) and torch.equal(t1, t2)
+    ref_table = table.clone()
+    r_ref = OG.gated_delta_decode_step(q, kx, vx, gamma, beta, ref_table, slots)
+    assert max_abs(r1, r_ref) < 2e-5 and max_abs(t1, ref_table) < 2e-6
+
+
 @pytest.mark.parametrize("decay_as_prob", [False, True])
 def test_gate_activations_vs_torch(dev, decay_as_prob):
     """The fused gate kernel == torch's logsigmoid / sigmoid of the biased logits
