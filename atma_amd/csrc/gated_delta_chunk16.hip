@@ -535,9 +535,10 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
     // barrier that began this step)
     copy_rec(min(c + 2, last), (slot + 2) % 3);
     // this wave's copies of chunk c + 1 (issued one step earlier) have landed: after them
-    // came the register loads of step c - 1, this step's O store and its copies (wave 0
-    // issues more copies, so the count is the smaller one)
-    wait_vmcnt<NDMA + NLOAD + 1>();
+    // came the register loads of step c - 1 and this step's copies (wave 0 issues more
+    // copies, so the count is the smaller one).  The O store issued between them is not
+    // counted: a store may complete before older loads, so only loads are counted.
+    wait_vmcnt<NDMA + NLOAD>();
     __syncthreads();
   };
 
