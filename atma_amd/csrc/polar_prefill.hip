@@ -559,23 +559,22 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ql = lane & 31, h = lane >> 5;
 
-  // ---- workgroup -> (b, q head, pair of query tiles), XCD-aware
+  // ---- workgroup -> (query tile, b, q head): one tile per workgroup, tiles in order of
+  // decreasing length (causal: the last tile first) so the dispatcher balances the
+  // triangle; within a rank the G query heads of a KV group share an XCD (its L2)
   const int G = args.Hq / args.Hkv;
-  int bid = blockIdx.x;
+  const int per_rank = args.B * args.Hq;
+  const int rank = blockIdx.x / per_rank;
+  int u = blockIdx.x % per_rank;
   if (args.xcd_remap) {
-    const int x = bid & 7, p = bid >> 3;
-    bid = (x + 8 * (p / G)) * G + p % G;
+    const int x = u & 7, p = u >> 3;
+    u = (x + 8 * (p / G)) * G + p % G;
   }
-  const int g = bid % G;
-  const int unit = bid / G;
-  const int npairs = (args.n_qtiles + 1) / 2;
-  const int pair = unit % npairs;
-  const int grp = unit / npairs;  // b * Hkv + kv head
+  const int g = u % G;
+  const int grp = u / G;  // b * Hkv + kv head
   const int b = grp / args.Hkv, hk = grp % args.Hkv;
   const int hq = hk * G + g;
-  const int npass = pair < args.n_qtiles - 1 - pair ? 2 : 1;
-  for (int pass = 0; pass < npass; ++pass) {
-  const int qt = pass == 0 ? args.n_qtiles - 1 - pair : pair;
+  const int qt = args.n_qtiles - 1 - rank;
   const int q0 = qt * BM;
 
   const T* qp = (const T*)args.q + b * args.q_sb + hq * args.q_sh;
@@ -730,7 +729,7 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int key = st_key(j, i, h);
-          sacc[j][i] = (key < key_hi) & (key >= key_lo) ? sacc[j][i] : -INFINITY;
+          sacc[j][i] = ((key < key_hi) & (key >= key_lo)) ? sacc[j][i] : -INFINITY;
         }
     }
     constexpr float kSafe = __is_same(T, bf16) ? 1048576.f : 16384.f;
@@ -864,19 +863,22 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
         }
     }
   }
-  __syncthreads();  // the next pass reuses the LDS tiles and bounds
-  }  // pass
 }
 
 template <typename T, int D>
 static int launch_fwd(PolarFwdArgs a, hipStream_t stream) {
-  const int64_t units = (int64_t)((a.n_qtiles + 1) / 2) * a.B * a.Hq;
   const int G = a.Hq / a.Hkv;
-  a.xcd_remap = (units % (8 * G) == 0) ? 1 : 0;
-  if constexpr (sizeof(T) == 2)
-    polar_fwd16_kernel<T, D><<<dim3((unsigned)units), dim3(256), 0, stream>>>(a);
-  else
+  if constexpr (sizeof(T) == 2) {
+    // one query tile per workgroup
+    const int64_t per_rank = (int64_t)a.B * a.Hq;
+    a.xcd_remap = (per_rank % (8 * G) == 0) ? 1 : 0;
+    polar_fwd16_kernel<T, D><<<dim3((unsigned)(a.n_qtiles * per_rank)), dim3(256), 0, stream>>>(a);
+  } else {
+    // a pair of query tiles (the i-th longest and the i-th shortest) per workgroup
+    const int64_t units = (int64_t)((a.n_qtiles + 1) / 2) * a.B * a.Hq;
+    a.xcd_remap = (units % (8 * G) == 0) ? 1 : 0;
     polar_fwd_kernel<T, D><<<dim3((unsigned)units), dim3(256), 0, stream>>>(a);
+  }
   return check_launch("polar_attention_fwd");
 }
 
@@ -900,7 +902,7 @@ extern "C" int atma_polar_attention_fwd(
   if (d != 64 && d != 128)
     return set_error(ATMA_ERR_UNSUPPORTED, "polar_attention_fwd: head_dim %lld (supported: 64, 128)",
                      (long long)d);
-  if (Tq > (1 << 30) || Tk > (1 << 30) || B * Hq > (1 << 24))
+  if (Tq > (1 << 30) || Tk > (1 << 30) || B * Hq > (1 << 24) || (Tq + 127) / 128 * B * Hq > 0x7fffffff)
     return set_error(ATMA_ERR_INVALID, "polar_attention_fwd: sizes too large");
   if (B == 0 || Tq == 0) return ATMA_OK;
   if (!q || !k || !v || !n_keys || !v_null || !null_base || !null_slope_raw || !len_gain_raw ||
