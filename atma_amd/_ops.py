@@ -151,7 +151,8 @@ def _(zg, zb, g_bias, b_bias, decay_as_prob):
 @torch.library.custom_op("atma_hip::chunk_gated_delta_rule", mutates_args=())
 def chunk_gated_delta_rule_op(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,
                               initial_state: Optional[Tensor], scale: float, use_qk_l2norm: bool,
-                              want_final: bool) -> List[Tensor]:
+                              want_final: bool, gate_logits: bool = False, g_bias: float = 0.0,
+                              b_bias: float = 0.0) -> List[Tensor]:
     _need_cuda(q, k, v, g, beta, initial_state)
     lib = _lib.load()
     q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
@@ -169,14 +170,15 @@ def chunk_gated_delta_rule_op(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: 
         v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
         g.data_ptr(), beta.data_ptr(), _lib.ptr(initial_state), _lib.ptr(final), o.data_ptr(),
         B, T, H, k.shape[2], dk, dv, _lib.dtype_code(q.dtype), scale, 1 if use_qk_l2norm else 0,
-        chunk,
+        1 if gate_logits else 0, g_bias, b_bias, chunk,
         ws.data_ptr(), ws.numel() * 4, _lib.stream_handle(q.device))
     _lib.check(rc, "chunk_gated_delta_rule")
     return [o, final] if want_final else [o]
 
 
 @chunk_gated_delta_rule_op.register_fake
-def _(q, k, v, g, beta, initial_state, scale, use_qk_l2norm, want_final):
+def _(q, k, v, g, beta, initial_state, scale, use_qk_l2norm, want_final, gate_logits=False,
+      g_bias=0.0, b_bias=0.0):
     B, T, H, dk = q.shape
     dv = v.shape[3]
     o = q.new_empty((B, T, H, dv))

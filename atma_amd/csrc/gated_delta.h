@@ -24,8 +24,30 @@ struct GdnArgs {
   int G;  // query heads per k / v head (k, v carry H / G heads)
   float scale;
   int l2norm;
+  int gate_logits;  // g, beta hold raw logits: the activations below are applied on load
+  float g_bias, b_bias;
   void* ws;
 };
+
+// The memory branch's gate activations (TitansMemory, model/blocks.py:426-490), shared by
+// the stand-alone gate kernel and the prefill's fused load so both give the same bits:
+// log-decay logsigmoid(z + bias) = min(x, 0) - log1p(exp(-|x|)) (stable for either sign)
+// and write strength sigmoid(z + bias).
+__device__ __forceinline__ float gdn_log_decay(float z, float bias) {
+  const float x = z + bias;
+  return fminf(x, 0.f) - log1pf(expf(-fabsf(x)));
+}
+__device__ __forceinline__ float gdn_write_strength(float z, float bias) {
+  const float y = z + bias;
+  return 1.f / (1.f + expf(-y));
+}
+// g and beta of one token as the recurrence takes them (log-decay, write strength)
+__device__ __forceinline__ float gdn_load_g(const GdnArgs& a, int64_t i) {
+  return a.gate_logits ? gdn_log_decay(a.g[i], a.g_bias) : a.g[i];
+}
+__device__ __forceinline__ float gdn_load_beta(const GdnArgs& a, int64_t i) {
+  return a.gate_logits ? gdn_write_strength(a.beta[i], a.b_bias) : a.beta[i];
+}
 
 // Workspace of the 16-bit path: for each of the n = B*H*NC (sequence, head, chunk)
 // records, these fields, each stored as its own array [n][...] so that consecutive

@@ -72,8 +72,8 @@ __global__ void __launch_bounds__(256) gdn_prep_kernel(GdnArgs a) {
     }
     if (lane == 0) {
       const int64_t gi = ((int64_t)b * a.T + t) * a.H + h;
-      lg[r] = ok ? a.g[gi] : 0.f;
-      bet[r] = ok ? a.beta[gi] : 0.f;
+      lg[r] = ok ? gdn_load_g(a, gi) : 0.f;
+      bet[r] = ok ? gdn_load_beta(a, gi) : 0.f;
     }
   }
   __syncthreads();
@@ -340,7 +340,8 @@ extern "C" int atma_chunk_gated_delta_rule(
     int64_t k_st, int64_t k_sh, const void* v, int64_t v_sb, int64_t v_st, int64_t v_sh,
     const float* g, const float* beta, const float* initial_state, float* final_state, void* o,
     int64_t B, int64_t T, int64_t H, int64_t Hkv, int64_t dk, int64_t dv, int dtype, float scale,
-    int use_qk_l2norm, int64_t chunk, void* workspace, size_t workspace_bytes, void* stream) {
+    int use_qk_l2norm, int gate_logits, float g_bias, float b_bias, int64_t chunk, void* workspace,
+    size_t workspace_bytes, void* stream) {
   using namespace atma;
   if (chunk != kChunk)
     return set_error(ATMA_ERR_UNSUPPORTED, "chunk_gated_delta_rule: chunk must be %d", kChunk);
@@ -380,6 +381,7 @@ extern "C" int atma_chunk_gated_delta_rule(
   a.B = (int)B; a.T = (int)T; a.H = (int)H; a.NC = (int)((T + chunk - 1) / chunk);
   a.G = (int)(H / Hkv);
   a.scale = scale; a.l2norm = use_qk_l2norm ? 1 : 0; a.ws = workspace;
+  a.gate_logits = gate_logits ? 1 : 0; a.g_bias = g_bias; a.b_bias = b_bias;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == ATMA_BF16 || dtype == ATMA_F16) return launch_gdn16(a, dtype, (int)dk, s);
   return dk == 128 ? launch_gdn<float, 128>(a, s) : launch_gdn<float, 64>(a, s);

@@ -93,8 +93,8 @@ __global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
     if (tid < C) {
       const int tt = c * C + tid;
       const int64_t gi = ((int64_t)b * a.T + tt) * a.H + h;
-      r.gl = tt < a.T ? a.g[gi] : 0.f;
-      r.bt = tt < a.T ? a.beta[gi] : 0.f;
+      r.gl = tt < a.T ? gdn_load_g(a, gi) : 0.f;
+      r.bt = tt < a.T ? gdn_load_beta(a, gi) : 0.f;
     }
   };
 

@@ -11,7 +11,7 @@
 // groups covering the dk rows.  The slab sits in registers between the two
 // column reductions (pred, then r), so each state byte crosses HBM exactly once
 // in each direction.
-#include "common.h"
+#include "gated_delta.h"
 
 namespace atma {
 
@@ -175,12 +175,9 @@ __global__ void gdn_gates_kernel(const float* __restrict__ zg, const float* __re
                                  float* __restrict__ beta, int64_t n, int decay_as_prob) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const float x = zg[i] + g_bias;
-  // logsigmoid(x) = min(x, 0) - log1p(exp(-|x|)), stable for either sign
-  const float ls = fminf(x, 0.f) - log1pf(expf(-fabsf(x)));
+  const float ls = gdn_log_decay(zg[i], g_bias);
   g[i] = decay_as_prob ? expf(ls) : ls;
-  const float y = zb[i] + b_bias;
-  beta[i] = 1.f / (1.f + expf(-y));
+  beta[i] = gdn_write_strength(zb[i], b_bias);
 }
 }  // namespace atma
 

@@ -48,7 +48,7 @@ def gated_delta_decode_step(q, k, v, gamma, beta, state_table, slots, eps=1e-12,
 @torch.no_grad()
 def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
                            output_final_state=False, use_qk_l2norm_in_kernel=False,
-                           cu_seqlens=None, head_first=False):
+                           cu_seqlens=None, head_first=False, gate_bias=None):
     """Chunked gated-delta prefill with state carry (FLA contract).
 
     q: (B, T, H, dk); k: (B, T, Hkv, dk); v: (B, T, Hkv, dv) with H % Hkv == 0 (query
@@ -57,6 +57,10 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
     ``use_qk_l2norm_in_kernel`` q and k are L2-normalised (x / max(|x|, 1e-12)) before
     the recurrence; q is then scaled by ``scale`` (default dk**-0.5, FLA's default;
     the reference passes 1.0).
+    ``gate_bias=(g_bias, b_bias)`` (an extension, no FLA counterpart): ``g`` and ``beta``
+    are the memory branch's raw gate logits, and the kernel applies
+    ``g = logsigmoid(g + g_bias)``, ``beta = sigmoid(beta + b_bias)`` as it loads them,
+    bit-identical to ``gated_delta_gates`` followed by the plain call, one launch fewer.
     Returns (o (B, T, H, dv) in q's dtype, final_state (B, H, dk, dv) fp32 or None)."""
     if cu_seqlens is not None or head_first:
         raise NotImplementedError("cu_seqlens / head_first layouts are not supported")
@@ -86,9 +90,11 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
         return o, final
     g = g.to(torch.float32).contiguous()
     beta = beta.to(torch.float32).contiguous()
+    gb, bb = (0.0, 0.0) if gate_bias is None else (float(gate_bias[0]), float(gate_bias[1]))
     outs = torch.ops.atma_hip.chunk_gated_delta_rule(q, k, v, g, beta, initial_state, float(scale),
                                                      bool(use_qk_l2norm_in_kernel),
-                                                     bool(output_final_state))
+                                                     bool(output_final_state), gate_bias is not None,
+                                                     gb, bb)
     return outs[0], (outs[1] if output_final_state else None)
 
 

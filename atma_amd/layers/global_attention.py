@@ -79,11 +79,12 @@ class TitansMemory(nn.Module):
         repeat_interleave expansion is not materialised).  initial_state:
         ``[K, V]`` (B, H, dk, dv) fp32 or None.  Returns (out (B, T, dim), final
         state or None) -- ``_mem_prefill_dense`` (``inference/models/atma.py:305-339``)."""
-        glog, beta = gated_delta_gates(*self.raw_logits(x), self.gamma_bias, self.beta_bias)
-        r, S = chunk_gated_delta_rule(q, k, v, glog, beta, scale=1.0,
+        zg, zb = self.raw_logits(x)   # activations applied inside the prefill's load
+        r, S = chunk_gated_delta_rule(q, k, v, zg, zb, scale=1.0,
                                       initial_state=initial_state,
                                       output_final_state=output_final_state,
-                                      use_qk_l2norm_in_kernel=True)
+                                      use_qk_l2norm_in_kernel=True,
+                                      gate_bias=(self.gamma_bias, self.beta_bias))
         return self._out(x, r), S
 
     def step(self, x, q, k, v, state_table, slots):

@@ -3,7 +3,7 @@
 Default workload (the `value`): BASELINE.json configs[1] -- bf16 global-layer prefill,
 B=8, T=2048, 8 query / 2 KV heads, d=128: Polar attention forward (GQA in-kernel) plus
 the gated-delta chunked prefill (C=64, fp32 state from zero, memory gate / beta logits
-through the layer's fused gate kernel: logsigmoid(z + 3.9), sigmoid(z)).  One step = both ops over
+activated inside the prefill kernel's load as the layer does: logsigmoid(z + 3.9), sigmoid(z)).  One step = both ops over
 the resident batch, back to back on one stream (the time with the memory branch on a
 second stream is reported as ms_overlap).
 value = (Polar + gated-delta algorithmic FLOPs) / step time.
@@ -56,9 +56,9 @@ class Prefill:
     """Resident inputs and one step of the prefill hot path."""
 
     def __init__(self, torch, dev, B, T, seed=0):
-        from atma_amd.kernel import chunk_gated_delta_rule, gated_delta_gates, polar_attention_fwd
+        from atma_amd.kernel import chunk_gated_delta_rule, polar_attention_fwd
         self.torch, self.B, self.T = torch, B, T
-        self.fwd, self.gdn, self.gates = polar_attention_fwd, chunk_gated_delta_rule, gated_delta_gates
+        self.fwd, self.gdn = polar_attention_fwd, chunk_gated_delta_rule
         g = torch.Generator(device=dev).manual_seed(seed)
         bf = torch.bfloat16
         self.q = torch.randn(B, HQ, T, D, device=dev, generator=g, dtype=bf)
@@ -80,9 +80,10 @@ class Prefill:
         return self.fwd(self.q, self.k, self.v, self.n_keys, **self.p)
 
     def memory(self):
-        glog, beta = self.gates(self.zg, self.zb, 3.9, 0.0)  # the layer's fused gate kernel
-        return self.gdn(self.qm, self.km, self.vm, glog, beta, scale=1.0, initial_state=self.s0,
-                        output_final_state=True, use_qk_l2norm_in_kernel=True)
+        # raw gate logits: the layer's activations (logsigmoid(z + 3.9), sigmoid(z)) are
+        # applied inside the prefill kernel's load, as TitansMemory does
+        return self.gdn(self.qm, self.km, self.vm, self.zg, self.zb, scale=1.0, initial_state=self.s0,
+                        output_final_state=True, use_qk_l2norm_in_kernel=True, gate_bias=(3.9, 0.0))
 
     def step(self):
         """Both ops of the mixer back to back on one stream."""

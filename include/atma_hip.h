@@ -161,7 +161,11 @@ size_t atma_chunk_gated_delta_workspace_bytes(int64_t B, int64_t T, int64_t H, i
  * g (log-decay) and beta: (B, T, H) fp32 contiguous; initial_state (nullable =
  * zeros) and final_state (nullable = not written): (B, H, dk, dv) fp32 [K, V].
  * Output o: (B, T, H, dv) dtype contiguous.  q, k are L2-normalised when
- * use_qk_l2norm != 0, then q is multiplied by `scale`.  chunk must be 64;
+ * use_qk_l2norm != 0, then q is multiplied by `scale`.  With gate_logits != 0, g and
+ * beta hold the memory branch's raw gate logits and the kernel applies the activations
+ * of atma_gated_delta_gates on load (log-decay logsigmoid(g + g_bias), write strength
+ * sigmoid(beta + b_bias)), bit-identical to calling it first (an extension with no
+ * FLA counterpart: one launch fewer for TitansMemory).  chunk must be 64;
  * dk = dv = 128 or 64.
  */
 int atma_chunk_gated_delta_rule(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
@@ -170,8 +174,9 @@ int atma_chunk_gated_delta_rule(const void* q, int64_t q_sb, int64_t q_st, int64
                                 const float* g, const float* beta, const float* initial_state,
                                 float* final_state, void* o, int64_t B, int64_t T, int64_t H,
                                 int64_t Hkv, int64_t dk, int64_t dv, int dtype, float scale,
-                                int use_qk_l2norm, int64_t chunk, void* workspace,
-                                size_t workspace_bytes, void* stream);
+                                int use_qk_l2norm, int gate_logits, float g_bias, float b_bias,
+                                int64_t chunk, void* workspace, size_t workspace_bytes,
+                                void* stream);
 
 #ifdef __cplusplus
 }

@@ -64,7 +64,8 @@ def test_validation_rejects_without_launch(lib):
     assert rc == 3
     # chunked gated delta: chunk must be 64; dk == dv
     assert lib.atma_chunk_gated_delta_rule(null, 0, 0, 0, null, 0, 0, 0, null, 0, 0, 0, null, null,
-                                           null, null, null, 1, 64, 2, 2, 128, 128, 1, 1.0, 1, 32,
+                                           null, null, null, 1, 64, 2, 2, 128, 128, 1, 1.0, 1, 0,
+                                           0.0, 0.0, 32,
                                            null, 0, null) == 2
     assert lib.atma_chunk_gated_delta_workspace_bytes(1, 65, 2, 128, 128, 64, 0) == 2 * 2 * (5 * 64 * 128 + 4) * 4
     # 16-bit path: per (sequence, head, chunk) w, u (C x d each) and rq (C x C) in 16

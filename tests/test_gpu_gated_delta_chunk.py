@@ -152,3 +152,33 @@ def test_grouped_kv_heads_equal_expanded(dev, dtype, d, T):
     kx, vx = (t.repeat_interleave(H // Hkv, 2) for t in (k, v))
     o2, S2 = _run(dev, q, kx, vx, glog, beta, **kw)
     assert torch.equal(o1, o2) and torch.equal(S1, S2)
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.float32, 128), (torch.bfloat16, 128), (torch.float16, 64)])
+def test_raw_gate_logits_equal_gate_kernel_then_call(dev, dtype, d):
+    """g / beta as raw logits with gate_bias (activations fused into the prefill's load)
+    == the stand-alone gate kernel followed by the plain call, bitwise; and the fused
+    form against the oracle fed torch's logsigmoid / sigmoid."""
+    from atma_amd.kernel import gated_delta_gates
+    B, T, H, Hkv = 2, 200, 4, 2
+    g = torch.Generator().manual_seed(31 + d)
+    q = torch.randn(B, T, H, d, generator=g).to(dtype)
+    k, v = (torch.randn(B, T, Hkv, d, generator=g).to(dtype) for _ in range(2))
+    zg = torch.randn(B, T, H, generator=g) * 3
+    zb = torch.randn(B, T, H, generator=g) * 3
+    S0 = torch.randn(B, H, d, d, generator=g) * 0.1
+    kw = dict(scale=1.0, initial_state=S0, output_final_state=True, use_qk_l2norm_in_kernel=True)
+    o1, S1 = _run(dev, q, k, v, zg, zb, gate_bias=(3.9, 0.5), **kw)
+    glog, beta = gated_delta_gates(zg.to(dev), zb.to(dev), 3.9, 0.5)
+    o2, S2 = _run(dev, q, k, v, glog, beta, **kw)
+    assert torch.equal(o1, o2) and torch.equal(S1, S2)
+    kx, vx = (t.repeat_interleave(H // Hkv, 2) for t in (k, v))
+    o_ref, S_ref = OG.chunk_gated_delta_rule(q.double(), kx.double(), vx.double(),
+                                             F.logsigmoid(zg.double() + 3.9),
+                                             torch.sigmoid(zb.double() + 0.5), scale=1.0,
+                                             initial_state=S0.double(), output_final_state=True,
+                                             use_qk_l2norm_in_kernel=True)
+    if dtype == torch.float32:
+        assert max_abs(o1, o_ref) <= 1e-4 and max_abs(S1, S_ref) <= 1e-4
+    else:
+        assert rel_err(o1, o_ref) <= 2e-2 and rel_err(S1, S_ref) <= 2e-2
