@@ -62,6 +62,37 @@ def _(q, k, v, n_keys, v_null, null_base, null_slope_raw, len_gain_raw, mag_beta
     return [q.new_empty((B, Hq, Tq, d)), q.new_empty((B, Hq, Tq))]
 
 
+# --------------------------------------------------------------------------- Polar packed fwd
+@torch.library.custom_op("atma_hip::polar_attention_packed_fwd", mutates_args=())
+def polar_attention_packed_fwd_op(q: Tensor, k: Tensor, v: Tensor, tile_seq_starts: Tensor,
+                                  tile_q_starts: Tensor, tile_seq_lens: Tensor, v_null: Tensor,
+                                  null_base: Tensor, null_slope_raw: Tensor, len_gain_raw: Tensor,
+                                  mag_beta_raw: Tensor, eps: float, window: int) -> List[Tensor]:
+    _need_cuda(q, k, v, tile_seq_starts, tile_q_starts, tile_seq_lens, v_null)
+    lib = _lib.load()
+    q, k, v = _rows16(q), _rows16(k), _rows16(v)
+    total, Hq, d = q.shape
+    c = torch.empty((total, Hq, d), device=q.device, dtype=q.dtype)
+    mag = torch.empty((total, Hq), device=q.device, dtype=q.dtype)
+    rc = lib.atma_polar_attention_packed_fwd(
+        q.data_ptr(), q.stride(0), q.stride(1), k.data_ptr(), k.stride(0), k.stride(1),
+        v.data_ptr(), v.stride(0), v.stride(1), tile_seq_starts.data_ptr(), tile_q_starts.data_ptr(),
+        tile_seq_lens.data_ptr(), tile_seq_starts.numel(), v_null.data_ptr(), null_base.data_ptr(),
+        null_slope_raw.data_ptr(), len_gain_raw.data_ptr(), mag_beta_raw.data_ptr(),
+        c.data_ptr(), c.stride(0), c.stride(1), mag.data_ptr(), mag.stride(0), mag.stride(1),
+        total, Hq, k.shape[1], d, _lib.dtype_code(q.dtype), window, eps,
+        _lib.stream_handle(q.device))
+    _lib.check(rc, "polar_attention_packed_fwd")
+    return [c, mag]
+
+
+@polar_attention_packed_fwd_op.register_fake
+def _(q, k, v, tile_seq_starts, tile_q_starts, tile_seq_lens, v_null, null_base, null_slope_raw,
+      len_gain_raw, mag_beta_raw, eps, window):
+    total, Hq, d = q.shape
+    return [q.new_empty((total, Hq, d)), q.new_empty((total, Hq))]
+
+
 # --------------------------------------------------------------------------- Polar decode
 @torch.library.custom_op("atma_hip::polar_attention_decode", mutates_args=())
 def polar_attention_decode_op(q: Tensor, k_cache: Tensor, v_cache: Tensor, block_tables: Tensor,

@@ -59,6 +59,16 @@ struct PolarFwdArgs {
   float eps;
   int n_qtiles;
   int xcd_remap;
+  // output strides (elements) of c (b, head, query) and of mag; the saved statistics
+  // keep the (B, Hq, Tq) layout
+  int64_t c_sb, c_sh, c_st, m_sb, m_sh, m_st;
+  // packed ragged fresh prefill (16-bit kernel only; null otherwise): tile i covers query
+  // rows tile_q_start[i] .. + 127 of the sequence stored at packed tokens
+  // tile_seq_start[i] .. + tile_seq_len[i] - 1; n = local position + 1, causal
+  const int* tile_seq_start;
+  const int* tile_q_start;
+  const int* tile_seq_len;
+  int total_tokens;
 };
 
 template <typename T, int D>
@@ -559,32 +569,55 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ql = lane & 31, h = lane >> 5;
 
-  // ---- workgroup -> (query tile, b, q head): one tile per workgroup, tiles in order of
-  // decreasing length (causal: the last tile first) so the dispatcher balances the
-  // triangle; within a rank the G query heads of a KV group share an XCD (its L2)
+  // ---- workgroup -> (query tile, b, q head): one tile per workgroup.  Dense: tiles in
+  // order of decreasing length (causal: the last tile first) so the dispatcher balances
+  // the triangle; within a rank the G query heads of a KV group share an XCD (its L2).
+  // Packed: workgroup = (tile of the map, q head), the G heads of a group adjacent.
   const int G = args.Hq / args.Hkv;
-  const int per_rank = args.B * args.Hq;
-  const int rank = blockIdx.x / per_rank;
-  int u = blockIdx.x % per_rank;
-  if (args.xcd_remap) {
-    const int x = u & 7, p = u >> 3;
-    u = (x + 8 * (p / G)) * G + p % G;
+  const bool packed = args.tile_seq_start != nullptr;
+  int b, hq, q0, Tq = args.Tq, Tk = args.Tk;
+  int64_t tok0 = 0;  // packed: first token of the sequence
+  if (!packed) {
+    const int per_rank = args.B * args.Hq;
+    const int rank = blockIdx.x / per_rank;
+    int u = blockIdx.x % per_rank;
+    if (args.xcd_remap) {
+      const int x = u & 7, p = u >> 3;
+      u = (x + 8 * (p / G)) * G + p % G;
+    }
+    const int grp = u / G;  // b * Hkv + kv head
+    b = grp / args.Hkv;
+    hq = (grp % args.Hkv) * G + u % G;
+    q0 = (args.n_qtiles - 1 - rank) * BM;
+  } else {
+    int u = blockIdx.x;
+    if (args.xcd_remap) {
+      const int x = u & 7, p = u >> 3;
+      u = (x + 8 * (p / G)) * G + p % G;
+    }
+    const int tile = u / args.Hq;
+    const int seq_start = args.tile_seq_start[tile], q_start = args.tile_q_start[tile];
+    const int seq_len = args.tile_seq_len[tile];
+    // a tile outside the packed tokens (or not on a 128-row boundary) is skipped whole
+    if (seq_start < 0 || seq_len < 1 || seq_len > args.total_tokens - seq_start || q_start < 0 ||
+        q_start >= seq_len || q_start % BM)
+      return;
+    b = 0;
+    hq = u % args.Hq;
+    q0 = q_start;
+    Tq = Tk = seq_len;
+    tok0 = seq_start;
   }
-  const int g = u % G;
-  const int grp = u / G;  // b * Hkv + kv head
-  const int b = grp / args.Hkv, hk = grp % args.Hkv;
-  const int hq = hk * G + g;
-  const int qt = args.n_qtiles - 1 - rank;
-  const int q0 = qt * BM;
+  const int hk = hq / G;
 
-  const T* qp = (const T*)args.q + b * args.q_sb + hq * args.q_sh;
-  const T* kp = (const T*)args.k + b * args.k_sb + hk * args.k_sh;
-  const T* vp = (const T*)args.v + b * args.v_sb + hk * args.v_sh;
+  const T* qp = (const T*)args.q + b * args.q_sb + hq * args.q_sh + tok0 * args.q_st;
+  const T* kp = (const T*)args.k + b * args.k_sb + hk * args.k_sh + tok0 * args.k_st;
+  const T* vp = (const T*)args.v + b * args.v_sb + hk * args.v_sh + tok0 * args.v_st;
 
   // ---- per-query calibration (lane pair owns query row qi)
   const int qi = q0 + wave * 32 + ql;
-  const bool q_ok = qi < args.Tq;
-  const float n_raw = q_ok ? args.n_keys[qi] : 0.f;
+  const bool q_ok = qi < Tq;
+  const float n_raw = q_ok ? (packed ? (float)(qi + 1) : args.n_keys[qi]) : 0.f;
   float n_cal = n_raw;
   if (args.window > 0) n_cal = fminf(n_cal, (float)args.window);
   n_cal = fmaxf(n_cal, 1.f);
@@ -616,9 +649,9 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
   }
   int kend = 0, kbeg = 0;
   if (g_nhi > 0.f) {
-    float hiF = fminf(g_nhi, (float)args.Tk);
+    float hiF = fminf(g_nhi, (float)Tk);
     kend = (int)ceilf(hiF);
-    if (args.is_causal) kend = min(kend, min(q0 + BM, args.Tk));
+    if (args.is_causal) kend = min(kend, min(q0 + BM, Tk));
     if (args.window > 0) kbeg = max((int)floorf(g_nlo) - args.window, 0);
     kbeg = (kbeg / BN) * BN;
   }
@@ -641,27 +674,44 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
   // ---- direct copies of one key block: this wave's rows 16 wave .. 16 wave + 15 of K
   // and V, RPI rows per instruction; lane l lands at chunk position l % CPR of row
   // l / CPR and fetches the logical chunk stored there.  The buffer ends after the
-  // last key row, so rows past Tk read as zeros (finite; their scores are masked and
-  // their p is exactly 0).  Per lane: one byte offset per copy instruction (the swizzle
-  // depends on the row only through RPI r + l / CPR, the same for every wave).
+  // last key row, so in a partial last block rows past Tk read as zeros (finite; their
+  // scores are masked and their p is exactly 0).  The descriptor's range check covers
+  // the per-lane and instruction offsets, not the scalar one: a full block keeps one
+  // byte offset per lane and copy instruction and puts the wave's row in the scalar
+  // offset, a partial block puts the whole row offset into the per-lane offset
+  // (recomputed from a laundered lane index, so it holds no extra registers).
   const uint32_t kst2 = (uint32_t)args.k_st * 2u, vst2 = (uint32_t)args.v_st * 2u;
-  const uint32_t lrow = (uint32_t)(lane / CPR);
   constexpr int NCP = BN / 4 / RPI;  // copy instructions per wave and tensor
+  static_assert(RPI * NCP == 16, "a wave copies 16 rows");
+  const uint32_t lrow = (uint32_t)(lane / CPR);
   uint32_t coff[NCP];
 #pragma unroll
   for (int r = 0; r < NCP; ++r) coff[r] = 16u * ((lane % CPR) ^ lds_swizzle<CPR>(RPI * r + lane / CPR));
   const uint32_t krow_off = lrow * kst2, vrow_off = lrow * vst2;
   auto copy_block = [&](int blk, int buf) {
-    const int rows = min(args.Tk - blk * BN, BN);
+    const int rows = min(Tk - blk * BN, BN);
     const auto krs = buffer_rsrc(kp + (int64_t)blk * BN * args.k_st,
                                  (uint32_t)((rows - 1) * args.k_st + D) * 2u);
     const auto vrs = buffer_rsrc(vp + (int64_t)blk * BN * args.v_st,
                                  (uint32_t)((rows - 1) * args.v_st + D) * 2u);
+    if (rows == BN) {
 #pragma unroll
-    for (int r = 0; r < NCP; ++r) {
-      const uint32_t row0 = 16u * wave + RPI * r;
-      dma_buf16(krs, krow_off + coff[r], row0 * kst2, Ks + buf * TILE + row0 * D);
-      dma_buf16(vrs, vrow_off + coff[r], row0 * vst2, Vs + buf * TILE + row0 * D);
+      for (int r = 0; r < NCP; ++r) {
+        const uint32_t row0 = 16u * wave + RPI * r;
+        dma_buf16(krs, krow_off + coff[r], row0 * kst2, Ks + buf * TILE + row0 * D);
+        dma_buf16(vrs, vrow_off + coff[r], row0 * vst2, Vs + buf * TILE + row0 * D);
+      }
+    } else {
+      uint32_t ln = (uint32_t)lane;
+      asm volatile("" : "+v"(ln));
+      const uint32_t lr = ln / CPR;
+#pragma unroll
+      for (int r = 0; r < NCP; ++r) {
+        const uint32_t row0 = 16u * wave + RPI * r;
+        const uint32_t co = 16u * ((ln % CPR) ^ lds_swizzle<CPR>(RPI * r + lr));
+        dma_buf16(krs, (row0 + lr) * kst2 + co, 0, Ks + buf * TILE + row0 * D);
+        dma_buf16(vrs, (row0 + lr) * vst2 + co, 0, Vs + buf * TILE + row0 * D);
+      }
     }
   };
   // element offset of logical chunk c of row r
@@ -715,12 +765,12 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
     }
 
     // ---- online softmax: optimistic pass against the running max (see polar_fwd_kernel)
-    const bool full = (k0 + BN <= (int)fminf(w_nlo, (float)args.Tk)) &&
+    const bool full = (k0 + BN <= (int)fminf(w_nlo, (float)Tk)) &&
                       (args.window <= 0 || (float)k0 >= w_nhi - (float)args.window);
     if (!full) {
       // key valid <=> key_lo <= key < key_hi (integer keys: key < n <=> key < ceil n,
       // key >= x <=> key >= ceil x)
-      const float tkf = (float)args.Tk;
+      const float tkf = (float)Tk;
       const int key_hi = (int)ceilf(fminf(n_raw, tkf)) - k0;
       const int key_lo =
           args.window > 0 ? (int)ceilf(fminf(n_raw - (float)args.window, tkf)) - k0 : -(1 << 30);
@@ -827,8 +877,8 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
   const float magv = tanhf(mbeta * log1pf(m_eff));
 
   if (q_ok) {
-    const int64_t row = ((int64_t)b * args.Hq + hq) * args.Tq + qi;
-    T* cp = (T*)args.c + row * D;
+    const int64_t row = ((int64_t)b * args.Hq + hq) * args.Tq + qi;  // saved statistics
+    T* cp = (T*)args.c + b * args.c_sb + hq * args.c_sh + (tok0 + qi) * args.c_st;
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
 #pragma unroll
@@ -846,7 +896,7 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
       }
     }
     if (h == 0) {
-      ((T*)args.mag)[row] = (T)magv;
+      ((T*)args.mag)[b * args.m_sb + hq * args.m_sh + (tok0 + qi) * args.m_st] = (T)magv;
       if (args.stat_m) args.stat_m[row] = mn * kLn2;
       if (args.stat_l) args.stat_l[row] = L;
       if (args.stat_q2) args.stat_q2[row] = Q2;
@@ -931,10 +981,71 @@ extern "C" int atma_polar_attention_fwd(
   a.window = window > 0 ? (int)window : 0;
   a.eps = eps;
   a.n_qtiles = (int)((Tq + 127) / 128);
+  a.c_st = d; a.c_sh = Tq * d; a.c_sb = Hq * Tq * d;  // c, mag contiguous (B, Hq, Tq[, d])
+  a.m_st = 1; a.m_sh = Tq; a.m_sb = Hq * Tq;
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
     case ATMA_BF16: return d == 128 ? launch_fwd<bf16, 128>(a, s) : launch_fwd<bf16, 64>(a, s);
     case ATMA_F16: return d == 128 ? launch_fwd<f16, 128>(a, s) : launch_fwd<f16, 64>(a, s);
     default: return d == 128 ? launch_fwd<float, 128>(a, s) : launch_fwd<float, 64>(a, s);
   }
+}
+
+extern "C" int atma_polar_attention_packed_fwd(
+    const void* q, int64_t q_st, int64_t q_sh, const void* k, int64_t k_st, int64_t k_sh,
+    const void* v, int64_t v_st, int64_t v_sh, const int32_t* tile_seq_start,
+    const int32_t* tile_q_start, const int32_t* tile_seq_len, int64_t n_tiles,
+    const float* v_null, const float* null_base, const float* null_slope_raw,
+    const float* len_gain_raw, const float* mag_beta_raw, void* c, int64_t c_st, int64_t c_sh,
+    void* mag, int64_t m_st, int64_t m_sh, int64_t total_tokens, int64_t Hq, int64_t Hkv,
+    int64_t d, int dtype, int64_t window, float eps, void* stream) {
+  using namespace atma;
+  if (n_tiles < 0 || total_tokens < 0 || Hq <= 0 || Hkv <= 0)
+    return set_error(ATMA_ERR_INVALID, "polar_attention_packed_fwd: bad sizes");
+  if (Hq % Hkv) return set_error(ATMA_ERR_INVALID, "polar_attention_packed_fwd: Hq %% Hkv != 0");
+  if (dtype != ATMA_BF16 && dtype != ATMA_F16)
+    return set_error(ATMA_ERR_UNSUPPORTED, "polar_attention_packed_fwd: 16-bit inputs only");
+  if (d != 64 && d != 128)
+    return set_error(ATMA_ERR_UNSUPPORTED, "polar_attention_packed_fwd: head_dim %lld (supported: 64, 128)",
+                     (long long)d);
+  if (total_tokens > (1 << 30) || n_tiles * Hq > 0x7fffffff)
+    return set_error(ATMA_ERR_INVALID, "polar_attention_packed_fwd: sizes too large");
+  if (n_tiles == 0 || total_tokens == 0) return ATMA_OK;
+  if (!q || !k || !v || !tile_seq_start || !tile_q_start || !tile_seq_len || !v_null || !null_base ||
+      !null_slope_raw || !len_gain_raw || !mag_beta_raw || !c || !mag)
+    return set_error(ATMA_ERR_INVALID, "polar_attention_packed_fwd: null pointer");
+  auto al16 = [](const void* p, int64_t s1, int64_t s2) {
+    return ((uintptr_t)p % 16 == 0) && ((s1 * 2) % 16 == 0) && ((s2 * 2) % 16 == 0);
+  };
+  if (!al16(q, q_st, q_sh) || !al16(k, k_st, k_sh) || !al16(v, v_st, v_sh) || !al16(c, c_st, c_sh))
+    return set_error(ATMA_ERR_INVALID, "polar_attention_packed_fwd: tensors must be 16-byte aligned rows");
+  if (q_st >= (1 << 24) || k_st >= (1 << 24) || v_st >= (1 << 24))
+    // a 64-row key block is copied through one buffer descriptor with 32-bit offsets
+    return set_error(ATMA_ERR_UNSUPPORTED, "polar_attention_packed_fwd: token stride too large");
+  PolarFwdArgs a{};
+  a.q = q; a.q_st = q_st; a.q_sh = q_sh;
+  a.k = k; a.k_st = k_st; a.k_sh = k_sh;
+  a.v = v; a.v_st = v_st; a.v_sh = v_sh;
+  a.v_null = v_null; a.null_base = null_base; a.null_slope_raw = null_slope_raw;
+  a.len_gain_raw = len_gain_raw; a.mag_beta_raw = mag_beta_raw;
+  a.c = c; a.mag = mag;
+  a.c_st = c_st; a.c_sh = c_sh; a.m_st = m_st; a.m_sh = m_sh;
+  a.B = 1; a.Hq = (int)Hq; a.Hkv = (int)Hkv;
+  a.is_causal = 1;
+  a.window = window > 0 ? (int)window : 0;
+  a.eps = eps;
+  a.tile_seq_start = tile_seq_start; a.tile_q_start = tile_q_start; a.tile_seq_len = tile_seq_len;
+  a.total_tokens = (int)total_tokens;
+  const int64_t G = Hq / Hkv;
+  const int64_t grid = n_tiles * Hq;
+  a.xcd_remap = (grid % (8 * G) == 0) ? 1 : 0;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == ATMA_BF16) {
+    if (d == 128) polar_fwd16_kernel<bf16, 128><<<dim3((unsigned)grid), dim3(256), 0, s>>>(a);
+    else polar_fwd16_kernel<bf16, 64><<<dim3((unsigned)grid), dim3(256), 0, s>>>(a);
+  } else {
+    if (d == 128) polar_fwd16_kernel<f16, 128><<<dim3((unsigned)grid), dim3(256), 0, s>>>(a);
+    else polar_fwd16_kernel<f16, 64><<<dim3((unsigned)grid), dim3(256), 0, s>>>(a);
+  }
+  return check_launch("polar_attention_packed_fwd");
 }

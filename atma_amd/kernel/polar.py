@@ -67,6 +67,42 @@ def polar_attention_fwd(q, k, v, n_keys, *, v_null, null_base, null_slope_raw, l
 
 
 @torch.no_grad()
+def polar_attention_packed_fwd(q, k, v, tile_seq_starts, tile_q_starts, tile_seq_lens, *, v_null,
+                               null_base, null_slope_raw, len_gain_raw, mag_beta_raw, eps=1e-6,
+                               input_precision="ieee", window=None):
+    """Grouped fresh-prefill Polar attention for packed variable-length requests.
+    Mirrors ``polar_attention_packed_fwd`` (``kernel/polar_triton.py:613-669``).
+
+    q: (total_tokens, Hq, d); k, v: (total_tokens, Hkv, d) with Hq % Hkv == 0 -- the
+    reference's expanded form (Hkv == Hq) or unexpanded GQA heads.  ``tile_*``: one
+    entry per 128-row query tile, (first packed token of the tile's sequence, the tile's
+    first query position in it, the sequence length), as the serving context builds
+    them (``inference/engine/model_runner.py:390-404``).  Every sequence is a fresh
+    causal prompt.  Returns (c (total_tokens, Hq, d), mag (total_tokens, Hq)) in q's dtype."""
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3 or k.shape != v.shape \
+            or k.shape[0] != q.shape[0] or k.shape[2] != q.shape[2] or q.shape[1] % k.shape[1]:
+        raise ValueError("q, k, and v must have identical [tokens, heads, dim] shapes "
+                         "(k, v may carry fewer heads dividing q's)")
+    total, heads, dk = q.shape
+    if q.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("packed Polar route is enabled only for 16-bit inference")
+    if k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("q, k, v must share a dtype")
+    if dk & (dk - 1):
+        raise ValueError(f"head_dim (dk={dk}) must be a power of two")
+    if not (tile_seq_starts.numel() == tile_q_starts.numel() == tile_seq_lens.numel()):
+        raise ValueError("packed Polar tile-map tensors must have equal lengths")
+    if input_precision not in ("ieee", "tf32", "tf32x3"):
+        raise ValueError(f"unknown input_precision {input_precision!r}")
+    maps = [t.to(device=q.device, dtype=torch.int32).reshape(-1).contiguous()
+            for t in (tile_seq_starts, tile_q_starts, tile_seq_lens)]
+    p = _params(q.device, v_null, null_base, null_slope_raw, len_gain_raw, mag_beta_raw)
+    c, mag = torch.ops.atma_hip.polar_attention_packed_fwd(q, k, v, *maps, *p, float(eps),
+                                                           _window_arg(window))
+    return c, mag
+
+
+@torch.no_grad()
 def polar_attention_decode(q, k_cache, v_cache, block_tables, context_lens, *, v_null, null_base,
                            null_slope_raw, len_gain_raw, mag_beta_raw, eps=1e-6, block_n=None,
                            num_warps=None, num_stages=None, window=None):

@@ -90,6 +90,32 @@ int atma_polar_attention_fwd(const void* q, int64_t q_sb, int64_t q_sh, int64_t 
                              void* stream);
 
 /*
+ * Grouped fresh-prefill Polar attention over packed ragged requests.  Replaces
+ * polar_attention_packed_fwd / _polar_packed_fwd_kernel (kernel/polar_triton.py:194-309,
+ * 613-669).  q: (total_tokens, Hq, d) strides (q_st, q_sh, 1); k, v: (total_tokens, Hkv, d)
+ * with Hq % Hkv == 0 (Hkv == Hq is the reference's expanded form).  Tile map (device,
+ * int32, n_tiles entries each, as the serving context builds it,
+ * inference/engine/model_runner.py:390-404): tile i covers query rows
+ * tile_q_start[i] .. + 127 (a multiple of 128) of the sequence stored at packed tokens
+ * tile_seq_start[i] .. + tile_seq_len[i] - 1.  Every sequence is a fresh causal prompt:
+ * query j sees keys 0..j of its own sequence (n = j + 1; with window > 0 only the last
+ * `window` of them, temp/null from max(min(n, window), 1)).  A tile outside
+ * [0, total_tokens) or off a 128-row boundary is skipped (its rows are not written).
+ * Outputs (dtype): c with strides (c_st, c_sh, 1), mag with strides (m_st, m_sh).
+ * Raw Polar parameters as atma_polar_attention_fwd.  bf16 / fp16 only; d = 64 or 128.
+ */
+int atma_polar_attention_packed_fwd(const void* q, int64_t q_st, int64_t q_sh, const void* k,
+                                    int64_t k_st, int64_t k_sh, const void* v, int64_t v_st,
+                                    int64_t v_sh, const int32_t* tile_seq_start,
+                                    const int32_t* tile_q_start, const int32_t* tile_seq_len,
+                                    int64_t n_tiles, const float* v_null, const float* null_base,
+                                    const float* null_slope_raw, const float* len_gain_raw,
+                                    const float* mag_beta_raw, void* c, int64_t c_st,
+                                    int64_t c_sh, void* mag, int64_t m_st, int64_t m_sh,
+                                    int64_t total_tokens, int64_t Hq, int64_t Hkv, int64_t d,
+                                    int dtype, int64_t window, float eps, void* stream);
+
+/*
  * Workspace bytes atma_polar_attention_decode needs for this launch shape.
  */
 size_t atma_polar_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t max_pages,

@@ -75,6 +75,13 @@ def test_validation_rejects_without_launch(lib):
     # gated delta step: unsupported dims
     assert lib.atma_gated_delta_decode_step(null, 0, 0, null, 0, 0, null, 0, 0, null, null, null, 1,
                                             null, null, 1, 1, 1, 96, 96, 1, 1e-12, null) == 2
+    # packed Polar prefill: 16-bit only; no tiles is a no-op
+    assert lib.atma_polar_attention_packed_fwd(null, 0, 0, null, 0, 0, null, 0, 0, null, null, null, 1,
+                                               null, null, null, null, null, null, 0, 0, null, 0, 0,
+                                               10, 8, 2, 128, 0, 0, 1e-6, null) == 2
+    assert lib.atma_polar_attention_packed_fwd(null, 0, 0, null, 0, 0, null, 0, 0, null, null, null, 0,
+                                               null, null, null, null, null, null, 0, 0, null, 0, 0,
+                                               10, 8, 2, 128, 1, 0, 1e-6, null) == 0
     # store_kvcache: unknown dtype
     assert lib.atma_store_kvcache(null, 0, null, 0, null, null, null, 1, 256, 8, 9, null) == 1
     # zero-size requests are no-ops
@@ -107,6 +114,25 @@ def test_gated_delta_wrappers_check_head_grouping():
     table = torch.zeros(2, 6, 64, 64)
     with pytest.raises(ValueError, match="multiple of k/v heads"):
         gated_delta_decode_step(q[:, 0], k[:, 0], k[:, 0], g[:, 0], g[:, 0], table, torch.zeros(1))
+
+
+def test_packed_wrapper_validates_like_the_reference():
+    """kernel/polar_triton.py:625-635: 16-bit only, [tokens, heads, dim] shapes, equal-length
+    tile maps, power-of-two head dim -- all checked before any device work."""
+    from atma_amd.kernel import polar_attention_packed_fwd
+    p = dict(v_null=torch.zeros(2, 128), null_base=torch.zeros(2), null_slope_raw=torch.zeros(2),
+             len_gain_raw=torch.zeros(2), mag_beta_raw=torch.zeros(2))
+    t = torch.zeros(3, dtype=torch.int32)
+    q = torch.zeros(10, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="16-bit"):
+        polar_attention_packed_fwd(q.float(), q.float(), q.float(), t, t, t, **p)
+    with pytest.raises(ValueError, match="equal lengths"):
+        polar_attention_packed_fwd(q, q, q, t, t, t[:2], **p)
+    with pytest.raises(ValueError, match="tokens, heads, dim"):
+        polar_attention_packed_fwd(q, q[:5], q[:5], t, t, t, **p)
+    q96 = torch.zeros(10, 2, 96, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="power of two"):
+        polar_attention_packed_fwd(q96, q96, q96, t, t, t, **p)
 
 
 def test_cpu_tensors_fail_loudly():
