@@ -39,6 +39,9 @@ SIGNATURES = {
     "atma_gated_delta_decode_step": (_i32, [
         _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _p, _p,
         _i64, _i64, _i64, _i64, _i64, _i32, _f32, _p]),
+    "atma_causal_conv1d_decode_step": (_i32, [
+        _p, _i64, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i32,
+        _i32, _p]),
     "atma_gated_delta_gates": (_i32, [_p, _p, _f32, _f32, _p, _p, _i64, _i32, _p]),
     "atma_chunk_gated_delta_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64, _i32]),
     "atma_chunk_gated_delta_rule": (_i32, [

@@ -156,6 +156,32 @@ def _(q, k, v, gamma, beta, state_table, slots, eps):
     return q.new_empty((B, H, state_table.shape[3]), dtype=torch.float32)
 
 
+# --------------------------------------------------------------------------- conv decode step
+@torch.library.custom_op("atma_hip::causal_conv1d_decode_step", mutates_args=("state_table",))
+def causal_conv1d_decode_step_op(x: Tensor, weight: Tensor, slots: Tensor, state_table: Tensor,
+                                 residual: bool) -> Tensor:
+    _need_cuda(x, weight, slots, state_table)
+    lib = _lib.load()
+    x = x if x.stride(-1) == 1 else x.contiguous()
+    B, D = x.shape
+    K = weight.shape[1]
+    out = torch.empty((B, D), device=x.device, dtype=x.dtype)
+    st = state_table.stride() if state_table.dim() == 3 else (0, 0, 0)   # unused when K == 1
+    rows = state_table.shape[0] if state_table.dim() == 3 else 0
+    rc = lib.atma_causal_conv1d_decode_step(
+        x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), weight.stride(1),
+        slots.data_ptr(), state_table.data_ptr(), st[0], st[1], st[2], rows, out.data_ptr(),
+        out.stride(0), B, D, K, 1 if residual else 0, _lib.dtype_code(x.dtype),
+        _lib.stream_handle(x.device))
+    _lib.check(rc, "causal_conv1d_decode_step")
+    return out
+
+
+@causal_conv1d_decode_step_op.register_fake
+def _(x, weight, slots, state_table, residual):
+    return torch.empty_like(x)
+
+
 # --------------------------------------------------------------------------- memory gates
 @torch.library.custom_op("atma_hip::gated_delta_gates", mutates_args=())
 def gated_delta_gates_op(zg: Tensor, zb: Tensor, g_bias: float, b_bias: float,

@@ -9,6 +9,7 @@ without the library or on CPU tensors raises (there is no silent fallback).
 import torch
 
 from .. import _lib
+from .conv import causal_conv1d_decode_step
 from .gated_delta import chunk_gated_delta_rule, gated_delta_decode_step, gated_delta_gates
 from .polar import polar_attention_decode, polar_attention_fwd, polar_attention_packed_fwd
 
@@ -22,4 +23,5 @@ __all__ = [
     "gated_delta_decode_step",
     "chunk_gated_delta_rule",
     "gated_delta_gates",
+    "causal_conv1d_decode_step",
 ]

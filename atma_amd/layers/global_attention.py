@@ -27,9 +27,8 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from ..kernel import (chunk_gated_delta_rule, gated_delta_decode_step, gated_delta_gates,
-                      polar_attention_decode,
-                      polar_attention_fwd)
+from ..kernel import (causal_conv1d_decode_step, chunk_gated_delta_rule, gated_delta_decode_step,
+                      gated_delta_gates, polar_attention_decode, polar_attention_fwd)
 from .attention import store_kvcache
 
 # Polar structural priors (model/reference.py:17-20)
@@ -187,12 +186,9 @@ class PolarAttention(nn.Module):
     @staticmethod
     def _conv_step(t, conv, tails, slots):
         """Residual conv for one new token per sequence, tails advanced in place
-        (``_gpu_conv_step``, ``inference/models/atma.py:165-192``).  t: (B, C)."""
-        w = conv.weight.squeeze(1).to(t.dtype)           # (C, K)
-        st = tails[slots].to(t.dtype)                    # (B, C, K-1)
-        out = (st * w[:, :-1]).sum(-1) + t * w[:, -1]
-        tails[slots] = torch.cat([st[:, :, 1:], t.unsqueeze(-1)], dim=-1).to(tails.dtype)
-        return t + out
+        (``_gpu_conv_step``, ``inference/models/atma.py:165-192``): one fused launch of
+        ``causal_conv1d_decode_step`` with the residual add.  t: (B, C)."""
+        return causal_conv1d_decode_step(t, conv.weight.squeeze(1), slots, tails, residual=True)
 
     def _combine(self, c, mag, gate):
         """``proj(c * sigmoid(gate)) + mu_proj(mag)`` (``inference/models/atma.py:246-252``).

@@ -160,6 +160,23 @@ int atma_gated_delta_decode_step(const void* q, int64_t q_sb, int64_t q_sh, cons
                                  int64_t dv, int dtype, float eps, void* stream);
 
 /*
+ * One depthwise causal-convolution step, slot-indexed state advanced IN PLACE.
+ * Replaces causal_conv1d_decode_step (kernel/causal_conv1d_triton.py:18-63), the
+ * global layer's Canon q / k / v convolution at decode (inference/models/atma.py:160-192).
+ * x: (B, D) strides (x_sb, 1); weight: (D, K) strides (w_sd, w_sk), x's dtype;
+ * state_table: (max_seqs, D, K - 1) strides (s_ss, s_sd, s_sk), x's dtype; slots: (B,)
+ * int64 rows of the table.  out (B, D) strides (o_sb, 1):
+ * x w[:, K-1] + sum_j state[slot, :, j] w[:, j] (plus x when residual != 0), accumulated
+ * in fp32; the state row becomes (state[slot, :, 1:], x).  K = 1 touches no state.  A
+ * slot outside [0, max_seqs) leaves the table untouched and yields NaN.  1 <= K <= 16.
+ */
+int atma_causal_conv1d_decode_step(const void* x, int64_t x_sb, const void* weight, int64_t w_sd,
+                                   int64_t w_sk, const int64_t* slots, void* state_table,
+                                   int64_t s_ss, int64_t s_sd, int64_t s_sk, int64_t max_seqs,
+                                   void* out, int64_t o_sb, int64_t B, int64_t D, int64_t K,
+                                   int residual, int dtype, void* stream);
+
+/*
  * Gate activations of the memory branch in one launch.  Replaces the torch
  * add / logsigmoid / sigmoid of TitansMemory (model/blocks.py:426-490,
  * inference/models/atma.py:305-375): g = logsigmoid(zg + g_bias) -- the log-decay

@@ -82,6 +82,11 @@ def test_validation_rejects_without_launch(lib):
     assert lib.atma_polar_attention_packed_fwd(null, 0, 0, null, 0, 0, null, 0, 0, null, null, null, 0,
                                                null, null, null, null, null, null, 0, 0, null, 0, 0,
                                                10, 8, 2, 128, 1, 0, 1e-6, null) == 0
+    # conv decode step: K out of range; zero rows are a no-op
+    assert lib.atma_causal_conv1d_decode_step(null, 0, null, 0, 0, null, null, 0, 0, 0, 1, null, 0,
+                                              1, 8, 17, 0, 1, null) == 1
+    assert lib.atma_causal_conv1d_decode_step(null, 0, null, 0, 0, null, null, 0, 0, 0, 1, null, 0,
+                                              0, 8, 4, 0, 1, null) == 0
     # store_kvcache: unknown dtype
     assert lib.atma_store_kvcache(null, 0, null, 0, null, null, null, 1, 256, 8, 9, null) == 1
     # zero-size requests are no-ops
