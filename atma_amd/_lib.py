@@ -27,7 +27,11 @@ SIGNATURES = {
     "atma_polar_attention_fwd": (_i32, [
         _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
         _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
-        _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i64, _f32, _p]),
+        _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i64, _i32, _f32, _p]),
+    "atma_polar_attention_bwd": (_i32, [
+        _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
+        _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i64,
+        _p]),
     "atma_polar_attention_packed_fwd": (_i32, [
         _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64,
         _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i64,

@@ -50,7 +50,7 @@ def polar_attention_fwd_op(q: Tensor, k: Tensor, v: Tensor, n_keys: Tensor, v_nu
         n_keys.data_ptr(), v_null.data_ptr(), null_base.data_ptr(), null_slope_raw.data_ptr(),
         len_gain_raw.data_ptr(), mag_beta_raw.data_ptr(), c.data_ptr(), mag.data_ptr(),
         None, None, None, None, B, Hq, Hkv, Tq, Tk, d, _lib.dtype_code(q.dtype),
-        1 if is_causal else 0, window, eps, _lib.stream_handle(q.device))
+        1 if is_causal else 0, window, 0, eps, _lib.stream_handle(q.device))
     _lib.check(rc, "polar_attention_fwd")
     return [c, mag]
 
@@ -60,6 +60,81 @@ def _(q, k, v, n_keys, v_null, null_base, null_slope_raw, len_gain_raw, mag_beta
       is_causal, window):
     B, Hq, Tq, d = q.shape
     return [q.new_empty((B, Hq, Tq, d)), q.new_empty((B, Hq, Tq))]
+
+
+# --------------------------------------------------------------------------- Polar training pair
+@torch.library.custom_op("atma_hip::polar_attention_fwd_train", mutates_args=())
+def polar_attention_fwd_train_op(q: Tensor, k: Tensor, v: Tensor, n_keys: Tensor, v_null: Tensor,
+                                 null_base: Tensor, null_slope_raw: Tensor, len_gain_raw: Tensor,
+                                 mag_beta_raw: Tensor, eps: float, is_causal: bool, window: int,
+                                 preserve_length: bool) -> List[Tensor]:
+    """Forward that also returns the saved statistics (M, L, Q2, s) of the backward."""
+    _need_cuda(q, k, v, n_keys, v_null)
+    lib = _lib.load()
+    q, k, v = _rows16(q), _rows16(k), _rows16(v)
+    B, Hq, Tq, d = q.shape
+    Hkv, Tk = k.shape[1], k.shape[2]
+    c = torch.empty((B, Hq, Tq, d), device=q.device, dtype=q.dtype)
+    mag = torch.empty((B, Hq, Tq), device=q.device, dtype=q.dtype)
+    M, L, Q2 = (torch.empty((B, Hq, Tq), device=q.device, dtype=torch.float32) for _ in range(3))
+    S = torch.empty((B, Hq, Tq, d), device=q.device, dtype=torch.float32)
+    rc = lib.atma_polar_attention_fwd(
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
+        k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
+        n_keys.data_ptr(), v_null.data_ptr(), null_base.data_ptr(), null_slope_raw.data_ptr(),
+        len_gain_raw.data_ptr(), mag_beta_raw.data_ptr(), c.data_ptr(), mag.data_ptr(),
+        M.data_ptr(), L.data_ptr(), Q2.data_ptr(), S.data_ptr(), B, Hq, Hkv, Tq, Tk, d,
+        _lib.dtype_code(q.dtype), 1 if is_causal else 0, window, 1 if preserve_length else 0, eps,
+        _lib.stream_handle(q.device))
+    _lib.check(rc, "polar_attention_fwd")
+    return [c, mag, M, L, Q2, S]
+
+
+@polar_attention_fwd_train_op.register_fake
+def _(q, k, v, n_keys, v_null, null_base, null_slope_raw, len_gain_raw, mag_beta_raw, eps,
+      is_causal, window, preserve_length):
+    B, Hq, Tq, d = q.shape
+    f = dict(dtype=torch.float32)
+    return [q.new_empty((B, Hq, Tq, d)), q.new_empty((B, Hq, Tq)), q.new_empty((B, Hq, Tq), **f),
+            q.new_empty((B, Hq, Tq), **f), q.new_empty((B, Hq, Tq), **f), q.new_empty((B, Hq, Tq, d), **f)]
+
+
+@torch.library.custom_op("atma_hip::polar_attention_bwd", mutates_args=())
+def polar_attention_bwd_op(q: Tensor, k: Tensor, v: Tensor, gs: Tensor, gL: Tensor, gQ2: Tensor,
+                           M: Tensor, temp: Tensor, n_keys: Tensor, is_causal: bool,
+                           window: int) -> List[Tensor]:
+    """The O(T^2) part of the backward: returns fp32 (dq, dt, dk, dv)."""
+    _need_cuda(q, k, v, gs, gL, gQ2, M, temp, n_keys)
+    lib = _lib.load()
+    q, k, v, gs = _rows16(q), _rows16(k), _rows16(v), _rows16(gs)
+    B, Hq, Tq, d = q.shape
+    Hkv, Tk = k.shape[1], k.shape[2]
+    f = dict(device=q.device, dtype=torch.float32)
+    dq = torch.zeros((B, Hq, Tq, d), **f)   # zeros: with no keys the launch is skipped
+    dt = torch.zeros((B, Hq, Tq), **f)
+    dk = torch.zeros((B, Hkv, Tk, d), **f)
+    dv = torch.zeros((B, Hkv, Tk, d), **f)
+    gL, gQ2, M, temp = (t.to(torch.float32).contiguous() for t in (gL, gQ2, M, temp))
+    rc = lib.atma_polar_attention_bwd(
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
+        k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
+        gs.data_ptr(), gs.stride(0), gs.stride(1), gs.stride(2),
+        gL.data_ptr(), gQ2.data_ptr(), M.data_ptr(), temp.data_ptr(), n_keys.data_ptr(),
+        dq.data_ptr(), dt.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, Hq, Hkv, Tq, Tk, d,
+        _lib.dtype_code(q.dtype), 1 if is_causal else 0, window, _lib.stream_handle(q.device))
+    _lib.check(rc, "polar_attention_bwd")
+    return [dq, dt, dk, dv]
+
+
+@polar_attention_bwd_op.register_fake
+def _(q, k, v, gs, gL, gQ2, M, temp, n_keys, is_causal, window):
+    B, Hq, Tq, d = q.shape
+    Hkv, Tk = k.shape[1], k.shape[2]
+    f = dict(dtype=torch.float32)
+    return [q.new_empty((B, Hq, Tq, d), **f), q.new_empty((B, Hq, Tq), **f),
+            q.new_empty((B, Hkv, Tk, d), **f), q.new_empty((B, Hkv, Tk, d), **f)]
 
 
 # --------------------------------------------------------------------------- Polar packed fwd

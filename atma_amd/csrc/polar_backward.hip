@@ -1,0 +1,401 @@
+// Polar attention backward: the two O(T^2) loops of _polar_backward
+// (kernel/polar_triton.py:861-1155).  The per-query preamble (gs, gL, gQ2 from the saved
+// statistics M, L, Q2, s and the output cotangents) and the parameter-gradient assembly
+// are O(B*H*T*d) and stay on the host side; these kernels take their results.
+//
+// For a valid (query i, key j) pair, with sig = q_i.k_j / sqrt(d), a = sig * temp_i and
+// p = exp(a - M_i) (the saved reference max; 0 for masked pairs):
+//   dLdp = gs_i.v_j + gL_i + 2 gQ2_i p,   da = dLdp * p,   gsig = da * temp_i
+//   dq_i += gsig * k_j / sqrt(d)     dt_i += da * sig
+//   dk_j += gsig * q_i / sqrt(d)     dv_j += p * gs_i
+// Validity is the forward's: key j < min(n_i, Tk) and, with a window, j >= n_i - window.
+//
+// MI355X mapping.  16-wide MFMA tiles (v_mfma_f32_16x16x32_{bf16,f16} for 16-bit inputs,
+// v_mfma_f32_16x16x4f32 for fp32), operands staged in padded row-major LDS tiles:
+//  * dq kernel: a workgroup owns 64 query rows of one head (16 per wave, q and gs as A
+//    fragments in registers) and walks 64-key blocks: S and dP (queries x keys) on MFMA,
+//    the elementwise gradient in registers, dS through a per-wave LDS tile (row-major, so
+//    it is read back as the A operand), then dQ += dS K with K^T fragments taken by
+//    transposing reads of the row-major K tile.
+//  * dk/dv kernel: a workgroup owns 64 keys of one KV head (k and v rows as A fragments)
+//    and walks the G query heads of the group x 64-query blocks: S^T and dP^T on MFMA,
+//    P^T and dS^T through per-wave LDS tiles, dV += P^T gs and dK += dS^T Q with gs / Q
+//    fragments by transposing reads.  GQA gradients are summed over the group in-kernel,
+//    so every dk / dv row is written once (no atomics).
+// Products accumulate in fp32; 16-bit inputs round P and dS to the input dtype for the
+// second products, as the reference does (kernel/polar_triton.py:942,1023-1024).
+#include <type_traits>
+
+#include "common.h"
+
+namespace atma {
+
+struct PolarBwdArgs {
+  const void* q;
+  int64_t q_sb, q_sh, q_st;
+  const void* k;
+  int64_t k_sb, k_sh, k_st;
+  const void* v;
+  int64_t v_sb, v_sh, v_st;
+  const void* gs;
+  int64_t g_sb, g_sh, g_st;
+  const float* gL;      // (B, Hq, Tq)
+  const float* gQ2;     // (B, Hq, Tq)
+  const float* M;       // (B, Hq, Tq) natural-log reference max of the forward
+  const float* temp;    // (Hq, Tq)
+  const float* n_keys;  // (Tq,)
+  float* dq;            // (B, Hq, Tq, D)
+  float* dt;            // (B, Hq, Tq)
+  float* dk;            // (B, Hkv, Tk, D)
+  float* dv;            // (B, Hkv, Tk, D)
+  int B, Hq, Hkv, Tq, Tk;
+  int is_causal, window;
+  float scale;
+};
+
+template <typename T>
+using BwFrag = std::conditional_t<sizeof(T) == 2, u32x4, float>;
+template <typename T>
+constexpr int kBwK = sizeof(T) == 2 ? 32 : 4;  // MFMA k depth
+template <typename T>
+constexpr int kBwPad = sizeof(T) == 2 ? 8 : 4;  // LDS row padding (elements): 16 B
+
+template <typename T>
+__device__ __forceinline__ f32x4 bw_mma(const BwFrag<T>& a, const BwFrag<T>& b, const f32x4& c) {
+  if constexpr (sizeof(T) == 2) return mfma16x16x32<T>(a, b, c);
+  else return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Fragment (A rows or B columns) whose 16 lines are rows r0.. of a row-major tile with
+// the k dimension contiguous: lane l takes line r0 + l % 16 at k = k0 + (8 | 1) (l / 16) ...
+template <typename T>
+__device__ __forceinline__ BwFrag<T> bw_rows(const T* base, int ld, int r0, int k0, int lane) {
+  if constexpr (sizeof(T) == 2)
+    return *(const u32x4*)(base + (r0 + (lane & 15)) * ld + k0 + 8 * (lane >> 4));
+  else
+    return base[(r0 + (lane & 15)) * ld + k0 + (lane >> 4)];
+}
+// B fragment with k along the rows of a row-major tile: lane l takes column n0 + l % 16 at
+// rows k0 + 8 (l / 16) .. + 7 (two transposing reads of 4 rows) or, for fp32, row
+// k0 + l / 16.
+template <typename T>
+__device__ __forceinline__ BwFrag<T> bw_cols(const T* base, int ld, int k0, int n0, int lane) {
+  if constexpr (sizeof(T) == 2) {
+    const int g = lane >> 4, i = lane & 15;
+    const T* p = base + (k0 + 8 * g + (i >> 2)) * ld + n0 + 4 * (i & 3);
+    const u32x2 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 4 * ld);
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  } else {
+    return base[(k0 + (lane >> 4)) * ld + n0 + (lane & 15)];
+  }
+}
+// A fragment of 16 rows straight from global memory (rows past `rows` read as zeros).
+template <typename T>
+__device__ __forceinline__ BwFrag<T> bw_global_rows(const T* base, int64_t st, int r0, int rows, int k0,
+                                                     int lane) {
+  const int r = r0 + (lane & 15);
+  if constexpr (sizeof(T) == 2) {
+    return r < rows ? *(const u32x4*)(base + (int64_t)r * st + k0 + 8 * (lane >> 4)) : u32x4{0, 0, 0, 0};
+  } else {
+    return r < rows ? base[(int64_t)r * st + k0 + (lane >> 4)] : 0.f;
+  }
+}
+// Cooperative copy of rows r0 .. r0 + 63 of a row-major (rows, D) source with row stride st
+// into a padded LDS tile (rows past `rows` become zeros), 16 bytes per thread and step.
+template <typename T, int D>
+__device__ __forceinline__ void bw_tile(T* dst, const T* src, int64_t st, int r0, int rows, int tid) {
+  constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
+  constexpr int CPR = D / EPC, LD = D + kBwPad<T>;
+#pragma unroll
+  for (int c = tid; c < 64 * CPR; c += 256) {
+    const int r = c / CPR, e = (c % CPR) * EPC;
+    const int gr = r0 + r;
+    u32x4 x = {0, 0, 0, 0};
+    if (gr < rows) x = *(const u32x4*)(src + (int64_t)gr * st + e);
+    *(u32x4*)(dst + r * LD + e) = x;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ T bw_round(float x) {
+  return (T)x;
+}
+
+// ---------------------------------------------------------------------------------------
+// dq, dt: workgroup = (64-row query tile, b * Hq + hq)
+template <typename T, int D>
+__global__ void __launch_bounds__(256) polar_bwd_dq_kernel(PolarBwdArgs a) {
+  constexpr int BM = 64, BN = 64, KD = kBwK<T>, LD = D + kBwPad<T>, SLD = BN + kBwPad<T>;
+  __shared__ __attribute__((aligned(16))) T Ks[BN * LD];
+  __shared__ __attribute__((aligned(16))) T Vs[BN * LD];
+  __shared__ __attribute__((aligned(16))) T Sd[4][16 * SLD];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = a.Hq / a.Hkv;
+  const int bh = blockIdx.y, b = bh / a.Hq, hq = bh % a.Hq, hk = hq / G;
+  const int q0 = blockIdx.x * BM, r0 = q0 + 16 * wave;
+  const T* qp = (const T*)a.q + b * a.q_sb + hq * a.q_sh;
+  const T* gp = (const T*)a.gs + b * a.g_sb + hq * a.g_sh;
+  const T* kp = (const T*)a.k + b * a.k_sb + hk * a.k_sh;
+  const T* vp = (const T*)a.v + b * a.v_sb + hk * a.v_sh;
+
+  BwFrag<T> qf[D / KD], gf[D / KD];
+#pragma unroll
+  for (int s = 0; s < D / KD; ++s) {
+    qf[s] = bw_global_rows<T>(qp, a.q_st, r0, a.Tq, KD * s, lane);
+    gf[s] = bw_global_rows<T>(gp, a.g_st, r0, a.Tq, KD * s, lane);
+  }
+  // per-row values for the C rows of this lane: r0 + 4 (lane / 16) + j
+  float m2[4], c1[4], gl[4], gq2[4], nr[4], tp[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = r0 + 4 * (lane >> 4) + j;
+    const bool ok = row < a.Tq;
+    const int64_t i = (int64_t)bh * a.Tq + row;
+    tp[j] = ok ? a.temp[(int64_t)hq * a.Tq + row] : 1.f;
+    m2[j] = ok ? a.M[i] * kLog2e : 0.f;
+    c1[j] = a.scale * tp[j] * kLog2e;
+    gl[j] = ok ? a.gL[i] : 0.f;
+    gq2[j] = ok ? a.gQ2[i] : 0.f;
+    nr[j] = ok ? a.n_keys[row] : 0.f;  // no valid key for rows past Tq
+  }
+
+  f32x4 dq[D / 16];
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t) dq[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float dt[4] = {0.f, 0.f, 0.f, 0.f};
+
+  const int hi = a.is_causal ? min(q0 + BM, a.Tk) : a.Tk;
+  const int lo = a.window > 0 ? (max(q0 - a.window, 0) / BN) * BN : 0;
+  T* sd = Sd[wave];
+  for (int k0 = lo; k0 < hi; k0 += BN) {
+    __syncthreads();  // every wave is done with the previous block
+    bw_tile<T, D>(Ks, kp, a.k_st, k0, a.Tk, tid);
+    bw_tile<T, D>(Vs, vp, a.v_st, k0, a.Tk, tid);
+    __syncthreads();
+    // S = Q K^T and dP = gs V^T for 4 key tiles of 16
+    f32x4 s[4], p[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      s[t] = p[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < D / KD; ++ks) {
+        s[t] = bw_mma<T>(qf[ks], bw_rows<T>(Ks, LD, 16 * t, KD * ks, lane), s[t]);
+        p[t] = bw_mma<T>(gf[ks], bw_rows<T>(Vs, LD, 16 * t, KD * ks, lane), p[t]);
+      }
+    }
+    // elementwise gradient; C element (row 4 (lane / 16) + j, key k0 + 16 t + lane % 16)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int key = k0 + 16 * t + (lane & 15);
+      const float kf = (float)key;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool valid = key < a.Tk && kf < nr[j] && (a.window <= 0 || kf >= nr[j] - (float)a.window);
+        const float pr = valid ? __builtin_amdgcn_exp2f(s[t][j] * c1[j] - m2[j]) : 0.f;
+        const float da = valid ? (p[t][j] + gl[j] + 2.f * gq2[j] * pr) * pr : 0.f;
+        dt[j] += da * (s[t][j] * a.scale);
+        sd[(4 * (lane >> 4) + j) * SLD + 16 * t + (lane & 15)] = bw_round<T>(da * tp[j]);
+      }
+    }
+    wave_sync();
+    // dQ += dS K: A = dS rows (k = keys), B = K with k along its rows
+#pragma unroll
+    for (int nt = 0; nt < D / 16; ++nt)
+#pragma unroll
+      for (int ks = 0; ks < BN / KD; ++ks)
+        dq[nt] = bw_mma<T>(bw_rows<T>(sd, SLD, 0, KD * ks, lane), bw_cols<T>(Ks, LD, KD * ks, 16 * nt, lane),
+                           dq[nt]);
+  }
+
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = r0 + 4 * (lane >> 4) + j;
+    float x = dt[j];
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) x += __shfl_xor(x, m, 64);  // the 16 key columns of the row
+    if (row < a.Tq) {
+      float* out = a.dq + ((int64_t)bh * a.Tq + row) * D + (lane & 15);
+#pragma unroll
+      for (int nt = 0; nt < D / 16; ++nt) out[16 * nt] = dq[nt][j] * a.scale;
+      if ((lane & 15) == 0) a.dt[(int64_t)bh * a.Tq + row] = x;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// dk, dv: workgroup = (64-key tile, b * Hkv + hk); loops over the group's query heads
+template <typename T, int D>
+__global__ void __launch_bounds__(256) polar_bwd_dkdv_kernel(PolarBwdArgs a) {
+  constexpr int BK = 64, BQ = 64, KD = kBwK<T>, LD = D + kBwPad<T>, SLD = BQ + kBwPad<T>;
+  __shared__ __attribute__((aligned(16))) T Qs[BQ * LD];
+  __shared__ __attribute__((aligned(16))) T Gs[BQ * LD];
+  __shared__ __attribute__((aligned(16))) T Pt[4][16 * SLD];
+  __shared__ __attribute__((aligned(16))) T Dt[4][16 * SLD];
+  __shared__ float s_m2[BQ], s_c1[BQ], s_gl[BQ], s_gq2[BQ], s_nr[BQ], s_tp[BQ];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = a.Hq / a.Hkv;
+  const int bhk = blockIdx.y, b = bhk / a.Hkv, hk = bhk % a.Hkv;
+  const int k0 = blockIdx.x * BK, kr0 = k0 + 16 * wave;
+  const T* kp = (const T*)a.k + b * a.k_sb + hk * a.k_sh;
+  const T* vp = (const T*)a.v + b * a.v_sb + hk * a.v_sh;
+
+  BwFrag<T> kf[D / KD], vf[D / KD];
+#pragma unroll
+  for (int s = 0; s < D / KD; ++s) {
+    kf[s] = bw_global_rows<T>(kp, a.k_st, kr0, a.Tk, KD * s, lane);
+    vf[s] = bw_global_rows<T>(vp, a.v_st, kr0, a.Tk, KD * s, lane);
+  }
+  f32x4 dk[D / 16], dv[D / 16];
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t) dk[t] = dv[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int lo = a.is_causal ? (k0 / BQ) * BQ : 0;
+  const int hi = a.window > 0 ? min(k0 + BK + a.window, a.Tq) : a.Tq;
+  T* pt = Pt[wave];
+  T* dst = Dt[wave];
+  for (int g = 0; g < G; ++g) {
+    const int hq = hk * G + g;
+    const int bh = b * a.Hq + hq;
+    const T* qp = (const T*)a.q + b * a.q_sb + hq * a.q_sh;
+    const T* gp = (const T*)a.gs + b * a.g_sb + hq * a.g_sh;
+    for (int q0 = lo; q0 < hi; q0 += BQ) {
+      __syncthreads();  // every wave is done with the previous block
+      bw_tile<T, D>(Qs, qp, a.q_st, q0, a.Tq, tid);
+      bw_tile<T, D>(Gs, gp, a.g_st, q0, a.Tq, tid);
+      if (tid < BQ) {
+        const int row = q0 + tid;
+        const bool ok = row < a.Tq;
+        const int64_t i = (int64_t)bh * a.Tq + row;
+        const float tpv = ok ? a.temp[(int64_t)hq * a.Tq + row] : 1.f;
+        s_tp[tid] = tpv;
+        s_c1[tid] = a.scale * tpv * kLog2e;
+        s_m2[tid] = ok ? a.M[i] * kLog2e : 0.f;
+        s_gl[tid] = ok ? a.gL[i] : 0.f;
+        s_gq2[tid] = ok ? a.gQ2[i] : 0.f;
+        s_nr[tid] = ok ? a.n_keys[row] : 0.f;
+      }
+      __syncthreads();
+      // S^T = K Q^T and dP^T = V gs^T for 4 query tiles of 16
+      f32x4 s[4], p[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        s[t] = p[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < D / KD; ++ks) {
+          s[t] = bw_mma<T>(kf[ks], bw_rows<T>(Qs, LD, 16 * t, KD * ks, lane), s[t]);
+          p[t] = bw_mma<T>(vf[ks], bw_rows<T>(Gs, LD, 16 * t, KD * ks, lane), p[t]);
+        }
+      }
+      // C element (key kr0 + 4 (lane / 16) + j, query q0 + 16 t + lane % 16)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int qi = 16 * t + (lane & 15);
+        const float nrq = s_nr[qi], c1 = s_c1[qi], m2 = s_m2[qi], glq = s_gl[qi], gq2 = s_gq2[qi];
+        const float tpq = s_tp[qi];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = kr0 + 4 * (lane >> 4) + j;
+          const float kf_ = (float)key;
+          const bool valid = key < a.Tk && kf_ < nrq && (a.window <= 0 || kf_ >= nrq - (float)a.window);
+          const float pr = valid ? __builtin_amdgcn_exp2f(s[t][j] * c1 - m2) : 0.f;
+          const float da = valid ? (p[t][j] + glq + 2.f * gq2 * pr) * pr : 0.f;
+          const int e = (4 * (lane >> 4) + j) * SLD + qi;
+          pt[e] = bw_round<T>(pr);
+          dst[e] = bw_round<T>(da * tpq);
+        }
+      }
+      wave_sync();
+      // dV += P^T gs, dK += dS^T Q: A = the per-wave tiles (k = queries), B = gs / Q
+#pragma unroll
+      for (int nt = 0; nt < D / 16; ++nt)
+#pragma unroll
+        for (int ks = 0; ks < BQ / KD; ++ks) {
+          dv[nt] = bw_mma<T>(bw_rows<T>(pt, SLD, 0, KD * ks, lane), bw_cols<T>(Gs, LD, KD * ks, 16 * nt, lane),
+                             dv[nt]);
+          dk[nt] = bw_mma<T>(bw_rows<T>(dst, SLD, 0, KD * ks, lane), bw_cols<T>(Qs, LD, KD * ks, 16 * nt, lane),
+                             dk[nt]);
+        }
+    }
+  }
+
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = kr0 + 4 * (lane >> 4) + j;
+    if (row < a.Tk) {
+      const int64_t base = ((int64_t)bhk * a.Tk + row) * D + (lane & 15);
+#pragma unroll
+      for (int nt = 0; nt < D / 16; ++nt) {
+        a.dk[base + 16 * nt] = dk[nt][j] * a.scale;
+        a.dv[base + 16 * nt] = dv[nt][j];
+      }
+    }
+  }
+}
+
+template <typename T, int D>
+static int launch_bwd(const PolarBwdArgs& a, hipStream_t s) {
+  polar_bwd_dq_kernel<T, D><<<dim3((unsigned)((a.Tq + 63) / 64), (unsigned)(a.B * a.Hq)), dim3(256), 0, s>>>(a);
+  int rc = check_launch("polar_attention_bwd(dq)");
+  if (rc) return rc;
+  polar_bwd_dkdv_kernel<T, D><<<dim3((unsigned)((a.Tk + 63) / 64), (unsigned)(a.B * a.Hkv)), dim3(256), 0, s>>>(a);
+  return check_launch("polar_attention_bwd(dkdv)");
+}
+
+}  // namespace atma
+
+extern "C" int atma_polar_attention_bwd(
+    const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb, int64_t k_sh,
+    int64_t k_st, const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, const void* gs,
+    int64_t g_sb, int64_t g_sh, int64_t g_st, const float* gL, const float* gQ2, const float* M,
+    const float* temp, const float* n_keys, float* dq, float* dt, float* dk, float* dv, int64_t B,
+    int64_t Hq, int64_t Hkv, int64_t Tq, int64_t Tk, int64_t d, int dtype, int is_causal,
+    int64_t window, void* stream) {
+  using namespace atma;
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || Tq < 0 || Tk < 0)
+    return set_error(ATMA_ERR_INVALID, "polar_attention_bwd: bad sizes");
+  if (Hq % Hkv) return set_error(ATMA_ERR_INVALID, "polar_attention_bwd: Hq %% Hkv != 0");
+  if (is_causal && Tq != Tk)
+    return set_error(ATMA_ERR_INVALID, "polar_attention_bwd: is_causal=True requires Tq == Tk");
+  if (d != 64 && d != 128)
+    return set_error(ATMA_ERR_UNSUPPORTED, "polar_attention_bwd: head_dim %lld (supported: 64, 128)",
+                     (long long)d);
+  if (Tq > (1 << 30) || Tk > (1 << 30) || B * Hq > 65535 || B * Hkv > 65535)
+    return set_error(ATMA_ERR_INVALID, "polar_attention_bwd: sizes too large");
+  if (B == 0 || Tq == 0) return ATMA_OK;
+  const int es = dtype_size(dtype);
+  if (!es) return set_error(ATMA_ERR_INVALID, "polar_attention_bwd: unknown dtype %d", dtype);
+  if (!q || !k || !v || !gs || !gL || !gQ2 || !M || !temp || !n_keys || !dq || !dt || !dk || !dv)
+    return set_error(ATMA_ERR_INVALID, "polar_attention_bwd: null pointer");
+  auto al16 = [&](const void* p, int64_t s1, int64_t s2, int64_t s3) {
+    return ((uintptr_t)p % 16 == 0) && ((s1 * es) % 16 == 0) && ((s2 * es) % 16 == 0) &&
+           ((s3 * es) % 16 == 0);
+  };
+  if (!al16(q, q_sb, q_sh, q_st) || !al16(k, k_sb, k_sh, k_st) || !al16(v, v_sb, v_sh, v_st) ||
+      !al16(gs, g_sb, g_sh, g_st))
+    return set_error(ATMA_ERR_INVALID, "polar_attention_bwd: tensors must be 16-byte aligned rows");
+  if (Tk == 0) {
+    // no keys: every gradient of the O(T^2) part is zero (the callers' buffers are zeroed)
+    return ATMA_OK;
+  }
+  PolarBwdArgs a{};
+  a.q = q; a.q_sb = q_sb; a.q_sh = q_sh; a.q_st = q_st;
+  a.k = k; a.k_sb = k_sb; a.k_sh = k_sh; a.k_st = k_st;
+  a.v = v; a.v_sb = v_sb; a.v_sh = v_sh; a.v_st = v_st;
+  a.gs = gs; a.g_sb = g_sb; a.g_sh = g_sh; a.g_st = g_st;
+  a.gL = gL; a.gQ2 = gQ2; a.M = M; a.temp = temp; a.n_keys = n_keys;
+  a.dq = dq; a.dt = dt; a.dk = dk; a.dv = dv;
+  a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.Tq = (int)Tq; a.Tk = (int)Tk;
+  a.is_causal = is_causal ? 1 : 0;
+  a.window = window > 0 ? (int)window : 0;
+  a.scale = 1.f / sqrtf((float)d);
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case ATMA_BF16: return d == 128 ? launch_bwd<bf16, 128>(a, s) : launch_bwd<bf16, 64>(a, s);
+    case ATMA_F16: return d == 128 ? launch_bwd<f16, 128>(a, s) : launch_bwd<f16, 64>(a, s);
+    default: return d == 128 ? launch_bwd<float, 128>(a, s) : launch_bwd<float, 64>(a, s);
+  }
+}

@@ -59,6 +59,7 @@ struct PolarFwdArgs {
   float eps;
   int n_qtiles;
   int xcd_remap;
+  int preserve_length;  // temp / null from the raw count even under a window
   // output strides (elements) of c (b, head, query) and of mag; the saved statistics
   // keep the (B, Hq, Tq) layout
   int64_t c_sb, c_sh, c_st, m_sb, m_sh, m_st;
@@ -153,7 +154,7 @@ __global__ void __launch_bounds__(256, 2) polar_fwd_kernel(PolarFwdArgs args) {
   const bool q_ok = qi < args.Tq;
   const float n_raw = q_ok ? args.n_keys[qi] : 0.f;
   float n_cal = n_raw;
-  if (args.window > 0) n_cal = fminf(n_cal, (float)args.window);
+  if (args.window > 0 && !args.preserve_length) n_cal = fminf(n_cal, (float)args.window);
   n_cal = fmaxf(n_cal, 1.f);
   const float spg = softplus(args.len_gain_raw[hq]);
   const float sps = softplus(args.null_slope_raw[hq]);
@@ -619,7 +620,7 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
   const bool q_ok = qi < Tq;
   const float n_raw = q_ok ? (packed ? (float)(qi + 1) : args.n_keys[qi]) : 0.f;
   float n_cal = n_raw;
-  if (args.window > 0) n_cal = fminf(n_cal, (float)args.window);
+  if (args.window > 0 && !args.preserve_length) n_cal = fminf(n_cal, (float)args.window);
   n_cal = fmaxf(n_cal, 1.f);
   const float spg = softplus(args.len_gain_raw[hq]);
   const float sps = softplus(args.null_slope_raw[hq]);
@@ -940,7 +941,8 @@ extern "C" int atma_polar_attention_fwd(
     const float* n_keys, const float* v_null, const float* null_base, const float* null_slope_raw,
     const float* len_gain_raw, const float* mag_beta_raw, void* c, void* mag, float* stat_m,
     float* stat_l, float* stat_q2, float* stat_s, int64_t B, int64_t Hq, int64_t Hkv, int64_t Tq,
-    int64_t Tk, int64_t d, int dtype, int is_causal, int64_t window, float eps, void* stream) {
+    int64_t Tk, int64_t d, int dtype, int is_causal, int64_t window, int preserve_length, float eps,
+    void* stream) {
   using namespace atma;
   if (B < 0 || Hq <= 0 || Hkv <= 0 || Tq < 0 || Tk < 0)
     return set_error(ATMA_ERR_INVALID, "polar_attention_fwd: bad sizes");
@@ -979,6 +981,7 @@ extern "C" int atma_polar_attention_fwd(
   a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.Tq = (int)Tq; a.Tk = (int)Tk;
   a.is_causal = is_causal ? 1 : 0;
   a.window = window > 0 ? (int)window : 0;
+  a.preserve_length = preserve_length ? 1 : 0;
   a.eps = eps;
   a.n_qtiles = (int)((Tq + 127) / 128);
   a.c_st = d; a.c_sh = Tq * d; a.c_sb = Hq * Tq * d;  // c, mag contiguous (B, Hq, Tq[, d])

@@ -76,7 +76,8 @@ int atma_store_kvcache(const void* key, int64_t key_stride, const void* value,
  * unnormalised direction.
  * is_causal requires Tq == Tk and bounds each query tile's key loop at the tile's
  * last row (kernel/polar_triton.py:110-113,522-526).  window <= 0 disables the
- * sliding window.  d must be 64 or 128.
+ * sliding window; with preserve_length != 0, temp / null use the raw count even under
+ * a window (kernel/polar_triton.py:93-96).  d must be 64 or 128.
  */
 int atma_polar_attention_fwd(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                              const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
@@ -86,8 +87,8 @@ int atma_polar_attention_fwd(const void* q, int64_t q_sb, int64_t q_sh, int64_t 
                              const float* mag_beta_raw, void* c, void* mag, float* stat_m,
                              float* stat_l, float* stat_q2, float* stat_s, int64_t B,
                              int64_t Hq, int64_t Hkv, int64_t Tq, int64_t Tk, int64_t d,
-                             int dtype, int is_causal, int64_t window, float eps,
-                             void* stream);
+                             int dtype, int is_causal, int64_t window, int preserve_length,
+                             float eps, void* stream);
 
 /*
  * Grouped fresh-prefill Polar attention over packed ragged requests.  Replaces
@@ -114,6 +115,27 @@ int atma_polar_attention_packed_fwd(const void* q, int64_t q_st, int64_t q_sh, c
                                     int64_t c_sh, void* mag, int64_t m_st, int64_t m_sh,
                                     int64_t total_tokens, int64_t Hq, int64_t Hkv, int64_t d,
                                     int dtype, int64_t window, float eps, void* stream);
+
+/*
+ * Polar attention backward: the two O(T^2) loops of _polar_backward
+ * (kernel/polar_triton.py:861-1155; _polar_bwd_dq_kernel :870-947,
+ * _polar_bwd_dkdv_kernel :951-1030).  q, gs: (B, Hq, Tq, d) and k, v: (B, Hkv, Tk, d)
+ * in dtype with strides (x_sb, x_sh, x_st, 1) (GQA resolved in-kernel; dk / dv are
+ * summed over the query heads of a group); gL, gQ2, M: (B, Hq, Tq) fp32 contiguous (the
+ * preamble's per-query cotangents and the forward's natural-log reference max);
+ * temp: (Hq, Tq) fp32; n_keys: (Tq,) raw counts (the mask).  Outputs, fp32 contiguous,
+ * every element written: dq (B, Hq, Tq, d), dt (B, Hq, Tq) (= sum_j da * sig, the real
+ * keys' share of dL/dtemp), dk, dv (B, Hkv, Tk, d).  d = 64 or 128.
+ */
+int atma_polar_attention_bwd(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                             const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                             const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                             const void* gs, int64_t g_sb, int64_t g_sh, int64_t g_st,
+                             const float* gL, const float* gQ2, const float* M,
+                             const float* temp, const float* n_keys, float* dq, float* dt,
+                             float* dk, float* dv, int64_t B, int64_t Hq, int64_t Hkv,
+                             int64_t Tq, int64_t Tk, int64_t d, int dtype, int is_causal,
+                             int64_t window, void* stream);
 
 /*
  * Workspace bytes atma_polar_attention_decode needs for this launch shape.

@@ -107,10 +107,13 @@ def _count_for_calibration(n_keys, window):
     return torch.minimum(n_keys, torch.full_like(n_keys, float(window)))
 
 
-def polar_dense(q, k, v, n_keys, *, params, eps=1e-6, window=None):
+def polar_dense(q, k, v, n_keys, *, params, eps=1e-6, window=None, preserve_length=False):
     """Materialised Polar attention for (B,Hq,Tq,d) q against (B,Hkv,Tk,d) k/v with
     an arbitrary per-query valid count ``n_keys`` (Tq,).  This is the CPU route of
-    ``AtmaAttention._polar`` (``inference/models/atma.py:236-244``) -> ``polar_reduce``."""
+    ``AtmaAttention._polar`` (``inference/models/atma.py:236-244``) -> ``polar_reduce``.
+    ``preserve_length`` keeps temp/null on the raw count under a window
+    (``kernel/polar_triton.py:1049-1053``).  Differentiable (autograd), which the
+    backward tests use in fp64."""
     B, H, Tq, d = q.shape
     wd = _work_dtype(q.dtype)
     kx, vx = _expand_kv(k, H), _expand_kv(v, H)
@@ -118,12 +121,12 @@ def polar_dense(q, k, v, n_keys, *, params, eps=1e-6, window=None):
     sigma = (q.to(wd) @ kx.to(wd).transpose(-1, -2)) / math.sqrt(d)
     ok = _valid_mask(n_keys.to(q.device), Tk, window, q.device)
     sigma = sigma.masked_fill(~ok[None, None], float("-inf"))
-    return polar_reduce(sigma, vx.to(q.dtype), _count_for_calibration(n_keys, window), eps=eps,
-                        **{n: params[n] for n in _PARAM_NAMES})
+    cal = _count_for_calibration(n_keys, None if preserve_length else window)
+    return polar_reduce(sigma, vx.to(q.dtype), cal, eps=eps, **{n: params[n] for n in _PARAM_NAMES})
 
 
 def polar_online(q, k, v, n_keys, *, params, k_block=512, eps=1e-6, window=None,
-                 q2_floor=1e-30, return_stats=False):
+                 q2_floor=1e-30, return_stats=False, preserve_length=False):
     """Streaming Polar forward: the formulation every GPU kernel implements.
 
     Follows ``model/blocks.py:181-250`` (running max M, L = sum p, Q2 = sum p^2
@@ -133,6 +136,9 @@ def polar_online(q, k, v, n_keys, *, params, k_block=512, eps=1e-6, window=None,
     sentinel -1e38 and contribute p = 0.
 
     q: (B,Hq,Tq,d); k,v: (B,Hkv,Tk,d) (GQA expanded here); n_keys: (Tq,).
+    ``preserve_length`` keeps temp/null on the raw count under a window.  Differentiable
+    (autograd): this streaming form is the oracle the backward is checked against, as the
+    reference checks its backward against ``model/blocks.py:polar_attention_online``.
     Returns c, mag in q's dtype (and, with ``return_stats``, fp M, L, Q2, s)."""
     B, H, Tq, d = q.shape
     wd = _work_dtype(q.dtype)
@@ -140,7 +146,7 @@ def polar_online(q, k, v, n_keys, *, params, k_block=512, eps=1e-6, window=None,
     kx, vx = _expand_kv(k, H).to(wd), _expand_kv(v, H).to(wd)
     Tk = kx.shape[2]
     n_keys = n_keys.to(device=q.device, dtype=wd)
-    temp, null = polar_temp_null(_count_for_calibration(n_keys, window),
+    temp, null = polar_temp_null(_count_for_calibration(n_keys, None if preserve_length else window),
                                  params["len_gain_raw"].to(wd), params["null_base"].to(wd),
                                  params["null_slope_raw"].to(wd))
     sentinel = -1e38

@@ -39,12 +39,12 @@ def test_validation_rejects_without_launch(lib):
     # is_causal with Tq != Tk
     rc = lib.atma_polar_attention_fwd(null, 0, 0, 0, null, 0, 0, 0, null, 0, 0, 0, null, null, null,
                                       null, null, null, null, null, null, null, null, null,
-                                      1, 8, 2, 16, 32, 128, 1, 1, 0, 1e-6, null)
+                                      1, 8, 2, 16, 32, 128, 1, 1, 0, 0, 1e-6, null)
     assert rc == 1 and b"Tq == Tk" in lib.atma_last_error()
     # unsupported head dim
     rc = lib.atma_polar_attention_fwd(null, 0, 0, 0, null, 0, 0, 0, null, 0, 0, 0, null, null, null,
                                       null, null, null, null, null, null, null, null, null,
-                                      1, 8, 2, 16, 16, 96, 1, 0, 0, 1e-6, null)
+                                      1, 8, 2, 16, 16, 96, 1, 0, 0, 0, 1e-6, null)
     assert rc == 2
     # GQA group not dividing
     rc = lib.atma_polar_attention_decode(null, 0, 0, null, null, 4, 256, 3, null, 0, 2, null, null,
@@ -87,6 +87,13 @@ def test_validation_rejects_without_launch(lib):
                                               1, 8, 17, 0, 1, null) == 1
     assert lib.atma_causal_conv1d_decode_step(null, 0, null, 0, 0, null, null, 0, 0, 0, 1, null, 0,
                                               0, 8, 4, 0, 1, null) == 0
+    # Polar backward: causal needs Tq == Tk; head dim 96 unsupported; grouping; empty is a no-op
+    bwd0 = [null, 0, 0, 0] * 4 + [null] * 9
+    assert lib.atma_polar_attention_bwd(*bwd0, 1, 8, 2, 16, 32, 128, 1, 1, 0, null) == 1
+    assert b"Tq == Tk" in lib.atma_last_error()
+    assert lib.atma_polar_attention_bwd(*bwd0, 1, 8, 2, 16, 16, 96, 1, 1, 0, null) == 2
+    assert lib.atma_polar_attention_bwd(*bwd0, 1, 8, 3, 16, 16, 128, 1, 1, 0, null) == 1
+    assert lib.atma_polar_attention_bwd(*bwd0, 1, 8, 2, 0, 0, 128, 1, 1, 0, null) == 0
     # store_kvcache: unknown dtype
     assert lib.atma_store_kvcache(null, 0, null, 0, null, null, null, 1, 256, 8, 9, null) == 1
     # zero-size requests are no-ops

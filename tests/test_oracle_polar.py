@@ -162,6 +162,48 @@ def test_window_equals_recompute_on_band():
         assert (mw[:, :, i:i + 1] - mb).abs().max() < 1e-10
 
 
+def test_preserve_length_calibrates_on_the_raw_count():
+    """Under a window, preserve_length keeps the band mask but feeds temp/null the raw
+    count n_i instead of min(n_i, W) (kernel/polar_triton.py:1049-1053)."""
+    B, H, T, d, W = 1, 2, 30, 8, 7
+    q, k, v = _qkv(B, H, H, T, d, seed=21)
+    p = _p64(H, d, seed=22)
+    n = torch.arange(1, T + 1, dtype=torch.float64)
+    cp, mp = P.polar_dense(q, k, v, n, params=p, window=W, preserve_length=True)
+    cw, mw = P.polar_dense(q, k, v, n, params=p, window=W)
+    co, mo = P.polar_online(q, k, v, n, params=p, window=W, preserve_length=True, k_block=8)
+    assert (cp - co).abs().max() < 1e-12 and (mp - mo).abs().max() < 1e-12
+    assert (cp[:, :, :W] - cw[:, :, :W]).abs().max() < 1e-12       # n <= W: identical
+    assert (mp[:, :, W:] - mw[:, :, W:]).abs().min() > 0           # n > W: the count matters
+    for i in (0, 6, 7, 19, 29):
+        lo = max(0, i + 1 - W)
+        sig = torch.full((B, H, 1, T), float("-inf"), dtype=torch.float64)
+        sig[..., lo:i + 1] = q[:, :, i:i + 1] @ k[:, :, lo:i + 1].transpose(-1, -2) / math.sqrt(d)
+        cr, mr = P.polar_reduce(sig, v, torch.tensor([float(i + 1)], dtype=torch.float64), **p)
+        assert (cp[:, :, i:i + 1] - cr).abs().max() < 1e-12 and (mp[:, :, i:i + 1] - mr).abs().max() < 1e-12
+
+
+@pytest.mark.parametrize("form", ["dense", "online"])
+@pytest.mark.parametrize("window,preserve", [(None, False), (3, False), (3, True)])
+def test_autograd_matches_finite_differences(form, window, preserve):
+    """The backward tests differentiate the streaming oracle in fp64; its autograd graph
+    (the masking, the running-max shifts, the sink fold, the clamps) and the materialised
+    form's agree with central differences for every input and parameter."""
+    B, Hq, Hkv, T, d = 1, 2, 1, 6, 4
+    q, k, v = (t.clone().requires_grad_() for t in _qkv(B, Hq, Hkv, T, d, seed=23))
+    p = {a: b.clone().requires_grad_() for a, b in _p64(Hq, d, seed=24).items()}
+    n = torch.arange(1, T + 1, dtype=torch.float64)
+    names = list(p)
+
+    def f(q, k, v, *ps):
+        kw = dict(params=dict(zip(names, ps)), window=window, preserve_length=preserve)
+        if form == "online":
+            return P.polar_online(q, k, v, n, k_block=4, **kw)
+        return P.polar_dense(q, k, v, n, **kw)
+
+    assert torch.autograd.gradcheck(f, (q, k, v, *p.values()), eps=1e-6, atol=1e-7, rtol=1e-5)
+
+
 def test_gqa_equals_expanded_and_online_equals_dense():
     B, Hq, Hkv, T, d = 2, 8, 2, 23, 16
     q, k, v = _qkv(B, Hq, Hkv, T, d, seed=11)
