@@ -51,7 +51,8 @@ SIGNATURES = {
     "atma_chunk_gated_delta_rule": (_i32, [
         _p, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _i64, _i64,
         _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _f32, _i32, _i32, _f32, _f32,
-        _i64, _p, _sz, _p]),
+        _i64, _p, _sz, _p, _i32, _p]),
+    "atma_wait_start_flag": (_i32, [_p, _i32, _i64, _p]),
 }
 
 _lock = threading.Lock()

@@ -280,10 +280,11 @@ def _(zg, zb, g_bias, b_bias, decay_as_prob):
 
 
 # --------------------------------------------------------------------------- chunked gated delta
-@torch.library.custom_op("atma_hip::chunk_gated_delta_rule", mutates_args=())
+@torch.library.custom_op("atma_hip::chunk_gated_delta_rule", mutates_args=("start_flag",))
 def chunk_gated_delta_rule_op(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,
                               initial_state: Optional[Tensor], scale: float, use_qk_l2norm: bool,
-                              want_final: bool, gate_logits: bool = False, g_bias: float = 0.0,
+                              want_final: bool, start_flag: Optional[Tensor], start_epoch: int,
+                              gate_logits: bool = False, g_bias: float = 0.0,
                               b_bias: float = 0.0) -> List[Tensor]:
     _need_cuda(q, k, v, g, beta, initial_state)
     lib = _lib.load()
@@ -303,18 +304,33 @@ def chunk_gated_delta_rule_op(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: 
         g.data_ptr(), beta.data_ptr(), _lib.ptr(initial_state), _lib.ptr(final), o.data_ptr(),
         B, T, H, k.shape[2], dk, dv, _lib.dtype_code(q.dtype), scale, 1 if use_qk_l2norm else 0,
         1 if gate_logits else 0, g_bias, b_bias, chunk,
-        ws.data_ptr(), ws.numel() * 4, _lib.stream_handle(q.device))
+        ws.data_ptr(), ws.numel() * 4, _lib.ptr(start_flag), start_epoch, _lib.stream_handle(q.device))
     _lib.check(rc, "chunk_gated_delta_rule")
     return [o, final] if want_final else [o]
 
 
 @chunk_gated_delta_rule_op.register_fake
-def _(q, k, v, g, beta, initial_state, scale, use_qk_l2norm, want_final, gate_logits=False,
-      g_bias=0.0, b_bias=0.0):
+def _(q, k, v, g, beta, initial_state, scale, use_qk_l2norm, want_final, start_flag, start_epoch,
+      gate_logits=False, g_bias=0.0, b_bias=0.0):
     B, T, H, dk = q.shape
     dv = v.shape[3]
     o = q.new_empty((B, T, H, dv))
     return [o, q.new_empty((B, H, dk, dv), dtype=torch.float32)] if want_final else [o]
+
+
+@torch.library.custom_op("atma_hip::wait_start_flag", mutates_args=("flag",))
+def wait_start_flag_op(flag: Tensor, epoch: int, timeout_us: int) -> None:
+    _need_cuda(flag)
+    if flag.dtype != torch.int32 or flag.numel() < 1:
+        raise ValueError("wait_start_flag: flag must be an int32 device tensor")
+    rc = _lib.load().atma_wait_start_flag(flag.data_ptr(), epoch, timeout_us,
+                                          _lib.stream_handle(flag.device))
+    _lib.check(rc, "wait_start_flag")
+
+
+@wait_start_flag_op.register_fake
+def _(flag, epoch, timeout_us):
+    return None
 
 
 # --------------------------------------------------------------------------- paged KV write

@@ -27,7 +27,18 @@ struct GdnArgs {
   int gate_logits;  // g, beta hold raw logits: the activations below are applied on load
   float g_bias, b_bias;
   void* ws;
+  int* start_flag;  // optional: the scan's first workgroup stores start_epoch here on entry
+  int start_epoch;
 };
+
+// Start signal of the recurrence kernel.  The scan is latency-bound and needs a whole CU
+// per workgroup (its LDS), so a long prefill overlaps it with Polar attention on another
+// stream only if the scan's workgroups are resident before Polar's fill the GPU: the
+// caller orders the two launches with atma_wait_start_flag on Polar's stream.
+__device__ __forceinline__ void gdn_signal_start(const GdnArgs& a) {
+  if (a.start_flag && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
+    __hip_atomic_store(a.start_flag, a.start_epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // The memory branch's gate activations (TitansMemory, model/blocks.py:426-490), shared by
 // the stand-alone gate kernel and the prefill's fused load so both give the same bits:

@@ -225,6 +225,7 @@ __global__ void __launch_bounds__(256) gdn_scan_kernel(GdnArgs a) {
   __shared__ float Wl[C * P], Ql[C * P], Kl[C * P];
   __shared__ float Ss[D * (VS + 1)], Ul[C * (VS + 1)];
   __shared__ float U0l[C * VS], R0l[C * VS];
+  gdn_signal_start(a);
 
   const int tid = threadIdx.x;
   const int bh = blockIdx.x, v0 = blockIdx.y * VS;
@@ -341,7 +342,7 @@ extern "C" int atma_chunk_gated_delta_rule(
     const float* g, const float* beta, const float* initial_state, float* final_state, void* o,
     int64_t B, int64_t T, int64_t H, int64_t Hkv, int64_t dk, int64_t dv, int dtype, float scale,
     int use_qk_l2norm, int gate_logits, float g_bias, float b_bias, int64_t chunk, void* workspace,
-    size_t workspace_bytes, void* stream) {
+    size_t workspace_bytes, int32_t* start_flag, int32_t start_epoch, void* stream) {
   using namespace atma;
   if (chunk != kChunk)
     return set_error(ATMA_ERR_UNSUPPORTED, "chunk_gated_delta_rule: chunk must be %d", kChunk);
@@ -382,7 +383,41 @@ extern "C" int atma_chunk_gated_delta_rule(
   a.G = (int)(H / Hkv);
   a.scale = scale; a.l2norm = use_qk_l2norm ? 1 : 0; a.ws = workspace;
   a.gate_logits = gate_logits ? 1 : 0; a.g_bias = g_bias; a.b_bias = b_bias;
+  a.start_flag = start_flag; a.start_epoch = start_epoch;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == ATMA_BF16 || dtype == ATMA_F16) return launch_gdn16(a, dtype, (int)dk, s);
   return dk == 128 ? launch_gdn<float, 128>(a, s) : launch_gdn<float, 64>(a, s);
+}
+
+namespace atma {
+
+// One lane polls the flag (agent-scope loads, which see another kernel's store across the
+// XCDs' L2s) with a sleep between polls, and gives up after limit_ticks of the constant
+// wall clock, so the kernel always ends; a timeout only costs the overlap, never results.
+__global__ void __launch_bounds__(64) start_wait_kernel(const int* flag, int epoch, uint64_t limit_ticks) {
+  if (threadIdx.x != 0) return;
+  const uint64_t t0 = wall_clock64();
+  while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != epoch) {
+    if (wall_clock64() - t0 > limit_ticks) break;
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
+}  // namespace atma
+
+extern "C" int atma_wait_start_flag(const int32_t* flag, int32_t epoch, int64_t timeout_us, void* stream) {
+  using namespace atma;
+  if (!flag) return set_error(ATMA_ERR_INVALID, "wait_start_flag: null flag");
+  if (timeout_us <= 0 || timeout_us > 10000000)
+    return set_error(ATMA_ERR_INVALID, "wait_start_flag: timeout_us must be in (0, 1e7]");
+  static int rate_khz = 0;  // wall clock rate; the same for every MI355X device
+  if (!rate_khz) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || rate_khz <= 0)
+      return set_error(ATMA_ERR_HIP, "wait_start_flag: wall clock rate unavailable");
+  }
+  const uint64_t ticks = (uint64_t)timeout_us * (uint64_t)rate_khz / 1000u;
+  start_wait_kernel<<<dim3(1), dim3(64), 0, (hipStream_t)stream>>>(flag, epoch, ticks);
+  return check_launch("wait_start_flag");
 }

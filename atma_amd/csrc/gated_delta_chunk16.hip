@@ -343,6 +343,7 @@ __global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
   __shared__ __attribute__((aligned(16))) T Kr[3 * QB];    // raw k rows of chunk j in slot j % 3
   __shared__ __attribute__((aligned(16))) T Rs[3 * RB];    // rq of chunk j in slot j % 3
   __shared__ __attribute__((aligned(16))) float Fs[3 * 3 * C];  // lg, kf, qs of chunk j
+  gdn_signal_start(a);
   __shared__ __attribute__((aligned(16))) T Os[4 * 16 * OP];   // per-wave O tile, [row][v]
 
   const int tid = threadIdx.x, lane = tid & 63;

@@ -10,13 +10,16 @@ import torch
 
 from .. import _lib
 from .conv import causal_conv1d_decode_step
-from .gated_delta import chunk_gated_delta_rule, gated_delta_decode_step, gated_delta_gates
+from .gated_delta import (StartSignal, chunk_gated_delta_rule, gated_delta_decode_step, gated_delta_gates,
+                          recurrence_pays_to_overlap)
 from .polar import polar_attention_decode, polar_attention_fwd, polar_attention_packed_fwd
 from .polar_train import polar_attention
 
 HAS_HIP = _lib.available() and torch.cuda.is_available()
 
 __all__ = [
+    "StartSignal",
+    "recurrence_pays_to_overlap",
     "HAS_HIP",
     "polar_attention_fwd",
     "polar_attention",

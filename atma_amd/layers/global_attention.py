@@ -13,11 +13,16 @@ gated-delta memory, with the reference's parameter names and three routes.
 
 The Polar and gated-delta arithmetic runs in the HIP kernels (``atma_amd.kernel``);
 projections, RMSNorm and the depthwise Canon conv stay eager, as in the reference.
-Unlike the reference, K/V reach the Polar kernels unexpanded (GQA is resolved
-in-kernel); the memory branch sees them expanded, as it does in the reference.
-With ``overlap=True`` the memory branch runs on a second HIP stream concurrently
-with Polar attention (the two only share their inputs); off by default, because
-the prefill kernels each fill the GPU and measured slower side by side.
+Unlike the reference, K/V reach the Polar and gated-delta kernels unexpanded (GQA is
+resolved in-kernel).
+Prefill schedule (``overlap``): the memory branch may run on a second HIP stream beside
+Polar attention (the two only share their inputs).  The gated-delta recurrence is
+latency-bound with one workgroup per CU, so this pays only when its grid is small (a
+quarter of the CUs or less: long sequences, small batches), and only if its workgroups
+start before Polar's fill the GPU; Polar's launch therefore waits on the recurrence's
+start signal (``StartSignal``).  ``overlap="auto"`` (default) takes the overlapped
+schedule exactly when ``recurrence_pays_to_overlap`` says so, ``True`` always, ``False``
+never.  Results are bitwise the same in every schedule.
 """
 
 from dataclasses import dataclass
@@ -27,8 +32,9 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from ..kernel import (causal_conv1d_decode_step, chunk_gated_delta_rule, gated_delta_decode_step,
-                      gated_delta_gates, polar_attention_decode, polar_attention_fwd)
+from ..kernel import (StartSignal, causal_conv1d_decode_step, chunk_gated_delta_rule,
+                      gated_delta_decode_step, gated_delta_gates, polar_attention_decode,
+                      polar_attention_fwd, recurrence_pays_to_overlap)
 from .attention import store_kvcache
 
 # Polar structural priors (model/reference.py:17-20)
@@ -72,18 +78,20 @@ class TitansMemory(nn.Module):
         r = F.rms_norm(r, (self.dk,)).reshape(*lead, self.H * self.dk).to(x.dtype)
         return self.proj(r * torch.sigmoid(self.gate(x)))
 
-    def forward(self, x, q, k, v, initial_state=None, output_final_state=False):
+    def forward(self, x, q, k, v, initial_state=None, output_final_state=False, start_signal=None):
         """x: (B, T, dim); q: (B, T, H, dk); k, v: (B, T, Hkv, dk) with H % Hkv == 0
         (the kernel maps query head h to KV head h // (H // Hkv), so the reference's
         repeat_interleave expansion is not materialised).  initial_state:
-        ``[K, V]`` (B, H, dk, dv) fp32 or None.  Returns (out (B, T, dim), final
+        ``[K, V]`` (B, H, dk, dv) fp32 or None.  ``start_signal``: raised as the recurrence
+        kernel starts (the overlapped prefill schedule).  Returns (out (B, T, dim), final
         state or None) -- ``_mem_prefill_dense`` (``inference/models/atma.py:305-339``)."""
         zg, zb = self.raw_logits(x)   # activations applied inside the prefill's load
         r, S = chunk_gated_delta_rule(q, k, v, zg, zb, scale=1.0,
                                       initial_state=initial_state,
                                       output_final_state=output_final_state,
                                       use_qk_l2norm_in_kernel=True,
-                                      gate_bias=(self.gamma_bias, self.beta_bias))
+                                      gate_bias=(self.gamma_bias, self.beta_bias),
+                                      start_signal=start_signal)
         return self._out(x, r), S
 
     def step(self, x, q, k, v, state_table, slots):
@@ -128,7 +136,7 @@ class PolarAttention(nn.Module):
 
     def __init__(self, dim, head_dim=128, num_kv_heads=None, kernel_size=4, window=None,
                  mem_enabled=True, mem_chunk=64, mem_gamma_bias=3.9, mem_beta_bias=0.0,
-                 num_heads=None, overlap=False):
+                 num_heads=None, overlap="auto"):
         super().__init__()
         self.num_heads = num_heads if num_heads is not None else dim // head_dim
         self.num_kv_heads = num_kv_heads if num_kv_heads is not None else self.num_heads // 4
@@ -152,8 +160,11 @@ class PolarAttention(nn.Module):
         self.mag_beta_raw = nn.Parameter(torch.full((H,), MAG_BETA_INIT))
         self.mem = (TitansMemory(dim, H, dk, chunk=mem_chunk, gamma_bias=mem_gamma_bias,
                                  beta_bias=mem_beta_bias) if mem_enabled else None)
+        if overlap not in (True, False, "auto"):
+            raise ValueError(f"overlap must be True, False or 'auto' (got {overlap!r})")
         self.overlap = overlap
         self._side = {}
+        self._signal = {}
 
     # ------------------------------------------------------------------ pieces
     def polar_params(self):
@@ -201,20 +212,32 @@ class PolarAttention(nn.Module):
         s = self._side.get(device)
         if s is None:
             s = self._side[device] = torch.cuda.Stream(device=device)  # default priority
+            self._signal[device] = StartSignal(device)
         return s
 
+    def _overlapped(self, B, dtype, device):
+        if self.mem is None or self.overlap is False or device.type != "cuda" \
+                or torch.cuda.is_current_stream_capturing():
+            return False
+        return self.overlap is True or recurrence_pays_to_overlap(B, self.num_heads, self.head_dim,
+                                                                  dtype, device)
+
     def _with_memory(self, polar_fn, mem_fn, inputs):
-        """Run the Polar part on the current stream and the memory branch, concurrently
-        on a side stream when ``overlap`` is set; return (polar result, memory result)."""
+        """Run the Polar part on the current stream and the memory branch (``mem_fn(signal)``)
+        in the layer's schedule; return (polar result, memory result)."""
         if self.mem is None:
             return polar_fn(), None
-        if not self.overlap or not inputs[0].is_cuda or torch.cuda.is_current_stream_capturing():
-            return polar_fn(), mem_fn()
-        main = torch.cuda.current_stream(inputs[0].device)
-        side = self._side_stream(inputs[0].device)
+        x = inputs[0]
+        if not self._overlapped(x.shape[0], x.dtype, x.device):
+            return polar_fn(), mem_fn(None)
+        main = torch.cuda.current_stream(x.device)
+        side = self._side_stream(x.device)
+        signal = self._signal[x.device]
+        signal.arm()
         side.wait_stream(main)
         with torch.cuda.stream(side):
-            m = mem_fn()
+            m = mem_fn(signal)
+        signal.wait()          # Polar is dispatched once the recurrence holds its CUs
         p = polar_fn()
         main.wait_stream(side)
         for t in inputs:
@@ -245,8 +268,9 @@ class PolarAttention(nn.Module):
                                          **self.polar_params())
             return self._combine(c.transpose(1, 2), mag.transpose(1, 2), gate)
 
-        def memory():
-            return self.mem(x, q, k, v, initial_state=S0, output_final_state=final_sink is not None)
+        def memory(signal):
+            return self.mem(x, q, k, v, initial_state=S0, output_final_state=final_sink is not None,
+                            start_signal=signal)
 
         out, m = self._with_memory(polar, memory, (x, q, k, v))
         if m is not None:
@@ -325,7 +349,7 @@ class GlobalBlock(nn.Module):
     ``x + attn(norm1 x)``, then ``x + mlp(norm2 x)``."""
 
     def __init__(self, dim, head_dim=128, num_kv_heads=None, attn_kernel_size=4, window=None,
-                 mem_enabled=True, mem_chunk=64, overlap=False):
+                 mem_enabled=True, mem_chunk=64, overlap="auto"):
         super().__init__()
         self.attn = PolarAttention(dim, head_dim=head_dim, num_kv_heads=num_kv_heads,
                                    kernel_size=attn_kernel_size, window=window, mem_enabled=mem_enabled,

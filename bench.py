@@ -4,8 +4,10 @@ Default workload (the `value`): BASELINE.json configs[1] -- bf16 global-layer pr
 B=8, T=2048, 8 query / 2 KV heads, d=128: Polar attention forward (GQA in-kernel) plus
 the gated-delta chunked prefill (C=64, fp32 state from zero, memory gate / beta logits
 activated inside the prefill kernel's load as the layer does: logsigmoid(z + 3.9), sigmoid(z)).  One step = both ops over
-the resident batch, back to back on one stream (the time with the memory branch on a
-second stream is reported as ms_overlap).
+the resident batch in the global layer's schedule for the shape: back to back on one
+stream, or -- when the recurrence kernel's grid takes at most a quarter of the CUs, as
+at B=1, T=65,536 -- the memory branch on a second stream with Polar launched once the
+recurrence has started (both schedules are reported: ms_sequential, ms_overlap).
 value = (Polar + gated-delta algorithmic FLOPs) / step time.
 
 Also reported in the same JSON line: configs[2] (B=1, T=65,536 and 262,144) and
@@ -56,7 +58,8 @@ class Prefill:
     """Resident inputs and one step of the prefill hot path."""
 
     def __init__(self, torch, dev, B, T, seed=0):
-        from atma_amd.kernel import chunk_gated_delta_rule, polar_attention_fwd
+        from atma_amd.kernel import (StartSignal, chunk_gated_delta_rule, polar_attention_fwd,
+                                     recurrence_pays_to_overlap)
         self.torch, self.B, self.T = torch, B, T
         self.fwd, self.gdn = polar_attention_fwd, chunk_gated_delta_rule
         g = torch.Generator(device=dev).manual_seed(seed)
@@ -75,29 +78,39 @@ class Prefill:
         self.n_keys = torch.arange(1, T + 1, device=dev, dtype=torch.float32)
         self.p = _params(torch, dev, seed)
         self.side = torch.cuda.Stream(device=dev)  # default priority
+        self.signal = StartSignal(dev)
+        # the global layer's schedule for this shape (PolarAttention(overlap="auto"))
+        self.overlap = recurrence_pays_to_overlap(B, HQ, D, torch.bfloat16, dev)
 
     def polar(self):
         return self.fwd(self.q, self.k, self.v, self.n_keys, **self.p)
 
-    def memory(self):
+    def memory(self, signal=None):
         # raw gate logits: the layer's activations (logsigmoid(z + 3.9), sigmoid(z)) are
         # applied inside the prefill kernel's load, as TitansMemory does
         return self.gdn(self.qm, self.km, self.vm, self.zg, self.zb, scale=1.0, initial_state=self.s0,
-                        output_final_state=True, use_qk_l2norm_in_kernel=True, gate_bias=(3.9, 0.0))
+                        output_final_state=True, use_qk_l2norm_in_kernel=True, gate_bias=(3.9, 0.0),
+                        start_signal=signal)
 
     def step(self):
-        """Both ops of the mixer back to back on one stream."""
+        """One mixer step in the global layer's schedule for this shape."""
+        return self.step_overlap() if self.overlap else self.step_sequential()
+
+    def step_sequential(self):
+        """Both ops back to back on one stream."""
         self.polar()
         self.memory()
 
     def step_overlap(self):
-        """The memory branch on a second stream concurrently with Polar attention
-        (``PolarAttention(overlap=True)``); slower today, since Polar fills every CU."""
+        """The memory branch on a second stream; Polar's launch waits (one-wave kernel) until
+        the recurrence's workgroups have started, then runs beside it."""
         torch = self.torch
         main = torch.cuda.current_stream()
+        self.signal.arm()
         self.side.wait_stream(main)
         with torch.cuda.stream(self.side):
-            self.memory()
+            self.memory(self.signal)
+        self.signal.wait()
         self.polar()
         main.wait_stream(self.side)
 
@@ -123,11 +136,13 @@ def bench_prefill(torch, dev, B, T, steps, warmup):
     w = Prefill(torch, dev, B, T)
     fp, fg = w.flops()
     ms_step = _time(torch, w.step, steps, warmup)
+    ms_seq = _time(torch, w.step_sequential, steps, max(1, warmup // 2))
     ms_ovl = _time(torch, w.step_overlap, steps, max(1, warmup // 2))
     ms_polar = _time(torch, w.polar, steps, max(1, warmup // 2))
     ms_gdn = _time(torch, w.memory, steps, max(1, warmup // 2))
     res = dict(B=B, T=T, ms_per_step=ms_step, tflops=(fp + fg) / (ms_step * 1e-3) / 1e12,
-               ms_overlap=ms_ovl,
+               schedule="overlap" if w.overlap else "sequential",
+               ms_sequential=ms_seq, ms_overlap=ms_ovl,
                polar_ms=ms_polar, polar_tflops=fp / (ms_polar * 1e-3) / 1e12,
                gdn_ms=ms_gdn, gdn_tflops=fg / (ms_gdn * 1e-3) / 1e12,
                polar_flops=fp, gdn_flops=fg)

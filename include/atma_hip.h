@@ -231,7 +231,9 @@ size_t atma_chunk_gated_delta_workspace_bytes(int64_t B, int64_t T, int64_t H, i
  * of atma_gated_delta_gates on load (log-decay logsigmoid(g + g_bias), write strength
  * sigmoid(beta + b_bias)), bit-identical to calling it first (an extension with no
  * FLA counterpart: one launch fewer for TitansMemory).  chunk must be 64;
- * dk = dv = 128 or 64.
+ * dk = dv = 128 or 64.  start_flag (nullable; no FLA counterpart): the recurrence
+ * kernel's first workgroup stores start_epoch there as it starts, for
+ * atma_wait_start_flag.
  */
 int atma_chunk_gated_delta_rule(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
                                 const void* k, int64_t k_sb, int64_t k_st, int64_t k_sh,
@@ -241,7 +243,19 @@ int atma_chunk_gated_delta_rule(const void* q, int64_t q_sb, int64_t q_st, int64
                                 int64_t Hkv, int64_t dk, int64_t dv, int dtype, float scale,
                                 int use_qk_l2norm, int gate_logits, float g_bias, float b_bias,
                                 int64_t chunk, void* workspace, size_t workspace_bytes,
-                                void* stream);
+                                int32_t* start_flag, int32_t start_epoch, void* stream);
+
+/*
+ * Launch-order helper with no counterpart in the reference: a one-wave kernel on
+ * `stream` that returns once *flag == epoch (the store atma_chunk_gated_delta_rule's
+ * recurrence kernel makes as it starts) or after timeout_us, whichever is first.
+ * Work queued behind it on `stream` is therefore dispatched after the recurrence's
+ * workgroups hold their CUs.  The overlapped prefill of the global layer uses it so that
+ * Polar attention (which fills every CU) runs beside the latency-bound recurrence
+ * instead of before it.  A timeout changes timing only, never results.
+ * timeout_us in (0, 1e7].
+ */
+int atma_wait_start_flag(const int32_t* flag, int32_t epoch, int64_t timeout_us, void* stream);
 
 #ifdef __cplusplus
 }

@@ -66,7 +66,11 @@ def test_validation_rejects_without_launch(lib):
     assert lib.atma_chunk_gated_delta_rule(null, 0, 0, 0, null, 0, 0, 0, null, 0, 0, 0, null, null,
                                            null, null, null, 1, 64, 2, 2, 128, 128, 1, 1.0, 1, 0,
                                            0.0, 0.0, 32,
-                                           null, 0, null) == 2
+                                           null, 0, null, 0, null) == 2
+    # start-flag wait: null flag, timeout out of range
+    assert lib.atma_wait_start_flag(null, 1, 1000, null) == 1
+    buf4 = ctypes.create_string_buffer(4)
+    assert lib.atma_wait_start_flag(buf4, 1, 0, null) == 1
     assert lib.atma_chunk_gated_delta_workspace_bytes(1, 65, 2, 128, 128, 64, 0) == 2 * 2 * (5 * 64 * 128 + 4) * 4
     # 16-bit path: per (sequence, head, chunk) w, u (C x d each) and rq (C x C) in 16
     # bits, then 3 x C fp32 per-token factors (log-decay, key and query weights)

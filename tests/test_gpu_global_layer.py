@@ -57,11 +57,15 @@ def test_mixer_bf16_vs_fp32_oracle(dev):
     assert rel_err(out.float(), ref) <= 2e-2, rel_err(out.float(), ref)
 
 
-def test_side_stream_overlap_is_bitwise_neutral(dev):
-    a = _block(overlap=True).attn.to(dev)
-    b = _block(overlap=False).attn.to(dev)
-    x = torch.randn(2, 96, DIM, device=dev)
-    assert torch.equal(a(x), b(x))
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_side_stream_overlap_is_bitwise_neutral(dev, dtype):
+    a = _block(overlap=True).attn.to(dev, dtype)
+    b = _block(overlap=False).attn.to(dev, dtype)
+    c = _block(overlap="auto").attn.to(dev, dtype)
+    x = torch.randn(2, 96, DIM, device=dev).to(dtype)
+    ref = b(x)
+    for _ in range(2):
+        assert torch.equal(a(x), ref) and torch.equal(c(x), ref)
 
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
