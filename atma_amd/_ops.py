@@ -100,6 +100,43 @@ def _(q, k, v, n_keys, v_null, null_base, null_slope_raw, len_gain_raw, mag_beta
             q.new_empty((B, Hq, Tq), **f), q.new_empty((B, Hq, Tq), **f), q.new_empty((B, Hq, Tq, d), **f)]
 
 
+@torch.library.custom_op("atma_hip::polar_attention_bwd_prep", mutates_args=())
+def polar_attention_bwd_prep_op(gc: Optional[Tensor], gm: Optional[Tensor], S: Tensor, M: Tensor,
+                                L: Tensor, Q2: Tensor, n_keys: Tensor, v_null: Tensor,
+                                null_base: Tensor, null_slope_raw: Tensor, len_gain_raw: Tensor,
+                                mag_beta_raw: Tensor, eps: float, window: int, preserve_length: bool,
+                                dtype: torch.dtype) -> List[Tensor]:
+    """The backward's per-query preamble: returns gs (dtype), gL, gQ2, temp (H, T) and the
+    per-block parameter partial sums (B * ceil(T / 16), H, d + 4), all fp32 but gs."""
+    _need_cuda(S, M, L, Q2, n_keys, v_null)
+    lib = _lib.load()
+    B, H, T, d = S.shape
+    f = dict(device=S.device, dtype=torch.float32)
+    gc = None if gc is None else gc.to(dtype).contiguous()
+    gm = None if gm is None else gm.to(dtype).contiguous()
+    gs = torch.empty((B, H, T, d), device=S.device, dtype=dtype)
+    gL = torch.empty((B, H, T), **f)
+    gQ2 = torch.empty((B, H, T), **f)
+    temp = torch.empty((H, T), **f)
+    part = torch.empty((B * ((T + 15) // 16), H, d + 4), **f)
+    rc = lib.atma_polar_attention_bwd_prep(
+        _lib.ptr(gc), _lib.ptr(gm), S.data_ptr(), M.data_ptr(), L.data_ptr(), Q2.data_ptr(),
+        n_keys.data_ptr(), v_null.data_ptr(), null_base.data_ptr(), null_slope_raw.data_ptr(),
+        len_gain_raw.data_ptr(), mag_beta_raw.data_ptr(), gs.data_ptr(), gL.data_ptr(), gQ2.data_ptr(),
+        temp.data_ptr(), part.data_ptr(), B, H, T, d, _lib.dtype_code(dtype), window,
+        1 if preserve_length else 0, eps, _lib.stream_handle(S.device))
+    _lib.check(rc, "polar_attention_bwd_prep")
+    return [gs, gL, gQ2, temp, part]
+
+
+@polar_attention_bwd_prep_op.register_fake
+def _(gc, gm, S, M, L, Q2, n_keys, v_null, null_base, null_slope_raw, len_gain_raw, mag_beta_raw, eps,
+      window, preserve_length, dtype):
+    B, H, T, d = S.shape
+    return [S.new_empty((B, H, T, d), dtype=dtype), S.new_empty((B, H, T)), S.new_empty((B, H, T)),
+            S.new_empty((H, T)), S.new_empty((B * ((T + 15) // 16), H, d + 4))]
+
+
 @torch.library.custom_op("atma_hip::polar_attention_bwd", mutates_args=())
 def polar_attention_bwd_op(q: Tensor, k: Tensor, v: Tensor, gs: Tensor, gL: Tensor, gQ2: Tensor,
                            M: Tensor, temp: Tensor, n_keys: Tensor, is_causal: bool,
@@ -111,10 +148,11 @@ def polar_attention_bwd_op(q: Tensor, k: Tensor, v: Tensor, gs: Tensor, gL: Tens
     B, Hq, Tq, d = q.shape
     Hkv, Tk = k.shape[1], k.shape[2]
     f = dict(device=q.device, dtype=torch.float32)
-    dq = torch.zeros((B, Hq, Tq, d), **f)   # zeros: with no keys the launch is skipped
-    dt = torch.zeros((B, Hq, Tq), **f)
-    dk = torch.zeros((B, Hkv, Tk, d), **f)
-    dv = torch.zeros((B, Hkv, Tk, d), **f)
+    new = torch.empty if Tk > 0 else torch.zeros   # with no keys nothing is written
+    dq = new((B, Hq, Tq, d), **f)
+    dt = new((B, Hq, Tq), **f)
+    dk = new((B, Hq, Tk, d), **f)   # each query head's share; the group sum follows
+    dv = new((B, Hq, Tk, d), **f)
     gL, gQ2, M, temp = (t.to(torch.float32).contiguous() for t in (gL, gQ2, M, temp))
     rc = lib.atma_polar_attention_bwd(
         q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
@@ -125,6 +163,9 @@ def polar_attention_bwd_op(q: Tensor, k: Tensor, v: Tensor, gs: Tensor, gL: Tens
         dq.data_ptr(), dt.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, Hq, Hkv, Tq, Tk, d,
         _lib.dtype_code(q.dtype), 1 if is_causal else 0, window, _lib.stream_handle(q.device))
     _lib.check(rc, "polar_attention_bwd")
+    if Hkv != Hq:   # grouped heads: fixed-order sum of the group's shares
+        dk = dk.view(B, Hkv, Hq // Hkv, Tk, d).sum(2)
+        dv = dv.view(B, Hkv, Hq // Hkv, Tk, d).sum(2)
     return [dq, dt, dk, dv]
 
 

@@ -17,11 +17,17 @@
 //    the elementwise gradient in registers, dS through a per-wave LDS tile (row-major, so
 //    it is read back as the A operand), then dQ += dS K with K^T fragments taken by
 //    transposing reads of the row-major K tile.
-//  * dk/dv kernel: a workgroup owns 64 keys of one KV head (k and v rows as A fragments)
-//    and walks the G query heads of the group x 64-query blocks: S^T and dP^T on MFMA,
-//    P^T and dS^T through per-wave LDS tiles, dV += P^T gs and dK += dS^T Q with gs / Q
-//    fragments by transposing reads.  GQA gradients are summed over the group in-kernel,
-//    so every dk / dv row is written once (no atomics).
+//  * dk/dv kernel: a workgroup owns 64 keys of one KV head for ONE query head (k and v
+//    rows as A fragments) and walks its 64-query blocks: S^T and dP^T on MFMA, P^T and
+//    dS^T through per-wave LDS tiles, dV += P^T gs and dK += dS^T Q with gs / Q fragments
+//    by transposing reads.  Its dk / dv rows go to that query head's slice of a
+//    (B, Hq, Tk, D) output (written once, no atomics); with grouped heads the caller sums
+//    the G slices of a group.  One workgroup per query head (not per KV head) gives G
+//    times the workgroups, which a causal T = 2,048 grid needs to fill 256 CUs.
+//  * Both kernels keep the next block's tiles in flight in registers while the current
+//    block is computed (one LDS buffer, two barriers per block), and order the grid
+//    longest-first (the causal work of a query block grows with its index, of a key
+//    block shrinks), so the short tail fills in behind the long blocks.
 // Products accumulate in fp32; 16-bit inputs round P and dS to the input dtype for the
 // second products, as the reference does (kernel/polar_triton.py:942,1023-1024).
 #include <type_traits>
@@ -46,8 +52,8 @@ struct PolarBwdArgs {
   const float* n_keys;  // (Tq,)
   float* dq;            // (B, Hq, Tq, D)
   float* dt;            // (B, Hq, Tq)
-  float* dk;            // (B, Hkv, Tk, D)
-  float* dv;            // (B, Hkv, Tk, D)
+  float* dk;            // (B, Hq, Tk, D): each query head's share; grouped heads summed by the caller
+  float* dv;            // (B, Hq, Tk, D)
   int B, Hq, Hkv, Tq, Tk;
   int is_causal, window;
   float scale;
@@ -101,18 +107,34 @@ __device__ __forceinline__ BwFrag<T> bw_global_rows(const T* base, int64_t st, i
   }
 }
 // Cooperative copy of rows r0 .. r0 + 63 of a row-major (rows, D) source with row stride st
-// into a padded LDS tile (rows past `rows` become zeros), 16 bytes per thread and step.
+// into a padded LDS tile (rows past `rows` become zeros), 16 bytes per thread and step, in
+// two halves: bw_fetch issues the global loads into registers, bw_put writes them to LDS,
+// so the loads of the next block can be in flight during the current block's products.
 template <typename T, int D>
-__device__ __forceinline__ void bw_tile(T* dst, const T* src, int64_t st, int r0, int rows, int tid) {
-  constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
-  constexpr int CPR = D / EPC, LD = D + kBwPad<T>;
+struct BwTile {
+  static constexpr int EPC = 16 / (int)sizeof(T);  // elements per 16-byte chunk
+  static constexpr int CPR = D / EPC;              // chunks per row
+  static constexpr int N = 64 * CPR / 256;         // chunks per thread
+  u32x4 x[N];
+};
+template <typename T, int D>
+__device__ __forceinline__ void bw_fetch(BwTile<T, D>& t, const T* src, int64_t st, int r0, int rows, int tid) {
+  using TT = BwTile<T, D>;
 #pragma unroll
-  for (int c = tid; c < 64 * CPR; c += 256) {
-    const int r = c / CPR, e = (c % CPR) * EPC;
+  for (int i = 0; i < TT::N; ++i) {
+    const int c = tid + 256 * i, r = c / TT::CPR, e = (c % TT::CPR) * TT::EPC;
     const int gr = r0 + r;
-    u32x4 x = {0, 0, 0, 0};
-    if (gr < rows) x = *(const u32x4*)(src + (int64_t)gr * st + e);
-    *(u32x4*)(dst + r * LD + e) = x;
+    t.x[i] = gr < rows ? *(const u32x4*)(src + (int64_t)gr * st + e) : u32x4{0, 0, 0, 0};
+  }
+}
+template <typename T, int D>
+__device__ __forceinline__ void bw_put(T* dst, const BwTile<T, D>& t, int tid) {
+  using TT = BwTile<T, D>;
+  constexpr int LD = D + kBwPad<T>;
+#pragma unroll
+  for (int i = 0; i < TT::N; ++i) {
+    const int c = tid + 256 * i, r = c / TT::CPR, e = (c % TT::CPR) * TT::EPC;
+    *(u32x4*)(dst + r * LD + e) = t.x[i];
   }
 }
 
@@ -133,8 +155,9 @@ __global__ void __launch_bounds__(256) polar_bwd_dq_kernel(PolarBwdArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = a.Hq / a.Hkv;
-  const int bh = blockIdx.y, b = bh / a.Hq, hq = bh % a.Hq, hk = hq / G;
-  const int q0 = blockIdx.x * BM, r0 = q0 + 16 * wave;
+  // grid (B * Hq, query blocks) with the last query block (the most keys) first
+  const int bh = blockIdx.x, b = bh / a.Hq, hq = bh % a.Hq, hk = hq / G;
+  const int q0 = ((int)gridDim.y - 1 - (int)blockIdx.y) * BM, r0 = q0 + 16 * wave;
   const T* qp = (const T*)a.q + b * a.q_sb + hq * a.q_sh;
   const T* gp = (const T*)a.gs + b * a.g_sb + hq * a.g_sh;
   const T* kp = (const T*)a.k + b * a.k_sb + hk * a.k_sh;
@@ -169,10 +192,19 @@ __global__ void __launch_bounds__(256) polar_bwd_dq_kernel(PolarBwdArgs a) {
   const int hi = a.is_causal ? min(q0 + BM, a.Tk) : a.Tk;
   const int lo = a.window > 0 ? (max(q0 - a.window, 0) / BN) * BN : 0;
   T* sd = Sd[wave];
+  BwTile<T, D> kn, vn;  // the next key block, in flight
+  if (lo < hi) {
+    bw_fetch<T, D>(kn, kp, a.k_st, lo, a.Tk, tid);
+    bw_fetch<T, D>(vn, vp, a.v_st, lo, a.Tk, tid);
+  }
   for (int k0 = lo; k0 < hi; k0 += BN) {
     __syncthreads();  // every wave is done with the previous block
-    bw_tile<T, D>(Ks, kp, a.k_st, k0, a.Tk, tid);
-    bw_tile<T, D>(Vs, vp, a.v_st, k0, a.Tk, tid);
+    bw_put<T, D>(Ks, kn, tid);
+    bw_put<T, D>(Vs, vn, tid);
+    if (k0 + BN < hi) {
+      bw_fetch<T, D>(kn, kp, a.k_st, k0 + BN, a.Tk, tid);
+      bw_fetch<T, D>(vn, vp, a.v_st, k0 + BN, a.Tk, tid);
+    }
     __syncthreads();
     // S = Q K^T and dP = gs V^T for 4 key tiles of 16
     f32x4 s[4], p[4];
@@ -225,7 +257,7 @@ __global__ void __launch_bounds__(256) polar_bwd_dq_kernel(PolarBwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
-// dk, dv: workgroup = (64-key tile, b * Hkv + hk); loops over the group's query heads
+// dk, dv: workgroup = (b * Hq + hq, 64-key tile); writes hq's slice of (B, Hq, Tk, D)
 template <typename T, int D>
 __global__ void __launch_bounds__(256) polar_bwd_dkdv_kernel(PolarBwdArgs a) {
   constexpr int BK = 64, BQ = 64, KD = kBwK<T>, LD = D + kBwPad<T>, SLD = BQ + kBwPad<T>;
@@ -238,10 +270,13 @@ __global__ void __launch_bounds__(256) polar_bwd_dkdv_kernel(PolarBwdArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = a.Hq / a.Hkv;
-  const int bhk = blockIdx.y, b = bhk / a.Hkv, hk = bhk % a.Hkv;
-  const int k0 = blockIdx.x * BK, kr0 = k0 + 16 * wave;
+  // grid (B * Hq, key blocks), key block 0 (the most queries) first
+  const int bh = blockIdx.x, b = bh / a.Hq, hq = bh % a.Hq, hk = hq / G;
+  const int k0 = blockIdx.y * BK, kr0 = k0 + 16 * wave;
   const T* kp = (const T*)a.k + b * a.k_sb + hk * a.k_sh;
   const T* vp = (const T*)a.v + b * a.v_sb + hk * a.v_sh;
+  const T* qp = (const T*)a.q + b * a.q_sb + hq * a.q_sh;
+  const T* gp = (const T*)a.gs + b * a.g_sb + hq * a.g_sh;
 
   BwFrag<T> kf[D / KD], vf[D / KD];
 #pragma unroll
@@ -257,76 +292,89 @@ __global__ void __launch_bounds__(256) polar_bwd_dkdv_kernel(PolarBwdArgs a) {
   const int hi = a.window > 0 ? min(k0 + BK + a.window, a.Tq) : a.Tq;
   T* pt = Pt[wave];
   T* dst = Dt[wave];
-  for (int g = 0; g < G; ++g) {
-    const int hq = hk * G + g;
-    const int bh = b * a.Hq + hq;
-    const T* qp = (const T*)a.q + b * a.q_sb + hq * a.q_sh;
-    const T* gp = (const T*)a.gs + b * a.g_sb + hq * a.g_sh;
-    for (int q0 = lo; q0 < hi; q0 += BQ) {
-      __syncthreads();  // every wave is done with the previous block
-      bw_tile<T, D>(Qs, qp, a.q_st, q0, a.Tq, tid);
-      bw_tile<T, D>(Gs, gp, a.g_st, q0, a.Tq, tid);
-      if (tid < BQ) {
-        const int row = q0 + tid;
-        const bool ok = row < a.Tq;
-        const int64_t i = (int64_t)bh * a.Tq + row;
-        const float tpv = ok ? a.temp[(int64_t)hq * a.Tq + row] : 1.f;
-        s_tp[tid] = tpv;
-        s_c1[tid] = a.scale * tpv * kLog2e;
-        s_m2[tid] = ok ? a.M[i] * kLog2e : 0.f;
-        s_gl[tid] = ok ? a.gL[i] : 0.f;
-        s_gq2[tid] = ok ? a.gQ2[i] : 0.f;
-        s_nr[tid] = ok ? a.n_keys[row] : 0.f;
-      }
-      __syncthreads();
-      // S^T = K Q^T and dP^T = V gs^T for 4 query tiles of 16
-      f32x4 s[4], p[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        s[t] = p[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ks = 0; ks < D / KD; ++ks) {
-          s[t] = bw_mma<T>(kf[ks], bw_rows<T>(Qs, LD, 16 * t, KD * ks, lane), s[t]);
-          p[t] = bw_mma<T>(vf[ks], bw_rows<T>(Gs, LD, 16 * t, KD * ks, lane), p[t]);
-        }
-      }
-      // C element (key kr0 + 4 (lane / 16) + j, query q0 + 16 t + lane % 16)
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int qi = 16 * t + (lane & 15);
-        const float nrq = s_nr[qi], c1 = s_c1[qi], m2 = s_m2[qi], glq = s_gl[qi], gq2 = s_gq2[qi];
-        const float tpq = s_tp[qi];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int key = kr0 + 4 * (lane >> 4) + j;
-          const float kf_ = (float)key;
-          const bool valid = key < a.Tk && kf_ < nrq && (a.window <= 0 || kf_ >= nrq - (float)a.window);
-          const float pr = valid ? __builtin_amdgcn_exp2f(s[t][j] * c1 - m2) : 0.f;
-          const float da = valid ? (p[t][j] + glq + 2.f * gq2 * pr) * pr : 0.f;
-          const int e = (4 * (lane >> 4) + j) * SLD + qi;
-          pt[e] = bw_round<T>(pr);
-          dst[e] = bw_round<T>(da * tpq);
-        }
-      }
-      wave_sync();
-      // dV += P^T gs, dK += dS^T Q: A = the per-wave tiles (k = queries), B = gs / Q
-#pragma unroll
-      for (int nt = 0; nt < D / 16; ++nt)
-#pragma unroll
-        for (int ks = 0; ks < BQ / KD; ++ks) {
-          dv[nt] = bw_mma<T>(bw_rows<T>(pt, SLD, 0, KD * ks, lane), bw_cols<T>(Gs, LD, KD * ks, 16 * nt, lane),
-                             dv[nt]);
-          dk[nt] = bw_mma<T>(bw_rows<T>(dst, SLD, 0, KD * ks, lane), bw_cols<T>(Qs, LD, KD * ks, 16 * nt, lane),
-                             dk[nt]);
-        }
+  // per-query scalars of the next block (thread tid < 64 holds row q0 + tid)
+  auto row_vals = [&](int q0, float& tp, float& m, float& gl, float& gq2, float& nr) {
+    const int row = q0 + tid;
+    const bool ok = tid < BQ && row < a.Tq;
+    const int64_t i = (int64_t)bh * a.Tq + row;
+    tp = ok ? a.temp[(int64_t)hq * a.Tq + row] : 1.f;
+    m = ok ? a.M[i] : 0.f;
+    gl = ok ? a.gL[i] : 0.f;
+    gq2 = ok ? a.gQ2[i] : 0.f;
+    nr = ok ? a.n_keys[row] : 0.f;  // no valid key for rows past Tq
+  };
+  BwTile<T, D> qn, gn;
+  float n_tp = 1.f, n_m = 0.f, n_gl = 0.f, n_gq2 = 0.f, n_nr = 0.f;
+  if (lo < hi) {
+    bw_fetch<T, D>(qn, qp, a.q_st, lo, a.Tq, tid);
+    bw_fetch<T, D>(gn, gp, a.g_st, lo, a.Tq, tid);
+    row_vals(lo, n_tp, n_m, n_gl, n_gq2, n_nr);
+  }
+  for (int q0 = lo; q0 < hi; q0 += BQ) {
+    __syncthreads();  // every wave is done with the previous block
+    bw_put<T, D>(Qs, qn, tid);
+    bw_put<T, D>(Gs, gn, tid);
+    if (tid < BQ) {
+      s_tp[tid] = n_tp;
+      s_c1[tid] = a.scale * n_tp * kLog2e;
+      s_m2[tid] = n_m * kLog2e;
+      s_gl[tid] = n_gl;
+      s_gq2[tid] = n_gq2;
+      s_nr[tid] = n_nr;
     }
+    if (q0 + BQ < hi) {
+      bw_fetch<T, D>(qn, qp, a.q_st, q0 + BQ, a.Tq, tid);
+      bw_fetch<T, D>(gn, gp, a.g_st, q0 + BQ, a.Tq, tid);
+      row_vals(q0 + BQ, n_tp, n_m, n_gl, n_gq2, n_nr);
+    }
+    __syncthreads();
+    // S^T = K Q^T and dP^T = V gs^T for 4 query tiles of 16
+    f32x4 s[4], p[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      s[t] = p[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < D / KD; ++ks) {
+        s[t] = bw_mma<T>(kf[ks], bw_rows<T>(Qs, LD, 16 * t, KD * ks, lane), s[t]);
+        p[t] = bw_mma<T>(vf[ks], bw_rows<T>(Gs, LD, 16 * t, KD * ks, lane), p[t]);
+      }
+    }
+    // C element (key kr0 + 4 (lane / 16) + j, query q0 + 16 t + lane % 16)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int qi = 16 * t + (lane & 15);
+      const float nrq = s_nr[qi], c1 = s_c1[qi], m2 = s_m2[qi], glq = s_gl[qi], gq2 = s_gq2[qi];
+      const float tpq = s_tp[qi];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int key = kr0 + 4 * (lane >> 4) + j;
+        const float kf_ = (float)key;
+        const bool valid = key < a.Tk && kf_ < nrq && (a.window <= 0 || kf_ >= nrq - (float)a.window);
+        const float pr = valid ? __builtin_amdgcn_exp2f(s[t][j] * c1 - m2) : 0.f;
+        const float da = valid ? (p[t][j] + glq + 2.f * gq2 * pr) * pr : 0.f;
+        const int e = (4 * (lane >> 4) + j) * SLD + qi;
+        pt[e] = bw_round<T>(pr);
+        dst[e] = bw_round<T>(da * tpq);
+      }
+    }
+    wave_sync();
+    // dV += P^T gs, dK += dS^T Q: A = the per-wave tiles (k = queries), B = gs / Q
+#pragma unroll
+    for (int nt = 0; nt < D / 16; ++nt)
+#pragma unroll
+      for (int ks = 0; ks < BQ / KD; ++ks) {
+        dv[nt] = bw_mma<T>(bw_rows<T>(pt, SLD, 0, KD * ks, lane), bw_cols<T>(Gs, LD, KD * ks, 16 * nt, lane),
+                           dv[nt]);
+        dk[nt] = bw_mma<T>(bw_rows<T>(dst, SLD, 0, KD * ks, lane), bw_cols<T>(Qs, LD, KD * ks, 16 * nt, lane),
+                           dk[nt]);
+      }
   }
 
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int row = kr0 + 4 * (lane >> 4) + j;
     if (row < a.Tk) {
-      const int64_t base = ((int64_t)bhk * a.Tk + row) * D + (lane & 15);
+      const int64_t base = ((int64_t)bh * a.Tk + row) * D + (lane & 15);
 #pragma unroll
       for (int nt = 0; nt < D / 16; ++nt) {
         a.dk[base + 16 * nt] = dk[nt][j] * a.scale;
@@ -338,11 +386,135 @@ __global__ void __launch_bounds__(256) polar_bwd_dkdv_kernel(PolarBwdArgs a) {
 
 template <typename T, int D>
 static int launch_bwd(const PolarBwdArgs& a, hipStream_t s) {
-  polar_bwd_dq_kernel<T, D><<<dim3((unsigned)((a.Tq + 63) / 64), (unsigned)(a.B * a.Hq)), dim3(256), 0, s>>>(a);
+  polar_bwd_dq_kernel<T, D><<<dim3((unsigned)(a.B * a.Hq), (unsigned)((a.Tq + 63) / 64)), dim3(256), 0, s>>>(a);
   int rc = check_launch("polar_attention_bwd(dq)");
   if (rc) return rc;
-  polar_bwd_dkdv_kernel<T, D><<<dim3((unsigned)((a.Tk + 63) / 64), (unsigned)(a.B * a.Hkv)), dim3(256), 0, s>>>(a);
+  polar_bwd_dkdv_kernel<T, D><<<dim3((unsigned)(a.B * a.Hq), (unsigned)((a.Tk + 63) / 64)), dim3(256), 0, s>>>(a);
   return check_launch("polar_attention_bwd(dkdv)");
+}
+
+// ---------------------------------------------------------------------------------------
+// Per-query preamble and parameter-gradient partial sums (kernel/polar_triton.py:1049-1155).
+// One wave per query row (4 rows per wave, 16 per workgroup): the row's direction
+// cotangent gs = (gc - (gc.c) c) / max(|s|, eps) with c = s / max(|s|, eps), the
+// magnitude path's cotangents of L and Q2 through m_eff = L^3 / (Q2 Z), Z = L + p_null,
+// and the null sink's share.  Everything the parameter gradients need except the real
+// keys' dL/dtemp (the dq loop's dt) is summed per workgroup into one record
+// [v_null (D) | sum g_anull nu log n | sum g_anull temp | sum g_anull temp sqrt(log(n+1)) |
+// sum gm (1 - mag^2) log1p(m_eff)], summed over workgroups by the caller (fixed order).
+struct PolarPrepArgs {
+  const void* gc;  // (B, H, T, D) dtype, or null (zero cotangent)
+  const void* gm;  // (B, H, T) dtype, or null
+  const float* S;  // (B, H, T, D) the forward's unnormalised direction s
+  const float* M;  // (B, H, T) natural-log reference max
+  const float* L;
+  const float* Q2;
+  const float* n_keys;  // (T,)
+  const float* v_null;  // (H, D)
+  const float *null_base, *null_slope_raw, *len_gain_raw, *mag_beta_raw;  // (H,)
+  void* gs;       // (B, H, T, D) dtype
+  float* gL;      // (B, H, T)
+  float* gQ2;     // (B, H, T)
+  float* temp;    // (H, T), written by the b == 0 workgroups
+  float* part;    // (B * ceil(T / 16), H, D + 4)
+  int B, H, T, window, preserve_length;
+  float eps;
+};
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256) polar_bwd_prep_kernel(PolarPrepArgs a) {
+  constexpr int E = D / 64;  // elements per lane
+  constexpr float kTiny = 1.0e-30f;
+  __shared__ float s_vn[4][D];
+  __shared__ float s_sc[4][4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
+  const float sp_lg = softplus(a.len_gain_raw[h]), sp_ns = softplus(a.null_slope_raw[h]);
+  const float beta = softplus(a.mag_beta_raw[h]), nb = a.null_base[h];
+  float vn[E], vnull[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    vn[e] = 0.f;
+    vnull[e] = a.v_null[(int64_t)h * D + 64 * e + lane];
+  }
+  float acc1 = 0.f, acc2 = 0.f, acc3 = 0.f, acc4 = 0.f;
+  for (int i = 0; i < 4; ++i) {
+    const int t = blockIdx.x * 16 + wave * 4 + i;
+    if (t >= a.T) break;  // uniform per wave
+    const int64_t row = (int64_t)bh * a.T + t;
+    float n = a.n_keys[t];
+    if (a.window > 0 && !a.preserve_length) n = fminf(n, (float)a.window);
+    n = fmaxf(n, 1.f);
+    const float logn = logf(n), root = sqrtf(logf(n + 1.f));
+    const float temp = 1.f + sp_lg * logn, nu = nb + sp_ns * root;
+    const float Lr = a.L[row], Q2r = a.Q2[row];
+    const float p_null = expf(temp * nu - a.M[row]);
+    const float Z = Lr + p_null;
+    const float Zc = fmaxf(Z, kTiny), Q2c = fmaxf(Q2r, kTiny);
+    const float me = (Lr * Lr / Q2c) * (Lr / Zc);
+    const float lm = log1pf(me);
+    const float mag = tanhf(beta * lm);
+    const float gmr = a.gm ? to_f32(((const T*)a.gm)[row]) : 0.f;
+    const float gme = gmr * beta * (1.f - mag * mag) / (1.f + me);
+    const float dme_dL = Lr > 0.f ? 3.f * me / Lr : 0.f;
+    const float dme_dQ2 = Q2r > kTiny ? -me / Q2c : 0.f;
+    const float dme_dZ = Z > kTiny ? -me / Zc : 0.f;
+    // direction path
+    float sv[E], gv[E];
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      sv[e] = a.S[row * D + 64 * e + lane];
+      gv[e] = a.gc ? to_f32(((const T*)a.gc)[row * D + 64 * e + lane]) : 0.f;
+      ss = fmaf(sv[e], sv[e], ss);
+    }
+    const float snorm = fmaxf(sqrtf(wave_sum(ss)), a.eps);
+    const float inv = 1.f / snorm;
+    float gcc = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) gcc = fmaf(gv[e], sv[e] * inv, gcc);
+    gcc = wave_sum(gcc);
+    float gsv = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float g = (gv[e] - gcc * (sv[e] * inv)) * inv;
+      ((T*)a.gs)[row * D + 64 * e + lane] = from_f32<T>(g);
+      gsv = fmaf(g, vnull[e], gsv);
+      vn[e] = fmaf(p_null, g, vn[e]);
+    }
+    gsv = wave_sum(gsv);
+    const float g_anull = (gsv + gme * dme_dZ) * p_null;
+    if (lane == 0) {
+      a.gL[row] = gme * (dme_dL + dme_dZ);
+      a.gQ2[row] = gme * dme_dQ2;
+      if (b == 0) a.temp[(int64_t)h * a.T + t] = temp;
+    }
+    acc1 = fmaf(g_anull * nu, logn, acc1);
+    acc2 = fmaf(g_anull, temp, acc2);
+    acc3 = fmaf(g_anull * temp, root, acc3);
+    acc4 = fmaf(gmr * (1.f - mag * mag), lm, acc4);
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) s_vn[wave][64 * e + lane] = vn[e];
+  if (lane == 0) {
+    s_sc[wave][0] = acc1;
+    s_sc[wave][1] = acc2;
+    s_sc[wave][2] = acc3;
+    s_sc[wave][3] = acc4;
+  }
+  __syncthreads();
+  float* rec = a.part + ((int64_t)(b * gridDim.x + blockIdx.x) * a.H + h) * (D + 4);
+  if (tid < D) rec[tid] = s_vn[0][tid] + s_vn[1][tid] + s_vn[2][tid] + s_vn[3][tid];
+  else if (tid < D + 4) {
+    const int j = tid - D;
+    rec[D + j] = s_sc[0][j] + s_sc[1][j] + s_sc[2][j] + s_sc[3][j];
+  }
+}
+
+template <typename T, int D>
+static int launch_prep(const PolarPrepArgs& a, hipStream_t s) {
+  polar_bwd_prep_kernel<T, D><<<dim3((unsigned)((a.T + 15) / 16), (unsigned)(a.B * a.H)), dim3(256), 0, s>>>(a);
+  return check_launch("polar_attention_bwd_prep");
 }
 
 }  // namespace atma
@@ -363,7 +535,7 @@ extern "C" int atma_polar_attention_bwd(
   if (d != 64 && d != 128)
     return set_error(ATMA_ERR_UNSUPPORTED, "polar_attention_bwd: head_dim %lld (supported: 64, 128)",
                      (long long)d);
-  if (Tq > (1 << 30) || Tk > (1 << 30) || B * Hq > 65535 || B * Hkv > 65535)
+  if (Tq > 64 * 65535 || Tk > 64 * 65535 || B * Hq > 0x7fffffffll)
     return set_error(ATMA_ERR_INVALID, "polar_attention_bwd: sizes too large");
   if (B == 0 || Tq == 0) return ATMA_OK;
   const int es = dtype_size(dtype);
@@ -397,5 +569,37 @@ extern "C" int atma_polar_attention_bwd(
     case ATMA_BF16: return d == 128 ? launch_bwd<bf16, 128>(a, s) : launch_bwd<bf16, 64>(a, s);
     case ATMA_F16: return d == 128 ? launch_bwd<f16, 128>(a, s) : launch_bwd<f16, 64>(a, s);
     default: return d == 128 ? launch_bwd<float, 128>(a, s) : launch_bwd<float, 64>(a, s);
+  }
+}
+
+extern "C" int atma_polar_attention_bwd_prep(
+    const void* gc, const void* gm, const float* S, const float* M, const float* L, const float* Q2,
+    const float* n_keys, const float* v_null, const float* null_base, const float* null_slope_raw,
+    const float* len_gain_raw, const float* mag_beta_raw, void* gs, float* gL, float* gQ2, float* temp,
+    float* part, int64_t B, int64_t H, int64_t T, int64_t d, int dtype, int64_t window,
+    int preserve_length, float eps, void* stream) {
+  using namespace atma;
+  if (B < 0 || H <= 0 || T < 0) return set_error(ATMA_ERR_INVALID, "polar_attention_bwd_prep: bad sizes");
+  if (d != 64 && d != 128)
+    return set_error(ATMA_ERR_UNSUPPORTED, "polar_attention_bwd_prep: head_dim %lld (supported: 64, 128)",
+                     (long long)d);
+  if (B * H > 65535 || T > (1ll << 30))
+    return set_error(ATMA_ERR_INVALID, "polar_attention_bwd_prep: sizes too large");
+  if (B == 0 || T == 0) return ATMA_OK;
+  if (!dtype_size(dtype)) return set_error(ATMA_ERR_INVALID, "polar_attention_bwd_prep: unknown dtype %d", dtype);
+  if (!S || !M || !L || !Q2 || !n_keys || !v_null || !null_base || !null_slope_raw || !len_gain_raw ||
+      !mag_beta_raw || !gs || !gL || !gQ2 || !temp || !part)
+    return set_error(ATMA_ERR_INVALID, "polar_attention_bwd_prep: null pointer");
+  PolarPrepArgs a{};
+  a.gc = gc; a.gm = gm; a.S = S; a.M = M; a.L = L; a.Q2 = Q2; a.n_keys = n_keys; a.v_null = v_null;
+  a.null_base = null_base; a.null_slope_raw = null_slope_raw; a.len_gain_raw = len_gain_raw;
+  a.mag_beta_raw = mag_beta_raw; a.gs = gs; a.gL = gL; a.gQ2 = gQ2; a.temp = temp; a.part = part;
+  a.B = (int)B; a.H = (int)H; a.T = (int)T;
+  a.window = window > 0 ? (int)window : 0; a.preserve_length = preserve_length ? 1 : 0; a.eps = eps;
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case ATMA_BF16: return d == 128 ? launch_prep<bf16, 128>(a, s) : launch_prep<bf16, 64>(a, s);
+    case ATMA_F16: return d == 128 ? launch_prep<f16, 128>(a, s) : launch_prep<f16, 64>(a, s);
+    default: return d == 128 ? launch_prep<float, 128>(a, s) : launch_prep<float, 64>(a, s);
   }
 }

@@ -120,13 +120,36 @@ int atma_polar_attention_packed_fwd(const void* q, int64_t q_st, int64_t q_sh, c
  * Polar attention backward: the two O(T^2) loops of _polar_backward
  * (kernel/polar_triton.py:861-1155; _polar_bwd_dq_kernel :870-947,
  * _polar_bwd_dkdv_kernel :951-1030).  q, gs: (B, Hq, Tq, d) and k, v: (B, Hkv, Tk, d)
- * in dtype with strides (x_sb, x_sh, x_st, 1) (GQA resolved in-kernel; dk / dv are
- * summed over the query heads of a group); gL, gQ2, M: (B, Hq, Tq) fp32 contiguous (the
+ * in dtype with strides (x_sb, x_sh, x_st, 1) (GQA resolved in-kernel: query head h
+ * reads KV head h / (Hq / Hkv)); gL, gQ2, M: (B, Hq, Tq) fp32 contiguous (the
  * preamble's per-query cotangents and the forward's natural-log reference max);
  * temp: (Hq, Tq) fp32; n_keys: (Tq,) raw counts (the mask).  Outputs, fp32 contiguous,
- * every element written: dq (B, Hq, Tq, d), dt (B, Hq, Tq) (= sum_j da * sig, the real
- * keys' share of dL/dtemp), dk, dv (B, Hkv, Tk, d).  d = 64 or 128.
+ * every element written when Tk > 0: dq (B, Hq, Tq, d), dt (B, Hq, Tq) (= sum_j da * sig,
+ * the real keys' share of dL/dtemp), dk, dv (B, Hq, Tk, d): each query head's share, so
+ * with Hkv < Hq the caller sums the Hq / Hkv consecutive heads of a group (one workgroup
+ * per query head fills the GPU at causal T = 2,048; a deterministic sum, no atomics).
+ * d = 64 or 128.
  */
+/*
+ * Polar attention backward, per-query preamble (kernel/polar_triton.py:1049-1088) and
+ * parameter-gradient partial sums (:1139-1150).  gc: (B, H, T, d), gm: (B, H, T) in dtype
+ * (nullable: a zero cotangent); S: (B, H, T, d), M, L, Q2: (B, H, T) fp32, the forward's
+ * statistics (M in natural-log units); n_keys: (T,); the five Polar parameters (fp32);
+ * window / preserve_length as in the forward.  Writes gs (B, H, T, d) in dtype, gL, gQ2
+ * (B, H, T) fp32 (the inputs of atma_polar_attention_bwd), temp (H, T) fp32, and per
+ * 16-row block part (B * ceil(T / 16), H, d + 4) fp32: [sum p_null gs | sum dL/da_null nu
+ * log n | sum dL/da_null temp | sum dL/da_null temp sqrt(log(n + 1)) | sum gm (1 - mag^2)
+ * log1p(m_eff)], which the caller sums over blocks.  d = 64 or 128.
+ */
+int atma_polar_attention_bwd_prep(const void* gc, const void* gm, const float* S, const float* M,
+                                  const float* L, const float* Q2, const float* n_keys,
+                                  const float* v_null, const float* null_base,
+                                  const float* null_slope_raw, const float* len_gain_raw,
+                                  const float* mag_beta_raw, void* gs, float* gL, float* gQ2,
+                                  float* temp, float* part, int64_t B, int64_t H, int64_t T,
+                                  int64_t d, int dtype, int64_t window, int preserve_length,
+                                  float eps, void* stream);
+
 int atma_polar_attention_bwd(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                              const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
                              const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,

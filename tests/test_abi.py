@@ -98,6 +98,11 @@ def test_validation_rejects_without_launch(lib):
     assert lib.atma_polar_attention_bwd(*bwd0, 1, 8, 2, 16, 16, 96, 1, 1, 0, null) == 2
     assert lib.atma_polar_attention_bwd(*bwd0, 1, 8, 3, 16, 16, 128, 1, 1, 0, null) == 1
     assert lib.atma_polar_attention_bwd(*bwd0, 1, 8, 2, 0, 0, 128, 1, 1, 0, null) == 0
+    # backward preamble: head dim 96 unsupported; no rows is a no-op; null statistics
+    prep0 = [null] * 17
+    assert lib.atma_polar_attention_bwd_prep(*prep0, 2, 8, 16, 96, 1, 0, 0, 1e-6, null) == 2
+    assert lib.atma_polar_attention_bwd_prep(*prep0, 2, 8, 0, 128, 1, 0, 0, 1e-6, null) == 0
+    assert lib.atma_polar_attention_bwd_prep(*prep0, 2, 8, 16, 128, 1, 0, 0, 1e-6, null) == 1
     # store_kvcache: unknown dtype
     assert lib.atma_store_kvcache(null, 0, null, 0, null, null, null, 1, 256, 8, 9, null) == 1
     # zero-size requests are no-ops
