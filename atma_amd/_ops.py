@@ -141,7 +141,7 @@ def _(gc, gm, S, M, L, Q2, n_keys, v_null, null_base, null_slope_raw, len_gain_r
 def polar_attention_bwd_op(q: Tensor, k: Tensor, v: Tensor, gs: Tensor, gL: Tensor, gQ2: Tensor,
                            M: Tensor, temp: Tensor, n_keys: Tensor, is_causal: bool,
                            window: int) -> List[Tensor]:
-    """The O(T^2) part of the backward: returns fp32 (dq, dt, dk, dv)."""
+    """The O(T^2) part of the backward: returns dq, dk, dv in q's dtype and dt in fp32."""
     _need_cuda(q, k, v, gs, gL, gQ2, M, temp, n_keys)
     lib = _lib.load()
     q, k, v, gs = _rows16(q), _rows16(k), _rows16(v), _rows16(gs)
@@ -163,19 +163,30 @@ def polar_attention_bwd_op(q: Tensor, k: Tensor, v: Tensor, gs: Tensor, gL: Tens
         dq.data_ptr(), dt.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, Hq, Hkv, Tq, Tk, d,
         _lib.dtype_code(q.dtype), 1 if is_causal else 0, window, _lib.stream_handle(q.device))
     _lib.check(rc, "polar_attention_bwd")
-    if Hkv != Hq:   # grouped heads: fixed-order sum of the group's shares
-        dk = dk.view(B, Hkv, Hq // Hkv, Tk, d).sum(2)
-        dv = dv.view(B, Hkv, Hq // Hkv, Tk, d).sum(2)
+    # dq in q's dtype; dk / dv: the group's shares summed (fixed order) into k's dtype
+    if q.dtype != torch.float32:
+        dq = _group_sum(lib, dq, 1, B * Hq * Tq * d, 1, q.dtype)
+    if Hkv != Hq or q.dtype != torch.float32:
+        dk = _group_sum(lib, dk, B * Hkv, Tk * d, Hq // Hkv, q.dtype).view(B, Hkv, Tk, d)
+        dv = _group_sum(lib, dv, B * Hkv, Tk * d, Hq // Hkv, q.dtype).view(B, Hkv, Tk, d)
     return [dq, dt, dk, dv]
+
+
+def _group_sum(lib, part, n_groups, elems, G, dtype):
+    """out[g0] = sum of part's G consecutive (elems,) slices g0 * G .. g0 * G + G - 1, in dtype."""
+    out = torch.empty(n_groups * elems, device=part.device, dtype=dtype)
+    rc = lib.atma_polar_bwd_group_sum(part.data_ptr(), out.data_ptr(), n_groups, G, elems,
+                                      _lib.dtype_code(dtype), _lib.stream_handle(part.device))
+    _lib.check(rc, "polar_bwd_group_sum")
+    return out.view(part.shape) if G == 1 else out
 
 
 @polar_attention_bwd_op.register_fake
 def _(q, k, v, gs, gL, gQ2, M, temp, n_keys, is_causal, window):
     B, Hq, Tq, d = q.shape
     Hkv, Tk = k.shape[1], k.shape[2]
-    f = dict(dtype=torch.float32)
-    return [q.new_empty((B, Hq, Tq, d), **f), q.new_empty((B, Hq, Tq), **f),
-            q.new_empty((B, Hkv, Tk, d), **f), q.new_empty((B, Hkv, Tk, d), **f)]
+    return [q.new_empty((B, Hq, Tq, d)), q.new_empty((B, Hq, Tq), dtype=torch.float32),
+            q.new_empty((B, Hkv, Tk, d)), q.new_empty((B, Hkv, Tk, d))]
 
 
 # --------------------------------------------------------------------------- Polar packed fwd

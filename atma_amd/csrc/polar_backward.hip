@@ -424,83 +424,119 @@ struct PolarPrepArgs {
 template <typename T, int D>
 __global__ void __launch_bounds__(256) polar_bwd_prep_kernel(PolarPrepArgs a) {
   constexpr int E = D / 64;  // elements per lane
+  constexpr int R = 4;       // rows per wave, processed together (independent chains)
   constexpr float kTiny = 1.0e-30f;
   __shared__ float s_vn[4][D];
   __shared__ float s_sc[4][4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
-  const float sp_lg = softplus(a.len_gain_raw[h]), sp_ns = softplus(a.null_slope_raw[h]);
-  const float beta = softplus(a.mag_beta_raw[h]), nb = a.null_base[h];
-  float vn[E], vnull[E];
+  const int t0 = blockIdx.x * 16 + wave * R;
+  // The per-row scalar chain (log, exp, log1p, tanh, divisions) runs once per row: lane
+  // i < R computes row t0 + i, and the results are read back with shuffles.
+  const int my = lane & (R - 1);
+  const bool my_ok = t0 + my < a.T;
+  const int64_t my_row = (int64_t)bh * a.T + (my_ok ? t0 + my : 0);
+  float n = a.n_keys[my_ok ? t0 + my : 0];
+  if (a.window > 0 && !a.preserve_length) n = fminf(n, (float)a.window);
+  n = fmaxf(n, 1.f);
+  const float logn = logf(n), root = sqrtf(logf(n + 1.f));
+  const float temp = 1.f + softplus(a.len_gain_raw[h]) * logn;
+  const float nu = a.null_base[h] + softplus(a.null_slope_raw[h]) * root;
+  const float p_null = my_ok ? expf(temp * nu - a.M[my_row]) : 0.f;
+  const float Lr = my_ok ? a.L[my_row] : 0.f, Q2r = my_ok ? a.Q2[my_row] : 0.f;
+  const float gmr = (my_ok && a.gm) ? to_f32(((const T*)a.gm)[my_row]) : 0.f;
+
+  bool ok[R];
+  int64_t row[R];
+  float sv[R][E], gv[R][E], vnull[E];
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    vn[e] = 0.f;
-    vnull[e] = a.v_null[(int64_t)h * D + 64 * e + lane];
+  for (int e = 0; e < E; ++e) vnull[e] = a.v_null[(int64_t)h * D + 64 * e + lane];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    ok[i] = t0 + i < a.T;
+    row[i] = (int64_t)bh * a.T + (ok[i] ? t0 + i : 0);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      sv[i][e] = ok[i] ? a.S[row[i] * D + 64 * e + lane] : 0.f;
+      gv[i][e] = (ok[i] && a.gc) ? to_f32(((const T*)a.gc)[row[i] * D + 64 * e + lane]) : 0.f;
+    }
   }
-  float acc1 = 0.f, acc2 = 0.f, acc3 = 0.f, acc4 = 0.f;
-  for (int i = 0; i < 4; ++i) {
-    const int t = blockIdx.x * 16 + wave * 4 + i;
-    if (t >= a.T) break;  // uniform per wave
-    const int64_t row = (int64_t)bh * a.T + t;
-    float n = a.n_keys[t];
-    if (a.window > 0 && !a.preserve_length) n = fminf(n, (float)a.window);
-    n = fmaxf(n, 1.f);
-    const float logn = logf(n), root = sqrtf(logf(n + 1.f));
-    const float temp = 1.f + sp_lg * logn, nu = nb + sp_ns * root;
-    const float Lr = a.L[row], Q2r = a.Q2[row];
-    const float p_null = expf(temp * nu - a.M[row]);
-    const float Z = Lr + p_null;
-    const float Zc = fmaxf(Z, kTiny), Q2c = fmaxf(Q2r, kTiny);
-    const float me = (Lr * Lr / Q2c) * (Lr / Zc);
-    const float lm = log1pf(me);
-    const float mag = tanhf(beta * lm);
-    const float gmr = a.gm ? to_f32(((const T*)a.gm)[row]) : 0.f;
-    const float gme = gmr * beta * (1.f - mag * mag) / (1.f + me);
-    const float dme_dL = Lr > 0.f ? 3.f * me / Lr : 0.f;
-    const float dme_dQ2 = Q2r > kTiny ? -me / Q2c : 0.f;
-    const float dme_dZ = Z > kTiny ? -me / Zc : 0.f;
-    // direction path
-    float sv[E], gv[E];
-    float ss = 0.f;
+  float ss[R], gcs[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    ss[i] = 0.f;
+    gcs[i] = 0.f;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      sv[e] = a.S[row * D + 64 * e + lane];
-      gv[e] = a.gc ? to_f32(((const T*)a.gc)[row * D + 64 * e + lane]) : 0.f;
-      ss = fmaf(sv[e], sv[e], ss);
+      ss[i] = fmaf(sv[i][e], sv[i][e], ss[i]);
+      gcs[i] = fmaf(gv[i][e], sv[i][e], gcs[i]);
     }
-    const float snorm = fmaxf(sqrtf(wave_sum(ss)), a.eps);
-    const float inv = 1.f / snorm;
-    float gcc = 0.f;
+  }
 #pragma unroll
-    for (int e = 0; e < E; ++e) gcc = fmaf(gv[e], sv[e] * inv, gcc);
-    gcc = wave_sum(gcc);
-    float gsv = 0.f;
+  for (int i = 0; i < R; ++i) {
+    ss[i] = wave_sum(ss[i]);
+    gcs[i] = wave_sum(gcs[i]);
+  }
+  float vn[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) vn[e] = 0.f;
+  float gsv[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const float pn = __shfl(p_null, i, 64);
+    // gs = (gc - (gc.c) c) / |s|  with c = s / |s|:  (gc - (gc.s / |s|) s / |s|) / |s|
+    const float inv = 1.f / fmaxf(sqrtf(ss[i]), a.eps);
+    const float gcc = gcs[i] * inv;
+    gsv[i] = 0.f;
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      const float g = (gv[e] - gcc * (sv[e] * inv)) * inv;
-      ((T*)a.gs)[row * D + 64 * e + lane] = from_f32<T>(g);
-      gsv = fmaf(g, vnull[e], gsv);
-      vn[e] = fmaf(p_null, g, vn[e]);
+      const float g = (gv[i][e] - gcc * (sv[i][e] * inv)) * inv;
+      if (ok[i]) ((T*)a.gs)[row[i] * D + 64 * e + lane] = from_f32<T>(g);
+      gsv[i] = fmaf(g, vnull[e], gsv[i]);
+      vn[e] = fmaf(pn, g, vn[e]);
     }
-    gsv = wave_sum(gsv);
-    const float g_anull = (gsv + gme * dme_dZ) * p_null;
-    if (lane == 0) {
-      a.gL[row] = gme * (dme_dL + dme_dZ);
-      a.gQ2[row] = gme * dme_dQ2;
-      if (b == 0) a.temp[(int64_t)h * a.T + t] = temp;
-    }
-    acc1 = fmaf(g_anull * nu, logn, acc1);
-    acc2 = fmaf(g_anull, temp, acc2);
-    acc3 = fmaf(g_anull * temp, root, acc3);
-    acc4 = fmaf(gmr * (1.f - mag * mag), lm, acc4);
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i) gsv[i] = wave_sum(gsv[i]);
+  // lane my: the rest of row t0 + my's chain
+  float my_gsv = gsv[0];
+#pragma unroll
+  for (int i = 1; i < R; ++i) my_gsv = my == i ? gsv[i] : my_gsv;
+  const float beta = softplus(a.mag_beta_raw[h]);
+  const float Z = Lr + p_null;
+  const float Zc = fmaxf(Z, kTiny), Q2c = fmaxf(Q2r, kTiny);
+  const float me = (Lr * Lr / Q2c) * (Lr / Zc);
+  const float lm = log1pf(me);
+  const float mag = tanhf(beta * lm);
+  const float gme = gmr * beta * (1.f - mag * mag) / (1.f + me);
+  const float dme_dL = Lr > 0.f ? 3.f * me / Lr : 0.f;
+  const float dme_dQ2 = Q2r > kTiny ? -me / Q2c : 0.f;
+  const float dme_dZ = Z > kTiny ? -me / Zc : 0.f;
+  const float g_anull = (my_gsv + gme * dme_dZ) * p_null;
+  const bool lead = lane < R && my_ok;
+  if (lead) {
+    a.gL[my_row] = gme * (dme_dL + dme_dZ);
+    a.gQ2[my_row] = gme * dme_dQ2;
+    if (b == 0) a.temp[(int64_t)h * a.T + t0 + my] = temp;
+  }
+  float t1 = lead ? g_anull * nu * logn : 0.f;
+  float t2 = lead ? g_anull * temp : 0.f;
+  float t3 = lead ? g_anull * temp * root : 0.f;
+  float t4 = lead ? gmr * (1.f - mag * mag) * lm : 0.f;
+#pragma unroll
+  for (int m = 1; m < R; m <<= 1) {  // sum over the R leading lanes
+    t1 += __shfl_xor(t1, m, 64);
+    t2 += __shfl_xor(t2, m, 64);
+    t3 += __shfl_xor(t3, m, 64);
+    t4 += __shfl_xor(t4, m, 64);
   }
 #pragma unroll
   for (int e = 0; e < E; ++e) s_vn[wave][64 * e + lane] = vn[e];
   if (lane == 0) {
-    s_sc[wave][0] = acc1;
-    s_sc[wave][1] = acc2;
-    s_sc[wave][2] = acc3;
-    s_sc[wave][3] = acc4;
+    s_sc[wave][0] = t1;
+    s_sc[wave][1] = t2;
+    s_sc[wave][2] = t3;
+    s_sc[wave][3] = t4;
   }
   __syncthreads();
   float* rec = a.part + ((int64_t)(b * gridDim.x + blockIdx.x) * a.H + h) * (D + 4);
@@ -509,6 +545,26 @@ __global__ void __launch_bounds__(256) polar_bwd_prep_kernel(PolarPrepArgs a) {
     const int j = tid - D;
     rec[D + j] = s_sc[0][j] + s_sc[1][j] + s_sc[2][j] + s_sc[3][j];
   }
+}
+
+// Sum of the G consecutive query heads' shares of dk / dv (or, with G = 1, a copy) into
+// the output dtype: out[b, hk, r] = sum_g part[b, hk G + g, r], r over Tk * D elements,
+// four per thread.
+template <typename T>
+__global__ void __launch_bounds__(256) polar_bwd_group_sum_kernel(const float* __restrict__ part, T* __restrict__ out,
+                                                                   int64_t rows4, int G) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // float4 index within (b, hk)
+  if (i >= rows4) return;
+  const int64_t bhk = blockIdx.y;
+  const f32x4* src = (const f32x4*)part + bhk * G * rows4 + i;
+  f32x4 acc = src[0];
+  for (int g = 1; g < G; ++g) {
+    const f32x4 x = src[(int64_t)g * rows4];
+    acc = f32x4{acc[0] + x[0], acc[1] + x[1], acc[2] + x[2], acc[3] + x[3]};
+  }
+  T* o = out + (bhk * rows4 + i) * 4;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = from_f32<T>(acc[e]);
 }
 
 template <typename T, int D>
@@ -602,4 +658,26 @@ extern "C" int atma_polar_attention_bwd_prep(
     case ATMA_F16: return d == 128 ? launch_prep<f16, 128>(a, s) : launch_prep<f16, 64>(a, s);
     default: return d == 128 ? launch_prep<float, 128>(a, s) : launch_prep<float, 64>(a, s);
   }
+}
+
+extern "C" int atma_polar_bwd_group_sum(const float* part, void* out, int64_t n_groups, int64_t G,
+                                        int64_t elems, int dtype, void* stream) {
+  using namespace atma;
+  if (n_groups < 0 || G <= 0 || elems < 0 || elems % 4)
+    return set_error(ATMA_ERR_INVALID, "polar_bwd_group_sum: bad sizes (elems %% 4 == 0)");
+  if (n_groups == 0 || elems == 0) return ATMA_OK;
+  if (n_groups > 65535 || elems / 4 > 0x7fffffffll * 256)
+    return set_error(ATMA_ERR_INVALID, "polar_bwd_group_sum: sizes too large");
+  if (!part || !out || (uintptr_t)part % 16)
+    return set_error(ATMA_ERR_INVALID, "polar_bwd_group_sum: null or misaligned pointer");
+  const int64_t rows4 = elems / 4;
+  const dim3 grid((unsigned)((rows4 + 255) / 256), (unsigned)n_groups);
+  hipStream_t s = (hipStream_t)stream;
+  switch (dtype) {
+    case ATMA_BF16: polar_bwd_group_sum_kernel<bf16><<<grid, dim3(256), 0, s>>>(part, (bf16*)out, rows4, (int)G); break;
+    case ATMA_F16: polar_bwd_group_sum_kernel<f16><<<grid, dim3(256), 0, s>>>(part, (f16*)out, rows4, (int)G); break;
+    case ATMA_F32: polar_bwd_group_sum_kernel<float><<<grid, dim3(256), 0, s>>>(part, (float*)out, rows4, (int)G); break;
+    default: return set_error(ATMA_ERR_INVALID, "polar_bwd_group_sum: unknown dtype %d", dtype);
+  }
+  return check_launch("polar_bwd_group_sum");
 }

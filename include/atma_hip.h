@@ -150,6 +150,17 @@ int atma_polar_attention_bwd_prep(const void* gc, const void* gm, const float* S
                                   int64_t d, int dtype, int64_t window, int preserve_length,
                                   float eps, void* stream);
 
+/*
+ * Final step of the backward's dk / dv (and the dtype cast of dq), no reference
+ * counterpart (the reference's loops write per-KV-head fp32 gradients that autograd casts):
+ * out[g0, r] = sum_{g < G} part[g0 * G + g, r] in dtype, for n_groups groups of G
+ * consecutive slices of `elems` fp32 elements (elems % 4 == 0; part 16-byte aligned).
+ * With the (B, Hq, Tk, d) shares of atma_polar_attention_bwd: n_groups = B * Hkv,
+ * G = Hq / Hkv, elems = Tk * d.  A fixed-order sum: deterministic.
+ */
+int atma_polar_bwd_group_sum(const float* part, void* out, int64_t n_groups, int64_t G,
+                             int64_t elems, int dtype, void* stream);
+
 int atma_polar_attention_bwd(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                              const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
                              const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
