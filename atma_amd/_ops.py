@@ -309,6 +309,65 @@ def _(x, weight, slots, state_table, residual):
     return torch.empty_like(x)
 
 
+# --------------------------------------------------------------------------- inference fusions
+@torch.library.custom_op("atma_hip::squared_relu_gate", mutates_args=())
+def squared_relu_gate_op(x: Tensor, gate: Tensor) -> Tensor:
+    _need_cuda(x, gate)
+    lib = _lib.load()
+    rows, width = x.shape
+    out = torch.empty((rows, width), device=x.device, dtype=x.dtype)
+    rc = lib.atma_squared_relu_gate(x.data_ptr(), x.stride(0), x.stride(1), gate.data_ptr(), gate.stride(0),
+                                    gate.stride(1), out.data_ptr(), rows, width, _lib.dtype_code(x.dtype),
+                                    _lib.stream_handle(x.device))
+    _lib.check(rc, "squared_relu_gate")
+    return out
+
+
+@squared_relu_gate_op.register_fake
+def _(x, gate):
+    return x.new_empty(x.shape)
+
+
+@torch.library.custom_op("atma_hip::softcap_logits", mutates_args=())
+def softcap_logits_op(logits: Tensor) -> Tensor:
+    _need_cuda(logits)
+    lib = _lib.load()
+    logits = logits.contiguous()
+    out = torch.empty_like(logits)
+    rc = lib.atma_softcap_logits(logits.data_ptr(), out.data_ptr(), logits.numel(),
+                                 _lib.dtype_code(logits.dtype), _lib.stream_handle(logits.device))
+    _lib.check(rc, "softcap_logits")
+    return out
+
+
+@softcap_logits_op.register_fake
+def _(logits):
+    return torch.empty_like(logits)
+
+
+@torch.library.custom_op("atma_hip::packed_causal_conv1d", mutates_args=("state_table",))
+def packed_causal_conv1d_op(x: Tensor, weight: Tensor, state_table: Tensor, token_seq_starts: Tensor,
+                            token_seq_ends: Tensor, token_seq_slots: Tensor) -> Tensor:
+    _need_cuda(x, weight, state_table, token_seq_starts, token_seq_ends, token_seq_slots)
+    lib = _lib.load()
+    total, channels = x.shape
+    K = weight.shape[1]
+    out = torch.empty((total, channels), device=x.device, dtype=x.dtype)
+    ss = state_table.stride()
+    rc = lib.atma_packed_causal_conv1d(
+        x.data_ptr(), x.stride(0), x.stride(1), weight.data_ptr(), weight.stride(0), weight.stride(1),
+        out.data_ptr(), state_table.data_ptr(), ss[0], ss[1], ss[2], state_table.shape[0],
+        token_seq_starts.data_ptr(), token_seq_ends.data_ptr(), token_seq_slots.data_ptr(), total, channels, K,
+        _lib.dtype_code(x.dtype), _lib.dtype_code(state_table.dtype), _lib.stream_handle(x.device))
+    _lib.check(rc, "packed_causal_conv1d")
+    return out
+
+
+@packed_causal_conv1d_op.register_fake
+def _(x, weight, state_table, token_seq_starts, token_seq_ends, token_seq_slots):
+    return x.new_empty(x.shape)
+
+
 # --------------------------------------------------------------------------- memory gates
 @torch.library.custom_op("atma_hip::gated_delta_gates", mutates_args=())
 def gated_delta_gates_op(zg: Tensor, zb: Tensor, g_bias: float, b_bias: float,

@@ -10,6 +10,7 @@ import torch
 
 from .. import _lib
 from .conv import causal_conv1d_decode_step
+from .inference_ops import packed_causal_conv1d, softcap_logits, squared_relu_gate
 from .gated_delta import (StartSignal, chunk_gated_delta_rule, gated_delta_decode_step, gated_delta_gates,
                           recurrence_pays_to_overlap)
 from .polar import polar_attention_decode, polar_attention_fwd, polar_attention_packed_fwd
@@ -29,4 +30,7 @@ __all__ = [
     "chunk_gated_delta_rule",
     "gated_delta_gates",
     "causal_conv1d_decode_step",
+    "squared_relu_gate",
+    "softcap_logits",
+    "packed_causal_conv1d",
 ]

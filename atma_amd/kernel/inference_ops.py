@@ -1,0 +1,59 @@
+"""Forward-only fusions of the paged inference model, backed by libatma_hip.so.
+
+Mirrors ``kernel/inference_ops_triton.py`` of the reference (same names, arguments and
+errors): ``squared_relu_gate`` (:123-135, the MLP activation of
+``inference/models/atma.py:87-96``), ``softcap_logits`` (:214-223, the output soft cap of
+``inference/models/atma.py:750-754``) and ``packed_causal_conv1d`` (:138-160, the grouped
+fresh prefill's depthwise convolutions, ``inference/models/atma.py:431-442, 648-652``).
+The prototype ``linear_head_rms`` (:163-189) is not part of the served path and is not
+provided.
+"""
+
+import torch
+
+from .. import _ops  # noqa: F401  (registers torch.ops.atma_hip.*)
+
+
+@torch.no_grad()
+def squared_relu_gate(x, gate):
+    """Fused gate * relu(x)^2, preserving eager BF16's intermediate rounding.
+
+    x, gate: (rows, width) (strided views such as the two halves of one fc output are
+    read in place).  Returns a contiguous (rows, width) tensor in x's dtype."""
+    if x.dim() != 2 or gate.shape != x.shape:
+        raise ValueError("expected x and gate of the same [rows, width] shape")
+    if gate.dtype != x.dtype:
+        raise ValueError("x and gate must share a dtype")
+    return torch.ops.atma_hip.squared_relu_gate(x, gate)
+
+
+@torch.no_grad()
+def softcap_logits(logits):
+    """Fuse the elementwise 15*x/sqrt(x^2+225) output soft cap (any shape, logits' dtype)."""
+    return torch.ops.atma_hip.softcap_logits(logits)
+
+
+@torch.no_grad()
+def packed_causal_conv1d(x, weight, state_table, token_seq_starts, token_seq_ends, token_seq_slots):
+    """Fresh causal depthwise convolution over packed variable-length sequences.
+
+    x: (tokens, channels); weight: (channels, kernel) with kernel 3 or 4 (ATMA's sizes);
+    state_table: (slots, channels, kernel - 1), updated IN PLACE with each sequence's last
+    kernel - 1 inputs; token_seq_starts / ends / slots: (tokens,) int32 per-token maps.
+    Returns the convolution (tokens, channels) in x's dtype."""
+    if not x.is_cuda:
+        raise RuntimeError("packed_causal_conv1d requires a GPU (HIP)")
+    if x.ndim != 2 or weight.ndim != 2 or weight.shape[0] != x.shape[1]:
+        raise ValueError("expected x [tokens, channels], weight [channels, kernel]")
+    kernel_size = weight.shape[1]
+    if kernel_size not in (3, 4):
+        raise ValueError("packed convolution supports ATMA kernel sizes 3 and 4")
+    if state_table.dim() != 3 or state_table.shape[1:] != (x.shape[1], kernel_size - 1):
+        raise ValueError(f"state_table {tuple(state_table.shape)} must be (slots, {x.shape[1]}, "
+                         f"{kernel_size - 1})")
+    maps = [t.to(device=x.device, dtype=torch.int32).reshape(-1).contiguous()
+            for t in (token_seq_starts, token_seq_ends, token_seq_slots)]
+    if any(m.numel() != x.shape[0] for m in maps):
+        raise ValueError("token maps must have one entry per token")
+    weight = weight.to(dtype=x.dtype)
+    return torch.ops.atma_hip.packed_causal_conv1d(x, weight, state_table, *maps)

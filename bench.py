@@ -190,12 +190,22 @@ class Decode:
         self.p = _params(torch, dev, seed)
         self.B, self.pages = B, pool
         self.ctx_sum = int(ctx.sum())
+        self.side = torch.cuda.Stream(device=dev)  # default priority
         self.graph = None
 
     def step(self):
+        """The layer's decode schedule: the memory step (independent of attention) on a
+        forked stream, store_kvcache then the paged attention on the main stream; a
+        captured graph holds the two as parallel branches."""
+        torch = self.torch
+        main = torch.cuda.current_stream()
+        self.side.wait_stream(main)
+        with torch.cuda.stream(self.side):
+            r = self.step_mem(self.q, self.knew, self.vnew, self.gamma, self.beta, self.table, self.slots)
         self.store(self.knew, self.vnew, self.kc, self.vc, self.slot_map)
         c, mag = self.dec(self.q, self.kc, self.vc, self.bt, self.ctx, **self.p)
-        r = self.step_mem(self.q, self.knew, self.vnew, self.gamma, self.beta, self.table, self.slots)
+        main.wait_stream(self.side)
+        r.record_stream(main)
         return c, mag, r
 
     def attention(self):

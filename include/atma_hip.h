@@ -233,6 +233,46 @@ int atma_causal_conv1d_decode_step(const void* x, int64_t x_sb, const void* weig
                                    int residual, int dtype, void* stream);
 
 /*
+ * Fused MLP activation out = gate * relu(x)^2.  Replaces squared_relu_gate
+ * (kernel/inference_ops_triton.py:102-135), called by InferenceMLP.forward
+ * (inference/models/atma.py:87-96).  x, gate: (rows, width) with strides (x_s0, x_s1),
+ * (g_s0, g_s1) -- typically the two halves of one fc output; out: (rows, width)
+ * contiguous, same dtype.  bf16 inputs round relu(x)^2 to bf16 before the gate multiply
+ * (eager bf16's intermediate rounding); the product is computed in fp32 and rounded once.
+ */
+int atma_squared_relu_gate(const void* x, int64_t x_s0, int64_t x_s1, const void* gate, int64_t g_s0,
+                           int64_t g_s1, void* out, int64_t rows, int64_t width, int dtype, void* stream);
+
+/*
+ * Output soft cap out = 15 x / sqrt(x^2 + 225) over n contiguous elements.  Replaces
+ * softcap_logits (kernel/inference_ops_triton.py:194-223), called by compute_logits
+ * (inference/models/atma.py:750-754).  For bf16, 15 x, x^2, x^2 + 225 and the reciprocal
+ * square root (the correctly rounded 1 / sqrt) are each rounded to bf16 before the final
+ * product; fp32 / fp16 round only the output.
+ */
+int atma_softcap_logits(const void* logits, void* out, int64_t n, int dtype, void* stream);
+
+/*
+ * Depthwise causal convolution over packed variable-length sequences.  Replaces
+ * packed_causal_conv1d (kernel/inference_ops_triton.py:17-63, 138-160), called by the
+ * grouped fresh prefill (inference/models/atma.py:431-442, 648-652).
+ * x: (total, channels) strides (x_st, x_sc); weight: (channels, K) strides (w_sc, w_sk),
+ * x's dtype; out: (total, channels) contiguous, x's dtype:
+ *   out[t, c] = sum_{j < K} [t - (K-1-j) >= token_seq_starts[t]] x[t - (K-1-j), c] w[c, j]
+ * accumulated in fp32 (fused multiply-add in tap order).  token_seq_starts / ends / slots:
+ * (total,) int32, the packed start, end and state-table row of each token's sequence.
+ * The last token of each sequence (t == ends[t] - 1) writes state_table[slot, c, j] =
+ * x[ends - (K-1) + j, c] for j < K - 1 (0 before the sequence's start), in state_dtype;
+ * state_table: (num_slots, channels, K - 1) strides (s_ss, s_sc, s_sk).  A slot outside
+ * [0, num_slots) writes nothing.  2 <= K <= 8.
+ */
+int atma_packed_causal_conv1d(const void* x, int64_t x_st, int64_t x_sc, const void* weight, int64_t w_sc,
+                              int64_t w_sk, void* out, void* state_table, int64_t s_ss, int64_t s_sc,
+                              int64_t s_sk, int64_t num_slots, const int32_t* token_seq_starts,
+                              const int32_t* token_seq_ends, const int32_t* token_seq_slots, int64_t total,
+                              int64_t channels, int64_t K, int dtype, int state_dtype, void* stream);
+
+/*
  * Gate activations of the memory branch in one launch.  Replaces the torch
  * add / logsigmoid / sigmoid of TitansMemory (model/blocks.py:426-490,
  * inference/models/atma.py:305-375): g = logsigmoid(zg + g_bias) -- the log-decay

@@ -10,7 +10,9 @@ algorithm of the four hot-path operations the HIP library implements:
   ``chunk_gated_delta_rule`` contract and the single-token decode step --
   ``oracle.gated_delta``;
 * the paged KV write ``store_kvcache`` -- ``oracle.kvcache``;
-* one global block (Polar + memory + MLP) for the CPU baseline -- ``oracle.block``.
+* one global block (Polar + memory + MLP) for the CPU baseline -- ``oracle.block``;
+* the inference fusions (``squared_relu_gate``, ``softcap_logits``,
+  ``packed_causal_conv1d``) -- ``oracle.inference_ops``.
 
 Every function cites the reference file:line it follows (paths relative to the
 akbar2habibullah/atma repository root).
