@@ -35,6 +35,7 @@ from torch import nn
 from ..kernel import (StartSignal, causal_conv1d_decode_step, chunk_gated_delta_rule,
                       gated_delta_decode_step, gated_delta_gates, polar_attention_decode,
                       polar_attention_fwd, recurrence_pays_to_overlap)
+from ..kernel.inference_ops import squared_relu_gate
 from .attention import store_kvcache
 
 # Polar structural priors (model/reference.py:17-20)
@@ -183,13 +184,18 @@ class PolarAttention(nn.Module):
         return F.rms_norm(q, (dk,)), gate.reshape(*lead, H * dk), F.rms_norm(k, (dk,)), v
 
     @staticmethod
-    def _conv_prefill(t, conv, tails=None, slots=None):
+    def _conv_prefill(t, conv, tails=None, slots=None, continuing=False):
         """Residual causal depthwise conv over (B, T, C); optionally stores the last K-1
-        inputs per sequence (``prefill_causal_conv1d_dense``, ``inference/models/atma.py:148-162``)."""
+        inputs per sequence (``prefill_causal_conv1d_dense``, ``inference/models/atma.py:148-162``).
+        ``continuing``: the left context is the stored tail of each sequence instead of
+        zeros (a chunked-prefill continuation, ``inference/models/atma.py:128-130``)."""
         w = conv.weight
         K = w.shape[-1]
         x_in = t.transpose(1, 2)
-        padded = F.pad(x_in, (K - 1, 0))
+        if continuing:
+            padded = torch.cat([tails[slots].to(t.dtype), x_in], dim=2)
+        else:
+            padded = F.pad(x_in, (K - 1, 0))
         out = F.conv1d(padded, w.to(t.dtype), groups=x_in.shape[1])
         if tails is not None:
             tails[slots] = padded[:, :, padded.shape[2] - (K - 1):].to(tails.dtype)
@@ -300,6 +306,51 @@ class PolarAttention(nn.Module):
 
         return self._attend_prefill(x, q, gate, k, v, S0, sink)
 
+    def prefill_continue(self, x, cache: GlobalLayerCache, slots, slot_mapping, block_tables, cached):
+        """Chunked-prefill continuation of B sequences by T tokens each
+        (``inference/models/atma.py:509-544``): the Canon convs continue from the stored
+        tails, the chunk's K/V go to the pages, each sequence attends over its gathered
+        prefix plus the chunk with ``is_causal=False`` and absolute ``n_keys =
+        cached + 1 .. cached + T``, and the memory continues from its table state.
+
+        x: (B, T, dim); slots: (B,) int64 table rows; slot_mapping: (B*T,) int32 cache slots
+        of the chunk; block_tables: (B, max_pages) int32; cached: B ints (tokens already in
+        the pages; 0 makes that sequence a fresh prefill)."""
+        B, T, _ = x.shape
+        H, Hkv, dk = self.num_heads, self.num_kv_heads, self.head_dim
+        cached = [int(c) for c in cached]
+        q, gate, k, v = self._project(x)
+        q = self._conv_prefill(q.reshape(B, T, H * dk), self.canon_q, cache.conv_q, slots, True).view(B, T, H, dk)
+        k = self._conv_prefill(k.reshape(B, T, Hkv * dk), self.canon_k, cache.conv_k, slots, True).view(
+            B, T, Hkv, dk)
+        v = self._conv_prefill(v.reshape(B, T, Hkv * dk), self.canon_v, cache.conv_v, slots, True).view(
+            B, T, Hkv, dk)
+        store_kvcache(k.reshape(B * T, Hkv, dk), v.reshape(B * T, Hkv, dk), cache.k_cache, cache.v_cache,
+                      slot_mapping)
+        page = cache.k_cache.shape[1]
+        cs, ms = [], []
+        for b in range(B):
+            n = cached[b]
+            if n > 0:
+                pages = block_tables[b, :(n + page - 1) // page].long()
+                kp = cache.k_cache[pages].reshape(-1, Hkv, dk)[:n]
+                vp = cache.v_cache[pages].reshape(-1, Hkv, dk)[:n]
+                kb, vb = torch.cat([kp, k[b]], 0), torch.cat([vp, v[b]], 0)
+            else:
+                kb, vb = k[b], v[b]
+            n_keys = torch.arange(n + 1, n + T + 1, device=x.device, dtype=torch.float32)
+            c, mag = polar_attention_fwd(q[b].transpose(0, 1).unsqueeze(0), kb.transpose(0, 1).unsqueeze(0),
+                                         vb.transpose(0, 1).unsqueeze(0), n_keys, is_causal=n == 0,
+                                         window=self.window, **self.polar_params())
+            cs.append(c[0].transpose(0, 1))
+            ms.append(mag[0].transpose(0, 1))
+        out = self._combine(torch.stack(cs), torch.stack(ms), gate)
+        if self.mem is not None:
+            r, S = self.mem(x, q, k, v, initial_state=cache.mem_table[slots], output_final_state=True)
+            cache.mem_table[slots] = S
+            out = out + r
+        return out
+
     def decode(self, x, cache: GlobalLayerCache, slots, block_tables, context_lens, slot_mapping):
         """One token per sequence (``inference/models/atma.py:546-618``).
 
@@ -358,6 +409,12 @@ class MLP(nn.Module):
 
     def forward(self, x):
         a, gate = torch.chunk(self.fc(x), 2, dim=-1)
+        if x.is_cuda and not torch.is_grad_enabled():
+            # InferenceMLP (inference/models/atma.py:87-96): the fused HIP activation,
+            # equal to the eager form bit for bit (bf16 rounds the square as eager does)
+            lead = a.shape[:-1]
+            h = squared_relu_gate(a.reshape(-1, a.shape[-1]), gate.reshape(-1, gate.shape[-1]))
+            return self.proj(h.view(*lead, -1))
         return self.proj(gate * a.relu().square())
 
 

@@ -15,7 +15,7 @@ configs[3] (paged decode step: 64 sequences, ctx ~ U[1024, 32768], 256-token pag
 a shuffled pool, store_kvcache + Polar decode + gated-delta step, replayed as a HIP
 graph), each with its roofline fraction, plus the CPU oracle timed on this host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4|ops] [--no-cpu]
 """
 
 import argparse
@@ -254,6 +254,40 @@ def bench_decode(torch, dev, steps, warmup, full=False):
     return res
 
 
+def bench_inference_ops(torch, dev, steps, warmup):
+    """The inference fusions at configs[4] shapes (hidden 1024, MLP 4x, vocab 50,304,
+    32 prompts x 2,048 tokens), bf16, each as achieved HBM GB/s of its compulsory bytes:
+    squared_relu_gate over one prefill step's MLP activations (65,536 x 4,096: read x and
+    gate, write out), softcap_logits over one decode step's logits (32 x 50,304 read +
+    written), packed_causal_conv1d over the packed prefill's q projection (65,536 tokens x
+    1,024 channels, K = 4: read x, write out)."""
+    from atma_amd.kernel import packed_causal_conv1d, softcap_logits, squared_relu_gate
+    g = torch.Generator(device=dev).manual_seed(0)
+    bf = torch.bfloat16
+    res = {}
+    fc = torch.randn(65536, 8192, device=dev, generator=g, dtype=bf)
+    a, gate = fc.chunk(2, dim=-1)
+    ms = _time(torch, lambda: squared_relu_gate(a, gate), steps, warmup)
+    res["squared_relu_gate"] = dict(shape=[65536, 4096], ms=ms, gbs=3 * a.numel() * 2 / (ms * 1e-3) / 1e9)
+    del fc, a, gate
+    logits = torch.randn(32, 50304, device=dev, generator=g, dtype=bf)
+    ms = _time(torch, lambda: softcap_logits(logits), steps, warmup)
+    res["softcap_logits"] = dict(shape=[32, 50304], ms=ms, gbs=2 * logits.numel() * 2 / (ms * 1e-3) / 1e9)
+    T, C, S = 65536, 1024, 32
+    x = torch.randn(T, C, device=dev, generator=g, dtype=bf)
+    w = torch.randn(C, 4, device=dev, generator=g, dtype=bf)
+    table = torch.zeros(S, C, 3, device=dev, dtype=bf)
+    seq = torch.arange(T, device=dev, dtype=torch.int32) // (T // S)
+    starts, ends = seq * (T // S), (seq + 1) * (T // S)
+    ms = _time(torch, lambda: packed_causal_conv1d(x, w, table, starts, ends, seq), steps, warmup)
+    res["packed_causal_conv1d"] = dict(shape=[T, C], ms=ms, gbs=(2 * x.numel() * 2 + 3 * T * 4) / (ms * 1e-3) / 1e9)
+    for r in res.values():
+        r["hbm_frac"] = r["gbs"] / PEAK_HBM_GBS
+    del x, table
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(torch):
     """The CPU oracle (oracle/: Polar streaming form + gated-delta chunked UT form, fp32)
     on a bounded sample of configs[1]: one of the 8 sequences, full T = 2048, all heads."""
@@ -326,7 +360,7 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "ops", "copy"], default=None,
                     help="one workload; 'copy' runs a plain 512 MiB device copy, the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--no-cpu", action="store_true")
@@ -365,6 +399,10 @@ def main(argv=None):
         c4w = bench_decode(torch, dev, max(5, args.steps // 2), 2, full=True)
         print(f"# c4 decode 64x32768: {json.dumps(c4w)}", file=sys.stderr, flush=True)
         out["c4"] = [c4, c4w]
+    if args.only in (None, "ops"):
+        ops = bench_inference_ops(torch, dev, args.steps, args.warmup)
+        print(f"# inference ops: {json.dumps(ops)}", file=sys.stderr, flush=True)
+        out["ops"] = ops
     if args.only is not None:
         print(json.dumps(out))
         return 0
@@ -395,6 +433,8 @@ def main(argv=None):
                          for r in out["c3"]],
         "decode": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
                    for r in out["c4"]],
+        "inference_ops": {n: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
+                          for n, r in out["ops"].items()},
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch)

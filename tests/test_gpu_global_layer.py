@@ -40,12 +40,15 @@ def test_mixer_fp32_vs_oracle(dev, window):
     assert max_abs(out, ref) <= 1e-4, max_abs(out, ref)
 
 
-def test_block_fp32_vs_oracle(dev):
+@pytest.mark.parametrize("grad", [True, False])
+def test_block_fp32_vs_oracle(dev, grad):
+    """With grad off the MLP runs the fused squared_relu_gate kernel (InferenceMLP)."""
     blk = _block()
     x = torch.randn(1, 200, DIM, generator=torch.Generator().manual_seed(2))
     sd = {k: v.detach().cpu().clone() for k, v in blk.state_dict().items()}
     ref = OB.global_block(sd, x, H=H, Hkv=HKV, dk=DK)
-    out = blk.to(dev)(x.to(dev))
+    with torch.set_grad_enabled(grad):
+        out = blk.to(dev)(x.to(dev))
     assert max_abs(out, ref) <= 1e-4, max_abs(out, ref)
 
 
@@ -100,3 +103,41 @@ def test_prefill_then_decode_equals_full_forward(dev, dtype, tol):
         y = attn.decode(x[:, pos], cache, slots, bt, ctx, smap1)
         err = max_abs(y, full[:, pos]) if dtype == torch.float32 else rel_err(y.float(), full[:, pos].float())
         assert err <= tol, (i, err)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+def test_chunked_prefill_continuation_equals_full_forward(dev, dtype, tol):
+    """Fresh prefill of T0 tokens, two continuation chunks (gathered paged prefix +
+    chunk with is_causal=False and absolute n_keys, conv tails as left context, memory
+    from the table state; inference/models/atma.py:509-544), then a decode step, reproduce
+    the causal full-sequence forward row for row."""
+    from atma_amd.layers.global_attention import GlobalLayerCache
+    attn = _block().attn.to(dev, dtype)
+    B, T0, T1, T2, page = 2, 37, 29, 64, 16
+    T = T0 + T1 + T2 + 1
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(B, T, DIM, generator=g).to(dev, dtype)
+    full = attn(x)
+    max_pages = (T + page - 1) // page
+    num_pages = B * max_pages + 3
+    cache = GlobalLayerCache.allocate(attn, num_pages, page, max_seqs=B + 2, device=dev, dtype=dtype)
+    perm = torch.randperm(num_pages, generator=g)[:B * max_pages].view(B, max_pages).int()
+    bt = perm.to(dev)
+    slots = torch.tensor([3, 1], device=dev)
+
+    def smap(lo, hi):
+        return torch.tensor([int(perm[b, t // page]) * page + t % page for b in range(B) for t in range(lo, hi)],
+                            dtype=torch.int32, device=dev)
+
+    def check(y, lo, hi):
+        ref = full[:, lo:hi]
+        err = max_abs(y, ref) if dtype == torch.float32 else rel_err(y.float(), ref.float())
+        assert err <= tol, (lo, hi, err)
+
+    check(attn.prefill(x[:, :T0], cache, slots, smap(0, T0)), 0, T0)
+    check(attn.prefill_continue(x[:, T0:T0 + T1], cache, slots, smap(T0, T0 + T1), bt, [T0] * B), T0, T0 + T1)
+    lo = T0 + T1
+    check(attn.prefill_continue(x[:, lo:lo + T2], cache, slots, smap(lo, lo + T2), bt, [lo] * B), lo, lo + T2)
+    pos = T - 1
+    ctx = torch.full((B,), pos + 1, dtype=torch.int32, device=dev)
+    check(attn.decode(x[:, pos], cache, slots, bt, ctx, smap(pos, pos + 1)).unsqueeze(1), pos, pos + 1)
