@@ -309,6 +309,43 @@ def _(x, weight, slots, state_table, residual):
     return torch.empty_like(x)
 
 
+# --------------------------------------------------------------------------- gated delta backward
+@torch.library.custom_op("atma_hip::gated_delta_bwd", mutates_args=())
+def gated_delta_bwd_op(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,
+                       initial_state: Optional[Tensor], d_out: Tensor,
+                       d_final_state: Optional[Tensor]) -> List[Tensor]:
+    """fp32 contiguous (B, T, H, .) inputs; returns dq, dk, dv, dg, dbeta, d_initial_state."""
+    _need_cuda(q, k, v, g, beta, d_out)
+    lib = _lib.load()
+    B, T, H, dk = q.shape
+    dv = v.shape[3]
+    JB = dv // 16
+    f = dict(device=q.device, dtype=torch.float32)
+    dq_part = torch.empty((JB, B, T, H, dk), **f)
+    dk_part = torch.empty((JB, B, T, H, dk), **f)
+    dg_part = torch.empty((JB, B, T, H), **f)
+    db_part = torch.empty((JB, B, T, H), **f)
+    dv_out = torch.empty((B, T, H, dv), **f)
+    ds0 = torch.empty((B, H, dk, dv), **f)
+    ws_bytes = lib.atma_gated_delta_bwd_workspace_bytes(B, T, H, dk, dv)
+    ws = torch.empty((max(ws_bytes, 4) // 4,), **f)
+    rc = lib.atma_gated_delta_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
+                                  _lib.ptr(initial_state), d_out.data_ptr(), _lib.ptr(d_final_state),
+                                  dq_part.data_ptr(), dk_part.data_ptr(), dv_out.data_ptr(), dg_part.data_ptr(),
+                                  db_part.data_ptr(), ds0.data_ptr(), B, T, H, dk, dv, ws.data_ptr(),
+                                  ws.numel() * 4, _lib.stream_handle(q.device))
+    _lib.check(rc, "gated_delta_bwd")
+    return [dq_part.sum(0), dk_part.sum(0), dv_out, dg_part.sum(0), db_part.sum(0), ds0]
+
+
+@gated_delta_bwd_op.register_fake
+def _(q, k, v, g, beta, initial_state, d_out, d_final_state):
+    B, T, H, dk = q.shape
+    dv = v.shape[3]
+    return [q.new_empty(q.shape), q.new_empty(q.shape), v.new_empty(v.shape), g.new_empty(g.shape),
+            g.new_empty(g.shape), q.new_empty((B, H, dk, dv))]
+
+
 # --------------------------------------------------------------------------- inference fusions
 @torch.library.custom_op("atma_hip::squared_relu_gate", mutates_args=())
 def squared_relu_gate_op(x: Tensor, gate: Tensor) -> Tensor:

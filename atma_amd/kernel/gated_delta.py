@@ -45,7 +45,6 @@ def gated_delta_decode_step(q, k, v, gamma, beta, state_table, slots, eps=1e-12,
                                                       float(eps))
 
 
-@torch.no_grad()
 def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
                            output_final_state=False, use_qk_l2norm_in_kernel=False,
                            cu_seqlens=None, head_first=False, gate_bias=None, start_signal=None):
@@ -67,6 +66,19 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
     Returns (o (B, T, H, dv) in q's dtype, final_state (B, H, dk, dv) fp32 or None)."""
     if cu_seqlens is not None or head_first:
         raise NotImplementedError("cu_seqlens / head_first layouts are not supported")
+    if q.dim() == 4 and q.shape[1] > 0 and torch.is_grad_enabled() and \
+            any(isinstance(t, torch.Tensor) and t.requires_grad for t in (q, k, v, g, beta, initial_state)):
+        if gate_bias is not None or start_signal is not None:
+            raise ValueError("gate_bias / start_signal are inference-only extensions (no autograd)")
+        return _chunk_gated_delta_train(q, k, v, g, beta, scale, initial_state, output_final_state,
+                                        use_qk_l2norm_in_kernel)
+    with torch.no_grad():
+        return _chunk_gated_delta_infer(q, k, v, g, beta, scale, initial_state, output_final_state,
+                                        use_qk_l2norm_in_kernel, gate_bias, start_signal)
+
+
+def _chunk_gated_delta_infer(q, k, v, g, beta, scale, initial_state, output_final_state,
+                             use_qk_l2norm_in_kernel, gate_bias, start_signal):
     if q.dim() != 4 or k.dim() != 4 or k.shape[:2] != q.shape[:2] or k.shape[3] != q.shape[3] \
             or v.dim() != 4 or v.shape[:3] != k.shape[:3]:
         raise ValueError("q: (B, T, H, dk), k: (B, T, Hkv, dk) and v: (B, T, Hkv, dv) required")
@@ -103,6 +115,48 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
                                                      0 if start_signal is None else start_signal.epoch,
                                                      gate_bias is not None, gb, bb)
     return outs[0], (outs[1] if output_final_state else None)
+
+
+class _GatedDeltaFn(torch.autograd.Function):
+    """The recurrence on prepared fp32 operands (q scaled and normalised, k normalised,
+    log decay g, beta, [K, V] initial state): forward by the chunked prefill kernel,
+    backward by ``gated_delta_bwd`` (state checkpoints every 64 tokens, sub-blocks
+    recomputed in registers)."""
+
+    @staticmethod
+    def forward(ctx, qs, kn, v, g, beta, S0):
+        o, S = torch.ops.atma_hip.chunk_gated_delta_rule(qs, kn, v, g, beta, S0, 1.0, False, True, None, 0,
+                                                         False, 0.0, 0.0)
+        ctx.save_for_backward(qs, kn, v, g, beta, S0)
+        return o, S
+
+    @staticmethod
+    def backward(ctx, dO, dS):
+        qs, kn, v, g, beta, S0 = ctx.saved_tensors
+        dO = torch.zeros_like(v) if dO is None else dO.to(torch.float32).contiguous()
+        dS = None if dS is None else dS.to(torch.float32).contiguous()
+        dq, dk, dv, dg, db, ds0 = torch.ops.atma_hip.gated_delta_bwd(qs, kn, v, g, beta, S0, dO, dS)
+        return dq, dk, dv, dg, db, (ds0 if S0 is not None else None)
+
+
+def _chunk_gated_delta_train(q, k, v, g, beta, scale, initial_state, output_final_state, use_qk_l2norm):
+    """Differentiable ``chunk_gated_delta_rule`` (the FLA autograd the reference trains
+    through, ``model/blocks.py:44-84``).  The l2 norm, the scale and grouped-head expansion
+    are torch ops (autograd differentiates them); the recurrence and its backward are HIP.
+    Arithmetic in fp32; o is returned in q's dtype."""
+    B, T, H, dk = q.shape
+    if k.shape[2] != H:
+        rep = H // k.shape[2]
+        k, v = k.repeat_interleave(rep, dim=2), v.repeat_interleave(rep, dim=2)
+    qf, kf = q.float(), k.float()
+    if use_qk_l2norm:
+        qf = torch.nn.functional.normalize(qf, dim=-1, eps=1e-12)
+        kf = torch.nn.functional.normalize(kf, dim=-1, eps=1e-12)
+    qs = qf * (dk ** -0.5 if scale is None else float(scale))
+    S0 = None if initial_state is None else initial_state.float().contiguous()
+    o, S = _GatedDeltaFn.apply(qs.contiguous(), kf.contiguous(), v.float().contiguous(),
+                               g.float().contiguous(), beta.float().contiguous(), S0)
+    return o.to(q.dtype), (S if output_final_state else None)
 
 
 def recurrence_pays_to_overlap(B, H, dv, dtype, device):

@@ -233,6 +233,25 @@ int atma_causal_conv1d_decode_step(const void* x, int64_t x_sb, const void* weig
                                    int residual, int dtype, void* stream);
 
 /*
+ * Backward of the gated-delta recurrence, the training path of chunk_gated_delta_rule
+ * (FLA autograd in the reference: model/blocks.py:44-84, caller TitansMemory.forward
+ * model/blocks.py:470-479; recurrence scripts/titans_proto.py:53-76).  All fp32 and
+ * contiguous: q (scaled and normalised), k (normalised): (B, T, H, dk); v, d_out: (B, T, H, dv);
+ * g (log decay), beta: (B, T, H); initial_state, d_final_state: (B, H, dk, dv) [K, V] or NULL
+ * (zero).  Writes dv (B, T, H, dv) and d_initial_state (B, H, dk, dv) in full, and per
+ * 16-column block of V (JB = dv / 16) the partial sums dq_part, dk_part (JB, B, T, H, dk) and
+ * dg_part (d/dg, already times exp(g)), dbeta_part (JB, B, T, H): the caller sums axis 0.
+ * dk in {64, 128}; dv a multiple of 16.  workspace: atma_gated_delta_bwd_workspace_bytes
+ * (state checkpoints every 64 tokens).
+ */
+size_t atma_gated_delta_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv);
+int atma_gated_delta_bwd(const float* q, const float* k, const float* v, const float* g, const float* beta,
+                         const float* initial_state, const float* d_out, const float* d_final_state,
+                         float* dq_part, float* dk_part, float* dv, float* dg_part, float* dbeta_part,
+                         float* d_initial_state, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv_dim,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Fused MLP activation out = gate * relu(x)^2.  Replaces squared_relu_gate
  * (kernel/inference_ops_triton.py:102-135), called by InferenceMLP.forward
  * (inference/models/atma.py:87-96).  x, gate: (rows, width) with strides (x_s0, x_s1),

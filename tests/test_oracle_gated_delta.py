@@ -142,3 +142,19 @@ def test_flops_formula():
     from oracle.polar import prefill_flops
     assert prefill_flops(8, 8, 2048, 128) == pytest.approx(6.875e10, rel=1e-3)
     assert prefill_flops(1, 8, 65536, 128) == pytest.approx(8.796e12, rel=1e-3)
+
+
+def test_sequential_autograd_is_pinned_by_gradcheck():
+    """The backward's oracle is torch autograd through ``gated_delta_sequential``; central
+    differences (fp64) pin it for every input, the initial state included."""
+    g = torch.Generator().manual_seed(11)
+    B, H, N, dk, dv = 1, 2, 5, 4, 3
+    q = torch.randn(B, H, N, dk, generator=g, dtype=torch.float64, requires_grad=True)
+    k = torch.nn.functional.normalize(torch.randn(B, H, N, dk, generator=g, dtype=torch.float64), dim=-1)
+    k.requires_grad_(True)
+    v = torch.randn(B, H, N, dv, generator=g, dtype=torch.float64, requires_grad=True)
+    gam = torch.rand(B, H, N, generator=g, dtype=torch.float64).mul(0.5).add(0.45).requires_grad_(True)
+    bet = torch.rand(B, H, N, generator=g, dtype=torch.float64).requires_grad_(True)
+    S0 = torch.randn(B, H, dv, dk, generator=g, dtype=torch.float64, requires_grad=True)
+    f = lambda *a: G.gated_delta_sequential(*a)  # noqa: E731
+    assert torch.autograd.gradcheck(f, (q, k, v, gam, bet, S0))
