@@ -16,10 +16,12 @@
 // of one (sequence, head) state (dk x 16 fp32, RPT = dk / 16 rows per lane; lane =
 // column * 16 + row group, so a column's row reduction is a 16-lane shuffle).  Pass 1
 // walks forward and checkpoints the state every 64 tokens in the workspace.  Pass 2
-// walks the chunks backwards; each 8-token sub-block is recomputed from its chunk's
+// walks the chunks backwards.  Each chunk's operands (k rows, the block's 16 columns
+// of v and dO, gamma, beta) are staged in LDS once, since the recomputation
+// reads them several times; each 8-token sub-block is recomputed from its chunk's
 // checkpoint into registers (the states before and after each token, u and v - pred),
-// then the 8 reverse steps run on registers.  Sums over columns (dq, dk, db, dg) go
-// through LDS once per sub-block (double-buffered, one barrier), and each workgroup
+// then the 8 reverse steps run on registers.  Row sums are DPP row reductions; sums
+// over columns (dq, dk, db, dg) go through LDS once per sub-block, and each workgroup
 // writes its column block's partial sums; the caller adds the dv / 16 partials.
 #include "common.h"
 
@@ -51,7 +53,14 @@ template <int RPT>
 __global__ void __launch_bounds__(256) gdn_bwd_kernel(GdnBwdArgs a) {
   constexpr int DK = 16 * RPT;
   constexpr int NRED = 2 * DK + 2;  // dq[DK], dk[DK], db, dg per wave
-  __shared__ float red[2][kBwdSub][4][NRED];
+  __shared__ float red[kBwdSub][4][NRED];
+  // the current chunk's operands: k rows, this block's 16 columns of v and dO, gamma, beta
+  // (q is read once per token, from memory), 73.5 KiB in all with red: two workgroups per CU
+  __shared__ __attribute__((aligned(16))) float sk[kBwdChunk][DK];
+  __shared__ float sv[kBwdChunk][16];
+  __shared__ float sdo[kBwdChunk][16];
+  __shared__ float sgam[kBwdChunk];
+  __shared__ float sbet[kBwdChunk];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = tid >> 4, rg = tid & 15;
@@ -64,8 +73,9 @@ __global__ void __launch_bounds__(256) gdn_bwd_kernel(GdnBwdArgs a) {
   const int NC = (T + kBwdChunk - 1) / kBwdChunk;
   const int64_t tok0 = (int64_t)b * T;  // token row base of this sequence
 
-  auto rows = [&](const float* base, int t, float* out) {
-    const float* p = base + ((tok0 + t) * H + h) * DK + rg * RPT;
+  // rows rg * RPT .. of a DK-float row
+  auto rows = [&](const float* p0, float* out) {
+    const float* p = p0 + rg * RPT;
 #pragma unroll
     for (int i = 0; i < RPT; i += 4) {
       const f32x4 x = *(const f32x4*)(p + i);
@@ -73,19 +83,52 @@ __global__ void __launch_bounds__(256) gdn_bwd_kernel(GdnBwdArgs a) {
       for (int e = 0; e < 4; ++e) out[i + e] = x[e];
     }
   };
-  auto row_sum = [&](float x) {  // over the 16 row groups of a column
-#pragma unroll
-    for (int m = 1; m < 16; m <<= 1) x += __shfl_xor(x, m, 64);
+  // stage chunk c (tokens cb .. ce) into LDS; with_grad adds dO
+  auto stage = [&](int cb, int ce, bool with_grad) {
+    __syncthreads();  // the previous chunk's readers are done
+    const int n = ce - cb;
+    for (int idx = tid; idx < n * (DK / 4); idx += 256) {
+      const int tl = idx / (DK / 4), e4 = idx % (DK / 4);
+      const int64_t off = ((tok0 + cb + tl) * H + h) * DK + 4 * e4;
+      *(f32x4*)&sk[tl][4 * e4] = *(const f32x4*)(a.k + off);
+    }
+    for (int idx = tid; idx < n * 16; idx += 256) {
+      const int tl = idx / 16, cc = idx % 16;
+      const int64_t th = (tok0 + cb + tl) * H + h;
+      sv[tl][cc] = a.v[th * DV + jb * 16 + cc];
+      if (with_grad) sdo[tl][cc] = a.dO[th * DV + jb * 16 + cc];
+    }
+    for (int tl = tid; tl < n; tl += 256) {
+      const int64_t th = (tok0 + cb + tl) * H + h;
+      sgam[tl] = __expf(a.g[th]);
+      sbet[tl] = a.beta[th];
+    }
+    __syncthreads();
+  };
+  // sum over the 16 row groups of a column = one 16-lane DPP row: swap neighbours and
+  // pairs within quads, then rotate the row by 4 and by 8 (every lane ends with the sum)
+  auto dpp = [](float x, int ctrl) -> float {
+    switch (ctrl) {  // the control must be a constant
+      case 0xB1: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false));
+      case 0x4E: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false));
+      case 0x124: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x124, 0xF, 0xF, false));
+      default: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x128, 0xF, 0xF, false));
+    }
+  };
+  auto row_sum = [&](float x) {
+    x += dpp(x, 0xB1);   // quad_perm [1,0,3,2]
+    x += dpp(x, 0x4E);   // quad_perm [2,3,0,1]
+    x += dpp(x, 0x124);  // row_ror:4
+    x += dpp(x, 0x128);  // row_ror:8
     return x;
   };
   // one forward step: S (state before t) -> S (state after t); returns v - pred and u
-  auto step = [&](int t, float* S, float& vm, float& u) {
+  auto step = [&](int tl, float* S, float& vm, float& u) {  // tl: index in the staged chunk
     float kr[RPT];
-    rows(a.k, t, kr);
-    const int64_t th = (tok0 + t) * H + h;
-    const float gam = __expf(a.g[th]);
-    const float bet = a.beta[th];
-    const float vj = a.v[th * DV + j];
+    rows(sk[tl], kr);
+    const float gam = sgam[tl];
+    const float bet = sbet[tl];
+    const float vj = sv[tl][col];
     float pred = 0.f;
 #pragma unroll
     for (int i = 0; i < RPT; ++i) {
@@ -111,9 +154,10 @@ __global__ void __launch_bounds__(256) gdn_bwd_kernel(GdnBwdArgs a) {
 #pragma unroll
     for (int i = 0; i < RPT; i += 4) *(f32x4*)(cp + i) = f32x4{S[i], S[i + 1], S[i + 2], S[i + 3]};
     const int te = min((c + 1) * kBwdChunk, T);
-    for (int t = c * kBwdChunk; t < te; ++t) {
+    stage(c * kBwdChunk, te, false);
+    for (int tl = 0; tl < te - c * kBwdChunk; ++tl) {
       float vm, u;
-      step(t, S, vm, u);
+      step(tl, S, vm, u);
     }
   }
 
@@ -121,10 +165,10 @@ __global__ void __launch_bounds__(256) gdn_bwd_kernel(GdnBwdArgs a) {
   float G[RPT];
 #pragma unroll
   for (int i = 0; i < RPT; ++i) G[i] = a.dST ? a.dST[sidx + (int64_t)i * DV] : 0.f;
-  int buf = 0;
   for (int c = NC - 1; c >= 0; --c) {
     const int cb = c * kBwdChunk, ce = min(cb + kBwdChunk, T);
     const int nsub = (ce - cb + kBwdSub - 1) / kBwdSub;
+    stage(cb, ce, true);
     for (int sb = nsub - 1; sb >= 0; --sb) {
       const int t0 = cb + sb * kBwdSub;
       const int n = min(kBwdSub, ce - t0);  // tokens in this sub-block (uniform)
@@ -138,9 +182,9 @@ __global__ void __launch_bounds__(256) gdn_bwd_kernel(GdnBwdArgs a) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) Sb[0][i + e] = x[e];
         }
-        for (int t = cb; t < t0; ++t) {
+        for (int tl = 0; tl < t0 - cb; ++tl) {
           float vm, u;
-          step(t, Sb[0], vm, u);
+          step(tl, Sb[0], vm, u);
         }
       }
       float VM[kBwdSub], U[kBwdSub];
@@ -149,21 +193,21 @@ __global__ void __launch_bounds__(256) gdn_bwd_kernel(GdnBwdArgs a) {
         if (s < n) {
 #pragma unroll
           for (int i = 0; i < RPT; ++i) Sb[s + 1][i] = Sb[s][i];
-          step(t0 + s, Sb[s + 1], VM[s], U[s]);
+          step(t0 - cb + s, Sb[s + 1], VM[s], U[s]);
         }
       }
       // reverse steps on registers; column sums of each token to LDS slot s
 #pragma unroll
       for (int s = kBwdSub - 1; s >= 0; --s) {
         if (s < n) {
-          const int t = t0 + s;
-          const int64_t th = (tok0 + t) * H + h;
+          const int tl = t0 - cb + s;
+          const int64_t th = (tok0 + t0 + s) * H + h;
           float qr[RPT], kr[RPT];
-          rows(a.q, t, qr);
-          rows(a.k, t, kr);
-          const float gam = __expf(a.g[th]);
-          const float bet = a.beta[th];
-          const float dOj = a.dO[th * DV + j];
+          rows(a.q + th * DK, qr);
+          rows(sk[tl], kr);
+          const float gam = sgam[tl];
+          const float bet = sbet[tl];
+          const float dOj = sdo[tl][col];
           float dq[RPT], dk[RPT];
           float du = 0.f;
 #pragma unroll
@@ -195,7 +239,7 @@ __global__ void __launch_bounds__(256) gdn_bwd_kernel(GdnBwdArgs a) {
           }
           dgl = wave_sum(dgl);
           dbl = wave_sum(dbl);
-          float* r = red[buf][s][wave];
+          float* r = red[s][wave];
           if (lane < 16) {
 #pragma unroll
             for (int i = 0; i < RPT; ++i) {
@@ -213,7 +257,7 @@ __global__ void __launch_bounds__(256) gdn_bwd_kernel(GdnBwdArgs a) {
       // add the 4 waves and write this column block's partial sums
       for (int idx = tid; idx < n * NRED; idx += 256) {
         const int s = idx / NRED, e = idx % NRED;
-        const float* r0 = red[buf][s][0];
+        const float* r0 = red[s][0];
         const float sum = r0[e] + r0[NRED + e] + r0[2 * NRED + e] + r0[3 * NRED + e];
         const int64_t th = (tok0 + t0 + s) * H + h;
         const int64_t plane = (int64_t)a.B * T * H;
@@ -224,9 +268,9 @@ __global__ void __launch_bounds__(256) gdn_bwd_kernel(GdnBwdArgs a) {
         else if (e == 2 * DK)
           a.db_part[jb * plane + th] = sum;
         else
-          a.dg_part[jb * plane + th] = sum * __expf(a.g[th]);  // d/d(log decay) = dgamma * gamma
+          a.dg_part[jb * plane + th] = sum * sgam[t0 - cb + s];  // d/d(log decay) = dgamma * gamma
       }
-      buf ^= 1;
+      __syncthreads();  // red is reused by the next sub-block
     }
   }
 #pragma unroll
