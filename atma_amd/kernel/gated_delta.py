@@ -68,8 +68,11 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
         raise NotImplementedError("cu_seqlens / head_first layouts are not supported")
     if q.dim() == 4 and q.shape[1] > 0 and torch.is_grad_enabled() and \
             any(isinstance(t, torch.Tensor) and t.requires_grad for t in (q, k, v, g, beta, initial_state)):
-        if gate_bias is not None or start_signal is not None:
-            raise ValueError("gate_bias / start_signal are inference-only extensions (no autograd)")
+        if gate_bias is not None:   # raw logits: the activations as differentiable torch ops
+            g = torch.nn.functional.logsigmoid(g.float() + float(gate_bias[0]))
+            beta = torch.sigmoid(beta.float() + float(gate_bias[1]))
+        if start_signal is not None:  # nothing to overlap with: release the waiting stream now
+            start_signal.flag.fill_(start_signal.epoch)
         return _chunk_gated_delta_train(q, k, v, g, beta, scale, initial_state, output_final_state,
                                         use_qk_l2norm_in_kernel)
     with torch.no_grad():
