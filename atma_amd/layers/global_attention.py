@@ -166,7 +166,6 @@ class PolarAttention(nn.Module):
         self.overlap = overlap
         self._side = {}
         self._signal = {}
-        self._decode_side = {}
 
     # ------------------------------------------------------------------ pieces
     def polar_params(self):
@@ -362,28 +361,14 @@ class PolarAttention(nn.Module):
         q = self._conv_step(q.reshape(Bn, H * dk), self.canon_q, cache.conv_q, slots).view(Bn, H, dk)
         k = self._conv_step(k.reshape(Bn, Hkv * dk), self.canon_k, cache.conv_k, slots).view(Bn, Hkv, dk)
         v = self._conv_step(v.reshape(Bn, Hkv * dk), self.canon_v, cache.conv_v, slots).view(Bn, Hkv, dk)
-        m = None
-        if self.mem is not None:
-            # the memory step is independent of the attention: it runs on a forked stream
-            # (a parallel branch when the decode is captured in a graph)
-            main = torch.cuda.current_stream(x.device)
-            side = self._decode_side.get(x.device)
-            if side is None:
-                side = self._decode_side[x.device] = torch.cuda.Stream(device=x.device)  # default priority
-            side.wait_stream(main)
-            with torch.cuda.stream(side):
-                m = self.mem.step(x, q, k, v, cache.mem_table, slots)
         store_kvcache(k, v, cache.k_cache, cache.v_cache, slot_mapping)
         c, mag = polar_attention_decode(q, cache.k_cache, cache.v_cache, block_tables, context_lens,
                                         window=self.window, **self.polar_params())
         out = self._combine(c, mag, gate)
-        if m is not None:
-            main.wait_stream(side)
-            for t in (x, q, k, v, slots):
-                if isinstance(t, torch.Tensor) and t.is_cuda:
-                    t.record_stream(side)
-            m.record_stream(main)
-            out = out + m
+        if self.mem is not None:
+            # one stream: a forked memory branch measured slower (it competes with the
+            # split kernel for CU slots)
+            out = out + self.mem.step(x, q, k, v, cache.mem_table, slots)
         return out
 
 

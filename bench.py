@@ -15,7 +15,7 @@ configs[3] (paged decode step: 64 sequences, ctx ~ U[1024, 32768], 256-token pag
 a shuffled pool, store_kvcache + Polar decode + gated-delta step, replayed as a HIP
 graph), each with its roofline fraction, plus the CPU oracle timed on this host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4|ops] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4|ops|train] [--no-cpu]
 """
 
 import argparse
@@ -190,22 +190,12 @@ class Decode:
         self.p = _params(torch, dev, seed)
         self.B, self.pages = B, pool
         self.ctx_sum = int(ctx.sum())
-        self.side = torch.cuda.Stream(device=dev)  # default priority
         self.graph = None
 
     def step(self):
-        """The layer's decode schedule: the memory step (independent of attention) on a
-        forked stream, store_kvcache then the paged attention on the main stream; a
-        captured graph holds the two as parallel branches."""
-        torch = self.torch
-        main = torch.cuda.current_stream()
-        self.side.wait_stream(main)
-        with torch.cuda.stream(self.side):
-            r = self.step_mem(self.q, self.knew, self.vnew, self.gamma, self.beta, self.table, self.slots)
         self.store(self.knew, self.vnew, self.kc, self.vc, self.slot_map)
         c, mag = self.dec(self.q, self.kc, self.vc, self.bt, self.ctx, **self.p)
-        main.wait_stream(self.side)
-        r.record_stream(main)
+        r = self.step_mem(self.q, self.knew, self.vnew, self.gamma, self.beta, self.table, self.slots)
         return c, mag, r
 
     def attention(self):
@@ -288,6 +278,27 @@ def bench_inference_ops(torch, dev, steps, warmup):
     return res
 
 
+def bench_memory_train(torch, dev, steps, warmup):
+    """Training step of the memory branch at the configs[1] shape (B=8, T=2048, 8 heads,
+    d=128, bf16 q/k/v): chunk_gated_delta_rule forward (fp32 on normalised operands) and
+    its HIP backward (gated_delta_bwd), timed together with HIP events."""
+    from atma_amd.kernel import chunk_gated_delta_rule
+    B, T = 8, 2048
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v = (torch.randn(B, T, HQ, D, device=dev, generator=g, dtype=torch.bfloat16).requires_grad_(True)
+               for _ in range(3))
+    gl = torch.nn.functional.logsigmoid(torch.randn(B, T, HQ, device=dev, generator=g) + 3.9).requires_grad_(True)
+    beta = torch.sigmoid(torch.randn(B, T, HQ, device=dev, generator=g)).requires_grad_(True)
+    dO = torch.randn(B, T, HQ, D, device=dev, generator=g, dtype=torch.bfloat16)
+
+    def step():
+        o, _ = chunk_gated_delta_rule(q, k, v, gl, beta, scale=1.0, use_qk_l2norm_in_kernel=True)
+        torch.autograd.grad(o, (q, k, v, gl, beta), dO)
+
+    ms = _time(torch, step, steps, warmup)
+    return dict(B=B, T=T, ms_fwd_bwd=ms)
+
+
 def cpu_baseline(torch):
     """The CPU oracle (oracle/: Polar streaming form + gated-delta chunked UT form, fp32)
     on a bounded sample of configs[1]: one of the 8 sequences, full T = 2048, all heads."""
@@ -360,7 +371,7 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "ops", "copy"], default=None,
+    ap.add_argument("--only", choices=["c2", "c3", "c4", "ops", "train", "copy"], default=None,
                     help="one workload; 'copy' runs a plain 512 MiB device copy, the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--no-cpu", action="store_true")
@@ -399,6 +410,8 @@ def main(argv=None):
         c4w = bench_decode(torch, dev, max(5, args.steps // 2), 2, full=True)
         print(f"# c4 decode 64x32768: {json.dumps(c4w)}", file=sys.stderr, flush=True)
         out["c4"] = [c4, c4w]
+    if args.only == "train":
+        out["train"] = bench_memory_train(torch, dev, max(3, args.steps // 4), 2)
     if args.only in (None, "ops"):
         ops = bench_inference_ops(torch, dev, args.steps, args.warmup)
         print(f"# inference ops: {json.dumps(ops)}", file=sys.stderr, flush=True)
