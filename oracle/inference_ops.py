@@ -31,11 +31,12 @@ def squared_relu_gate(x, gate):
     ``out = gate * square`` in fp32, stored in x's dtype.  NaN inputs stay NaN, as
     torch's relu (the reference test's eager form, ``tests/test_decode_kernels.py:62``)."""
     xf, gf = _f32(x), _f32(gate)
-    pos = np.where(xf < 0, np.float32(0), xf).astype(np.float32)
-    sq = (pos * pos).astype(np.float32)
-    if x.dtype == torch.bfloat16:
-        sq = round_bf16(sq)
-    return _out(gf * sq, x.dtype)
+    with np.errstate(over="ignore", invalid="ignore"):   # inf / NaN inputs propagate as IEEE says
+        pos = np.where(xf < 0, np.float32(0), xf).astype(np.float32)
+        sq = (pos * pos).astype(np.float32)
+        if x.dtype == torch.bfloat16:
+            sq = round_bf16(sq)
+        return _out(gf * sq, x.dtype)
 
 
 def softcap_logits(logits):
@@ -46,11 +47,12 @@ def softcap_logits(logits):
     x = _f32(logits)
     bf = logits.dtype == torch.bfloat16
     rnd = round_bf16 if bf else (lambda a: np.asarray(a, dtype=np.float32))
-    left = rnd(np.float32(15) * x)
-    square = rnd(x * x)
-    denom = rnd(square + np.float32(225))
-    inv = rnd(np.float32(1) / np.sqrt(denom))
-    return _out(left * inv, logits.dtype)
+    with np.errstate(over="ignore", invalid="ignore"):   # huge inputs overflow to inf as IEEE says
+        left = rnd(np.float32(15) * x)
+        square = rnd(x * x)
+        denom = rnd(square + np.float32(225))
+        inv = rnd(np.float32(1) / np.sqrt(denom))
+        return _out(left * inv, logits.dtype)
 
 
 def _fma32(a, b, c):
