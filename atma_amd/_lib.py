@@ -68,8 +68,13 @@ _lock = threading.Lock()
 _lib = None
 
 
-class HipLibraryMissing(RuntimeError):
-    """libatma_hip.so is not built (or failed to load)."""
+class HipLibraryMissing(ImportError, RuntimeError):
+    """libatma_hip.so is not built (or failed to load).
+
+    An ImportError, so that importing the ops package without the library fails the
+    way a missing kernel backend fails in the reference (its callers guard the import
+    with ``try/except`` and take their eager path); also a RuntimeError for callers
+    that load the library lazily."""
 
 
 def load():

@@ -428,12 +428,8 @@ def _(zg, zb, g_bias, b_bias, decay_as_prob):
 
 
 # --------------------------------------------------------------------------- chunked gated delta
-@torch.library.custom_op("atma_hip::chunk_gated_delta_rule", mutates_args=("start_flag",))
-def chunk_gated_delta_rule_op(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,
-                              initial_state: Optional[Tensor], scale: float, use_qk_l2norm: bool,
-                              want_final: bool, start_flag: Optional[Tensor], start_epoch: int,
-                              gate_logits: bool = False, g_bias: float = 0.0,
-                              b_bias: float = 0.0) -> List[Tensor]:
+def _chunk_gated_delta(q, k, v, g, beta, initial_state, scale, use_qk_l2norm, want_final, start_flag,
+                       start_epoch, gate_logits, g_bias, b_bias):
     _need_cuda(q, k, v, g, beta, initial_state)
     lib = _lib.load()
     q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
@@ -455,6 +451,33 @@ def chunk_gated_delta_rule_op(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: 
         ws.data_ptr(), ws.numel() * 4, _lib.ptr(start_flag), start_epoch, _lib.stream_handle(q.device))
     _lib.check(rc, "chunk_gated_delta_rule")
     return [o, final] if want_final else [o]
+
+
+@torch.library.custom_op("atma_hip::chunk_gated_delta_rule", mutates_args=("start_flag",))
+def chunk_gated_delta_rule_op(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,
+                              initial_state: Optional[Tensor], scale: float, use_qk_l2norm: bool,
+                              want_final: bool, start_flag: Optional[Tensor], start_epoch: int,
+                              gate_logits: bool = False, g_bias: float = 0.0,
+                              b_bias: float = 0.0) -> List[Tensor]:
+    """Inference prefill; ``start_flag`` (mutated) is raised as the recurrence starts."""
+    return _chunk_gated_delta(q, k, v, g, beta, initial_state, scale, use_qk_l2norm, want_final,
+                              start_flag, start_epoch, gate_logits, g_bias, b_bias)
+
+
+@torch.library.custom_op("atma_hip::gated_delta_fwd", mutates_args=())
+def gated_delta_fwd_op(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,
+                       initial_state: Optional[Tensor]) -> List[Tensor]:
+    """The recurrence forward of the autograd route on prepared fp32 operands (q scaled
+    and normalised, k normalised, log decay, beta): same kernels, no start flag, so it
+    mutates nothing and functionalises under torch.compile.  Returns [o, final state]."""
+    return _chunk_gated_delta(q, k, v, g, beta, initial_state, 1.0, False, True, None, 0, False, 0.0, 0.0)
+
+
+@gated_delta_fwd_op.register_fake
+def _(q, k, v, g, beta, initial_state):
+    B, T, H, dk = q.shape
+    dv = v.shape[3]
+    return [q.new_empty((B, T, H, dv)), q.new_empty((B, H, dk, dv), dtype=torch.float32)]
 
 
 @chunk_gated_delta_rule_op.register_fake

@@ -66,7 +66,8 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
     Returns (o (B, T, H, dv) in q's dtype, final_state (B, H, dk, dv) fp32 or None)."""
     if cu_seqlens is not None or head_first:
         raise NotImplementedError("cu_seqlens / head_first layouts are not supported")
-    if q.dim() == 4 and q.shape[1] > 0 and torch.is_grad_enabled() and \
+    _check_args(q, k, v, g, beta, initial_state)
+    if q.shape[1] > 0 and torch.is_grad_enabled() and \
             any(isinstance(t, torch.Tensor) and t.requires_grad for t in (q, k, v, g, beta, initial_state)):
         if gate_bias is not None:   # raw logits: the activations as differentiable torch ops
             g = torch.nn.functional.logsigmoid(g.float() + float(gate_bias[0]))
@@ -80,8 +81,10 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
                                         use_qk_l2norm_in_kernel, gate_bias, start_signal)
 
 
-def _chunk_gated_delta_infer(q, k, v, g, beta, scale, initial_state, output_final_state,
-                             use_qk_l2norm_in_kernel, gate_bias, start_signal):
+def _check_args(q, k, v, g, beta, initial_state):
+    """Shapes and dtypes of ``chunk_gated_delta_rule``'s operands, checked before any
+    launch on both the inference and the autograd route (the kernels index g, beta and
+    the state by these shapes without bounds checks)."""
     if q.dim() != 4 or k.dim() != 4 or k.shape[:2] != q.shape[:2] or k.shape[3] != q.shape[3] \
             or v.dim() != 4 or v.shape[:3] != k.shape[:3]:
         raise ValueError("q: (B, T, H, dk), k: (B, T, Hkv, dk) and v: (B, T, Hkv, dv) required")
@@ -89,13 +92,19 @@ def _chunk_gated_delta_infer(q, k, v, g, beta, scale, initial_state, output_fina
     if k.shape[2] < 1 or H % k.shape[2]:
         raise ValueError(f"q heads ({H}) must be a multiple of k/v heads ({k.shape[2]})")
     dv = v.shape[3]
-    if g.shape != (B, T, H) or beta.shape != (B, T, H):
+    if tuple(g.shape) != (B, T, H) or tuple(beta.shape) != (B, T, H):
         raise ValueError("g and beta must be (B, T, H)")
     if k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError("q, k, v must share a dtype")
+    if initial_state is not None and tuple(initial_state.shape) != (B, H, dk, dv):
+        raise ValueError(f"initial_state must be (B, H, dk, dv) = {(B, H, dk, dv)}")
+
+
+def _chunk_gated_delta_infer(q, k, v, g, beta, scale, initial_state, output_final_state,
+                             use_qk_l2norm_in_kernel, gate_bias, start_signal):
+    B, T, H, dk = q.shape
+    dv = v.shape[3]
     if initial_state is not None:
-        if initial_state.shape != (B, H, dk, dv):
-            raise ValueError(f"initial_state must be (B, H, dk, dv) = {(B, H, dk, dv)}")
         initial_state = initial_state.to(torch.float32).contiguous()
     if scale is None:
         scale = dk ** -0.5
@@ -128,8 +137,7 @@ class _GatedDeltaFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, qs, kn, v, g, beta, S0):
-        o, S = torch.ops.atma_hip.chunk_gated_delta_rule(qs, kn, v, g, beta, S0, 1.0, False, True, None, 0,
-                                                         False, 0.0, 0.0)
+        o, S = torch.ops.atma_hip.gated_delta_fwd(qs, kn, v, g, beta, S0)
         ctx.save_for_backward(qs, kn, v, g, beta, S0)
         return o, S
 

@@ -23,6 +23,11 @@ start before Polar's fill the GPU; Polar's launch therefore waits on the recurre
 start signal (``StartSignal``).  ``overlap="auto"`` (default) takes the overlapped
 schedule exactly when ``recurrence_pays_to_overlap`` says so, ``True`` always, ``False``
 never.  Results are bitwise the same in every schedule.
+Training: when autograd must see the call (grad mode on and an input or parameter
+requiring grad), the full-sequence route runs the differentiable ops -- ``polar_attention``
+(HIP forward with saved statistics + HIP backward) and the autograd form of
+``chunk_gated_delta_rule`` -- back to back on one stream, as the reference's training
+layer is differentiable (``model/reference.py:172``, ``train/model.py:747-754``).
 """
 
 from dataclasses import dataclass
@@ -33,7 +38,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from ..kernel import (StartSignal, causal_conv1d_decode_step, chunk_gated_delta_rule,
-                      gated_delta_decode_step, gated_delta_gates, polar_attention_decode,
+                      gated_delta_decode_step, gated_delta_gates, polar_attention, polar_attention_decode,
                       polar_attention_fwd, recurrence_pays_to_overlap)
 from ..kernel.inference_ops import squared_relu_gate
 from .attention import store_kvcache
@@ -221,8 +226,14 @@ class PolarAttention(nn.Module):
             self._signal[device] = StartSignal(device)
         return s
 
-    def _overlapped(self, B, dtype, device):
-        if self.mem is None or self.overlap is False or device.type != "cuda" \
+    def _training(self, *inputs):
+        """True when autograd must see this call: grad mode is on and an input or a
+        parameter of the layer requires grad."""
+        return torch.is_grad_enabled() and (any(t.requires_grad for t in inputs)
+                                            or any(p.requires_grad for p in self.parameters()))
+
+    def _overlapped(self, B, dtype, device, training=False):
+        if self.mem is None or self.overlap is False or device.type != "cuda" or training \
                 or torch.cuda.is_current_stream_capturing():
             return False
         return self.overlap is True or recurrence_pays_to_overlap(B, self.num_heads, self.head_dim,
@@ -234,7 +245,7 @@ class PolarAttention(nn.Module):
         if self.mem is None:
             return polar_fn(), None
         x = inputs[0]
-        if not self._overlapped(x.shape[0], x.dtype, x.device):
+        if not self._overlapped(x.shape[0], x.dtype, x.device, self._training(*inputs)):
             return polar_fn(), mem_fn(None)
         main = torch.cuda.current_stream(x.device)
         side = self._side_stream(x.device)
@@ -269,9 +280,12 @@ class PolarAttention(nn.Module):
         n_keys = torch.arange(1, T + 1, device=x.device, dtype=torch.float32)
         qh, kh, vh = (t.transpose(1, 2) for t in (q, k, v))   # (B, heads, T, dk) views
 
+        # under autograd the differentiable op (HIP forward with saved statistics, HIP
+        # backward loops); otherwise the forward-only kernel
+        attend = polar_attention if self._training(x, q, k, v) else polar_attention_fwd
+
         def polar():
-            c, mag = polar_attention_fwd(qh, kh, vh, n_keys, is_causal=True, window=self.window,
-                                         **self.polar_params())
+            c, mag = attend(qh, kh, vh, n_keys, is_causal=True, window=self.window, **self.polar_params())
             return self._combine(c.transpose(1, 2), mag.transpose(1, 2), gate)
 
         def memory(signal):

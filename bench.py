@@ -211,7 +211,7 @@ class Decode:
         torch.cuda.current_stream().wait_stream(s)
         self.graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph):
-            self.step()
+            self.graph_out = self.step()   # (c, mag, r): rewritten by every replay
 
     def replay(self):
         self.graph.replay()

@@ -35,6 +35,17 @@ def linear(x, sd, name):
     return F.linear(x, sd[name + ".weight"].to(x.dtype), None if b is None else b.to(x.dtype))
 
 
+def head_rms_norm(x, dk):
+    """Per-head ``F.rms_norm(x, (dk,))`` with torch's default epsilon of the model's
+    compute dtype (``model/reference.py:136-137``, ``model/blocks.py:488``).  Left to
+    itself torch uses ``finfo(x.dtype).eps``, so an fp64 oracle would compute a
+    different function (eps 2.2e-16 instead of fp32's 1.2e-7), visible on rows whose
+    readout is tiny (the memory's first token); the fp64 form therefore keeps fp32's
+    epsilon and differs from the fp32 model only by rounding."""
+    eps = torch.finfo(torch.float32).eps if x.dtype == torch.float64 else None
+    return F.rms_norm(x, (dk,), eps=eps)
+
+
 def causal_depthwise(x_in, weight):
     """Causal depthwise conv over time: x_in (B, C, T), weight (C, 1, K), left zero pad
     K-1 (``model/reference.py:143-145``)."""
@@ -50,8 +61,8 @@ def attention_qkv(sd, x, H, Hkv, dk):
     q, gate = torch.chunk(qg, 2, dim=-1)
     k = linear(x, sd, "k").view(B, T, Hkv, dk)
     v = linear(x, sd, "v").view(B, T, Hkv, dk)
-    q = F.rms_norm(q, (dk,))
-    k = F.rms_norm(k, (dk,))
+    q = head_rms_norm(q, dk)
+    k = head_rms_norm(k, dk)
     outs = []
     for t, name, h in ((q, "canon_q", H), (k, "canon_k", Hkv), (v, "canon_v", Hkv)):
         t_in = t.reshape(B, T, h * dk).transpose(1, 2)
@@ -78,7 +89,7 @@ def memory_branch(sd, x, q_t, k_t, v_t, S0=None, chunk=64):
     kn = l2_normalize(k_t.to(wd))
     S0t = None if S0 is None else S0.to(wd).transpose(-1, -2)
     r, S = gated_delta_chunked(qn, kn, v_t.to(wd), gamma, beta, chunk=chunk, S0=S0t)
-    r = F.rms_norm(r.transpose(1, 2), (dk,))
+    r = head_rms_norm(r.transpose(1, 2), dk)
     r_flat = r.reshape(B, T, H * dk).to(x.dtype)
     out = linear(r_flat * torch.sigmoid(linear(x, sd, "mem.gate")), sd, "mem.proj")
     return out, S.transpose(-1, -2)

@@ -140,6 +140,29 @@ def test_gated_delta_wrappers_check_head_grouping():
         gated_delta_decode_step(q[:, 0], k[:, 0], k[:, 0], g[:, 0], g[:, 0], table, torch.zeros(1))
 
 
+@pytest.mark.parametrize("bad", ["g", "beta", "initial_state", "raw_g"])
+def test_gated_delta_autograd_route_checks_shapes_first(bad):
+    """Inputs that require grad take the autograd route; a mis-shaped g, beta or initial
+    state must raise ValueError there too, before any launch (CPU tensors reach the check)."""
+    from atma_amd.kernel import chunk_gated_delta_rule
+    B, T, H, d = 1, 5, 4, 64
+    q = torch.zeros(B, T, H, d, requires_grad=True)
+    k = torch.zeros(B, T, 2, d, requires_grad=True)
+    g, beta = torch.zeros(B, T, H, requires_grad=True), torch.zeros(B, T, H, requires_grad=True)
+    S0 = torch.zeros(B, H, d, d, requires_grad=True)
+    kw = {}
+    if bad == "g":
+        g = torch.zeros(B, T + 1, H, requires_grad=True)
+    elif bad == "beta":
+        beta = torch.zeros(B, T, H - 1, requires_grad=True)
+    elif bad == "initial_state":
+        S0 = torch.zeros(B, H, d, d // 2, requires_grad=True)
+    else:
+        g, kw = torch.zeros(B, T, 1, requires_grad=True), {"gate_bias": (3.9, 0.0)}
+    with pytest.raises(ValueError):
+        chunk_gated_delta_rule(q, k, k, g, beta, initial_state=S0, **kw)
+
+
 def test_packed_wrapper_validates_like_the_reference():
     """kernel/polar_triton.py:625-635: 16-bit only, [tokens, heads, dim] shapes, equal-length
     tile maps, power-of-two head dim -- all checked before any device work."""

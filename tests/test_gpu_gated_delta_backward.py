@@ -89,3 +89,38 @@ def test_unused_output_and_determinism(dev):
     assert runs[0][0].abs().max() == 0            # o unused: no gradient reaches q
     for a, b in zip(*runs):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("B,T,H,Hkv,d,dtype,tol", [
+    (2, 130, 4, 2, 64, torch.float32, 1e-4),
+    (1, 2048, 8, 2, 128, torch.bfloat16, 2e-2),    # configs[1] heads at training shape
+])
+def test_raw_logit_gates_backward_vs_fp64(dev, B, T, H, Hkv, d, dtype, tol):
+    """TitansMemory's call: raw gate logits with gate_bias=(3.9, 0.0), differentiated
+    through logsigmoid(z + 3.9) / sigmoid(z) and the recurrence, against fp64 autograd of
+    the same activations through the oracle (the sequential definition for the short
+    case; the chunked form, pinned against it, for T = 2,048)."""
+    from atma_amd.kernel import chunk_gated_delta_rule
+    gen = torch.Generator().manual_seed(T + d)
+    q = torch.randn(B, T, H, d, generator=gen).to(dtype)
+    k = torch.randn(B, T, Hkv, d, generator=gen).to(dtype)
+    v = torch.randn(B, T, Hkv, d, generator=gen).to(dtype)
+    zg, zb = torch.randn(B, T, H, generator=gen), torch.randn(B, T, H, generator=gen)
+    Wo = torch.randn(B, T, H, d, generator=gen)
+
+    leaves = [x.clone().double().requires_grad_(True) for x in (q, k, v, zg, zb)]
+    q64, k64, v64, zg64, zb64 = leaves
+    rep = H // Hkv
+    kx, vx = k64.repeat_interleave(rep, 2), v64.repeat_interleave(rep, 2)
+    gl, bt = torch.nn.functional.logsigmoid(zg64 + 3.9), torch.sigmoid(zb64)
+    if T <= 256:
+        o_ref, _ = _oracle(q64, kx, vx, gl, bt, None, 1.0, True)
+    else:
+        o_ref, _ = OG.chunk_gated_delta_rule(q64, kx, vx, gl, bt, scale=1.0, use_qk_l2norm_in_kernel=True)
+    ref = torch.autograd.grad((o_ref * Wo.double()).sum(), leaves)
+
+    dl = [x.to(dev).requires_grad_(True) for x in (q, k, v, zg, zb)]
+    od, _ = chunk_gated_delta_rule(*dl, scale=1.0, use_qk_l2norm_in_kernel=True, gate_bias=(3.9, 0.0))
+    got = torch.autograd.grad((od.float() * Wo.to(dev)).sum(), dl)
+    errs = {n: rel_err(a, b) for n, a, b in zip(["dq", "dk", "dv", "dzg", "dzb"], got, ref)}
+    assert all(e <= tol for e in errs.values()), errs

@@ -141,3 +141,35 @@ def test_chunked_prefill_continuation_equals_full_forward(dev, dtype, tol):
     pos = T - 1
     ctx = torch.full((B,), pos + 1, dtype=torch.int32, device=dev)
     check(attn.decode(x[:, pos], cache, slots, bt, ctx, smap(pos, pos + 1)).unsqueeze(1), pos, pos + 1)
+
+
+@pytest.mark.parametrize("overlap", [True, False])
+def test_block_fp32_gradients_vs_fp64_oracle(dev, overlap):
+    """Training through the layer: every parameter's gradient (and the input's) from
+    loss.backward() on the GPU block against fp64 torch autograd through
+    ``oracle/block.global_block`` (the reference forward is differentiable,
+    model/reference.py:172).  The Polar branch must reach v_null, null_base,
+    null_slope_raw, len_gain_raw, mag_beta_raw and, through c and mag, the projections
+    and Canon convs; per-tensor bar max|a-b| / max|b| <= 1e-3 (the fp32 bar of the
+    reference's Polar backward test, kernel/test_polar_kernel.py:81-117)."""
+    blk = _block(overlap=overlap)
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(1, 200, DIM, generator=g)
+    w = torch.randn(1, 200, DIM, generator=g)
+    sd = {k: v.detach().double().clone().requires_grad_(True) for k, v in blk.state_dict().items()}
+    x64 = x.double().requires_grad_(True)
+    ref_out = OB.global_block(sd, x64, H=H, Hkv=HKV, dk=DK)
+    names = [n for n, _ in blk.named_parameters()]
+    ref = torch.autograd.grad((ref_out * w.double()).sum(), [x64] + [sd[n] for n in names])
+
+    blk = blk.to(dev)
+    xd = x.to(dev).requires_grad_(True)
+    out = blk(xd)
+    got = torch.autograd.grad((out * w.to(dev)).sum(), [xd] + [p for _, p in blk.named_parameters()])
+    assert max_abs(out.detach(), ref_out.detach()) <= 1e-4
+    bad = {}
+    for name, a, b in zip(["x"] + names, got, ref):
+        e = rel_err(a, b)
+        if not e <= 1e-3:
+            bad[name] = e
+    assert not bad, bad

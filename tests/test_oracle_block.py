@@ -100,7 +100,9 @@ def test_memory_branch_readout_equals_sequential_definition():
     r, S_seq = OG.gated_delta_sequential(OG.l2_normalize(q), OG.l2_normalize(km), vm,
                                          torch.sigmoid(g_logit).transpose(1, 2),
                                          torch.sigmoid(b_logit).transpose(1, 2))
-    r = torch.nn.functional.rms_norm(r.transpose(1, 2), (64,)).reshape(1, 70, 256)
+    # per-head RMSNorm with the fp32 model's default epsilon (the fp64 oracle's convention)
+    r = torch.nn.functional.rms_norm(r.transpose(1, 2), (64,), eps=torch.finfo(torch.float32).eps)
+    r = r.reshape(1, 70, 256)
     ref = OB.linear(r * torch.sigmoid(OB.linear(x, sd, "mem.gate")), sd, "mem.proj")
     assert (out - ref).abs().max() < 1e-10
     assert (S - S_seq.transpose(-1, -2)).abs().max() < 1e-10
@@ -115,3 +117,25 @@ def test_window_only_changes_rows_past_the_window(window):
     b = OB.polar_attention(sd, x, H=4, Hkv=1, dk=64, window=None, mem=False)
     w = window or 20
     assert torch.allclose(a[:, :w], b[:, :w], atol=1e-6)
+
+
+def test_fp64_oracle_is_the_fp32_function():
+    """The fp64 block oracle (the gradient reference of the GPU training tests) computes
+    the fp32 model's function at higher precision: per-head RMSNorm keeps fp32's default
+    epsilon, so the memory's first rows (tiny readout) agree too."""
+    from atma_amd.layers.global_attention import GlobalBlock
+    torch.manual_seed(0)
+    dim, dk = 256, 64
+    blk = GlobalBlock(dim, head_dim=dk)
+    with torch.no_grad():
+        for n, p in blk.named_parameters():
+            if not n.startswith("norm"):
+                p.normal_(0.0, 0.02)
+            if n in ("attn.null_base", "attn.mag_beta_raw"):
+                p.normal_(0.0, 1.0)
+    sd = {k: v.detach().clone() for k, v in blk.state_dict().items()}
+    x = torch.randn(1, 200, dim, generator=torch.Generator().manual_seed(11))
+    o32 = OB.global_block(sd, x, H=dim // dk, Hkv=dim // dk // 4, dk=dk)
+    o64 = OB.global_block({k: v.double() for k, v in sd.items()}, x.double(), H=dim // dk,
+                          Hkv=dim // dk // 4, dk=dk)
+    assert (o32.double() - o64).abs().max().item() <= 5e-6
