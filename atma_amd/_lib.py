@@ -42,6 +42,10 @@ SIGNATURES = {
     "atma_polar_attention_decode": (_i32, [
         _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _i64, _p,
         _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i64, _f32, _p, _sz, _p]),
+    "atma_polar_decode_noalloc_max_bytes": (_sz, []),
+    "atma_polar_attention_decode_noalloc": (_i32, [
+        _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _i64, _p,
+        _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i64, _f32, _p]),
     "atma_gated_delta_decode_step": (_i32, [
         _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _p, _p,
         _i64, _i64, _i64, _i64, _i64, _i32, _f32, _p]),

@@ -23,6 +23,7 @@
 //  * pass 2 (merge): one workgroup per (sequence, query head) combines the live
 //    spans (m = max, rescale by 2^(m_i - m)), folds the null sink and writes c, mag.
 // The grid depends only on (B, Hq, max_pages): graph capturable.
+#include <mutex>
 #include "common.h"
 
 namespace atma {
@@ -602,4 +603,65 @@ extern "C" int atma_polar_attention_decode(
     case ATMA_F16: return d == 128 ? dispatch_gp<f16, 128>(a, s) : dispatch_gp<f16, 64>(a, s);
     default: return d == 128 ? dispatch_gp<float, 128>(a, s) : dispatch_gp<float, 64>(a, s);
   }
+}
+
+// ---------------------------------------------------------------------------------------
+// No-allocation variant.  The split records live in a file-scope device array instead of
+// a caller workspace.  Each GPU holds its own copy of the array (at its own address) from
+// the library's load until the process ends; the host keeps that address per device,
+// looked up once with hipGetSymbolAddress on the entry point's first call on the device.
+// Calls that overlap on one GPU share the array and race; nothing in it needs to start at
+// zero (every record the merge reads is written by the split pass of the same call).
+namespace atma {
+namespace {
+constexpr size_t kDecodeScratchBytes = size_t(16) << 20;
+__device__ __align__(256) unsigned char decode_scratch[kDecodeScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int decode_scratch_ptr(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(ATMA_ERR_HIP, "polar_attention_decode_noalloc: no current device");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(decode_scratch));
+    if (e != hipSuccess || !ptr)
+      return set_error(ATMA_ERR_HIP, "polar_attention_decode_noalloc: hipGetSymbolAddress: %s",
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return ATMA_OK;
+}
+}  // namespace
+}  // namespace atma
+
+extern "C" size_t atma_polar_decode_noalloc_max_bytes(void) { return atma::kDecodeScratchBytes; }
+
+extern "C" int atma_polar_attention_decode_noalloc(
+    const void* q, int64_t q_sb, int64_t q_sh, const void* k_cache, const void* v_cache,
+    int64_t num_pages, int64_t page_size, int64_t Hkv, const int32_t* block_tables, int64_t bt_sb,
+    int64_t max_pages, const int32_t* context_lens, const float* v_null, const float* null_base,
+    const float* null_slope_raw, const float* len_gain_raw, const float* mag_beta_raw, void* c,
+    void* mag, int64_t B, int64_t Hq, int64_t d, int dtype, int64_t window, float eps, void* stream) {
+  using namespace atma;
+  const size_t need = atma_polar_decode_workspace_bytes(B, Hq, max_pages, page_size, d);
+  if (need > kDecodeScratchBytes)
+    return set_error(ATMA_ERR_WORKSPACE,
+                     "polar_attention_decode_noalloc: this launch needs %zu bytes of split records, "
+                     "above the fixed scratch maximum of %zu bytes (use atma_polar_attention_decode "
+                     "with a workspace)", need, kDecodeScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = decode_scratch_ptr(&ws);
+    if (rc) return rc;
+  }
+  return atma_polar_attention_decode(q, q_sb, q_sh, k_cache, v_cache, num_pages, page_size, Hkv,
+                                     block_tables, bt_sb, max_pages, context_lens, v_null, null_base,
+                                     null_slope_raw, len_gain_raw, mag_beta_raw, c, mag, B, Hq, d, dtype,
+                                     window, eps, ws, need > 0 ? kDecodeScratchBytes : 0, stream);
 }

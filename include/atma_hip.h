@@ -199,6 +199,27 @@ int atma_polar_attention_decode(const void* q, int64_t q_sb, int64_t q_sh, const
                                 void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * No counterpart in the reference: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * atma_polar_attention_decode with the split records in a fixed file-scope device
+ * array of atma_polar_decode_noalloc_max_bytes() bytes (16 MiB) instead of a caller
+ * workspace; same arguments minus the workspace, same kernels, same results.  A launch
+ * whose records need more (atma_polar_decode_workspace_bytes) is rejected with
+ * ATMA_ERR_WORKSPACE.  Allocates nothing; every call on one GPU shares that GPU's array,
+ * so calls that overlap on one GPU race.
+ */
+size_t atma_polar_decode_noalloc_max_bytes(void);
+int atma_polar_attention_decode_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
+                                        const void* k_cache, const void* v_cache, int64_t num_pages,
+                                        int64_t page_size, int64_t Hkv, const int32_t* block_tables,
+                                        int64_t bt_sb, int64_t max_pages,
+                                        const int32_t* context_lens, const float* v_null,
+                                        const float* null_base, const float* null_slope_raw,
+                                        const float* len_gain_raw, const float* mag_beta_raw,
+                                        void* c, void* mag, int64_t B, int64_t Hq, int64_t d,
+                                        int dtype, int64_t window, float eps, void* stream);
+
+/*
  * One gated-delta decode step, IN PLACE on the slot-indexed fp32 state table.
  * Replaces gated_delta_decode_step (kernel/gated_delta_triton.py:78-117).
  * q: (B, H, d), k, v: (B, Hkv, d) with H % Hkv == 0, strides (x_sb, x_sh, 1) -- query

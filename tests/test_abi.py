@@ -189,3 +189,18 @@ def test_cpu_tensors_fail_loudly():
     q = torch.zeros(1, 2, 4, 128)
     with pytest.raises(RuntimeError, match="GPU only"):
         polar_attention_fwd(q, q, q, torch.arange(1, 5.0), **p)
+
+
+def test_noalloc_decode_rejects_requests_above_its_scratch(lib):
+    """The no-allocation decode refuses, before touching any device, a launch whose split
+    records exceed its fixed scratch array."""
+    cap = lib.atma_polar_decode_noalloc_max_bytes()
+    assert cap == 16 << 20
+    B, Hq, page, d = 4096, 8, 256, 128
+    max_pages = 256
+    assert lib.atma_polar_decode_workspace_bytes(B, Hq, max_pages, page, d) > cap
+    null = None
+    rc = lib.atma_polar_attention_decode_noalloc(null, 0, 0, null, null, 16, page, 2, null, 0, max_pages,
+                                                 null, null, null, null, null, null, null, null, B, Hq, d,
+                                                 1, 0, 1e-6, null)
+    assert rc == 3 and b"scratch maximum" in lib.atma_last_error()
