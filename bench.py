@@ -15,7 +15,7 @@ configs[3] (paged decode step: 64 sequences, ctx ~ U[1024, 32768], 256-token pag
 a shuffled pool, store_kvcache + Polar decode + gated-delta step, replayed as a HIP
 graph), each with its roofline fraction, plus the CPU oracle timed on this host.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c2|c3|c4|ops|train] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1|c2|c3|c4|ops|train|copy|cpu] [--no-cpu]
 """
 
 import argparse
@@ -299,9 +299,70 @@ def bench_memory_train(torch, dev, steps, warmup):
     return dict(B=B, T=T, ms_fwd_bwd=ms)
 
 
+def c1_state(torch, seed=0):
+    """one global block, hidden 1,024, 8 / 2 heads, d = 128, no window, memory
+    chunk 64; every parameter N(0, 0.02) from seed 0 (the reference's test convention,
+    tests/test_dense_prefill.py:105-106); input (1, 2048, 1024) N(0, 1) from seed 0.
+    Returns (the block module on the CPU, x)."""
+    from atma_amd.layers.global_attention import GlobalBlock
+    torch.manual_seed(seed)
+    blk = GlobalBlock(1024, head_dim=128, mem_chunk=CHUNK)
+    with torch.no_grad():
+        for p in blk.parameters():
+            p.normal_(0.0, 0.02)
+    x = torch.randn(1, 2048, 1024, generator=torch.Generator().manual_seed(seed))
+    return blk, x
+
+
+def _median_runs(fn, budget_s, min_runs=3, max_runs=10):
+    """1 warm-up, then timed runs until min_runs and the time budget are both spent."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_runs or (time.perf_counter() < t_end and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_c1(torch):
+    """BASELINE configs[0] on the host CPU: the oracle's global block (oracle/block.py, the
+    restatement of model/reference.py:127-233) in fp32 -- the mixer alone (Polar +
+    memory) and the whole block (+ norms, MLP) -- as tokens/s (median of >= 3 runs)."""
+    from oracle import block as OB
+    blk, x = c1_state(torch)
+    sd = {k: v.detach().clone() for k, v in blk.state_dict().items()}
+    attn_sd = {k[5:]: v for k, v in sd.items() if k.startswith("attn.")}
+    xn = OB.rms_norm_weighted(x, sd["norm1.weight"])
+    T = x.shape[1]
+    with torch.no_grad():
+        s_mix, n_mix = _median_runs(lambda: OB.polar_attention(attn_sd, xn, H=HQ, Hkv=HKV, dk=D), 8.0)
+        s_blk, n_blk = _median_runs(lambda: OB.global_block(sd, x, H=HQ, Hkv=HKV, dk=D), 8.0)
+    return {"mixer_tok_s": T / s_mix, "mixer_ms": s_mix * 1e3, "mixer_runs": n_mix,
+            "block_tok_s": T / s_blk, "block_ms": s_blk * 1e3, "block_runs": n_blk}
+
+
+def bench_c1_gpu(torch, dev, steps, warmup):
+    """configs[0] on the GPU, fp32 (the 1e-4 parity mode): the same block and input as
+    cpu_c1, forward only (the HIP kernels for Polar and the memory, eager glue), as
+    tokens/s for the mixer and the block."""
+    blk, x = c1_state(torch)
+    blk = blk.to(dev)
+    x = x.to(dev)
+    xn = blk.norm1(x)
+    T = x.shape[1]
+    with torch.no_grad():
+        ms_mix = _time(torch, lambda: blk.attn(xn), steps, warmup)
+        ms_blk = _time(torch, lambda: blk(x), steps, warmup)
+    return {"mixer_tok_s": T / (ms_mix * 1e-3), "mixer_ms": ms_mix, "block_tok_s": T / (ms_blk * 1e-3),
+            "block_ms": ms_blk, "dtype": "fp32"}
+
+
 def cpu_baseline(torch):
     """The CPU oracle (oracle/: Polar streaming form + gated-delta chunked UT form, fp32)
-    on a bounded sample of configs[1]: one of the 8 sequences, full T = 2048, all heads."""
+    on a bounded sample of configs[1]: one of the 8 sequences, full T = 2048, all heads;
+    plus configs[0] (the whole global block) as tokens/s."""
     from oracle import gated_delta as OG
     from oracle import polar as OP
     threads = len(os.sched_getaffinity(0))
@@ -322,14 +383,7 @@ def cpu_baseline(torch):
                                   torch.nn.functional.logsigmoid(zg + 3.9), torch.sigmoid(zb),
                                   scale=1.0, output_final_state=True, use_qk_l2norm_in_kernel=True)
 
-    run()
-    times = []
-    t_end = time.perf_counter() + 20.0
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 10):
-        t0 = time.perf_counter()
-        run()
-        times.append(time.perf_counter() - t0)
-    sec = statistics.median(times)
+    sec, runs = _median_runs(run, 12.0)
     flops = polar_flops(1, T) + gdn_flops(1, T)
     model = ""
     try:
@@ -341,8 +395,11 @@ def cpu_baseline(torch):
         pass
     return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
             "sample": f"configs[1] sequence 0 of 8 (B=1, T=2048, 8/2 heads, d=128), fp32 torch CPU, "
-                      f"median of {len(times)} runs = {sec:.3f} s",
-            "torch_threads": torch.get_num_threads(), "cpu_model": model}
+                      f"median of {runs} runs = {sec:.3f} s",
+            "torch_threads": torch.get_num_threads(), "cpu_model": model,
+            "c1": dict(cpu_c1(torch), workload="configs[0]: one global block (Polar + gated-delta "
+                                                "memory + MLP), B=1, T=2048, hidden 1024, 8/2 heads, "
+                                                "d=128, fp32, params N(0,0.02) seed 0")}
 
 
 def copy_calibration(torch, dev, steps):
@@ -371,7 +428,7 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["c2", "c3", "c4", "ops", "train", "copy"], default=None,
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "ops", "train", "copy", "cpu"], default=None,
                     help="one workload; 'copy' runs a plain 512 MiB device copy, the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--no-cpu", action="store_true")
@@ -393,6 +450,9 @@ def main(argv=None):
         out["copy"] = copy_calibration(torch, dev, args.steps)
         print(json.dumps(out))
         return 0
+    if args.only == "cpu":
+        print(json.dumps({"cpu_baseline": cpu_baseline(torch)}))
+        return 0
     if args.only in (None, "c2"):
         c2 = bench_prefill(torch, dev, 8, 2048, args.steps, args.warmup)
         print(f"# c2 prefill: {json.dumps(c2)}", file=sys.stderr, flush=True)
@@ -412,6 +472,10 @@ def main(argv=None):
         out["c4"] = [c4, c4w]
     if args.only == "train":
         out["train"] = bench_memory_train(torch, dev, max(3, args.steps // 4), 2)
+    if args.only in (None, "c1"):
+        c1 = bench_c1_gpu(torch, dev, max(3, args.steps // 2), 2)
+        print(f"# c1 block fp32 (GPU): {json.dumps(c1)}", file=sys.stderr, flush=True)
+        out["c1"] = c1
     if args.only in (None, "ops"):
         ops = bench_inference_ops(torch, dev, args.steps, args.warmup)
         print(f"# inference ops: {json.dumps(ops)}", file=sys.stderr, flush=True)
@@ -448,6 +512,7 @@ def main(argv=None):
                    for r in out["c4"]],
         "inference_ops": {n: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
                           for n, r in out["ops"].items()},
+        "block_c1_gpu": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out["c1"].items()},
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch)
