@@ -1,0 +1,297 @@
+"""Model runner of the paged engine (``inference/engine/model_runner.py:13-533``).
+
+It owns the device state of a serving process: the model, the per-sequence state
+tables (keys ``attn_{i}_{q,k,v}``, ``conv_{i}_gated``, ``mem_{i}``, as the reference,
+``:161-211``), one paged KV tensor ``(2, n_global, num_pages, page_size, Hkv, d)``
+(``:73-155``), and the decode step captured as HIP graphs per batch-size bucket
+(``:254-310``).  ``prepare_prefill`` / ``prepare_decode`` turn scheduled sequences into
+the device tensors and routing flags of the ``Context`` (``:316-480``); ``run`` runs the
+model and samples (``:491-533``).
+
+Differences from the reference, each deliberate:
+
+* The state tables carry one extra row (index ``max_num_seqs``) that no sequence owns.
+  Graph rows beyond the live batch point there, so a padded replay advances no real
+  sequence's conv / memory state (the reference leaves those rows' slots stale).
+* The tables are zeroed after warm-up and capture, whose dummy steps write into them.
+* The KV page count comes from ``Config.num_kvcache_blocks`` or, when -1, from
+  ``max_num_seqs x max_model_len`` within ``gpu_memory_utilization`` of free memory,
+  instead of a profiling prefill at the full batch budget.
+* The grouped (tile-mapped) Polar route is taken for 16-bit models only, the dtype its
+  kernel serves (``kernel/polar_triton.py:625-627``); fp32 ragged prompts take the
+  per-sequence route.
+"""
+
+from collections import deque
+
+import torch
+
+from ..layers.attention import Attention
+from .config import Config
+from .context import get_context, reset_context, set_context
+from .model import Atma, Sampler
+from .sequence import Sequence
+
+POLAR_TILE_ROWS = 128    # query rows per tile of the packed Polar launch
+
+
+class ModelRunner:
+
+    def __init__(self, config: Config, model: Atma = None):
+        self.config = config
+        hf = config.hf_config
+        self.block_size = config.kvcache_block_size
+        Sequence.block_size = config.kvcache_block_size
+        self.enforce_eager = config.enforce_eager
+        if not torch.cuda.is_available():
+            raise RuntimeError("ModelRunner serves on the GPU only (HIP kernels); no GPU is visible")
+        self.device = torch.device("cuda", torch.cuda.current_device())
+        if model is None:
+            model = Atma(hf)
+            if config.model:
+                from ..layers.loader import load_model
+                load_model(model, config.model, strict=config.strict_weights)
+            else:
+                model.init_weights(config.init_std, config.seed)
+        self.model = model.to(self.device, hf.dtype).eval()
+        self.sampler = Sampler()
+        self.last_logits = None
+        self.allocate_conv_state_tables()
+        self.allocate_kv_cache()
+        self.warmup_model()
+        if not self.enforce_eager:
+            self.capture_cudagraph()
+        self._zero_state_tables()
+
+    def exit(self):
+        for name in ("graphs", "graph_pool", "graph_vars"):
+            if hasattr(self, name):
+                delattr(self, name)
+        torch.cuda.synchronize(self.device)
+
+    # ------------------------------------------------------------------ state
+    def allocate_conv_state_tables(self):
+        hf = self.config.hf_config
+        rows = self.config.max_num_seqs + 1          # + the padding row no sequence owns
+        dev, dt = self.device, hf.dtype
+        kv_hidden = hf.num_key_value_heads * hf.head_dim
+        self.conv_state_tables = {}
+        for i in range(hf.num_hidden_layers):
+            if hf.is_attention_layer(i):
+                for s, dim in (("q", hf.hidden_size), ("k", kv_hidden), ("v", kv_hidden)):
+                    self.conv_state_tables[f"attn_{i}_{s}"] = torch.zeros(
+                        rows, dim, hf.attn_kernel_size - 1, device=dev, dtype=dt)
+                if hf.mem_enabled:
+                    self.conv_state_tables[f"mem_{i}"] = torch.zeros(
+                        rows, hf.num_attention_heads, hf.head_dim, hf.head_dim, device=dev, dtype=torch.float32)
+            else:
+                self.conv_state_tables[f"conv_{i}_gated"] = torch.zeros(
+                    rows, hf.hidden_size, hf.conv_kernel_size - 1, device=dev, dtype=dt)
+        self.pad_slot = self.config.max_num_seqs
+        self._free_slots = deque(range(self.config.max_num_seqs))
+
+    def _zero_state_tables(self):
+        for t in self.conv_state_tables.values():
+            t.zero_()
+
+    def allocate_kv_cache(self):
+        hf, cfg = self.config.hf_config, self.config
+        self.attn_modules = [m for m in self.model.modules() if isinstance(m, Attention)]
+        n_attn = len(self.attn_modules)
+        if n_attn == 0:
+            return
+        item = torch.empty((), dtype=hf.dtype).element_size()
+        page_bytes = 2 * n_attn * self.block_size * hf.num_key_value_heads * hf.head_dim * item
+        if cfg.num_kvcache_blocks <= 0:
+            want = cfg.max_num_seqs * ((cfg.max_model_len + self.block_size - 1) // self.block_size)
+            free, _ = torch.cuda.mem_get_info(self.device)
+            cap = int(free * cfg.gpu_memory_utilization) // page_bytes
+            cfg.num_kvcache_blocks = max(16, min(want, cap))
+        self.kv_cache = torch.zeros(2, n_attn, cfg.num_kvcache_blocks, self.block_size, hf.num_key_value_heads,
+                                    hf.head_dim, device=self.device, dtype=hf.dtype)
+        for idx, m in enumerate(self.attn_modules):
+            m.k_cache = self.kv_cache[0, idx]
+            m.v_cache = self.kv_cache[1, idx]
+
+    def alloc_seq_slot(self, seq: Sequence) -> int:
+        seq.seq_slot = self._free_slots.popleft()
+        return seq.seq_slot
+
+    def free_seq_slot(self, seq: Sequence):
+        """Release a sequence's table rows, zeroed for the next owner (``:205-211``)."""
+        if seq.seq_slot < 0:
+            return
+        for t in self.conv_state_tables.values():
+            t[seq.seq_slot].zero_()
+        self._free_slots.append(seq.seq_slot)
+        seq.seq_slot = -1
+
+    # ------------------------------------------------------------------ warm-up / graphs
+    def warmup_model(self):
+        """One short prefill and one decode step through every kernel (``:229-248``)."""
+        n = min(64, self.config.max_num_batched_tokens, self.config.max_model_len)
+        pre = Sequence([0] * n)
+        pre.num_scheduled_tokens = n
+        pre.block_table = list(range(min((n + self.block_size - 1) // self.block_size,
+                                         self.config.num_kvcache_blocks)))
+        dec = Sequence([0])
+        dec.num_scheduled_tokens = 1
+        dec.block_table = [0]
+        try:
+            self.run([pre], is_prefill=True)
+            self.free_seq_slot(pre)
+            self.run([dec], is_prefill=False)
+        finally:
+            for s in (pre, dec):
+                self.free_seq_slot(s)
+        torch.cuda.synchronize(self.device)
+
+    @torch.inference_mode()
+    def capture_cudagraph(self):
+        """The decode forward captured once per batch-size bucket (``:254-310``)."""
+        hf, cfg = self.config.hf_config, self.config
+        max_bs = cfg.max_num_seqs
+        max_blocks = (cfg.max_model_len + self.block_size - 1) // self.block_size
+        dev = self.device
+        gv = dict(input_ids=torch.zeros(max_bs, dtype=torch.int64, device=dev),
+                  positions=torch.zeros(max_bs, dtype=torch.int64, device=dev),
+                  slot_mapping=torch.full((max_bs,), -1, dtype=torch.int32, device=dev),
+                  context_lens=torch.zeros(max_bs, dtype=torch.int32, device=dev),
+                  block_tables=torch.zeros(max_bs, max_blocks, dtype=torch.int32, device=dev),
+                  seq_slots=torch.full((max_bs,), self.pad_slot, dtype=torch.int64, device=dev),
+                  outputs=torch.zeros(max_bs, hf.hidden_size, device=dev, dtype=hf.dtype))
+        self.graph_bs = sorted({b for b in [1, 2, 4, 8] + list(range(16, max_bs + 1, 16)) + [max_bs]
+                                if b <= max_bs})
+        self.graphs, self.graph_pool = {}, None
+        for bs in reversed(self.graph_bs):
+            graph = torch.cuda.CUDAGraph()
+            set_context(False, slot_mapping=gv["slot_mapping"][:bs], context_lens=gv["context_lens"][:bs],
+                        block_tables=gv["block_tables"][:bs], seq_slots=gv["seq_slots"][:bs],
+                        conv_state_tables=self.conv_state_tables)
+            gv["outputs"][:bs] = self.model(gv["input_ids"][:bs], gv["positions"][:bs])   # warm-up
+            with torch.cuda.graph(graph, self.graph_pool):
+                gv["outputs"][:bs] = self.model(gv["input_ids"][:bs], gv["positions"][:bs])
+            if self.graph_pool is None:
+                self.graph_pool = graph.pool()
+            self.graphs[bs] = graph
+            torch.cuda.synchronize(dev)
+            reset_context()
+        self.graph_vars = gv
+
+    # ------------------------------------------------------------------ inputs
+    def _to_dev(self, values, dtype):
+        t = torch.tensor(values, dtype=dtype)
+        if self.device.type != "cuda":
+            return t
+        return t.pin_memory().to(self.device, non_blocking=True)
+
+    def prepare_block_tables(self, seqs):
+        width = max(len(s.block_table) for s in seqs) if seqs else 0
+        return self._to_dev([s.block_table + [-1] * (width - len(s.block_table)) for s in seqs], torch.int32)
+
+    def prepare_prefill(self, seqs):
+        """Token ids, cache slots and the route of one prefill batch (``:328-449``)."""
+        input_ids, positions, slot_mapping = [], [], []
+        cu_q, cu_k = [0], [0]
+        max_q = max_k = 0
+        for seq in seqs:
+            start = seq.num_cached_tokens
+            end = start + seq.num_scheduled_tokens
+            input_ids.extend(seq[start:end])
+            positions.extend(range(start, end))
+            cu_q.append(cu_q[-1] + end - start)
+            cu_k.append(cu_k[-1] + end)
+            max_q, max_k = max(max_q, end - start), max(max_k, end)
+            for pos in range(start, end):     # page = block_table[pos // page_size], row = pos % page_size
+                slot_mapping.append(seq.block_table[pos // self.block_size] * self.block_size + pos % self.block_size)
+        seqlens = [cu_q[i + 1] - cu_q[i] for i in range(len(seqs))]
+        fresh = all(s.num_cached_tokens == 0 and s.num_scheduled_tokens == s.num_tokens for s in seqs)
+        within = sum(seqlens) <= self.config.max_num_batched_tokens
+        dense = len(seqs) > 1 and seqlens[0] > 0 and len(set(seqlens)) == 1 and fresh and within
+        grouped = (len(seqs) > 1 and not dense and all(n > 0 for n in seqlens) and fresh and within
+                   and self.config.hf_config.dtype in (torch.bfloat16, torch.float16))
+        block_tables = self.prepare_block_tables(seqs) if cu_k[-1] > cu_q[-1] else None
+        kw = {}
+        if fresh and all(n > 0 for n in seqlens):
+            # per-token (sequence start, end, table row): the packed convolutions' map
+            starts, ends, slots, packed = [], [], [], 0
+            for seq, n in zip(seqs, seqlens):
+                starts += [packed] * n
+                ends += [packed + n] * n
+                slots += [seq.seq_slot] * n
+                packed += n
+            kw.update(token_seq_starts=self._to_dev(starts, torch.int32), token_seq_ends=self._to_dev(ends, torch.int32),
+                      token_seq_slots=self._to_dev(slots, torch.int32))
+        if grouped:
+            ts, tq, tl, packed = [], [], [], 0
+            for n in seqlens:                 # one entry per 128-row query tile (:390-404)
+                for q0 in range(0, n, POLAR_TILE_ROWS):
+                    ts.append(packed)
+                    tq.append(q0)
+                    tl.append(n)
+                packed += n
+            kw.update(polar_tile_seq_starts=self._to_dev(ts, torch.int32),
+                      polar_tile_q_starts=self._to_dev(tq, torch.int32),
+                      polar_tile_seq_lens=self._to_dev(tl, torch.int32))
+        ctx = set_context(True, cu_seqlens_q=self._to_dev(cu_q, torch.int32),
+                          cu_seqlens_k=self._to_dev(cu_k, torch.int32), max_seqlen_q=max_q, max_seqlen_k=max_k,
+                          slot_mapping=self._to_dev(slot_mapping, torch.int32), block_tables=block_tables,
+                          seqlens_q=seqlens, conv_state_tables=self.conv_state_tables,
+                          seq_slots=self._to_dev([s.seq_slot for s in seqs], torch.int64),
+                          dense_prefill=dense, dense_batch_size=len(seqs) if dense else 0,
+                          dense_seq_len=seqlens[0] if dense else 0, grouped_polar_prefill=grouped, **kw)
+        ctx.seqs = seqs
+        return self._to_dev(input_ids, torch.int64), self._to_dev(positions, torch.int64)
+
+    def prepare_decode(self, seqs):
+        """One new token per sequence (``:451-480``): ``context_lens`` includes it, its cache
+        slot is the last page's next row."""
+        input_ids = [s.last_token for s in seqs]
+        positions = [len(s) - 1 for s in seqs]
+        context_lens = [len(s) for s in seqs]
+        slot_mapping = [s.block_table[-1] * self.block_size + s.last_block_num_tokens - 1 for s in seqs]
+        set_context(False, slot_mapping=self._to_dev(slot_mapping, torch.int32),
+                    context_lens=self._to_dev(context_lens, torch.int32),
+                    block_tables=self.prepare_block_tables(seqs), conv_state_tables=self.conv_state_tables,
+                    seq_slots=self._to_dev([s.seq_slot for s in seqs], torch.int64))
+        return self._to_dev(input_ids, torch.int64), self._to_dev(positions, torch.int64)
+
+    # ------------------------------------------------------------------ forward
+    @torch.inference_mode()
+    def run_model(self, input_ids, positions, is_prefill):
+        """Prefill eager; decode by replaying the smallest captured bucket that fits (``:491-513``)."""
+        bs = input_ids.size(0)
+        if is_prefill or self.enforce_eager or not hasattr(self, "graphs") or bs > self.config.max_num_seqs:
+            return self.model.compute_logits(self.model(input_ids, positions))
+        ctx = get_context()
+        graph = self.graphs[next(b for b in self.graph_bs if b >= bs)]
+        gv = self.graph_vars
+        gv["input_ids"][:bs] = input_ids
+        gv["positions"][:bs] = positions
+        gv["slot_mapping"].fill_(-1)
+        gv["slot_mapping"][:bs] = ctx.slot_mapping
+        gv["context_lens"].zero_()
+        gv["context_lens"][:bs] = ctx.context_lens
+        n_blocks = ctx.block_tables.size(1)
+        gv["block_tables"][:bs, :n_blocks] = ctx.block_tables
+        gv["block_tables"][:bs, n_blocks:].zero_()
+        gv["seq_slots"].fill_(self.pad_slot)
+        gv["seq_slots"][:bs] = ctx.seq_slots
+        graph.replay()
+        return self.model.compute_logits(gv["outputs"][:bs])
+
+    @torch.inference_mode()
+    def run(self, seqs, is_prefill):
+        """Schedule-step entry (``:520-533``): slots for new sequences, inputs, forward,
+        sampling; returns one token id per sequence.  ``last_logits`` keeps the step's
+        logits (one row per sequence)."""
+        for seq in seqs:
+            if seq.seq_slot < 0:
+                self.alloc_seq_slot(seq)
+        input_ids, positions = self.prepare_prefill(seqs) if is_prefill else self.prepare_decode(seqs)
+        temps = [s.temperature for s in seqs]
+        logits = self.run_model(input_ids, positions, is_prefill)
+        self.last_logits = logits
+        tok = self.sampler(logits, self._to_dev(temps, torch.float32), all_greedy=all(t == 0 for t in temps))
+        reset_context()
+        return tok.tolist()

@@ -39,8 +39,8 @@ from torch import nn
 
 from ..kernel import (StartSignal, causal_conv1d_decode_step, chunk_gated_delta_rule,
                       gated_delta_decode_step, gated_delta_gates, polar_attention, polar_attention_decode,
-                      polar_attention_fwd, recurrence_pays_to_overlap)
-from ..kernel.inference_ops import squared_relu_gate
+                      polar_attention_fwd, polar_attention_packed_fwd, recurrence_pays_to_overlap)
+from ..kernel.inference_ops import packed_causal_conv1d, squared_relu_gate
 from .attention import store_kvcache
 
 # Polar structural priors (model/reference.py:17-20)
@@ -206,6 +206,22 @@ class PolarAttention(nn.Module):
         return t + out.transpose(1, 2)
 
     @staticmethod
+    def _conv_packed(t, conv, tails, token_maps):
+        """Residual Canon conv over packed fresh sequences in one HIP launch
+        (``packed_causal_conv1d``, ``inference/models/atma.py:431-442``): t (tokens, C);
+        each sequence's last K-1 inputs go to its row of ``tails``."""
+        return t + packed_causal_conv1d(t, conv.weight.squeeze(1), tails, *token_maps)
+
+    @staticmethod
+    def dense_token_maps(B, T, slots):
+        """Per-token (sequence start, sequence end, table row) of B equal-length fresh
+        sequences packed along tokens (the engine's token map, ``inference/engine/
+        model_runner.py:390-404``, for the dense batch)."""
+        dev = slots.device
+        start = torch.arange(B, device=dev, dtype=torch.int32).repeat_interleave(T) * T
+        return start, start + T, slots.to(torch.int32).repeat_interleave(T)
+
+    @staticmethod
     def _conv_step(t, conv, tails, slots):
         """Residual conv for one new token per sequence, tails advanced in place
         (``_gpu_conv_step``, ``inference/models/atma.py:165-192``): one fused launch of
@@ -307,9 +323,10 @@ class PolarAttention(nn.Module):
         B, T, _ = x.shape
         H, Hkv, dk = self.num_heads, self.num_kv_heads, self.head_dim
         q, gate, k, v = self._project(x)
-        q = self._conv_prefill(q.reshape(B, T, H * dk), self.canon_q, cache.conv_q, slots).view(B, T, H, dk)
-        k = self._conv_prefill(k.reshape(B, T, Hkv * dk), self.canon_k, cache.conv_k, slots).view(B, T, Hkv, dk)
-        v = self._conv_prefill(v.reshape(B, T, Hkv * dk), self.canon_v, cache.conv_v, slots).view(B, T, Hkv, dk)
+        maps = self.dense_token_maps(B, T, slots)
+        q = self._conv_packed(q.reshape(B * T, H * dk), self.canon_q, cache.conv_q, maps).view(B, T, H, dk)
+        k = self._conv_packed(k.reshape(B * T, Hkv * dk), self.canon_k, cache.conv_k, maps).view(B, T, Hkv, dk)
+        v = self._conv_packed(v.reshape(B * T, Hkv * dk), self.canon_v, cache.conv_v, maps).view(B, T, Hkv, dk)
         store_kvcache(k.reshape(B * T, Hkv, dk), v.reshape(B * T, Hkv, dk), cache.k_cache, cache.v_cache,
                       slot_mapping)
         S0 = cache.mem_table[slots] if self.mem is not None else None
@@ -318,6 +335,41 @@ class PolarAttention(nn.Module):
             cache.mem_table[slots] = S
 
         return self._attend_prefill(x, q, gate, k, v, S0, sink)
+
+    def prefill_packed(self, x, cache: GlobalLayerCache, seq_lens, slots, slot_mapping, tile_maps, token_maps):
+        """Grouped fresh prefill of ragged prompts packed along tokens
+        (``inference/models/atma.py:431-507``): the Canon convs as one packed launch each
+        (tails written per sequence), the K/V rows to the pages, ONE tile-mapped Polar
+        launch over every sequence (``polar_attention_packed_fwd``, 16-bit inputs), and the
+        memory per sequence from its table state.
+
+        x: (tokens, dim) packed in sequence order; seq_lens: the B prompt lengths; slots: (B,)
+        int64 table rows; slot_mapping: (tokens,) int32 cache slots; tile_maps: (tile_seq_starts,
+        tile_q_starts, tile_seq_lens) int32 (one entry per 128-row query tile); token_maps:
+        (token_seq_starts, token_seq_ends, token_seq_slots) int32 (one entry per token)."""
+        total = x.shape[0]
+        H, Hkv, dk = self.num_heads, self.num_kv_heads, self.head_dim
+        q, gate, k, v = self._project(x)
+        q = self._conv_packed(q.reshape(total, H * dk), self.canon_q, cache.conv_q, token_maps).view(total, H, dk)
+        k = self._conv_packed(k.reshape(total, Hkv * dk), self.canon_k, cache.conv_k, token_maps).view(
+            total, Hkv, dk)
+        v = self._conv_packed(v.reshape(total, Hkv * dk), self.canon_v, cache.conv_v, token_maps).view(
+            total, Hkv, dk)
+        store_kvcache(k, v, cache.k_cache, cache.v_cache, slot_mapping)
+        c, mag = polar_attention_packed_fwd(q, k, v, *tile_maps, window=self.window, **self.polar_params())
+        out = self._combine(c, mag, gate)
+        if self.mem is not None:
+            parts, start = [], 0
+            for i, n in enumerate(int(t) for t in seq_lens):
+                sl = slots[i:i + 1]
+                seg = slice(start, start + n)
+                r, S = self.mem(x[seg][None], q[seg][None], k[seg][None], v[seg][None],
+                                initial_state=cache.mem_table[sl], output_final_state=True)
+                cache.mem_table[sl] = S
+                parts.append(r[0])
+                start += n
+            out = out + torch.cat(parts, 0)
+        return out
 
     def prefill_continue(self, x, cache: GlobalLayerCache, slots, slot_mapping, block_tables, cached):
         """Chunked-prefill continuation of B sequences by T tokens each

@@ -13,9 +13,12 @@ value = (Polar + gated-delta algorithmic FLOPs) / step time.
 Also reported in the same JSON line: configs[2] (B=1, T=65,536 and 262,144) and
 configs[3] (paged decode step: 64 sequences, ctx ~ U[1024, 32768], 256-token pages in
 a shuffled pool, store_kvcache + Polar decode + gated-delta step, replayed as a HIP
-graph), each with its roofline fraction, plus the CPU oracle timed on this host.
+graph), each with its roofline fraction; configs[4] (the 378M model served through the
+paged engine, 32 x 2,048-token prompts -> 256 greedy tokens: prefill / decode tok/s and
+wall time); configs[0] (one global block in fp32 on the GPU); plus the CPU oracle timed
+on this host (configs[1] sample and configs[0]).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1|c2|c3|c4|ops|train|copy|cpu] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1|c2|c3|c4|c5|ops|train|copy|cpu] [--no-cpu]
 """
 
 import argparse
@@ -359,6 +362,43 @@ def bench_c1_gpu(torch, dev, steps, warmup):
             "block_ms": ms_blk, "dtype": "fp32"}
 
 
+def bench_c5(torch, dev, n_prompts=32, prompt_len=2048, new_tokens=256, seed=0):
+    """the 378M ATMA (16 blocks, hidden 1,024, vocab 50,304; every
+    parameter N(0, 0.02) from seed 0; bf16) served through the paged engine: 32 prompts of
+    2,048 uniform random token ids (seed 0) -> 256 greedy tokens each, ignore_eos.  The
+    prompts prefill as one dense batch; decode replays the captured HIP graph.  Prefill and
+    decode tok/s are the engine's own (HIP events around each step, as the reference's
+    LLMEngine.generate); wall_s is the whole timed generate.  A short untimed generate on
+    the same prompts runs first (kernel and library warm-up at the full prefill shape)."""
+    from atma_amd.engine import AtmaConfig, Config, LLMEngine, SamplingParams
+    pages = (prompt_len + new_tokens + 255) // 256
+    cfg = Config(kvcache_block_size=256, max_num_seqs=n_prompts, max_num_batched_tokens=n_prompts * prompt_len,
+                 max_model_len=prompt_len + new_tokens, num_kvcache_blocks=n_prompts * pages + 8,
+                 init_std=0.02, seed=seed, hf_config=AtmaConfig())
+    t0 = time.perf_counter()
+    engine = LLMEngine(cfg)
+    t_init = time.perf_counter() - t0
+    g = torch.Generator().manual_seed(seed)
+    prompts = torch.randint(0, cfg.hf_config.vocab_size, (n_prompts, prompt_len), generator=g).tolist()
+    engine.generate(prompts, SamplingParams(temperature=0.0, max_tokens=2, ignore_eos=True))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    res = engine.generate(prompts, SamplingParams(temperature=0.0, max_tokens=new_tokens, ignore_eos=True))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    m = engine.last_metrics
+    n_params = sum(p.numel() for p in engine.model_runner.model.parameters())
+    assert all(len(r["token_ids"]) == new_tokens for r in res)
+    engine.exit()
+    del engine
+    torch.cuda.empty_cache()
+    return {"model_params": n_params, "requests": n_prompts, "prompt_len": prompt_len, "new_tokens": new_tokens,
+            "prefill_tok_s": m["prefill_throughput"], "decode_tok_s": m["decode_throughput"],
+            "prefill_ms": m["prefill_time"] * 1e3, "decode_ms_per_step": m["decode_time"] * 1e3 /
+            max(1, m["decode_tokens"] // n_prompts), "wall_s": wall, "init_s": t_init,
+            "prefill_tokens": m["prefill_tokens"], "decode_tokens": m["decode_tokens"]}
+
+
 def cpu_baseline(torch):
     """The CPU oracle (oracle/: Polar streaming form + gated-delta chunked UT form, fp32)
     on a bounded sample of configs[1]: one of the 8 sequences, full T = 2048, all heads;
@@ -428,7 +468,7 @@ def main(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "ops", "train", "copy", "cpu"], default=None,
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "c5", "ops", "train", "copy", "cpu"], default=None,
                     help="one workload; 'copy' runs a plain 512 MiB device copy, the "
                          "reference kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--no-cpu", action="store_true")
@@ -472,6 +512,10 @@ def main(argv=None):
         out["c4"] = [c4, c4w]
     if args.only == "train":
         out["train"] = bench_memory_train(torch, dev, max(3, args.steps // 4), 2)
+    if args.only in (None, "c5"):
+        c5 = bench_c5(torch, dev)
+        print(f"# c5 served 378M: {json.dumps(c5)}", file=sys.stderr, flush=True)
+        out["c5"] = c5
     if args.only in (None, "c1"):
         c1 = bench_c1_gpu(torch, dev, max(3, args.steps // 2), 2)
         print(f"# c1 block fp32 (GPU): {json.dumps(c1)}", file=sys.stderr, flush=True)
@@ -513,6 +557,7 @@ def main(argv=None):
         "inference_ops": {n: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
                           for n, r in out["ops"].items()},
         "block_c1_gpu": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out["c1"].items()},
+        "serve_c5": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out["c5"].items()},
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch)
