@@ -173,3 +173,83 @@ def test_block_fp32_gradients_vs_fp64_oracle(dev, overlap):
         if not e <= 1e-3:
             bad[name] = e
     assert not bad, bad
+
+
+def _packed_maps(lengths, slots, dev):
+    """The engine's tile map (one entry per 128-row query tile) and token map."""
+    ts, tq, tl, st, en, sl, packed = [], [], [], [], [], [], 0
+    for n, s in zip(lengths, slots):
+        for q0 in range(0, n, 128):
+            ts.append(packed)
+            tq.append(q0)
+            tl.append(n)
+        st += [packed] * n
+        en += [packed + n] * n
+        sl += [s] * n
+        packed += n
+    t = lambda v: torch.tensor(v, dtype=torch.int32, device=dev)  # noqa: E731
+    return (t(ts), t(tq), t(tl)), (t(st), t(en), t(sl))
+
+
+def _fresh_cache(attn, dev, dtype, pages=40, page=16, seqs=6):
+    from atma_amd.layers.global_attention import GlobalLayerCache
+    return GlobalLayerCache.allocate(attn, pages, page, max_seqs=seqs, device=dev, dtype=dtype)
+
+
+def _cache_state(cache):
+    return [cache.k_cache, cache.v_cache, cache.conv_q, cache.conv_k, cache.conv_v, cache.mem_table]
+
+
+def test_grouped_route_equals_dense_route(dev):
+    """Equal-length prompts through the grouped route (packed Canon convs, one tile-mapped
+    Polar launch, memory per sequence) and the dense route: the KV pages and conv tails come
+    from identical launches and agree bit for bit; the outputs and memory states agree to
+    the bf16 bar (the grouped route runs the memory's projections per sequence, GEMMs of
+    another row count whose library kernels may round differently)."""
+    attn = _block(seed=5).attn.to(dev, torch.bfloat16)
+    B, T, page = 3, 150, 16
+    x = torch.randn(B, T, DIM, generator=torch.Generator().manual_seed(7)).to(dev, torch.bfloat16)
+    slots = torch.tensor([4, 1, 2], device=dev)
+    smap = torch.arange(B * T, dtype=torch.int32, device=dev) + 37           # any distinct slots
+    with torch.no_grad():
+        dense_cache = _fresh_cache(attn, dev, torch.bfloat16)
+        ref = attn.prefill(x, dense_cache, slots, smap)
+        grouped_cache = _fresh_cache(attn, dev, torch.bfloat16)
+        tiles, tokens = _packed_maps([T] * B, slots.tolist(), dev)
+        out = attn.prefill_packed(x.reshape(B * T, DIM), grouped_cache, [T] * B, slots, smap, tiles, tokens)
+    assert rel_err(out.view(B, T, DIM).float(), ref.float()) <= 2e-2
+    g, d = _cache_state(grouped_cache), _cache_state(dense_cache)
+    for a, b in zip(g[:5], d[:5]):
+        assert torch.equal(a, b)
+    assert rel_err(g[5], d[5]) <= 2e-2
+
+
+def test_grouped_route_matches_per_sequence_route(dev):
+    """Ragged fresh prompts: the grouped route against the per-sequence route (each prompt
+    alone, ``prefill_continue`` with nothing cached), outputs and every state within the
+    bf16 bar, the KV pages within one bf16 rounding (the two routes' Canon convs round
+    once each, in different kernels) -- the reference's
+    tests/test_dense_prefill.py:148-204 pattern."""
+    attn = _block(seed=6).attn.to(dev, torch.bfloat16)
+    lengths = [3, 5, 130, 77]
+    slots = [2, 0, 5, 3]
+    total = sum(lengths)
+    x = torch.randn(total, DIM, generator=torch.Generator().manual_seed(8)).to(dev, torch.bfloat16)
+    smap = (torch.randperm(40 * 16, generator=torch.Generator().manual_seed(9))[:total]).int().to(dev)
+    slots_t = torch.tensor(slots, device=dev)
+    with torch.no_grad():
+        per_cache = _fresh_cache(attn, dev, torch.bfloat16)
+        parts, start = [], 0
+        for i, n in enumerate(lengths):
+            parts.append(attn.prefill_continue(x[start:start + n][None], per_cache, slots_t[i:i + 1],
+                                               smap[start:start + n], None, [0])[0])
+            start += n
+        ref = torch.cat(parts, 0)
+        grp_cache = _fresh_cache(attn, dev, torch.bfloat16)
+        tiles, tokens = _packed_maps(lengths, slots, dev)
+        out = attn.prefill_packed(x, grp_cache, lengths, slots_t, smap, tiles, tokens)
+    assert rel_err(out.float(), ref.float()) <= 2e-2
+    for a, b in zip(_cache_state(grp_cache)[2:], _cache_state(per_cache)[2:]):
+        assert rel_err(a.float(), b.float()) <= 2e-2
+    torch.testing.assert_close(grp_cache.k_cache, per_cache.k_cache)    # bf16 default: one rounding
+    torch.testing.assert_close(grp_cache.v_cache, per_cache.v_cache)
