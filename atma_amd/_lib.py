@@ -38,7 +38,7 @@ SIGNATURES = {
         _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64,
         _p, _p, _p, _p, _p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i64,
         _f32, _p]),
-    "atma_polar_decode_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64]),
+    "atma_polar_decode_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64, _i64, _i32]),
     "atma_polar_attention_decode": (_i32, [
         _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _i64, _i64, _p,
         _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _i64, _f32, _p, _sz, _p]),

@@ -236,7 +236,7 @@ def polar_attention_decode_op(q: Tensor, k_cache: Tensor, v_cache: Tensor, block
     max_pages = block_tables.shape[1]
     c = torch.empty((B, Hq, d), device=q.device, dtype=q.dtype)
     mag = torch.empty((B, Hq), device=q.device, dtype=q.dtype)
-    ws_bytes = lib.atma_polar_decode_workspace_bytes(B, Hq, max_pages, page, d)
+    ws_bytes = lib.atma_polar_decode_workspace_bytes(B, Hq, Hkv, max_pages, page, d, _lib.dtype_code(q.dtype))
     ws = torch.empty((max(ws_bytes, 4) // 4,), device=q.device, dtype=torch.float32)
     rc = lib.atma_polar_attention_decode(
         q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),

@@ -23,6 +23,7 @@
 //  * pass 2 (merge): one workgroup per (sequence, query head) combines the live
 //    spans (m = max, rescale by 2^(m_i - m)), folds the null sink and writes c, mag.
 // The grid depends only on (B, Hq, max_pages): graph capturable.
+#include <algorithm>
 #include <mutex>
 #include "common.h"
 
@@ -59,7 +60,8 @@ struct DecodeArgs {
   int window;
   float eps;
   int max_splits;
-  float* ws;  // [B][Hq][max_splits][D + 4]
+  float* ws;  // [B][Hq][max_splits][D + 4] (span split) or [NW + B*Hkv][G][D + 4] (balanced)
+  int nw;     // waves launched by the balanced split
 };
 
 __device__ __forceinline__ void span_of(int ctx, int window, int sp, int& t0, int& t1) {
@@ -519,12 +521,482 @@ __global__ void __launch_bounds__(256) polar_decode_merge_kernel(DecodeArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Length-balanced split (16-bit K/V, pages a multiple of 32 keys).
+//
+// The unit of work is one 32-key sub-block of one (sequence, KV head) pair, counted from
+// the window start rounded down to 32.  All KV heads of a sequence have the same number
+// of units, so the per-sequence prefix pre[b] orders the units as (b, head, sub-block).
+// Every workgroup recomputes pre[] in LDS from context_lens (so the launch depends only
+// on the shapes: graph capturable), and wave w of NW = min(waves launched, U) takes the
+// contiguous range [w U / NW, (w + 1) U / NW): every wave streams the same number of keys
+// (+-32) whatever the context lengths.  A wave keeps the online statistics of the pair it
+// is in; when its range moves to the next pair it writes the partial (m, L, Q2, acc) as
+// record w + sh (sh = b Hkv + h; injective over the pairs a wave touches, since the
+// ranges are ordered) and starts afresh.  The merge combines the records of waves
+// w_first(sh) .. w_last(sh).
+constexpr int kBalWaves = 2048;     // at most this many waves (512 workgroups of 4)
+constexpr int kBalMaxSeqs = 8192;   // sequences the in-LDS prefix holds
+
+// Balanced-split workspace: the unit prefix pre[0 .. B] (written by workgroup 0 of the
+// split, read by the merge) in a header of whole 256-byte blocks, then the records.
+__host__ __device__ __forceinline__ int64_t bal_header_floats(int64_t B) {
+  return ((B + 1) * 4 + 255) / 256 * 64;
+}
+
+__device__ __forceinline__ int bal_units(int ctx, int window) {
+  const int lo = window > 0 ? max(ctx - window, 0) : 0;
+  return ctx > lo ? (ctx - (lo & ~31) + 31) >> 5 : 0;
+}
+
+// Exclusive prefix over the sequences' unit counts into pre[0 .. B] (pre[B] = total);
+// the whole workgroup takes part, and a barrier ends it.
+__device__ void bal_prefix(const DecodeArgs& a, int* pre) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int E = (a.B + 255) / 256;
+  const int i0 = min(tid * E, a.B), i1 = min(i0 + E, a.B);
+  int sum = 0;
+  for (int i = i0; i < i1; ++i) sum += bal_units(a.ctx[i], a.window);
+  int incl = sum;  // inclusive scan within the wave
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += t;
+  }
+  __shared__ int wave_tot[4];
+  if (lane == 63) wave_tot[wave] = incl;
+  __syncthreads();
+  int base = 0;
+  for (int v = 0; v < wave; ++v) base += wave_tot[v];
+  int run = base + incl - sum;
+  for (int i = i0; i < i1; ++i) {
+    pre[i] = run;
+    run += bal_units(a.ctx[i], a.window);
+  }
+  if (tid == 255) pre[a.B] = base + incl;
+  __syncthreads();
+}
+
+template <typename T, int D, int GP>
+__global__ void __launch_bounds__(256, 2) polar_decode_balanced_kernel(DecodeArgs a) {
+  static_assert(sizeof(T) == 2, "balanced split: 16-bit K/V");
+  constexpr int DCH = D / 8;        // lanes per key row in the PV pass (8 dims each)
+  constexpr int KPI = 64 / DCH;     // keys per PV step
+  constexpr int SUBK = 32;          // keys per unit
+  constexpr int NT16 = SUBK / 16;   // 16-key MFMA tiles per unit
+  constexpr int NIT = SUBK / KPI;   // PV steps per unit
+  constexpr int EP = 8;             // 16-bit elements per 16-byte piece
+  constexpr int KV = D / 32;        // 16-byte K loads per lane per 16-key tile
+  __shared__ int pre[kBalMaxSeqs + 1];
+  __shared__ __attribute__((aligned(16))) float Ps[4][32][GP];
+  __shared__ float Alpha[4][GP];
+  // per wave, per unit of the current 63-unit chunk: pair, first key, physical page,
+  // context length of the pair's sequence.  Read back as one uniform 16-byte LDS load,
+  // whose wait (lgkmcnt) leaves the K / V loads in flight alone.
+  __shared__ __attribute__((aligned(16))) int uinfo[4][64][4];
+
+  bal_prefix(a, pre);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  if (blockIdx.x == 0) {  // publish the prefix for the merge
+    int* hdr = (int*)a.ws;
+    for (int i = tid; i <= a.B; i += 256) hdr[i] = pre[i];
+  }
+  const int U = a.Hkv * pre[a.B];
+  const int NW = min(a.nw, U);
+  const int w = blockIdx.x * 4 + wave;
+  if (w >= NW) return;  // no barrier follows
+  const int u_beg = (int)((int64_t)w * U / NW), u_end = (int)((int64_t)(w + 1) * U / NW);
+
+  const int col = lane & 15, grp4 = lane >> 4;
+  const int dch = lane % DCH, kg = lane / DCH;
+  const T* kc = (const T*)a.kc;
+  const T* vc = (const T*)a.vc;
+  const uint32_t row_bytes = (uint32_t)a.Hkv * D * sizeof(T);
+  const uint32_t page_bytes = (uint32_t)a.page_size * row_bytes;
+  const uint32_t k_voff = col * row_bytes + (uint32_t)(EP * grp4 * sizeof(T));
+  const uint32_t v_voff = kg * row_bytes + (uint32_t)(8 * dch * sizeof(T));
+  const int np32 = (int)min(a.num_pages, (int64_t)0x7fffffff);
+  const int64_t page_elems = (int64_t)a.page_size * a.Hkv * D;
+
+  // per-pair state
+  int cur = -1, cur_b = 0, t0 = 0, t1 = 0;
+  float m_run[4], l_part[4], q2_part[4], c1r[4];
+  float acc[GP][8];
+  u32x4 qa[KV];
+
+  auto setup = [&](int sh) {
+    cur = sh;
+    cur_b = sh / a.Hkv;
+    const int hk = sh - cur_b * a.Hkv;
+    const int ctx = __builtin_amdgcn_readfirstlane(a.ctx[cur_b]);
+    t0 = a.window > 0 ? max(ctx - a.window, 0) : 0;
+    t1 = ctx;
+    float n_cal = (float)ctx;
+    if (a.window > 0) n_cal = fminf(n_cal, (float)a.window);
+    const float logn = logf(fmaxf(n_cal, 1.f));
+    const float c1_col = (1.f + softplus(a.len_gain_raw[hk * a.G + (col < a.G ? col : 0)]) * logn) *
+                         kLog2e * (1.f / sqrtf((float)D));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) c1r[i] = __shfl(c1_col, (4 * grp4 + i) & 15, 64);
+    const bool ok = col < a.G;
+    const T* qp = (const T*)a.q + cur_b * a.q_sb + (int64_t)(hk * a.G + (ok ? col : 0)) * a.q_sh + EP * grp4;
+#pragma unroll
+    for (int s = 0; s < KV; ++s) qa[s] = ok ? *(const u32x4*)(qp + 4 * EP * s) : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      m_run[i] = kSentinel;
+      l_part[i] = 0.f;
+      q2_part[i] = 0.f;
+    }
+#pragma unroll
+    for (int r = 0; r < GP; ++r)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[r][e] = 0.f;
+    // q and the parameters arrive before the run starts (once per pair): otherwise the
+    // wait for them, the newest loads, would be merged into every iteration's wait for
+    // its K and drain the V loads in flight.  A compiler-visible s_waitcnt vmcnt(0)
+    // (expcnt / lgkmcnt fields at their maxima), so its wait bookkeeping sees q complete.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+  };
+  // this pair's partial statistics -> record (w + sh), one row per query head of the group
+  auto flush = [&]() {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int m = 8; m >= 1; m >>= 1) {
+        l_part[i] += __shfl_xor(l_part[i], m, 64);
+        q2_part[i] += __shfl_xor(q2_part[i], m, 64);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < GP; ++r)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+#pragma unroll
+        for (int m = DCH; m < 64; m <<= 1) acc[r][e] += __shfl_xor(acc[r][e], m, 64);
+      }
+    float* rec = a.ws + bal_header_floats(a.B) + (int64_t)(w + cur) * a.G * (D + 4);
+    if (col == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * grp4 + i;
+        if (r < a.G) {
+          rec[(int64_t)r * (D + 4) + 0] = m_run[i];
+          rec[(int64_t)r * (D + 4) + 1] = l_part[i];
+          rec[(int64_t)r * (D + 4) + 2] = q2_part[i];
+        }
+      }
+    }
+    if (kg == 0) {
+#pragma unroll
+      for (int r = 0; r < GP; ++r) {
+        if (r < a.G) {
+          float* dst = rec + (int64_t)r * (D + 4) + 4 + 8 * dch;
+          *(f32x4*)dst = f32x4{acc[r][0], acc[r][1], acc[r][2], acc[r][3]};
+          *(f32x4*)(dst + 4) = f32x4{acc[r][4], acc[r][5], acc[r][6], acc[r][7]};
+        }
+      }
+    }
+  };
+
+  // unit info of the chunk starting at unit c0, lane s -> unit c0 + s
+  auto fill = [&](int c0) {
+    const int u = c0 + lane;
+    int info_sh = 0, info_pos = 0, info_pg = -1, info_ctx = 0;
+    if (lane < 63 && u < u_end) {
+      int lo = 0, hi = a.B - 1;  // last b with Hkv pre[b] <= u (it has units; see above)
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (a.Hkv * pre[mid] <= u) lo = mid; else hi = mid - 1;
+      }
+      const int b = lo;
+      const int nb = pre[b + 1] - pre[b];
+      const int rr = u - a.Hkv * pre[b];
+      const int hk = rr / nb, j = rr - hk * nb;
+      const int ctx = a.ctx[b];
+      const int lw = a.window > 0 ? max(ctx - a.window, 0) : 0;
+      info_ctx = ctx;
+      info_sh = b * a.Hkv + hk;
+      info_pos = (lw & ~31) + SUBK * j;
+      const int lp = info_pos / a.page_size;
+      info_pg = lp < a.max_pages ? a.bt[(int64_t)b * a.bt_sb + lp] : -1;
+    }
+    *(int4*)&uinfo[wave][lane][0] = make_int4(info_sh, info_pos, info_pg, info_ctx);
+    wave_sync();
+  };
+  auto unit_info = [&](int s) {   // (pair, first key, page, ctx) of unit s, in scalar registers
+    const int4 v = *(const int4*)&uinfo[wave][s][0];
+    return make_int4(__builtin_amdgcn_readfirstlane(v.x), __builtin_amdgcn_readfirstlane(v.y),
+                     __builtin_amdgcn_readfirstlane(v.z), __builtin_amdgcn_readfirstlane(v.w));
+  };
+
+  bool kok[NT16];
+  u32x4 kb[NT16][KV];
+  bool vok[NIT];
+  u32x4 vb[NIT];
+  // unit s: buffer over its page (empty for a page outside the pool), the scalar offset
+  // of its first row plus the pair's head, and the key bounds [lw, ctx) of its sequence
+  auto unit_rsrc = [&](int s, const T* base, int& pos, int& lw, int& ctx, uint32_t& soff, bool& pg) {
+    const int4 ui = unit_info(s);
+    const int sh = ui.x;
+    pos = ui.y;
+    ctx = ui.w;
+    lw = a.window > 0 ? max(ctx - a.window, 0) : 0;
+    const int phys = ui.z;
+    pg = (phys >= 0) & (phys < np32);
+    const int hk = sh % a.Hkv;
+    soff = (uint32_t)(pos % a.page_size) * row_bytes + (uint32_t)(hk * D * sizeof(T));
+    return buffer_rsrc(base + (pg ? (int64_t)phys * page_elems : 0), pg ? page_bytes : 0u);
+  };
+  // K / V of unit s; keys outside [lw, ctx) of the unit's own sequence are flagged (one
+  // lane value against scalar bounds; constant offsets ride in the scalar offset)
+  auto load_k = [&](int s) {
+    int pos, lw, ctx;
+    uint32_t soff;
+    bool pg;
+    const auto rs = unit_rsrc(s, kc, pos, lw, ctx, soff, pg);
+#pragma unroll
+    for (int j = 0; j < NT16; ++j) {
+      const int rel = pos + 16 * j;
+      kok[j] = pg & (col >= lw - rel) & (col < ctx - rel);
+#pragma unroll
+      for (int q = 0; q < KV; ++q) kb[j][q] = buffer_load16(rs, k_voff, soff + 16u * j * row_bytes + 64u * q);
+    }
+  };
+  auto load_v = [&](int s) {
+    int pos, lw, ctx;
+    uint32_t soff;
+    bool pg;
+    const auto rs = unit_rsrc(s, vc, pos, lw, ctx, soff, pg);
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+      const int rel = pos + it * KPI;
+      vok[it] = pg & (kg >= lw - rel) & (kg < ctx - rel);
+      vb[it] = buffer_load16(rs, v_voff, soff + (uint32_t)(it * KPI) * row_bytes);
+    }
+  };
+
+  for (int c0 = u_beg; c0 < u_end; c0 += 63) {
+    fill(c0);
+    const int n = min(63, u_end - c0);
+    load_k(0);
+    load_v(0);
+    int s = 0;
+    while (s < n) {
+      // a run of units of one pair: its statistics start afresh unless the run
+      // continues the pair the previous chunk ended in
+      const int run_sh = unit_info(s).x;
+      if (run_sh != cur) {
+        if (cur >= 0) flush();
+        setup(run_sh);
+      }
+      for (; s < n && unit_info(s).x == run_sh; ++s) {
+      const int sb = unit_info(s).y;
+      // ---- S = Q K^T (rows = query heads of the group, columns = keys)
+      f32x4 sc[NT16];
+#pragma unroll
+      for (int j = 0; j < NT16; ++j) {
+        sc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < KV; ++q) sc[j] = mfma16x16x32<T>(qa[q], kb[j][q], sc[j]);
+      }
+      bool kok_cur[NT16];
+#pragma unroll
+      for (int j = 0; j < NT16; ++j) kok_cur[j] = kok[j];
+      const bool full = sb >= t0 && sb + SUBK <= t1 && vok[0] && vok[NIT - 1];
+      // K of unit s + 1 in flight during the softmax and PV.  Issued unconditionally: past
+      // the chunk's last unit the unit info holds page -1, an empty buffer that fetches
+      // nothing, and the compiler sees one fixed order of loads, so its waits stay partial.
+      load_k(s + 1);
+      float alpha_r[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < NT16; ++j) {
+          sc[j][i] = kok_cur[j] ? sc[j][i] : -INFINITY;
+          mx = fmaxf(mx, sc[j][i]);
+        }
+#pragma unroll
+        for (int m = 8; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+        const float m_new = fmaxf(m_run[i], mx * c1r[i]);
+        const float alpha = __builtin_amdgcn_exp2f(m_run[i] - m_new);
+        m_run[i] = m_new;
+        float ls = 0.f, qs = 0.f;
+#pragma unroll
+        for (int j = 0; j < NT16; ++j) {
+          const float pv = __builtin_amdgcn_exp2f(fmaf(sc[j][i], c1r[i], -m_new));
+          sc[j][i] = pv;
+          ls += pv;
+          qs = fmaf(pv, pv, qs);
+        }
+        l_part[i] = l_part[i] * alpha + ls;
+        q2_part[i] = q2_part[i] * alpha * alpha + qs;
+        alpha_r[i] = alpha;
+      }
+      if (4 * grp4 < GP) {
+#pragma unroll
+        for (int j = 0; j < NT16; ++j) *(f32x4*)&Ps[wave][16 * j + col][4 * grp4] = sc[j];
+        if (col == 0) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) Alpha[wave][4 * grp4 + i] = alpha_r[i];
+        }
+      }
+      wave_sync();
+      {
+        float al[GP];
+#pragma unroll
+        for (int r = 0; r < GP; ++r) al[r] = Alpha[wave][r];
+#pragma unroll
+        for (int r = 0; r < GP; ++r)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[r][e] *= al[r];
+      }
+#pragma unroll
+      for (int it = 0; it < NIT; ++it) {
+        const int kk = it * KPI + kg;
+        float vv[8];
+        unpack8(vb[it], vv, T{});
+        if (!full) {  // masked rows (even NaN) never enter the sums
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vv[e] = vok[it] ? vv[e] : 0.f;
+        }
+#pragma unroll
+        for (int r4 = 0; r4 < GP / 4; ++r4) {
+          const f32x4 p4 = *(const f32x4*)&Ps[wave][kk][4 * r4];
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[4 * r4 + rr][e] = fmaf(p4[rr], vv[e], acc[4 * r4 + rr][e]);
+        }
+      }
+      load_v(s + 1);
+      wave_sync();
+      }
+    }
+  }
+  if (cur >= 0) flush();
+}
+
+// One workgroup (256 threads) per (sequence, query head): combine the records of the
+// waves that streamed its pair (sh = b Hkv + h) in one pass -- each thread group keeps a
+// running max and rescales as it goes -- then fold the null sink.  The unit prefix comes
+// from the workspace header the split wrote.
+template <typename T, int D>
+__global__ void __launch_bounds__(256) polar_decode_balanced_merge_kernel(DecodeArgs a) {
+  constexpr int NG = 256 / D;
+  __shared__ float red[4];
+  __shared__ float s_part[NG][D];
+  __shared__ float s_mlq[NG][3];
+  const int bh = blockIdx.x;
+  const int b = bh / a.Hq, hq = bh % a.Hq;
+  const int hk = hq / a.G, r = hq - hk * a.G;
+  const int sh = b * a.Hkv + hk;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int* hdr = (const int*)a.ws;
+  const int ctx = a.ctx[b];
+  const int pb = hdr[b], nb = hdr[b + 1] - pb;
+  const int U = a.Hkv * hdr[a.B];
+  const int NW = min(a.nw, U);
+  int w0 = 0, w1 = -1;  // the waves that own this pair's units (none without keys)
+  if (nb > 0) {
+    const int64_t x0 = (int64_t)a.Hkv * pb + (int64_t)hk * nb;
+    w0 = (int)(((x0 + 1) * NW - 1) / U);
+    w1 = (int)(((x0 + nb) * NW - 1) / U);
+  }
+  const float* recs = a.ws + bal_header_floats(a.B);
+  const int grp = tid / D, d = tid % D;
+  float M = kSentinel, S = 0.f, L = 0.f, Q2 = 0.f;
+#pragma unroll 4
+  for (int wv = w0 + grp; wv <= w1; wv += NG) {
+    const float* rc = recs + ((int64_t)(wv + sh) * a.G + r) * (D + 4);
+    const float mi = rc[0];
+    const float mn = fmaxf(M, mi);
+    const float fo = exp2f(M - mn), fi = exp2f(mi - mn);
+    S = S * fo + rc[4 + d] * fi;
+    L = L * fo + rc[1] * fi;
+    Q2 = Q2 * fo * fo + rc[2] * fi * fi;
+    M = mn;
+  }
+  s_part[grp][d] = S;
+  if (d == 0) {
+    s_mlq[grp][0] = M;
+    s_mlq[grp][1] = L;
+    s_mlq[grp][2] = Q2;
+  }
+  __syncthreads();
+  const bool act = tid < D;
+  M = kSentinel;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) M = fmaxf(M, s_mlq[g][0]);
+  S = 0.f;
+  L = 0.f;
+  Q2 = 0.f;
+#pragma unroll
+  for (int g = 0; g < NG; ++g) {
+    const float f = exp2f(s_mlq[g][0] - M);
+    S += s_part[g][d] * f;
+    L += s_mlq[g][1] * f;
+    Q2 += s_mlq[g][2] * f * f;
+  }
+  float n_cal = (float)ctx;
+  if (a.window > 0) n_cal = fminf(n_cal, (float)a.window);
+  n_cal = fmaxf(n_cal, 1.f);
+  const float temp = 1.f + softplus(a.len_gain_raw[hq]) * logf(n_cal);
+  const float nullv = a.null_base[hq] + softplus(a.null_slope_raw[hq]) * sqrtf(logf(n_cal + 1.f));
+  const float an2 = temp * nullv * kLog2e;
+  const float mn = fmaxf(M, an2);
+  const float al = exp2f(M - mn);
+  L *= al;
+  Q2 *= al * al;
+  const float pn = exp2f(an2 - mn);
+  const float Z = L + pn;
+  const float sv = act ? S * al + pn * a.v_null[(int64_t)hq * D + d] : 0.f;
+  const float ss_w = wave_sum(sv * sv);
+  if (lane == 0) red[wave] = ss_w;
+  __syncthreads();
+  float ss = 0.f;
+#pragma unroll
+  for (int v = 0; v < D / 64; ++v) ss += red[v];
+  const float inv = 1.f / fmaxf(sqrtf(ss), a.eps);
+  if (act) ((T*)a.c)[((int64_t)b * a.Hq + hq) * D + d] = (T)(sv * inv);
+  if (tid == 0) {
+    const float n_eff = L * L / fmaxf(Q2, 1e-30f);
+    const float m_eff = n_eff * (L / fmaxf(Z, a.eps));
+    const float beta = softplus(a.mag_beta_raw[hq]);
+    ((T*)a.mag)[(int64_t)b * a.Hq + hq] = (T)tanhf(beta * log1pf(m_eff));
+  }
+}
+
 static int max_splits_for(int64_t max_pages, int64_t page_size) {
   return (int)((max_pages * page_size + kSplitTokens - 1) / kSplitTokens);
 }
 
+// The balanced split serves 16-bit caches whose pages hold whole 32-key units; the span
+// split serves the rest (fp32, other page sizes, more sequences than the LDS prefix holds).
+static bool use_balanced(int dtype, int64_t page_size, int64_t B) {
+  return (dtype == ATMA_BF16 || dtype == ATMA_F16) && page_size % 32 == 0 && B <= kBalMaxSeqs;
+}
+
+// Waves the balanced split launches: enough for every unit a shape can hold, at most
+// kBalWaves (a function of the shapes only, so a captured graph stays valid).
+static int balanced_waves(int64_t B, int64_t Hkv, int64_t max_pages, int64_t page_size) {
+  const int64_t units = B * Hkv * ((max_pages * page_size + 31) / 32);
+  return (int)(4 * std::min<int64_t>(kBalWaves / 4, (units + 3) / 4));
+}
+
 template <typename T, int D, int GP>
 static int launch_decode(DecodeArgs a, hipStream_t s) {
+  if constexpr (sizeof(T) == 2) {
+    if (a.nw > 0) {  // balanced split (chosen by the host; nw = waves launched)
+      polar_decode_balanced_kernel<T, D, GP><<<dim3((unsigned)(a.nw / 4)), dim3(256), 0, s>>>(a);
+      int rc = check_launch("polar_attention_decode(balanced split)");
+      if (rc) return rc;
+      polar_decode_balanced_merge_kernel<T, D><<<dim3((unsigned)(a.B * a.Hq)), dim3(256), 0, s>>>(a);
+      return check_launch("polar_attention_decode(balanced merge)");
+    }
+  }
   if (a.max_splits > 0) {
     const dim3 grid((unsigned)(a.B * a.Hkv), (unsigned)a.max_splits);
     if (a.page_size % 32 == 0)
@@ -547,9 +1019,14 @@ static int dispatch_gp(DecodeArgs a, hipStream_t s) {
 
 }  // namespace atma
 
-extern "C" size_t atma_polar_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t max_pages,
-                                                    int64_t page_size, int64_t d) {
-  if (B <= 0 || Hq <= 0 || max_pages <= 0 || page_size <= 0 || d <= 0) return 0;
+extern "C" size_t atma_polar_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_pages,
+                                                    int64_t page_size, int64_t d, int dtype) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv || max_pages <= 0 || page_size <= 0 || d <= 0) return 0;
+  if (atma::use_balanced(dtype, page_size, B)) {
+    // one (m, L, Q2, pad, acc[d]) row per query head of each (wave, pair) record
+    const int64_t nw = atma::balanced_waves(B, Hkv, max_pages, page_size);
+    return (size_t)(atma::bal_header_floats(B) + (nw + B * Hkv) * (Hq / Hkv) * (d + 4)) * sizeof(float);
+  }
   return (size_t)B * Hq * atma::max_splits_for(max_pages, page_size) * (d + 4) * sizeof(float);
 }
 
@@ -581,7 +1058,7 @@ extern "C" int atma_polar_attention_decode(
   if ((uintptr_t)q % 16 || (q_sb * es) % 16 || (q_sh * es) % 16 || (uintptr_t)k_cache % 16 ||
       (uintptr_t)v_cache % 16)
     return set_error(ATMA_ERR_INVALID, "polar_attention_decode: tensors must be 16-byte aligned");
-  const size_t need = atma_polar_decode_workspace_bytes(B, Hq, max_pages, page_size, d);
+  const size_t need = atma_polar_decode_workspace_bytes(B, Hq, Hkv, max_pages, page_size, d, dtype);
   if (need > 0 && (!workspace || workspace_bytes < need))
     return set_error(ATMA_ERR_WORKSPACE, "polar_attention_decode: workspace %zu < %zu bytes",
                      workspace_bytes, need);
@@ -597,6 +1074,7 @@ extern "C" int atma_polar_attention_decode(
   a.window = window > 0 ? (int)window : 0; a.eps = eps;
   a.max_splits = max_splits_for(max_pages, page_size);
   a.ws = (float*)workspace;
+  a.nw = (max_pages > 0 && use_balanced(dtype, page_size, B)) ? balanced_waves(B, Hkv, max_pages, page_size) : 0;
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
     case ATMA_BF16: return d == 128 ? dispatch_gp<bf16, 128>(a, s) : dispatch_gp<bf16, 64>(a, s);
@@ -614,7 +1092,7 @@ extern "C" int atma_polar_attention_decode(
 // zero (every record the merge reads is written by the split pass of the same call).
 namespace atma {
 namespace {
-constexpr size_t kDecodeScratchBytes = size_t(16) << 20;
+constexpr size_t kDecodeScratchBytes = size_t(32) << 20;
 __device__ __align__(256) unsigned char decode_scratch[kDecodeScratchBytes];
 
 constexpr int kMaxDevices = 64;
@@ -649,7 +1127,7 @@ extern "C" int atma_polar_attention_decode_noalloc(
     const float* null_slope_raw, const float* len_gain_raw, const float* mag_beta_raw, void* c,
     void* mag, int64_t B, int64_t Hq, int64_t d, int dtype, int64_t window, float eps, void* stream) {
   using namespace atma;
-  const size_t need = atma_polar_decode_workspace_bytes(B, Hq, max_pages, page_size, d);
+  const size_t need = atma_polar_decode_workspace_bytes(B, Hq, Hkv, max_pages, page_size, d, dtype);
   if (need > kDecodeScratchBytes)
     return set_error(ATMA_ERR_WORKSPACE,
                      "polar_attention_decode_noalloc: this launch needs %zu bytes of split records, "

@@ -172,10 +172,11 @@ int atma_polar_attention_bwd(const void* q, int64_t q_sb, int64_t q_sh, int64_t 
                              int64_t window, void* stream);
 
 /*
- * Workspace bytes atma_polar_attention_decode needs for this launch shape.
+ * Workspace bytes atma_polar_attention_decode needs for this launch shape (a function of
+ * the shapes and dtype only, never of the context lengths).
  */
-size_t atma_polar_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t max_pages,
-                                         int64_t page_size, int64_t d);
+size_t atma_polar_decode_workspace_bytes(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_pages,
+                                         int64_t page_size, int64_t d, int dtype);
 
 /*
  * Paged Polar GQA decode (split-K over pages + merge).  Replaces
@@ -202,7 +203,7 @@ int atma_polar_attention_decode(const void* q, int64_t q_sb, int64_t q_sh, const
  * No counterpart in the reference: for callers that cannot allocate device memory
  * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * atma_polar_attention_decode with the split records in a fixed file-scope device
- * array of atma_polar_decode_noalloc_max_bytes() bytes (16 MiB) instead of a caller
+ * array of atma_polar_decode_noalloc_max_bytes() bytes (32 MiB) instead of a caller
  * workspace; same arguments minus the workspace, same kernels, same results.  A launch
  * whose records need more (atma_polar_decode_workspace_bytes) is rejected with
  * ATMA_ERR_WORKSPACE.  Allocates nothing; every call on one GPU shares that GPU's array,

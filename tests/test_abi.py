@@ -52,12 +52,21 @@ def test_validation_rejects_without_launch(lib):
                                          null, 0, null)
     assert rc == 1
     # decode workspace too small
-    # one (m, L, Q2, pad, acc[d]) fp32 record per (sequence, query head, span)
-    need = lib.atma_polar_decode_workspace_bytes(2, 8, 4, 256, 128)
+    # span split (fp32): one (m, L, Q2, pad, acc[d]) fp32 record per (sequence, query head, span)
+    need = lib.atma_polar_decode_workspace_bytes(2, 8, 2, 4, 256, 128, 0)
     rec = 2 * 8 * (128 + 4) * 4
     assert need > 0 and need % rec == 0
-    assert lib.atma_polar_decode_workspace_bytes(2, 8, 128, 256, 128) >= need
-    assert lib.atma_polar_decode_workspace_bytes(2, 8, 0, 256, 128) == 0
+    assert lib.atma_polar_decode_workspace_bytes(2, 8, 2, 128, 256, 128, 0) >= need
+    assert lib.atma_polar_decode_workspace_bytes(2, 8, 2, 0, 256, 128, 0) == 0
+    # balanced split (16-bit, pages of 32-key multiples): (waves + B * Hkv) records of G rows;
+    # waves = 4 * min(512, ceil(units / 4)) with units = B * Hkv * ceil(max_pages * page / 32)
+    # after a header of whole 256-byte blocks holding the B + 1 prefix entries
+    row = (128 + 4) * 4
+    assert lib.atma_polar_decode_workspace_bytes(2, 8, 2, 4, 256, 128, 1) == 256 + (128 + 4) * 4 * row
+    assert lib.atma_polar_decode_workspace_bytes(64, 8, 2, 128, 256, 128, 1) == 512 + (2048 + 128) * 4 * row
+    # a page size that is not a multiple of 32 keys takes the span split
+    assert lib.atma_polar_decode_workspace_bytes(2, 8, 2, 4, 16, 128, 1) == \
+        lib.atma_polar_decode_workspace_bytes(2, 8, 2, 4, 16, 128, 0)
     buf = ctypes.create_string_buffer(16)
     rc = lib.atma_polar_attention_decode(buf, 8, 8, buf, buf, 4, 256, 2, buf, 4, 4, buf, buf, buf,
                                          buf, buf, buf, buf, buf, 2, 8, 128, 1, 0, 1e-6, buf, 16, null)
@@ -195,12 +204,12 @@ def test_noalloc_decode_rejects_requests_above_its_scratch(lib):
     """The no-allocation decode refuses, before touching any device, a launch whose split
     records exceed its fixed scratch array."""
     cap = lib.atma_polar_decode_noalloc_max_bytes()
-    assert cap == 16 << 20
+    assert cap == 32 << 20
     B, Hq, page, d = 4096, 8, 256, 128
     max_pages = 256
-    assert lib.atma_polar_decode_workspace_bytes(B, Hq, max_pages, page, d) > cap
+    assert lib.atma_polar_decode_workspace_bytes(B, Hq, 2, max_pages, page, d, 0) > cap
     null = None
     rc = lib.atma_polar_attention_decode_noalloc(null, 0, 0, null, null, 16, page, 2, null, 0, max_pages,
                                                  null, null, null, null, null, null, null, null, B, Hq, d,
-                                                 1, 0, 1e-6, null)
+                                                 0, 0, 1e-6, null)
     assert rc == 3 and b"scratch maximum" in lib.atma_last_error()

@@ -147,3 +147,33 @@ def test_full_size_decode_bf16(dev):
     sample = [0, 1, 17, 33, 63]
     c_ref, m_ref = _oracle(q[sample].float(), kc, vc, bt[sample], ctx[sample], p)
     assert rel_err(c[sample], c_ref) <= 2e-2 and rel_err(m[sample], m_ref) <= 2e-2
+
+
+@pytest.mark.parametrize("dtype,page", [(torch.bfloat16, 32), (torch.float16, 256), (torch.bfloat16, 256)])
+@pytest.mark.parametrize("Hq,Hkv", [(8, 2), (16, 2), (8, 8), (4, 1)])
+def test_balanced_split_16bit(dev, dtype, page, Hq, Hkv):
+    """The length-balanced split (16-bit caches, pages of whole 32-key units): waves take
+    equal unit ranges across ragged, empty and windowed contexts and flush a record per
+    (sequence, KV head) they touch; NaN-poisoned unused pages are never read."""
+    ctx = [0, 1, 31, 32, 33, 700, 2049, 64, 0, 5000]
+    d = 128
+    q, kc, vc, bt, c_ = _paged(len(ctx), Hq, Hkv, d, ctx, page, dtype, seed=Hq + Hkv + page)
+    p = polar_params(Hq, d, seed=Hq + 5)
+    for window in (None, 100, 1500):
+        c, m = _run(dev, q, kc, vc, bt, c_, p, window=window)
+        c_ref, m_ref = _oracle(q.float(), kc.float(), vc.float(), bt, c_, p, window=window)
+        assert torch.isfinite(c.float()).all() and torch.isfinite(m.float()).all()
+        assert rel_err(c, c_ref) <= 2e-2 and rel_err(m, m_ref) <= 2e-2, window
+        assert m[0].abs().max() == 0 and m[8].abs().max() == 0      # empty contexts drain to the sink
+
+
+def test_balanced_split_many_short_sequences(dev):
+    """More sequences than waves' worth of units per pair: each wave crosses many
+    (sequence, KV head) boundaries; ragged contexts of a few units each."""
+    g = torch.Generator().manual_seed(21)
+    ctx = torch.randint(0, 200, (300,), generator=g).tolist()
+    q, kc, vc, bt, c_ = _paged(300, 8, 2, 128, ctx, 64, torch.bfloat16, seed=21)
+    p = polar_params(8, 128, seed=21)
+    c, m = _run(dev, q, kc, vc, bt, c_, p)
+    c_ref, m_ref = _oracle(q.float(), kc.float(), vc.float(), bt, c_, p)
+    assert rel_err(c, c_ref) <= 2e-2 and rel_err(m, m_ref) <= 2e-2
