@@ -132,6 +132,15 @@ __device__ __forceinline__ void dma_buf16(__amdgpu_buffer_rsrc_t r, uint32_t vof
                : "memory");
 }
 
+// The same copy with the LDS destination given as a wave-uniform byte offset (for
+// callers that keep their LDS bases in scalar registers).
+__device__ __forceinline__ void dma_buf16_at(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                             uint32_t lds_byte_offset) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff),
+               "{m0}"(__builtin_amdgcn_readfirstlane(lds_byte_offset))
+               : "memory");
+}
+
 // 4 bytes per lane (buffer_load_dword ... lds): lane i's dword lands at lds_wave_base + 4*i.
 __device__ __forceinline__ void dma_buf4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
                                          const void* lds_wave_base) {

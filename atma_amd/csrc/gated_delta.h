@@ -60,31 +60,22 @@ __device__ __forceinline__ float gdn_load_beta(const GdnArgs& a, int64_t i) {
   return a.gate_logits ? gdn_write_strength(a.beta[i], a.b_bias) : a.beta[i];
 }
 
-// Workspace of the 16-bit path: for each of the n = B*H*NC (sequence, head, chunk)
-// records, these fields, each stored as its own array [n][...] so that consecutive
-// chunks of one head are adjacent in memory (element offsets in 16-bit units; C = 64
-// tokens, D = head dim):
-//   w   [C][D]  T diag(beta * ge) Kn      (the state's pull on each row's update)
-//   us  [D/32][4][64][8]  u = T diag(beta) V in the scan's register order: for column
-//               slab s, wave w, lane l = 16 g + c, entries vt*4 + i hold u at token
-//               16 w + 4 g + i, column 32 s + 16 vt + c (one 16-byte load per lane)
-//   rq  [C][C]  exp(lg_p - lg_s) qn_p . kn_s for s <= p, else 0
-//   f32 [3][C]  per token (fp32; f32_byte is a byte offset): lg, the inclusive
-//               log-decays; kf = exp(lg_C - lg) / |k| (the write-back weight of the raw
-//               key row, 1 / |k| only with l2norm); qs = scale / |q| (the raw query row's
-//               factor, 1 / |q| only with l2norm)
-// T = (I + A)^-1 with A[p,s] = beta_p exp(lg_p - lg_s) kn_p . kn_s (s < p), ge_p = exp(lg_p).
-// The scan reads q and k rows straight from the inputs and applies qs and kf itself.
-struct Gdn16Ws {
-  int D;
-  int64_t n;
-  __host__ __device__ constexpr int64_t cd() const { return (int64_t)kChunk * D; }
-  __host__ __device__ constexpr int64_t w(int64_t i) const { return i * cd(); }
-  __host__ __device__ constexpr int64_t us(int64_t i) const { return (n + i) * cd(); }
-  __host__ __device__ constexpr int64_t rq(int64_t i) const { return 2 * n * cd() + i * kChunk * kChunk; }
-  __host__ __device__ constexpr int64_t f32_byte(int64_t i) const { return rq(n) * 2 + i * 3 * kChunk * 4; }
-  __host__ __device__ constexpr int64_t bytes() const { return f32_byte(n); }
-};
+// Workspace of the 16-bit path: one record of kGdn16RecBytes per (sequence, head, chunk)
+// item, item = (b * H + h) * NC + chunk, written by the prep kernel and copied whole into
+// LDS by the scan.  With C = 64 tokens, T = (I + A)^-1, A[p,s] = beta_p exp(lg_p - lg_s)
+// kn_p . kn_s (s < p) and Rq[p,s] = exp(lg_p - lg_s) qn_p . kn_s (s <= p):
+//   Tb  [6][64 lanes][8]  T diag(beta), lower 16 x 32 blocks as MFMA A fragments: fragment
+//       f = (P, j) in the order (0,0) (1,0) (2,0) (2,1) (3,0) (3,1); lane (g, r) holds row
+//       16 P + r, columns 32 j + 4 g + [0, 4) and 32 j + 16 + 4 g + [0, 4)
+//   Rb  [6][64 lanes][8]  Rq in the same fragment order: lane (g, c) holds row 16 P + c,
+//       columns 32 j + 4 g + [0, 4) and 32 j + 16 + 4 g + [0, 4) (the MFMA B operand of
+//       U^T Rq^T)
+//   F   [4][64] fp32  per token: kf = exp(lg_C - lg) ik (the key row's write-back weight),
+//       geik = exp(lg) ik (its weight in the state readout), geqs = exp(lg) iq (the query
+//       row's weight, scale included); F[3][0] = exp(lg_C)
+// with ik = 1 / |k|, iq = scale / |q| (1 and scale without l2norm; 0 past T) and lg the
+// inclusive log-decays (13 KiB in all).
+constexpr int kGdn16Tb = 0, kGdn16Rb = 6144, kGdn16F = 12288, kGdn16RecBytes = 13312;
 
 int launch_gdn16(const GdnArgs& a, int dtype, int D, hipStream_t stream);
 

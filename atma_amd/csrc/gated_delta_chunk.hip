@@ -331,7 +331,7 @@ extern "C" size_t atma_chunk_gated_delta_workspace_bytes(int64_t B, int64_t T, i
   if (B <= 0 || T <= 0 || H <= 0 || chunk != atma::kChunk || (dk != 64 && dk != 128)) return 0;
   const int64_t nc = (T + chunk - 1) / chunk;
   if (dtype == ATMA_BF16 || dtype == ATMA_F16)
-    return (size_t)atma::Gdn16Ws{(int)dk, B * H * nc}.bytes();
+    return (size_t)(B * H * nc) * (size_t)atma::kGdn16RecBytes;
   const int64_t rec = 5 * chunk * dk + 4;
   return (size_t)(B * H * nc * rec) * sizeof(float);
 }
@@ -367,9 +367,10 @@ extern "C" int atma_chunk_gated_delta_rule(
     return set_error(ATMA_ERR_INVALID, "chunk_gated_delta_rule: null pointer");
   if (es == 2 && T * H * dk * 2 >= (1ll << 32))  // one sequence's output rows form one buffer
     return set_error(ATMA_ERR_UNSUPPORTED, "chunk_gated_delta_rule: T*H*d too large for one sequence");
-  if (es == 2 && (q_st >= (1 << 24) || k_st >= (1 << 24) || q_st < dk || k_st < dk))
-    // the scan copies a chunk's q / k rows through one buffer descriptor each
-    return set_error(ATMA_ERR_UNSUPPORTED, "chunk_gated_delta_rule: q/k token stride out of range");
+  if (es == 2 && (q_st >= (1 << 24) || k_st >= (1 << 24) || v_st >= (1 << 24) || q_st < dk || k_st < dk ||
+                  v_st < dv))
+    // the kernels copy a chunk's q / k / v rows through one buffer descriptor each
+    return set_error(ATMA_ERR_UNSUPPORTED, "chunk_gated_delta_rule: q/k/v token stride out of range");
   const size_t need = atma_chunk_gated_delta_workspace_bytes(B, T, H, dk, dv, chunk, dtype);
   if (!workspace || workspace_bytes < need)
     return set_error(ATMA_ERR_WORKSPACE, "chunk_gated_delta_rule: workspace %zu < %zu bytes",

@@ -2,29 +2,35 @@
 //
 // Algebra of gated_delta_chunked (model/blocks.py:375-423; FLA convention: decay
 // first, undecayed write, self-inclusive readout).  Inside a 64-token chunk with
-// inclusive log-decays lg_p, ge_p = exp(lg_p), A[p,s] = beta_p exp(lg_p - lg_s)
-// kn_p.kn_s (s < p) and T = (I + A)^-1, the carried state S ([K, V]) gives
-//     U = T diag(beta) V - T diag(beta ge) Kn S  =  u - w S
-//     O = diag(ge) Qn S + Rq U,          Rq[p,s] = exp(lg_p - lg_s) qn_p.kn_s (s <= p)
-//     S <- exp(lg_C) S + (diag(exp(lg_C - lg)) Kn)^T U
-// Everything that does not depend on S is computed chunk-parallel, so the
-// sequential pass only runs two dependent products per chunk (plus two independent
-// ones for the output):
+// inclusive log-decays lg_p, ge_p = exp(lg_p), row weights ik = 1 / |k|, iq = scale / |q|,
+// A[p,s] = beta_p exp(lg_p - lg_s) kn_p.kn_s (s < p) and T = (I + A)^-1, the carried state
+// S ([K, V]) gives
+//     U = T diag(beta) (V - diag(ge ik) K S)                      (raw k rows K)
+//     O = diag(ge iq) Q S + Rq U,          Rq[p,s] = exp(lg_p - lg_s) qn_p.kn_s (s <= p)
+//     S <- exp(lg_C) S + K^T diag(exp(lg_C - lg) ik) U
 //
-//  pass 1, gdn_prep16 -- one workgroup per (sequence, head, chunk): L2-normalise the
-//    rows, Gram blocks Kn Kn^T and Qn Kn^T on MFMA, T by a blocked fp32 inverse
-//    (forward substitution on the 16x16 diagonal blocks, then three levels of block
-//    products), then w = T (beta ge Kn) and u = T (beta V) on MFMA.  Writes the
-//    per-chunk record (w, qn, kdT, u, rq in 16 bits; lg in fp32).
+//  pass 1, gdn_prep16 -- one wave per (sequence, head, chunk) item, no workgroup
+//    barriers: k and q rows straight from memory into MFMA fragments, row norms and the
+//    log-decay prefix in registers, the Gram blocks K K^T and K Q^T on MFMA, T by forward
+//    substitution on the 16 x 16 diagonal blocks (fp32, one lane per column) and three
+//    levels of fp32 block products, then the record (T diag(beta) and Rq as MFMA
+//    fragments, per-token factors; 14 KiB, layout in gated_delta.h).
 //
-//  pass 2, gdn_scan16 -- one workgroup per (sequence, head, 32-column slab of the
-//    [K, V] state), chunks in order.  The 128 x 32 fp32 slab stays in VGPRs; a 16-bit
-//    copy in LDS feeds the B operands.  Per chunk: U = u - w S and O = diag(ge) Qn S,
-//    U^T to LDS, then S <- gC S + kdT U and O += Rq U: two dependent products and two
-//    workgroup barriers on the recurrence, the output products beside them.  The
-//    recurrence operands of the next three chunks are in flight into registers (A
-//    fragments straight from memory); qn, rq and lg of the next two chunks are copied
-//    straight into LDS.  The output slab leaves through LDS as 16-byte stores.
+//  pass 2, gdn_scan16 -- one workgroup of two waves per (sequence, head, 32-column slab
+//    of the state); each wave owns 16 whole columns, and the columns of the recurrence
+//    are independent, so a chunk step needs no exchange between waves.  Per chunk a wave
+//    runs K S (16 MFMAs) -> X -> U = T diag(beta) X (6) -> S update (16) in registers, and
+//    the output O^T = S^T Q^T diag(geqs) + U^T Rq^T (22) beside the chain.  The k, q rows,
+//    the v slab and the record of chunk c + 2 stream into a third LDS slot (direct buffer
+//    copies) while chunk c computes; one workgroup barrier per chunk guards the slots.
+//
+// Fragment layouts (v_mfma_f32_16x16x32: A lane (g, r) holds row r, k = 8g + [0, 8); B lane
+// (g, c) holds column c, same k; accumulator lane (g, c) register i holds row 4g + i,
+// column c).  State tile t of a wave holds rows k = 32 (t/2) + 8g + 4 (t%2) + i, so two
+// tiles give the B fragment of k-step t/2 in natural k order.  Token contractions use the
+// slot order 32 j + 4g + [0, 4), 32 j + 16 + 4g + [0, 4), which two accumulator tiles of
+// consecutive 16-token blocks give without data movement; the record's fragments and the
+// transposing LDS reads of k and v rows follow that order.
 #include <algorithm>
 #include <type_traits>
 
@@ -34,295 +40,281 @@ namespace atma {
 
 __device__ __forceinline__ u32x4 lds16(const void* p) { return *(const u32x4*)p; }
 
+// 16-bit element e (0..3) of an 8-byte vector, as float.
 template <typename T>
-__device__ __forceinline__ u32x4 scale8(const u32x4& x, float f) {
-  u32x4 o;
-#pragma unroll
-  for (int w = 0; w < 4; ++w) o[w] = pack2<T>(elem16<T>(x, 2 * w) * f, elem16<T>(x, 2 * w + 1) * f);
-  return o;
+__device__ __forceinline__ float elem16x2(const u32x2& x, int e) {
+  const uint16_t u = (uint16_t)(x[e >> 1] >> ((e & 1) * 16));
+  return (float)__builtin_bit_cast(T, u);
 }
 
-// (tp, ts) of the 6 strictly-upper 16x16 blocks of a 64x64 matrix, blk = 0..5
-__device__ __forceinline__ void upper_block(int blk, int& tp, int& ts) {
-  tp = blk < 3 ? 0 : (blk < 5 ? 1 : 2);
-  ts = blk < 3 ? blk + 1 : (blk < 5 ? blk - 1 : 3);
+// Eight floats (two accumulator tiles) -> one 16-byte MFMA fragment.
+template <typename T>
+__device__ __forceinline__ u32x4 pack8(const f32x4& lo, const f32x4& hi) {
+  return u32x4{pack2<T>(lo[0], lo[1]), pack2<T>(lo[2], lo[3]), pack2<T>(hi[0], hi[1]), pack2<T>(hi[2], hi[3])};
 }
+
+// X Y of fp32 16 x 16 blocks on v_mfma_f32_16x16x4f32, with X entering transposed: xt and y
+// are in the accumulator layout (lane (g, c) register i = row 4g + i, column c), and step i
+// contracts k = 4g + i, so xt[i] is the A operand (X[c][4g + i]) and y[i] the B operand.
+__device__ __forceinline__ f32x4 blk_mul(const f32x4& xt, const f32x4& y, f32x4 acc) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xt[i], y[i], acc, 0, 0, 0);
+  return acc;
+}
+
+// Lower-triangle 16-token block pairs (k, P), k <= P, in the order (0,0) (0,1) (1,1) (0,2) ...
+__host__ __device__ constexpr int tri(int k, int P) { return P * (P + 1) / 2 + k; }
 
 template <typename T, int D>
-__global__ void __launch_bounds__(256, 2) gdn_prep16_kernel(GdnArgs a) {
-  constexpr int C = kChunk, KP = D + 8, FP = C + 4;
-  constexpr int DC = D / 8;           // 16-byte chunks per row
-  constexpr int NE = (C / 4) * DC;    // (4 tokens x 8 dims) groups
-  __shared__ __attribute__((aligned(16))) T R1[C * KP];  // Kn rows, then beta ge Kn rows
-  __shared__ __attribute__((aligned(16))) T R2[C * KP];  // Qn rows, then beta V rows
-  __shared__ __attribute__((aligned(16))) float Af[C * FP];
-  __shared__ float Tf[C * FP];
-  __shared__ float Yf[3 * 256];
-  __shared__ __attribute__((aligned(16))) float lg[C], bet[C], sge[C], ikn[C], iqs[C];
+__global__ void __launch_bounds__(256) gdn_prep16_kernel(GdnArgs a) {
+  constexpr int C = kChunk, KS = D / 32;
+  __shared__ __attribute__((aligned(16))) float Nb[4][4 * 256];  // per wave: N^T of the diagonal blocks
+  __shared__ __attribute__((aligned(16))) float Mb[4][4 * 256];  // per wave: T^T of the diagonal blocks
+  __shared__ __attribute__((aligned(16))) float Tk[4][4][C];     // per wave: lg, beta, ik, iq of each token
 
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches
-  const int c16 = lane & 15, g = lane >> 4;
-  const Gdn16Ws W{D, (int64_t)a.B * a.H * a.NC};
-  T* ws16 = (T*)a.ws;
-  const bool act = tid < NE;
-  const int p4 = tid / DC, dc = tid % DC;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = lane >> 4, c16 = lane & 15;
+  const int64_t item = (int64_t)blockIdx.x * 4 + wave;
+  if (item >= (int64_t)a.B * a.H * a.NC) return;  // a whole wave; the kernel has no barrier
+  const int bh = (int)(item / a.NC), c = (int)(item % a.NC);
+  const int b = bh / a.H, h = bh % a.H;
+  const int rows = min(a.T - c * C, C);
+  float* tlg = Tk[wave][0];
+  float* tbt = Tk[wave][1];
+  float* tik = Tk[wave][2];
+  float* tiq = Tk[wave][3];
+  float* nb = Nb[wave];
+  float* mb = Mb[wave];
+  char* rec = (char*)a.ws + item * kGdn16RecBytes;
 
-  // ---- the rows of one (sequence, head, chunk) item: thread (p4, dc) holds tokens
-  // 4p4..4p4+3, dims 8dc..8dc+7 of k, q, v; threads < C one token's g and beta
-  struct Rows {
-    u32x4 k[4], q[4], v[4];
-    float gl, bt;
-  };
-  auto load_rows = [&](Rows& r, int item) {
-    const int bh = item / a.NC, c = item % a.NC;
-    const int b = bh / a.H, h = bh % a.H;
-    if (act) {
+  // ---- k and q rows as MFMA fragments: lane (g, r) holds row 16p + r, columns 32s + 8g ..
+  // (rows past T read as zeros)
+  const auto krs = buffer_rsrc((const T*)a.k + b * a.k_sb + (int64_t)c * C * a.k_st + (h / a.G) * a.k_sh,
+                               (uint32_t)(((rows - 1) * a.k_st + D) * 2));
+  const auto qrs = buffer_rsrc((const T*)a.q + b * a.q_sb + (int64_t)c * C * a.q_st + h * a.q_sh,
+                               (uint32_t)(((rows - 1) * a.q_st + D) * 2));
+  u32x4 kf[4][KS], qf[4][KS];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t t = (int64_t)c * C + 4 * p4 + i;
-        const bool ok = t < a.T;
-        r.k[i] = ok ? *(const u32x4*)((const T*)a.k + b * a.k_sb + t * a.k_st + (h / a.G) * a.k_sh + 8 * dc)
-                    : u32x4{0, 0, 0, 0};
-        r.q[i] = ok ? *(const u32x4*)((const T*)a.q + b * a.q_sb + t * a.q_st + h * a.q_sh + 8 * dc)
-                    : u32x4{0, 0, 0, 0};
-        r.v[i] = ok ? *(const u32x4*)((const T*)a.v + b * a.v_sb + t * a.v_st + (h / a.G) * a.v_sh + 8 * dc)
-                    : u32x4{0, 0, 0, 0};
-      }
-    }
-    if (tid < C) {
-      const int tt = c * C + tid;
-      const int64_t gi = ((int64_t)b * a.T + tt) * a.H + h;
-      r.gl = tt < a.T ? gdn_load_g(a, gi) : 0.f;
-      r.bt = tt < a.T ? gdn_load_beta(a, gi) : 0.f;
-    }
-  };
-
-  auto process = [&](Rows& r, int item, int next) {
-  const int bh = item / a.NC, c = item % a.NC;
-  const int64_t ri = (int64_t)bh * a.NC + c;
-  lds_barrier();  // the previous item is done with every LDS buffer
-  u32x4* kn = r.k;
-  u32x4* vr = r.v;
-  if (act) {
-    float ks[4], qs[4];
+  for (int p = 0; p < 4; ++p)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      ks[i] = qs[i] = 0.f;
+    for (int s = 0; s < KS; ++s) {
+      kf[p][s] = buffer_load16(krs, (uint32_t)(((16 * p + c16) * a.k_st + 32 * s + 8 * g) * 2), 0);
+      qf[p][s] = buffer_load16(qrs, (uint32_t)(((16 * p + c16) * a.q_st + 32 * s + 8 * g) * 2), 0);
+    }
+
+  // ---- gates (lane = token) and the inclusive prefix sum of the log-decays
+  float gl = 0.f, bt = 0.f;
+  if (lane < rows) {
+    const int64_t gi = ((int64_t)b * a.T + c * C + lane) * a.H + h;
+    gl = gdn_load_g(a, gi);
+    bt = gdn_load_beta(a, gi);
+  }
+  float lg = gl;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float y = __shfl_up(lg, off, 64);
+    if (lane >= off) lg += y;
+  }
+  tlg[lane] = lg;
+  tbt[lane] = bt;
+
+  // ---- row norms: partial sums over this lane's columns, then over the four lane groups
+  float nk[4], nq[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    nk[p] = nq[p] = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float x = elem16<T>(kn[i], e), y = elem16<T>(r.q[i], e);
-        ks[i] = fmaf(x, x, ks[i]);
-        qs[i] = fmaf(y, y, qs[i]);
+        const float x = elem16<T>(kf[p][s], e), y = elem16<T>(qf[p][s], e);
+        nk[p] = fmaf(x, x, nk[p]);
+        nq[p] = fmaf(y, y, nq[p]);
+      }
+    nk[p] += __shfl_xor(nk[p], 16, 64);
+    nq[p] += __shfl_xor(nq[p], 16, 64);
+    nk[p] += __shfl_xor(nk[p], 32, 64);
+    nq[p] += __shfl_xor(nq[p], 32, 64);
+  }
+  if (g == 0) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int row = 16 * p + c16;
+      const bool ok = row < rows;
+      tik[row] = ok ? (a.l2norm ? 1.f / fmaxf(sqrtf(nk[p]), 1e-12f) : 1.f) : 0.f;
+      tiq[row] = ok ? (a.l2norm ? 1.f / fmaxf(sqrtf(nq[p]), 1e-12f) : 1.f) * a.scale : 0.f;
+    }
+  }
+  wave_sync();
+
+  // ---- per-token factors of the scan
+  {
+    const float lgC = __shfl(lg, 63, 64);
+    const float ge = __builtin_amdgcn_exp2f(lg * kLog2e);
+    float* F = (float*)(rec + kGdn16F);
+    F[lane] = __builtin_amdgcn_exp2f((lgC - lg) * kLog2e) * tik[lane];
+    F[64 + lane] = ge * tik[lane];
+    F[128 + lane] = ge * tiq[lane];
+    if (lane == 0) F[192] = __builtin_amdgcn_exp2f(lgC * kLog2e);
+  }
+
+  // ---- Gram blocks on MFMA: gk(k, P) lane (g, c) register i = k_{16k+4g+i} . k_{16P+c},
+  // gq(S, P) register i = k_{16S+4g+i} . q_{16P+c}
+  f32x4 gk[10], gq[10];
+#pragma unroll
+  for (int P = 0; P < 4; ++P)
+#pragma unroll
+    for (int k = 0; k <= P; ++k) {
+      f32x4 x = {0.f, 0.f, 0.f, 0.f}, y = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        x = mfma16x16x32<T>(kf[k][s], kf[P][s], x);
+        y = mfma16x16x32<T>(kf[k][s], qf[P][s], y);
+      }
+      gk[tri(k, P)] = x;
+      gq[tri(k, P)] = y;
+    }
+
+  // ---- Rq, transposed: block (S, P) register i = Rq[16P + c][16S + 4g + i]; written as the
+  // scan's B fragments (fragment (P, j) = blocks (2j, P), (2j + 1, P); blocks above the
+  // diagonal are zero)
+  {
+    f32x4 rq[10];
+#pragma unroll
+    for (int P = 0; P < 4; ++P) {
+      const int pt = 16 * P + c16;
+      const float lgp = tlg[pt], iqp = tiq[pt];
+#pragma unroll
+      for (int S = 0; S <= P; ++S) {
+        const f32x4 lgs = *(const f32x4*)(tlg + 16 * S + 4 * g);
+        const f32x4 iks = *(const f32x4*)(tik + 16 * S + 4 * g);
+        f32x4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float dec = __builtin_amdgcn_exp2f((lgp - lgs[i]) * kLog2e);
+          v[i] = (16 * S + 4 * g + i <= pt) ? dec * iqp * iks[i] * gq[tri(S, P)][i] : 0.f;
+        }
+        rq[tri(S, P)] = v;
       }
     }
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    u32x4* Rb = (u32x4*)(rec + kGdn16Rb);
+    Rb[0 * 64 + lane] = pack8<T>(rq[tri(0, 0)], z);
+    Rb[1 * 64 + lane] = pack8<T>(rq[tri(0, 1)], rq[tri(1, 1)]);
+    Rb[2 * 64 + lane] = pack8<T>(rq[tri(0, 2)], rq[tri(1, 2)]);
+    Rb[3 * 64 + lane] = pack8<T>(rq[tri(2, 2)], z);
+    Rb[4 * 64 + lane] = pack8<T>(rq[tri(0, 3)], rq[tri(1, 3)]);
+    Rb[5 * 64 + lane] = pack8<T>(rq[tri(2, 3)], rq[tri(3, 3)]);
+  }
+
+  // ---- A blocks.  Off-diagonal (k < P), transposed: at(k, P) register i = A[16P + c][16k + 4g + i].
+  // Diagonal, plain (row 16P + 4g + i, column 16P + c), stored as rows of N^T in LDS.
+  f32x4 at[10];
 #pragma unroll
-    for (int m = 1; m < DC; m <<= 1)
+  for (int P = 1; P < 4; ++P) {
+    const int t = 16 * P + c16;
+    const float lgt = tlg[t], wt = tbt[t] * tik[t];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        ks[i] += __shfl_xor(ks[i], m, 64);
-        qs[i] += __shfl_xor(qs[i], m, 64);
-      }
+    for (int k = 0; k < P; ++k) {
+      const f32x4 lgu = *(const f32x4*)(tlg + 16 * k + 4 * g);
+      const f32x4 iku = *(const f32x4*)(tik + 16 * k + 4 * g);
+      f32x4 v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        v[i] = wt * iku[i] * __builtin_amdgcn_exp2f((lgt - lgu[i]) * kLog2e) * gk[tri(k, P)][i];
+      at[tri(k, P)] = v;
+    }
+  }
+#pragma unroll
+  for (int P = 0; P < 4; ++P) {
+    const int u = 16 * P + c16;
+    const float lgu = tlg[u], iku = tik[u];
+    const f32x4 lgr = *(const f32x4*)(tlg + 16 * P + 4 * g);
+    const f32x4 btr = *(const f32x4*)(tbt + 16 * P + 4 * g);
+    const f32x4 ikr = *(const f32x4*)(tik + 16 * P + 4 * g);
+    f32x4 v;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float ik = a.l2norm ? 1.f / fmaxf(sqrtf(ks[i]), 1e-12f) : 1.f;
-      const float iq = (a.l2norm ? 1.f / fmaxf(sqrtf(qs[i]), 1e-12f) : 1.f) * a.scale;
-      const int p = 4 * p4 + i;
-      kn[i] = scale8<T>(kn[i], ik);
-      *(u32x4*)(R1 + p * KP + 8 * dc) = kn[i];
-      *(u32x4*)(R2 + p * KP + 8 * dc) = scale8<T>(r.q[i], iq);
-      if (dc == 0) {
-        ikn[p] = ik;
-        iqs[p] = iq;
-      }
+      const float dec = __builtin_amdgcn_exp2f((lgr[i] - lgu) * kLog2e);  // discarded above the diagonal
+      v[i] = (c16 < 4 * g + i) ? btr[i] * ikr[i] * iku * dec * gk[tri(P, P)][i] : 0.f;
     }
+    *(f32x4*)(nb + P * 256 + c16 * 16 + 4 * g) = v;  // N^T[c][4g + i] = N[4g + i][c]
   }
-  if (tid < C) {
-    lg[tid] = r.gl;
-    bet[tid] = r.bt;
-  }
-  __syncthreads();
-  if (wave == 0) {  // inclusive prefix sum of the log-decays
-    float x = lg[lane];
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float y = __shfl_up(x, off, 64);
-      if (lane >= off) x += y;
-    }
-    lg[lane] = x;
-    sge[lane] = expf(x);
-    const float last = __shfl(x, 63, 64);
-    const float tail = expf(last - x);
-    float* rec = (float*)((char*)a.ws + W.f32_byte(ri));
-    rec[lane] = x;
-    rec[C + lane] = tail * ikn[lane];
-    rec[2 * C + lane] = iqs[lane];
-  }
-  __syncthreads();
+  wave_sync();
 
-  // ---- Gram tiles, transposed: for the 10 lower-triangle block pairs (tp >= ts) the
-  // tile rows are keys s (16 ts + 4g + i) and the columns tokens p (16 tp + c16), so a
-  // lane holds 4 consecutive s of one row p: one 16-byte LDS write of A[p][s..s+3] and
-  // one 8-byte store of rq[p][s..s+3].
+  // ---- T_PP = (I + N)^-1 by forward substitution: lane (g, c) solves column c of block g
   {
-    // this wave's 5 tasks (wave, wave + 4, ..., wave + 16) as independent MFMA chains
-    constexpr int NT = 5;
-    int tp_[NT], ts_[NT];
-    const T* ar[NT];
-    const T* br[NT];
+    const float* nt = nb + g * 256;
+    float x[16];
 #pragma unroll
-    for (int k = 0; k < NT; ++k) {
-      const int task = wave + 4 * k, which = task / 10, idx = task % 10;
-      tp_[k] = (idx >= 1) + (idx >= 3) + (idx >= 6);
-      ts_[k] = idx - tp_[k] * (tp_[k] + 1) / 2;
-      ar[k] = R1 + (16 * ts_[k] + c16) * KP + 8 * g;
-      br[k] = (which ? R2 : R1) + (16 * tp_[k] + c16) * KP + 8 * g;
-    }
-    f32x4 acc[NT];
+    for (int r = 0; r < 16; ++r) x[r] = (r == c16) ? 1.f : 0.f;
 #pragma unroll
-    for (int k = 0; k < NT; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < 15; ++j) {
+      float n[16];
 #pragma unroll
-    for (int s = 0; s < D / 32; ++s)
+      for (int q = 0; q < 4; ++q) {
+        const f32x4 v = *(const f32x4*)(nt + j * 16 + 4 * q);  // column j of N
 #pragma unroll
-      for (int k = 0; k < NT; ++k) acc[k] = mfma16x16x32<T>(lds16(ar[k] + 32 * s), lds16(br[k] + 32 * s), acc[k]);
-#pragma unroll
-    for (int k = 0; k < NT; ++k) {
-      const int which = (wave + 4 * k) / 10;
-      const int p = 16 * tp_[k] + c16, s0 = 16 * ts_[k] + 4 * g;
-      // decays and masks without branches (an overflowing exp above the diagonal is
-      // discarded by the select)
-      const float lgp = lg[p], bp = which == 0 ? bet[p] : 1.f;
-      const f32x4 lgs = *(const f32x4*)(lg + s0);
-      float v[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int sx = s0 + i;
-        const float dec = __builtin_amdgcn_exp2f((lgp - lgs[i]) * kLog2e);
-        const bool keep = which == 0 ? sx < p : sx <= p;
-        v[i] = keep ? bp * dec * acc[k][i] : 0.f;
+        for (int e = 0; e < 4; ++e) n[4 * q + e] = v[e];
       }
-      if (which == 0) {
-        *(f32x4*)(Af + p * FP + s0) = f32x4{v[0], v[1], v[2], v[3]};
-      } else {
-        *(u32x2*)(ws16 + W.rq(ri) + p * C + s0) = u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
-      }
+#pragma unroll
+      for (int r = j + 1; r < 16; ++r) x[r] = fmaf(-n[r], x[j], x[r]);
     }
+    float* mt = mb + g * 256 + c16 * 16;  // T^T row c = column c of T
+#pragma unroll
+    for (int q = 0; q < 4; ++q) *(f32x4*)(mt + 4 * q) = f32x4{x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]};
   }
-  for (int e = tid; e < 6 * 64; e += 256) {  // rq is zero above the block diagonal
-    int tp, ts;
-    upper_block(e >> 6, tp, ts);
-    const int r = (e >> 2) & 15, c4 = e & 3;
-    *(u32x2*)(ws16 + W.rq(ri) + (16 * tp + r) * C + 16 * ts + 4 * c4) = u32x2{0u, 0u};
-  }
-  __syncthreads();  // Gram done: R1 / R2 are free, A is complete
-
-  // ---- scaled operands of the w / u products, row-major like Kn (conflict-free writes;
-  // the products read them transposed)
-  if (act) {
+  wave_sync();
+  f32x4 tpp[4], tppT[4];  // T_PP and T_PP^T in the accumulator layout
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int p = 4 * p4 + i;
-      const float fv = bet[p], fk = fv * sge[p];
-      *(u32x4*)(R1 + p * KP + 8 * dc) = scale8<T>(kn[i], fk);
-      *(u32x4*)(R2 + p * KP + 8 * dc) = scale8<T>(vr[i], fv);
-    }
-  }
-  // the row registers are free from here: the next item's rows load during the inverse
-  if (next < a.B * a.H * a.NC) load_rows(r, next);
-  // ---- T = (I + A)^-1: diagonal 16x16 blocks by forward substitution (lane = column)
-  if (wave == 0) {
-    const int bb = lane >> 4, cc = lane & 15;
-    float col[16];
+  for (int P = 0; P < 4; ++P) {
+    tpp[P] = *(const f32x4*)(mb + P * 256 + c16 * 16 + 4 * g);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float acc = (r == cc) ? 1.f : 0.f;
-#pragma unroll
-      for (int j = 0; j < r; ++j) acc -= Af[(16 * bb + r) * FP + 16 * bb + j] * col[j];
-      col[r] = acc;
-    }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) Tf[(16 * bb + r) * FP + 16 * bb + cc] = col[r];
-  }
-  for (int e = tid; e < 6 * 256; e += 256) {  // T is zero above the block diagonal
-    int tp, ts;
-    upper_block(e >> 8, tp, ts);
-    Tf[(16 * tp + ((e >> 4) & 15)) * FP + 16 * ts + (e & 15)] = 0.f;
-  }
-  __syncthreads();
-  // ---- off-diagonal blocks: T_ij = -T_ii * sum_{k=j}^{i-1} A_ik T_kj, level L = i - j,
-  // one wave per block, 16x16 products on v_mfma_f32_16x16x4f32 (full fp32)
-  for (int L = 1; L < 4; ++L) {
-    if (wave < 4 - L) {
-      const int i = L + wave, j = wave;
-      f32x4 y = {0.f, 0.f, 0.f, 0.f};
-      for (int kk = j; kk < i; ++kk)
-#pragma unroll
-        for (int st = 0; st < 4; ++st)
-          y = __builtin_amdgcn_mfma_f32_16x16x4f32(Af[(16 * i + c16) * FP + 16 * kk + 4 * st + g],
-                                                   Tf[(16 * kk + 4 * st + g) * FP + 16 * j + c16], y, 0, 0, 0);
-      float* yw = Yf + wave * 256;  // this wave's 16x16 scratch, [row][col]
-#pragma unroll
-      for (int r = 0; r < 4; ++r) yw[(4 * g + r) * 16 + c16] = y[r];
-      wave_sync();
-      f32x4 t = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int st = 0; st < 4; ++st)
-        t = __builtin_amdgcn_mfma_f32_16x16x4f32(Tf[(16 * i + c16) * FP + 16 * i + 4 * st + g],
-                                                 yw[(4 * st + g) * 16 + c16], t, 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) Tf[(16 * i + 4 * g + r) * FP + 16 * j + c16] = -t[r];
-    }
-    __syncthreads();
+    for (int i = 0; i < 4; ++i) tppT[P][i] = mb[P * 256 + (4 * g + i) * 16 + c16];
   }
 
-  // ---- w = T (beta ge Kn), u = T (beta V): wave = 16-row block of T, all column tiles.
-  // Both products take 8 consecutive tokens of one head-dim column per lane from the
-  // row-major tiles: two transposing reads (ds_read_b64_tr_b16) of 4 tokens each.
+  // ---- off-diagonal blocks, level L = P - S: T_PS = -T_PP Y_PS with Y_PS = sum_{k=S}^{P-1}
+  // A_Pk T_kS, and (T^T)_SP = -Y_PS^T T_PP^T (left factors enter transposed: at, tppT, Y)
+  const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+  const f32x4 y10 = blk_mul(at[tri(0, 1)], tpp[0], z);
+  const f32x4 y21 = blk_mul(at[tri(1, 2)], tpp[1], z);
+  const f32x4 y32 = blk_mul(at[tri(2, 3)], tpp[2], z);
+  const f32x4 t10 = -blk_mul(tppT[1], y10, z);
+  const f32x4 t21 = -blk_mul(tppT[2], y21, z);
+  const f32x4 tt01 = -blk_mul(y10, tppT[1], z);
+  const f32x4 tt12 = -blk_mul(y21, tppT[2], z);
+  const f32x4 tt23 = -blk_mul(y32, tppT[3], z);
+  const f32x4 y20 = blk_mul(at[tri(1, 2)], t10, blk_mul(at[tri(0, 2)], tpp[0], z));
+  const f32x4 y31 = blk_mul(at[tri(2, 3)], t21, blk_mul(at[tri(1, 3)], tpp[1], z));
+  const f32x4 t20 = -blk_mul(tppT[2], y20, z);
+  const f32x4 tt02 = -blk_mul(y20, tppT[2], z);
+  const f32x4 tt13 = -blk_mul(y31, tppT[3], z);
+  const f32x4 y30 =
+      blk_mul(at[tri(2, 3)], t20, blk_mul(at[tri(1, 3)], t10, blk_mul(at[tri(0, 3)], tpp[0], z)));
+  const f32x4 tt03 = -blk_mul(y30, tppT[3], z);
+
+  // ---- T diag(beta), transposed blocks (S, P) scaled by beta on row 16S + 4g + i, written
+  // as the scan's A fragments (fragment (P, j) = blocks (2j, P), (2j + 1, P))
   {
-    const int rb = wave;
-    const int nsteps = rb < 2 ? 1 : 2;  // T is lower triangular: later tokens are 0
-    u32x4 tfrag[2];
+    f32x4 bs[4];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const float* tr = Tf + (16 * rb + c16) * FP + 32 * s + 8 * g;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) tfrag[s][w] = pack2<T>(tr[2 * w], tr[2 * w + 1]);
-    }
-    // lane (g, c16) reads token row 32 s + 8 g + c16 / 4 (+4), columns 16 ct + 4 (c16 % 4)
-    auto colfrag = [&](const T* R, int ct, int s) {
-      const T* p = R + (32 * s + 8 * g + (c16 >> 2)) * KP + 16 * ct + 4 * (c16 & 3);
-      const u32x2 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 4 * KP);
-      return u32x4{lo[0], lo[1], hi[0], hi[1]};
-    };
-#pragma unroll
-    for (int ct = 0; ct < D / 16; ++ct) {
-      f32x4 aw = {0.f, 0.f, 0.f, 0.f}, au = {0.f, 0.f, 0.f, 0.f};
-      for (int s = 0; s < nsteps; ++s) {
-        // w^T = (beta ge Kn)^T T^T: the T fragment is the B operand here (same registers)
-        aw = mfma16x16x32<T>(colfrag(R1, ct, s), tfrag[s], aw);
-        au = mfma16x16x32<T>(tfrag[s], colfrag(R2, ct, s), au);
-      }
-      // w row 16rb + c16, columns 16ct + 4g ..;  u in the scan's register order
-      *(u32x2*)(ws16 + W.w(ri) + (16 * rb + c16) * D + 16 * ct + 4 * g) =
-          u32x2{pack2<T>(aw[0], aw[1]), pack2<T>(aw[2], aw[3])};
-      u32x2 pk = {pack2<T>(au[0], au[1]), pack2<T>(au[2], au[3])};
-      *(u32x2*)(ws16 + W.us(ri) + (((ct >> 1) * 4 + rb) * 64 + lane) * 8 + (ct & 1) * 4) = pk;
-    }
+    for (int S = 0; S < 4; ++S) bs[S] = *(const f32x4*)(tbt + 16 * S + 4 * g);
+    u32x4* Tb = (u32x4*)(rec + kGdn16Tb);
+    Tb[0 * 64 + lane] = pack8<T>(tppT[0] * bs[0], z);
+    Tb[1 * 64 + lane] = pack8<T>(tt01 * bs[0], tppT[1] * bs[1]);
+    Tb[2 * 64 + lane] = pack8<T>(tt02 * bs[0], tt12 * bs[1]);
+    Tb[3 * 64 + lane] = pack8<T>(tppT[2] * bs[2], z);
+    Tb[4 * 64 + lane] = pack8<T>(tt03 * bs[0], tt13 * bs[1]);
+    Tb[5 * 64 + lane] = pack8<T>(tt23 * bs[2], tppT[3] * bs[3]);
   }
-  };
-
-  // ---- persistent: workgroup w takes items w, w + G, w + 2G, ...; the rows of the next
-  // item load while the current one finishes its inverse and w / u products
-  const int total = a.B * a.H * a.NC, step = gridDim.x;
-  Rows r;
-  if ((int)blockIdx.x < total) load_rows(r, blockIdx.x);
-  for (int item = blockIdx.x; item < total; item += step) process(r, item, item + step);
 }
 
-// Swizzle of 16-byte chunks in the LDS copies of the qn / rq records: logical chunk c of
-// row r sits at chunk position c ^ f(r), so the 16 rows an A-fragment read touches (one
-// chunk each) fall in distinct banks: f(r) = r mod 16 for 256-byte rows, (r / 2) mod 8
-// for 128-byte rows (two rows share one 256-byte bank line).
+// Chunk swizzle of the q rows in LDS (rows of CPR 16-byte chunks): logical chunk c of row r
+// sits at c ^ f(r), so the 16 consecutive rows a B-fragment read touches (one chunk each)
+// fall in distinct banks: f(r) = r mod 16 for 256-byte rows, (r / 2) mod 8 for 128-byte rows
+// (two rows share one 256-byte bank line).  The k rows use lds_swizzle, which also keeps the
+// transposing reads conflict-free.
 template <int CPR>
 __device__ __forceinline__ int rec_swizzle(int r) {
   static_assert(CPR == 8 || CPR == 16, "64- or 128-element rows");
@@ -330,266 +322,312 @@ __device__ __forceinline__ int rec_swizzle(int r) {
 }
 
 template <typename T, int D>
-__global__ void __launch_bounds__(256, 1) gdn_scan16_kernel(GdnArgs a) {
-  constexpr int C = kChunk, VS = 32, KP = D + 8, CP = C + 8, OP = VS + 8;
-  constexpr int KS = D / 32;   // MFMA k-steps over the head dim
-  constexpr int KTW = D / 64;  // 16-row state tiles per wave
-  constexpr int QCPR = D / 8, RCPR = C / 8;  // 16-byte chunks per q / k and rq row
-  constexpr int QB = C * D, RB = C * C;      // elements of one q / k block and rq record
-  __shared__ __attribute__((aligned(16))) T Sb[VS * KP];   // S^T slab, 16-bit: [v][k]
-  __shared__ __attribute__((aligned(16))) T Ub[VS * CP];   // U^T, 16-bit: [v][token]
-  __shared__ __attribute__((aligned(16))) T Ubk[VS * CP];  // (diag(kf) U)^T
-  __shared__ __attribute__((aligned(16))) T Qs[3 * QB];    // raw q rows of chunk j in slot j % 3
-  __shared__ __attribute__((aligned(16))) T Kr[3 * QB];    // raw k rows of chunk j in slot j % 3
-  __shared__ __attribute__((aligned(16))) T Rs[3 * RB];    // rq of chunk j in slot j % 3
-  __shared__ __attribute__((aligned(16))) float Fs[3 * 3 * C];  // lg, kf, qs of chunk j
-  gdn_signal_start(a);
-  __shared__ __attribute__((aligned(16))) T Os[4 * 16 * OP];   // per-wave O tile, [row][v]
+__global__ void __launch_bounds__(128, 1) gdn_scan16_kernel(GdnArgs a) {
+  constexpr int C = kChunk, KS = D / 32, ST = D / 16;
+  constexpr int CPR = D / 8;                    // 16-byte chunks per k / q row
+  constexpr int KB = C * D, VB = C * 32;        // elements of one slot's k (q) rows, v slab
+  constexpr int RB = kGdn16RecBytes;            // bytes of one slot's record
+  constexpr int RPI = 64 / CPR;                 // k / q rows per copy instruction
+  constexpr int NKQ = 32 / RPI;                 // copy instructions per wave for its 32 k (q) rows
+  constexpr int NREC = (RB / 1024 + 1) / 2;     // record blocks per wave (wave 1 repeats its last)
+  constexpr int NDMA = 2 * NKQ + 2 + NREC;      // copies per wave per chunk
+  static_assert(RB % 1024 == 0, "record of whole 1 KiB blocks");
+  // three slots per array: chunk c lives in slot c % 3, so within the three-times unrolled
+  // loop every slot offset is an instruction immediate
+  __shared__ __attribute__((aligned(16))) T Ks[3 * KB];
+  __shared__ __attribute__((aligned(16))) T Qs[3 * KB];
+  __shared__ __attribute__((aligned(16))) T Vs[3 * VB];
+  __shared__ __attribute__((aligned(16))) char Rs[3 * RB];
 
+  gdn_signal_start(a);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c16 = lane & 15, g = lane >> 4;
-  const int bh = blockIdx.x, v0 = blockIdx.y * VS;
-  const int b = bh / a.H, h = bh % a.H;
-  const Gdn16Ws W{D, (int64_t)a.B * a.H * a.NC};
-  const int64_t ri0 = (int64_t)bh * a.NC;
-  const T* ws16 = (const T*)a.ws;
+  const int g = lane >> 4, c16 = lane & 15;
+  const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H, hk = h / a.G;
+  const int vw = 32 * blockIdx.y;    // the workgroup's 32 state columns
+  const int v0 = vw + 16 * wave;     // this wave's 16
 
-  // ---- state slab: tile (k-tile wave*KTW + j, v-tile vt); rows k = 16kt + 4g + i, cols v
-  f32x4 S[KTW][2];
+  // ---- state: tile t, register i <-> row k = 32 (t/2) + 8g + 4 (t%2) + i, column v0 + c16
+  f32x4 S[ST];
 #pragma unroll
-  for (int j = 0; j < KTW; ++j)
+  for (int t = 0; t < ST; ++t)
 #pragma unroll
-    for (int vt = 0; vt < 2; ++vt) {
-      const int kt = wave * KTW + j;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kx = 16 * kt + 4 * g + i, vx = v0 + 16 * vt + c16;
-        S[j][vt][i] = a.s0 ? a.s0[((int64_t)bh * D + kx) * D + vx] : 0.f;
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int kx = 32 * (t >> 1) + 8 * g + 4 * (t & 1) + i;
+      S[t][i] = a.s0 ? a.s0[((int64_t)bh * D + kx) * D + v0 + c16] : 0.f;
     }
-  // 16-bit copy of the state entering the next chunk, in LDS (B operands)
-  auto publish_state = [&]() {
-#pragma unroll
-    for (int j = 0; j < KTW; ++j)
-#pragma unroll
-      for (int vt = 0; vt < 2; ++vt) {
-        const int kt = wave * KTW + j;
-        const u32x2 pk = {pack2<T>(S[j][vt][0], S[j][vt][1]), pack2<T>(S[j][vt][2], S[j][vt][3])};
-        *(u32x2*)(Sb + (16 * vt + c16) * KP + 16 * kt + 4 * g) = pk;
-      }
-  };
 
-  // ---- raw q and k rows, rq and the per-token factors of chunk j, copied straight into
-  // LDS slot j % 3 (buffer DMA, no registers): wave w copies token rows 16w .. 16w + 15
-  // of q, k and rq, wave 0 the 3 x 64 factors.  Rows past T read as zeros.  q rows use
-  // the A-fragment swizzle, k rows the transposing-read swizzle (lds_swizzle).
-  constexpr int QRPI = 64 / QCPR, RRPI = 64 / RCPR;  // rows per copy instruction
-  constexpr int NQ = 16 / QRPI, NR = 16 / RRPI;
-  constexpr int NDMA = 2 * NQ + NR;  // copy instructions of waves 1..3 per chunk
-  constexpr int NLOAD = KS + 1;      // register loads per chunk (w, u)
-  const uint32_t qst2 = (uint32_t)a.q_st * 2u, kst2 = (uint32_t)a.k_st * 2u;
-  auto copy_rec = [&](int j, int slot) {
-    const int64_t ri = ri0 + j;
+  // ---- lane parts of the LDS addresses (elements; tile and slot offsets are immediates).
+  // k rows use lds_swizzle, whose value for the rows a lane touches is fixed: A fragments
+  // read row 16p + c16 (swizzle of c16), transposing reads row 32j + 4g + c16/4 (+16)
+  // (swizzle 4 (c16/4) + g); q rows use rec_swizzle (c16 for 256-byte rows).
+  const int ksw = lds_swizzle<CPR>(c16);
+  int kAo[KS], qBo[KS], kTo[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    kAo[s] = c16 * D + 8 * ((4 * s + g) ^ ksw);
+    qBo[s] = c16 * D + 8 * ((4 * s + g) ^ rec_swizzle<CPR>(c16));
+    // tile t = 2s (+1): lane supplies columns 32 s + 8 (c16 % 4) + 4 (t % 2) of row
+    // 4g + c16/4 (+ 32j, + 16): chunk 4s + c16 % 4
+    const int r0 = 4 * g + (c16 >> 2);
+    kTo[s] = r0 * D + 8 * ((4 * s + (c16 & 3)) ^ lds_swizzle<CPR>(r0));
+  }
+  const int vo = (4 * g + (c16 >> 2)) * 32 + 16 * wave + 4 * (c16 & 3);
+
+  // ---- copies of chunk j into slot sl: wave w copies k and q rows 32w .. 32w + 31 (k with
+  // lds_swizzle, q with rec_swizzle), v slab rows 32w .. 32w + 31 (64 bytes each) and half
+  // of the record's 1 KiB blocks (with an odd count, wave 1 copies its last block twice so
+  // both waves issue the same number of copies).  Rows past T read as zeros.
+  const uint32_t kst2 = (uint32_t)a.k_st * 2u, qst2 = (uint32_t)a.q_st * 2u, vst2 = (uint32_t)a.v_st * 2u;
+  uint32_t kvo[NKQ], qvo[NKQ], vvo[2];
+#pragma unroll
+  for (int r = 0; r < NKQ; ++r) {
+    const int row = 32 * wave + RPI * r + lane / CPR, pc = lane % CPR;
+    kvo[r] = row * kst2 + 16u * (pc ^ lds_swizzle<CPR>(row));
+    qvo[r] = row * qst2 + 16u * (pc ^ rec_swizzle<CPR>(row));
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r) vvo[r] = (32 * wave + 16 * r + lane / 4) * vst2 + 16u * (lane % 4);
+  const uint32_t rvo = 16u * lane;  // record blocks: the block offset is a scalar (always in range)
+  const T* kb = (const T*)a.k + b * a.k_sb + hk * a.k_sh;
+  const T* qb = (const T*)a.q + b * a.q_sb + h * a.q_sh;
+  const T* vb = (const T*)a.v + b * a.v_sb + hk * a.v_sh + vw;
+  const char* rb0 = (const char*)a.ws + (int64_t)bh * a.NC * RB;
+  const int last = a.NC - 1;
+  // LDS byte offsets of this wave's copy destinations, in scalar registers
+  const uint32_t mk = __builtin_amdgcn_readfirstlane(lds_offset(Ks + 32 * wave * D));
+  const uint32_t mq = __builtin_amdgcn_readfirstlane(lds_offset(Qs + 32 * wave * D));
+  const uint32_t mv = __builtin_amdgcn_readfirstlane(lds_offset(Vs + 32 * wave * 32));
+  const uint32_t mr = __builtin_amdgcn_readfirstlane(lds_offset(Rs));
+  auto copy_chunk = [&](int j, auto slot_c) {
+    constexpr int sl = decltype(slot_c)::value;
     const int rows = min(a.T - j * C, C);
-    const auto qrs = buffer_rsrc((const T*)a.q + b * a.q_sb + (int64_t)j * C * a.q_st + h * a.q_sh,
-                                 (uint32_t)((rows - 1) * a.q_st + D) * 2u);
-    const auto krs = buffer_rsrc((const T*)a.k + b * a.k_sb + (int64_t)j * C * a.k_st + (h / a.G) * a.k_sh,
-                                 (uint32_t)((rows - 1) * a.k_st + D) * 2u);
-    const auto rrs = buffer_rsrc(ws16 + W.rq(ri), RB * 2);
+    const auto krs = buffer_rsrc(kb + (int64_t)j * C * a.k_st, (uint32_t)((rows - 1) * a.k_st + D) * 2u);
+    const auto qrs = buffer_rsrc(qb + (int64_t)j * C * a.q_st, (uint32_t)((rows - 1) * a.q_st + D) * 2u);
+    const auto vrs = buffer_rsrc(vb + (int64_t)j * C * a.v_st, (uint32_t)((rows - 1) * a.v_st + 32) * 2u);
+    const auto rrs = buffer_rsrc(rb0 + (int64_t)j * RB, RB);
 #pragma unroll
-    for (int r = 0; r < NQ; ++r) {
-      const int row = 16 * wave + QRPI * r + lane / QCPR, pc = lane % QCPR;
-      const uint32_t lq = pc ^ rec_swizzle<QCPR>(row), lk = pc ^ lds_swizzle<QCPR>(row);
-      dma_buf16(qrs, row * qst2 + 16u * lq, 0, Qs + slot * QB + (16 * wave + QRPI * r) * D);
-      dma_buf16(krs, row * kst2 + 16u * lk, 0, Kr + slot * QB + (16 * wave + QRPI * r) * D);
+    for (int r = 0; r < NKQ; ++r) {
+      dma_buf16_at(krs, kvo[r], 0, mk + (sl * KB + RPI * r * D) * 2);
+      dma_buf16_at(qrs, qvo[r], 0, mq + (sl * KB + RPI * r * D) * 2);
     }
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-      const int row = 16 * wave + RRPI * r + lane / RCPR, pc = lane % RCPR;
-      const int lc = pc ^ rec_swizzle<RCPR>(row);
-      dma_buf16(rrs, (uint32_t)(row * C + 8 * lc) * 2u, 0, Rs + slot * RB + (16 * wave + RRPI * r) * C);
-    }
-    if (wave == 0) {
-      const auto frs = buffer_rsrc((const char*)a.ws + W.f32_byte(ri), 3 * C * 4);
+    for (int r = 0; r < 2; ++r) dma_buf16_at(vrs, vvo[r], 0, mv + (sl * VB + 16 * r * 32) * 2);
 #pragma unroll
-      for (int r = 0; r < 3; ++r)
-        dma_buf4(frs, (uint32_t)(r * C + lane) * 4u, 0, Fs + slot * 3 * C + r * C);
+    for (int r = 0; r < NREC; ++r) {
+      const uint32_t blk = (uint32_t)min(NREC * wave + r, RB / 1024 - 1) * 1024u;
+      dma_buf16_at(rrs, rvo, blk, mr + sl * RB + blk);
     }
-  };
-
-  // ---- one chunk's recurrence operands in registers (A fragments straight from
-  // memory).  Three sets rotate with the three LDS slots: a set is refilled with chunk
-  // c + 3 right after chunk c used it, so each load has two chunk steps to arrive, no
-  // set is ever copied, and every slot index is a constant.
-  struct Frag {
-    u32x4 w[KS], u;
-  };
-  auto load = [&](Frag& f, int c) {
-    const int64_t ri = ri0 + c;
-    const int row = 16 * wave + c16;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) f.w[s] = *(const u32x4*)(ws16 + W.w(ri) + row * D + 32 * s + 8 * g);
-    f.u = *(const u32x4*)(ws16 + W.us(ri) + ((blockIdx.y * 4 + wave) * 64 + lane) * 8);
   };
 
   // this sequence's output rows as one buffer: rows past T are dropped
-  const auto orsrc = buffer_rsrc((const T*)a.o + (int64_t)b * a.T * a.H * D,
-                                 (uint32_t)((int64_t)a.T * a.H * D * 2));
-  const int last = a.NC - 1;
-  const int qrow = 16 * wave + c16;
-  auto body = [&](const Frag& f, int c, auto slot_c) {
-    constexpr int slot = decltype(slot_c)::value;  // c % 3, a constant per call site
-    const T* qs = Qs + slot * QB + qrow * D;
-    const T* rs = Rs + slot * RB + qrow * C;
-    const T* kr = Kr + slot * QB;
-    const float* fs = Fs + slot * 3 * C;
-    // ---- U = u - w S and O = diag(ge qs) Q S (rows 16*wave + 4g + i, columns v0 + 16vt + c16);
-    // all B fragments of S and A fragments of Q are requested before the first product
-    u32x4 sbf[2][KS], qf[KS];
+  const auto orsrc = buffer_rsrc((const T*)a.o + (int64_t)b * a.T * a.H * D, (uint32_t)((int64_t)a.T * a.H * D * 2));
+  const uint32_t oo = (uint32_t)((c16 * a.H + h) * D + v0 + 4 * g) * 2u;  // lane part of the output offset
+  const uint32_t otok = (uint32_t)a.H * D * 2u;                          // bytes per token
+
+  auto body = [&](int c, auto slot_c) {
+    constexpr int sl = decltype(slot_c)::value;
+    // this wave's copies of chunk c have landed (only those of chunk c + 1 may be in
+    // flight: loads complete in order, and stores are not counted), then the other's
+    wait_vmcnt<NDMA>();
+    __syncthreads();
+    // chunk c + 2 goes to the slot chunk c - 1 used (both waves are past it); past the
+    // last chunk the copies repeat it, so every step issues the same count
+    copy_chunk(min(c + 2, last), std::integral_constant<int, (sl + 2) % 3>{});
+
+    const T* Kl = Ks + sl * KB;
+    const T* Ql = Qs + sl * KB;
+    const T* Vl = Vs + sl * VB;
+    const char* Rl = Rs + sl * RB;
+    const float* Fp = (const float*)(Rl + kGdn16F);
+    const u32x4* Tb = (const u32x4*)(Rl + kGdn16Tb);
+    const u32x4* Rb = (const u32x4*)(Rl + kGdn16Rb);
+
+    // The LDS reads of each phase are issued before its first product and the scheduling
+    // barriers keep that order (one wave per SIMD: no other wave hides a read's latency).
+    // (1) reads: k rows as A fragments of K S (tile p: row 16p + c16), gC
+    u32x4 kA[4][KS];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      qf[s] = lds16(qs + 8 * ((4 * s + g) ^ rec_swizzle<QCPR>(qrow)));
+    for (int p = 0; p < 4; ++p)
 #pragma unroll
-      for (int vt = 0; vt < 2; ++vt) sbf[vt][s] = lds16(Sb + (16 * vt + c16) * KP + 32 * s + 8 * g);
-    }
+      for (int s = 0; s < KS; ++s) kA[p][s] = lds16(Kl + 16 * p * D + kAo[s]);
+    const float gC = Fp[192];
     __builtin_amdgcn_sched_barrier(0);
-    f32x4 acc[2], o[2];
+
+    // (2) K S with S as B fragments (k-step s: tiles 2s, 2s + 1); the same registers are the
+    // A fragments of S^T; independent products adjacent, and S <- gC S issued between them
+    // (a wave issues one instruction per cycle slot, so VALU work placed between products
+    // runs while the matrix unit is busy)
+    u32x4 sf[KS];
 #pragma unroll
-    for (int vt = 0; vt < 2; ++vt) acc[vt] = o[vt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < KS; ++s) sf[s] = pack8<T>(S[2 * s], S[2 * s + 1]);
+    f32x4 ks[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) ks[p] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < KS; ++s)
 #pragma unroll
-      for (int vt = 0; vt < 2; ++vt) {
-        acc[vt] = mfma16x16x32<T>(f.w[s], sbf[vt][s], acc[vt]);
-        o[vt] = mfma16x16x32<T>(qf[s], sbf[vt][s], o[vt]);
-      }
-    const f32x4 lg4 = *(const f32x4*)(fs + 16 * wave + 4 * g);
-    const f32x4 kf4 = *(const f32x4*)(fs + C + 16 * wave + 4 * g);
-    const f32x4 qs4 = *(const f32x4*)(fs + 2 * C + 16 * wave + 4 * g);
+      for (int p = 0; p < 4; ++p) ks[p] = mfma16x16x32<T>(kA[p][s], sf[s], ks[p]);
 #pragma unroll
-    for (int vt = 0; vt < 2; ++vt) {
-      float uv[4];
+    for (int t = 0; t < ST; ++t) S[t] *= gC;
+    __builtin_amdgcn_sched_group_barrier(0x002, 2 * KS, 0);  // the S fragments
 #pragma unroll
-      for (int i = 0; i < 4; ++i) uv[i] = elem16<T>(f.u, 4 * vt + i) - acc[vt][i];
-      const u32x2 pk = {pack2<T>(uv[0], uv[1]), pack2<T>(uv[2], uv[3])};
-      const u32x2 pkk = {pack2<T>(uv[0] * kf4[0], uv[1] * kf4[1]), pack2<T>(uv[2] * kf4[2], uv[3] * kf4[3])};
-      *(u32x2*)(Ub + (16 * vt + c16) * CP + 16 * wave + 4 * g) = pk;
-      *(u32x2*)(Ubk + (16 * vt + c16) * CP + 16 * wave + 4 * g) = pkk;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float sc = __builtin_amdgcn_exp2f(lg4[i] * kLog2e) * qs4[i];
-#pragma unroll
-      for (int vt = 0; vt < 2; ++vt) o[vt][i] *= sc;
-    }
-    const float gC = __builtin_amdgcn_exp2f(fs[C - 1] * kLog2e);
-    __syncthreads();
-    // ---- S = gC S + K^T diag(kf) U  (A fragments: raw k columns by transposing reads);
-    // O += Rq U
-    u32x4 uf[2][2], ukf[2][2], rf[2], kt_[KTW][2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      rf[s] = lds16(rs + 8 * ((4 * s + g) ^ rec_swizzle<RCPR>(qrow)));
-#pragma unroll
-      for (int vt = 0; vt < 2; ++vt) {
-        uf[vt][s] = lds16(Ub + (16 * vt + c16) * CP + 32 * s + 8 * g);
-        ukf[vt][s] = lds16(Ubk + (16 * vt + c16) * CP + 32 * s + 8 * g);
-      }
-      // lane (g, c16) reads token rows 32 s + 8 g + c16 / 4 (+4), columns 16 kt + 4 (c16 % 4)
-#pragma unroll
-      for (int jj = 0; jj < KTW; ++jj) {
-        const int kt = wave * KTW + jj, r0 = 32 * s + 8 * g + (c16 >> 2), col = 16 * kt + 4 * (c16 & 3);
-        const int c8 = col >> 3, e = col & 7;
-        const u32x2 lo = lds_read_tr16(kr + r0 * D + 8 * (c8 ^ lds_swizzle<QCPR>(r0)) + e);
-        const u32x2 hi = lds_read_tr16(kr + (r0 + 4) * D + 8 * (c8 ^ lds_swizzle<QCPR>(r0 + 4)) + e);
-        kt_[jj][s] = u32x4{lo[0], lo[1], hi[0], hi[1]};
-      }
+    for (int i = 0; i < 4 * KS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
+
+    // (3) reads: q rows as B fragments of S^T Q^T (tile p': row 16p' + c16) and geqs of the
+    // lane's tokens; for X and U, v by transposing reads of the slab (lane c16 supplies row
+    // r0 + c16 / 4, columns 16 wave + 4 (c16 % 4)) in the token slot order
+    // 32j + 4g + [0,4), 32j + 16 + 4g + [0,4), geik of the same tokens, T diag(beta)
+    u32x4 qB[4][KS];
+    float wq[4];
 #pragma unroll
-    for (int vt = 0; vt < 2; ++vt)
+    for (int p = 0; p < 4; ++p) {
 #pragma unroll
-      for (int jj = 0; jj < KTW; ++jj) S[jj][vt] *= gC;
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int vt = 0; vt < 2; ++vt) {
-#pragma unroll
-        for (int jj = 0; jj < KTW; ++jj) S[jj][vt] = mfma16x16x32<T>(kt_[jj][s], ukf[vt][s], S[jj][vt]);
-        o[vt] = mfma16x16x32<T>(rf[s], uf[vt][s], o[vt]);
-      }
-    publish_state();
-    // ---- O tile (16 tokens x 32 columns) through LDS to one 16-byte store per lane
-    {
-      T* ow = Os + wave * 16 * OP;
-#pragma unroll
-      for (int vt = 0; vt < 2; ++vt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ow[(4 * g + i) * OP + 16 * vt + c16] = (T)o[vt][i];
-      wave_sync();
-      const int r = lane >> 2, q = lane & 3;
-      const uint32_t t = c * C + 16 * wave + r;
-      buffer_store16(orsrc, ((t * a.H + h) * D + v0 + 8 * q) * 2u, lds16(ow + r * OP + 8 * q));
+      for (int s = 0; s < KS; ++s) qB[p][s] = lds16(Ql + 16 * p * D + qBo[s]);
+      wq[p] = Fp[128 + 16 * p + c16];
     }
-    // copies of chunk c + 2 into the slot chunk c - 1 used (its readers are past the
-    // barrier that began this step)
-    copy_rec(min(c + 2, last), (slot + 2) % 3);
-    // this wave's copies of chunk c + 1 (issued one step earlier) have landed: after them
-    // came the register loads of step c - 1 and this step's copies (wave 0 issues more
-    // copies, so the count is the smaller one).  The O store issued between them is not
-    // counted: a store may complete before older loads, so only loads are counted.
-    wait_vmcnt<NDMA + NLOAD>();
-    __syncthreads();
+    u32x2 vlo[2], vhi[2];
+    f32x4 wl[2], wh[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      vlo[j] = lds_read_tr16(Vl + 32 * j * 32 + vo);
+      vhi[j] = lds_read_tr16(Vl + (32 * j + 16) * 32 + vo);
+      wl[j] = *(const f32x4*)(Fp + 64 + 32 * j + 4 * g);
+      wh[j] = *(const f32x4*)(Fp + 64 + 32 * j + 16 + 4 * g);
+    }
+    u32x4 tb[6];
+#pragma unroll
+    for (int f = 0; f < 6; ++f) tb[f] = Tb[f * 64 + lane];
+    __builtin_amdgcn_sched_barrier(0);
+
+    // (4) output, first term: O^T tile p' (rows = columns v0 + 4g + i, cols = tokens
+    // 16p' + c16) = S^T Q^T, scaled by geqs of the token; with it X = V - geik K S as B
+    // fragments over token steps j
+    f32x4 o[4];
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) o[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) o[pp] = mfma16x16x32<T>(sf[s], qB[pp][s], o[pp]);
+    u32x4 xf[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      f32x4 xl, xh;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        xl[i] = elem16x2<T>(vlo[j], i) - wl[j][i] * ks[2 * j][i];
+        xh[i] = elem16x2<T>(vhi[j], i) - wh[j][i] * ks[2 * j + 1][i];
+      }
+      xf[j] = pack8<T>(xl, xh);
+    }
+#pragma unroll
+    for (int i = 0; i < 4 * KS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // (5) reads for the state update and the output's second term: A fragments of K^T by
+    // transposing reads (for tile t, lane c16 supplies row r0 + c16 / 4 and the 4 columns
+    // 32 (t/2) + 8 (c16 % 4) + 4 (t%2) .., so lane r receives column 32 (t/2) + 8 (r/4) +
+    // 4 (t%2) + r % 4, the state row of tile t); Rq fragments; kf of the token slots
+    u32x4 kT[2][ST];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int t = 0; t < ST; ++t) {
+        const T* pl = Kl + 32 * j * D + kTo[t >> 1] + 4 * (t & 1);
+        const u32x2 lo = lds_read_tr16(pl);
+        const u32x2 hi = lds_read_tr16(pl + 16 * D);
+        kT[j][t] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      }
+    u32x4 rq[6];
+#pragma unroll
+    for (int f = 0; f < 6; ++f) rq[f] = Rb[f * 64 + lane];
+    f32x4 kl[2], kh[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      kl[j] = *(const f32x4*)(Fp + 32 * j + 4 * g);
+      kh[j] = *(const f32x4*)(Fp + 32 * j + 16 + 4 * g);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // (6) U = T diag(beta) X: tile P = tokens 16P + 4g + i (T is lower triangular); U as
+    // fragments in the token slot order, plain (U^T A fragments of the output) and weighted
+    // by kf (B fragments of the update)
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    f32x4 U[4];
+    U[0] = mfma16x16x32<T>(tb[0], xf[0], z);
+    U[1] = mfma16x16x32<T>(tb[1], xf[0], z);
+    U[2] = mfma16x16x32<T>(tb[2], xf[0], z);
+    U[3] = mfma16x16x32<T>(tb[4], xf[0], z);
+    U[2] = mfma16x16x32<T>(tb[3], xf[1], U[2]);
+    U[3] = mfma16x16x32<T>(tb[5], xf[1], U[3]);
+    u32x4 uf[2], ukf[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      uf[j] = pack8<T>(U[2 * j], U[2 * j + 1]);
+      ukf[j] = pack8<T>(U[2 * j] * kl[j], U[2 * j + 1] * kh[j]);
+    }
+
+    // (7) output second term + U^T Rq^T and the 8-byte row pieces O[token][v0 + 4g ..] (stored
+    // before the update's products, so they complete before the next chunk's copy wait), then
+    // S += K^T diag(kf) U
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      f32x4 x = o[pp] * wq[pp];
+      if (pp < 2) {
+        x = mfma16x16x32<T>(uf[0], rq[pp], x);
+      } else {
+        x = mfma16x16x32<T>(uf[0], rq[2 * pp - 2], x);
+        x = mfma16x16x32<T>(uf[1], rq[2 * pp - 1], x);
+      }
+      const u32x2 pk = {pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3])};
+      // (the whole offset in the lane's voffset: only that part is range-checked)
+      __builtin_amdgcn_raw_buffer_store_b64(pk, orsrc, oo + (uint32_t)(c * C + 16 * pp) * otok, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int t = 0; t < ST; ++t) S[t] = mfma16x16x32<T>(kT[j][t], ukf[j], S[t]);
   };
 
-  // (Past the last chunk the loads and copies re-read it: every step issues the same
-  // memory operations in the same order, so all waits on them stay partial.)
-  publish_state();
-  copy_rec(0, 0);
-  copy_rec(min(1, last), 1);
-  Frag f0, f1, f2;
-  load(f0, 0);
-  load(f1, min(1, last));
-  load(f2, min(2, last));
-  wait_vmcnt<0>();
-  __syncthreads();
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
   using S2 = std::integral_constant<int, 2>;
+  copy_chunk(0, S0{});
+  copy_chunk(min(1, last), S1{});
   for (int c = 0; c < a.NC; c += 3) {
-    body(f0, c, S0{});
-    load(f0, min(c + 3, last));
-    if (c + 1 < a.NC) body(f1, c + 1, S1{});
-    load(f1, min(c + 4, last));
-    if (c + 2 < a.NC) body(f2, c + 2, S2{});
-    load(f2, min(c + 5, last));
+    body(c, S0{});
+    if (c + 1 < a.NC) body(c + 1, S1{});
+    if (c + 2 < a.NC) body(c + 2, S2{});
   }
 
   if (a.s_out) {
 #pragma unroll
-    for (int j = 0; j < KTW; ++j)
+    for (int t = 0; t < ST; ++t)
 #pragma unroll
-      for (int vt = 0; vt < 2; ++vt) {
-        const int kt = wave * KTW + j;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int kx = 16 * kt + 4 * g + i, vx = v0 + 16 * vt + c16;
-          a.s_out[((int64_t)bh * D + kx) * D + vx] = S[j][vt][i];
-        }
+      for (int i = 0; i < 4; ++i) {
+        const int kx = 32 * (t >> 1) + 8 * g + 4 * (t & 1) + i;
+        a.s_out[((int64_t)bh * D + kx) * D + v0 + c16] = S[t][i];
       }
   }
+  // the copies issued past the last chunk land before the workgroup's LDS is released
+  wait_vmcnt<0>();
 }
 
 template <typename T, int D>
 static int launch16(const GdnArgs& a, hipStream_t s) {
-  // persistent prep: two workgroups per CU (its LDS footprint), each walking items
   const int64_t items = (int64_t)a.NC * a.B * a.H;
-  const int64_t grid = std::min<int64_t>(items, 2 * (int64_t)device_cu_count());
-  gdn_prep16_kernel<T, D><<<dim3((unsigned)grid), dim3(256), 0, s>>>(a);
+  gdn_prep16_kernel<T, D><<<dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s>>>(a);
   int rc = check_launch("chunk_gated_delta_rule(prep16)");
   if (rc) return rc;
-  gdn_scan16_kernel<T, D><<<dim3((unsigned)(a.B * a.H), D / 32), dim3(256), 0, s>>>(a);
+  gdn_scan16_kernel<T, D><<<dim3((unsigned)(a.B * a.H), D / 32), dim3(128), 0, s>>>(a);
   return check_launch("chunk_gated_delta_rule(scan16)");
 }
 

@@ -81,10 +81,11 @@ def test_validation_rejects_without_launch(lib):
     buf4 = ctypes.create_string_buffer(4)
     assert lib.atma_wait_start_flag(buf4, 1, 0, null) == 1
     assert lib.atma_chunk_gated_delta_workspace_bytes(1, 65, 2, 128, 128, 64, 0) == 2 * 2 * (5 * 64 * 128 + 4) * 4
-    # 16-bit path: per (sequence, head, chunk) w, u (C x d each) and rq (C x C) in 16
-    # bits, then 3 x C fp32 per-token factors (log-decay, key and query weights)
-    assert lib.atma_chunk_gated_delta_workspace_bytes(1, 65, 2, 128, 128, 64, 1) == \
-        2 * 2 * ((2 * 64 * 128 + 64 * 64) * 2 + 3 * 64 * 4)
+    # 16-bit path: one 13 KiB record per (sequence, head, chunk): T diag(beta) and Rq as six
+    # 16 x 32 16-bit MFMA fragments each, then 4 x 64 fp32 per-token factors
+    rec16 = 6 * 1024 + 6 * 1024 + 4 * 64 * 4
+    assert lib.atma_chunk_gated_delta_workspace_bytes(1, 65, 2, 128, 128, 64, 1) == 2 * 2 * rec16
+    assert lib.atma_chunk_gated_delta_workspace_bytes(3, 64, 4, 64, 64, 64, 2) == 3 * 4 * 1 * rec16
     # gated delta step: unsupported dims
     assert lib.atma_gated_delta_decode_step(null, 0, 0, null, 0, 0, null, 0, 0, null, null, null, 1,
                                             null, null, 1, 1, 1, 96, 96, 1, 1e-12, null) == 2
