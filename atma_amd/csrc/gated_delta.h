@@ -29,7 +29,28 @@ struct GdnArgs {
   void* ws;
   int* start_flag;  // optional: the scan's first workgroup stores start_epoch here on entry
   int start_epoch;
+  // Segmented recurrence (16-bit path, long sequences with few heads): blockIdx.z = segment
+  // seg runs chunks [seg * seg_len, min(NC, (seg + 1) * seg_len)).  seg_mode 0: one segment,
+  // the plain scan.  1: segment summaries -- no output; state columns >= D start from the
+  // identity with v = 0, so a segment's exit state holds its affine map [B | M] (exit = M
+  // entry + B), written to seg_sum.  2: replay -- each segment starts from seg_in and
+  // writes its output; the last one writes s_out.
+  int seg_len, nseg, seg_mode;
+  float* seg_sum;  // [B*H][nseg][D][2D] fp32
+  float* seg_in;   // [B*H][nseg][D][D] fp32
 };
+
+// Segments of the 16-bit recurrence for B*H sequence-heads of NC chunks at head dim D on a
+// device with `cus` compute units: enough that the summary pass (B*H*(2D/32) workgroups
+// per segment, one per CU) fills the device, each segment at least 8 chunks; 1 (the plain
+// scan) when the heads alone fill half of it.
+inline int gdn16_segments(int64_t BH, int64_t NC, int D, int cus) {
+  const int64_t per = BH * (2 * D / 32);  // summary workgroups of one segment
+  if (NC < 16 || 2 * per > cus) return 1;
+  int64_t n = 1 + cus / per;
+  n = n < NC / 8 ? n : NC / 8;
+  return n < 2 ? 1 : (int)n;
+}
 
 // Start signal of the recurrence kernel.  The scan is latency-bound and needs a whole CU
 // per workgroup (its LDS), so a long prefill overlaps it with Polar attention on another
@@ -78,5 +99,8 @@ __device__ __forceinline__ float gdn_load_beta(const GdnArgs& a, int64_t i) {
 constexpr int kGdn16Tb = 0, kGdn16Rb = 6144, kGdn16F = 12288, kGdn16RecBytes = 13312;
 
 int launch_gdn16(const GdnArgs& a, int dtype, int D, hipStream_t stream);
+// Workspace of the 16-bit path: the records, plus the segment summaries and entry states
+// when the launch splits the recurrence into segments.
+size_t gdn16_workspace_bytes(int64_t BH, int64_t NC, int D);
 
 }  // namespace atma

@@ -331,7 +331,7 @@ extern "C" size_t atma_chunk_gated_delta_workspace_bytes(int64_t B, int64_t T, i
   if (B <= 0 || T <= 0 || H <= 0 || chunk != atma::kChunk || (dk != 64 && dk != 128)) return 0;
   const int64_t nc = (T + chunk - 1) / chunk;
   if (dtype == ATMA_BF16 || dtype == ATMA_F16)
-    return (size_t)(B * H * nc) * (size_t)atma::kGdn16RecBytes;
+    return atma::gdn16_workspace_bytes(B * H, nc, (int)dk);
   const int64_t rec = 5 * chunk * dk + 4;
   return (size_t)(B * H * nc * rec) * sizeof(float);
 }

@@ -321,7 +321,9 @@ __device__ __forceinline__ int rec_swizzle(int r) {
   return CPR == 16 ? (r & 15) : ((r >> 1) & 7);
 }
 
-template <typename T, int D>
+// OUT: the plain scan and segment replays (seg_mode 0, 2) produce the output; segment
+// summaries (seg_mode 1) skip the q rows and every output product.
+template <typename T, int D, bool OUT>
 __global__ void __launch_bounds__(128, 1) gdn_scan16_kernel(GdnArgs a) {
   constexpr int C = kChunk, KS = D / 32, ST = D / 16;
   constexpr int CPR = D / 8;                    // 16-byte chunks per k / q row
@@ -339,13 +341,17 @@ __global__ void __launch_bounds__(128, 1) gdn_scan16_kernel(GdnArgs a) {
   __shared__ __attribute__((aligned(16))) T Vs[3 * VB];
   __shared__ __attribute__((aligned(16))) char Rs[3 * RB];
 
-  gdn_signal_start(a);
+  if (a.seg_mode != 2) gdn_signal_start(a);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c16 = lane & 15;
   const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H, hk = h / a.G;
-  const int vw = 32 * blockIdx.y;    // the workgroup's 32 state columns
+  const int vw = 32 * blockIdx.y;    // the workgroup's 32 state columns (>= D: a summary's transition)
   const int v0 = vw + 16 * wave;     // this wave's 16
+  const int seg = blockIdx.z;
+  const int c_begin = seg * a.seg_len, c_end = min(a.NC, c_begin + a.seg_len);
+  const bool summary = !OUT;             // no output; columns >= D carry the transition
+  const bool trans = summary && vw >= D;
 
   // ---- state: tile t, register i <-> row k = 32 (t/2) + 8g + 4 (t%2) + i, column v0 + c16
   f32x4 S[ST];
@@ -354,7 +360,11 @@ __global__ void __launch_bounds__(128, 1) gdn_scan16_kernel(GdnArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int kx = 32 * (t >> 1) + 8 * g + 4 * (t & 1) + i;
-      S[t][i] = a.s0 ? a.s0[((int64_t)bh * D + kx) * D + v0 + c16] : 0.f;
+      float x;
+      if (a.seg_mode == 0) x = a.s0 ? a.s0[((int64_t)bh * D + kx) * D + v0 + c16] : 0.f;
+      else if (a.seg_mode == 2) x = a.seg_in[(((int64_t)bh * a.nseg + seg) * D + kx) * D + v0 + c16];
+      else x = (trans && kx == v0 + c16 - D) ? 1.f : 0.f;
+      S[t][i] = x;
     }
 
   // ---- lane parts of the LDS addresses (elements; tile and slot offsets are immediates).
@@ -391,9 +401,9 @@ __global__ void __launch_bounds__(128, 1) gdn_scan16_kernel(GdnArgs a) {
   const uint32_t rvo = 16u * lane;  // record blocks: the block offset is a scalar (always in range)
   const T* kb = (const T*)a.k + b * a.k_sb + hk * a.k_sh;
   const T* qb = (const T*)a.q + b * a.q_sb + h * a.q_sh;
-  const T* vb = (const T*)a.v + b * a.v_sb + hk * a.v_sh + vw;
+  const T* vb = (const T*)a.v + b * a.v_sb + hk * a.v_sh + (trans ? 0 : vw);
   const char* rb0 = (const char*)a.ws + (int64_t)bh * a.NC * RB;
-  const int last = a.NC - 1;
+  const int last = c_end - 1;
   // LDS byte offsets of this wave's copy destinations, in scalar registers
   const uint32_t mk = __builtin_amdgcn_readfirstlane(lds_offset(Ks + 32 * wave * D));
   const uint32_t mq = __builtin_amdgcn_readfirstlane(lds_offset(Qs + 32 * wave * D));
@@ -403,8 +413,10 @@ __global__ void __launch_bounds__(128, 1) gdn_scan16_kernel(GdnArgs a) {
     constexpr int sl = decltype(slot_c)::value;
     const int rows = min(a.T - j * C, C);
     const auto krs = buffer_rsrc(kb + (int64_t)j * C * a.k_st, (uint32_t)((rows - 1) * a.k_st + D) * 2u);
-    const auto qrs = buffer_rsrc(qb + (int64_t)j * C * a.q_st, (uint32_t)((rows - 1) * a.q_st + D) * 2u);
-    const auto vrs = buffer_rsrc(vb + (int64_t)j * C * a.v_st, (uint32_t)((rows - 1) * a.v_st + 32) * 2u);
+    // (a summary reads no q rows, and its transition columns take v = 0: empty ranges, so
+    // the copies only write zeros)
+    const auto qrs = buffer_rsrc(qb + (int64_t)j * C * a.q_st, summary ? 0u : (uint32_t)((rows - 1) * a.q_st + D) * 2u);
+    const auto vrs = buffer_rsrc(vb + (int64_t)j * C * a.v_st, trans ? 0u : (uint32_t)((rows - 1) * a.v_st + 32) * 2u);
     const auto rrs = buffer_rsrc(rb0 + (int64_t)j * RB, RB);
 #pragma unroll
     for (int r = 0; r < NKQ; ++r) {
@@ -431,9 +443,6 @@ __global__ void __launch_bounds__(128, 1) gdn_scan16_kernel(GdnArgs a) {
     // flight: loads complete in order, and stores are not counted), then the other's
     wait_vmcnt<NDMA>();
     __syncthreads();
-    // chunk c + 2 goes to the slot chunk c - 1 used (both waves are past it); past the
-    // last chunk the copies repeat it, so every step issues the same count
-    copy_chunk(min(c + 2, last), std::integral_constant<int, (sl + 2) % 3>{});
 
     const T* Kl = Ks + sl * KB;
     const T* Ql = Qs + sl * KB;
@@ -477,6 +486,10 @@ __global__ void __launch_bounds__(128, 1) gdn_scan16_kernel(GdnArgs a) {
       __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
+    // chunk c + 2 goes to the slot chunk c - 1 used (both waves are past the barrier above);
+    // issued here, behind the products, so the copies' issue does not delay them.  Past the
+    // last chunk the copies repeat it, so every step issues the same count.
+    copy_chunk(min(c + 2, last), std::integral_constant<int, (sl + 2) % 3>{});
 
     // (3) reads: q rows as B fragments of S^T Q^T (tile p': row 16p' + c16) and geqs of the
     // lane's tokens; for X and U, v by transposing reads of the slab (lane c16 supplies row
@@ -484,11 +497,13 @@ __global__ void __launch_bounds__(128, 1) gdn_scan16_kernel(GdnArgs a) {
     // 32j + 4g + [0,4), 32j + 16 + 4g + [0,4), geik of the same tokens, T diag(beta)
     u32x4 qB[4][KS];
     float wq[4];
+    if constexpr (OUT) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
+      for (int p = 0; p < 4; ++p) {
 #pragma unroll
-      for (int s = 0; s < KS; ++s) qB[p][s] = lds16(Ql + 16 * p * D + qBo[s]);
-      wq[p] = Fp[128 + 16 * p + c16];
+        for (int s = 0; s < KS; ++s) qB[p][s] = lds16(Ql + 16 * p * D + qBo[s]);
+        wq[p] = Fp[128 + 16 * p + c16];
+      }
     }
     u32x2 vlo[2], vhi[2];
     f32x4 wl[2], wh[2];
@@ -508,12 +523,14 @@ __global__ void __launch_bounds__(128, 1) gdn_scan16_kernel(GdnArgs a) {
     // 16p' + c16) = S^T Q^T, scaled by geqs of the token; with it X = V - geik K S as B
     // fragments over token steps j
     f32x4 o[4];
+    if constexpr (OUT) {
 #pragma unroll
-    for (int pp = 0; pp < 4; ++pp) o[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int pp = 0; pp < 4; ++pp) o[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
+      for (int s = 0; s < KS; ++s)
 #pragma unroll
-      for (int pp = 0; pp < 4; ++pp) o[pp] = mfma16x16x32<T>(sf[s], qB[pp][s], o[pp]);
+        for (int pp = 0; pp < 4; ++pp) o[pp] = mfma16x16x32<T>(sf[s], qB[pp][s], o[pp]);
+    }
     u32x4 xf[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -547,8 +564,10 @@ __global__ void __launch_bounds__(128, 1) gdn_scan16_kernel(GdnArgs a) {
         kT[j][t] = u32x4{lo[0], lo[1], hi[0], hi[1]};
       }
     u32x4 rq[6];
+    if constexpr (OUT) {
 #pragma unroll
-    for (int f = 0; f < 6; ++f) rq[f] = Rb[f * 64 + lane];
+      for (int f = 0; f < 6; ++f) rq[f] = Rb[f * 64 + lane];
+    }
     f32x4 kl[2], kh[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -578,18 +597,20 @@ __global__ void __launch_bounds__(128, 1) gdn_scan16_kernel(GdnArgs a) {
     // (7) output second term + U^T Rq^T and the 8-byte row pieces O[token][v0 + 4g ..] (stored
     // before the update's products, so they complete before the next chunk's copy wait), then
     // S += K^T diag(kf) U
+    if constexpr (OUT) {
 #pragma unroll
-    for (int pp = 0; pp < 4; ++pp) {
-      f32x4 x = o[pp] * wq[pp];
-      if (pp < 2) {
-        x = mfma16x16x32<T>(uf[0], rq[pp], x);
-      } else {
-        x = mfma16x16x32<T>(uf[0], rq[2 * pp - 2], x);
-        x = mfma16x16x32<T>(uf[1], rq[2 * pp - 1], x);
+      for (int pp = 0; pp < 4; ++pp) {
+        f32x4 x = o[pp] * wq[pp];
+        if (pp < 2) {
+          x = mfma16x16x32<T>(uf[0], rq[pp], x);
+        } else {
+          x = mfma16x16x32<T>(uf[0], rq[2 * pp - 2], x);
+          x = mfma16x16x32<T>(uf[1], rq[2 * pp - 1], x);
+        }
+        const u32x2 pk = {pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3])};
+        // (the whole offset in the lane's voffset: only that part is range-checked)
+        __builtin_amdgcn_raw_buffer_store_b64(pk, orsrc, oo + (uint32_t)(c * C + 16 * pp) * otok, 0, 0);
       }
-      const u32x2 pk = {pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3])};
-      // (the whole offset in the lane's voffset: only that part is range-checked)
-      __builtin_amdgcn_raw_buffer_store_b64(pk, orsrc, oo + (uint32_t)(c * C + 16 * pp) * otok, 0, 0);
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j)
@@ -600,35 +621,116 @@ __global__ void __launch_bounds__(128, 1) gdn_scan16_kernel(GdnArgs a) {
   using S0 = std::integral_constant<int, 0>;
   using S1 = std::integral_constant<int, 1>;
   using S2 = std::integral_constant<int, 2>;
-  copy_chunk(0, S0{});
-  copy_chunk(min(1, last), S1{});
-  for (int c = 0; c < a.NC; c += 3) {
+  copy_chunk(c_begin, S0{});
+  copy_chunk(min(c_begin + 1, last), S1{});
+  for (int c = c_begin; c < c_end; c += 3) {
     body(c, S0{});
-    if (c + 1 < a.NC) body(c + 1, S1{});
-    if (c + 2 < a.NC) body(c + 2, S2{});
+    if (c + 1 < c_end) body(c + 1, S1{});
+    if (c + 2 < c_end) body(c + 2, S2{});
   }
 
-  if (a.s_out) {
+  float* sdst = nullptr;  // the exit state: [k][col] rows of D (2D for a summary) floats
+  int64_t sld = D;
+  if (a.seg_mode == 1) {
+    sdst = a.seg_sum + ((int64_t)bh * a.nseg + seg) * D * 2 * D;
+    sld = 2 * D;
+  } else if (seg == a.nseg - 1 && a.s_out) {
+    sdst = a.s_out + (int64_t)bh * D * D;
+  }
+  if (sdst) {
 #pragma unroll
     for (int t = 0; t < ST; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int kx = 32 * (t >> 1) + 8 * g + 4 * (t & 1) + i;
-        a.s_out[((int64_t)bh * D + kx) * D + v0 + c16] = S[t][i];
+        sdst[kx * sld + v0 + c16] = S[t][i];
       }
   }
   // the copies issued past the last chunk land before the workgroup's LDS is released
   wait_vmcnt<0>();
 }
 
+// Entry states of the segments from their summaries (fp32): seg_in[0] = s0 (or 0) and
+// seg_in[s] = M_{s-1} seg_in[s-1] + B_{s-1}, where summary s - 1 holds [B | M] row by row.
+// One workgroup per (sequence-head, 16 state columns); M is staged in LDS (rows padded
+// against bank conflicts) and thread t owns row t % D and D / 16 of the columns.
+template <int D>
+__global__ void __launch_bounds__(256) gdn_seg_combine_kernel(GdnArgs a) {
+  constexpr int NCOL = D / 16, MP = D + 1;
+  __shared__ float Ms[D * MP];
+  __shared__ float cur[D][16];
+  const int bh = blockIdx.x, j0 = 16 * blockIdx.y, tid = threadIdx.x;
+  const int k = tid % D, jc = NCOL * (tid / D);
+  for (int e = tid; e < D * 16; e += 256) {
+    const int r = e / 16, jj = e % 16;
+    const float x = a.s0 ? a.s0[((int64_t)bh * D + r) * D + j0 + jj] : 0.f;
+    cur[r][jj] = x;
+    a.seg_in[((int64_t)bh * a.nseg * D + r) * D + j0 + jj] = x;
+  }
+  for (int sg = 1; sg < a.nseg; ++sg) {
+    const float* sum = a.seg_sum + ((int64_t)bh * a.nseg + sg - 1) * D * 2 * D;
+    __syncthreads();  // the previous step's reads of Ms and cur are done
+    for (int e = tid; e < D * D; e += 256) Ms[(e / D) * MP + e % D] = sum[(e / D) * 2 * D + D + e % D];
+    __syncthreads();
+    float acc[NCOL];
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) acc[c] = sum[k * 2 * D + j0 + jc + c];
+    for (int m = 0; m < D; ++m) {
+      const float mk = Ms[k * MP + m];
+#pragma unroll
+      for (int c = 0; c < NCOL; ++c) acc[c] = fmaf(mk, cur[m][jc + c], acc[c]);
+    }
+    __syncthreads();  // every thread has read cur
+#pragma unroll
+    for (int c = 0; c < NCOL; ++c) {
+      cur[k][jc + c] = acc[c];
+      a.seg_in[(((int64_t)bh * a.nseg + sg) * D + k) * D + j0 + jc + c] = acc[c];
+    }
+  }
+}
+
+// Segment count and length of a launch (nseg = 1: the plain scan); no segment is empty.
+// The plan assumes MI355X's 256 compute units rather than querying the device, so the
+// results of a given shape do not depend on the GPU (or partition) that computes them.
+static void gdn16_plan(int64_t BH, int NC, int D, int& nseg, int& seg_len) {
+  nseg = gdn16_segments(BH, NC, D, 256);
+  seg_len = (NC + nseg - 1) / nseg;
+  nseg = (NC + seg_len - 1) / seg_len;
+}
+
+size_t gdn16_workspace_bytes(int64_t BH, int64_t NC, int D) {
+  int nseg, seg_len;
+  gdn16_plan(BH, (int)NC, D, nseg, seg_len);
+  const size_t recs = (size_t)(BH * NC) * (size_t)kGdn16RecBytes;
+  return nseg == 1 ? recs : recs + (size_t)BH * nseg * D * 3 * D * sizeof(float);
+}
+
 template <typename T, int D>
-static int launch16(const GdnArgs& a, hipStream_t s) {
-  const int64_t items = (int64_t)a.NC * a.B * a.H;
+static int launch16(const GdnArgs& a0, hipStream_t s) {
+  GdnArgs a = a0;
+  const int64_t BH = (int64_t)a.B * a.H, items = (int64_t)a.NC * BH;
   gdn_prep16_kernel<T, D><<<dim3((unsigned)((items + 3) / 4)), dim3(256), 0, s>>>(a);
   int rc = check_launch("chunk_gated_delta_rule(prep16)");
   if (rc) return rc;
-  gdn_scan16_kernel<T, D><<<dim3((unsigned)(a.B * a.H), D / 32), dim3(128), 0, s>>>(a);
-  return check_launch("chunk_gated_delta_rule(scan16)");
+  gdn16_plan(BH, a.NC, D, a.nseg, a.seg_len);
+  if (a.nseg == 1) {
+    a.seg_mode = 0;
+    gdn_scan16_kernel<T, D, true><<<dim3((unsigned)BH, D / 32, 1), dim3(128), 0, s>>>(a);
+    return check_launch("chunk_gated_delta_rule(scan16)");
+  }
+  // long sequences with few heads: segment summaries, their entry states, then the replays
+  a.seg_sum = (float*)((char*)a.ws + (size_t)items * kGdn16RecBytes);
+  a.seg_in = a.seg_sum + BH * a.nseg * D * 2 * D;
+  a.seg_mode = 1;
+  gdn_scan16_kernel<T, D, false><<<dim3((unsigned)BH, 2 * D / 32, a.nseg - 1), dim3(128), 0, s>>>(a);
+  rc = check_launch("chunk_gated_delta_rule(summary16)");
+  if (rc) return rc;
+  gdn_seg_combine_kernel<D><<<dim3((unsigned)BH, D / 16), dim3(256), 0, s>>>(a);
+  rc = check_launch("chunk_gated_delta_rule(combine16)");
+  if (rc) return rc;
+  a.seg_mode = 2;
+  gdn_scan16_kernel<T, D, true><<<dim3((unsigned)BH, D / 32, a.nseg), dim3(128), 0, s>>>(a);
+  return check_launch("chunk_gated_delta_rule(replay16)");
 }
 
 int launch_gdn16(const GdnArgs& a, int dtype, int D, hipStream_t s) {

@@ -86,6 +86,11 @@ def test_validation_rejects_without_launch(lib):
     rec16 = 6 * 1024 + 6 * 1024 + 4 * 64 * 4
     assert lib.atma_chunk_gated_delta_workspace_bytes(1, 65, 2, 128, 128, 64, 1) == 2 * 2 * rec16
     assert lib.atma_chunk_gated_delta_workspace_bytes(3, 64, 4, 64, 64, 64, 2) == 3 * 4 * 1 * rec16
+    # a long sequence with few heads splits the recurrence into segments (here 5 of 205
+    # chunks: 8 heads x 8 summary workgroups per segment on 256 compute units), adding the
+    # segments' [B | M] summaries (d x 2d fp32) and entry states (d x d fp32)
+    assert lib.atma_chunk_gated_delta_workspace_bytes(1, 65536, 8, 128, 128, 64, 1) == \
+        8 * 1024 * rec16 + 8 * 5 * 128 * 3 * 128 * 4
     # gated delta step: unsupported dims
     assert lib.atma_gated_delta_decode_step(null, 0, 0, null, 0, 0, null, 0, 0, null, null, null, 1,
                                             null, null, 1, 1, 1, 96, 96, 1, 1e-12, null) == 2

@@ -153,7 +153,9 @@ def test_configs2_gated_delta_t262144_bf16(dev):
     o1, S1 = chunk_gated_delta_rule(qd[:, :h], kd[:, :h], vd[:, :h], zgd[:, :h], zbd[:, :h], **kw)
     o2, S2 = chunk_gated_delta_rule(qd[:, h:], kd[:, h:], vd[:, h:], zgd[:, h:], zbd[:, h:],
                                     initial_state=S1, **kw)
-    assert torch.equal(torch.cat([o1, o2], 1), o) and torch.equal(S2, S)
+    # (one head group of a sequence this long takes the segmented recurrence, whose
+    # segment entry states are combined in fp32: a split run agrees to rounding)
+    assert rel_err(torch.cat([o1, o2], 1), o) <= 5e-3 and rel_err(S2, S) <= 5e-3
     o, S = o.cpu(), S.cpu()
     del qd, kd, vd, o1, o2
     kx, vx = (t.repeat_interleave(HQ // HKV, 2).float() for t in (k, v))

@@ -119,7 +119,10 @@ def test_half_strided_inputs_bitwise(dev):
 
 def test_half_long_sequence(dev):
     """configs[2] length, 16-bit: against the fp32 oracle (whole output), and one call ==
-    two calls split at a chunk boundary with the fp32 state carried (bitwise)."""
+    two calls split at a chunk boundary with the fp32 state carried.  A sequence this long
+    with two heads takes the segmented recurrence (segment summaries combined in fp32), so
+    the split run agrees to rounding, not bit for bit; the plain scan's bitwise split is
+    pinned by test_split_bitwise_plain."""
     B, T, H, d = 1, 65536, 2, 128
     q, k, v, glog, beta, _ = _inputs(B, T, H, d, torch.bfloat16, seed=14)
     kw = dict(scale=1.0, output_final_state=True, use_qk_l2norm_in_kernel=True)
@@ -127,7 +130,7 @@ def test_half_long_sequence(dev):
     h = T // 2
     o1, S1 = _run(dev, q[:, :h], k[:, :h], v[:, :h], glog[:, :h], beta[:, :h], initial_state=None, **kw)
     o2, S2 = _run(dev, q[:, h:], k[:, h:], v[:, h:], glog[:, h:], beta[:, h:], initial_state=S1, **kw)
-    assert torch.equal(torch.cat([o1, o2], 1), o) and torch.equal(S2, S)
+    assert rel_err(torch.cat([o1, o2], 1), o) <= 5e-3 and rel_err(S2, S) <= 5e-3
     o_ref, S_ref = OG.chunk_gated_delta_rule(q.float(), k.float(), v.float(), glog, beta, scale=1.0,
                                              output_final_state=True, use_qk_l2norm_in_kernel=True)
     assert rel_err(o, o_ref) <= 2e-2 and rel_err(S, S_ref) <= 2e-2
@@ -182,3 +185,30 @@ def test_raw_gate_logits_equal_gate_kernel_then_call(dev, dtype, d):
         assert max_abs(o1, o_ref) <= 1e-4 and max_abs(S1, S_ref) <= 1e-4
     else:
         assert rel_err(o1, o_ref) <= 2e-2 and rel_err(S1, S_ref) <= 2e-2
+
+
+def test_split_bitwise_plain(dev):
+    """Enough sequence-heads to fill the device take the plain (unsegmented) scan: one call
+    == two calls split at a chunk boundary with the fp32 state carried, bit for bit."""
+    B, T, H, d = 3, 1024, 8, 128
+    q, k, v, glog, beta, _ = _inputs(B, T, H, d, torch.bfloat16, seed=15)
+    kw = dict(scale=1.0, output_final_state=True, use_qk_l2norm_in_kernel=True)
+    o, S = _run(dev, q, k, v, glog, beta, initial_state=None, **kw)
+    h = 576  # a chunk boundary
+    o1, S1 = _run(dev, q[:, :h], k[:, :h], v[:, :h], glog[:, :h], beta[:, :h], initial_state=None, **kw)
+    o2, S2 = _run(dev, q[:, h:], k[:, h:], v[:, h:], glog[:, h:], beta[:, h:], initial_state=S1, **kw)
+    assert torch.equal(torch.cat([o1, o2], 1), o) and torch.equal(S2, S)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_segmented_recurrence(dev, dtype):
+    """A long sequence with few heads (two heads, 4,096 tokens: 8 segments of 8 chunks)
+    against the fp32 oracle, from an initial state, with its final state."""
+    B, T, H, d = 1, 4096, 2, 128
+    q, k, v, glog, beta, S0 = _inputs(B, T, H, d, dtype, seed=16)
+    kw = dict(scale=1.0, output_final_state=True, use_qk_l2norm_in_kernel=True)
+    o, S = _run(dev, q, k, v, glog, beta, initial_state=S0, **kw)
+    o_ref, S_ref = OG.chunk_gated_delta_rule(q.float(), k.float(), v.float(), glog, beta, scale=1.0,
+                                             initial_state=S0, output_final_state=True,
+                                             use_qk_l2norm_in_kernel=True)
+    assert rel_err(o, o_ref) <= 2e-2 and rel_err(S, S_ref) <= 2e-2
