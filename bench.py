@@ -135,30 +135,16 @@ def _time(torch, fn, steps, warmup):
     return e0.elapsed_time(e1) / steps
 
 
-def _time_each(torch, fn, steps, warmup):
-    """Average ms of one call of fn, each call bracketed by its own pair of HIP events on
-    the current stream (the launch's own duration, as a kernel trace reports it, without
-    the gaps between consecutive launches)."""
-    for _ in range(warmup):
-        fn()
-    torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    for e0, e1 in ev:
-        e0.record()
-        fn()
-        e1.record()
-    torch.cuda.synchronize()
-    return sum(e0.elapsed_time(e1) for e0, e1 in ev) / steps
-
-
 def bench_prefill(torch, dev, B, T, steps, warmup):
     w = Prefill(torch, dev, B, T)
     fp, fg = w.flops()
-    ms_step = _time(torch, w.step, steps, warmup)
+    # the component legs first (they also bring the GPU to its steady clocks), then the
+    # step in the layer's schedule: `warmup` untimed steps and `steps` timed ones
+    ms_polar = _time(torch, w.polar, steps, max(1, warmup // 2))
+    ms_gdn = _time(torch, w.memory, steps, max(1, warmup // 2))
     ms_seq = _time(torch, w.step_sequential, steps, max(1, warmup // 2))
     ms_ovl = _time(torch, w.step_overlap, steps, max(1, warmup // 2))
-    ms_polar = _time_each(torch, w.polar, steps, max(1, warmup // 2))
-    ms_gdn = _time(torch, w.memory, steps, max(1, warmup // 2))
+    ms_step = _time(torch, w.step, steps, warmup)
     res = dict(B=B, T=T, ms_per_step=ms_step, tflops=(fp + fg) / (ms_step * 1e-3) / 1e12,
                schedule="overlap" if w.overlap else "sequential",
                ms_sequential=ms_seq, ms_overlap=ms_ovl,
