@@ -30,6 +30,8 @@
 //    leaves the safe range -- the first block, or a new maximum far above the old.
 //  * bf16/fp16 use v_mfma_f32_32x32x16_{bf16,f16}; fp32 inputs use
 //    v_mfma_f32_32x32x2f32 (full fp32 products: the 1e-4 mode).
+#include <type_traits>
+
 #include "common.h"
 
 namespace atma {
@@ -565,6 +567,7 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
   __shared__ __attribute__((aligned(16))) T Ks[2 * TILE];
   __shared__ __attribute__((aligned(16))) T Vs[2 * TILE];
   __shared__ float s_bounds[4][2];
+  __shared__ float s_vnull[D];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -614,6 +617,59 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
   const T* qp = (const T*)args.q + b * args.q_sb + hq * args.q_sh + tok0 * args.q_st;
   const T* kp = (const T*)args.k + b * args.k_sb + hk * args.k_sh + tok0 * args.k_st;
   const T* vp = (const T*)args.v + b * args.v_sb + hk * args.v_sh + tok0 * args.v_st;
+
+  // ---- direct copies of one key block: this wave's rows 16 wave .. 16 wave + 15 of K
+  // and V, RPI rows per instruction; lane l lands at chunk position l % CPR of row
+  // l / CPR and fetches the logical chunk stored there.  The buffer ends after the
+  // last key row, so in a partial last block rows past Tk read as zeros (finite; their
+  // scores are masked and their p is exactly 0).  The descriptor's range check covers
+  // the per-lane and instruction offsets, not the scalar one: a full block keeps one
+  // byte offset per lane and copy instruction and puts the wave's row in the scalar
+  // offset, a partial block puts the whole row offset into the per-lane offset
+  // (recomputed from a laundered lane index, so it holds no extra registers).
+  const uint32_t kst2 = (uint32_t)args.k_st * 2u, vst2 = (uint32_t)args.v_st * 2u;
+  constexpr int NCP = BN / 4 / RPI;  // copy instructions per wave and tensor
+  static_assert(RPI * NCP == 16, "a wave copies 16 rows");
+  const uint32_t lrow = (uint32_t)(lane / CPR);
+  uint32_t coff[NCP];
+#pragma unroll
+  for (int r = 0; r < NCP; ++r) coff[r] = 16u * ((lane % CPR) ^ lds_swizzle<CPR>(RPI * r + lane / CPR));
+  const uint32_t krow_off = lrow * kst2, vrow_off = lrow * vst2;
+  auto copy_block = [&](int blk, int buf) {
+    const int rows = min(Tk - blk * BN, BN);
+    const auto krs = buffer_rsrc(kp + (int64_t)blk * BN * args.k_st,
+                                 (uint32_t)((rows - 1) * args.k_st + D) * 2u);
+    const auto vrs = buffer_rsrc(vp + (int64_t)blk * BN * args.v_st,
+                                 (uint32_t)((rows - 1) * args.v_st + D) * 2u);
+    if (rows == BN) {
+#pragma unroll
+      for (int r = 0; r < NCP; ++r) {
+        const uint32_t row0 = 16u * wave + RPI * r;
+        dma_buf16(krs, krow_off + coff[r], row0 * kst2, Ks + buf * TILE + row0 * D);
+        dma_buf16(vrs, vrow_off + coff[r], row0 * vst2, Vs + buf * TILE + row0 * D);
+      }
+    } else {
+      uint32_t ln = (uint32_t)lane;
+      asm volatile("" : "+v"(ln));
+      const uint32_t lr = ln / CPR;
+#pragma unroll
+      for (int r = 0; r < NCP; ++r) {
+        const uint32_t row0 = 16u * wave + RPI * r;
+        const uint32_t co = 16u * ((ln % CPR) ^ lds_swizzle<CPR>(RPI * r + lr));
+        dma_buf16(krs, (row0 + lr) * kst2 + co, 0, Ks + buf * TILE + row0 * D);
+        dma_buf16(vrs, (row0 + lr) * vst2 + co, 0, Vs + buf * TILE + row0 * D);
+      }
+    }
+  };
+  // element offset of logical chunk c of row r
+  auto swz = [](int r, int c) { return r * D + 8 * (c ^ lds_swizzle<CPR>(r)); };
+
+  // Without a window the key loop starts at block 0: its copy is issued now, so its
+  // latency overlaps the query loads and the calibration below.
+  const bool early_copy = args.window <= 0 && Tk > 0;
+  if (early_copy) copy_block(0, 0);
+  // the null value vector, read once by the epilogue
+  if (tid < D) s_vnull[tid] = args.v_null[(int64_t)hq * D + tid];
 
   // ---- per-query calibration (lane pair owns query row qi)
   const int qi = q0 + wave * 32 + ql;
@@ -672,54 +728,9 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
 #pragma unroll
   for (int t = 0; t < NT; ++t) oacc[t] = f32x16{};
 
-  // ---- direct copies of one key block: this wave's rows 16 wave .. 16 wave + 15 of K
-  // and V, RPI rows per instruction; lane l lands at chunk position l % CPR of row
-  // l / CPR and fetches the logical chunk stored there.  The buffer ends after the
-  // last key row, so in a partial last block rows past Tk read as zeros (finite; their
-  // scores are masked and their p is exactly 0).  The descriptor's range check covers
-  // the per-lane and instruction offsets, not the scalar one: a full block keeps one
-  // byte offset per lane and copy instruction and puts the wave's row in the scalar
-  // offset, a partial block puts the whole row offset into the per-lane offset
-  // (recomputed from a laundered lane index, so it holds no extra registers).
-  const uint32_t kst2 = (uint32_t)args.k_st * 2u, vst2 = (uint32_t)args.v_st * 2u;
-  constexpr int NCP = BN / 4 / RPI;  // copy instructions per wave and tensor
-  static_assert(RPI * NCP == 16, "a wave copies 16 rows");
-  const uint32_t lrow = (uint32_t)(lane / CPR);
-  uint32_t coff[NCP];
-#pragma unroll
-  for (int r = 0; r < NCP; ++r) coff[r] = 16u * ((lane % CPR) ^ lds_swizzle<CPR>(RPI * r + lane / CPR));
-  const uint32_t krow_off = lrow * kst2, vrow_off = lrow * vst2;
-  auto copy_block = [&](int blk, int buf) {
-    const int rows = min(Tk - blk * BN, BN);
-    const auto krs = buffer_rsrc(kp + (int64_t)blk * BN * args.k_st,
-                                 (uint32_t)((rows - 1) * args.k_st + D) * 2u);
-    const auto vrs = buffer_rsrc(vp + (int64_t)blk * BN * args.v_st,
-                                 (uint32_t)((rows - 1) * args.v_st + D) * 2u);
-    if (rows == BN) {
-#pragma unroll
-      for (int r = 0; r < NCP; ++r) {
-        const uint32_t row0 = 16u * wave + RPI * r;
-        dma_buf16(krs, krow_off + coff[r], row0 * kst2, Ks + buf * TILE + row0 * D);
-        dma_buf16(vrs, vrow_off + coff[r], row0 * vst2, Vs + buf * TILE + row0 * D);
-      }
-    } else {
-      uint32_t ln = (uint32_t)lane;
-      asm volatile("" : "+v"(ln));
-      const uint32_t lr = ln / CPR;
-#pragma unroll
-      for (int r = 0; r < NCP; ++r) {
-        const uint32_t row0 = 16u * wave + RPI * r;
-        const uint32_t co = 16u * ((ln % CPR) ^ lds_swizzle<CPR>(RPI * r + lr));
-        dma_buf16(krs, (row0 + lr) * kst2 + co, 0, Ks + buf * TILE + row0 * D);
-        dma_buf16(vrs, (row0 + lr) * vst2 + co, 0, Vs + buf * TILE + row0 * D);
-      }
-    }
-  };
-  // element offset of logical chunk c of row r
-  auto swz = [](int r, int c) { return r * D + 8 * (c ^ lds_swizzle<CPR>(r)); };
 
   const int nblk = nblk_end - nblk_beg;
-  if (nblk > 0) copy_block(nblk_beg, 0);
+  if (nblk > 0 && !early_copy) copy_block(nblk_beg, 0);
   const int arow = a_row_key(ql);
   // V^T operand reads: lane group gq = lane / 16 holds d rows 16 (gq % 2) + (lane % 16)
   // and keys 8 (gq / 2) + 0..7 of a 16-key step; lane s of the group reads key
@@ -728,8 +739,12 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
   const int vkey = 8 * (gq >> 1) + (sl >> 2);
   const int vcol = 16 * (gq & 1) + 4 * (sl & 3);
 
-  for (int it = 0; it < nblk; ++it) {
-    const int blk = nblk_beg + it, buf = it & 1;
+  // One 64-key block.  BUF, the LDS half that holds it, is a compile-time constant (the
+  // loop below runs blocks in pairs), so every LDS operand address is a loop-invariant
+  // lane offset plus an immediate.
+  auto key_block = [&](int it, auto BUF) {
+    constexpr int buf = decltype(BUF)::value;
+    const int blk = nblk_beg + it;
     const int k0 = blk * BN;
     wait_vmcnt<0>();  // this wave's copies of block blk have landed
     lds_barrier();    // everyone's have; everyone is done with buf ^ 1
@@ -808,8 +823,14 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
           qs = dot2<T>(pb[ps][w], pb[ps][w], qs);
         }
     };
-    exp_pack();
-    if (__ballot(!(ls <= kSafe)) != 0) {
+    // the first block takes its maximum at once (against the initial sentinel every p
+    // would overflow); later blocks try the running maximum first
+    bool redo = it == 0;
+    if (!redo) {
+      exp_pack();
+      redo = __ballot(!(ls <= kSafe)) != 0;
+    }
+    if (redo) {
       float mx = -INFINITY;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
@@ -847,7 +868,13 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
         vc = vn;
       }
     }
+  };
+  for (int it = 0; it < nblk; it += 2) {
+    key_block(it, std::integral_constant<int, 0>{});
+    if (it + 1 == nblk) break;
+    key_block(it + 1, std::integral_constant<int, 1>{});
   }
+  wait_vmcnt<0>();  // an early copy with no key block to consume it has landed
 
   // ---- fold the null sink, normalise, magnitude
   float L = l_part + __shfl_xor(l_part, 32, 64);
@@ -859,14 +886,13 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
   Q2 *= al * al;
   const float pn = exp2f(an2 - mn);
   const float Z = L + pn;
-  const float* vn = args.v_null + (int64_t)hq * D;
   float ss = 0.f;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int d = 32 * t + 8 * (i >> 2) + 4 * h + (i & 3);
-      const float s = oacc[t][i] * al + pn * vn[d];
+      const float s = oacc[t][i] * al + pn * s_vnull[d];
       oacc[t][i] = s;
       ss += s * s;
     }
