@@ -614,6 +614,16 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
   }
   const int hk = hq / G;
 
+  // ---- the head's parameters and this lane's key count are read first: later reads
+  // sit behind the direct copies, whose memory clobber would turn the uniform parameter
+  // reads into vector loads, each waited on in turn
+  const int hq_u = __builtin_amdgcn_readfirstlane(hq);
+  const float lg_raw = args.len_gain_raw[hq_u], ns_raw = args.null_slope_raw[hq_u];
+  const float nb = args.null_base[hq_u], mb_raw = args.mag_beta_raw[hq_u];
+  const int qi = q0 + wave * 32 + ql;
+  const bool q_ok = qi < Tq;
+  const float n_ld = packed ? 0.f : args.n_keys[min(qi, Tq - 1)];
+
   const T* qp = (const T*)args.q + b * args.q_sb + hq * args.q_sh + tok0 * args.q_st;
   const T* kp = (const T*)args.k + b * args.k_sb + hk * args.k_sh + tok0 * args.k_st;
   const T* vp = (const T*)args.v + b * args.v_sb + hk * args.v_sh + tok0 * args.v_st;
@@ -664,24 +674,29 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
   // element offset of logical chunk c of row r
   auto swz = [](int r, int c) { return r * D + 8 * (c ^ lds_swizzle<CPR>(r)); };
 
-  // Without a window the key loop starts at block 0: its copy is issued now, so its
-  // latency overlaps the query loads and the calibration below.
+  // ---- every load of the prologue is issued before any is consumed, so the tile pays
+  // one memory latency: after the parameters and key count, the query operand (B of
+  // S^T, consumed by the key loop), then the direct copies -- key block 0 when the loop
+  // starts there (no window) and the null value vector for the epilogue.
+  u32x4 qreg16[QSTEPS];
+#pragma unroll
+  for (int s = 0; s < QSTEPS; ++s)
+    qreg16[s] = q_ok ? *(const u32x4*)(qp + (int64_t)qi * args.q_st + 16 * s + 8 * h)
+                     : u32x4{0, 0, 0, 0};
   const bool early_copy = args.window <= 0 && Tk > 0;
   if (early_copy) copy_block(0, 0);
-  // the null value vector, read once by the epilogue
-  if (tid < D) s_vnull[tid] = args.v_null[(int64_t)hq * D + tid];
+  if (64 * wave < D)  // 64 floats per wave, straight into LDS
+    dma_buf4(buffer_rsrc(args.v_null + (int64_t)hq * D, (uint32_t)D * 4u), 4u * (uint32_t)lane,
+             256u * (uint32_t)wave, s_vnull + 64 * wave);
 
   // ---- per-query calibration (lane pair owns query row qi)
-  const int qi = q0 + wave * 32 + ql;
-  const bool q_ok = qi < Tq;
-  const float n_raw = q_ok ? (packed ? (float)(qi + 1) : args.n_keys[qi]) : 0.f;
+  const float n_raw = q_ok ? (packed ? (float)(qi + 1) : n_ld) : 0.f;
   float n_cal = n_raw;
   if (args.window > 0 && !args.preserve_length) n_cal = fminf(n_cal, (float)args.window);
   n_cal = fmaxf(n_cal, 1.f);
-  const float spg = softplus(args.len_gain_raw[hq]);
-  const float sps = softplus(args.null_slope_raw[hq]);
-  const float nb = args.null_base[hq];
-  const float mbeta = softplus(args.mag_beta_raw[hq]);
+  const float spg = softplus(lg_raw);
+  const float sps = softplus(ns_raw);
+  const float mbeta = softplus(mb_raw);
   const float temp = 1.f + spg * logf(n_cal);
   const float nullv = nb + sps * sqrtf(logf(n_cal + 1.f));
   const float c1 = temp * kLog2e * (1.f / sqrtf((float)D));
@@ -714,12 +729,7 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
   }
   const int nblk_beg = kbeg / BN, nblk_end = (kend + BN - 1) / BN;
 
-  // ---- query operand (B of S^T) in registers, consumed before the key loop
-  u32x4 qreg16[QSTEPS];
-#pragma unroll
-  for (int s = 0; s < QSTEPS; ++s)
-    qreg16[s] = q_ok ? *(const u32x4*)(qp + (int64_t)qi * args.q_st + 16 * s + 8 * h)
-                     : u32x4{0, 0, 0, 0};
+
 #pragma unroll
   for (int s = 0; s < QSTEPS; ++s) asm volatile("" ::"v"(qreg16[s]));
 
@@ -874,7 +884,8 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
     if (it + 1 == nblk) break;
     key_block(it + 1, std::integral_constant<int, 1>{});
   }
-  wait_vmcnt<0>();  // an early copy with no key block to consume it has landed
+  wait_vmcnt<0>();  // the copies have landed (also with no key block to consume them) ...
+  __syncthreads();  // ... for every wave: the epilogue reads the null vector
 
   // ---- fold the null sink, normalise, magnitude
   float L = l_part + __shfl_xor(l_part, 32, 64);
