@@ -98,6 +98,13 @@ __device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t r, uint32_
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
+// The same load marked non-temporal (nt): data read once (a KV cache streamed by decode)
+// does not displace reusable lines in L2 / MALL, and streams measurably faster.
+__device__ __forceinline__ u32x4 buffer_load16_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                                  uint32_t soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 2));
+}
+
 template <typename T>
 __device__ __forceinline__ void buffer_store16b(__amdgpu_buffer_rsrc_t r, uint32_t voff, T x) {
   static_assert(sizeof(T) == 2, "16-bit element");
@@ -196,6 +203,29 @@ __device__ __forceinline__ void wave_sync() {
 template <typename T>
 __device__ __forceinline__ T wave_xor(T x, int mask) {
   return __shfl_xor(x, mask, 64);
+}
+
+// Lane exchange inside each row of 16 lanes through DPP (no LDS crossbar round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL,
+                                                               0xF, 0xF, false));
+}
+// Max / sum over the 16 lanes of each row, the result in every lane of the row: pairs
+// within quads (quad_perm [1,0,3,2], then [2,3,0,1]), then the two quads of each half
+// row (row_half_mirror: lane i with 7 - i), then the two half rows (row_mirror: lane i
+// with 15 - i).  Every step combines one lane of each group, so all lanes agree.
+__device__ __forceinline__ float row16_max(float x) {
+  x = fmaxf(x, dpp_f32<0xB1>(x));
+  x = fmaxf(x, dpp_f32<0x4E>(x));
+  x = fmaxf(x, dpp_f32<0x141>(x));
+  return fmaxf(x, dpp_f32<0x140>(x));
+}
+__device__ __forceinline__ float row16_sum(float x) {
+  x += dpp_f32<0xB1>(x);
+  x += dpp_f32<0x4E>(x);
+  x += dpp_f32<0x141>(x);
+  return x + dpp_f32<0x140>(x);
 }
 
 __device__ __forceinline__ float wave_sum(float x) {

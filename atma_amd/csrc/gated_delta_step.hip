@@ -35,6 +35,21 @@ gated_delta_step_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, con
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
 
+  // the slot, the gates and this thread's state rows are read first, so their latency
+  // overlaps the operand loads and the norms (one wait on memory)
+  const int64_t slot = slots[b];
+  const bool ok = slot >= 0 && slot < max_seqs;
+  const int cg = tid & 15;   // float4 column group
+  const int rg = tid >> 4;   // row group
+  float* base = state + ((ok ? slot : 0) * H + h) * (int64_t)D * D + col0 + cg * 4;
+  const float g = gamma[b * H + h];
+  const float bt = beta[b * H + h];
+  f32x4 sd[RPT];
+  if (ok) {
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) sd[j] = *(const f32x4*)(base + (int64_t)(rg + 16 * j) * D);
+  }
+
   if (tid < D) {
     s_q[tid] = to_f32(q[b * q_sb + h * q_sh + tid]);
     s_k[tid] = to_f32(k[b * k_sb + (h / G) * k_sh + tid]);
@@ -51,22 +66,12 @@ gated_delta_step_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, con
   __syncthreads();
   const float inv_q = s_norm[0], inv_k = s_norm[1];
 
-  const int64_t slot = slots[b];
-  const bool ok = slot >= 0 && slot < max_seqs;
-  const int cg = tid & 15;   // float4 column group
-  const int rg = tid >> 4;   // row group
-  float* base = state + ((slot * H + h) * (int64_t)D) * D + col0 + cg * 4;
-
-  const float g = gamma[b * H + h];
-  const float bt = beta[b * H + h];
-  f32x4 sd[RPT];
   f32x4 pred = {0.f, 0.f, 0.f, 0.f};
   if (ok) {
 #pragma unroll
     for (int j = 0; j < RPT; ++j) {
       const int row = rg + 16 * j;
-      f32x4 s = *(const f32x4*)(base + (int64_t)row * D);
-      sd[j] = g * s;
+      sd[j] = g * sd[j];
       pred += (s_k[row] * inv_k) * sd[j];
     }
   }

@@ -224,7 +224,7 @@ __global__ void __launch_bounds__(256, GP == 4 ? 2 : 1) polar_decode_split_kerne
         kok[j] = pg & (pos >= t0) & (pos < t1);
 #pragma unroll
         for (int s = 0; s < KV; ++s)
-          kb[j][s] = buffer_load16(rs, k_voff + 64u * s, soff + 16u * j * row_bytes);
+          kb[j][s] = buffer_load16_nt(rs, k_voff + 64u * s, soff + 16u * j * row_bytes);
       }
     } else {
 #pragma unroll
@@ -254,7 +254,7 @@ __global__ void __launch_bounds__(256, GP == 4 ? 2 : 1) polar_decode_split_kerne
         vok[it] = pg & (pos >= t0) & (pos < t1);
 #pragma unroll
         for (int w = 0; w < VV; ++w)
-          vb[it][w] = buffer_load16(rs, v_voff + 16u * w, soff + (uint32_t)(it * KPI) * row_bytes);
+          vb[it][w] = buffer_load16_nt(rs, v_voff + 16u * w, soff + (uint32_t)(it * KPI) * row_bytes);
       }
     } else {
 #pragma unroll
@@ -313,8 +313,7 @@ __global__ void __launch_bounds__(256, GP == 4 ? 2 : 1) polar_decode_split_kerne
         sc[j][i] = kok_cur[j] ? sc[j][i] : -INFINITY;
         mx = fmaxf(mx, sc[j][i]);
       }
-#pragma unroll
-      for (int m = 8; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+      mx = row16_max(mx);  // over the 16 key columns of the row
       const float m_new = fmaxf(m_run[i], mx * c1r[i]);
       const float alpha = __builtin_amdgcn_exp2f(m_run[i] - m_new);
       m_run[i] = m_new;
@@ -381,11 +380,8 @@ __global__ void __launch_bounds__(256, GP == 4 ? 2 : 1) polar_decode_split_kerne
   // ---- reduce this wave: L, Q2 over the 16 key columns; acc over the key groups
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int m = 8; m >= 1; m >>= 1) {
-      l_part[i] += __shfl_xor(l_part[i], m, 64);
-      q2_part[i] += __shfl_xor(q2_part[i], m, 64);
-    }
+    l_part[i] = row16_sum(l_part[i]);
+    q2_part[i] = row16_sum(q2_part[i]);
   }
 #pragma unroll
   for (int r = 0; r < GP; ++r)
@@ -663,11 +659,8 @@ __global__ void __launch_bounds__(256, 2) polar_decode_balanced_kernel(DecodeArg
   auto flush = [&]() {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int m = 8; m >= 1; m >>= 1) {
-        l_part[i] += __shfl_xor(l_part[i], m, 64);
-        q2_part[i] += __shfl_xor(q2_part[i], m, 64);
-      }
+      l_part[i] = row16_sum(l_part[i]);
+      q2_part[i] = row16_sum(q2_part[i]);
     }
 #pragma unroll
     for (int r = 0; r < GP; ++r)
@@ -761,7 +754,7 @@ __global__ void __launch_bounds__(256, 2) polar_decode_balanced_kernel(DecodeArg
       const int rel = pos + 16 * j;
       kok[j] = pg & (col >= lw - rel) & (col < ctx - rel);
 #pragma unroll
-      for (int q = 0; q < KV; ++q) kb[j][q] = buffer_load16(rs, k_voff, soff + 16u * j * row_bytes + 64u * q);
+      for (int q = 0; q < KV; ++q) kb[j][q] = buffer_load16_nt(rs, k_voff, soff + 16u * j * row_bytes + 64u * q);
     }
   };
   auto load_v = [&](int s) {
@@ -773,7 +766,7 @@ __global__ void __launch_bounds__(256, 2) polar_decode_balanced_kernel(DecodeArg
     for (int it = 0; it < NIT; ++it) {
       const int rel = pos + it * KPI;
       vok[it] = pg & (kg >= lw - rel) & (kg < ctx - rel);
-      vb[it] = buffer_load16(rs, v_voff, soff + (uint32_t)(it * KPI) * row_bytes);
+      vb[it] = buffer_load16_nt(rs, v_voff, soff + (uint32_t)(it * KPI) * row_bytes);
     }
   };
 
@@ -818,8 +811,7 @@ __global__ void __launch_bounds__(256, 2) polar_decode_balanced_kernel(DecodeArg
           sc[j][i] = kok_cur[j] ? sc[j][i] : -INFINITY;
           mx = fmaxf(mx, sc[j][i]);
         }
-#pragma unroll
-        for (int m = 8; m >= 1; m >>= 1) mx = fmaxf(mx, __shfl_xor(mx, m, 64));
+        mx = row16_max(mx);  // over the 16 key columns of the row
         const float m_new = fmaxf(m_run[i], mx * c1r[i]);
         const float alpha = __builtin_amdgcn_exp2f(m_run[i] - m_new);
         m_run[i] = m_new;
@@ -895,6 +887,11 @@ __global__ void __launch_bounds__(256) polar_decode_balanced_merge_kernel(Decode
   const int sh = b * a.Hkv + hk;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int* hdr = (const int*)a.ws;
+  // every input of the epilogue is read up front, beside the header and the records, so
+  // the workgroup waits on memory once
+  const float lg_raw = a.len_gain_raw[hq], nbase = a.null_base[hq];
+  const float ns_raw = a.null_slope_raw[hq], mb_raw = a.mag_beta_raw[hq];
+  const float vnull = a.v_null[(int64_t)hq * D + (tid % D)];
   const int ctx = a.ctx[b];
   const int pb = hdr[b], nb = hdr[b + 1] - pb;
   const int U = a.Hkv * hdr[a.B];
@@ -943,8 +940,8 @@ __global__ void __launch_bounds__(256) polar_decode_balanced_merge_kernel(Decode
   float n_cal = (float)ctx;
   if (a.window > 0) n_cal = fminf(n_cal, (float)a.window);
   n_cal = fmaxf(n_cal, 1.f);
-  const float temp = 1.f + softplus(a.len_gain_raw[hq]) * logf(n_cal);
-  const float nullv = a.null_base[hq] + softplus(a.null_slope_raw[hq]) * sqrtf(logf(n_cal + 1.f));
+  const float temp = 1.f + softplus(lg_raw) * logf(n_cal);
+  const float nullv = nbase + softplus(ns_raw) * sqrtf(logf(n_cal + 1.f));
   const float an2 = temp * nullv * kLog2e;
   const float mn = fmaxf(M, an2);
   const float al = exp2f(M - mn);
@@ -952,7 +949,7 @@ __global__ void __launch_bounds__(256) polar_decode_balanced_merge_kernel(Decode
   Q2 *= al * al;
   const float pn = exp2f(an2 - mn);
   const float Z = L + pn;
-  const float sv = act ? S * al + pn * a.v_null[(int64_t)hq * D + d] : 0.f;
+  const float sv = act ? S * al + pn * vnull : 0.f;
   const float ss_w = wave_sum(sv * sv);
   if (lane == 0) red[wave] = ss_w;
   __syncthreads();
@@ -964,7 +961,7 @@ __global__ void __launch_bounds__(256) polar_decode_balanced_merge_kernel(Decode
   if (tid == 0) {
     const float n_eff = L * L / fmaxf(Q2, 1e-30f);
     const float m_eff = n_eff * (L / fmaxf(Z, a.eps));
-    const float beta = softplus(a.mag_beta_raw[hq]);
+    const float beta = softplus(mb_raw);
     ((T*)a.mag)[(int64_t)b * a.Hq + hq] = (T)tanhf(beta * log1pf(m_eff));
   }
 }
