@@ -49,6 +49,11 @@ SIGNATURES = {
     "atma_gated_delta_decode_step": (_i32, [
         _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _p, _p,
         _i64, _i64, _i64, _i64, _i64, _i32, _f32, _p]),
+    "atma_global_decode_step_supported": (_i32, [_i64, _i64, _i64, _i64, _i64, _i64, _i32]),
+    "atma_global_decode_step": (_i32, [
+        _p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _p, _p, _i64, _i64,
+        _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _i32, _i64,
+        _f32, _f32, _p, _sz, _p]),
     "atma_gated_delta_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64]),
     "atma_gated_delta_bwd": (_i32, [_p] * 14 + [_i64] * 5 + [_p, _sz, _p]),
     "atma_squared_relu_gate": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i32, _p]),

@@ -283,6 +283,52 @@ def _(q, k, v, gamma, beta, state_table, slots, eps):
     return q.new_empty((B, H, state_table.shape[3]), dtype=torch.float32)
 
 
+# --------------------------------------------------------------------------- fused decode step
+@torch.library.custom_op("atma_hip::global_decode_step",
+                         mutates_args=("k_cache", "v_cache", "state_table"))
+def global_decode_step_op(q: Tensor, k_new: Tensor, v_new: Tensor, k_cache: Tensor, v_cache: Tensor,
+                          slot_mapping: Tensor, block_tables: Tensor, context_lens: Tensor,
+                          v_null: Tensor, null_base: Tensor, null_slope_raw: Tensor,
+                          len_gain_raw: Tensor, mag_beta_raw: Tensor, gamma: Tensor, beta: Tensor,
+                          state_table: Tensor, slots: Tensor, eps: float, mem_eps: float,
+                          window: int) -> List[Tensor]:
+    _need_cuda(q, k_new, v_new, k_cache, v_cache, slot_mapping, block_tables, context_lens, gamma,
+               beta, state_table, slots)
+    lib = _lib.load()
+    q, k_new, v_new = _rows16(q), _rows16(k_new), _rows16(v_new)
+    if not k_cache.is_contiguous() or not v_cache.is_contiguous():
+        raise ValueError("k_cache / v_cache must be contiguous (num_pages, page_size, Hkv, d)")
+    if not state_table.is_contiguous() or state_table.dtype != torch.float32:
+        raise ValueError("state_table must be a contiguous float32 (max_seqs, H, dk, dv) tensor")
+    B, Hq, d = q.shape
+    num_pages, page, Hkv, _ = k_cache.shape
+    max_pages = block_tables.shape[1]
+    code = _lib.dtype_code(q.dtype)
+    c = torch.empty((B, Hq, d), device=q.device, dtype=q.dtype)
+    mag = torch.empty((B, Hq), device=q.device, dtype=q.dtype)
+    r = torch.empty((B, Hq, d), device=q.device, dtype=torch.float32)
+    ws_bytes = lib.atma_polar_decode_workspace_bytes(B, Hq, Hkv, max_pages, page, d, code)
+    ws = torch.empty((max(ws_bytes, 4) // 4,), device=q.device, dtype=torch.float32)
+    rc = lib.atma_global_decode_step(
+        q.data_ptr(), q.stride(0), q.stride(1), k_new.data_ptr(), k_new.stride(0), k_new.stride(1),
+        v_new.data_ptr(), v_new.stride(0), v_new.stride(1), k_cache.data_ptr(), v_cache.data_ptr(),
+        num_pages, page, Hkv, slot_mapping.data_ptr(), block_tables.data_ptr(), block_tables.stride(0),
+        max_pages, context_lens.data_ptr(), v_null.data_ptr(), null_base.data_ptr(),
+        null_slope_raw.data_ptr(), len_gain_raw.data_ptr(), mag_beta_raw.data_ptr(), c.data_ptr(),
+        mag.data_ptr(), gamma.data_ptr(), beta.data_ptr(), state_table.data_ptr(), state_table.shape[0],
+        slots.data_ptr(), r.data_ptr(), B, Hq, d, code, window, eps, mem_eps, ws.data_ptr(),
+        ws.numel() * 4, _lib.stream_handle(q.device))
+    _lib.check(rc, "global_decode_step")
+    return [c, mag, r]
+
+
+@global_decode_step_op.register_fake
+def _(q, k_new, v_new, k_cache, v_cache, slot_mapping, block_tables, context_lens, v_null, null_base,
+      null_slope_raw, len_gain_raw, mag_beta_raw, gamma, beta, state_table, slots, eps, mem_eps, window):
+    B, Hq, d = q.shape
+    return [q.new_empty((B, Hq, d)), q.new_empty((B, Hq)), q.new_empty((B, Hq, d), dtype=torch.float32)]
+
+
 # --------------------------------------------------------------------------- conv decode step
 @torch.library.custom_op("atma_hip::causal_conv1d_decode_step", mutates_args=("state_table",))
 def causal_conv1d_decode_step_op(x: Tensor, weight: Tensor, slots: Tensor, state_table: Tensor,

@@ -12,99 +12,13 @@
 // column reductions (pred, then r), so each state byte crosses HBM exactly once
 // in each direction.
 #include "gated_delta.h"
+#include "gated_delta_step.h"
 
 namespace atma {
 
 template <typename T, int D>
-__global__ void __launch_bounds__(256)
-gated_delta_step_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, const T* __restrict__ k,
-                        int64_t k_sb, int64_t k_sh, const T* __restrict__ v, int64_t v_sb,
-                        int64_t v_sh, const float* __restrict__ gamma,
-                        const float* __restrict__ beta, float* __restrict__ state,
-                        int64_t max_seqs, const int64_t* __restrict__ slots, float* __restrict__ r,
-                        int H, int G, float eps) {
-  constexpr int VC = 64;            // state columns per workgroup
-  constexpr int RPT = D / 16;       // state rows per thread
-  __shared__ float s_q[D], s_k[D], s_v[VC], s_u[VC];
-  __shared__ float s_red[16][VC + 4];
-  __shared__ float s_norm[2];
-
-  const int bh = blockIdx.x;
-  const int b = bh / H, h = bh % H;
-  const int col0 = blockIdx.y * VC;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-
-  // the slot, the gates and this thread's state rows are read first, so their latency
-  // overlaps the operand loads and the norms (one wait on memory)
-  const int64_t slot = slots[b];
-  const bool ok = slot >= 0 && slot < max_seqs;
-  const int cg = tid & 15;   // float4 column group
-  const int rg = tid >> 4;   // row group
-  float* base = state + ((ok ? slot : 0) * H + h) * (int64_t)D * D + col0 + cg * 4;
-  const float g = gamma[b * H + h];
-  const float bt = beta[b * H + h];
-  f32x4 sd[RPT];
-  if (ok) {
-#pragma unroll
-    for (int j = 0; j < RPT; ++j) sd[j] = *(const f32x4*)(base + (int64_t)(rg + 16 * j) * D);
-  }
-
-  if (tid < D) {
-    s_q[tid] = to_f32(q[b * q_sb + h * q_sh + tid]);
-    s_k[tid] = to_f32(k[b * k_sb + (h / G) * k_sh + tid]);
-  }
-  if (tid < VC) s_v[tid] = to_f32(v[b * v_sb + (h / G) * v_sh + col0 + tid]);
-  __syncthreads();
-  if (wave < 2) {  // wave 0: |q|^2, wave 1: |k|^2
-    const float* src = wave == 0 ? s_q : s_k;
-    float acc = 0.f;
-    for (int i = lane; i < D; i += 64) acc += src[i] * src[i];
-    acc = wave_sum(acc);
-    if (lane == 0) s_norm[wave] = 1.f / fmaxf(sqrtf(acc), eps);
-  }
-  __syncthreads();
-  const float inv_q = s_norm[0], inv_k = s_norm[1];
-
-  f32x4 pred = {0.f, 0.f, 0.f, 0.f};
-  if (ok) {
-#pragma unroll
-    for (int j = 0; j < RPT; ++j) {
-      const int row = rg + 16 * j;
-      sd[j] = g * sd[j];
-      pred += (s_k[row] * inv_k) * sd[j];
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) s_red[rg][cg * 4 + e] = pred[e];
-  __syncthreads();
-  if (tid < VC) {
-    float p = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) p += s_red[i][tid];
-    s_u[tid] = bt * (s_v[tid] - p);
-  }
-  __syncthreads();
-  f32x4 u = *(const f32x4*)(s_u + cg * 4);
-  f32x4 racc = {0.f, 0.f, 0.f, 0.f};
-  if (ok) {
-#pragma unroll
-    for (int j = 0; j < RPT; ++j) {
-      const int row = rg + 16 * j;
-      f32x4 sn = sd[j] + (s_k[row] * inv_k) * u;
-      *(f32x4*)(base + (int64_t)row * D) = sn;
-      racc += (s_q[row] * inv_q) * sn;
-    }
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) s_red[rg][cg * 4 + e] = racc[e];
-  __syncthreads();
-  if (tid < VC) {
-    float acc = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc += s_red[i][tid];
-    r[((int64_t)b * H + h) * D + col0 + tid] = ok ? acc : __builtin_nanf("");
-  }
+__global__ void __launch_bounds__(256) gated_delta_step_kernel(GdnStepArgs a) {
+  gdn_step_block<T, D>(a, blockIdx.x, blockIdx.y);
 }
 
 template <typename T, int D>
@@ -112,10 +26,9 @@ static int launch_step(const void* q, int64_t q_sb, int64_t q_sh, const void* k,
                        int64_t k_sh, const void* v, int64_t v_sb, int64_t v_sh, const float* gamma,
                        const float* beta, float* state, int64_t max_seqs, const int64_t* slots,
                        float* r, int64_t B, int64_t H, int64_t G, float eps, hipStream_t stream) {
-  dim3 grid((unsigned)(B * H), D / 64);
-  gated_delta_step_kernel<T, D><<<grid, dim3(256), 0, stream>>>(
-      (const T*)q, q_sb, q_sh, (const T*)k, k_sb, k_sh, (const T*)v, v_sb, v_sh, gamma, beta,
-      state, max_seqs, slots, r, (int)H, (int)G, eps);
+  GdnStepArgs a{q, q_sb, q_sh, k, k_sb, k_sh, v, v_sb, v_sh, gamma, beta, state, max_seqs, slots, r,
+                (int)H, (int)G, eps};
+  gated_delta_step_kernel<T, D><<<dim3((unsigned)(B * H), gdn_step_slabs<D>()), dim3(256), 0, stream>>>(a);
   return check_launch("gated_delta_decode_step");
 }
 

@@ -26,6 +26,7 @@
 #include <algorithm>
 #include <mutex>
 #include "common.h"
+#include "gated_delta_step.h"
 
 namespace atma {
 
@@ -62,6 +63,15 @@ struct DecodeArgs {
   int max_splits;
   float* ws;  // [B][Hq][max_splits][D + 4] (span split) or [NW + B*Hkv][G][D + 4] (balanced)
   int nw;     // waves launched by the balanced split
+  // Fused decode step (balanced split only): the split streams keys [.., ctx - 1) of the
+  // cache and the tail adds the newest key ctx - 1 from k_new / v_new (B, Hkv, D rows), then
+  // writes that row into the cache at slot_mapping[b] (skipped when outside the cache).
+  int excl_last;
+  const void* k_new;
+  int64_t kn_sb, kn_sh;
+  const void* v_new;
+  int64_t vn_sb, vn_sh;
+  const int32_t* slot_mapping;
 };
 
 __device__ __forceinline__ void span_of(int ctx, int window, int sp, int& t0, int& t1) {
@@ -540,9 +550,12 @@ __host__ __device__ __forceinline__ int64_t bal_header_floats(int64_t B) {
   return ((B + 1) * 4 + 255) / 256 * 64;
 }
 
-__device__ __forceinline__ int bal_units(int ctx, int window) {
+// Units of one (sequence, KV head): keys [lo, ctx - excl) from the window start lo (of the
+// full context) rounded down to 32.
+__device__ __forceinline__ int bal_units(int ctx, int window, int excl) {
   const int lo = window > 0 ? max(ctx - window, 0) : 0;
-  return ctx > lo ? (ctx - (lo & ~31) + 31) >> 5 : 0;
+  const int hi = ctx - excl;
+  return hi > lo ? (hi - (lo & ~31) + 31) >> 5 : 0;
 }
 
 // Exclusive prefix over the sequences' unit counts into pre[0 .. B] (pre[B] = total);
@@ -552,7 +565,7 @@ __device__ void bal_prefix(const DecodeArgs& a, int* pre) {
   const int E = (a.B + 255) / 256;
   const int i0 = min(tid * E, a.B), i1 = min(i0 + E, a.B);
   int sum = 0;
-  for (int i = i0; i < i1; ++i) sum += bal_units(a.ctx[i], a.window);
+  for (int i = i0; i < i1; ++i) sum += bal_units(a.ctx[i], a.window, a.excl_last);
   int incl = sum;  // inclusive scan within the wave
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
@@ -567,7 +580,7 @@ __device__ void bal_prefix(const DecodeArgs& a, int* pre) {
   int run = base + incl - sum;
   for (int i = i0; i < i1; ++i) {
     pre[i] = run;
-    run += bal_units(a.ctx[i], a.window);
+    run += bal_units(a.ctx[i], a.window, a.excl_last);
   }
   if (tid == 255) pre[a.B] = base + incl;
   __syncthreads();
@@ -627,7 +640,7 @@ __global__ void __launch_bounds__(256, 2) polar_decode_balanced_kernel(DecodeArg
     const int hk = sh - cur_b * a.Hkv;
     const int ctx = __builtin_amdgcn_readfirstlane(a.ctx[cur_b]);
     t0 = a.window > 0 ? max(ctx - a.window, 0) : 0;
-    t1 = ctx;
+    t1 = ctx - a.excl_last;  // the fused step's tail adds key ctx - 1
     float n_cal = (float)ctx;
     if (a.window > 0) n_cal = fminf(n_cal, (float)a.window);
     const float logn = logf(fmaxf(n_cal, 1.f));
@@ -730,12 +743,14 @@ __global__ void __launch_bounds__(256, 2) polar_decode_balanced_kernel(DecodeArg
   u32x4 vb[NIT];
   // unit s: buffer over its page (empty for a page outside the pool), the scalar offset
   // of its first row plus the pair's head, and the key bounds [lw, ctx) of its sequence
+  // (ctx excluding the newest key when the fused step's tail adds it)
   auto unit_rsrc = [&](int s, const T* base, int& pos, int& lw, int& ctx, uint32_t& soff, bool& pg) {
     const int4 ui = unit_info(s);
     const int sh = ui.x;
     pos = ui.y;
     ctx = ui.w;
     lw = a.window > 0 ? max(ctx - a.window, 0) : 0;
+    ctx -= a.excl_last;
     const int phys = ui.z;
     pg = (phys >= 0) & (phys < np32);
     const int hk = sh % a.Hkv;
@@ -874,14 +889,16 @@ __global__ void __launch_bounds__(256, 2) polar_decode_balanced_kernel(DecodeArg
 // One workgroup (256 threads) per (sequence, query head): combine the records of the
 // waves that streamed its pair (sh = b Hkv + h) in one pass -- each thread group keeps a
 // running max and rescales as it goes -- then fold the null sink.  The unit prefix comes
-// from the workspace header the split wrote.
+// from the workspace header the split wrote.  In the fused decode step (excl_last) the
+// newest key, ctx - 1, joins as one more partial (score from q . k_new, weight 1, value
+// v_new), and the first query head of each KV group writes the k_new / v_new row into the
+// cache at slot_mapping[b].
 template <typename T, int D>
-__global__ void __launch_bounds__(256) polar_decode_balanced_merge_kernel(DecodeArgs a) {
+__device__ __forceinline__ void bal_merge_block(const DecodeArgs& a, int bh) {
   constexpr int NG = 256 / D;
   __shared__ float red[4];
   __shared__ float s_part[NG][D];
   __shared__ float s_mlq[NG][3];
-  const int bh = blockIdx.x;
   const int b = bh / a.Hq, hq = bh % a.Hq;
   const int hk = hq / a.G, r = hq - hk * a.G;
   const int sh = b * a.Hkv + hk;
@@ -893,6 +910,25 @@ __global__ void __launch_bounds__(256) polar_decode_balanced_merge_kernel(Decode
   const float ns_raw = a.null_slope_raw[hq], mb_raw = a.mag_beta_raw[hq];
   const float vnull = a.v_null[(int64_t)hq * D + (tid % D)];
   const int ctx = a.ctx[b];
+  const bool add_new = a.excl_last && ctx >= 1;
+  float qk = 0.f, vnew = 0.f;
+  if (a.excl_last) {
+    const int d = tid % D;
+    const T* kn = (const T*)a.k_new + b * a.kn_sb + hk * a.kn_sh;
+    const T* vn = (const T*)a.v_new + b * a.vn_sb + hk * a.vn_sh;
+    if (tid < D) qk = to_f32(((const T*)a.q)[b * a.q_sb + hq * a.q_sh + d]) * to_f32(kn[d]);
+    vnew = to_f32(vn[d]);
+    if (r == 0 && tid < 2 * D / 8) {  // the cache row: 16 bytes per thread, K then V
+      const int64_t slot = a.slot_mapping[b];
+      if (slot >= 0 && slot < a.num_pages * (int64_t)a.page_size) {
+        const bool is_v = tid >= D / 8;
+        const int e = 8 * (tid % (D / 8));
+        const T* src = (is_v ? vn : kn) + e;
+        T* dst = (T*)(is_v ? a.vc : a.kc) + (slot * a.Hkv + hk) * D + e;
+        *(u32x4*)dst = *(const u32x4*)src;
+      }
+    }
+  }
   const int pb = hdr[b], nb = hdr[b + 1] - pb;
   const int U = a.Hkv * hdr[a.B];
   const int NW = min(a.nw, U);
@@ -922,11 +958,27 @@ __global__ void __launch_bounds__(256) polar_decode_balanced_merge_kernel(Decode
     s_mlq[grp][1] = L;
     s_mlq[grp][2] = Q2;
   }
+  if (a.excl_last) {  // q . k_new over the head dims
+    const float w = wave_sum(qk);
+    if (lane == 0) red[wave] = w;
+  }
   __syncthreads();
+  float n_cal = (float)ctx;
+  if (a.window > 0) n_cal = fminf(n_cal, (float)a.window);
+  n_cal = fmaxf(n_cal, 1.f);
+  const float temp = 1.f + softplus(lg_raw) * logf(n_cal);
   const bool act = tid < D;
   M = kSentinel;
 #pragma unroll
   for (int g = 0; g < NG; ++g) M = fmaxf(M, s_mlq[g][0]);
+  float m_new = kSentinel;
+  if (add_new) {
+    float sdot = 0.f;
+#pragma unroll
+    for (int v = 0; v < D / 64; ++v) sdot += red[v];
+    m_new = sdot * (temp * kLog2e * (1.f / sqrtf((float)D)));
+    M = fmaxf(M, m_new);
+  }
   S = 0.f;
   L = 0.f;
   Q2 = 0.f;
@@ -937,10 +989,12 @@ __global__ void __launch_bounds__(256) polar_decode_balanced_merge_kernel(Decode
     L += s_mlq[g][1] * f;
     Q2 += s_mlq[g][2] * f * f;
   }
-  float n_cal = (float)ctx;
-  if (a.window > 0) n_cal = fminf(n_cal, (float)a.window);
-  n_cal = fmaxf(n_cal, 1.f);
-  const float temp = 1.f + softplus(lg_raw) * logf(n_cal);
+  if (add_new) {  // the newest key: p = 2^(m_new - M), value v_new
+    const float f = exp2f(m_new - M);
+    S += vnew * f;
+    L += f;
+    Q2 += f * f;
+  }
   const float nullv = nbase + softplus(ns_raw) * sqrtf(logf(n_cal + 1.f));
   const float an2 = temp * nullv * kLog2e;
   const float mn = fmaxf(M, an2);
@@ -951,6 +1005,7 @@ __global__ void __launch_bounds__(256) polar_decode_balanced_merge_kernel(Decode
   const float Z = L + pn;
   const float sv = act ? S * al + pn * vnull : 0.f;
   const float ss_w = wave_sum(sv * sv);
+  __syncthreads();  // red is reused
   if (lane == 0) red[wave] = ss_w;
   __syncthreads();
   float ss = 0.f;
@@ -963,6 +1018,25 @@ __global__ void __launch_bounds__(256) polar_decode_balanced_merge_kernel(Decode
     const float m_eff = n_eff * (L / fmaxf(Z, a.eps));
     const float beta = softplus(mb_raw);
     ((T*)a.mag)[(int64_t)b * a.Hq + hq] = (T)tanhf(beta * log1pf(m_eff));
+  }
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256) polar_decode_balanced_merge_kernel(DecodeArgs a) {
+  bal_merge_block<T, D>(a, blockIdx.x);
+}
+
+// The fused decode step's tail: the merge workgroups (with the newest key and the cache
+// row write) first, then the gated-delta memory step's workgroups, in one launch -- the
+// merge is latency bound, the memory step bandwidth bound, so they overlap.
+template <typename T, int D>
+__global__ void __launch_bounds__(256) global_decode_tail_kernel(DecodeArgs a, GdnStepArgs m) {
+  const int nm = a.B * a.Hq;
+  if ((int)blockIdx.x < nm) {
+    bal_merge_block<T, D>(a, blockIdx.x);
+  } else {
+    const int i = (int)blockIdx.x - nm;
+    gdn_step_block<T, D>(m, i / gdn_step_slabs<D>(), i % gdn_step_slabs<D>());
   }
 }
 
@@ -1078,6 +1152,94 @@ extern "C" int atma_polar_attention_decode(
     case ATMA_F16: return d == 128 ? dispatch_gp<f16, 128>(a, s) : dispatch_gp<f16, 64>(a, s);
     default: return d == 128 ? dispatch_gp<float, 128>(a, s) : dispatch_gp<float, 64>(a, s);
   }
+}
+
+// ---------------------------------------------------------------------------------------
+// Fused decode step of the global layer: store_kvcache + polar_attention_decode +
+// gated_delta_decode_step in two launches (the balanced split over the cached keys, then
+// one tail launch: merge with the newest key taken from k_new / v_new, the cache row
+// write, and the memory step).  Same results as the three calls in that order when
+// slot_mapping[b] is the cache slot of position context_lens[b] - 1 (the engine's
+// invariant); a row whose slot is -1 is not written and still attends k_new / v_new as
+// its newest key.
+namespace atma {
+
+template <typename T, int D>
+static int launch_global_step(DecodeArgs a, GdnStepArgs m, hipStream_t s) {
+  const int GP = a.G <= 4 ? 4 : a.G <= 8 ? 8 : 16;
+  if (GP == 4) polar_decode_balanced_kernel<T, D, 4><<<dim3((unsigned)(a.nw / 4)), dim3(256), 0, s>>>(a);
+  else if (GP == 8) polar_decode_balanced_kernel<T, D, 8><<<dim3((unsigned)(a.nw / 4)), dim3(256), 0, s>>>(a);
+  else polar_decode_balanced_kernel<T, D, 16><<<dim3((unsigned)(a.nw / 4)), dim3(256), 0, s>>>(a);
+  int rc = check_launch("global_decode_step(split)");
+  if (rc) return rc;
+  const unsigned grid = (unsigned)(a.B * a.Hq + a.B * m.H * gdn_step_slabs<D>());
+  global_decode_tail_kernel<T, D><<<dim3(grid), dim3(256), 0, s>>>(a, m);
+  return check_launch("global_decode_step(tail)");
+}
+
+}  // namespace atma
+
+extern "C" int atma_global_decode_step_supported(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_pages,
+                                                 int64_t page_size, int64_t d, int dtype) {
+  return B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && Hq / Hkv <= 16 && (d == 64 || d == 128) &&
+         max_pages > 0 && atma::use_balanced(dtype, page_size, B);
+}
+
+extern "C" int atma_global_decode_step(
+    const void* q, int64_t q_sb, int64_t q_sh, const void* k_new, int64_t kn_sb, int64_t kn_sh,
+    const void* v_new, int64_t vn_sb, int64_t vn_sh, void* k_cache, void* v_cache, int64_t num_pages,
+    int64_t page_size, int64_t Hkv, const int32_t* slot_mapping, const int32_t* block_tables,
+    int64_t bt_sb, int64_t max_pages, const int32_t* context_lens, const float* v_null,
+    const float* null_base, const float* null_slope_raw, const float* len_gain_raw,
+    const float* mag_beta_raw, void* c, void* mag, const float* gamma, const float* beta,
+    float* state_table, int64_t max_seqs, const int64_t* slots, float* r, int64_t B, int64_t Hq,
+    int64_t d, int dtype, int64_t window, float eps, float mem_eps, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  using namespace atma;
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || page_size <= 0 || max_pages < 0 || num_pages < 0 || max_seqs < 0)
+    return set_error(ATMA_ERR_INVALID, "global_decode_step: bad sizes");
+  if (B == 0) return ATMA_OK;
+  if (!atma_global_decode_step_supported(B, Hq, Hkv, max_pages, page_size, d, dtype))
+    return set_error(ATMA_ERR_UNSUPPORTED,
+                     "global_decode_step: 16-bit caches with pages of whole 32-key units, a page "
+                     "table, head_dim 64 / 128, groups <= 16 and at most %d sequences", kBalMaxSeqs);
+  if (!q || !k_new || !v_new || !k_cache || !v_cache || !slot_mapping || !block_tables ||
+      !context_lens || !v_null || !null_base || !null_slope_raw || !len_gain_raw || !mag_beta_raw ||
+      !c || !mag || !gamma || !beta || !state_table || !slots || !r || num_pages <= 0)
+    return set_error(ATMA_ERR_INVALID, "global_decode_step: null pointer or empty cache");
+  const int es = 2;
+  auto al16 = [&](const void* p, int64_t s1, int64_t s2) {
+    return (uintptr_t)p % 16 == 0 && (s1 * es) % 16 == 0 && (s2 * es) % 16 == 0;
+  };
+  if (!al16(q, q_sb, q_sh) || !al16(k_new, kn_sb, kn_sh) || !al16(v_new, vn_sb, vn_sh) ||
+      (uintptr_t)k_cache % 16 || (uintptr_t)v_cache % 16)
+    return set_error(ATMA_ERR_INVALID, "global_decode_step: tensors must be 16-byte aligned rows");
+  const size_t need = atma_polar_decode_workspace_bytes(B, Hq, Hkv, max_pages, page_size, d, dtype);
+  if (!workspace || workspace_bytes < need)
+    return set_error(ATMA_ERR_WORKSPACE, "global_decode_step: workspace %zu < %zu bytes",
+                     workspace_bytes, need);
+  if (max_pages * page_size > (1ll << 30) || B * Hkv > 0x7fffffffll || B * Hq > 0x7fffffffll)
+    return set_error(ATMA_ERR_INVALID, "global_decode_step: sizes too large");
+  DecodeArgs a{};
+  a.q = q; a.q_sb = q_sb; a.q_sh = q_sh; a.kc = k_cache; a.vc = v_cache;
+  a.num_pages = num_pages; a.page_size = (int)page_size; a.Hkv = (int)Hkv;
+  a.bt = block_tables; a.bt_sb = bt_sb; a.max_pages = (int)max_pages; a.ctx = context_lens;
+  a.v_null = v_null; a.null_base = null_base; a.null_slope_raw = null_slope_raw;
+  a.len_gain_raw = len_gain_raw; a.mag_beta_raw = mag_beta_raw;
+  a.c = c; a.mag = mag; a.B = (int)B; a.Hq = (int)Hq; a.G = (int)(Hq / Hkv);
+  a.window = window > 0 ? (int)window : 0; a.eps = eps;
+  a.ws = (float*)workspace;
+  a.nw = balanced_waves(B, Hkv, max_pages, page_size);
+  a.excl_last = 1;
+  a.k_new = k_new; a.kn_sb = kn_sb; a.kn_sh = kn_sh;
+  a.v_new = v_new; a.vn_sb = vn_sb; a.vn_sh = vn_sh;
+  a.slot_mapping = slot_mapping;
+  GdnStepArgs m{q, q_sb, q_sh, k_new, kn_sb, kn_sh, v_new, vn_sb, vn_sh, gamma, beta, state_table,
+                max_seqs, slots, r, (int)Hq, (int)(Hq / Hkv), mem_eps};
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == ATMA_BF16)
+    return d == 128 ? launch_global_step<bf16, 128>(a, m, s) : launch_global_step<bf16, 64>(a, m, s);
+  return d == 128 ? launch_global_step<f16, 128>(a, m, s) : launch_global_step<f16, 64>(a, m, s);
 }
 
 // ---------------------------------------------------------------------------------------

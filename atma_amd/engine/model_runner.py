@@ -163,17 +163,23 @@ class ModelRunner:
         self.graph_bs = sorted({b for b in [1, 2, 4, 8] + list(range(16, max_bs + 1, 16)) + [max_bs]
                                 if b <= max_bs})
         self.graphs, self.graph_pool = {}, None
+        # two execs per bucket, replayed in turn: a graph exec relaunched right behind
+        # itself waits for its previous launch to retire, two alternating ones do not
+        self.graph_flip = 0
         for bs in reversed(self.graph_bs):
-            graph = torch.cuda.CUDAGraph()
             set_context(False, slot_mapping=gv["slot_mapping"][:bs], context_lens=gv["context_lens"][:bs],
                         block_tables=gv["block_tables"][:bs], seq_slots=gv["seq_slots"][:bs],
                         conv_state_tables=self.conv_state_tables)
             gv["outputs"][:bs] = self.model(gv["input_ids"][:bs], gv["positions"][:bs])   # warm-up
-            with torch.cuda.graph(graph, self.graph_pool):
-                gv["outputs"][:bs] = self.model(gv["input_ids"][:bs], gv["positions"][:bs])
-            if self.graph_pool is None:
-                self.graph_pool = graph.pool()
-            self.graphs[bs] = graph
+            pair = []
+            for _ in range(2):
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, self.graph_pool):
+                    gv["outputs"][:bs] = self.model(gv["input_ids"][:bs], gv["positions"][:bs])
+                if self.graph_pool is None:
+                    self.graph_pool = graph.pool()
+                pair.append(graph)
+            self.graphs[bs] = pair
             torch.cuda.synchronize(dev)
             reset_context()
         self.graph_vars = gv
@@ -264,7 +270,8 @@ class ModelRunner:
         if is_prefill or self.enforce_eager or not hasattr(self, "graphs") or bs > self.config.max_num_seqs:
             return self.model.compute_logits(self.model(input_ids, positions))
         ctx = get_context()
-        graph = self.graphs[next(b for b in self.graph_bs if b >= bs)]
+        graph = self.graphs[next(b for b in self.graph_bs if b >= bs)][self.graph_flip]
+        self.graph_flip ^= 1
         gv = self.graph_vars
         gv["input_ids"][:bs] = input_ids
         gv["positions"][:bs] = positions

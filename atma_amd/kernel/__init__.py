@@ -23,7 +23,8 @@ from .conv import causal_conv1d_decode_step  # noqa: E402
 from .inference_ops import packed_causal_conv1d, softcap_logits, squared_relu_gate  # noqa: E402
 from .gated_delta import (StartSignal, chunk_gated_delta_rule, gated_delta_decode_step,  # noqa: E402
                           gated_delta_gates, recurrence_pays_to_overlap)
-from .polar import polar_attention_decode, polar_attention_fwd, polar_attention_packed_fwd  # noqa: E402
+from .polar import (global_decode_step, global_decode_step_supported, polar_attention_decode,  # noqa: E402
+                    polar_attention_fwd, polar_attention_packed_fwd)
 from .polar_train import polar_attention  # noqa: E402
 
 HAS_HIP = torch.cuda.is_available()
@@ -38,6 +39,8 @@ __all__ = [
     "polar_attention",
     "polar_attention_packed_fwd",
     "polar_attention_decode",
+    "global_decode_step",
+    "global_decode_step_supported",
     "gated_delta_decode_step",
     "chunk_gated_delta_rule",
     "gated_delta_gates",

@@ -8,7 +8,7 @@ unit direction ``c`` and a bounded magnitude ``mag``.
 
 import torch
 
-from .. import _ops  # noqa: F401  (registers torch.ops.atma_hip.*)
+from .. import _lib, _ops  # noqa: F401  (_ops registers torch.ops.atma_hip.*)
 
 
 def _params(device, v_null, null_base, null_slope_raw, len_gain_raw, mag_beta_raw):
@@ -133,3 +133,58 @@ def polar_attention_decode(q, k_cache, v_cache, block_tables, context_lens, *, v
                                                        context_lens, *p, float(eps),
                                                        _window_arg(window))
     return c, mag
+
+
+def global_decode_step_supported(q, k_cache, block_tables):
+    """True when ``global_decode_step`` runs fused for these shapes: 16-bit caches whose
+    pages hold whole 32-key units, head_dim 64 / 128, GQA groups of at most 16."""
+    B, Hq, d = q.shape
+    return bool(_lib.load().atma_global_decode_step_supported(
+        B, Hq, k_cache.shape[2], block_tables.shape[1], k_cache.shape[1], d, _lib.dtype_code(q.dtype)))
+
+
+def global_decode_step(q, k_new, v_new, k_cache, v_cache, slot_mapping, block_tables, context_lens,
+                       gamma, beta, state_table, slots, *, v_null, null_base, null_slope_raw,
+                       len_gain_raw, mag_beta_raw, eps=1e-6, mem_eps=1e-12, window=None):
+    """The global layer's decode mixer (``inference/models/atma.py:546-618``): the calls
+    ``store_kvcache(k_new, v_new, caches, slot_mapping)``, ``polar_attention_decode(q,
+    caches, ...)`` and ``gated_delta_decode_step(q, k_new, v_new, gamma, beta, state_table,
+    slots)`` in that order, fused into two launches where the shapes allow it (the newest
+    key joins the attention from k_new / v_new, the cache row is written after the split
+    pass; equal to the three calls when slot_mapping[b] is the slot of position
+    context_lens[b] - 1, as the engine builds it), else the three calls.
+
+    q: (B, Hq, d); k_new, v_new: (B, Hkv, d); caches (num_pages, page_size, Hkv, d)
+    contiguous, written in place; state_table (max_seqs, Hq, d, d) fp32, advanced in place.
+    Returns (c, mag, r)."""
+    from .gated_delta import gated_delta_decode_step
+    from ..layers.attention import store_kvcache
+    if q.dim() != 3 or k_new.dim() != 3 or v_new.shape != k_new.shape or k_cache.dim() != 4 \
+            or k_cache.shape != v_cache.shape or k_new.shape[1:] != k_cache.shape[2:]:
+        raise ValueError("q (B, Hq, d), k_new / v_new (B, Hkv, d) and caches (pages, page_size, Hkv, d)")
+    if q.shape[2] != k_cache.shape[3] or q.shape[1] % k_cache.shape[2]:
+        raise ValueError(f"q {tuple(q.shape)} incompatible with cache {tuple(k_cache.shape)}")
+    if not global_decode_step_supported(q, k_cache, block_tables) or k_new.dtype != q.dtype \
+            or v_new.dtype != q.dtype or k_cache.dtype != q.dtype:
+        store_kvcache(k_new, v_new, k_cache, v_cache, slot_mapping)
+        c, mag = polar_attention_decode(q, k_cache, v_cache, block_tables, context_lens, v_null=v_null,
+                                        null_base=null_base, null_slope_raw=null_slope_raw,
+                                        len_gain_raw=len_gain_raw, mag_beta_raw=mag_beta_raw, eps=eps,
+                                        window=window)
+        r = gated_delta_decode_step(q, k_new, v_new, gamma, beta, state_table, slots, eps=mem_eps)
+        return c, mag, r
+    B, H, d = q.shape
+    if state_table.dim() != 4 or state_table.shape[1:] != (H, d, d):
+        raise ValueError(f"state_table {tuple(state_table.shape)} incompatible with q {tuple(q.shape)}")
+    if block_tables.dtype != torch.int32 or block_tables.stride(1) != 1:
+        block_tables = block_tables.to(torch.int32).contiguous()
+    context_lens = context_lens.to(device=q.device, dtype=torch.int32).contiguous()
+    slot_mapping = slot_mapping.to(device=q.device, dtype=torch.int32).contiguous()
+    gamma = gamma.to(torch.float32).reshape(B, H).contiguous()
+    beta = beta.to(torch.float32).reshape(B, H).contiguous()
+    slots = slots.to(device=q.device, dtype=torch.int64).reshape(B).contiguous()
+    p = _params(q.device, v_null, null_base, null_slope_raw, len_gain_raw, mag_beta_raw)
+    c, mag, r = torch.ops.atma_hip.global_decode_step(
+        q, k_new, v_new, k_cache, v_cache, slot_mapping, block_tables, context_lens, *p, gamma, beta,
+        state_table, slots, float(eps), float(mem_eps), _window_arg(window))
+    return c, mag, r

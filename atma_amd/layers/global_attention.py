@@ -38,8 +38,9 @@ import torch.nn.functional as F
 from torch import nn
 
 from ..kernel import (StartSignal, causal_conv1d_decode_step, chunk_gated_delta_rule,
-                      gated_delta_decode_step, gated_delta_gates, polar_attention, polar_attention_decode,
-                      polar_attention_fwd, polar_attention_packed_fwd, recurrence_pays_to_overlap)
+                      gated_delta_decode_step, gated_delta_gates, global_decode_step, polar_attention,
+                      polar_attention_decode, polar_attention_fwd, polar_attention_packed_fwd,
+                      recurrence_pays_to_overlap)
 from ..kernel.inference_ops import packed_causal_conv1d, squared_relu_gate
 from .attention import store_kvcache
 
@@ -100,12 +101,17 @@ class TitansMemory(nn.Module):
                                       start_signal=start_signal)
         return self._out(x, r), S
 
+    def decode_gates(self, x):
+        """(gamma, beta) of one decode step: retention sigmoid(w_gamma x + gamma_bias) and
+        write strength sigmoid(w_beta x + beta_bias), fp32 (B, H)."""
+        return gated_delta_gates(*self.raw_logits(x), self.gamma_bias, self.beta_bias,
+                                 decay_as_prob=True)
+
     def step(self, x, q, k, v, state_table, slots):
         """One decode step, state table advanced in place (``_mem_decode``,
         ``inference/models/atma.py:341-375``).  x: (B, dim); q: (B, H, dk); k, v:
         (B, Hkv, dk), grouped heads read in-kernel."""
-        gamma, beta = gated_delta_gates(*self.raw_logits(x), self.gamma_bias, self.beta_bias,
-                                        decay_as_prob=True)
+        gamma, beta = self.decode_gates(x)
         r = gated_delta_decode_step(q, k, v, gamma, beta, state_table, slots)
         return self._out(x, r)
 
@@ -427,15 +433,19 @@ class PolarAttention(nn.Module):
         q = self._conv_step(q.reshape(Bn, H * dk), self.canon_q, cache.conv_q, slots).view(Bn, H, dk)
         k = self._conv_step(k.reshape(Bn, Hkv * dk), self.canon_k, cache.conv_k, slots).view(Bn, Hkv, dk)
         v = self._conv_step(v.reshape(Bn, Hkv * dk), self.canon_v, cache.conv_v, slots).view(Bn, Hkv, dk)
+        if self.mem is not None:
+            # the KV write, the attention and the memory step as one fused call (two
+            # launches where the shapes allow it: the memory step runs in the attention's
+            # merge launch, and the newest key joins from k / v)
+            gamma, beta = self.mem.decode_gates(x)
+            c, mag, r = global_decode_step(q, k, v, cache.k_cache, cache.v_cache, slot_mapping,
+                                           block_tables, context_lens, gamma, beta, cache.mem_table,
+                                           slots, window=self.window, **self.polar_params())
+            return self._combine(c, mag, gate) + self.mem._out(x, r)
         store_kvcache(k, v, cache.k_cache, cache.v_cache, slot_mapping)
         c, mag = polar_attention_decode(q, cache.k_cache, cache.v_cache, block_tables, context_lens,
                                         window=self.window, **self.polar_params())
-        out = self._combine(c, mag, gate)
-        if self.mem is not None:
-            # one stream: a forked memory branch measured slower (it competes with the
-            # split kernel for CU slots)
-            out = out + self.mem.step(x, q, k, v, cache.mem_table, slots)
-        return out
+        return self._combine(c, mag, gate)
 
 
 class RMSNorm(nn.Module):

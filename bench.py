@@ -12,8 +12,9 @@ value = (Polar + gated-delta algorithmic FLOPs) / step time.
 
 Also reported in the same JSON line: configs[2] (B=1, T=65,536 and 262,144) and
 configs[3] (paged decode step: 64 sequences, ctx ~ U[1024, 32768], 256-token pages in
-a shuffled pool, store_kvcache + Polar decode + gated-delta step, replayed as a HIP
-graph), each with its roofline fraction; configs[4] (the 378M model served through the
+a shuffled pool: the layer's fused decode route -- KV write + Polar decode + gated-delta
+step in two launches -- replayed as a HIP graph; the three separate calls timed beside
+it), each with its roofline fraction; configs[4] (the 378M model served through the
 paged engine, 32 x 2,048-token prompts -> 256 greedy tokens: prefill / decode tok/s and
 wall time); configs[0] (one global block in fp32 on the GPU); plus the CPU oracle timed
 on this host (configs[1] sample and configs[0]).
@@ -162,10 +163,11 @@ class Decode:
     """one paged decode step for 64 sequences."""
 
     def __init__(self, torch, dev, seed=0, B=64, ctx_lo=1024, ctx_hi=32768, page=256, full=False):
-        from atma_amd.kernel import gated_delta_decode_step, polar_attention_decode
+        from atma_amd.kernel import gated_delta_decode_step, global_decode_step, polar_attention_decode
         from atma_amd.layers.attention import store_kvcache
         self.torch = torch
         self.dec, self.step_mem, self.store = polar_attention_decode, gated_delta_decode_step, store_kvcache
+        self.fused = global_decode_step
         gc = torch.Generator().manual_seed(seed)
         ctx = (torch.full((B,), ctx_hi) if full else torch.randint(ctx_lo, ctx_hi + 1, (B,), generator=gc))
         npg = (ctx + page - 1) // page
@@ -198,6 +200,13 @@ class Decode:
         self.graph = None
 
     def step(self):
+        """The global layer's decode route: KV write + attention + memory step, fused
+        (two launches)."""
+        return self.fused(self.q, self.knew, self.vnew, self.kc, self.vc, self.slot_map, self.bt, self.ctx,
+                          self.gamma, self.beta, self.table, self.slots, **self.p)
+
+    def step_separate(self):
+        """The same step as the reference's three calls."""
         self.store(self.knew, self.vnew, self.kc, self.vc, self.slot_map)
         c, mag = self.dec(self.q, self.kc, self.vc, self.bt, self.ctx, **self.p)
         r = self.step_mem(self.q, self.knew, self.vnew, self.gamma, self.beta, self.table, self.slots)
@@ -214,11 +223,24 @@ class Decode:
             for _ in range(2):
                 self.step()
         torch.cuda.current_stream().wait_stream(s)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self.graph_out = self.step()   # (c, mag, r): rewritten by every replay
+        # two captures of the same step, replayed in turn: relaunching one graph exec
+        # right behind itself waits for its previous launch to retire (about 8 us per
+        # step on this runtime); alternating two execs keeps the queue fed, as the
+        # engine's graph runner does
+        self.graphs = []
+        for _ in range(2):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                self.graph_out = self.step()   # (c, mag, r): rewritten by every replay
+            self.graphs.append(g)
+        self.graph = self.graphs[0]
+        self.flip = 0
 
     def replay(self):
+        self.graphs[self.flip].replay()
+        self.flip ^= 1
+
+    def replay_one(self):
         self.graph.replay()
 
     def bytes(self):
@@ -234,12 +256,17 @@ class Decode:
 def bench_decode(torch, dev, steps, warmup, full=False):
     w = Decode(torch, dev, full=full)
     w.capture()
+    # bring the GPU to its steady clocks before the first timed leg (8-16 ms of steps)
+    _time(torch, w.replay, 40, 0)
     ms_graph = _time(torch, w.replay, steps, warmup)
+    ms_one = _time(torch, w.replay_one, steps, warmup)
     ms_eager = _time(torch, w.step, steps, warmup)
+    ms_sep = _time(torch, w.step_separate, steps, warmup)
     ms_attn = _time(torch, w.attention, steps, warmup)
     kv, state, small = w.bytes()
     total = kv + state + small
     res = dict(B=w.B, ctx_sum=w.ctx_sum, pages=w.pages, ms_per_step=ms_graph, ms_eager=ms_eager,
+               ms_one_graph_exec=ms_one, ms_separate_calls_eager=ms_sep,
                tok_per_s=w.B / (ms_graph * 1e-3), bytes=total, gbs=total / (ms_graph * 1e-3) / 1e9,
                attn_ms=ms_attn, attn_bytes=kv, attn_gbs=kv / (ms_attn * 1e-3) / 1e9)
     res["hbm_frac"] = res["gbs"] / PEAK_HBM_GBS

@@ -238,6 +238,39 @@ int atma_gated_delta_decode_step(const void* q, int64_t q_sb, int64_t q_sh, cons
                                  int64_t dv, int dtype, float eps, void* stream);
 
 /*
+ * The global layer's decode mixer in two launches: the calls
+ *   store_kvcache(k_new, v_new, caches, slot_mapping)      (inference/layers/attention.py:30-56)
+ *   polar_attention_decode(q, caches, block_tables, ...)    (kernel/polar_triton.py:682-858)
+ *   gated_delta_decode_step(q, k_new, v_new, gamma, beta, state_table, slots)
+ *                                                           (kernel/gated_delta_triton.py:78-117)
+ * as made in that order by the reference's decode route (inference/models/atma.py:546-618,
+ * _mem_decode :341-375).  The length-balanced split streams the cached keys before the
+ * newest; one tail launch merges the splits with the newest key taken from k_new / v_new,
+ * writes the k_new / v_new rows into the caches at slot_mapping, and runs the memory step.
+ * Equal to the three calls when slot_mapping[b] is the cache slot of position
+ * context_lens[b] - 1 (a slot outside the cache is not written; that row still attends
+ * k_new / v_new as its newest key).  Arguments are those of the three entries:
+ * k_new, v_new: (B, Hkv, d) strides (x_sb, x_sh, 1); caches written in place;
+ * workspace: atma_polar_decode_workspace_bytes() bytes.  Serves 16-bit caches whose pages
+ * hold whole 32-key units (atma_global_decode_step_supported); ATMA_ERR_UNSUPPORTED
+ * otherwise, and the caller makes the three calls.
+ */
+int atma_global_decode_step_supported(int64_t B, int64_t Hq, int64_t Hkv, int64_t max_pages,
+                                      int64_t page_size, int64_t d, int dtype);
+int atma_global_decode_step(const void* q, int64_t q_sb, int64_t q_sh, const void* k_new,
+                            int64_t kn_sb, int64_t kn_sh, const void* v_new, int64_t vn_sb,
+                            int64_t vn_sh, void* k_cache, void* v_cache, int64_t num_pages,
+                            int64_t page_size, int64_t Hkv, const int32_t* slot_mapping,
+                            const int32_t* block_tables, int64_t bt_sb, int64_t max_pages,
+                            const int32_t* context_lens, const float* v_null,
+                            const float* null_base, const float* null_slope_raw,
+                            const float* len_gain_raw, const float* mag_beta_raw, void* c,
+                            void* mag, const float* gamma, const float* beta, float* state_table,
+                            int64_t max_seqs, const int64_t* slots, float* r, int64_t B,
+                            int64_t Hq, int64_t d, int dtype, int64_t window, float eps,
+                            float mem_eps, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * One depthwise causal-convolution step, slot-indexed state advanced IN PLACE.
  * Replaces causal_conv1d_decode_step (kernel/causal_conv1d_triton.py:18-63), the
  * global layer's Canon q / k / v convolution at decode (inference/models/atma.py:160-192).
