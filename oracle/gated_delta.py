@@ -77,6 +77,92 @@ def gated_delta_chunked(q, k, v, gamma, beta, chunk=64, S0=None):
     return torch.cat(pieces, dim=2), M
 
 
+def gated_delta_chunked_backward(q, k, v, gl, beta, S0, dO, dST, chunk=64):
+    """Chunked (WY / UT) backward of the recurrence, per sequence-head, in the ``[K, V]``
+    layout (S (dk, dv)).  The algorithm FLA's autograd of ``chunk_gated_delta_rule``
+    follows (the reference trains through it, ``model/blocks.py:44-84``), restated from
+    the chunked forward of ``gated_delta_chunked`` by reverse-mode differentiation.
+
+    q, k: (T, dk) (q already scaled / normalised, k normalised); v, dO: (T, dv); gl: (T,)
+    log decay; beta: (T,); S0, dST: (dk, dv) (dST = dL/dS_final).  Inside a chunk with
+    inclusive log decays lg, Ga = exp(lg), E[p,s] = exp(lg_p - lg_s), A = E o K K^T
+    (strictly lower), T = (I + diag(beta) A)^-1, Rq = E o Q K^T (lower incl.) and
+    w = exp(lg_C - lg), the forward is U = T diag(beta)(V - diag(Ga) K S0),
+    O = diag(Ga) Q S0 + Rq U, S_end = Ga_C S0 + K^T diag(w) U.  Backward, with dS the
+    gradient of S_end::
+
+        dU = Rq^T dO + diag(w) K dS;   dY = T^T dU;   dV = diag(beta) dY
+        dS0 = Ga_C dS + Q^T diag(Ga) dO - K^T diag(Ga beta) dY
+        dL = -(dY U^T) (strictly lower);  dA = diag(beta) dL;  dRq = dO U^T (lower)
+        dbeta = rowsum(dY o (V - diag(Ga) K S0)) + rowsum(dL o A)
+        dK = (dA o E) K + (dA o E)^T K + (dRq o E)^T Q - diag(Ga beta) dY S0^T + diag(w) U dS^T
+        dQ = (dRq o E) K + diag(Ga) dO S0^T
+        dlg = rowsum - colsum of (dA o A) and of (dRq o Rq) + Ga o (rowsum(dO o Q S0)
+              - beta o rowsum(dY o K S0)) - w o rowsum(K dS o U),
+              dlg[C-1] += sum(w o rowsum(K dS o U)) + Ga_C <dS, S0>;  dgl = reverse cumsum
+
+    Returns (dq, dk, dv, dgl, dbeta, dS0) in the inputs' dtype."""
+    T = q.shape[0]
+    dt = q.dtype
+    S = S0.clone()
+    entry = []
+    for c0 in range(0, T, chunk):                      # entry states of the chunks
+        c1 = min(c0 + chunk, T)
+        Q, K, V, g, b = q[c0:c1], k[c0:c1], v[c0:c1], gl[c0:c1], beta[c0:c1]
+        n = c1 - c0
+        lg = torch.cumsum(g, 0)
+        Ga = torch.exp(lg)
+        E = torch.exp(lg[:, None] - lg[None, :])
+        A = E * torch.tril(torch.ones(n, n, dtype=dt), -1) * (K @ K.T)
+        Tm = torch.linalg.inv(torch.eye(n, dtype=dt) + b[:, None] * A)
+        U = Tm @ (b[:, None] * (V - Ga[:, None] * (K @ S)))
+        entry.append(S)
+        S = Ga[-1] * S + K.T @ (torch.exp(lg[-1] - lg)[:, None] * U)
+    dq, dk, dv = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
+    dgl, db = torch.zeros_like(gl), torch.zeros_like(beta)
+    dS = dST.clone()
+    starts = list(range(0, T, chunk))
+    for ci in reversed(range(len(starts))):
+        c0 = starts[ci]
+        c1 = min(c0 + chunk, T)
+        n = c1 - c0
+        Q, K, V, g, b, dOc, S0c = q[c0:c1], k[c0:c1], v[c0:c1], gl[c0:c1], beta[c0:c1], dO[c0:c1], entry[ci]
+        lg = torch.cumsum(g, 0)
+        Ga = torch.exp(lg)
+        E = torch.exp(lg[:, None] - lg[None, :])
+        lower = torch.tril(torch.ones(n, n, dtype=dt), -1)
+        incl = torch.tril(torch.ones(n, n, dtype=dt))
+        A = E * lower * (K @ K.T)
+        Tm = torch.linalg.inv(torch.eye(n, dtype=dt) + b[:, None] * A)
+        KS, QS = K @ S0c, Q @ S0c
+        Vres = V - Ga[:, None] * KS
+        U = Tm @ (b[:, None] * Vres)
+        Rq = E * incl * (Q @ K.T)
+        w = torch.exp(lg[-1] - lg)
+        KdS = K @ dS
+        dU = Rq.T @ dOc + w[:, None] * KdS
+        dY = Tm.T @ dU
+        dS0 = Ga[-1] * dS + Q.T @ (Ga[:, None] * dOc) - K.T @ ((Ga * b)[:, None] * dY)
+        dv[c0:c1] = b[:, None] * dY
+        dL = -(dY @ U.T) * lower
+        dA = b[:, None] * dL
+        db[c0:c1] = (dY * Vres).sum(1) + (dL * A).sum(1)
+        GA = dA * E
+        dRq = (dOc @ U.T) * incl
+        GR = dRq * E
+        dk[c0:c1] = (GA @ K + GA.T @ K + GR.T @ Q - (Ga * b)[:, None] * (dY @ S0c.T)
+                     + w[:, None] * (U @ dS.T))
+        dq[c0:c1] = GR @ K + Ga[:, None] * (dOc @ S0c.T)
+        dlg = (dA * A).sum(1) - (dA * A).sum(0) + (dRq * Rq).sum(1) - (dRq * Rq).sum(0)
+        dlg = dlg + Ga * ((dOc * QS).sum(1) - b * (dY * KS).sum(1))
+        dw = (KdS * U).sum(1)
+        dlg = dlg - w * dw
+        dlg[-1] = dlg[-1] + (w * dw).sum() + Ga[-1] * (dS * S0c).sum()
+        dgl[c0:c1] = torch.flip(torch.cumsum(torch.flip(dlg, [0]), 0), [0])
+        dS = dS0
+    return dq, dk, dv, dgl, db, dS
+
+
 def l2_normalize(x, eps=1e-12):
     """``F.normalize(x, dim=-1)``: x / max(|x|, eps) -- the unit-key normalisation of the
     memory branch (``model/blocks.py:481-482``, ``kernel/gated_delta_triton.py:58-60``)."""
