@@ -392,6 +392,53 @@ def _(q, k, v, g, beta, initial_state, d_out, d_final_state):
             g.new_empty(g.shape), q.new_empty((B, H, dk, dv))]
 
 
+@torch.library.custom_op("atma_hip::gated_delta_bwd16_chain", mutates_args=())
+def gated_delta_bwd16_chain_op(kr: Tensor, kt: Tensor, qt: Tensor, tm: Tensor, tt: Tensor, rt: Tensor,
+                               vt: Tensor, ot: Tensor, got: Tensor, f: Tensor,
+                               initial_state: Optional[Tensor],
+                               d_final_state: Optional[Tensor]) -> List[Tensor]:
+    """The state chains of the chunked 16-bit backward: kr (BH, NC, 64, d); kt, qt, vt, ot,
+    got (BH, NC, d, 64); tm, tt, rt (BH, NC, 64, 64), 16-bit; f (BH, NC, 4, 64) fp32;
+    initial_state, d_final_state (BH, d, d) fp32 or None.  Returns [s_entry (BH, NC, d, d),
+    ds_end (BH, NC, d, d), dy (BH, NC, 64, d), d_initial_state (BH, d, d)], fp32."""
+    _need_cuda(kr, kt, qt, tm, tt, rt, vt, ot, got, f, initial_state, d_final_state)
+    BH, NC, C, d = kr.shape
+    tiles = (kr, kt, qt, tm, tt, rt, vt, ot, got)
+    shapes = [(BH, NC, C, d), (BH, NC, d, C), (BH, NC, d, C), (BH, NC, C, C), (BH, NC, C, C),
+              (BH, NC, C, C), (BH, NC, d, C), (BH, NC, d, C), (BH, NC, d, C)]
+    if C != 64 or any(tuple(t.shape) != s for t, s in zip(tiles, shapes)) \
+            or any(t.dtype != kr.dtype for t in tiles) or tuple(f.shape) != (BH, NC, 4, C) \
+            or f.dtype != torch.float32:
+        raise ValueError("gated_delta_bwd16_chain: tile shapes / dtypes do not match")
+    for st in (initial_state, d_final_state):
+        if st is not None and (tuple(st.shape) != (BH, d, d) or st.dtype != torch.float32):
+            raise ValueError("gated_delta_bwd16_chain: states must be (BH, d, d) fp32")
+    lib = _lib.load()
+    tiles = [t.contiguous() for t in tiles]
+    f = f.contiguous()
+    initial_state = None if initial_state is None else initial_state.contiguous()
+    d_final_state = None if d_final_state is None else d_final_state.contiguous()
+    o = dict(device=kr.device, dtype=torch.float32)
+    s_entry = torch.empty((BH, NC, d, d), **o)
+    ds_end = torch.empty((BH, NC, d, d), **o)
+    dy = torch.empty((BH, NC, C, d), **o)
+    ds0 = torch.empty((BH, d, d), **o)
+    rc = lib.atma_gated_delta_bwd16_chain(*[t.data_ptr() for t in tiles], f.data_ptr(), _lib.ptr(initial_state),
+                                          _lib.ptr(d_final_state), s_entry.data_ptr(), ds_end.data_ptr(),
+                                          dy.data_ptr(), ds0.data_ptr(), BH, NC, d, _lib.dtype_code(kr.dtype),
+                                          _lib.stream_handle(kr.device))
+    _lib.check(rc, "gated_delta_bwd16_chain")
+    return [s_entry, ds_end, dy, ds0]
+
+
+@gated_delta_bwd16_chain_op.register_fake
+def _(kr, kt, qt, tm, tt, rt, vt, ot, got, f, initial_state, d_final_state):
+    BH, NC, C, d = kr.shape
+    o = dict(dtype=torch.float32)
+    return [kr.new_empty((BH, NC, d, d), **o), kr.new_empty((BH, NC, d, d), **o),
+            kr.new_empty((BH, NC, C, d), **o), kr.new_empty((BH, d, d), **o)]
+
+
 # --------------------------------------------------------------------------- inference fusions
 @torch.library.custom_op("atma_hip::squared_relu_gate", mutates_args=())
 def squared_relu_gate_op(x: Tensor, gate: Tensor) -> Tensor:

@@ -307,6 +307,26 @@ int atma_gated_delta_bwd(const float* q, const float* k, const float* v, const f
                          void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Sequential part of the chunked (WY) backward of the same recurrence, for 16-bit
+ * training (the FLA chunk_gated_delta_rule autograd the reference trains through,
+ * model/blocks.py:44-84; its backward carries the state gradient across 64-token chunks
+ * the same way).  N = BH * NC chunk-heads, chunk-head major (n = bh * NC + c), d in
+ * {64, 128}; dtype ATMA_BF16 or ATMA_F16 for the tiles, all 16-byte aligned and
+ * contiguous: kr (N, 64, d) chunk rows of k (normalised); kt, qt (N, d, 64) k^T and q^T
+ * (q scaled and normalised); tm, tt, rt (N, 64, 64) T = (I + diag(beta) A)^-1, T^T and
+ * Rq^T; vt, ot, got (N, d, 64) v^T, dO^T and (diag(Ga) dO)^T; f (N, 4, 64) fp32 rows Ga,
+ * w = exp(lg_C - lg), beta, and Ga_C in f[n][3][0].  s0, dst (BH, d, d) [K, V] fp32 or
+ * NULL (zero).  Writes s_entry (N, d, d) each chunk's entry state, ds_end (N, d, d) the
+ * gradient of each chunk's exit state, dy (N, 64, d) dY = T^T dU, and ds0 (BH, d, d).
+ * Zero-padded tokens (k = v = 0, beta = 0, log decay 0) leave every output exact.
+ */
+int atma_gated_delta_bwd16_chain(const void* kr, const void* kt, const void* qt, const void* tm,
+                                 const void* tt, const void* rt, const void* vt, const void* ot,
+                                 const void* got, const float* f, const float* s0, const float* dst,
+                                 float* s_entry, float* ds_end, float* dy, float* ds0, int64_t BH,
+                                 int64_t NC, int64_t d, int dtype, void* stream);
+
+/*
  * Fused MLP activation out = gate * relu(x)^2.  Replaces squared_relu_gate
  * (kernel/inference_ops_triton.py:102-135), called by InferenceMLP.forward
  * (inference/models/atma.py:87-96).  x, gate: (rows, width) with strides (x_s0, x_s1),

@@ -1,0 +1,102 @@
+"""GPU parity of the chunked (WY) 16-bit training backward of the gated-delta recurrence
+(the algorithm of the FLA autograd the reference trains through, model/blocks.py:44-84).
+
+  * the state-chain kernel (``gated_delta_bwd16_chain``) against its fp32 torch
+    restatement on the same 16-bit tiles (2e-2 of max|x| per output: the kernel rounds
+    the state and the per-chunk intermediates to 16 bits as MFMA operands);
+  * the whole 16-bit route of ``chunk_gated_delta_rule``'s autograd against fp64 autograd
+    of the sequential definition (scripts/titans_proto.py:53-76, pinned by gradcheck in
+    the oracle tests): every gradient within 2e-2 of max|grad| per tensor, over ragged
+    lengths, both head dims, bf16 and fp16, grouped KV heads, an initial state and a
+    final-state cotangent or none."""
+
+import pytest
+import torch
+
+from helpers import bwd16_chain_reference, rel_err
+from oracle import gated_delta as OG
+
+pytestmark = pytest.mark.gpu
+
+
+def _prepared(B, T, H, d, dtype, seed, dev):
+    g = torch.Generator().manual_seed(seed)
+    q = OG.l2_normalize(torch.randn(B, T, H, d, generator=g))
+    k = OG.l2_normalize(torch.randn(B, T, H, d, generator=g))
+    v, dO = torch.randn(B, T, H, d, generator=g).to(dtype), torch.randn(B, T, H, d, generator=g).to(dtype)
+    gl = torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=g) + 3.0)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g))
+    S0 = torch.randn(B, H, d, d, generator=g) * 0.3
+    dST = torch.randn(B, H, d, d, generator=g)
+    return [x.to(dev) for x in (q, k, v, gl, beta, dO, S0, dST)]
+
+
+@pytest.mark.parametrize("B,T,H,d,dtype,states", [
+    (1, 64, 1, 128, torch.bfloat16, True),
+    (2, 300, 3, 64, torch.bfloat16, True),
+    (1, 1000, 2, 128, torch.float16, False),
+    (8, 2048, 8, 128, torch.bfloat16, False),   # configs[1] training shape
+])
+def test_chain_kernel_vs_fp32_restatement(dev, B, T, H, d, dtype, states):
+    from atma_amd.kernel.gated_delta import _bwd16_prep
+    q, k, v, gl, beta, dO, S0, dST = _prepared(B, T, H, d, dtype, T + d, dev)
+    prep = _bwd16_prep(q, k, v, gl, beta, dO, dtype)
+    s0 = S0.reshape(B * H, d, d) if states else None
+    dst = dST.reshape(B * H, d, d) if states else None
+    print(f"chain B={B} T={T} H={H} d={d} {dtype}", flush=True)
+    got = torch.ops.atma_hip.gated_delta_bwd16_chain(*prep["tiles"], s0, dst)
+    torch.cuda.synchronize()
+    ref = bwd16_chain_reference(*prep["tiles"], s0, dst)
+    for name, a, r in zip(["s_entry", "ds_end", "dy", "ds0"], got, ref):
+        assert torch.isfinite(a).all(), name
+        assert rel_err(a, r) <= 2e-2, (name, rel_err(a, r))
+
+
+def _oracle(q, k, v, g, beta, S0, scale):
+    H = q.shape[2]
+    if k.shape[2] != H:
+        k, v = k.repeat_interleave(H // k.shape[2], 2), v.repeat_interleave(H // k.shape[2], 2)
+    qf, kf, vf = (OG.l2_normalize(x.double().transpose(1, 2)) if i < 2 else x.double().transpose(1, 2)
+                  for i, x in enumerate((q, k, v)))
+    R, S = OG.gated_delta_sequential(qf * scale, kf, vf, torch.exp(g.double()).transpose(1, 2),
+                                     beta.double().transpose(1, 2),
+                                     None if S0 is None else S0.double().transpose(-1, -2))
+    return R.transpose(1, 2), S.transpose(-1, -2)
+
+
+@pytest.mark.parametrize("B,T,H,Hkv,d,dtype,s0,dfinal", [
+    (1, 1, 2, 2, 64, torch.bfloat16, True, True),
+    (1, 63, 2, 1, 128, torch.bfloat16, False, True),
+    (2, 129, 2, 2, 64, torch.float16, True, False),
+    (1, 200, 4, 2, 128, torch.bfloat16, True, True),
+    (2, 256, 2, 2, 128, torch.float16, False, False),
+])
+def test_bwd16_route_vs_fp64_autograd(dev, B, T, H, Hkv, d, dtype, s0, dfinal):
+    from atma_amd.kernel import chunk_gated_delta_rule
+    gen = torch.Generator().manual_seed(T * 3 + d)
+    q = torch.randn(B, T, H, d, generator=gen).to(dtype)
+    k = torch.randn(B, T, Hkv, d, generator=gen).to(dtype)
+    v = torch.randn(B, T, Hkv, d, generator=gen).to(dtype)
+    g = torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=gen) + 2.0)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=gen))
+    S0 = torch.randn(B, H, d, d, generator=gen) * 0.3 if s0 else None
+    Wo, Ws = torch.randn(B, T, H, d, generator=gen), torch.randn(B, H, d, d, generator=gen)
+
+    leaves = [x.clone().double().requires_grad_(True) for x in (q, k, v, g, beta)]
+    S0r = S0.clone().double().requires_grad_(True) if s0 else None
+    o, S = _oracle(*leaves, S0r, 1.0)
+    loss = (o * Wo.double()).sum() + ((S * Ws.double()).sum() if dfinal else 0.0)
+    ref = torch.autograd.grad(loss, leaves + ([S0r] if s0 else []))
+
+    print(f"route B={B} T={T} H={H}/{Hkv} d={d} {dtype}", flush=True)
+    dl = [x.to(dev).requires_grad_(True) for x in (q, k, v, g, beta)]
+    S0d = S0.to(dev).requires_grad_(True) if s0 else None
+    od, Sd = chunk_gated_delta_rule(*dl, scale=1.0, initial_state=S0d, output_final_state=True,
+                                    use_qk_l2norm_in_kernel=True)
+    assert od.dtype == dtype
+    lossd = (od.float() * Wo.to(dev)).sum() + ((Sd * Ws.to(dev)).sum() if dfinal else 0.0)
+    got = torch.autograd.grad(lossd, dl + ([S0d] if s0 else []))
+    for name, a, b in zip(["dq", "dk", "dv", "dg", "dbeta", "dS0"], got, ref):
+        assert a.shape == b.shape, name
+        assert torch.isfinite(a.float()).all(), name
+        assert rel_err(a.float(), b) <= 2e-2, (name, rel_err(a.float(), b))
