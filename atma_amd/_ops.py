@@ -392,51 +392,123 @@ def _(q, k, v, g, beta, initial_state, d_out, d_final_state):
             g.new_empty(g.shape), q.new_empty((B, H, dk, dv))]
 
 
-@torch.library.custom_op("atma_hip::gated_delta_bwd16_chain", mutates_args=())
-def gated_delta_bwd16_chain_op(kr: Tensor, kt: Tensor, qt: Tensor, tm: Tensor, tt: Tensor, rt: Tensor,
-                               vt: Tensor, ot: Tensor, got: Tensor, f: Tensor,
-                               initial_state: Optional[Tensor],
-                               d_final_state: Optional[Tensor]) -> List[Tensor]:
-    """The state chains of the chunked 16-bit backward: kr (BH, NC, 64, d); kt, qt, vt, ot,
-    got (BH, NC, d, 64); tm, tt, rt (BH, NC, 64, 64), 16-bit; f (BH, NC, 4, 64) fp32;
-    initial_state, d_final_state (BH, d, d) fp32 or None.  Returns [s_entry (BH, NC, d, d),
-    ds_end (BH, NC, d, d), dy (BH, NC, 64, d), d_initial_state (BH, d, d)], fp32."""
-    _need_cuda(kr, kt, qt, tm, tt, rt, vt, ot, got, f, initial_state, d_final_state)
-    BH, NC, C, d = kr.shape
-    tiles = (kr, kt, qt, tm, tt, rt, vt, ot, got)
-    shapes = [(BH, NC, C, d), (BH, NC, d, C), (BH, NC, d, C), (BH, NC, C, C), (BH, NC, C, C),
-              (BH, NC, C, C), (BH, NC, d, C), (BH, NC, d, C), (BH, NC, d, C)]
-    if C != 64 or any(tuple(t.shape) != s for t, s in zip(tiles, shapes)) \
-            or any(t.dtype != kr.dtype for t in tiles) or tuple(f.shape) != (BH, NC, 4, C) \
-            or f.dtype != torch.float32:
-        raise ValueError("gated_delta_bwd16_chain: tile shapes / dtypes do not match")
-    for st in (initial_state, d_final_state):
-        if st is not None and (tuple(st.shape) != (BH, d, d) or st.dtype != torch.float32):
-            raise ValueError("gated_delta_bwd16_chain: states must be (BH, d, d) fp32")
+def _bwd16_check(q, k, v, d_out, g, beta):
+    _need_cuda(q, k, v, d_out, g, beta)
+    if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape or d_out.shape != q.shape:
+        raise ValueError("gated_delta_bwd16: q, k, v, d_out must all be (B, T, H, d)")
+    B, T, H, d = q.shape
+    if tuple(g.shape) != (B, T, H) or tuple(beta.shape) != (B, T, H):
+        raise ValueError("gated_delta_bwd16: g and beta must be (B, T, H)")
+    if q.dtype != torch.float32 or k.dtype != torch.float32 or g.dtype != torch.float32 \
+            or beta.dtype != torch.float32:
+        raise ValueError("gated_delta_bwd16: q, k, g, beta must be fp32")
+    if v.dtype not in (torch.bfloat16, torch.float16) or d_out.dtype != v.dtype:
+        raise ValueError("gated_delta_bwd16: v and d_out must share a 16-bit dtype")
+    return [t.contiguous() for t in (q, k, v, d_out, g, beta)]
+
+
+def _bwd16_prep(q, k, v, d_out, g, beta):
     lib = _lib.load()
-    tiles = [t.contiguous() for t in tiles]
-    f = f.contiguous()
-    initial_state = None if initial_state is None else initial_state.contiguous()
-    d_final_state = None if d_final_state is None else d_final_state.contiguous()
-    o = dict(device=kr.device, dtype=torch.float32)
-    s_entry = torch.empty((BH, NC, d, d), **o)
-    ds_end = torch.empty((BH, NC, d, d), **o)
-    dy = torch.empty((BH, NC, C, d), **o)
-    ds0 = torch.empty((BH, d, d), **o)
-    rc = lib.atma_gated_delta_bwd16_chain(*[t.data_ptr() for t in tiles], f.data_ptr(), _lib.ptr(initial_state),
-                                          _lib.ptr(d_final_state), s_entry.data_ptr(), ds_end.data_ptr(),
-                                          dy.data_ptr(), ds0.data_ptr(), BH, NC, d, _lib.dtype_code(kr.dtype),
-                                          _lib.stream_handle(kr.device))
-    _lib.check(rc, "gated_delta_bwd16_chain")
-    return [s_entry, ds_end, dy, ds0]
+    B, T, H, d = q.shape
+    NC = (T + 63) // 64
+    BH = B * H
+    t16 = dict(device=q.device, dtype=v.dtype)
+    kr, qr = (torch.empty((BH, NC, 64, d), **t16) for _ in range(2))
+    kt, qt, vt, ot, got = (torch.empty((BH, NC, d, 64), **t16) for _ in range(5))
+    tm, tt, rt = (torch.empty((BH, NC, 64, 64), **t16) for _ in range(3))
+    f = torch.empty((BH, NC, 5, 64), device=q.device, dtype=torch.float32)
+    rc = lib.atma_gated_delta_bwd16_prep(q.data_ptr(), k.data_ptr(), v.data_ptr(), d_out.data_ptr(), g.data_ptr(),
+                                         beta.data_ptr(), kr.data_ptr(), kt.data_ptr(), qr.data_ptr(), qt.data_ptr(),
+                                         tm.data_ptr(), tt.data_ptr(), rt.data_ptr(), vt.data_ptr(), ot.data_ptr(),
+                                         got.data_ptr(), f.data_ptr(), B, T, H, d, _lib.dtype_code(v.dtype),
+                                         _lib.stream_handle(q.device))
+    _lib.check(rc, "gated_delta_bwd16_prep")
+    return [kr, kt, qr, qt, tm, tt, rt, vt, ot, got, f]
 
 
-@gated_delta_bwd16_chain_op.register_fake
-def _(kr, kt, qt, tm, tt, rt, vt, ot, got, f, initial_state, d_final_state):
+def _bwd16_chain(kr, kt, qt, tm, tt, rt, vt, ot, got, f, s0, dst):
+    lib = _lib.load()
     BH, NC, C, d = kr.shape
-    o = dict(dtype=torch.float32)
-    return [kr.new_empty((BH, NC, d, d), **o), kr.new_empty((BH, NC, d, d), **o),
-            kr.new_empty((BH, NC, C, d), **o), kr.new_empty((BH, d, d), **o)]
+    t16 = dict(device=kr.device, dtype=kr.dtype)
+    s_entry, ds_end = (torch.empty((BH, NC, d, d), **t16) for _ in range(2))
+    u = torch.empty((BH, NC, C, d), **t16)
+    dy = torch.empty((BH, NC, C, d), device=kr.device, dtype=torch.float32)
+    ds0 = torch.empty((BH, d, d), device=kr.device, dtype=torch.float32)
+    rc = lib.atma_gated_delta_bwd16_chain(kr.data_ptr(), kt.data_ptr(), qt.data_ptr(), tm.data_ptr(), tt.data_ptr(),
+                                          rt.data_ptr(), vt.data_ptr(), ot.data_ptr(), got.data_ptr(), f.data_ptr(),
+                                          _lib.ptr(s0), _lib.ptr(dst), s_entry.data_ptr(), ds_end.data_ptr(),
+                                          u.data_ptr(), dy.data_ptr(), ds0.data_ptr(), BH, NC, d,
+                                          _lib.dtype_code(kr.dtype), _lib.stream_handle(kr.device))
+    _lib.check(rc, "gated_delta_bwd16_chain")
+    return [s_entry, ds_end, u, dy, ds0]
+
+
+def _bwd16_local(B, T, H, kr, kt, qr, qt, v, d_out, f, s_entry, ds_end, u, dy):
+    lib = _lib.load()
+    d = kr.shape[-1]
+    f32 = dict(device=kr.device, dtype=torch.float32)
+    dq, dk = (torch.empty((B, T, H, d), **f32) for _ in range(2))
+    dv = torch.empty((B, T, H, d), device=kr.device, dtype=v.dtype)
+    dg, db = (torch.empty((B, T, H), **f32) for _ in range(2))
+    rc = lib.atma_gated_delta_bwd16_local(kr.data_ptr(), kt.data_ptr(), qr.data_ptr(), qt.data_ptr(), v.data_ptr(),
+                                          d_out.data_ptr(), f.data_ptr(), s_entry.data_ptr(), ds_end.data_ptr(),
+                                          u.data_ptr(), dy.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                                          dg.data_ptr(), db.data_ptr(), B, T, H, d, _lib.dtype_code(v.dtype),
+                                          _lib.stream_handle(kr.device))
+    _lib.check(rc, "gated_delta_bwd16_local")
+    return [dq, dk, dv, dg, db]
+
+
+@torch.library.custom_op("atma_hip::gated_delta_bwd16", mutates_args=())
+def gated_delta_bwd16_op(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,
+                         initial_state: Optional[Tensor], d_out: Tensor,
+                         d_final_state: Optional[Tensor]) -> List[Tensor]:
+    """Chunked (WY) backward for 16-bit training: q (scaled, normalised), k (normalised)
+    (B, T, H, d) fp32; v, d_out (B, T, H, d) 16-bit; g (log decay), beta (B, T, H) fp32;
+    initial_state, d_final_state (B, H, d, d) fp32 or None.  Returns dq, dk (fp32), dv (v's
+    dtype), dg, dbeta, d_initial_state (fp32).  Three launches: prep, chain, local."""
+    q, k, v, d_out, g, beta = _bwd16_check(q, k, v, d_out, g, beta)
+    B, T, H, d = q.shape
+    f32 = dict(device=q.device, dtype=torch.float32)
+    if T == 0:
+        ds0 = torch.zeros((B, H, d, d), **f32) if d_final_state is None else d_final_state.float().clone()
+        return [torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v), torch.zeros_like(g),
+                torch.zeros_like(beta), ds0]
+    st = [None if x is None else x.to(torch.float32).contiguous().reshape(B * H, d, d)
+          for x in (initial_state, d_final_state)]
+    for x in st:
+        if x is not None and x.numel() != B * H * d * d:
+            raise ValueError("gated_delta_bwd16: states must be (B, H, d, d)")
+    kr, kt, qr, qt, tm, tt, rt, vt, ot, got, f = _bwd16_prep(q, k, v, d_out, g, beta)
+    s_entry, ds_end, u, dy, ds0 = _bwd16_chain(kr, kt, qt, tm, tt, rt, vt, ot, got, f, st[0], st[1])
+    dq, dk, dv, dg, db = _bwd16_local(B, T, H, kr, kt, qr, qt, v, d_out, f, s_entry, ds_end, u, dy)
+    return [dq, dk, dv, dg, db, ds0.reshape(B, H, d, d)]
+
+
+@gated_delta_bwd16_op.register_fake
+def _(q, k, v, g, beta, initial_state, d_out, d_final_state):
+    B, T, H, d = q.shape
+    return [q.new_empty(q.shape), q.new_empty(q.shape), v.new_empty(v.shape), g.new_empty(g.shape),
+            g.new_empty(g.shape), q.new_empty((B, H, d, d))]
+
+
+def gated_delta_bwd16_stages(q, k, v, g, beta, initial_state, d_out, d_final_state):
+    """The three launches of ``gated_delta_bwd16`` with every intermediate returned (for
+    tests): dict of the prep's tiles (kr, kt, qr, qt, tm, tt, rt, vt, ot, got, f; chunk-head
+    tensors shaped (B*H, NC, ...)), the chain's outputs (s_entry, ds_end, u, dy, ds0) and
+    the local gradients (dq, dk, dv, dg, db)."""
+    q, k, v, d_out, g, beta = _bwd16_check(q, k, v, d_out, g, beta)
+    B, T, H, d = q.shape
+    st = [None if x is None else x.to(torch.float32).contiguous().reshape(B * H, d, d)
+          for x in (initial_state, d_final_state)]
+    names = ["kr", "kt", "qr", "qt", "tm", "tt", "rt", "vt", "ot", "got", "f"]
+    out = dict(zip(names, _bwd16_prep(q, k, v, d_out, g, beta)))
+    chain = _bwd16_chain(*(out[n] for n in ("kr", "kt", "qt", "tm", "tt", "rt", "vt", "ot", "got", "f")), *st)
+    out.update(zip(["s_entry", "ds_end", "u", "dy", "ds0"], chain))
+    loc = _bwd16_local(B, T, H, out["kr"], out["kt"], out["qr"], out["qt"], v, d_out, out["f"], out["s_entry"],
+                       out["ds_end"], out["u"], out["dy"])
+    out.update(zip(["dq", "dk", "dv", "dg", "db"], loc))
+    return out
 
 
 # --------------------------------------------------------------------------- inference fusions

@@ -22,9 +22,13 @@
 // v_mfma_f32_16x16x32 (fp32 accumulation); the state and every per-column intermediate
 // (Y, U, dU, dY) go through a per-wave transposed bf16 buffer ([column][k], 16 bytes per
 // lane per fragment) to become the B operand of the next product.
+#include <initializer_list>
+
 #include "common.h"
 
 namespace atma {
+
+constexpr int kFRows = 5;  // per-token factor rows of a chunk: Ga, w, beta, Ga_C, lg
 
 struct Bwd16ChainArgs {
   const void* kr;    // [N][64][D]  k rows of each chunk (N = BH * NC, chunk-head major)
@@ -36,15 +40,33 @@ struct Bwd16ChainArgs {
   const void* vt;    // [N][D][64]  v^T
   const void* ot;    // [N][D][64]  dO^T
   const void* got;   // [N][D][64]  (diag(Ga) dO)^T
-  const float* f;    // [N][4][64]  Ga, w, beta, then Ga_C at [3][0]
+  const float* f;    // [N][5][64]  Ga, w, beta, Ga_C (all 64 entries), lg
   const float* s0;   // [BH][D][D] initial state, or null (zero)
   const float* dst;  // [BH][D][D] final-state cotangent, or null (zero)
-  float* s_entry;    // [N][D][D]  out: each chunk's entry state
-  float* ds_end;     // [N][D][D]  out: the gradient of each chunk's exit state
+  void* s_entry;     // [N][D][D]  out (16-bit): each chunk's entry state
+  void* ds_end;      // [N][D][D]  out (16-bit): the gradient of each chunk's exit state
+  void* u;           // [N][64][D] out (16-bit): U = T diag(beta) (V - diag(Ga) K S)
   float* dy;         // [N][64][D] out: dY
   float* ds0;        // [BH][D][D] out: the gradient of the initial state
   int BH, NC;
 };
+
+// A contiguous 16-bit tile of N * 256 16-byte chunks: thread tid holds chunks tid + 256 j.
+template <int N>
+__device__ __forceinline__ void tile_load(u32x4 (&r)[N], const void* src, int tid) {
+  const u32x4* s = (const u32x4*)src;
+#pragma unroll
+  for (int j = 0; j < N; ++j) r[j] = s[tid + 256 * j];
+}
+// ... into LDS rows of CPR chunks, padded to PITCH elements
+template <int N, int CPR, int PITCH, typename T>
+__device__ __forceinline__ void tile_store(T* dst, const u32x4 (&r)[N], int tid) {
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const int i = tid + 256 * j;
+    *(u32x4*)(dst + (i / CPR) * PITCH + 8 * (i % CPR)) = r[j];
+  }
+}
 
 template <typename T, int D>
 __global__ void __launch_bounds__(256, 1) gdn_bwd16_chain_kernel(Bwd16ChainArgs a) {
@@ -70,22 +92,18 @@ __global__ void __launch_bounds__(256, 1) gdn_bwd16_chain_kernel(Bwd16ChainArgs 
   const int v0 = 64 * (blockIdx.x % (D / 64)) + 16 * wave;  // the wave's first column
   const int col = v0 + c16;                                  // the lane's column (C layout)
 
-  // 64-row x `cols` tile from global (row-major, unpadded) into padded LDS, all threads
-  auto copy_tile = [&](T* dst, const void* src, int rows, int cols, int pitch) {
-    const int cpr = cols / 8;
-    const T* s = (const T*)src;
-    for (int i = tid; i < rows * cpr; i += 256) {
-      const int r = i / cpr, ch = i - r * cpr;
-      *(u32x4*)(dst + r * pitch + 8 * ch) = *(const u32x4*)(s + (int64_t)r * cols + 8 * ch);
-    }
+  constexpr int NT = D / 32;  // chunks per thread of a 64 x D or D x 64 tile
+  // the wave's 16 rows of a [D][64] tile: 2 chunks per lane
+  auto rows16_load = [&](u32x4 (&r)[2], const void* src) {
+    const u32x4* s = (const u32x4*)src;
+    r[0] = s[lane];
+    r[1] = s[lane + 64];
   };
-  // the wave's 16 rows of a [D][64] tile
-  auto copy_rows16 = [&](T* dst, const void* src) {
-    const T* s = (const T*)src;
+  auto rows16_store = [&](T* dst, const u32x4 (&r)[2]) {
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-      const int i = lane + 64 * k, r = i >> 3, ch = i & 7;
-      *(u32x4*)(dst + r * PC + 8 * ch) = *(const u32x4*)(s + r * C + 8 * ch);
+      const int i = lane + 64 * k;
+      *(u32x4*)(dst + (i >> 3) * PC + 8 * (i & 7)) = r[k];
     }
   };
   // fragment: row (row0 + c16) of a padded tile, 8 elements from column k0 + 8 g (the A
@@ -108,23 +126,34 @@ __global__ void __launch_bounds__(256, 1) gdn_bwd16_chain_kernel(Bwd16ChainArgs 
     for (int i = 0; i < 4; ++i)
       S[t][i] = a.s0 ? a.s0[((int64_t)bh * D + rows_of(t, i)) * D + col] : 0.f;
 
+  // the next chunk's operands are loaded into registers while this one computes
+  u32x4 rk[NT], rkt[NT], rtm[2];
+  u32x2 rv[4];
+  float rf;
+  auto fwd_load = [&](int64_t n) {
+    tile_load(rk, (const T*)a.kr + n * C * D, tid);
+    tile_load(rkt, (const T*)a.kt + n * D * C, tid);
+    tile_load(rtm, (const T*)a.tm + n * C * C, tid);
+    rf = a.f[n * kFRows * C + tid];
+    const T* vrow = (const T*)a.vt + (n * D + col) * C;
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) rv[rt] = *(const u32x2*)(vrow + 16 * rt + 4 * g);
+  };
+  fwd_load((int64_t)bh * a.NC);
   for (int c = 0; c < a.NC; ++c) {
     const int64_t n = (int64_t)bh * a.NC + c;
     __syncthreads();  // every wave is done with the previous chunk's tiles
-    copy_tile(Kr, (const T*)a.kr + n * C * D, C, D, PD);
-    copy_tile(Kt, (const T*)a.kt + n * D * C, D, C, PC);
-    copy_tile(Tm, (const T*)a.tm + n * C * C, C, C, PC);
-    if (tid < 4 * C) Fs[tid] = a.f[n * 4 * C + tid];
+    tile_store<NT, D / 8, PD>(Kr, rk, tid);
+    tile_store<NT, 8, PC>(Kt, rkt, tid);
+    tile_store<2, 8, PC>(Tm, rtm, tid);
+    Fs[tid] = rf;
     f32x4 Vc[4];  // v of the lane's column, C layout (rows = tokens)
-    {
-      const T* vrow = (const T*)a.vt + (n * D + col) * C;
 #pragma unroll
-      for (int rt = 0; rt < 4; ++rt) {
-        const u32x2 x = *(const u32x2*)(vrow + 16 * rt + 4 * g);
-        Vc[rt] = f32x4{elem16<T>(u32x4{x[0], x[1], 0, 0}, 0), elem16<T>(u32x4{x[0], x[1], 0, 0}, 1),
-                       elem16<T>(u32x4{x[0], x[1], 0, 0}, 2), elem16<T>(u32x4{x[0], x[1], 0, 0}, 3)};
-      }
+    for (int rt = 0; rt < 4; ++rt) {
+      const u32x4 x = {rv[rt][0], rv[rt][1], 0, 0};
+      Vc[rt] = f32x4{elem16<T>(x, 0), elem16<T>(x, 1), elem16<T>(x, 2), elem16<T>(x, 3)};
     }
+    if (c + 1 < a.NC) fwd_load(n + 1);
 #pragma unroll
     for (int t = 0; t < DT; ++t) put_t(Sb[wave], PD, t, S[t]);
     __syncthreads();
@@ -161,6 +190,11 @@ __global__ void __launch_bounds__(256, 1) gdn_bwd16_chain_kernel(Bwd16ChainArgs 
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt) U[rt] = mfma16x16x32<T>(frag(Tm, PC, 16 * rt, 32 * s), bf, U[rt]);
     }
+    T* uo = (T*)a.u + n * C * D;
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) uo[rows_of(rt, i) * D + col] = from_f32<T>(U[rt][i]);
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       f32x4 x;
@@ -170,11 +204,11 @@ __global__ void __launch_bounds__(256, 1) gdn_bwd16_chain_kernel(Bwd16ChainArgs 
     }
     wave_sync();
     // the entry state, then S <- Ga_C S + K^T diag(w) U
-    float* se = a.s_entry + n * D * D;
+    T* se = (T*)a.s_entry + n * D * D;
 #pragma unroll
     for (int t = 0; t < DT; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) se[rows_of(t, i) * D + col] = S[t][i];
+      for (int i = 0; i < 4; ++i) se[rows_of(t, i) * D + col] = from_f32<T>(S[t][i]);
     const float gC = Fs[3 * C];
 #pragma unroll
     for (int t = 0; t < DT; ++t) S[t] *= gC;
@@ -194,23 +228,36 @@ __global__ void __launch_bounds__(256, 1) gdn_bwd16_chain_kernel(Bwd16ChainArgs 
     for (int i = 0; i < 4; ++i)
       dS[t][i] = a.dst ? a.dst[((int64_t)bh * D + rows_of(t, i)) * D + col] : 0.f;
 
+  u32x4 rq[NT], rrt[2], ro[2], rgo[2];
+  auto bwd_load = [&](int64_t n) {
+    tile_load(rk, (const T*)a.kr + n * C * D, tid);
+    tile_load(rkt, (const T*)a.kt + n * D * C, tid);
+    tile_load(rq, (const T*)a.qt + n * D * C, tid);
+    tile_load(rtm, (const T*)a.tt + n * C * C, tid);
+    tile_load(rrt, (const T*)a.rt + n * C * C, tid);
+    rf = a.f[n * kFRows * C + tid];
+    rows16_load(ro, (const T*)a.ot + (n * D + v0) * C);
+    rows16_load(rgo, (const T*)a.got + (n * D + v0) * C);
+  };
+  bwd_load((int64_t)bh * a.NC + a.NC - 1);
   for (int c = a.NC - 1; c >= 0; --c) {
     const int64_t n = (int64_t)bh * a.NC + c;
     __syncthreads();
-    copy_tile(Kr, (const T*)a.kr + n * C * D, C, D, PD);
-    copy_tile(Kt, (const T*)a.kt + n * D * C, D, C, PC);
-    copy_tile(Qt, (const T*)a.qt + n * D * C, D, C, PC);
-    copy_tile(Tm, (const T*)a.tt + n * C * C, C, C, PC);
-    copy_tile(Rt, (const T*)a.rt + n * C * C, C, C, PC);
-    if (tid < 4 * C) Fs[tid] = a.f[n * 4 * C + tid];
-    copy_rows16(XO[wave], (const T*)a.ot + (n * D + v0) * C);
-    copy_rows16(XG[wave], (const T*)a.got + (n * D + v0) * C);
+    tile_store<NT, D / 8, PD>(Kr, rk, tid);
+    tile_store<NT, 8, PC>(Kt, rkt, tid);
+    tile_store<NT, 8, PC>(Qt, rq, tid);
+    tile_store<2, 8, PC>(Tm, rtm, tid);
+    tile_store<2, 8, PC>(Rt, rrt, tid);
+    Fs[tid] = rf;
+    rows16_store(XO[wave], ro);
+    rows16_store(XG[wave], rgo);
+    if (c > 0) bwd_load(n - 1);
     // the exit-state gradient of this chunk
-    float* de = a.ds_end + n * D * D;
+    T* de = (T*)a.ds_end + n * D * D;
 #pragma unroll
     for (int t = 0; t < DT; ++t)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) de[rows_of(t, i) * D + col] = dS[t][i];
+      for (int i = 0; i < 4; ++i) de[rows_of(t, i) * D + col] = from_f32<T>(dS[t][i]);
 #pragma unroll
     for (int t = 0; t < DT; ++t) put_t(Sb[wave], PD, t, dS[t]);
     __syncthreads();
@@ -282,39 +329,562 @@ __global__ void __launch_bounds__(256, 1) gdn_bwd16_chain_kernel(Bwd16ChainArgs 
     for (int i = 0; i < 4; ++i) a.ds0[((int64_t)bh * D + rows_of(t, i)) * D + col] = dS[t][i];
 }
 
+// ------------------------------------------------------------------------------ prep
+// One workgroup per chunk-head item n (4 waves): the operand tiles of the chain and of the
+// chunk-local gradients.  k, q rows (fp32, prepared) are rounded to 16 bits once; wave P
+// forms row block P of K K^T and Q K^T on MFMA and from them N = diag(beta) A (fp32, LDS)
+// and Rq^T; then wave 0 inverts I + N by forward substitution (lane j solves column j of T,
+// 64 x 64 fully unrolled, N read as broadcast rows) while waves 1-3 write the transposed
+// tiles k^T, q^T, v^T, dO^T and (diag(Ga) dO)^T from the LDS rows.
+struct Bwd16PrepArgs {
+  const float* q;     // (B, T, H, D) fp32, scaled and normalised, contiguous
+  const float* k;     // (B, T, H, D) fp32, normalised
+  const void* v;      // (B, T, H, D) 16-bit
+  const void* dO;     // (B, T, H, D) 16-bit
+  const float* g;     // (B, T, H) log decay
+  const float* beta;  // (B, T, H)
+  void *kr, *kt, *qr, *qt, *tm, *tt, *rt, *vt, *ot, *got;
+  float* f;
+  int B, T, H, NC;
+};
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256) gdn_bwd16_prep_kernel(Bwd16PrepArgs a) {
+  constexpr int C = 64, PD = D + 8, NP = 68, KS = D / 32;
+  constexpr int NF = D / 16, NV = D / 32;  // float4 / 16-byte row chunks per thread
+  __shared__ __attribute__((aligned(16))) T Ks[C * PD];
+  __shared__ __attribute__((aligned(16))) T Qs[C * PD];
+  __shared__ __attribute__((aligned(16))) T Vs[C * PD];
+  __shared__ __attribute__((aligned(16))) T Os[C * PD];
+  __shared__ __attribute__((aligned(16))) float Ns[C * NP];
+  __shared__ float Lg[C], Bt[C], Gs[C];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, c16 = lane & 15;
+  const int64_t n = blockIdx.x;
+  const int bh = (int)(n / a.NC), c = (int)(n % a.NC);
+  const int b = bh / a.H, h = bh % a.H;
+  const int rows = min(a.T - c * C, C);
+  const int64_t tok0 = (int64_t)b * a.T + (int64_t)c * C;
+  const int64_t rs = (int64_t)a.H * D;  // token stride (elements)
+  const int64_t base = tok0 * rs + (int64_t)h * D;
+
+  // rows (zero past the sequence's end), all loads issued before the stores
+  {
+    f32x4 kx[NF], qx[NF];
+    u32x4 vx[NV], ox[NV];
+#pragma unroll
+    for (int j = 0; j < NF; ++j) {
+      const int i = tid + 256 * j, r = i / (D / 4), q4 = i % (D / 4);
+      kx[j] = qx[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (r < rows) {
+        kx[j] = *(const f32x4*)(a.k + base + r * rs + 4 * q4);
+        qx[j] = *(const f32x4*)(a.q + base + r * rs + 4 * q4);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int i = tid + 256 * j, r = i / (D / 8), ch = i % (D / 8);
+      vx[j] = ox[j] = u32x4{0u, 0u, 0u, 0u};
+      if (r < rows) {
+        vx[j] = *(const u32x4*)((const T*)a.v + base + r * rs + 8 * ch);
+        ox[j] = *(const u32x4*)((const T*)a.dO + base + r * rs + 8 * ch);
+      }
+    }
+    float gl = 0.f, bt = 0.f;
+    if (wave == 0 && lane < rows) {
+      gl = a.g[(tok0 + lane) * a.H + h];
+      bt = a.beta[(tok0 + lane) * a.H + h];
+    }
+#pragma unroll
+    for (int j = 0; j < NF; ++j) {
+      const int i = tid + 256 * j, r = i / (D / 4), q4 = i % (D / 4);
+      const u32x2 kp = {pack2<T>(kx[j][0], kx[j][1]), pack2<T>(kx[j][2], kx[j][3])};
+      const u32x2 qp = {pack2<T>(qx[j][0], qx[j][1]), pack2<T>(qx[j][2], qx[j][3])};
+      *(u32x2*)(Ks + r * PD + 4 * q4) = kp;
+      *(u32x2*)(Qs + r * PD + 4 * q4) = qp;
+      *(u32x2*)((T*)a.kr + (n * C + r) * D + 4 * q4) = kp;
+      *(u32x2*)((T*)a.qr + (n * C + r) * D + 4 * q4) = qp;
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int i = tid + 256 * j, r = i / (D / 8), ch = i % (D / 8);
+      *(u32x4*)(Vs + r * PD + 8 * ch) = vx[j];
+      *(u32x4*)(Os + r * PD + 8 * ch) = ox[j];
+    }
+    if (wave == 0) {  // inclusive prefix sum of the log decays, per-token factors
+      float lg = gl;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float y = __shfl_up(lg, off, 64);
+        if (lane >= off) lg += y;
+      }
+      const float lgC = __shfl(lg, 63, 64);
+      const float ga = expf(lg);
+      Lg[lane] = lg;
+      Bt[lane] = bt;
+      Gs[lane] = ga;
+      float* fo = a.f + n * kFRows * C;
+      fo[lane] = ga;
+      fo[C + lane] = expf(lgC - lg);
+      fo[2 * C + lane] = bt;
+      fo[3 * C + lane] = expf(lgC);
+      fo[4 * C + lane] = lg;
+    }
+  }
+  __syncthreads();
+
+  // row block P = wave of K K^T and Q K^T: N and Rq^T
+  {
+    const int P = wave;
+    u32x4 ka[KS], qa[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      ka[s] = *(const u32x4*)(Ks + (16 * P + c16) * PD + 32 * s + 8 * g);
+      qa[s] = *(const u32x4*)(Qs + (16 * P + c16) * PD + 32 * s + 8 * g);
+    }
+#pragma unroll
+    for (int S = 0; S < 4; ++S) {
+      f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const u32x4 kb = *(const u32x4*)(Ks + (16 * S + c16) * PD + 32 * s + 8 * g);
+        kk = mfma16x16x32<T>(ka[s], kb, kk);
+        qk = mfma16x16x32<T>(qa[s], kb, qk);
+      }
+      const int sc = 16 * S + c16;
+      const float lgs = Lg[sc];
+      f32x4 rq;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int p = 16 * P + 4 * g + i;
+        const float e = sc <= p ? expf(Lg[p] - lgs) : 0.f;
+        Ns[p * NP + sc] = sc < p ? Bt[p] * e * kk[i] : 0.f;
+        rq[i] = e * qk[i];
+      }
+      *(u32x2*)((T*)a.rt + (n * C + sc) * C + 16 * P + 4 * g) = u32x2{pack2<T>(rq[0], rq[1]), pack2<T>(rq[2], rq[3])};
+    }
+  }
+  __syncthreads();
+
+  if (wave == 0) {
+    // T = (I + N)^-1: x[i] = T[i][j] for the lane's column j
+    float x[C];
+#pragma unroll
+    for (int i = 0; i < C; ++i) x[i] = i == lane ? 1.f : 0.f;
+#pragma unroll
+    for (int i = 1; i < C; ++i) {
+      float acc = 0.f;
+#pragma unroll
+      for (int s4 = 0; s4 < (i + 3) / 4; ++s4) {
+        const f32x4 nv = *(const f32x4*)(Ns + i * NP + 4 * s4);  // N[i][s] = 0 for s >= i
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc = fmaf(nv[e], x[4 * s4 + e], acc);
+      }
+      x[i] -= acc;
+    }
+    T* tmo = (T*)a.tm + n * C * C;
+#pragma unroll
+    for (int i = 0; i < C; ++i) tmo[i * C + lane] = from_f32<T>(x[i]);
+    T* tto = (T*)a.tt + (n * C + lane) * C;
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      *(u32x4*)(tto + 8 * q) = u32x4{pack2<T>(x[8 * q], x[8 * q + 1]), pack2<T>(x[8 * q + 2], x[8 * q + 3]),
+                                     pack2<T>(x[8 * q + 4], x[8 * q + 5]), pack2<T>(x[8 * q + 6], x[8 * q + 7])};
+  } else {
+    // [D][64] tiles from the LDS rows: lane pairs (d, 8 tokens), d fastest
+    for (int i = tid - 64; i < 5 * D * 8; i += 192) {
+      const int tile = i / (D * 8), j = i % (D * 8);
+      const int d = j % D, ch = j / D;
+      const T* src = tile == 0 ? Ks : tile == 1 ? Qs : tile == 2 ? Vs : Os;
+      uint32_t w[4];
+      if (tile < 4) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[e] = (uint32_t)__builtin_bit_cast(uint16_t, src[(8 * ch + 2 * e) * PD + d]) |
+                 ((uint32_t)__builtin_bit_cast(uint16_t, src[(8 * ch + 2 * e + 1) * PD + d]) << 16);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[e] = pack2<T>(Gs[8 * ch + 2 * e] * to_f32(src[(8 * ch + 2 * e) * PD + d]),
+                          Gs[8 * ch + 2 * e + 1] * to_f32(src[(8 * ch + 2 * e + 1) * PD + d]));
+      }
+      void* dst = tile == 0 ? a.kt : tile == 1 ? a.qt : tile == 2 ? a.vt : tile == 3 ? a.ot : a.got;
+      *(u32x4*)((T*)dst + (n * D + d) * C + 8 * ch) = u32x4{w[0], w[1], w[2], w[3]};
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------ local
+// One workgroup per chunk-head item n (4 waves); wave w owns token rows 16 w .. 16 w + 15 of
+// every row-indexed product.  Staged in LDS: the entry state S0 (then the exit-state
+// gradient dS, same buffer), U, k rows, k^T, q^T, and the 64 x 64 weight matrices
+// GA + GA^T, GR, GR^T built by the waves.  Products on v_mfma_f32_16x16x32 (16-bit
+// operands, fp32 accumulation): K K^T, Q K^T, dY U^T, dO U^T (64 x 64), dY S0^T, dO S0^T,
+// U dS^T (64 x d), then dK = (GA + GA^T) K + GR^T Q - diag(Ga beta) dY S0^T + diag(w) U dS^T
+// and dQ = GR K + diag(Ga) dO S0^T.  The sums over d that the gradients of beta and the
+// log decays take reduce to row sums of these products with k and q:
+// rowsum(dY o K S0) = rowsum(K o dY S0^T), rowsum(dO o Q S0) = rowsum(Q o dO S0^T),
+// rowsum(K dS o U) = rowsum(K o U dS^T).
+struct Bwd16LocalArgs {
+  const void *kr, *kt, *qr, *qt;
+  const void* v;   // (B, T, H, D) 16-bit
+  const void* dO;  // (B, T, H, D) 16-bit
+  const float* f;  // [N][5][64]
+  const void *s_entry, *ds_end, *u;
+  const float* dy;
+  float *dq, *dk;  // (B, T, H, D) fp32
+  void* dv;        // (B, T, H, D) 16-bit
+  float *dg, *db;  // (B, T, H)
+  int B, T, H, NC;
+};
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256, 1) gdn_bwd16_local_kernel(Bwd16LocalArgs a) {
+  constexpr int C = 64, PD = D + 8, PC = C + 8, KS = D / 32, DT = D / 16, NT = D / 32, NSS = D * D / 2048;
+  __shared__ __attribute__((aligned(16))) T SS[D * PD];
+  __shared__ __attribute__((aligned(16))) T Us[C * PD];
+  __shared__ __attribute__((aligned(16))) T Kr[C * PD];
+  __shared__ __attribute__((aligned(16))) T Kt[D * PC];
+  __shared__ __attribute__((aligned(16))) T Qt[D * PC];
+  __shared__ __attribute__((aligned(16))) T M1[C * PC];   // GA
+  __shared__ __attribute__((aligned(16))) T M1t[C * PC];  // GA^T
+  __shared__ __attribute__((aligned(16))) T GRs[C * PC];  // GR
+  __shared__ __attribute__((aligned(16))) T GRt[C * PC];  // GR^T
+  __shared__ float Fs[kFRows * C];
+  __shared__ float colp[4][C];
+  __shared__ float dyv[C], dlgs[C], red[2][4];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, c16 = lane & 15;
+  const int64_t n = blockIdx.x;
+  const int bh = (int)(n / a.NC), c = (int)(n % a.NC);
+  const int b = bh / a.H, h = bh % a.H;
+  const int rows = min(a.T - c * C, C);
+  const int64_t tok0 = (int64_t)b * a.T + (int64_t)c * C;
+  const int64_t rs = (int64_t)a.H * D;
+  const int64_t base = tok0 * rs + (int64_t)h * D;
+  const int ra = 16 * wave + c16;  // the lane's row as an A operand
+
+  // staged tiles and the wave's A-operand rows, all loads first
+  u32x4 rss[NSS], rds[NSS], ru[NT], rk[NT], rkt[NT], rqt[NT];
+  tile_load(rss, (const T*)a.s_entry + n * D * D, tid);
+  tile_load(rds, (const T*)a.ds_end + n * D * D, tid);
+  tile_load(ru, (const T*)a.u + n * C * D, tid);
+  tile_load(rk, (const T*)a.kr + n * C * D, tid);
+  tile_load(rkt, (const T*)a.kt + n * D * C, tid);
+  tile_load(rqt, (const T*)a.qt + n * D * C, tid);
+  f32x4 dyl[KS][2];
+  u32x4 doA[KS], vA[KS], uA[KS], kA[KS], qA[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    const float* yr = a.dy + (n * C + ra) * D + 32 * s + 8 * g;
+    dyl[s][0] = *(const f32x4*)yr;
+    dyl[s][1] = *(const f32x4*)(yr + 4);
+    doA[s] = vA[s] = u32x4{0u, 0u, 0u, 0u};
+    if (ra < rows) {
+      doA[s] = *(const u32x4*)((const T*)a.dO + base + ra * rs + 32 * s + 8 * g);
+      vA[s] = *(const u32x4*)((const T*)a.v + base + ra * rs + 32 * s + 8 * g);
+    }
+    uA[s] = *(const u32x4*)((const T*)a.u + (n * C + ra) * D + 32 * s + 8 * g);
+    kA[s] = *(const u32x4*)((const T*)a.kr + (n * C + ra) * D + 32 * s + 8 * g);
+    qA[s] = *(const u32x4*)((const T*)a.qr + (n * C + ra) * D + 32 * s + 8 * g);
+  }
+  for (int i = tid; i < kFRows * C; i += 256) Fs[i] = a.f[n * kFRows * C + i];
+  tile_store<NSS, D / 8, PD>(SS, rss, tid);
+  tile_store<NT, D / 8, PD>(Us, ru, tid);
+  tile_store<NT, D / 8, PD>(Kr, rk, tid);
+  tile_store<NT, 8, PC>(Kt, rkt, tid);
+  tile_store<NT, 8, PC>(Qt, rqt, tid);
+  const float* Ga = Fs;
+  const float* Wf = Fs + C;
+  const float* Bf = Fs + 2 * C;
+  const float* Lgf = Fs + 4 * C;
+  __syncthreads();
+
+  // dV = diag(beta) dY and rowsum(dY o V) from the wave's rows; dY as A operand
+  u32x4 dyA[KS];
+  {
+    const float bt = Bf[ra];
+    float part = 0.f;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const f32x4 y0 = dyl[s][0], y1 = dyl[s][1];
+      dyA[s] = u32x4{pack2<T>(y0[0], y0[1]), pack2<T>(y0[2], y0[3]), pack2<T>(y1[0], y1[1]), pack2<T>(y1[2], y1[3])};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) part = fmaf(y0[e], elem16<T>(vA[s], e), fmaf(y1[e], elem16<T>(vA[s], 4 + e), part));
+      if (ra < rows)
+        *(u32x4*)((T*)a.dv + base + ra * rs + 32 * s + 8 * g) =
+            u32x4{pack2<T>(bt * y0[0], bt * y0[1]), pack2<T>(bt * y0[2], bt * y0[3]),
+                  pack2<T>(bt * y1[0], bt * y1[1]), pack2<T>(bt * y1[2], bt * y1[3])};
+    }
+    part += __shfl_xor(part, 16, 64);
+    part += __shfl_xor(part, 32, 64);
+    if (g == 0) dyv[ra] = part;
+  }
+
+  // 64 x 64 products of the wave's rows: A, Rq, dL, dRq, and the weights GA, GR
+  float dbl[4] = {0.f, 0.f, 0.f, 0.f}, lgl[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int S = 0; S < 4; ++S) {
+    f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = kk, yl = kk, ou = kk;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const u32x4 kb = *(const u32x4*)(Kr + (16 * S + c16) * PD + 32 * s + 8 * g);
+      const u32x4 ub = *(const u32x4*)(Us + (16 * S + c16) * PD + 32 * s + 8 * g);
+      kk = mfma16x16x32<T>(kA[s], kb, kk);
+      qk = mfma16x16x32<T>(qA[s], kb, qk);
+      yl = mfma16x16x32<T>(dyA[s], ub, yl);
+      ou = mfma16x16x32<T>(doA[s], ub, ou);
+    }
+    const int sc = 16 * S + c16;
+    const float lgs = Lgf[sc];
+    f32x4 ga, gr;
+    float colv = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = 16 * wave + 4 * g + i;
+      const float e = sc <= p ? expf(Lgf[p] - lgs) : 0.f;
+      const float A = sc < p ? e * kk[i] : 0.f;
+      const float Rq = e * qk[i];
+      const float dL = sc < p ? -yl[i] : 0.f;
+      const float dA = Bf[p] * dL;
+      const float dRq = sc <= p ? ou[i] : 0.f;
+      ga[i] = dA * e;
+      gr[i] = dRq * e;
+      dbl[i] = fmaf(dL, A, dbl[i]);
+      const float x = fmaf(dA, A, dRq * Rq);
+      lgl[i] += x;
+      colv += x;
+      M1[p * PC + sc] = from_f32<T>(ga[i]);
+      GRs[p * PC + sc] = from_f32<T>(gr[i]);
+    }
+    const int p0 = 16 * wave + 4 * g;
+    *(u32x2*)(M1t + sc * PC + p0) = u32x2{pack2<T>(ga[0], ga[1]), pack2<T>(ga[2], ga[3])};
+    *(u32x2*)(GRt + sc * PC + p0) = u32x2{pack2<T>(gr[0], gr[1]), pack2<T>(gr[2], gr[3])};
+    colv += __shfl_xor(colv, 16, 64);
+    colv += __shfl_xor(colv, 32, 64);
+    if (g == 0) colp[wave][sc] = colv;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    dbl[i] = row16_sum(dbl[i]);
+    lgl[i] = row16_sum(lgl[i]);
+  }
+
+  // dY S0^T and dO S0^T (B operand: S0 rows = output columns)
+  f32x4 P1[DT], P2[DT], P3[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    P1[t] = P2[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const u32x4 sb = *(const u32x4*)(SS + (16 * t + c16) * PD + 32 * s + 8 * g);
+      P1[t] = mfma16x16x32<T>(dyA[s], sb, P1[t]);
+      P2[t] = mfma16x16x32<T>(doA[s], sb, P2[t]);
+    }
+  }
+  // <dS, S0> over the thread's chunks, then dS replaces S0
+  {
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < NSS; ++j) {
+      const int i = tid + 256 * j;
+      const u32x4 sx = *(const u32x4*)(SS + (i / (D / 8)) * PD + 8 * (i % (D / 8)));
+#pragma unroll
+      for (int e = 0; e < 8; ++e) part = fmaf(elem16<T>(sx, e), elem16<T>(rds[j], e), part);
+    }
+    part = wave_sum(part);
+    if (lane == 0) red[0][wave] = part;
+  }
+  __syncthreads();
+  tile_store<NSS, D / 8, PD>(SS, rds, tid);
+  __syncthreads();
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    P3[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      P3[t] = mfma16x16x32<T>(uA[s], *(const u32x4*)(SS + (16 * t + c16) * PD + 32 * s + 8 * g), P3[t]);
+  }
+
+  // dK, dQ: A operands (GA + GA^T), GR^T, GR rows; B operands k^T, q^T rows (= columns d)
+  u32x4 g1A[2], grtA[2], grA[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const u32x4 m = *(const u32x4*)(M1 + ra * PC + 32 * j + 8 * g);
+    const u32x4 mt = *(const u32x4*)(M1t + ra * PC + 32 * j + 8 * g);
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      w[e] = pack2<T>(elem16<T>(m, 2 * e) + elem16<T>(mt, 2 * e), elem16<T>(m, 2 * e + 1) + elem16<T>(mt, 2 * e + 1));
+    g1A[j] = u32x4{w[0], w[1], w[2], w[3]};
+    grtA[j] = *(const u32x4*)(GRt + ra * PC + 32 * j + 8 * g);
+    grA[j] = *(const u32x4*)(GRs + ra * PC + 32 * j + 8 * g);
+  }
+  float rk1[4] = {0.f, 0.f, 0.f, 0.f}, rq2[4] = {0.f, 0.f, 0.f, 0.f}, rk3[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    f32x4 dk = {0.f, 0.f, 0.f, 0.f}, dq = dk;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const u32x4 kb = *(const u32x4*)(Kt + (16 * t + c16) * PC + 32 * j + 8 * g);
+      const u32x4 qb = *(const u32x4*)(Qt + (16 * t + c16) * PC + 32 * j + 8 * g);
+      dk = mfma16x16x32<T>(g1A[j], kb, dk);
+      dk = mfma16x16x32<T>(grtA[j], qb, dk);
+      dq = mfma16x16x32<T>(grA[j], kb, dq);
+    }
+    const int d = 16 * t + c16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = 16 * wave + 4 * g + i;
+      const float kv = to_f32(Kt[d * PC + p]), qv = to_f32(Qt[d * PC + p]);
+      rk1[i] = fmaf(kv, P1[t][i], rk1[i]);
+      rq2[i] = fmaf(qv, P2[t][i], rq2[i]);
+      rk3[i] = fmaf(kv, P3[t][i], rk3[i]);
+      if (p < rows) {
+        const int64_t o = base + p * rs + d;
+        a.dk[o] = dk[i] - Ga[p] * Bf[p] * P1[t][i] + Wf[p] * P3[t][i];
+        a.dq[o] = dq[i] + Ga[p] * P2[t][i];
+      }
+    }
+  }
+  // gradients of beta and of the log decays, per row
+  float wsum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int p = 16 * wave + 4 * g + i;
+    const float k1 = row16_sum(rk1[i]), q2 = row16_sum(rq2[i]), k3 = row16_sum(rk3[i]);
+    if (c16 == 0) {
+      if (p < rows) a.db[(tok0 + p) * a.H + h] = dyv[p] - Ga[p] * k1 + dbl[i];
+      dlgs[p] = lgl[i] + Ga[p] * (q2 - Bf[p] * k1) - Wf[p] * k3;
+      wsum = fmaf(Wf[p], k3, wsum);
+    }
+  }
+  wsum = wave_sum(wsum);
+  if (lane == 0) red[1][wave] = wsum;
+  __syncthreads();
+  if (wave == 0) {
+    float x = dlgs[lane] - (colp[0][lane] + colp[1][lane] + colp[2][lane] + colp[3][lane]);
+    if (lane == C - 1)
+      x += red[1][0] + red[1][1] + red[1][2] + red[1][3] +
+           Fs[3 * C] * (red[0][0] + red[0][1] + red[0][2] + red[0][3]);
+    // reverse cumulative sum: dg[p] = sum over s >= p
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float y = __shfl_down(x, off, 64);
+      if (lane + off < 64) x += y;
+    }
+    if (lane < rows) a.dg[(tok0 + lane) * a.H + h] = x;
+  }
+}
+
 }  // namespace atma
+
+// ------------------------------------------------------------------------------ C ABI
+namespace {
+
+bool bwd16_dims_ok(int64_t d, int dtype, const char* who) {
+  using namespace atma;
+  if (d != 64 && d != 128) {
+    set_error(ATMA_ERR_UNSUPPORTED, "%s: d = %lld (supported: 64, 128)", who, (long long)d);
+    return false;
+  }
+  if (dtype != ATMA_BF16 && dtype != ATMA_F16) {
+    set_error(ATMA_ERR_UNSUPPORTED, "%s: 16-bit operands only", who);
+    return false;
+  }
+  return true;
+}
+
+bool aligned16(std::initializer_list<const void*> ps) {
+  for (const void* p : ps)
+    if ((uintptr_t)p % 16) return false;
+  return true;
+}
+
+}  // namespace
+
+#define ATMA_BWD16_DISPATCH(KERNEL, grid, stream, args)                                  \
+  do {                                                                                   \
+    if (dtype == ATMA_BF16) {                                                            \
+      if (d == 128) atma::KERNEL<atma::bf16, 128><<<grid, dim3(256), 0, stream>>>(args); \
+      else atma::KERNEL<atma::bf16, 64><<<grid, dim3(256), 0, stream>>>(args);           \
+    } else {                                                                             \
+      if (d == 128) atma::KERNEL<atma::f16, 128><<<grid, dim3(256), 0, stream>>>(args);  \
+      else atma::KERNEL<atma::f16, 64><<<grid, dim3(256), 0, stream>>>(args);            \
+    }                                                                                    \
+  } while (0)
+
+extern "C" int atma_gated_delta_bwd16_prep(const float* q, const float* k, const void* v, const void* d_out,
+                                           const float* g, const float* beta, void* kr, void* kt, void* qr,
+                                           void* qt, void* tm, void* tt, void* rt, void* vt, void* ot, void* got,
+                                           float* f, int64_t B, int64_t T, int64_t H, int64_t d, int dtype,
+                                           void* stream) {
+  using namespace atma;
+  if (!bwd16_dims_ok(d, dtype, "gated_delta_bwd16_prep")) return ATMA_ERR_UNSUPPORTED;
+  if (B < 0 || T < 0 || H <= 0) return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_prep: bad sizes");
+  const int64_t NC = (T + 63) / 64;
+  if (B == 0 || NC == 0) return ATMA_OK;
+  if (!q || !k || !v || !d_out || !g || !beta || !kr || !kt || !qr || !qt || !tm || !tt || !rt || !vt || !ot ||
+      !got || !f)
+    return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_prep: null pointer");
+  if (!aligned16({q, k, v, d_out, kr, kt, qr, qt, tm, tt, rt, vt, ot, got}))
+    return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_prep: operands must be 16-byte aligned");
+  if (B * H * NC > 0x7fffffff || B * T > 0x7fffffff)
+    return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_prep: sizes too large");
+  Bwd16PrepArgs a{q, k, v, d_out, g, beta, kr, kt, qr, qt, tm, tt, rt, vt, ot, got, f,
+                  (int)B, (int)T, (int)H, (int)NC};
+  const dim3 grid((unsigned)(B * H * NC));
+  ATMA_BWD16_DISPATCH(gdn_bwd16_prep_kernel, grid, (hipStream_t)stream, a);
+  return check_launch("gated_delta_bwd16_prep");
+}
 
 extern "C" int atma_gated_delta_bwd16_chain(const void* kr, const void* kt, const void* qt, const void* tm,
                                             const void* tt, const void* rt, const void* vt, const void* ot,
-                                            const void* got, const float* f, const float* s0,
-                                            const float* dst, float* s_entry, float* ds_end, float* dy,
-                                            float* ds0, int64_t BH, int64_t NC, int64_t d, int dtype,
-                                            void* stream) {
+                                            const void* got, const float* f, const float* s0, const float* dst,
+                                            void* s_entry, void* ds_end, void* u, float* dy, float* ds0,
+                                            int64_t BH, int64_t NC, int64_t d, int dtype, void* stream) {
   using namespace atma;
+  if (!bwd16_dims_ok(d, dtype, "gated_delta_bwd16_chain")) return ATMA_ERR_UNSUPPORTED;
   if (BH < 0 || NC < 0) return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_chain: bad sizes");
-  if (d != 64 && d != 128)
-    return set_error(ATMA_ERR_UNSUPPORTED, "gated_delta_bwd16_chain: d = %lld (supported: 64, 128)",
-                     (long long)d);
-  if (dtype != ATMA_BF16 && dtype != ATMA_F16)
-    return set_error(ATMA_ERR_UNSUPPORTED, "gated_delta_bwd16_chain: 16-bit operands only");
   if (BH == 0 || NC == 0) return ATMA_OK;
-  if (!kr || !kt || !qt || !tm || !tt || !rt || !vt || !ot || !got || !f || !s_entry || !ds_end || !dy ||
+  if (!kr || !kt || !qt || !tm || !tt || !rt || !vt || !ot || !got || !f || !s_entry || !ds_end || !u || !dy ||
       !ds0)
     return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_chain: null pointer");
-  const void* ptrs[] = {kr, kt, qt, tm, tt, rt, vt, ot, got};
-  for (const void* p : ptrs)
-    if ((uintptr_t)p % 16) return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_chain: tiles must be 16-byte aligned");
-  if (BH * (d / 64) > 0x7fffffff || BH * NC > (1ll << 31))
+  if (!aligned16({kr, kt, qt, tm, tt, rt, vt, ot, got}))
+    return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_chain: tiles must be 16-byte aligned");
+  if (BH * (d / 64) > 0x7fffffff || BH * NC > 0x7fffffff)
     return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_chain: sizes too large");
-  Bwd16ChainArgs a{kr, kt, qt, tm, tt, rt, vt, ot, got, f, s0, dst, s_entry, ds_end, dy, ds0, (int)BH, (int)NC};
-  hipStream_t s = (hipStream_t)stream;
+  Bwd16ChainArgs a{kr, kt, qt, tm, tt, rt, vt, ot, got, f, s0, dst, s_entry, ds_end, u, dy, ds0,
+                   (int)BH, (int)NC};
   const dim3 grid((unsigned)(BH * (d / 64)));
-  if (dtype == ATMA_BF16) {
-    if (d == 128) gdn_bwd16_chain_kernel<bf16, 128><<<grid, dim3(256), 0, s>>>(a);
-    else gdn_bwd16_chain_kernel<bf16, 64><<<grid, dim3(256), 0, s>>>(a);
-  } else {
-    if (d == 128) gdn_bwd16_chain_kernel<f16, 128><<<grid, dim3(256), 0, s>>>(a);
-    else gdn_bwd16_chain_kernel<f16, 64><<<grid, dim3(256), 0, s>>>(a);
-  }
+  ATMA_BWD16_DISPATCH(gdn_bwd16_chain_kernel, grid, (hipStream_t)stream, a);
   return check_launch("gated_delta_bwd16_chain");
+}
+
+extern "C" int atma_gated_delta_bwd16_local(const void* kr, const void* kt, const void* qr, const void* qt,
+                                            const void* v, const void* d_out, const float* f, const void* s_entry,
+                                            const void* ds_end, const void* u, const float* dy, float* dq,
+                                            float* dk, void* dv, float* dg, float* dbeta, int64_t B, int64_t T,
+                                            int64_t H, int64_t d, int dtype, void* stream) {
+  using namespace atma;
+  if (!bwd16_dims_ok(d, dtype, "gated_delta_bwd16_local")) return ATMA_ERR_UNSUPPORTED;
+  if (B < 0 || T < 0 || H <= 0) return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_local: bad sizes");
+  const int64_t NC = (T + 63) / 64;
+  if (B == 0 || NC == 0) return ATMA_OK;
+  if (!kr || !kt || !qr || !qt || !v || !d_out || !f || !s_entry || !ds_end || !u || !dy || !dq || !dk || !dv ||
+      !dg || !dbeta)
+    return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_local: null pointer");
+  if (!aligned16({kr, kt, qr, qt, v, d_out, s_entry, ds_end, u, dy, dv}))
+    return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_local: operands must be 16-byte aligned");
+  if (B * H * NC > 0x7fffffff || B * T > 0x7fffffff)
+    return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_local: sizes too large");
+  Bwd16LocalArgs a{kr, kt, qr, qt, v, d_out, f, s_entry, ds_end, u, dy, dq, dk, dv, dg, dbeta,
+                   (int)B, (int)T, (int)H, (int)NC};
+  const dim3 grid((unsigned)(B * H * NC));
+  ATMA_BWD16_DISPATCH(gdn_bwd16_local_kernel, grid, (hipStream_t)stream, a);
+  return check_launch("gated_delta_bwd16_local");
 }

@@ -150,125 +150,13 @@ class _GatedDeltaFn(torch.autograd.Function):
         return dq, dk, dv, dg, db, (ds0 if S0 is not None else None)
 
 
-_CH = 64  # chunk length of the chunked (WY) form
-
-
-def _to_chunks(x, NC):
-    """(B, T, H, ...) -> (B*H, NC, 64, ...), zero-padded to NC * 64 tokens."""
-    B, T, H = x.shape[:3]
-    pad = NC * _CH - T
-    if pad:
-        x = torch.nn.functional.pad(x, (0, 0) * (x.dim() - 2) + (0, pad))
-    return x.movedim(2, 1).reshape(B * H, NC, _CH, *x.shape[3:])
-
-
-def _from_chunks(x, B, T):
-    """(B*H, NC, 64, ...) -> (B, T, H, ...)."""
-    BH, NC = x.shape[:2]
-    return x.reshape(B, BH // B, NC * _CH, *x.shape[3:]).movedim(1, 2)[:, :T].contiguous()
-
-
-def _gated_delta_bwd16(qs, kn, v, g, beta, S0, dO, dST, tile_dtype):
-    """Chunked (WY) backward of the recurrence for 16-bit training, the algorithm of the
-    FLA autograd the reference trains through (``model/blocks.py:44-84``).  In a chunk with
-    inclusive log decays lg, Ga = exp(lg), w = exp(lg_C - lg), E[p,s] = exp(lg_p - lg_s)
-    (s <= p), A = E o K K^T (strictly lower), T = (I + diag(beta) A)^-1, Rq = E o Q K^T:
-    U = T diag(beta)(V - diag(Ga) K S0), O = diag(Ga) Q S0 + Rq U,
-    S_end = Ga_C S0 + K^T diag(w) U.  The state gradient dS runs backwards over the chunks:
-    dU = Rq^T dO + diag(w) K dS, dY = T^T dU, dS <- Ga_C dS + Q^T diag(Ga) dO
-    - K^T diag(Ga beta) dY.  That chain (and the forward one that recovers each chunk's
-    S0) is ``gated_delta_bwd16_chain`` (16-bit MFMA, fp32 state); the per-chunk matrices
-    it takes and every gradient local to a chunk are batched fp32 products here:
-    dV = diag(beta) dY; dL = -(dY U^T) strictly lower, dA = diag(beta) dL;
-    dRq = dO U^T lower; dbeta = rowsum(dY o (V - diag(Ga) K S0)) + rowsum(dL o A);
-    dK = (dA o E + (dA o E)^T) K + (dRq o E)^T Q - diag(Ga beta) dY S0^T + diag(w) U dS^T;
-    dQ = (dRq o E) K + diag(Ga) dO S0^T; dlg = rowsum - colsum of dA o A and dRq o Rq
-    + Ga o (rowsum(dO o Q S0) - beta o rowsum(dY o K S0)) - w o rowsum(K dS o U), plus
-    sum(w o rowsum(K dS o U)) + Ga_C <dS, S0> at the chunk's last token; dg = the
-    reverse cumulative sum of dlg within the chunk.
-
-    qs, kn, v, dO: (B, T, H, d) (q scaled and normalised, k normalised); g, beta (B, T, H);
-    S0, dST (B, H, d, d) or None.  Returns dq, dk, dv, dg, dbeta (fp32, (B, T, H, .)) and
-    dS0 (B, H, d, d)."""
-    prep = _bwd16_prep(qs, kn, v, g, beta, dO, tile_dtype)
-    B, H, D = qs.shape[0], qs.shape[2], qs.shape[3]
-    s_entry, ds_end, dY, ds0 = torch.ops.atma_hip.gated_delta_bwd16_chain(
-        *prep["tiles"], None if S0 is None else S0.float().reshape(B * H, D, D),
-        None if dST is None else dST.float().reshape(B * H, D, D))
-    return _bwd16_local(prep, s_entry, ds_end, dY) + (ds0.reshape(B, H, D, D),)
-
-
-def _bwd16_prep(qs, kn, v, g, beta, dO, tile_dtype):
-    """The per-chunk matrices of the chunked backward, and the operand tiles of
-    ``gated_delta_bwd16_chain`` in ``tile_dtype`` (argument order of the op, up to f)."""
-    B, T, H, D = qs.shape
-    NC = (T + _CH - 1) // _CH
-    BH = B * H
-    dev = qs.device
-    Q, K, V, dOc = (_to_chunks(t.float(), NC) for t in (qs, kn, v, dO))      # (BH, NC, C, D)
-    gc, bc = _to_chunks(g.float(), NC), _to_chunks(beta.float(), NC)        # (BH, NC, C)
-    lg = gc.cumsum(-1)
-    Ga = lg.exp()
-    w = (lg[..., -1:] - lg).exp()
-    GaC = Ga[..., -1]
-    idx = torch.arange(_CH, device=dev)
-    incl = idx[:, None] >= idx[None, :]
-    strict = idx[:, None] > idx[None, :]
-    E = (lg[..., :, None] - lg[..., None, :]).masked_fill(~incl, float("-inf")).exp()
-    Kt = K.transpose(-1, -2)
-    A = (E * (K @ Kt)).masked_fill(~strict, 0.0)
-    eye = torch.eye(_CH, device=dev, dtype=torch.float32)
-    Tm = torch.linalg.solve_triangular(eye + bc[..., :, None] * A, eye.expand(BH, NC, _CH, _CH),
-                                       upper=False, unitriangular=True)
-    Rq = E * (Q @ Kt)
-
-    def tile(x):
-        return x.to(tile_dtype).contiguous()
-    f = torch.stack((Ga, w, bc, GaC[..., None].expand_as(Ga)), dim=-2).contiguous()
-    tiles = (tile(K), tile(Kt), tile(Q.transpose(-1, -2)), tile(Tm), tile(Tm.transpose(-1, -2)),
-             tile(Rq.transpose(-1, -2)), tile(V.transpose(-1, -2)), tile(dOc.transpose(-1, -2)),
-             tile((Ga[..., None] * dOc).transpose(-1, -2)), f)
-    return dict(B=B, T=T, Q=Q, K=K, V=V, dOc=dOc, bc=bc, Ga=Ga, w=w, GaC=GaC, incl=incl, strict=strict,
-                E=E, A=A, Tm=Tm, Rq=Rq, tiles=tiles)
-
-
-def _bwd16_local(p, s_entry, ds_end, dY):
-    """Every gradient local to a chunk, from the chains' outputs (each chunk's entry
-    state, the gradient of its exit state, dY).  Returns dq, dk, dv, dg, dbeta."""
-    Q, K, V, dOc, bc, Ga, w, GaC = (p[n] for n in ("Q", "K", "V", "dOc", "bc", "Ga", "w", "GaC"))
-    E, A, Tm, Rq, incl, strict = (p[n] for n in ("E", "A", "Tm", "Rq", "incl", "strict"))
-    B, T = p["B"], p["T"]
-    KS, QS = K @ s_entry, Q @ s_entry
-    Vres = V - Ga[..., None] * KS
-    U = Tm @ (bc[..., None] * Vres)
-    Ut = U.transpose(-1, -2)
-    KdS = K @ ds_end
-    dV = bc[..., None] * dY
-    dL = -(dY @ Ut).masked_fill(~strict, 0.0)
-    dA = bc[..., None] * dL
-    db = (dY * Vres).sum(-1) + (dL * A).sum(-1)
-    GA = dA * E
-    dRq = (dOc @ Ut).masked_fill(~incl, 0.0)
-    GR = dRq * E
-    S0t = s_entry.transpose(-1, -2)
-    dK = ((GA + GA.transpose(-1, -2)) @ K + GR.transpose(-1, -2) @ Q
-          - (Ga * bc)[..., None] * (dY @ S0t) + w[..., None] * (U @ ds_end.transpose(-1, -2)))
-    dQ = GR @ K + Ga[..., None] * (dOc @ S0t)
-    dAA, dRR = dA * A, dRq * Rq
-    dw = (KdS * U).sum(-1)
-    dlg = (dAA.sum(-1) - dAA.sum(-2) + dRR.sum(-1) - dRR.sum(-2)
-           + Ga * ((dOc * QS).sum(-1) - bc * (dY * KS).sum(-1)) - w * dw)
-    dlg[..., -1] += (w * dw).sum(-1) + GaC * (ds_end * s_entry).sum((-2, -1))
-    dg = dlg.flip(-1).cumsum(-1).flip(-1)
-    return (_from_chunks(dQ, B, T), _from_chunks(dK, B, T), _from_chunks(dV, B, T),
-            _from_chunks(dg, B, T), _from_chunks(db, B, T))
-
-
 class _GatedDelta16Fn(torch.autograd.Function):
     """The recurrence on prepared operands for 16-bit training (q scaled and normalised,
     k normalised, in fp32; v, log decay g, beta, fp32 [K, V] initial state): forward by
     the 16-bit chunked prefill kernel on the operands rounded to the input dtype,
-    backward by the chunked (WY) form (``_gated_delta_bwd16``)."""
+    backward by the chunked (WY) form (``gated_delta_bwd16``: a prep launch forming each
+    chunk's matrices, the chain launch carrying the state and its gradient across the
+    chunks, and a launch forming every gradient local to a chunk)."""
 
     @staticmethod
     def forward(ctx, qs, kn, v, g, beta, S0):
@@ -280,9 +168,9 @@ class _GatedDelta16Fn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dO, dS):
         qs, kn, v, g, beta, S0 = ctx.saved_tensors
-        dO = torch.zeros(v.shape, device=v.device, dtype=torch.float32) if dO is None else dO
-        dq, dk, dv, dg, db, ds0 = _gated_delta_bwd16(qs, kn, v, g, beta, S0, dO, dS, v.dtype)
-        return dq, dk, dv.to(v.dtype), dg, db, (ds0 if S0 is not None else None)
+        dO = torch.zeros_like(v) if dO is None else dO.to(v.dtype)
+        dq, dk, dv, dg, db, ds0 = torch.ops.atma_hip.gated_delta_bwd16(qs, kn, v, g, beta, S0, dO, dS)
+        return dq, dk, dv, dg, db, (ds0 if S0 is not None else None)
 
 
 def _chunk_gated_delta_train(q, k, v, g, beta, scale, initial_state, output_final_state, use_qk_l2norm):

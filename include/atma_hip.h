@@ -307,24 +307,48 @@ int atma_gated_delta_bwd(const float* q, const float* k, const float* v, const f
                          void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Sequential part of the chunked (WY) backward of the same recurrence, for 16-bit
- * training (the FLA chunk_gated_delta_rule autograd the reference trains through,
- * model/blocks.py:44-84; its backward carries the state gradient across 64-token chunks
- * the same way).  N = BH * NC chunk-heads, chunk-head major (n = bh * NC + c), d in
- * {64, 128}; dtype ATMA_BF16 or ATMA_F16 for the tiles, all 16-byte aligned and
- * contiguous: kr (N, 64, d) chunk rows of k (normalised); kt, qt (N, d, 64) k^T and q^T
- * (q scaled and normalised); tm, tt, rt (N, 64, 64) T = (I + diag(beta) A)^-1, T^T and
- * Rq^T; vt, ot, got (N, d, 64) v^T, dO^T and (diag(Ga) dO)^T; f (N, 4, 64) fp32 rows Ga,
- * w = exp(lg_C - lg), beta, and Ga_C in f[n][3][0].  s0, dst (BH, d, d) [K, V] fp32 or
- * NULL (zero).  Writes s_entry (N, d, d) each chunk's entry state, ds_end (N, d, d) the
- * gradient of each chunk's exit state, dy (N, 64, d) dY = T^T dU, and ds0 (BH, d, d).
- * Zero-padded tokens (k = v = 0, beta = 0, log decay 0) leave every output exact.
+ * Chunked (WY) backward of the same recurrence for 16-bit training, in three launches: the
+ * algorithm of the FLA chunk_gated_delta_rule autograd the reference trains through
+ * (model/blocks.py:44-84), which carries the state gradient across 64-token chunks and
+ * forms every other gradient within a chunk.  N = B * H * NC chunk-head items,
+ * n = (b * H + h) * NC + c, NC = ceil(T / 64); d in {64, 128}; dtype ATMA_BF16 / ATMA_F16
+ * names the 16-bit type of v, d_out and every tile; all operands contiguous and 16-byte
+ * aligned.  Tokens past T act as zero-padding (k = q = v = dO = 0, beta = 0, log decay 0),
+ * which leaves every gradient exact.
+ *
+ * prep: q (scaled, normalised), k (normalised): (B, T, H, d) fp32; v, d_out: (B, T, H, d);
+ * g (log decay), beta: (B, T, H) fp32.  Writes the 16-bit tiles kr, qr (N, 64, d) rows;
+ * kt, qt, vt, ot, got (N, d, 64) = k^T, q^T, v^T, dO^T, (diag(Ga) dO)^T; tm, tt (N, 64, 64)
+ * T = (I + diag(beta) A)^-1 and T^T, A[p,s] = exp(lg_p - lg_s) k_p.k_s (s < p); rt
+ * (N, 64, 64) Rq^T, Rq[p,s] = exp(lg_p - lg_s) q_p.k_s (s <= p); and f (N, 5, 64) fp32 per
+ * token: Ga = exp(lg), w = exp(lg_C - lg), beta, Ga_C, lg (lg the in-chunk inclusive
+ * cumulative log decay).
+ *
+ * chain: the prep's tiles (BH = B * H); s0, dst (BH, d, d) [K, V] fp32 initial state and
+ * final-state cotangent, or NULL (zero).  Runs the state forward over the chunks, then the
+ * state gradient backwards (dU = Rq^T dO + diag(w) K dS, dY = T^T dU,
+ * dS <- Ga_C dS + Q^T diag(Ga) dO - K^T diag(Ga beta) dY), writing s_entry and ds_end
+ * (N, d, d) 16-bit (each chunk's entry state, the gradient of its exit state), u (N, 64, d)
+ * 16-bit (U = T diag(beta)(V - diag(Ga) K S)), dy (N, 64, d) fp32 and ds0 (BH, d, d) fp32.
+ *
+ * local: the prep's kr, kt, qr, qt, f, the chain's s_entry, ds_end, u, dy, and v, d_out as
+ * given to the prep.  Writes dq, dk (B, T, H, d) fp32, dv (B, T, H, d) 16-bit, dg, dbeta
+ * (B, T, H) fp32 (dg the gradient of the per-token log decay).
  */
+int atma_gated_delta_bwd16_prep(const float* q, const float* k, const void* v, const void* d_out,
+                                const float* g, const float* beta, void* kr, void* kt, void* qr, void* qt,
+                                void* tm, void* tt, void* rt, void* vt, void* ot, void* got, float* f,
+                                int64_t B, int64_t T, int64_t H, int64_t d, int dtype, void* stream);
 int atma_gated_delta_bwd16_chain(const void* kr, const void* kt, const void* qt, const void* tm,
                                  const void* tt, const void* rt, const void* vt, const void* ot,
                                  const void* got, const float* f, const float* s0, const float* dst,
-                                 float* s_entry, float* ds_end, float* dy, float* ds0, int64_t BH,
+                                 void* s_entry, void* ds_end, void* u, float* dy, float* ds0, int64_t BH,
                                  int64_t NC, int64_t d, int dtype, void* stream);
+int atma_gated_delta_bwd16_local(const void* kr, const void* kt, const void* qr, const void* qt,
+                                 const void* v, const void* d_out, const float* f, const void* s_entry,
+                                 const void* ds_end, const void* u, const float* dy, float* dq, float* dk,
+                                 void* dv, float* dg, float* dbeta, int64_t B, int64_t T, int64_t H,
+                                 int64_t d, int dtype, void* stream);
 
 /*
  * Fused MLP activation out = gate * relu(x)^2.  Replaces squared_relu_gate

@@ -1,9 +1,12 @@
 """GPU parity of the chunked (WY) 16-bit training backward of the gated-delta recurrence
 (the algorithm of the FLA autograd the reference trains through, model/blocks.py:44-84).
 
-  * the state-chain kernel (``gated_delta_bwd16_chain``) against its fp32 torch
-    restatement on the same 16-bit tiles (2e-2 of max|x| per output: the kernel rounds
-    the state and the per-chunk intermediates to 16 bits as MFMA operands);
+  * each of its three launches against its fp32 torch restatement (tests/helpers.py; the
+    restatements composed are pinned against the oracle's chunked backward on the CPU):
+    the prep's tiles (16-bit copies exact; T, T^T, Rq^T within 2e-2 of max|x|, the kernel
+    forming K K^T and Q K^T from 16-bit rows as the restatement does here), the chain's
+    states and U / dY on the prep's own tiles, and the local gradients on the chain's own
+    outputs, each within 2e-2 of max|x| (the kernels round products' operands to 16 bits);
   * the whole 16-bit route of ``chunk_gated_delta_rule``'s autograd against fp64 autograd
     of the sequential definition (scripts/titans_proto.py:53-76, pinned by gradcheck in
     the oracle tests): every gradient within 2e-2 of max|grad| per tensor, over ragged
@@ -13,7 +16,8 @@
 import pytest
 import torch
 
-from helpers import bwd16_chain_reference, rel_err
+from helpers import (CHAIN_TILES, bwd16_chain_reference, bwd16_local_reference, bwd16_prep_reference,
+                     rel_err)
 from oracle import gated_delta as OG
 
 pytestmark = pytest.mark.gpu
@@ -31,25 +35,58 @@ def _prepared(B, T, H, d, dtype, seed, dev):
     return [x.to(dev) for x in (q, k, v, gl, beta, dO, S0, dST)]
 
 
-@pytest.mark.parametrize("B,T,H,d,dtype,states", [
+STAGE_CASES = [
     (1, 64, 1, 128, torch.bfloat16, True),
     (2, 300, 3, 64, torch.bfloat16, True),
     (1, 1000, 2, 128, torch.float16, False),
+    (1, 77, 2, 64, torch.float16, True),
     (8, 2048, 8, 128, torch.bfloat16, False),   # configs[1] training shape
-])
-def test_chain_kernel_vs_fp32_restatement(dev, B, T, H, d, dtype, states):
-    from atma_amd.kernel.gated_delta import _bwd16_prep
+]
+
+
+def _stages(B, T, H, d, dtype, states, dev):
+    from atma_amd._ops import gated_delta_bwd16_stages
     q, k, v, gl, beta, dO, S0, dST = _prepared(B, T, H, d, dtype, T + d, dev)
-    prep = _bwd16_prep(q, k, v, gl, beta, dO, dtype)
-    s0 = S0.reshape(B * H, d, d) if states else None
-    dst = dST.reshape(B * H, d, d) if states else None
-    print(f"chain B={B} T={T} H={H} d={d} {dtype}", flush=True)
-    got = torch.ops.atma_hip.gated_delta_bwd16_chain(*prep["tiles"], s0, dst)
+    if not states:
+        S0 = dST = None
+    print(f"bwd16 stages B={B} T={T} H={H} d={d} {dtype}", flush=True)
+    st = gated_delta_bwd16_stages(q, k, v, gl, beta, S0, dO, dST)
     torch.cuda.synchronize()
-    ref = bwd16_chain_reference(*prep["tiles"], s0, dst)
-    for name, a, r in zip(["s_entry", "ds_end", "dy", "ds0"], got, ref):
-        assert torch.isfinite(a).all(), name
-        assert rel_err(a, r) <= 2e-2, (name, rel_err(a, r))
+    return (q, k, v, gl, beta, dO, S0, dST), st
+
+
+@pytest.mark.parametrize("B,T,H,d,dtype,states", STAGE_CASES)
+def test_prep_kernel_vs_restatement(dev, B, T, H, d, dtype, states):
+    (q, k, v, gl, beta, dO, _, _), st = _stages(B, T, H, d, dtype, states, dev)
+    # k and q enter the kernel's products rounded to 16 bits: so they do here
+    ref = bwd16_prep_reference(q.to(dtype), k.to(dtype), v, gl, beta, dO, dtype)
+    for name in ("kr", "kt", "qr", "qt", "vt", "ot", "got"):
+        assert torch.equal(st[name], ref[name]) or rel_err(st[name], ref[name]) <= 1e-2, name
+    for name in ("tm", "tt", "rt"):
+        assert rel_err(st[name], ref[name]) <= 2e-2, (name, rel_err(st[name], ref[name]))
+    assert rel_err(st["f"], ref["f"]) <= 1e-5
+
+
+@pytest.mark.parametrize("B,T,H,d,dtype,states", STAGE_CASES)
+def test_chain_kernel_vs_restatement(dev, B, T, H, d, dtype, states):
+    (_, _, _, _, _, _, S0, dST), st = _stages(B, T, H, d, dtype, states, dev)
+    BH = B * H
+    ref = bwd16_chain_reference(*(st[n] for n in CHAIN_TILES), None if S0 is None else S0.reshape(BH, d, d),
+                                None if dST is None else dST.reshape(BH, d, d))
+    for name, r in zip(["s_entry", "ds_end", "u", "dy", "ds0"], ref):
+        assert torch.isfinite(st[name].float()).all(), name
+        assert rel_err(st[name], r) <= 2e-2, (name, rel_err(st[name], r))
+
+
+@pytest.mark.parametrize("B,T,H,d,dtype,states", STAGE_CASES)
+def test_local_kernel_vs_restatement(dev, B, T, H, d, dtype, states):
+    (q, k, v, gl, beta, dO, _, _), st = _stages(B, T, H, d, dtype, states, dev)
+    p = bwd16_prep_reference(q.to(dtype), k.to(dtype), v, gl, beta, dO, dtype)
+    ref = bwd16_local_reference(p, st["s_entry"], st["ds_end"], st["u"], st["dy"])
+    for name, r in zip(["dq", "dk", "dv", "dg", "db"], ref):
+        assert st[name].shape == r.shape, name
+        assert torch.isfinite(st[name].float()).all(), name
+        assert rel_err(st[name], r) <= 2e-2, (name, rel_err(st[name], r))
 
 
 def _oracle(q, k, v, g, beta, S0, scale):

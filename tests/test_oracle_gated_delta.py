@@ -189,30 +189,32 @@ def test_chunked_backward_equals_sequential_autograd(T, chunk, dk, dv):
 
 @pytest.mark.parametrize("B,T,H,d,s0,dfinal", [(1, 150, 2, 64, True, True), (2, 64, 1, 128, False, True),
                                                (1, 33, 3, 64, True, False)])
-def test_bwd16_host_logic_vs_oracle(B, T, H, d, s0, dfinal):
-    """The host half of the 16-bit chunked backward (chunk matrices, padding to 64-token
-    chunks, the chunk-local gradients), with the two state chains restated in fp32 torch
-    (the HIP kernel's parity with that restatement is a GPU test), against the oracle's
-    chunked backward in fp64, to 1e-4 of max|grad|."""
-    from atma_amd.kernel.gated_delta import _bwd16_local, _bwd16_prep
-    from helpers import bwd16_chain_reference, rel_err
+def test_bwd16_restatements_vs_oracle(B, T, H, d, s0, dfinal):
+    """The torch restatements of the three launches of the 16-bit chunked backward (prep:
+    chunk matrices and padding to 64-token chunks; chain: the state and state-gradient
+    chains; local: the chunk-local gradients), composed in fp32, against the oracle's
+    chunked backward in fp64, to 1e-4 of max|grad|.  The GPU tests hold each HIP launch
+    to its restatement."""
+    from helpers import (CHAIN_TILES, bwd16_chain_reference, bwd16_local_reference, bwd16_prep_reference,
+                         rel_err)
     g = torch.Generator().manual_seed(T + d)
-    q = G.l2_normalize(torch.randn(B, T, H, d, generator=g)) * 0.7
-    k = G.l2_normalize(torch.randn(B, T, H, d, generator=g))
-    v, dO = torch.randn(B, T, H, d, generator=g), torch.randn(B, T, H, d, generator=g)
-    gl = torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=g) + 2.0)
-    beta = torch.sigmoid(torch.randn(B, T, H, generator=g))
-    S0 = torch.randn(B, H, d, d, generator=g) * 0.3 if s0 else None
-    dST = torch.randn(B, H, d, d, generator=g) if dfinal else None
-    prep = _bwd16_prep(q, k, v, gl, beta, dO, torch.float32)
+    f32 = dict(dtype=torch.float32)
+    q = G.l2_normalize(torch.randn(B, T, H, d, generator=g, **f32)) * 0.7
+    k = G.l2_normalize(torch.randn(B, T, H, d, generator=g, **f32))
+    v, dO = torch.randn(B, T, H, d, generator=g, **f32), torch.randn(B, T, H, d, generator=g, **f32)
+    gl = torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=g, **f32) + 2.0)
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=g, **f32))
+    S0 = torch.randn(B, H, d, d, generator=g, **f32) * 0.3 if s0 else None
+    dST = torch.randn(B, H, d, d, generator=g, **f32) if dfinal else None
+    prep = bwd16_prep_reference(q, k, v, gl, beta, dO, torch.float32)
     st = lambda x: None if x is None else x.reshape(B * H, d, d)  # noqa: E731
-    s_entry, ds_end, dy, ds0 = bwd16_chain_reference(*prep["tiles"], st(S0), st(dST))
-    got = _bwd16_local(prep, s_entry, ds_end, dy) + (ds0.reshape(B, H, d, d),)
-    ref = [torch.zeros(B, T, H, d, dtype=torch.float64) for _ in range(3)] + \
-          [torch.zeros(B, T, H, dtype=torch.float64) for _ in range(2)] + [torch.zeros(B, H, d, d, dtype=torch.float64)]
+    s_entry, ds_end, u, dy, ds0 = bwd16_chain_reference(*(prep[n] for n in CHAIN_TILES), st(S0), st(dST))
+    got = bwd16_local_reference(prep, s_entry, ds_end, u, dy) + (ds0.reshape(B, H, d, d),)
+    ref = [torch.zeros(B, T, H, d) for _ in range(3)] + [torch.zeros(B, T, H) for _ in range(2)] + \
+          [torch.zeros(B, H, d, d)]
     for b in range(B):
         for h in range(H):
-            z = torch.zeros(d, d, dtype=torch.float64)
+            z = torch.zeros(d, d)
             out = G.gated_delta_chunked_backward(
                 q[b, :, h].double(), k[b, :, h].double(), v[b, :, h].double(), gl[b, :, h].double(),
                 beta[b, :, h].double(), z if S0 is None else S0[b, h].double(), dO[b, :, h].double(),
