@@ -56,9 +56,9 @@ SIGNATURES = {
         _f32, _f32, _p, _sz, _p]),
     "atma_gated_delta_bwd_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64]),
     "atma_gated_delta_bwd": (_i32, [_p] * 14 + [_i64] * 5 + [_p, _sz, _p]),
-    "atma_gated_delta_bwd16_prep": (_i32, [_p] * 17 + [_i64] * 4 + [_i32, _p]),
+    "atma_gated_delta_bwd16_prep": (_i32, [_p] * 17 + [_i64] * 4 + [_f32, _i32, _i32, _p]),
     "atma_gated_delta_bwd16_chain": (_i32, [_p] * 17 + [_i64] * 3 + [_i32, _p]),
-    "atma_gated_delta_bwd16_local": (_i32, [_p] * 16 + [_i64] * 4 + [_i32, _p]),
+    "atma_gated_delta_bwd16_local": (_i32, [_p] * 18 + [_i64] * 4 + [_i32, _p]),
     "atma_squared_relu_gate": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i32, _p]),
     "atma_softcap_logits": (_i32, [_p, _p, _i64, _i32, _p]),
     "atma_packed_causal_conv1d": (_i32, [

@@ -399,15 +399,14 @@ def _bwd16_check(q, k, v, d_out, g, beta):
     B, T, H, d = q.shape
     if tuple(g.shape) != (B, T, H) or tuple(beta.shape) != (B, T, H):
         raise ValueError("gated_delta_bwd16: g and beta must be (B, T, H)")
-    if q.dtype != torch.float32 or k.dtype != torch.float32 or g.dtype != torch.float32 \
-            or beta.dtype != torch.float32:
-        raise ValueError("gated_delta_bwd16: q, k, g, beta must be fp32")
-    if v.dtype not in (torch.bfloat16, torch.float16) or d_out.dtype != v.dtype:
-        raise ValueError("gated_delta_bwd16: v and d_out must share a 16-bit dtype")
+    if g.dtype != torch.float32 or beta.dtype != torch.float32:
+        raise ValueError("gated_delta_bwd16: g and beta must be fp32")
+    if q.dtype not in (torch.bfloat16, torch.float16) or any(t.dtype != q.dtype for t in (k, v, d_out)):
+        raise ValueError("gated_delta_bwd16: q, k, v, d_out must share a 16-bit dtype")
     return [t.contiguous() for t in (q, k, v, d_out, g, beta)]
 
 
-def _bwd16_prep(q, k, v, d_out, g, beta):
+def _bwd16_prep(q, k, v, d_out, g, beta, scale, l2norm):
     lib = _lib.load()
     B, T, H, d = q.shape
     NC = (T + 63) // 64
@@ -416,12 +415,12 @@ def _bwd16_prep(q, k, v, d_out, g, beta):
     kr, qr = (torch.empty((BH, NC, 64, d), **t16) for _ in range(2))
     kt, qt, vt, ot, got = (torch.empty((BH, NC, d, 64), **t16) for _ in range(5))
     tm, tt, rt = (torch.empty((BH, NC, 64, 64), **t16) for _ in range(3))
-    f = torch.empty((BH, NC, 5, 64), device=q.device, dtype=torch.float32)
+    f = torch.empty((BH, NC, 9, 64), device=q.device, dtype=torch.float32)
     rc = lib.atma_gated_delta_bwd16_prep(q.data_ptr(), k.data_ptr(), v.data_ptr(), d_out.data_ptr(), g.data_ptr(),
                                          beta.data_ptr(), kr.data_ptr(), kt.data_ptr(), qr.data_ptr(), qt.data_ptr(),
                                          tm.data_ptr(), tt.data_ptr(), rt.data_ptr(), vt.data_ptr(), ot.data_ptr(),
-                                         got.data_ptr(), f.data_ptr(), B, T, H, d, _lib.dtype_code(v.dtype),
-                                         _lib.stream_handle(q.device))
+                                         got.data_ptr(), f.data_ptr(), B, T, H, d, float(scale), 1 if l2norm else 0,
+                                         _lib.dtype_code(v.dtype), _lib.stream_handle(q.device))
     _lib.check(rc, "gated_delta_bwd16_prep")
     return [kr, kt, qr, qt, tm, tt, rt, vt, ot, got, f]
 
@@ -443,69 +442,73 @@ def _bwd16_chain(kr, kt, qt, tm, tt, rt, vt, ot, got, f, s0, dst):
     return [s_entry, ds_end, u, dy, ds0]
 
 
-def _bwd16_local(B, T, H, kr, kt, qr, qt, v, d_out, f, s_entry, ds_end, u, dy):
+def _bwd16_local(kr, kt, qr, qt, q, k, v, d_out, f, s_entry, ds_end, u, dy):
     lib = _lib.load()
-    d = kr.shape[-1]
-    f32 = dict(device=kr.device, dtype=torch.float32)
-    dq, dk = (torch.empty((B, T, H, d), **f32) for _ in range(2))
-    dv = torch.empty((B, T, H, d), device=kr.device, dtype=v.dtype)
-    dg, db = (torch.empty((B, T, H), **f32) for _ in range(2))
-    rc = lib.atma_gated_delta_bwd16_local(kr.data_ptr(), kt.data_ptr(), qr.data_ptr(), qt.data_ptr(), v.data_ptr(),
-                                          d_out.data_ptr(), f.data_ptr(), s_entry.data_ptr(), ds_end.data_ptr(),
-                                          u.data_ptr(), dy.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                                          dg.data_ptr(), db.data_ptr(), B, T, H, d, _lib.dtype_code(v.dtype),
-                                          _lib.stream_handle(kr.device))
+    B, T, H, d = q.shape
+    t16 = dict(device=q.device, dtype=q.dtype)
+    dq, dk, dv = (torch.empty((B, T, H, d), **t16) for _ in range(3))
+    dg, db = (torch.empty((B, T, H), device=q.device, dtype=torch.float32) for _ in range(2))
+    rc = lib.atma_gated_delta_bwd16_local(kr.data_ptr(), kt.data_ptr(), qr.data_ptr(), qt.data_ptr(), q.data_ptr(),
+                                          k.data_ptr(), v.data_ptr(), d_out.data_ptr(), f.data_ptr(),
+                                          s_entry.data_ptr(), ds_end.data_ptr(), u.data_ptr(), dy.data_ptr(),
+                                          dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dg.data_ptr(), db.data_ptr(),
+                                          B, T, H, d, _lib.dtype_code(q.dtype), _lib.stream_handle(q.device))
     _lib.check(rc, "gated_delta_bwd16_local")
     return [dq, dk, dv, dg, db]
 
 
+def _bwd16_states(initial_state, d_final_state, B, H, d):
+    out = []
+    for x in (initial_state, d_final_state):
+        if x is not None and tuple(x.shape) != (B, H, d, d):
+            raise ValueError("gated_delta_bwd16: states must be (B, H, d, d)")
+        out.append(None if x is None else x.to(torch.float32).contiguous().reshape(B * H, d, d))
+    return out
+
+
 @torch.library.custom_op("atma_hip::gated_delta_bwd16", mutates_args=())
 def gated_delta_bwd16_op(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,
-                         initial_state: Optional[Tensor], d_out: Tensor,
-                         d_final_state: Optional[Tensor]) -> List[Tensor]:
-    """Chunked (WY) backward for 16-bit training: q (scaled, normalised), k (normalised)
-    (B, T, H, d) fp32; v, d_out (B, T, H, d) 16-bit; g (log decay), beta (B, T, H) fp32;
-    initial_state, d_final_state (B, H, d, d) fp32 or None.  Returns dq, dk (fp32), dv (v's
-    dtype), dg, dbeta, d_initial_state (fp32).  Three launches: prep, chain, local."""
+                         initial_state: Optional[Tensor], d_out: Tensor, d_final_state: Optional[Tensor],
+                         scale: float, l2norm: bool) -> List[Tensor]:
+    """Chunked (WY) backward for 16-bit training of ``chunk_gated_delta_rule`` with raw
+    q, k, v, d_out (B, T, H, d) of one 16-bit dtype (l2norm: q and k l2-normalised in the
+    recurrence, q then times scale); g (log decay), beta (B, T, H) fp32; initial_state,
+    d_final_state (B, H, d, d) fp32 or None.  Returns dq, dk, dv (16-bit), dg, dbeta,
+    d_initial_state (fp32).  Three launches: prep, chain, local."""
     q, k, v, d_out, g, beta = _bwd16_check(q, k, v, d_out, g, beta)
     B, T, H, d = q.shape
-    f32 = dict(device=q.device, dtype=torch.float32)
+    s0, dst = _bwd16_states(initial_state, d_final_state, B, H, d)
     if T == 0:
-        ds0 = torch.zeros((B, H, d, d), **f32) if d_final_state is None else d_final_state.float().clone()
+        ds0 = torch.zeros((B, H, d, d), device=q.device, dtype=torch.float32) if dst is None else \
+            dst.reshape(B, H, d, d).clone()
         return [torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v), torch.zeros_like(g),
                 torch.zeros_like(beta), ds0]
-    st = [None if x is None else x.to(torch.float32).contiguous().reshape(B * H, d, d)
-          for x in (initial_state, d_final_state)]
-    for x in st:
-        if x is not None and x.numel() != B * H * d * d:
-            raise ValueError("gated_delta_bwd16: states must be (B, H, d, d)")
-    kr, kt, qr, qt, tm, tt, rt, vt, ot, got, f = _bwd16_prep(q, k, v, d_out, g, beta)
-    s_entry, ds_end, u, dy, ds0 = _bwd16_chain(kr, kt, qt, tm, tt, rt, vt, ot, got, f, st[0], st[1])
-    dq, dk, dv, dg, db = _bwd16_local(B, T, H, kr, kt, qr, qt, v, d_out, f, s_entry, ds_end, u, dy)
+    kr, kt, qr, qt, tm, tt, rt, vt, ot, got, f = _bwd16_prep(q, k, v, d_out, g, beta, scale, l2norm)
+    s_entry, ds_end, u, dy, ds0 = _bwd16_chain(kr, kt, qt, tm, tt, rt, vt, ot, got, f, s0, dst)
+    dq, dk, dv, dg, db = _bwd16_local(kr, kt, qr, qt, q, k, v, d_out, f, s_entry, ds_end, u, dy)
     return [dq, dk, dv, dg, db, ds0.reshape(B, H, d, d)]
 
 
 @gated_delta_bwd16_op.register_fake
-def _(q, k, v, g, beta, initial_state, d_out, d_final_state):
+def _(q, k, v, g, beta, initial_state, d_out, d_final_state, scale, l2norm):
     B, T, H, d = q.shape
-    return [q.new_empty(q.shape), q.new_empty(q.shape), v.new_empty(v.shape), g.new_empty(g.shape),
-            g.new_empty(g.shape), q.new_empty((B, H, d, d))]
+    return [q.new_empty(q.shape), k.new_empty(k.shape), v.new_empty(v.shape), g.new_empty(g.shape),
+            g.new_empty(g.shape), g.new_empty((B, H, d, d))]
 
 
-def gated_delta_bwd16_stages(q, k, v, g, beta, initial_state, d_out, d_final_state):
+def gated_delta_bwd16_stages(q, k, v, g, beta, initial_state, d_out, d_final_state, scale, l2norm):
     """The three launches of ``gated_delta_bwd16`` with every intermediate returned (for
     tests): dict of the prep's tiles (kr, kt, qr, qt, tm, tt, rt, vt, ot, got, f; chunk-head
     tensors shaped (B*H, NC, ...)), the chain's outputs (s_entry, ds_end, u, dy, ds0) and
     the local gradients (dq, dk, dv, dg, db)."""
     q, k, v, d_out, g, beta = _bwd16_check(q, k, v, d_out, g, beta)
     B, T, H, d = q.shape
-    st = [None if x is None else x.to(torch.float32).contiguous().reshape(B * H, d, d)
-          for x in (initial_state, d_final_state)]
+    s0, dst = _bwd16_states(initial_state, d_final_state, B, H, d)
     names = ["kr", "kt", "qr", "qt", "tm", "tt", "rt", "vt", "ot", "got", "f"]
-    out = dict(zip(names, _bwd16_prep(q, k, v, d_out, g, beta)))
-    chain = _bwd16_chain(*(out[n] for n in ("kr", "kt", "qt", "tm", "tt", "rt", "vt", "ot", "got", "f")), *st)
+    out = dict(zip(names, _bwd16_prep(q, k, v, d_out, g, beta, scale, l2norm)))
+    chain = _bwd16_chain(*(out[n] for n in ("kr", "kt", "qt", "tm", "tt", "rt", "vt", "ot", "got", "f")), s0, dst)
     out.update(zip(["s_entry", "ds_end", "u", "dy", "ds0"], chain))
-    loc = _bwd16_local(B, T, H, out["kr"], out["kt"], out["qr"], out["qt"], v, d_out, out["f"], out["s_entry"],
+    loc = _bwd16_local(out["kr"], out["kt"], out["qr"], out["qt"], q, k, v, d_out, out["f"], out["s_entry"],
                        out["ds_end"], out["u"], out["dy"])
     out.update(zip(["dq", "dk", "dv", "dg", "db"], loc))
     return out

@@ -28,7 +28,11 @@
 
 namespace atma {
 
-constexpr int kFRows = 5;  // per-token factor rows of a chunk: Ga, w, beta, Ga_C, lg
+// Per-token factor rows of a chunk: Ga, w, beta, Ga_C, lg, then the l2-norm factors of
+// the q and k rows: iq = scale / max(|q|, eps), ik = 1 / max(|k|, eps) (scale and 1 without
+// l2norm) and uq2 = 1 / |q|^2, uk2 = 1 / |k|^2 where the norm exceeds eps (else 0; 0
+// without l2norm), all 0 past the sequence's end.
+constexpr int kFRows = 9;
 
 struct Bwd16ChainArgs {
   const void* kr;    // [N][64][D]  k rows of each chunk (N = BH * NC, chunk-head major)
@@ -331,27 +335,37 @@ __global__ void __launch_bounds__(256, 1) gdn_bwd16_chain_kernel(Bwd16ChainArgs 
 
 // ------------------------------------------------------------------------------ prep
 // One workgroup per chunk-head item n (4 waves): the operand tiles of the chain and of the
-// chunk-local gradients.  k, q rows (fp32, prepared) are rounded to 16 bits once; wave P
+// chunk-local gradients.  The raw k, q rows are l2-normalised (q also scaled, as the
+// forward does: x / max(|x|, 1e-12)) and rounded to 16 bits once; wave P
 // forms row block P of K K^T and Q K^T on MFMA and from them N = diag(beta) A (fp32, LDS)
 // and Rq^T; then wave 0 inverts I + N by forward substitution (lane j solves column j of T,
 // 64 x 64 fully unrolled, N read as broadcast rows) while waves 1-3 write the transposed
 // tiles k^T, q^T, v^T, dO^T and (diag(Ga) dO)^T from the LDS rows.
 struct Bwd16PrepArgs {
-  const float* q;     // (B, T, H, D) fp32, scaled and normalised, contiguous
-  const float* k;     // (B, T, H, D) fp32, normalised
+  const void* q;      // (B, T, H, D) 16-bit, raw
+  const void* k;      // (B, T, H, D) 16-bit, raw
   const void* v;      // (B, T, H, D) 16-bit
   const void* dO;     // (B, T, H, D) 16-bit
   const float* g;     // (B, T, H) log decay
   const float* beta;  // (B, T, H)
   void *kr, *kt, *qr, *qt, *tm, *tt, *rt, *vt, *ot, *got;
   float* f;
+  float scale;
+  int l2norm;
   int B, T, H, NC;
 };
+
+// Sum over each group of 8 lanes (the two quads of each half row), in every lane.
+__device__ __forceinline__ float row8_sum(float x) {
+  x += dpp_f32<0xB1>(x);
+  x += dpp_f32<0x4E>(x);
+  return x + dpp_f32<0x141>(x);
+}
 
 template <typename T, int D>
 __global__ void __launch_bounds__(256) gdn_bwd16_prep_kernel(Bwd16PrepArgs a) {
   constexpr int C = 64, PD = D + 8, NP = 68, KS = D / 32;
-  constexpr int NF = D / 16, NV = D / 32;  // float4 / 16-byte row chunks per thread
+  constexpr int NV = D / 32;  // 16-byte row chunks per thread
   __shared__ __attribute__((aligned(16))) T Ks[C * PD];
   __shared__ __attribute__((aligned(16))) T Qs[C * PD];
   __shared__ __attribute__((aligned(16))) T Vs[C * PD];
@@ -372,24 +386,17 @@ __global__ void __launch_bounds__(256) gdn_bwd16_prep_kernel(Bwd16PrepArgs a) {
 
   // rows (zero past the sequence's end), all loads issued before the stores
   {
-    f32x4 kx[NF], qx[NF];
-    u32x4 vx[NV], ox[NV];
-#pragma unroll
-    for (int j = 0; j < NF; ++j) {
-      const int i = tid + 256 * j, r = i / (D / 4), q4 = i % (D / 4);
-      kx[j] = qx[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (r < rows) {
-        kx[j] = *(const f32x4*)(a.k + base + r * rs + 4 * q4);
-        qx[j] = *(const f32x4*)(a.q + base + r * rs + 4 * q4);
-      }
-    }
+    u32x4 kx[NV], qx[NV], vx[NV], ox[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int i = tid + 256 * j, r = i / (D / 8), ch = i % (D / 8);
-      vx[j] = ox[j] = u32x4{0u, 0u, 0u, 0u};
+      kx[j] = qx[j] = vx[j] = ox[j] = u32x4{0u, 0u, 0u, 0u};
       if (r < rows) {
-        vx[j] = *(const u32x4*)((const T*)a.v + base + r * rs + 8 * ch);
-        ox[j] = *(const u32x4*)((const T*)a.dO + base + r * rs + 8 * ch);
+        const int64_t o = base + r * rs + 8 * ch;
+        kx[j] = *(const u32x4*)((const T*)a.k + o);
+        qx[j] = *(const u32x4*)((const T*)a.q + o);
+        vx[j] = *(const u32x4*)((const T*)a.v + o);
+        ox[j] = *(const u32x4*)((const T*)a.dO + o);
       }
     }
     float gl = 0.f, bt = 0.f;
@@ -397,19 +404,44 @@ __global__ void __launch_bounds__(256) gdn_bwd16_prep_kernel(Bwd16PrepArgs a) {
       gl = a.g[(tok0 + lane) * a.H + h];
       bt = a.beta[(tok0 + lane) * a.H + h];
     }
-#pragma unroll
-    for (int j = 0; j < NF; ++j) {
-      const int i = tid + 256 * j, r = i / (D / 4), q4 = i % (D / 4);
-      const u32x2 kp = {pack2<T>(kx[j][0], kx[j][1]), pack2<T>(kx[j][2], kx[j][3])};
-      const u32x2 qp = {pack2<T>(qx[j][0], qx[j][1]), pack2<T>(qx[j][2], qx[j][3])};
-      *(u32x2*)(Ks + r * PD + 4 * q4) = kp;
-      *(u32x2*)(Qs + r * PD + 4 * q4) = qp;
-      *(u32x2*)((T*)a.kr + (n * C + r) * D + 4 * q4) = kp;
-      *(u32x2*)((T*)a.qr + (n * C + r) * D + 4 * q4) = qp;
-    }
+    float* fo = a.f + n * kFRows * C;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int i = tid + 256 * j, r = i / (D / 8), ch = i % (D / 8);
+      // row norms: a row's D / 8 chunks sit in D / 8 consecutive lanes
+      float sk = 0.f, sq = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        sk = fmaf(elem16<T>(kx[j], e), elem16<T>(kx[j], e), sk);
+        sq = fmaf(elem16<T>(qx[j], e), elem16<T>(qx[j], e), sq);
+      }
+      if constexpr (D == 128) {
+        sk = row16_sum(sk);
+        sq = row16_sum(sq);
+      } else {
+        sk = row8_sum(sk);
+        sq = row8_sum(sq);
+      }
+      const float nk = sqrtf(sk), nq = sqrtf(sq);
+      const bool ok = r < rows;
+      const float ik = !ok ? 0.f : a.l2norm ? 1.f / fmaxf(nk, 1e-12f) : 1.f;
+      const float iq = !ok ? 0.f : (a.l2norm ? 1.f / fmaxf(nq, 1e-12f) : 1.f) * a.scale;
+      if (ch == 0) {
+        fo[5 * C + r] = iq;
+        fo[6 * C + r] = ik;
+        fo[7 * C + r] = ok && a.l2norm && nq > 1e-12f ? 1.f / sq : 0.f;
+        fo[8 * C + r] = ok && a.l2norm && nk > 1e-12f ? 1.f / sk : 0.f;
+      }
+      u32x4 kp, qp;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        kp[e] = pack2<T>(ik * elem16<T>(kx[j], 2 * e), ik * elem16<T>(kx[j], 2 * e + 1));
+        qp[e] = pack2<T>(iq * elem16<T>(qx[j], 2 * e), iq * elem16<T>(qx[j], 2 * e + 1));
+      }
+      *(u32x4*)(Ks + r * PD + 8 * ch) = kp;
+      *(u32x4*)(Qs + r * PD + 8 * ch) = qp;
+      *(u32x4*)((T*)a.kr + (n * C + r) * D + 8 * ch) = kp;
+      *(u32x4*)((T*)a.qr + (n * C + r) * D + 8 * ch) = qp;
       *(u32x4*)(Vs + r * PD + 8 * ch) = vx[j];
       *(u32x4*)(Os + r * PD + 8 * ch) = ox[j];
     }
@@ -425,7 +457,6 @@ __global__ void __launch_bounds__(256) gdn_bwd16_prep_kernel(Bwd16PrepArgs a) {
       Lg[lane] = lg;
       Bt[lane] = bt;
       Gs[lane] = ga;
-      float* fo = a.f + n * kFRows * C;
       fo[lane] = ga;
       fo[C + lane] = expf(lgC - lg);
       fo[2 * C + lane] = bt;
@@ -531,11 +562,11 @@ struct Bwd16LocalArgs {
   const void *kr, *kt, *qr, *qt;
   const void* v;   // (B, T, H, D) 16-bit
   const void* dO;  // (B, T, H, D) 16-bit
-  const float* f;  // [N][5][64]
+  const void *q, *k;  // (B, T, H, D) 16-bit, raw (the l2 norm's backward)
+  const float* f;  // [N][kFRows][64]
   const void *s_entry, *ds_end, *u;
   const float* dy;
-  float *dq, *dk;  // (B, T, H, D) fp32
-  void* dv;        // (B, T, H, D) 16-bit
+  void *dq, *dk, *dv;  // (B, T, H, D) 16-bit
   float *dg, *db;  // (B, T, H)
   int B, T, H, NC;
 };
@@ -725,6 +756,10 @@ __global__ void __launch_bounds__(256, 1) gdn_bwd16_local_kernel(Bwd16LocalArgs 
     grA[j] = *(const u32x4*)(GRs + ra * PC + 32 * j + 8 * g);
   }
   float rk1[4] = {0.f, 0.f, 0.f, 0.f}, rq2[4] = {0.f, 0.f, 0.f, 0.f}, rk3[4] = {0.f, 0.f, 0.f, 0.f};
+  // gradients of the normalised rows (dKn, dQs), then the l2 norm's backward:
+  // dx = i_x dX - i_x u_x2 x (x . dX) with x the raw row
+  f32x4 dKn[DT], dQs[DT], kraw[DT], qraw[DT];
+  float xk[4] = {0.f, 0.f, 0.f, 0.f}, xq[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int t = 0; t < DT; ++t) {
     f32x4 dk = {0.f, 0.f, 0.f, 0.f}, dq = dk;
@@ -744,10 +779,28 @@ __global__ void __launch_bounds__(256, 1) gdn_bwd16_local_kernel(Bwd16LocalArgs 
       rk1[i] = fmaf(kv, P1[t][i], rk1[i]);
       rq2[i] = fmaf(qv, P2[t][i], rq2[i]);
       rk3[i] = fmaf(kv, P3[t][i], rk3[i]);
+      dKn[t][i] = dk[i] - Ga[p] * Bf[p] * P1[t][i] + Wf[p] * P3[t][i];
+      dQs[t][i] = dq[i] + Ga[p] * P2[t][i];
+      kraw[t][i] = qraw[t][i] = 0.f;
       if (p < rows) {
-        const int64_t o = base + p * rs + d;
-        a.dk[o] = dk[i] - Ga[p] * Bf[p] * P1[t][i] + Wf[p] * P3[t][i];
-        a.dq[o] = dq[i] + Ga[p] * P2[t][i];
+        kraw[t][i] = to_f32(((const T*)a.k)[base + p * rs + d]);
+        qraw[t][i] = to_f32(((const T*)a.q)[base + p * rs + d]);
+      }
+      xk[i] = fmaf(kraw[t][i], dKn[t][i], xk[i]);
+      xq[i] = fmaf(qraw[t][i], dQs[t][i], xq[i]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int p = 16 * wave + 4 * g + i;
+    const float iq = Fs[5 * C + p], ik = Fs[6 * C + p];
+    const float pq = iq * Fs[7 * C + p] * row16_sum(xq[i]), pk = ik * Fs[8 * C + p] * row16_sum(xk[i]);
+    if (p < rows) {
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const int64_t o = base + p * rs + 16 * t + c16;
+        ((T*)a.dk)[o] = from_f32<T>(ik * dKn[t][i] - pk * kraw[t][i]);
+        ((T*)a.dq)[o] = from_f32<T>(iq * dQs[t][i] - pq * qraw[t][i]);
       }
     }
   }
@@ -818,11 +871,11 @@ bool aligned16(std::initializer_list<const void*> ps) {
     }                                                                                    \
   } while (0)
 
-extern "C" int atma_gated_delta_bwd16_prep(const float* q, const float* k, const void* v, const void* d_out,
+extern "C" int atma_gated_delta_bwd16_prep(const void* q, const void* k, const void* v, const void* d_out,
                                            const float* g, const float* beta, void* kr, void* kt, void* qr,
                                            void* qt, void* tm, void* tt, void* rt, void* vt, void* ot, void* got,
-                                           float* f, int64_t B, int64_t T, int64_t H, int64_t d, int dtype,
-                                           void* stream) {
+                                           float* f, int64_t B, int64_t T, int64_t H, int64_t d, float scale,
+                                           int l2norm, int dtype, void* stream) {
   using namespace atma;
   if (!bwd16_dims_ok(d, dtype, "gated_delta_bwd16_prep")) return ATMA_ERR_UNSUPPORTED;
   if (B < 0 || T < 0 || H <= 0) return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_prep: bad sizes");
@@ -835,7 +888,7 @@ extern "C" int atma_gated_delta_bwd16_prep(const float* q, const float* k, const
     return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_prep: operands must be 16-byte aligned");
   if (B * H * NC > 0x7fffffff || B * T > 0x7fffffff)
     return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_prep: sizes too large");
-  Bwd16PrepArgs a{q, k, v, d_out, g, beta, kr, kt, qr, qt, tm, tt, rt, vt, ot, got, f,
+  Bwd16PrepArgs a{q, k, v, d_out, g, beta, kr, kt, qr, qt, tm, tt, rt, vt, ot, got, f, scale, l2norm ? 1 : 0,
                   (int)B, (int)T, (int)H, (int)NC};
   const dim3 grid((unsigned)(B * H * NC));
   ATMA_BWD16_DISPATCH(gdn_bwd16_prep_kernel, grid, (hipStream_t)stream, a);
@@ -866,23 +919,23 @@ extern "C" int atma_gated_delta_bwd16_chain(const void* kr, const void* kt, cons
 }
 
 extern "C" int atma_gated_delta_bwd16_local(const void* kr, const void* kt, const void* qr, const void* qt,
-                                            const void* v, const void* d_out, const float* f, const void* s_entry,
-                                            const void* ds_end, const void* u, const float* dy, float* dq,
-                                            float* dk, void* dv, float* dg, float* dbeta, int64_t B, int64_t T,
-                                            int64_t H, int64_t d, int dtype, void* stream) {
+                                            const void* q, const void* k, const void* v, const void* d_out,
+                                            const float* f, const void* s_entry, const void* ds_end, const void* u,
+                                            const float* dy, void* dq, void* dk, void* dv, float* dg, float* dbeta,
+                                            int64_t B, int64_t T, int64_t H, int64_t d, int dtype, void* stream) {
   using namespace atma;
   if (!bwd16_dims_ok(d, dtype, "gated_delta_bwd16_local")) return ATMA_ERR_UNSUPPORTED;
   if (B < 0 || T < 0 || H <= 0) return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_local: bad sizes");
   const int64_t NC = (T + 63) / 64;
   if (B == 0 || NC == 0) return ATMA_OK;
-  if (!kr || !kt || !qr || !qt || !v || !d_out || !f || !s_entry || !ds_end || !u || !dy || !dq || !dk || !dv ||
-      !dg || !dbeta)
+  if (!kr || !kt || !qr || !qt || !q || !k || !v || !d_out || !f || !s_entry || !ds_end || !u || !dy || !dq ||
+      !dk || !dv || !dg || !dbeta)
     return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_local: null pointer");
   if (!aligned16({kr, kt, qr, qt, v, d_out, s_entry, ds_end, u, dy, dv}))
     return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_local: operands must be 16-byte aligned");
   if (B * H * NC > 0x7fffffff || B * T > 0x7fffffff)
     return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_local: sizes too large");
-  Bwd16LocalArgs a{kr, kt, qr, qt, v, d_out, f, s_entry, ds_end, u, dy, dq, dk, dv, dg, dbeta,
+  Bwd16LocalArgs a{kr, kt, qr, qt, v, d_out, q, k, f, s_entry, ds_end, u, dy, dq, dk, dv, dg, dbeta,
                    (int)B, (int)T, (int)H, (int)NC};
   const dim3 grid((unsigned)(B * H * NC));
   ATMA_BWD16_DISPATCH(gdn_bwd16_local_kernel, grid, (hipStream_t)stream, a);

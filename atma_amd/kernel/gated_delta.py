@@ -151,49 +151,53 @@ class _GatedDeltaFn(torch.autograd.Function):
 
 
 class _GatedDelta16Fn(torch.autograd.Function):
-    """The recurrence on prepared operands for 16-bit training (q scaled and normalised,
-    k normalised, in fp32; v, log decay g, beta, fp32 [K, V] initial state): forward by
-    the 16-bit chunked prefill kernel on the operands rounded to the input dtype,
-    backward by the chunked (WY) form (``gated_delta_bwd16``: a prep launch forming each
-    chunk's matrices, the chain launch carrying the state and its gradient across the
-    chunks, and a launch forming every gradient local to a chunk)."""
+    """The recurrence for 16-bit training on the raw q, k, v (H heads each), log decay g,
+    beta and fp32 [K, V] initial state: forward by the 16-bit chunked prefill kernel (l2
+    norm and scale applied in-kernel), backward by the chunked (WY) form
+    (``gated_delta_bwd16``: a prep launch forming each chunk's matrices from the
+    normalised rows, the chain launch carrying the state and its gradient across the
+    chunks, and a launch forming every gradient local to a chunk, taken back through the
+    l2 norm to the raw rows)."""
 
     @staticmethod
-    def forward(ctx, qs, kn, v, g, beta, S0):
-        td = v.dtype
-        o, S = torch.ops.atma_hip.gated_delta_fwd(qs.to(td), kn.to(td), v, g, beta, S0)
-        ctx.save_for_backward(qs, kn, v, g, beta, S0)
+    def forward(ctx, q, k, v, g, beta, S0, scale, l2norm):
+        o, S = torch.ops.atma_hip.chunk_gated_delta_rule(q, k, v, g, beta, S0, scale, l2norm, True, None, 0)
+        ctx.save_for_backward(q, k, v, g, beta, S0)
+        ctx.scale, ctx.l2norm = scale, l2norm
         return o, S
 
     @staticmethod
     def backward(ctx, dO, dS):
-        qs, kn, v, g, beta, S0 = ctx.saved_tensors
+        q, k, v, g, beta, S0 = ctx.saved_tensors
         dO = torch.zeros_like(v) if dO is None else dO.to(v.dtype)
-        dq, dk, dv, dg, db, ds0 = torch.ops.atma_hip.gated_delta_bwd16(qs, kn, v, g, beta, S0, dO, dS)
-        return dq, dk, dv, dg, db, (ds0 if S0 is not None else None)
+        dq, dk, dv, dg, db, ds0 = torch.ops.atma_hip.gated_delta_bwd16(q, k, v, g, beta, S0, dO, dS, ctx.scale,
+                                                                      ctx.l2norm)
+        return dq, dk, dv, dg, db, (ds0 if S0 is not None else None), None, None
 
 
 def _chunk_gated_delta_train(q, k, v, g, beta, scale, initial_state, output_final_state, use_qk_l2norm):
     """Differentiable ``chunk_gated_delta_rule`` (the FLA autograd the reference trains
-    through, ``model/blocks.py:44-84``).  The l2 norm, the scale and grouped-head expansion
-    are torch ops (autograd differentiates them); the recurrence and its backward are HIP.
-    fp32 inputs: fp32 arithmetic throughout (sequential backward).  16-bit inputs with
-    dk = dv in {64, 128}: the 16-bit chunked forward and the chunked (WY) backward, 16-bit
-    products with fp32 accumulation as FLA's kernels.  o is returned in q's dtype."""
+    through, ``model/blocks.py:44-84``).  Grouped KV heads are expanded by a torch op
+    (autograd sums their gradients).  16-bit inputs with dk = dv in {64, 128}: the raw rows
+    go to the 16-bit chunked forward and the chunked (WY) backward, which apply the l2 norm
+    and scale (and their backward) in-kernel, 16-bit products with fp32 accumulation as
+    FLA's kernels.  Other inputs: the l2 norm and scale as torch ops, then the recurrence
+    and its sequential backward in fp32.  o is returned in q's dtype."""
     B, T, H, dk = q.shape
     if k.shape[2] != H:
         rep = H // k.shape[2]
         k, v = k.repeat_interleave(rep, dim=2), v.repeat_interleave(rep, dim=2)
+    S0 = None if initial_state is None else initial_state.float().contiguous()
+    if q.dtype in (torch.bfloat16, torch.float16) and dk == v.shape[3] and dk in (64, 128):
+        o, S = _GatedDelta16Fn.apply(q.contiguous(), k.contiguous(), v.contiguous(), g.float().contiguous(),
+                                     beta.float().contiguous(), S0, float(dk ** -0.5 if scale is None else scale),
+                                     bool(use_qk_l2norm))
+        return o, (S if output_final_state else None)
     qf, kf = q.float(), k.float()
     if use_qk_l2norm:
         qf = torch.nn.functional.normalize(qf, dim=-1, eps=1e-12)
         kf = torch.nn.functional.normalize(kf, dim=-1, eps=1e-12)
     qs = qf * (dk ** -0.5 if scale is None else float(scale))
-    S0 = None if initial_state is None else initial_state.float().contiguous()
-    if q.dtype in (torch.bfloat16, torch.float16) and dk == v.shape[3] and dk in (64, 128):
-        o, S = _GatedDelta16Fn.apply(qs.contiguous(), kf.contiguous(), v.contiguous(),
-                                     g.float().contiguous(), beta.float().contiguous(), S0)
-        return o, (S if output_final_state else None)
     o, S = _GatedDeltaFn.apply(qs.contiguous(), kf.contiguous(), v.float().contiguous(),
                                g.float().contiguous(), beta.float().contiguous(), S0)
     return o.to(q.dtype), (S if output_final_state else None)

@@ -316,13 +316,17 @@ int atma_gated_delta_bwd(const float* q, const float* k, const float* v, const f
  * aligned.  Tokens past T act as zero-padding (k = q = v = dO = 0, beta = 0, log decay 0),
  * which leaves every gradient exact.
  *
- * prep: q (scaled, normalised), k (normalised): (B, T, H, d) fp32; v, d_out: (B, T, H, d);
- * g (log decay), beta: (B, T, H) fp32.  Writes the 16-bit tiles kr, qr (N, 64, d) rows;
+ * prep: q, k, v, d_out: (B, T, H, d) 16-bit (q and k raw: with l2norm != 0 each row is
+ * divided by max(|x|, 1e-12), q then times scale, as the forward with
+ * use_qk_l2norm_in_kernel); g (log decay), beta: (B, T, H) fp32.  Writes the 16-bit tiles
+ * kr, qr (N, 64, d) rows of the normalised k and scaled q;
  * kt, qt, vt, ot, got (N, d, 64) = k^T, q^T, v^T, dO^T, (diag(Ga) dO)^T; tm, tt (N, 64, 64)
  * T = (I + diag(beta) A)^-1 and T^T, A[p,s] = exp(lg_p - lg_s) k_p.k_s (s < p); rt
  * (N, 64, 64) Rq^T, Rq[p,s] = exp(lg_p - lg_s) q_p.k_s (s <= p); and f (N, 5, 64) fp32 per
  * token: Ga = exp(lg), w = exp(lg_C - lg), beta, Ga_C, lg (lg the in-chunk inclusive
- * cumulative log decay).
+ * cumulative log decay), and the row-norm factors iq = scale / max(|q|, eps),
+ * ik = 1 / max(|k|, eps), uq2 = 1 / |q|^2, uk2 = 1 / |k|^2 (0 where |x| <= eps; without
+ * l2norm: scale, 1, 0, 0) -- f is (N, 9, 64).
  *
  * chain: the prep's tiles (BH = B * H); s0, dst (BH, d, d) [K, V] fp32 initial state and
  * final-state cotangent, or NULL (zero).  Runs the state forward over the chunks, then the
@@ -331,24 +335,26 @@ int atma_gated_delta_bwd(const float* q, const float* k, const float* v, const f
  * (N, d, d) 16-bit (each chunk's entry state, the gradient of its exit state), u (N, 64, d)
  * 16-bit (U = T diag(beta)(V - diag(Ga) K S)), dy (N, 64, d) fp32 and ds0 (BH, d, d) fp32.
  *
- * local: the prep's kr, kt, qr, qt, f, the chain's s_entry, ds_end, u, dy, and v, d_out as
- * given to the prep.  Writes dq, dk (B, T, H, d) fp32, dv (B, T, H, d) 16-bit, dg, dbeta
- * (B, T, H) fp32 (dg the gradient of the per-token log decay).
+ * local: the prep's kr, kt, qr, qt, f, the chain's s_entry, ds_end, u, dy, and q, k, v,
+ * d_out as given to the prep.  Writes dq, dk, dv (B, T, H, d) 16-bit (dq, dk through the
+ * l2 norm and scale to the raw rows), dg, dbeta (B, T, H) fp32 (dg the gradient of the
+ * per-token log decay).
  */
-int atma_gated_delta_bwd16_prep(const float* q, const float* k, const void* v, const void* d_out,
+int atma_gated_delta_bwd16_prep(const void* q, const void* k, const void* v, const void* d_out,
                                 const float* g, const float* beta, void* kr, void* kt, void* qr, void* qt,
                                 void* tm, void* tt, void* rt, void* vt, void* ot, void* got, float* f,
-                                int64_t B, int64_t T, int64_t H, int64_t d, int dtype, void* stream);
+                                int64_t B, int64_t T, int64_t H, int64_t d, float scale, int l2norm, int dtype,
+                                void* stream);
 int atma_gated_delta_bwd16_chain(const void* kr, const void* kt, const void* qt, const void* tm,
                                  const void* tt, const void* rt, const void* vt, const void* ot,
                                  const void* got, const float* f, const float* s0, const float* dst,
                                  void* s_entry, void* ds_end, void* u, float* dy, float* ds0, int64_t BH,
                                  int64_t NC, int64_t d, int dtype, void* stream);
 int atma_gated_delta_bwd16_local(const void* kr, const void* kt, const void* qr, const void* qt,
-                                 const void* v, const void* d_out, const float* f, const void* s_entry,
-                                 const void* ds_end, const void* u, const float* dy, float* dq, float* dk,
-                                 void* dv, float* dg, float* dbeta, int64_t B, int64_t T, int64_t H,
-                                 int64_t d, int dtype, void* stream);
+                                 const void* q, const void* k, const void* v, const void* d_out,
+                                 const float* f, const void* s_entry, const void* ds_end, const void* u,
+                                 const float* dy, void* dq, void* dk, void* dv, float* dg, float* dbeta,
+                                 int64_t B, int64_t T, int64_t H, int64_t d, int dtype, void* stream);
 
 /*
  * Fused MLP activation out = gate * relu(x)^2.  Replaces squared_relu_gate

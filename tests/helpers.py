@@ -45,19 +45,31 @@ def _from_chunks(x, B, T):
     return x.reshape(B, BH // B, NC * _CH, *x.shape[3:]).movedim(1, 2)[:, :T].contiguous()
 
 
-def bwd16_prep_reference(qs, kn, v, g, beta, dO, tile_dtype):
-    """fp32 torch restatement of ``gated_delta_bwd16_prep``: per 64-token chunk (zero
-    padding past T) lg = cumsum(g), Ga = exp(lg), w = exp(lg_C - lg),
+def bwd16_prep_reference(q, k, v, g, beta, dO, tile_dtype, scale=1.0, l2norm=True):
+    """fp32 torch restatement of ``gated_delta_bwd16_prep``: the raw q, k rows
+    l2-normalised (x / max(|x|, 1e-12)) with q then times scale, and per 64-token chunk
+    (zero padding past T) lg = cumsum(g), Ga = exp(lg), w = exp(lg_C - lg),
     E[p,s] = exp(lg_p - lg_s) (s <= p), A = E o K K^T (s < p),
     T = (I + diag(beta) A)^-1, Rq = E o Q K^T.  Returns a dict with the op's tiles (kr, kt,
     qr, qt, tm, tt, rt, vt, ot, got in tile_dtype, f fp32) and the fp32 chunk matrices the
     local restatement takes."""
-    B, T, H, D = qs.shape
+    B, T, H, D = q.shape
     NC = (T + _CH - 1) // _CH
     BH = B * H
-    dev = qs.device
-    Q, K, V, dOc = (_to_chunks(t.float(), NC) for t in (qs, kn, v, dO))
+    dev = q.device
+    qf, kf = q.float(), k.float()
+    if l2norm:
+        nq, nk = qf.norm(dim=-1), kf.norm(dim=-1)
+        iq, ik = scale / nq.clamp_min(1e-12), 1.0 / nk.clamp_min(1e-12)
+        uq2 = torch.where(nq > 1e-12, 1.0 / nq.square(), torch.zeros_like(nq))
+        uk2 = torch.where(nk > 1e-12, 1.0 / nk.square(), torch.zeros_like(nk))
+    else:
+        iq, ik = torch.full_like(qf[..., 0], scale), torch.ones_like(kf[..., 0])
+        uq2, uk2 = torch.zeros_like(iq), torch.zeros_like(ik)
+    Q, K, V, dOc = (_to_chunks(t, NC) for t in (qf * iq[..., None], kf * ik[..., None], v.float(), dO.float()))
+    qraw, kraw = _to_chunks(qf, NC), _to_chunks(kf, NC)
     gc, bc = _to_chunks(g.float(), NC), _to_chunks(beta.float(), NC)
+    iq, ik, uq2, uk2 = (_to_chunks(x, NC) for x in (iq, ik, uq2, uk2))
     lg = gc.cumsum(-1)
     Ga = lg.exp()
     w = (lg[..., -1:] - lg).exp()
@@ -75,12 +87,12 @@ def bwd16_prep_reference(qs, kn, v, g, beta, dO, tile_dtype):
 
     def tile(x):
         return x.to(tile_dtype).contiguous()
-    f = torch.stack((Ga, w, bc, GaC[..., None].expand_as(Ga), lg), dim=-2).contiguous()
+    f = torch.stack((Ga, w, bc, GaC[..., None].expand_as(Ga), lg, iq, ik, uq2, uk2), dim=-2).contiguous()
     out = dict(kr=tile(K), kt=tile(Kt), qr=tile(Q), qt=tile(Q.transpose(-1, -2)), tm=tile(Tm),
                tt=tile(Tm.transpose(-1, -2)), rt=tile(Rq.transpose(-1, -2)), vt=tile(V.transpose(-1, -2)),
                ot=tile(dOc.transpose(-1, -2)), got=tile((Ga[..., None] * dOc).transpose(-1, -2)), f=f)
     out.update(B=B, T=T, Q=Q, K=K, V=V, dOc=dOc, bc=bc, Ga=Ga, w=w, GaC=GaC, incl=incl, strict=strict,
-               E=E, A=A, Tm=Tm, Rq=Rq)
+               E=E, A=A, Tm=Tm, Rq=Rq, qraw=qraw, kraw=kraw, iq=iq, ik=ik, uq2=uq2, uk2=uk2)
     return out
 
 
@@ -126,8 +138,8 @@ def bwd16_local_reference(p, s_entry, ds_end, u, dy):
     dQ = (dRq o E) K + diag(Ga) dO S0^T; dlg = rowsum - colsum of dA o A and dRq o Rq
     + Ga o (rowsum(dO o Q S0) - beta o rowsum(dY o K S0)) - w o rowsum(K dS o U), plus
     sum(w o rowsum(K dS o U)) + Ga_C <dS, S0> at the chunk's last token; dg = the
-    reverse cumulative sum of dlg within the chunk.  Returns dq, dk, dv, dg, dbeta in
-    (B, T, H, .) fp32."""
+    reverse cumulative sum of dlg within the chunk; dq, dk then taken through the l2 norm
+    and scale to the raw rows.  Returns dq, dk, dv, dg, dbeta in (B, T, H, .) fp32."""
     Q, K, V, dOc, bc, Ga, w, GaC = (p[n] for n in ("Q", "K", "V", "dOc", "bc", "Ga", "w", "GaC"))
     E, A, Rq, incl, strict = (p[n] for n in ("E", "A", "Rq", "incl", "strict"))
     B, T = p["B"], p["T"]
@@ -147,6 +159,10 @@ def bwd16_local_reference(p, s_entry, ds_end, u, dy):
     dK = ((GA + GA.transpose(-1, -2)) @ K + GR.transpose(-1, -2) @ Q
           - (Ga * bc)[..., None] * (dY @ S0t) + w[..., None] * (U @ dS.transpose(-1, -2)))
     dQ = GR @ K + Ga[..., None] * (dOc @ S0t)
+    # the l2 norm's backward to the raw rows: dx = i_x dX - i_x u_x2 x (x . dX)
+    qraw, kraw, iq, ik, uq2, uk2 = (p[n] for n in ("qraw", "kraw", "iq", "ik", "uq2", "uk2"))
+    dQ = iq[..., None] * dQ - (iq * uq2 * (qraw * dQ).sum(-1))[..., None] * qraw
+    dK = ik[..., None] * dK - (ik * uk2 * (kraw * dK).sum(-1))[..., None] * kraw
     dAA, dRR = dA * A, dRq * Rq
     dw = (KdS * U).sum(-1)
     dlg = (dAA.sum(-1) - dAA.sum(-2) + dRR.sum(-1) - dRR.sum(-2)

@@ -187,26 +187,31 @@ def test_chunked_backward_equals_sequential_autograd(T, chunk, dk, dv):
         assert torch.allclose(a, b, rtol=1e-9, atol=1e-10), name
 
 
-@pytest.mark.parametrize("B,T,H,d,s0,dfinal", [(1, 150, 2, 64, True, True), (2, 64, 1, 128, False, True),
-                                               (1, 33, 3, 64, True, False)])
-def test_bwd16_restatements_vs_oracle(B, T, H, d, s0, dfinal):
+@pytest.mark.parametrize("B,T,H,d,s0,dfinal,l2norm", [(1, 150, 2, 64, True, True, True),
+                                                      (2, 64, 1, 128, False, True, True),
+                                                      (1, 33, 3, 64, True, False, False)])
+def test_bwd16_restatements_vs_oracle(B, T, H, d, s0, dfinal, l2norm):
     """The torch restatements of the three launches of the 16-bit chunked backward (prep:
-    chunk matrices and padding to 64-token chunks; chain: the state and state-gradient
-    chains; local: the chunk-local gradients), composed in fp32, against the oracle's
-    chunked backward in fp64, to 1e-4 of max|grad|.  The GPU tests hold each HIP launch
-    to its restatement."""
+    l2 norm and scale of the raw rows, chunk matrices and padding to 64-token chunks;
+    chain: the state and state-gradient chains; local: the chunk-local gradients taken
+    back through the l2 norm), composed in fp32, against the oracle's chunked backward in
+    fp64 with fp64 autograd of the l2 norm and scale, to 1e-4 of max|grad|.  The GPU tests
+    hold each HIP launch to its restatement."""
     from helpers import (CHAIN_TILES, bwd16_chain_reference, bwd16_local_reference, bwd16_prep_reference,
                          rel_err)
     g = torch.Generator().manual_seed(T + d)
     f32 = dict(dtype=torch.float32)
-    q = G.l2_normalize(torch.randn(B, T, H, d, generator=g, **f32)) * 0.7
-    k = G.l2_normalize(torch.randn(B, T, H, d, generator=g, **f32))
+    scale = 0.7
+    q = torch.randn(B, T, H, d, generator=g, **f32)
+    k = torch.randn(B, T, H, d, generator=g, **f32)
+    if not l2norm:   # keep the recurrence contractive
+        q, k = G.l2_normalize(q), G.l2_normalize(k)
     v, dO = torch.randn(B, T, H, d, generator=g, **f32), torch.randn(B, T, H, d, generator=g, **f32)
     gl = torch.nn.functional.logsigmoid(torch.randn(B, T, H, generator=g, **f32) + 2.0)
     beta = torch.sigmoid(torch.randn(B, T, H, generator=g, **f32))
     S0 = torch.randn(B, H, d, d, generator=g, **f32) * 0.3 if s0 else None
     dST = torch.randn(B, H, d, d, generator=g, **f32) if dfinal else None
-    prep = bwd16_prep_reference(q, k, v, gl, beta, dO, torch.float32)
+    prep = bwd16_prep_reference(q, k, v, gl, beta, dO, torch.float32, scale, l2norm)
     st = lambda x: None if x is None else x.reshape(B * H, d, d)  # noqa: E731
     s_entry, ds_end, u, dy, ds0 = bwd16_chain_reference(*(prep[n] for n in CHAIN_TILES), st(S0), st(dST))
     got = bwd16_local_reference(prep, s_entry, ds_end, u, dy) + (ds0.reshape(B, H, d, d),)
@@ -215,11 +220,14 @@ def test_bwd16_restatements_vs_oracle(B, T, H, d, s0, dfinal):
     for b in range(B):
         for h in range(H):
             z = torch.zeros(d, d)
+            qr_ = q[b, :, h].double().requires_grad_(True)
+            kr_ = k[b, :, h].double().requires_grad_(True)
+            qn, kn = (scale * G.l2_normalize(qr_), G.l2_normalize(kr_)) if l2norm else (scale * qr_, kr_)
             out = G.gated_delta_chunked_backward(
-                q[b, :, h].double(), k[b, :, h].double(), v[b, :, h].double(), gl[b, :, h].double(),
-                beta[b, :, h].double(), z if S0 is None else S0[b, h].double(), dO[b, :, h].double(),
-                z if dST is None else dST[b, h].double())
-            for r, o in zip(ref[:5], out[:5]):
+                qn.detach(), kn.detach(), v[b, :, h].double(), gl[b, :, h].double(), beta[b, :, h].double(),
+                z if S0 is None else S0[b, h].double(), dO[b, :, h].double(), z if dST is None else dST[b, h].double())
+            dq_raw, dk_raw = torch.autograd.grad((qn, kn), (qr_, kr_), (out[0], out[1]))
+            for r, o in zip(ref[:5], (dq_raw, dk_raw) + tuple(out[2:5])):
                 r[b, :, h] = o
             ref[5][b, h] = out[5]
     for name, a, r in zip(["dq", "dk", "dv", "dg", "dbeta", "dS0"], got, ref):
