@@ -634,15 +634,17 @@ def chunk_gated_delta_rule_op(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: 
 
 @torch.library.custom_op("atma_hip::gated_delta_fwd", mutates_args=())
 def gated_delta_fwd_op(q: Tensor, k: Tensor, v: Tensor, g: Tensor, beta: Tensor,
-                       initial_state: Optional[Tensor]) -> List[Tensor]:
-    """The recurrence forward of the autograd route on prepared fp32 operands (q scaled
-    and normalised, k normalised, log decay, beta): same kernels, no start flag, so it
-    mutates nothing and functionalises under torch.compile.  Returns [o, final state]."""
-    return _chunk_gated_delta(q, k, v, g, beta, initial_state, 1.0, False, True, None, 0, False, 0.0, 0.0)
+                       initial_state: Optional[Tensor], scale: float = 1.0,
+                       l2norm: bool = False) -> List[Tensor]:
+    """The recurrence forward of the autograd routes (log decay, beta; q and k as given,
+    l2-normalised in-kernel with ``l2norm``, q then times ``scale``): the prefill kernels
+    with no start flag, so it mutates nothing and functionalises under torch.compile.
+    Returns [o, final state]."""
+    return _chunk_gated_delta(q, k, v, g, beta, initial_state, scale, l2norm, True, None, 0, False, 0.0, 0.0)
 
 
 @gated_delta_fwd_op.register_fake
-def _(q, k, v, g, beta, initial_state):
+def _(q, k, v, g, beta, initial_state, scale=1.0, l2norm=False):
     B, T, H, dk = q.shape
     dv = v.shape[3]
     return [q.new_empty((B, T, H, dv)), q.new_empty((B, H, dk, dv), dtype=torch.float32)]

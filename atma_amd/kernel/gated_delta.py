@@ -161,7 +161,7 @@ class _GatedDelta16Fn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, g, beta, S0, scale, l2norm):
-        o, S = torch.ops.atma_hip.chunk_gated_delta_rule(q, k, v, g, beta, S0, scale, l2norm, True, None, 0)
+        o, S = torch.ops.atma_hip.gated_delta_fwd(q, k, v, g, beta, S0, scale, l2norm)
         ctx.save_for_backward(q, k, v, g, beta, S0)
         ctx.scale, ctx.l2norm = scale, l2norm
         return o, S

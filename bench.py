@@ -230,21 +230,25 @@ class Decode:
         # right behind itself waits for its previous launch to retire (about 8 us per
         # step on this runtime); alternating two execs keeps the queue fed, as the
         # engine's graph runner does
-        self.graphs = []
+        self.graphs, self.outs = [], []
         for _ in range(2):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                self.graph_out = self.step()   # (c, mag, r): rewritten by every replay
+                self.outs.append(self.step())   # (c, mag, r) of this exec: rewritten by its replays
             self.graphs.append(g)
         self.graph = self.graphs[0]
+        self.graph_out = self.outs[0]
         self.flip = 0
 
     def replay(self):
+        """Replay the next exec; graph_out is then its (c, mag, r)."""
         self.graphs[self.flip].replay()
+        self.graph_out = self.outs[self.flip]
         self.flip ^= 1
 
     def replay_one(self):
         self.graph.replay()
+        self.graph_out = self.outs[0]
 
     def bytes(self):
         kv = self.ctx_sum * HKV * D * 2 * 2
