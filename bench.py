@@ -16,8 +16,9 @@ a shuffled pool: the layer's fused decode route -- KV write + Polar decode + gat
 step in two launches -- replayed as a HIP graph; the three separate calls timed beside
 it), each with its roofline fraction; configs[4] (the 378M model served through the
 paged engine, 32 x 2,048-token prompts -> 256 greedy tokens: prefill / decode tok/s and
-wall time); configs[0] (one global block in fp32 on the GPU); plus the CPU oracle timed
-on this host (configs[1] sample and configs[0]).
+wall time); configs[0] (one global block in fp32 on the GPU); the training steps of the
+layer's two branches at the configs[1] shape (Polar and the gated-delta memory, forward +
+backward); plus the CPU oracle timed on this host (configs[1] sample and configs[0]).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1|c2|c3|c4|c5|ops|train|copy|cpu] [--no-cpu]
 """
@@ -317,25 +318,60 @@ def bench_inference_ops(torch, dev, steps, warmup):
     return res
 
 
-def bench_memory_train(torch, dev, steps, warmup):
-    """Training step of the memory branch at the configs[1] shape (B=8, T=2048, 8 heads,
-    d=128, bf16 q/k/v): chunk_gated_delta_rule forward (fp32 on normalised operands) and
-    its HIP backward (gated_delta_bwd), timed together with HIP events."""
+def bench_train(torch, dev, steps, warmup):
+    """Training steps of the global layer's two branches at the configs[1] shape (B=8,
+    T=2048, 8 / 2 heads, d=128, bf16), each forward + backward (the gradients of every
+    input and parameter), timed with HIP events.
+
+    Memory branch: chunk_gated_delta_rule on raw q / k (l2 norm in-kernel), log decay and
+    beta leaves: the 16-bit chunked forward, then the chunked (WY) backward's three
+    launches.  Polar: polar_attention forward with saved statistics, then the backward
+    (preamble, dq and dk / dv loops, parameter sums); its matmul FLOPs are the forward's
+    plus the backward's 7 products of 2 d per causal pair (polar_bwd_flops), and the
+    backward alone is the step minus the forward with statistics."""
     from atma_amd.kernel import chunk_gated_delta_rule
+    from atma_amd.kernel.polar_train import polar_attention, polar_bwd_flops
     B, T = 8, 2048
     g = torch.Generator(device=dev).manual_seed(0)
-    q, k, v = (torch.randn(B, T, HQ, D, device=dev, generator=g, dtype=torch.bfloat16).requires_grad_(True)
-               for _ in range(3))
+    bf = dict(device=dev, dtype=torch.bfloat16)
+    q, k, v = (torch.randn(B, T, HQ, D, generator=g, **bf).requires_grad_(True) for _ in range(3))
     gl = torch.nn.functional.logsigmoid(torch.randn(B, T, HQ, device=dev, generator=g) + 3.9).requires_grad_(True)
     beta = torch.sigmoid(torch.randn(B, T, HQ, device=dev, generator=g)).requires_grad_(True)
-    dO = torch.randn(B, T, HQ, D, device=dev, generator=g, dtype=torch.bfloat16)
+    dO = torch.randn(B, T, HQ, D, generator=g, **bf)
 
-    def step():
+    def mem_step():
         o, _ = chunk_gated_delta_rule(q, k, v, gl, beta, scale=1.0, use_qk_l2norm_in_kernel=True)
         torch.autograd.grad(o, (q, k, v, gl, beta), dO)
 
-    ms = _time(torch, step, steps, warmup)
-    return dict(B=B, T=T, ms_fwd_bwd=ms)
+    pq = torch.randn(B, HQ, T, D, generator=g, **bf).requires_grad_(True)
+    pk, pv = (torch.randn(B, HKV, T, D, generator=g, **bf).requires_grad_(True) for _ in range(2))
+    prm = {n: t.clone().requires_grad_(True) for n, t in _params(torch, dev).items()}
+    n_keys = torch.arange(1, T + 1, device=dev, dtype=torch.float32)
+    dc = torch.randn(B, HQ, T, D, generator=g, **bf)
+    dm = torch.randn(B, HQ, T, generator=g, **bf)
+
+    def polar_step():
+        c, mag = polar_attention(pq, pk, pv, n_keys, is_causal=True, **prm)
+        torch.autograd.grad((c, mag), (pq, pk, pv, *prm.values()), (dc, dm))
+
+    def polar_fwd():
+        with torch.no_grad():
+            p = [t.detach() for t in prm.values()]
+            torch.ops.atma_hip.polar_attention_fwd_train(pq.detach(), pk.detach(), pv.detach(), n_keys, *p,
+                                                         1e-6, True, 0, False)
+
+    _time(torch, mem_step, 10, 2)
+    ms_mem = _time(torch, mem_step, steps, warmup)
+    _time(torch, polar_step, 5, 1)
+    ms_polar = _time(torch, polar_step, steps, warmup)
+    ms_pfwd = _time(torch, polar_fwd, steps, warmup)
+    f_fwd = 4.0 * B * HQ * D * T * (T + 1) / 2.0
+    f_bwd = float(polar_bwd_flops(B, HQ, T, D))
+    ms_pbwd = ms_polar - ms_pfwd
+    return dict(B=B, T=T, memory_ms_fwd_bwd=ms_mem, polar_ms_fwd_bwd=ms_polar, polar_ms_fwd=ms_pfwd,
+                polar_ms_bwd=ms_pbwd, polar_bwd_tflops=f_bwd / ms_pbwd / 1e9,
+                polar_bwd_mfma_frac=f_bwd / ms_pbwd / 1e9 / PEAK_BF16_TFLOPS,
+                polar_step_tflops=(f_fwd + f_bwd) / ms_polar / 1e9)
 
 
 def c1_state(torch, seed=0):
@@ -546,8 +582,10 @@ def main(argv=None):
         c4w = bench_decode(torch, dev, max(5, args.steps // 2), 2, full=True)
         print(f"# c4 decode 64x32768: {json.dumps(c4w)}", file=sys.stderr, flush=True)
         out["c4"] = [c4, c4w]
-    if args.only == "train":
-        out["train"] = bench_memory_train(torch, dev, max(3, args.steps // 4), 2)
+    if args.only in (None, "train"):
+        tr = bench_train(torch, dev, max(5, args.steps // 2), 2)
+        print(f"# train c2: {json.dumps(tr)}", file=sys.stderr, flush=True)
+        out["train"] = tr
     if args.only in (None, "c5"):
         c5 = bench_c5(torch, dev)
         print(f"# c5 served 378M: {json.dumps(c5)}", file=sys.stderr, flush=True)
@@ -594,6 +632,7 @@ def main(argv=None):
                           for n, r in out["ops"].items()},
         "block_c1_gpu": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out["c1"].items()},
         "serve_c5": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out["c5"].items()},
+        "train_c2": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out["train"].items()},
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch)
