@@ -112,8 +112,9 @@ def polar_attention_bwd_prep_op(gc: Optional[Tensor], gm: Optional[Tensor], S: T
     lib = _lib.load()
     B, H, T, d = S.shape
     f = dict(device=S.device, dtype=torch.float32)
-    gc = None if gc is None else gc.to(dtype).contiguous()
+    gc = None if gc is None else _rows16(gc.to(dtype).contiguous())
     gm = None if gm is None else gm.to(dtype).contiguous()
+    S, v_null = _rows16(S.contiguous()), _rows16(v_null.contiguous())
     gs = torch.empty((B, H, T, d), device=S.device, dtype=dtype)
     gL = torch.empty((B, H, T), **f)
     gQ2 = torch.empty((B, H, T), **f)
@@ -141,7 +142,9 @@ def _(gc, gm, S, M, L, Q2, n_keys, v_null, null_base, null_slope_raw, len_gain_r
 def polar_attention_bwd_op(q: Tensor, k: Tensor, v: Tensor, gs: Tensor, gL: Tensor, gQ2: Tensor,
                            M: Tensor, temp: Tensor, n_keys: Tensor, is_causal: bool,
                            window: int) -> List[Tensor]:
-    """The O(T^2) part of the backward: returns dq, dk, dv in q's dtype and dt in fp32."""
+    """The O(T^2) part of the backward: returns dq in q's dtype, dt in fp32 and dkv
+    (2, B, Hkv, Tk, d) in q's dtype (dk = dkv[0], dv = dkv[1]: one group-sum launch writes
+    both)."""
     _need_cuda(q, k, v, gs, gL, gQ2, M, temp, n_keys)
     lib = _lib.load()
     q, k, v, gs = _rows16(q), _rows16(k), _rows16(v), _rows16(gs)
@@ -151,8 +154,8 @@ def polar_attention_bwd_op(q: Tensor, k: Tensor, v: Tensor, gs: Tensor, gL: Tens
     new = torch.empty if Tk > 0 else torch.zeros   # with no keys nothing is written
     dq = new((B, Hq, Tq, d), **f)
     dt = new((B, Hq, Tq), **f)
-    dk = new((B, Hq, Tk, d), **f)   # each query head's share; the group sum follows
-    dv = new((B, Hq, Tk, d), **f)
+    dkv = new((2, B, Hq, Tk, d), **f)   # each query head's share of dk, dv; the group sum follows
+    dk, dv = dkv[0], dkv[1]   # the kernel's two outputs
     gL, gQ2, M, temp = (t.to(torch.float32).contiguous() for t in (gL, gQ2, M, temp))
     rc = lib.atma_polar_attention_bwd(
         q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
@@ -166,10 +169,9 @@ def polar_attention_bwd_op(q: Tensor, k: Tensor, v: Tensor, gs: Tensor, gL: Tens
     # dq in q's dtype; dk / dv: the group's shares summed (fixed order) into k's dtype
     if q.dtype != torch.float32:
         dq = _group_sum(lib, dq, 1, B * Hq * Tq * d, 1, q.dtype)
-    if Hkv != Hq or q.dtype != torch.float32:
-        dk = _group_sum(lib, dk, B * Hkv, Tk * d, Hq // Hkv, q.dtype).view(B, Hkv, Tk, d)
-        dv = _group_sum(lib, dv, B * Hkv, Tk * d, Hq // Hkv, q.dtype).view(B, Hkv, Tk, d)
-    return [dq, dt, dk, dv]
+    if Hkv != Hq or q.dtype != torch.float32:   # dk and dv in one launch
+        dkv = _group_sum(lib, dkv, 2 * B * Hkv, Tk * d, Hq // Hkv, q.dtype).view(2, B, Hkv, Tk, d)
+    return [dq, dt, dkv]
 
 
 def _group_sum(lib, part, n_groups, elems, G, dtype):
@@ -181,12 +183,46 @@ def _group_sum(lib, part, n_groups, elems, G, dtype):
     return out.view(part.shape) if G == 1 else out
 
 
+@torch.library.custom_op("atma_hip::polar_bwd_param_grads", mutates_args=())
+def polar_bwd_param_grads_op(part: Tensor, dt: Tensor, n_keys: Tensor, len_gain_raw: Tensor,
+                             null_slope_raw: Tensor, mag_beta_raw: Tensor, window: int,
+                             preserve_length: bool) -> List[Tensor]:
+    """The Polar parameters' gradients from the preamble's block sums (B * ceil(T / 16), H,
+    d + 4) and dt (B, H, T): returns [g_v_null (H, d), g (4, H) = null_base, null_slope_raw,
+    len_gain_raw, mag_beta_raw], fp32."""
+    _need_cuda(part, dt, n_keys, len_gain_raw, null_slope_raw, mag_beta_raw)
+    lib = _lib.load()
+    B, H, T = dt.shape
+    d = part.shape[-1] - 4
+    if part.dim() != 3 or part.shape[0] != B * ((T + 15) // 16) or part.shape[1] != H:
+        raise ValueError("polar_bwd_param_grads: part must be (B * ceil(T / 16), H, d + 4)")
+    f = dict(device=dt.device, dtype=torch.float32)
+    part, dt, n_keys = part.contiguous(), dt.contiguous(), n_keys.to(torch.float32).contiguous()
+    lg, ns, mb = (t.to(torch.float32).contiguous() for t in (len_gain_raw, null_slope_raw, mag_beta_raw))
+    gv = torch.empty((H, d), **f)
+    g4 = torch.empty((4, H), **f)
+    ws_bytes = lib.atma_polar_bwd_param_grads_workspace_bytes(H, d)
+    ws = torch.empty((ws_bytes // 4,), **f)
+    rc = lib.atma_polar_bwd_param_grads(part.data_ptr(), dt.data_ptr(), n_keys.data_ptr(), lg.data_ptr(),
+                                        ns.data_ptr(), mb.data_ptr(), gv.data_ptr(), g4.data_ptr(), B, H, T, d,
+                                        window, 1 if preserve_length else 0, ws.data_ptr(), ws_bytes,
+                                        _lib.stream_handle(dt.device))
+    _lib.check(rc, "polar_bwd_param_grads")
+    return [gv, g4]
+
+
+@polar_bwd_param_grads_op.register_fake
+def _(part, dt, n_keys, len_gain_raw, null_slope_raw, mag_beta_raw, window, preserve_length):
+    B, H, T = dt.shape
+    return [dt.new_empty((H, part.shape[-1] - 4)), dt.new_empty((4, H))]
+
+
 @polar_attention_bwd_op.register_fake
 def _(q, k, v, gs, gL, gQ2, M, temp, n_keys, is_causal, window):
     B, Hq, Tq, d = q.shape
     Hkv, Tk = k.shape[1], k.shape[2]
     return [q.new_empty((B, Hq, Tq, d)), q.new_empty((B, Hq, Tq), dtype=torch.float32),
-            q.new_empty((B, Hkv, Tk, d)), q.new_empty((B, Hkv, Tk, d))]
+            q.new_empty((2, B, Hkv, Tk, d))]
 
 
 # --------------------------------------------------------------------------- Polar packed fwd

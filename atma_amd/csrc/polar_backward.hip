@@ -384,18 +384,428 @@ __global__ void __launch_bounds__(256) polar_bwd_dkdv_kernel(PolarBwdArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// 16-bit loops.  Both compute the score tile transposed relative to the output they
+// accumulate, so the elementwise results (dS, P) are already the B operand of the second
+// products and never go through LDS:
+//  * dq: S^T = K Q^T, dP^T = V gs^T (rows = keys, columns = the wave's 16 queries), then
+//    dQ^T += K^T dS^T with K^T fragments from transposing LDS reads;
+//  * dk/dv: S = Q K^T, dP = gs V^T (rows = queries, columns = the wave's 16 keys), then
+//    dV^T += gs^T P and dK^T += Q^T dS with gs^T / Q^T from transposing reads.
+// A 32-wide contraction over keys (or queries) takes them in the order the accumulator
+// tiles hold them: lane group g's 8 values are rows 32 j + 4 g + [0, 4) of tile 2 j and
+// 32 j + 16 + 4 g + [0, 4) of tile 2 j + 1; the transposing reads fetch the A operand in the
+// same order.  Shared tiles use unpadded rows with 16-byte chunk c of row r stored at
+// c ^ f(r), f(r) = 2 (r mod 8) + (r / 8 mod 2) for 128-element rows: f is a bijection on
+// 16 rows (row-fragment reads: 16 rows x one chunk hit 16 distinct positions) and 2 (r mod 8)
+// is distinct on the 8 rows a half wave's transposing reads touch (two adjacent chunks per
+// row), so both read patterns are free of bank conflicts.  Blocks whose every (key, query)
+// pair is valid skip the mask.
+template <int CPR>
+__device__ __forceinline__ int bw_swz(int r) {
+  if constexpr (CPR == 16) return 2 * (r & 7) + ((r >> 3) & 1);
+  else return lds_swizzle<CPR>(r);
+}
+template <int D>
+__device__ __forceinline__ int bw_off(int r, int e) {  // element e of row r (e % 8 < 8)
+  return r * D + 8 * ((e >> 3) ^ bw_swz<D / 8>(r)) + (e & 7);
+}
+template <typename T, int D>
+__device__ __forceinline__ void bw_put_swz(T* dst, const BwTile<T, D>& t, int tid) {
+  using TT = BwTile<T, D>;
+#pragma unroll
+  for (int i = 0; i < TT::N; ++i) {
+    const int c = tid + 256 * i, r = c / TT::CPR, e = (c % TT::CPR) * TT::EPC;
+    *(u32x4*)(dst + bw_off<D>(r, e)) = t.x[i];
+  }
+}
+// A fragment: rows r0 + lane % 16 of a swizzled tile, k = k0 + 8 (lane / 16) .. + 7
+template <int D, typename T>
+__device__ __forceinline__ u32x4 bw_rows_swz(const T* tile, int r0, int k0, int lane) {
+  return *(const u32x4*)(tile + bw_off<D>(r0 + (lane & 15), k0 + 8 * (lane >> 4)));
+}
+// A fragment of the transposed tile: lane (g, i) holds column n0 + i at rows
+// 32 j + 4 g + [0, 4) and 32 j + 16 + 4 g + [0, 4) (the accumulator-tile order)
+template <int D, typename T>
+__device__ __forceinline__ u32x4 bw_tcols_swz(const T* tile, int j, int n0, int lane) {
+  const int g = lane >> 4, i = lane & 15;
+  const int r = 32 * j + 4 * g + (i >> 2), e = n0 + 4 * (i & 3);
+  const u32x2 lo = lds_read_tr16(tile + bw_off<D>(r, e)), hi = lds_read_tr16(tile + bw_off<D>(r + 16, e));
+  return u32x4{lo[0], lo[1], hi[0], hi[1]};
+}
+// B fragment of the accumulator tiles 2 j, 2 j + 1, rounded to 16 bits
+template <typename T>
+__device__ __forceinline__ u32x4 bw_pack_b(const f32x4& lo, const f32x4& hi) {
+  return u32x4{pack2<T>(lo[0], lo[1]), pack2<T>(lo[2], lo[3]), pack2<T>(hi[0], hi[1]), pack2<T>(hi[2], hi[3])};
+}
+__device__ __forceinline__ float bw_uniform(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
+}
+__device__ __forceinline__ float bw_lane(float x, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+
+// dq, dt for 16-bit inputs: workgroup = (b * Hq + hq, 64-row query tile, last tile first)
+template <typename T, int D>
+__global__ void __launch_bounds__(256, 2) polar_bwd16_dq_kernel(PolarBwdArgs a) {
+  constexpr int BM = 64, BN = 64, KS = D / 32, CPR = D / 8, NDMA = CPR / 4;
+  // double-buffered key blocks, filled by direct-to-LDS copies one block ahead
+  __shared__ __attribute__((aligned(16))) T Ks[2][BN * D];
+  __shared__ __attribute__((aligned(16))) T Vs[2][BN * D];
+
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = a.Hq / a.Hkv;
+  const int bh = blockIdx.x, b = bh / a.Hq, hq = bh % a.Hq, hk = hq / G;
+  const int q0 = ((int)gridDim.y - 1 - (int)blockIdx.y) * BM, r0 = q0 + 16 * wave;
+  const T* qp = (const T*)a.q + b * a.q_sb + hq * a.q_sh;
+  const T* gp = (const T*)a.gs + b * a.g_sb + hq * a.g_sh;
+  const T* kp = (const T*)a.k + b * a.k_sb + hk * a.k_sh;
+  const T* vp = (const T*)a.v + b * a.v_sb + hk * a.v_sh;
+
+  // the wave's 16 query rows as B operands; the lane's query is row r0 + c16
+  u32x4 qf[KS], gf[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    qf[s] = bw_global_rows<T>(qp, a.q_st, r0, a.Tq, 32 * s, lane);
+    gf[s] = bw_global_rows<T>(gp, a.g_st, r0, a.Tq, 32 * s, lane);
+  }
+  const int row = r0 + c16;
+  const bool rok = row < a.Tq;
+  const int64_t ri = (int64_t)bh * a.Tq + row;
+  const float tp = rok ? a.temp[(int64_t)hq * a.Tq + row] : 1.f;
+  const float c1 = a.scale * tp * kLog2e;
+  const float nm2 = rok ? -a.M[ri] * kLog2e : 0.f;
+  const float gl = rok ? a.gL[ri] : 0.f;
+  const float g2 = rok ? 2.f * a.gQ2[ri] : 0.f;
+  const float nr = rok ? a.n_keys[row] : 0.f;  // no valid key for rows past Tq
+  const float nmin = bw_uniform(-row16_max(-nr)), nmax = bw_uniform(row16_max(nr));
+
+  f32x4 dqT[D / 16];
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t) dqT[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float dt = 0.f;
+
+  const int hi = a.is_causal ? min(q0 + BM, a.Tk) : a.Tk;
+  const int lo = a.window > 0 ? (max(q0 - a.window, 0) / BN) * BN : 0;
+  // the (b, hk) slices of k and v as buffers: rows past Tk read as zeros; copy k of wave w
+  // fills LDS chunks (NDMA w + k) 64 + lane (row chunk / CPR, stored position chunk % CPR,
+  // loaded from global chunk position ^ f(row))
+  const auto krs = buffer_rsrc(kp, (uint32_t)((int64_t)a.Tk * a.k_st * 2));
+  const auto vrs = buffer_rsrc(vp, (uint32_t)((int64_t)a.Tk * a.v_st * 2));
+  uint32_t koff[NDMA], voff[NDMA];
+#pragma unroll
+  for (int k = 0; k < NDMA; ++k) {
+    const int q = (NDMA * wave + k) * 64 + lane, r = q / CPR, c = (q % CPR) ^ bw_swz<CPR>(r);
+    koff[k] = (uint32_t)((r * a.k_st + 8 * c) * 2);
+    voff[k] = (uint32_t)((r * a.v_st + 8 * c) * 2);
+  }
+  auto dma_block = [&](int k0, int buf) {
+    const uint32_t kb = (uint32_t)((int64_t)k0 * a.k_st * 2), vb = (uint32_t)((int64_t)k0 * a.v_st * 2);
+#pragma unroll
+    for (int k = 0; k < NDMA; ++k) {
+      dma_buf16(krs, koff[k] + kb, 0, &Ks[buf][(NDMA * wave + k) * 64 * 8]);
+      dma_buf16(vrs, voff[k] + vb, 0, &Vs[buf][(NDMA * wave + k) * 64 * 8]);
+    }
+  };
+  if (lo < hi) dma_block(lo, 0);
+  int cur = 0;
+  for (int k0 = lo; k0 < hi; k0 += BN) {
+    wait_vmcnt<0>();  // this wave's copies of block k0 (and every earlier load) are done
+    __syncthreads();  // ... and every wave's; buffer cur ^ 1 is no longer read
+    if (k0 + BN < hi) dma_block(k0 + BN, cur ^ 1);
+    const T* Kc = Ks[cur];
+    const T* Vc = Vs[cur];
+    cur ^= 1;
+    // S^T = K Q^T, dP^T = V gs^T: tile t holds keys k0 + 16 t + 4 g + i, query row
+    f32x4 st[4], pt[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      u32x4 ka[KS], va[KS];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        ka[s] = bw_rows_swz<D>(Kc, 16 * t, 32 * s, lane);
+        va[s] = bw_rows_swz<D>(Vc, 16 * t, 32 * s, lane);
+      }
+      st[t] = pt[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        st[t] = mfma16x16x32<T>(ka[s], qf[s], st[t]);
+        pt[t] = mfma16x16x32<T>(va[s], gf[s], pt[t]);
+      }
+    }
+    const bool full = k0 + BN <= a.Tk && (float)(k0 + BN - 1) < nmin &&
+                      (a.window <= 0 || (float)k0 >= nmax - (float)a.window);
+    f32x4 ds[4];
+    if (full) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pr = __builtin_amdgcn_exp2f(fmaf(st[t][i], c1, nm2));
+          const float da = fmaf(g2, pr, pt[t][i] + gl) * pr;
+          dt = fmaf(da, st[t][i], dt);
+          ds[t][i] = da * tp;
+        }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = k0 + 16 * t + 4 * g + i;
+          const float kf = (float)key;
+          const bool valid = key < a.Tk && kf < nr && (a.window <= 0 || kf >= nr - (float)a.window);
+          const float pr = valid ? __builtin_amdgcn_exp2f(fmaf(st[t][i], c1, nm2)) : 0.f;
+          const float da = valid ? fmaf(g2, pr, pt[t][i] + gl) * pr : 0.f;
+          dt = fmaf(da, st[t][i], dt);
+          ds[t][i] = da * tp;
+        }
+    }
+    // dQ^T += K^T dS^T
+    const u32x4 b0 = bw_pack_b<T>(ds[0], ds[1]), b1 = bw_pack_b<T>(ds[2], ds[3]);
+#pragma unroll
+    for (int nt = 0; nt < D / 16; nt += 4) {
+      u32x4 ka[4][2];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) ka[u][j] = bw_tcols_swz<D>(Kc, j, 16 * (nt + u), lane);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        dqT[nt + u] = mfma16x16x32<T>(ka[u][0], b0, dqT[nt + u]);
+        dqT[nt + u] = mfma16x16x32<T>(ka[u][1], b1, dqT[nt + u]);
+      }
+    }
+  }
+
+  dt += __shfl_xor(dt, 16, 64);
+  dt += __shfl_xor(dt, 32, 64);
+  if (rok) {
+    float* out = a.dq + ri * D + 4 * g;
+#pragma unroll
+    for (int nt = 0; nt < D / 16; ++nt) *(f32x4*)(out + 16 * nt) = dqT[nt] * a.scale;
+    if (g == 0) a.dt[ri] = dt * a.scale;
+  }
+}
+
+// dk, dv for 16-bit inputs: workgroup = (b * Hq + hq, 64-key tile); writes hq's slice of
+// (B, Hq, Tk, D)
+template <typename T, int D>
+__global__ void __launch_bounds__(256, 2) polar_bwd16_dkdv_kernel(PolarBwdArgs a) {
+  constexpr int BK = 64, BQ = 64, KS = D / 32, CPR = D / 8, NDMA = CPR / 4;
+  // double-buffered query blocks, filled by direct-to-LDS copies one block ahead
+  __shared__ __attribute__((aligned(16))) T Qs[2][BQ * D];
+  __shared__ __attribute__((aligned(16))) T Gs[2][BQ * D];
+  __shared__ __attribute__((aligned(16))) float s_c1[2][BQ];
+  __shared__ __attribute__((aligned(16))) float s_nm2[2][BQ];
+  __shared__ __attribute__((aligned(16))) float s_gl[2][BQ];
+  __shared__ __attribute__((aligned(16))) float s_g2[2][BQ];
+  __shared__ __attribute__((aligned(16))) float s_nr[2][BQ];
+  __shared__ __attribute__((aligned(16))) float s_tp[2][BQ];
+  __shared__ float s_lim[2][2];
+
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = a.Hq / a.Hkv;
+  const int bh = blockIdx.x, b = bh / a.Hq, hq = bh % a.Hq, hk = hq / G;
+  const int k0 = blockIdx.y * BK, kr0 = k0 + 16 * wave;
+  const T* kp = (const T*)a.k + b * a.k_sb + hk * a.k_sh;
+  const T* vp = (const T*)a.v + b * a.v_sb + hk * a.v_sh;
+  const T* qp = (const T*)a.q + b * a.q_sb + hq * a.q_sh;
+  const T* gp = (const T*)a.gs + b * a.g_sb + hq * a.g_sh;
+  // the (b, hq) slices of q and gs as buffers: rows past Tq read as zeros
+  const auto qrs = buffer_rsrc(qp, (uint32_t)((int64_t)a.Tq * a.q_st * 2));
+  const auto grs = buffer_rsrc(gp, (uint32_t)((int64_t)a.Tq * a.g_st * 2));
+  // copy k of wave w fills LDS chunks (NDMA w + k) 64 + lane: row r = chunk / CPR, stored
+  // position chunk % CPR, so it loads global chunk position ^ f(r)
+  uint32_t qoff[NDMA], goff[NDMA];
+#pragma unroll
+  for (int k = 0; k < NDMA; ++k) {
+    const int q = (NDMA * wave + k) * 64 + lane, r = q / CPR, c = (q % CPR) ^ bw_swz<CPR>(r);
+    qoff[k] = (uint32_t)((r * a.q_st + 8 * c) * 2);
+    goff[k] = (uint32_t)((r * a.g_st + 8 * c) * 2);
+  }
+  auto dma_block = [&](int q0, int buf) {
+    const uint32_t qb = (uint32_t)((int64_t)q0 * a.q_st * 2), gb = (uint32_t)((int64_t)q0 * a.g_st * 2);
+#pragma unroll
+    for (int k = 0; k < NDMA; ++k) {
+      dma_buf16(qrs, qoff[k] + qb, 0, &Qs[buf][(NDMA * wave + k) * 64 * 8]);
+      dma_buf16(grs, goff[k] + gb, 0, &Gs[buf][(NDMA * wave + k) * 64 * 8]);
+    }
+  };
+
+  // the wave's 16 keys as B operands; the lane's key is kr0 + c16
+  u32x4 kf[KS], vf[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    kf[s] = bw_global_rows<T>(kp, a.k_st, kr0, a.Tk, 32 * s, lane);
+    vf[s] = bw_global_rows<T>(vp, a.v_st, kr0, a.Tk, 32 * s, lane);
+  }
+  const int key = kr0 + c16;
+  const float keyf = (float)key;
+  f32x4 dkT[D / 16], dvT[D / 16];
+#pragma unroll
+  for (int t = 0; t < D / 16; ++t) dkT[t] = dvT[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int lo = a.is_causal ? (k0 / BQ) * BQ : 0;
+  const int hi = a.window > 0 ? min(k0 + BK + a.window, a.Tq) : a.Tq;
+  // per-query scalars of a block, wave 0 (one query per lane), into buffer buf
+  float n_tp = 1.f, n_m = 0.f, n_gl = 0.f, n_gq2 = 0.f, n_nr = 0.f;
+  auto row_vals = [&](int q0) {
+    const int row = q0 + lane;
+    const bool ok = row < a.Tq;
+    const int64_t i = (int64_t)bh * a.Tq + row;
+    n_tp = ok ? a.temp[(int64_t)hq * a.Tq + row] : 1.f;
+    n_m = ok ? a.M[i] : 0.f;
+    n_gl = ok ? a.gL[i] : 0.f;
+    n_gq2 = ok ? a.gQ2[i] : 0.f;
+    n_nr = ok ? a.n_keys[row] : 0.f;  // no valid key for rows past Tq
+  };
+  auto put_vals = [&](int buf) {
+    s_tp[buf][lane] = n_tp;
+    s_c1[buf][lane] = a.scale * n_tp * kLog2e;
+    s_nm2[buf][lane] = -n_m * kLog2e;
+    s_gl[buf][lane] = n_gl;
+    s_g2[buf][lane] = 2.f * n_gq2;
+    s_nr[buf][lane] = n_nr;
+    // min / max of the block's key counts: DPP within rows of 16, then the four rows
+    float mn = -row16_max(-n_nr), mx = row16_max(n_nr);
+    mn = fminf(fminf(bw_lane(mn, 0), bw_lane(mn, 16)), fminf(bw_lane(mn, 32), bw_lane(mn, 48)));
+    mx = fmaxf(fmaxf(bw_lane(mx, 0), bw_lane(mx, 16)), fmaxf(bw_lane(mx, 32), bw_lane(mx, 48)));
+    if (lane == 0) {
+      s_lim[buf][0] = mn;
+      s_lim[buf][1] = mx;
+    }
+  };
+  if (lo < hi) {
+    dma_block(lo, 0);
+    if (wave == 0) {
+      row_vals(lo);
+      put_vals(0);
+    }
+  }
+  int cur = 0;
+  for (int q0 = lo; q0 < hi; q0 += BQ) {
+    wait_vmcnt<0>();  // this wave's copies of block q0 (and every earlier load) are done
+    __syncthreads();  // ... and every wave's; buffer cur ^ 1 is no longer read
+    const bool more = q0 + BQ < hi;
+    if (more) {
+      dma_block(q0 + BQ, cur ^ 1);
+      if (wave == 0) row_vals(q0 + BQ);
+    }
+    const T* Qc = Qs[cur];
+    const T* Gc = Gs[cur];
+    const float nmin = s_lim[cur][0], nmax = s_lim[cur][1];
+    const bool full = kr0 + 16 <= a.Tk && (float)(kr0 + 15) < nmin &&
+                      (a.window <= 0 || (float)kr0 >= nmax - (float)a.window);
+    // two query halves of 32: S and dP of tiles 2 j, 2 j + 1 (each tile's operands read
+    // before its products are issued), the elementwise gradient, then P and dS packed as
+    // the B operands of half j
+    u32x4 pb[2], db[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      f32x4 sq[2], pq[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int t = 2 * j + u;
+        u32x4 qa[KS], ga[KS];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          qa[s] = bw_rows_swz<D>(Qc, 16 * t, 32 * s, lane);
+          ga[s] = bw_rows_swz<D>(Gc, 16 * t, 32 * s, lane);
+        }
+        sq[u] = pq[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          sq[u] = mfma16x16x32<T>(qa[s], kf[s], sq[u]);
+          pq[u] = mfma16x16x32<T>(ga[s], vf[s], pq[u]);
+        }
+      }
+      // S element (query q0 + 16 t + 4 g + i, the lane's key)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int qb = 16 * (2 * j + u) + 4 * g;
+        const f32x4 c1 = *(const f32x4*)(s_c1[cur] + qb), nm2 = *(const f32x4*)(s_nm2[cur] + qb);
+        const f32x4 gl = *(const f32x4*)(s_gl[cur] + qb), g2 = *(const f32x4*)(s_g2[cur] + qb);
+        const f32x4 tp = *(const f32x4*)(s_tp[cur] + qb);
+        if (full) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(sq[u][i], c1[i], nm2[i]));
+            pq[u][i] = fmaf(g2[i], p, pq[u][i] + gl[i]) * p * tp[i];
+            sq[u][i] = p;
+          }
+        } else {
+          const f32x4 nr = *(const f32x4*)(s_nr[cur] + qb);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool valid = (key < a.Tk) & (keyf < nr[i]) & ((a.window <= 0) | (keyf >= nr[i] - (float)a.window));
+            const float p = valid ? __builtin_amdgcn_exp2f(fmaf(sq[u][i], c1[i], nm2[i])) : 0.f;
+            pq[u][i] = valid ? fmaf(g2[i], p, pq[u][i] + gl[i]) * p * tp[i] : 0.f;
+            sq[u][i] = p;
+          }
+        }
+      }
+      pb[j] = bw_pack_b<T>(sq[0], sq[1]);
+      db[j] = bw_pack_b<T>(pq[0], pq[1]);
+    }
+    // dV^T += gs^T P, dK^T += Q^T dS
+#pragma unroll
+    for (int nt = 0; nt < D / 16; ++nt) {
+      u32x4 ga[2], qa[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        ga[j] = bw_tcols_swz<D>(Gc, j, 16 * nt, lane);
+        qa[j] = bw_tcols_swz<D>(Qc, j, 16 * nt, lane);
+      }
+      dvT[nt] = mfma16x16x32<T>(ga[0], pb[0], dvT[nt]);
+      dkT[nt] = mfma16x16x32<T>(qa[0], db[0], dkT[nt]);
+      dvT[nt] = mfma16x16x32<T>(ga[1], pb[1], dvT[nt]);
+      dkT[nt] = mfma16x16x32<T>(qa[1], db[1], dkT[nt]);
+    }
+    if (more && wave == 0) put_vals(cur ^ 1);
+    cur ^= 1;
+  }
+
+  if (key < a.Tk) {
+    const int64_t base = ((int64_t)bh * a.Tk + key) * D + 4 * g;
+#pragma unroll
+    for (int nt = 0; nt < D / 16; ++nt) {
+      *(f32x4*)(a.dk + base + 16 * nt) = dkT[nt] * a.scale;
+      *(f32x4*)(a.dv + base + 16 * nt) = dvT[nt];
+    }
+  }
+}
+
 template <typename T, int D>
 static int launch_bwd(const PolarBwdArgs& a, hipStream_t s) {
-  polar_bwd_dq_kernel<T, D><<<dim3((unsigned)(a.B * a.Hq), (unsigned)((a.Tq + 63) / 64)), dim3(256), 0, s>>>(a);
+  const dim3 gq((unsigned)(a.B * a.Hq), (unsigned)((a.Tq + 63) / 64));
+  const dim3 gk((unsigned)(a.B * a.Hq), (unsigned)((a.Tk + 63) / 64));
+  // the 16-bit loops address a (b, head) slice of k / v (dq) or q / gs (dk/dv) through a
+  // 32-bit buffer range; larger slices take the register-staged loops
+  constexpr int64_t kMax = 1ll << 32;
+  const bool kv_fits = (int64_t)a.Tk * a.k_st * 2 < kMax && (int64_t)a.Tk * a.v_st * 2 < kMax;
+  const bool qg_fits = (int64_t)a.Tq * a.q_st * 2 < kMax && (int64_t)a.Tq * a.g_st * 2 < kMax;
+  if constexpr (sizeof(T) == 2) {
+    if (kv_fits) polar_bwd16_dq_kernel<T, D><<<gq, dim3(256), 0, s>>>(a);
+    else polar_bwd_dq_kernel<T, D><<<gq, dim3(256), 0, s>>>(a);
+  } else {
+    polar_bwd_dq_kernel<T, D><<<gq, dim3(256), 0, s>>>(a);
+  }
   int rc = check_launch("polar_attention_bwd(dq)");
   if (rc) return rc;
-  polar_bwd_dkdv_kernel<T, D><<<dim3((unsigned)(a.B * a.Hq), (unsigned)((a.Tk + 63) / 64)), dim3(256), 0, s>>>(a);
+  if constexpr (sizeof(T) == 2) {
+    if (qg_fits) polar_bwd16_dkdv_kernel<T, D><<<gk, dim3(256), 0, s>>>(a);
+    else polar_bwd_dkdv_kernel<T, D><<<gk, dim3(256), 0, s>>>(a);
+  } else {
+    polar_bwd_dkdv_kernel<T, D><<<gk, dim3(256), 0, s>>>(a);
+  }
   return check_launch("polar_attention_bwd(dkdv)");
 }
 
 // ---------------------------------------------------------------------------------------
 // Per-query preamble and parameter-gradient partial sums (kernel/polar_triton.py:1049-1155).
-// One wave per query row (4 rows per wave, 16 per workgroup): the row's direction
+// Four query rows per wave (one per 16 lanes), 16 per workgroup: the row's direction
 // cotangent gs = (gc - (gc.c) c) / max(|s|, eps) with c = s / max(|s|, eps), the
 // magnitude path's cotangents of L and Q2 through m_eff = L^3 / (Q2 Z), Z = L + p_null,
 // and the null sink's share.  Everything the parameter gradients need except the real
@@ -423,85 +833,92 @@ struct PolarPrepArgs {
 
 template <typename T, int D>
 __global__ void __launch_bounds__(256) polar_bwd_prep_kernel(PolarPrepArgs a) {
-  constexpr int E = D / 64;  // elements per lane
-  constexpr int R = 4;       // rows per wave, processed together (independent chains)
+  // one query row per group of 16 lanes (E elements per lane): the row sums are DPP
+  // reductions within the group, and every lane of the group runs the row's scalar chain
+  constexpr int E = D / 16;
   constexpr float kTiny = 1.0e-30f;
   __shared__ float s_vn[4][D];
   __shared__ float s_sc[4][4];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4, l16 = lane & 15;
   const int bh = blockIdx.y, b = bh / a.H, h = bh % a.H;
-  const int t0 = blockIdx.x * 16 + wave * R;
-  // The per-row scalar chain (log, exp, log1p, tanh, divisions) runs once per row: lane
-  // i < R computes row t0 + i, and the results are read back with shuffles.
-  const int my = lane & (R - 1);
-  const bool my_ok = t0 + my < a.T;
-  const int64_t my_row = (int64_t)bh * a.T + (my_ok ? t0 + my : 0);
-  float n = a.n_keys[my_ok ? t0 + my : 0];
+  const int t = blockIdx.x * 16 + wave * 4 + grp;
+  const bool ok = t < a.T;
+  const int64_t row = (int64_t)bh * a.T + (ok ? t : 0);
+  float n = a.n_keys[ok ? t : 0];
   if (a.window > 0 && !a.preserve_length) n = fminf(n, (float)a.window);
   n = fmaxf(n, 1.f);
   const float logn = logf(n), root = sqrtf(logf(n + 1.f));
   const float temp = 1.f + softplus(a.len_gain_raw[h]) * logn;
   const float nu = a.null_base[h] + softplus(a.null_slope_raw[h]) * root;
-  const float p_null = my_ok ? expf(temp * nu - a.M[my_row]) : 0.f;
-  const float Lr = my_ok ? a.L[my_row] : 0.f, Q2r = my_ok ? a.Q2[my_row] : 0.f;
-  const float gmr = (my_ok && a.gm) ? to_f32(((const T*)a.gm)[my_row]) : 0.f;
+  const float p_null = ok ? expf(temp * nu - a.M[row]) : 0.f;
+  const float Lr = ok ? a.L[row] : 0.f, Q2r = ok ? a.Q2[row] : 0.f;
+  const float gmr = (ok && a.gm) ? to_f32(((const T*)a.gm)[row]) : 0.f;
 
-  bool ok[R];
-  int64_t row[R];
-  float sv[R][E], gv[R][E], vnull[E];
+  float sv[E], gv[E], vnull[E];
+  {
+    // 16-byte loads (rows of S, gc and v_null are 16-byte aligned)
+    const float* sp = a.S + row * D + l16 * E;
+    const float* vp = a.v_null + (int64_t)h * D + l16 * E;
 #pragma unroll
-  for (int e = 0; e < E; ++e) vnull[e] = a.v_null[(int64_t)h * D + 64 * e + lane];
+    for (int e4 = 0; e4 < E; e4 += 4) {
+      const f32x4 x = ok ? *(const f32x4*)(sp + e4) : f32x4{0.f, 0.f, 0.f, 0.f};
+      const f32x4 y = *(const f32x4*)(vp + e4);
 #pragma unroll
-  for (int i = 0; i < R; ++i) {
-    ok[i] = t0 + i < a.T;
-    row[i] = (int64_t)bh * a.T + (ok[i] ? t0 + i : 0);
+      for (int e = 0; e < 4; ++e) {
+        sv[e4 + e] = x[e];
+        vnull[e4 + e] = y[e];
+      }
+    }
+    if constexpr (sizeof(T) == 2) {
+      const T* gp = (const T*)a.gc + row * D + l16 * E;
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      sv[i][e] = ok[i] ? a.S[row[i] * D + 64 * e + lane] : 0.f;
-      gv[i][e] = (ok[i] && a.gc) ? to_f32(((const T*)a.gc)[row[i] * D + 64 * e + lane]) : 0.f;
+      for (int e8 = 0; e8 < E; e8 += 8) {
+        u32x4 x = u32x4{0u, 0u, 0u, 0u};
+        if (ok && a.gc) {
+          if constexpr (E >= 8) x = *(const u32x4*)(gp + e8);
+          else { const u32x2 y = *(const u32x2*)gp; x = u32x4{y[0], y[1], 0u, 0u}; }
+        }
+#pragma unroll
+        for (int e = 0; e < (E < 8 ? E : 8); ++e) gv[e8 + e] = elem16<T>(x, e);
+      }
+    } else {
+#pragma unroll
+      for (int e4 = 0; e4 < E; e4 += 4) {
+        const f32x4 x = (ok && a.gc) ? *(const f32x4*)((const float*)a.gc + row * D + l16 * E + e4)
+                                      : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) gv[e4 + e] = x[e];
+      }
     }
   }
-  float ss[R], gcs[R];
+  float ss = 0.f, gcs = 0.f;
 #pragma unroll
-  for (int i = 0; i < R; ++i) {
-    ss[i] = 0.f;
-    gcs[i] = 0.f;
+  for (int e = 0; e < E; ++e) {
+    ss = fmaf(sv[e], sv[e], ss);
+    gcs = fmaf(gv[e], sv[e], gcs);
+  }
+  ss = row16_sum(ss);
+  gcs = row16_sum(gcs);
+  // gs = (gc - (gc.c) c) / |s|  with c = s / |s|:  (gc - (gc.s / |s|) s / |s|) / |s|
+  const float inv = 1.f / fmaxf(sqrtf(ss), a.eps);
+  const float gcc = gcs * inv;
+  float g[E], gsv = 0.f;
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      ss[i] = fmaf(sv[i][e], sv[i][e], ss[i]);
-      gcs[i] = fmaf(gv[i][e], sv[i][e], gcs[i]);
+  for (int e = 0; e < E; ++e) {
+    g[e] = (gv[e] - gcc * (sv[e] * inv)) * inv;
+    gsv = fmaf(g[e], vnull[e], gsv);
+  }
+  if (ok) {
+    T* out = (T*)a.gs + row * D + l16 * E;
+    if constexpr (sizeof(T) == 2 && E == 8) {
+      *(u32x4*)out = u32x4{pack2<T>(g[0], g[1]), pack2<T>(g[2], g[3]), pack2<T>(g[4], g[5]), pack2<T>(g[6], g[7])};
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; ++e) out[e] = from_f32<T>(g[e]);
     }
   }
-#pragma unroll
-  for (int i = 0; i < R; ++i) {
-    ss[i] = wave_sum(ss[i]);
-    gcs[i] = wave_sum(gcs[i]);
-  }
-  float vn[E];
-#pragma unroll
-  for (int e = 0; e < E; ++e) vn[e] = 0.f;
-  float gsv[R];
-#pragma unroll
-  for (int i = 0; i < R; ++i) {
-    const float pn = __shfl(p_null, i, 64);
-    // gs = (gc - (gc.c) c) / |s|  with c = s / |s|:  (gc - (gc.s / |s|) s / |s|) / |s|
-    const float inv = 1.f / fmaxf(sqrtf(ss[i]), a.eps);
-    const float gcc = gcs[i] * inv;
-    gsv[i] = 0.f;
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const float g = (gv[i][e] - gcc * (sv[i][e] * inv)) * inv;
-      if (ok[i]) ((T*)a.gs)[row[i] * D + 64 * e + lane] = from_f32<T>(g);
-      gsv[i] = fmaf(g, vnull[e], gsv[i]);
-      vn[e] = fmaf(pn, g, vn[e]);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < R; ++i) gsv[i] = wave_sum(gsv[i]);
-  // lane my: the rest of row t0 + my's chain
-  float my_gsv = gsv[0];
-#pragma unroll
-  for (int i = 1; i < R; ++i) my_gsv = my == i ? gsv[i] : my_gsv;
+  gsv = row16_sum(gsv);
+  // the magnitude path through m_eff = L^3 / (Q2 Z), Z = L + p_null
   const float beta = softplus(a.mag_beta_raw[h]);
   const float Z = Lr + p_null;
   const float Zc = fmaxf(Z, kTiny), Q2c = fmaxf(Q2r, kTiny);
@@ -512,38 +929,39 @@ __global__ void __launch_bounds__(256) polar_bwd_prep_kernel(PolarPrepArgs a) {
   const float dme_dL = Lr > 0.f ? 3.f * me / Lr : 0.f;
   const float dme_dQ2 = Q2r > kTiny ? -me / Q2c : 0.f;
   const float dme_dZ = Z > kTiny ? -me / Zc : 0.f;
-  const float g_anull = (my_gsv + gme * dme_dZ) * p_null;
-  const bool lead = lane < R && my_ok;
-  if (lead) {
-    a.gL[my_row] = gme * (dme_dL + dme_dZ);
-    a.gQ2[my_row] = gme * dme_dQ2;
-    if (b == 0) a.temp[(int64_t)h * a.T + t0 + my] = temp;
+  const float g_anull = (gsv + gme * dme_dZ) * p_null;
+  if (ok && l16 == 0) {
+    a.gL[row] = gme * (dme_dL + dme_dZ);
+    a.gQ2[row] = gme * dme_dQ2;
+    if (b == 0) a.temp[(int64_t)h * a.T + t] = temp;
   }
-  float t1 = lead ? g_anull * nu * logn : 0.f;
-  float t2 = lead ? g_anull * temp : 0.f;
-  float t3 = lead ? g_anull * temp * root : 0.f;
-  float t4 = lead ? gmr * (1.f - mag * mag) * lm : 0.f;
+  // the workgroup's record: sums over its 16 rows (the wave's 4 groups, then the waves)
+  float sc[4] = {ok ? g_anull * nu * logn : 0.f, ok ? g_anull * temp : 0.f, ok ? g_anull * temp * root : 0.f,
+                 ok ? gmr * (1.f - mag * mag) * lm : 0.f};
+  float vn[E];
 #pragma unroll
-  for (int m = 1; m < R; m <<= 1) {  // sum over the R leading lanes
-    t1 += __shfl_xor(t1, m, 64);
-    t2 += __shfl_xor(t2, m, 64);
-    t3 += __shfl_xor(t3, m, 64);
-    t4 += __shfl_xor(t4, m, 64);
+  for (int e = 0; e < E; ++e) vn[e] = p_null * g[e];
+#pragma unroll
+  for (int m = 16; m < 64; m <<= 1) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) vn[e] += __shfl_xor(vn[e], m, 64);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) sc[k] += __shfl_xor(sc[k], m, 64);
   }
+  if (grp == 0) {
 #pragma unroll
-  for (int e = 0; e < E; ++e) s_vn[wave][64 * e + lane] = vn[e];
-  if (lane == 0) {
-    s_sc[wave][0] = t1;
-    s_sc[wave][1] = t2;
-    s_sc[wave][2] = t3;
-    s_sc[wave][3] = t4;
+    for (int e = 0; e < E; ++e) s_vn[wave][l16 * E + e] = vn[e];
+    if (l16 == 0) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) s_sc[wave][k] = sc[k];
+    }
   }
   __syncthreads();
   float* rec = a.part + ((int64_t)(b * gridDim.x + blockIdx.x) * a.H + h) * (D + 4);
   if (tid < D) rec[tid] = s_vn[0][tid] + s_vn[1][tid] + s_vn[2][tid] + s_vn[3][tid];
   else if (tid < D + 4) {
-    const int j = tid - D;
-    rec[D + j] = s_sc[0][j] + s_sc[1][j] + s_sc[2][j] + s_sc[3][j];
+    const int k = tid - D;
+    rec[D + k] = s_sc[0][k] + s_sc[1][k] + s_sc[2][k] + s_sc[3][k];
   }
 }
 
@@ -565,6 +983,72 @@ __global__ void __launch_bounds__(256) polar_bwd_group_sum_kernel(const float* _
   T* o = out + (bhk * rows4 + i) * 4;
 #pragma unroll
   for (int e = 0; e < 4; ++e) o[e] = from_f32<T>(acc[e]);
+}
+
+// Parameter gradients from the preamble's per-block partial sums and the dq loop's dt
+// (kernel/polar_triton.py:1139-1150): with temp = 1 + softplus(lg) log n,
+// nu = nb + softplus(ns) sqrt(log(n + 1)), mag = tanh(softplus(mb) log1p(m_eff)) and
+// d softplus = sigmoid:  g_v_null = sum_blocks part[:, :D];
+// g_len_gain = (sum_{b,t} dt log n + sum part[:, D]) sigmoid(lg); g_null_base = sum part[:, D+1];
+// g_null_slope = sum part[:, D+2] sigmoid(ns); g_mag_beta = sum part[:, D+3] sigmoid(mb).
+// Two launches, every sum in a fixed order (deterministic): kParamSplit workgroups per
+// head each sum a slice of the blocks and of the (b, t) pairs into a workspace row, then
+// one workgroup per head adds the rows and applies the chain rule.
+constexpr int kParamSplit = 32;
+
+__global__ void __launch_bounds__(256) polar_bwd_params_partial_kernel(const float* __restrict__ part,
+                                                                        const float* __restrict__ dt,
+                                                                        const float* __restrict__ n_keys,
+                                                                        float* __restrict__ ws, int nblk, int B,
+                                                                        int H, int T, int D, int window,
+                                                                        int preserve_length) {
+  __shared__ float red[256];
+  const int h = blockIdx.x, sp = blockIdx.y, tid = threadIdx.x, W = D + 4;
+  const int r0 = (int)((int64_t)nblk * sp / kParamSplit), r1 = (int)((int64_t)nblk * (sp + 1) / kParamSplit);
+  float* out = ws + ((int64_t)sp * H + h) * (W + 1);
+  if (tid < W) {
+    float col = 0.f;
+#pragma unroll 8
+    for (int r = r0; r < r1; ++r) col += part[((int64_t)r * H + h) * W + tid];
+    out[tid] = col;
+  }
+  const int64_t n = (int64_t)B * T, i0 = n * sp / kParamSplit, i1 = n * (sp + 1) / kParamSplit;
+  float acc = 0.f;
+  for (int64_t i = i0 + tid; i < i1; i += 256) {
+    const int b = (int)(i / T), t = (int)(i % T);
+    float nk = n_keys[t];
+    if (window > 0 && !preserve_length) nk = fminf(nk, (float)window);
+    acc += dt[((int64_t)b * H + h) * T + t] * logf(fmaxf(nk, 1.f));
+  }
+  red[tid] = acc;
+  __syncthreads();
+  for (int m = 128; m > 0; m >>= 1) {
+    if (tid < m) red[tid] += red[tid + m];
+    __syncthreads();
+  }
+  if (tid == 0) out[W] = red[0];
+}
+
+__global__ void __launch_bounds__(256) polar_bwd_params_final_kernel(const float* __restrict__ ws,
+                                                                      const float* __restrict__ len_gain_raw,
+                                                                      const float* __restrict__ null_slope_raw,
+                                                                      const float* __restrict__ mag_beta_raw,
+                                                                      float* __restrict__ g_v_null,
+                                                                      float* __restrict__ g4, int H, int D) {
+  __shared__ float dt_logn;
+  const int h = blockIdx.x, tid = threadIdx.x, W = D + 4;
+  float col = 0.f;
+  if (tid <= W)
+    for (int sp = 0; sp < kParamSplit; ++sp) col += ws[((int64_t)sp * H + h) * (W + 1) + tid];
+  if (tid == W) dt_logn = col;
+  __syncthreads();
+  auto sig = [](float x) { return 1.f / (1.f + expf(-x)); };
+  // g4 rows: null_base, null_slope_raw, len_gain_raw, mag_beta_raw
+  if (tid < D) g_v_null[(int64_t)h * D + tid] = col;
+  else if (tid == D) g4[2 * H + h] = (dt_logn + col) * sig(len_gain_raw[h]);
+  else if (tid == D + 1) g4[0 * H + h] = col;
+  else if (tid == D + 2) g4[1 * H + h] = col * sig(null_slope_raw[h]);
+  else if (tid == D + 3) g4[3 * H + h] = col * sig(mag_beta_raw[h]);
 }
 
 template <typename T, int D>
@@ -680,4 +1164,36 @@ extern "C" int atma_polar_bwd_group_sum(const float* part, void* out, int64_t n_
     default: return set_error(ATMA_ERR_INVALID, "polar_bwd_group_sum: unknown dtype %d", dtype);
   }
   return check_launch("polar_bwd_group_sum");
+}
+
+extern "C" size_t atma_polar_bwd_param_grads_workspace_bytes(int64_t H, int64_t d) {
+  return (size_t)atma::kParamSplit * (size_t)(H > 0 ? H : 0) * (size_t)(d + 5) * sizeof(float);
+}
+
+extern "C" int atma_polar_bwd_param_grads(const float* part, const float* dt, const float* n_keys,
+                                          const float* len_gain_raw, const float* null_slope_raw,
+                                          const float* mag_beta_raw, float* g_v_null, float* g_params,
+                                          int64_t B, int64_t H, int64_t T, int64_t d, int64_t window,
+                                          int preserve_length, void* workspace, size_t workspace_bytes,
+                                          void* stream) {
+  using namespace atma;
+  if (B < 0 || H <= 0 || T < 0 || (d != 64 && d != 128))
+    return set_error(ATMA_ERR_INVALID, "polar_bwd_param_grads: bad sizes (d = 64 or 128)");
+  if (H > 65535 || B * T > (1ll << 40)) return set_error(ATMA_ERR_INVALID, "polar_bwd_param_grads: sizes too large");
+  if (!part || !dt || !n_keys || !len_gain_raw || !null_slope_raw || !mag_beta_raw || !g_v_null || !g_params)
+    return set_error(ATMA_ERR_INVALID, "polar_bwd_param_grads: null pointer");
+  if (!workspace || workspace_bytes < atma_polar_bwd_param_grads_workspace_bytes(H, d))
+    return set_error(ATMA_ERR_WORKSPACE, "polar_bwd_param_grads: workspace too small");
+  const int64_t nblk = B * ((T + 15) / 16);
+  hipStream_t s = (hipStream_t)stream;
+  float* ws = (float*)workspace;
+  polar_bwd_params_partial_kernel<<<dim3((unsigned)H, kParamSplit), dim3(256), 0, s>>>(
+      part, dt, n_keys, ws, (int)nblk, (int)B, (int)H, (int)T, (int)d, window > 0 ? (int)window : 0,
+      preserve_length ? 1 : 0);
+  int rc = check_launch("polar_bwd_param_grads(partial)");
+  if (rc) return rc;
+  polar_bwd_params_final_kernel<<<dim3((unsigned)H), dim3(256), 0, s>>>(ws, len_gain_raw, null_slope_raw,
+                                                                          mag_beta_raw, g_v_null, g_params,
+                                                                          (int)H, (int)d);
+  return check_launch("polar_bwd_param_grads(final)");
 }

@@ -45,22 +45,16 @@ class PolarAttentionHip(torch.autograd.Function):
             gc, gm, S, M, L, Q2, nk, v_null, null_base, null_slope_raw, len_gain_raw, mag_beta_raw,
             float(ctx.eps), win, bool(ctx.preserve_length), q.dtype)
         # the O(T^2) loops
-        dq, dt, dk, dv = torch.ops.atma_hip.polar_attention_bwd(
+        dq, dt, dkv = torch.ops.atma_hip.polar_attention_bwd(
             q, k, v, gs, gL, gQ2, M, temp, nk, bool(ctx.is_causal), win)
-        # parameters: temp = 1 + softplus(lg) log n, nu = nb + softplus(ns) sqrt(log(n + 1)),
-        # mag = tanh(softplus(mb) log1p(m_eff)); d softplus = sigmoid.  The real keys' share
-        # of dL/dtemp is dt; the preamble summed the sink's share and the rest per block.
-        sums = part.sum(0)                                      # (H, d + 4)
-        n = nk.float()
-        if ctx.window is not None and not ctx.preserve_length:
-            n = torch.clamp(n, max=float(ctx.window))
-        logn = torch.log(n.clamp(min=1.0))
-        grad_v_null = sums[:, :d]
-        dt_logn = torch.mv(dt.sum(0), logn)                     # (H,)
-        grad_len_gain = (dt_logn + sums[:, d]) * torch.sigmoid(len_gain_raw)
-        grad_null_base = sums[:, d + 1]
-        grad_null_slope = sums[:, d + 2] * torch.sigmoid(null_slope_raw)
-        grad_mag_beta = sums[:, d + 3] * torch.sigmoid(mag_beta_raw)
+        dk, dv = dkv[0], dkv[1]
+        # parameters (one HIP launch): temp = 1 + softplus(lg) log n,
+        # nu = nb + softplus(ns) sqrt(log(n + 1)), mag = tanh(softplus(mb) log1p(m_eff));
+        # d softplus = sigmoid.  The real keys' share of dL/dtemp is dt; the preamble summed
+        # the sink's share and the rest per block.
+        grad_v_null, g4 = torch.ops.atma_hip.polar_bwd_param_grads(
+            part, dt, nk, len_gain_raw, null_slope_raw, mag_beta_raw, win, bool(ctx.preserve_length))
+        grad_null_base, grad_null_slope, grad_len_gain, grad_mag_beta = g4[0], g4[1], g4[2], g4[3]
 
         pd = ctx.param_dtypes
         return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None,

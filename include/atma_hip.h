@@ -161,6 +161,21 @@ int atma_polar_attention_bwd_prep(const void* gc, const void* gm, const float* S
 int atma_polar_bwd_group_sum(const float* part, void* out, int64_t n_groups, int64_t G,
                              int64_t elems, int dtype, void* stream);
 
+/*
+ * The parameter gradients of the Polar backward (kernel/polar_triton.py:1139-1150) from the
+ * preamble's per-block sums `part` (B * ceil(T / 16), H, d + 4) and the loops' dt (B, H, T),
+ * with n_keys (T,) and window / preserve_length as in the forward: g_v_null (H, d) and
+ * g_params (4, H) fp32 = the gradients of null_base, null_slope_raw, len_gain_raw and
+ * mag_beta_raw (two launches, fixed-order sums; workspace of
+ * atma_polar_bwd_param_grads_workspace_bytes).  d = 64 or 128.
+ */
+size_t atma_polar_bwd_param_grads_workspace_bytes(int64_t H, int64_t d);
+int atma_polar_bwd_param_grads(const float* part, const float* dt, const float* n_keys,
+                               const float* len_gain_raw, const float* null_slope_raw,
+                               const float* mag_beta_raw, float* g_v_null, float* g_params, int64_t B,
+                               int64_t H, int64_t T, int64_t d, int64_t window, int preserve_length,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
 int atma_polar_attention_bwd(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
                              const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
                              const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
