@@ -29,7 +29,7 @@ SIGNATURES = {
         _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
         _i64, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _i64, _i32, _f32, _p]),
     "atma_polar_attention_bwd_prep": (_i32, [_p] * 17 + [_i64, _i64, _i64, _i64, _i32, _i64, _i32, _f32, _p]),
-    "atma_polar_bwd_group_sum": (_i32, [_p, _p, _i64, _i64, _i64, _i32, _p]),
+    "atma_polar_bwd_group_sum": (_i32, [_p, _i32, _p, _i64, _i64, _i64, _i32, _p]),
     "atma_polar_bwd_param_grads_workspace_bytes": (_sz, [_i64, _i64]),
     "atma_polar_bwd_param_grads": (_i32, [_p] * 8 + [_i64] * 5 + [_i32, _p, _sz, _p]),
     "atma_polar_attention_bwd": (_i32, [

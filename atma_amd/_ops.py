@@ -152,9 +152,10 @@ def polar_attention_bwd_op(q: Tensor, k: Tensor, v: Tensor, gs: Tensor, gL: Tens
     Hkv, Tk = k.shape[1], k.shape[2]
     f = dict(device=q.device, dtype=torch.float32)
     new = torch.empty if Tk > 0 else torch.zeros   # with no keys nothing is written
-    dq = new((B, Hq, Tq, d), **f)
+    dq = new((B, Hq, Tq, d), device=q.device, dtype=q.dtype)
     dt = new((B, Hq, Tq), **f)
-    dkv = new((2, B, Hq, Tk, d), **f)   # each query head's share of dk, dv; the group sum follows
+    share = torch.float32 if q.dtype == torch.float32 else torch.bfloat16
+    dkv = new((2, B, Hq, Tk, d), device=q.device, dtype=share)   # each query head's share; the group sum follows
     dk, dv = dkv[0], dkv[1]   # the kernel's two outputs
     gL, gQ2, M, temp = (t.to(torch.float32).contiguous() for t in (gL, gQ2, M, temp))
     rc = lib.atma_polar_attention_bwd(
@@ -166,9 +167,7 @@ def polar_attention_bwd_op(q: Tensor, k: Tensor, v: Tensor, gs: Tensor, gL: Tens
         dq.data_ptr(), dt.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, Hq, Hkv, Tq, Tk, d,
         _lib.dtype_code(q.dtype), 1 if is_causal else 0, window, _lib.stream_handle(q.device))
     _lib.check(rc, "polar_attention_bwd")
-    # dq in q's dtype; dk / dv: the group's shares summed (fixed order) into k's dtype
-    if q.dtype != torch.float32:
-        dq = _group_sum(lib, dq, 1, B * Hq * Tq * d, 1, q.dtype)
+    # dk / dv: the group's shares summed (fixed order) into k's dtype
     if Hkv != Hq or q.dtype != torch.float32:   # dk and dv in one launch
         dkv = _group_sum(lib, dkv, 2 * B * Hkv, Tk * d, Hq // Hkv, q.dtype).view(2, B, Hkv, Tk, d)
     return [dq, dt, dkv]
@@ -177,8 +176,8 @@ def polar_attention_bwd_op(q: Tensor, k: Tensor, v: Tensor, gs: Tensor, gL: Tens
 def _group_sum(lib, part, n_groups, elems, G, dtype):
     """out[g0] = sum of part's G consecutive (elems,) slices g0 * G .. g0 * G + G - 1, in dtype."""
     out = torch.empty(n_groups * elems, device=part.device, dtype=dtype)
-    rc = lib.atma_polar_bwd_group_sum(part.data_ptr(), out.data_ptr(), n_groups, G, elems,
-                                      _lib.dtype_code(dtype), _lib.stream_handle(part.device))
+    rc = lib.atma_polar_bwd_group_sum(part.data_ptr(), _lib.dtype_code(part.dtype), out.data_ptr(), n_groups, G,
+                                      elems, _lib.dtype_code(dtype), _lib.stream_handle(part.device))
     _lib.check(rc, "polar_bwd_group_sum")
     return out.view(part.shape) if G == 1 else out
 

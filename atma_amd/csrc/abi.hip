@@ -46,6 +46,6 @@ int dtype_size(int dtype) {
 
 }  // namespace atma
 
-extern "C" int atma_abi_version(void) { return 1; }
+extern "C" int atma_abi_version(void) { return 2; }
 
 extern "C" const char* atma_last_error(void) { return atma::g_last_error; }

@@ -50,10 +50,12 @@ struct PolarBwdArgs {
   const float* M;       // (B, Hq, Tq) natural-log reference max of the forward
   const float* temp;    // (Hq, Tq)
   const float* n_keys;  // (Tq,)
-  float* dq;            // (B, Hq, Tq, D)
+  void* dq;             // (B, Hq, Tq, D) in the input dtype
   float* dt;            // (B, Hq, Tq)
-  float* dk;            // (B, Hq, Tk, D): each query head's share; grouped heads summed by the caller
-  float* dv;            // (B, Hq, Tk, D)
+  // (B, Hq, Tk, D): each query head's share, grouped heads summed by the caller; fp32 for
+  // fp32 inputs, bf16 for 16-bit inputs (BwShare<T>)
+  void* dk;
+  void* dv;
   int B, Hq, Hkv, Tq, Tk;
   int is_causal, window;
   float scale;
@@ -61,6 +63,8 @@ struct PolarBwdArgs {
 
 template <typename T>
 using BwFrag = std::conditional_t<sizeof(T) == 2, u32x4, float>;
+template <typename T>
+using BwShare = std::conditional_t<sizeof(T) == 2, bf16, float>;
 template <typename T>
 constexpr int kBwK = sizeof(T) == 2 ? 32 : 4;  // MFMA k depth
 template <typename T>
@@ -248,9 +252,9 @@ __global__ void __launch_bounds__(256) polar_bwd_dq_kernel(PolarBwdArgs a) {
 #pragma unroll
     for (int m = 1; m < 16; m <<= 1) x += __shfl_xor(x, m, 64);  // the 16 key columns of the row
     if (row < a.Tq) {
-      float* out = a.dq + ((int64_t)bh * a.Tq + row) * D + (lane & 15);
+      T* out = (T*)a.dq + ((int64_t)bh * a.Tq + row) * D + (lane & 15);
 #pragma unroll
-      for (int nt = 0; nt < D / 16; ++nt) out[16 * nt] = dq[nt][j] * a.scale;
+      for (int nt = 0; nt < D / 16; ++nt) out[16 * nt] = from_f32<T>(dq[nt][j] * a.scale);
       if ((lane & 15) == 0) a.dt[(int64_t)bh * a.Tq + row] = x;
     }
   }
@@ -377,8 +381,8 @@ __global__ void __launch_bounds__(256) polar_bwd_dkdv_kernel(PolarBwdArgs a) {
       const int64_t base = ((int64_t)bh * a.Tk + row) * D + (lane & 15);
 #pragma unroll
       for (int nt = 0; nt < D / 16; ++nt) {
-        a.dk[base + 16 * nt] = dk[nt][j] * a.scale;
-        a.dv[base + 16 * nt] = dv[nt][j];
+        ((BwShare<T>*)a.dk)[base + 16 * nt] = from_f32<BwShare<T>>(dk[nt][j] * a.scale);
+        ((BwShare<T>*)a.dv)[base + 16 * nt] = from_f32<BwShare<T>>(dv[nt][j]);
       }
     }
   }
@@ -581,9 +585,12 @@ __global__ void __launch_bounds__(256, 2) polar_bwd16_dq_kernel(PolarBwdArgs a) 
   dt += __shfl_xor(dt, 16, 64);
   dt += __shfl_xor(dt, 32, 64);
   if (rok) {
-    float* out = a.dq + ri * D + 4 * g;
+    T* out = (T*)a.dq + ri * D + 4 * g;
 #pragma unroll
-    for (int nt = 0; nt < D / 16; ++nt) *(f32x4*)(out + 16 * nt) = dqT[nt] * a.scale;
+    for (int nt = 0; nt < D / 16; ++nt) {
+      const f32x4 x = dqT[nt] * a.scale;
+      *(u32x2*)(out + 16 * nt) = u32x2{pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3])};
+    }
     if (g == 0) a.dt[ri] = dt * a.scale;
   }
 }
@@ -771,8 +778,9 @@ __global__ void __launch_bounds__(256, 2) polar_bwd16_dkdv_kernel(PolarBwdArgs a
     const int64_t base = ((int64_t)bh * a.Tk + key) * D + 4 * g;
 #pragma unroll
     for (int nt = 0; nt < D / 16; ++nt) {
-      *(f32x4*)(a.dk + base + 16 * nt) = dkT[nt] * a.scale;
-      *(f32x4*)(a.dv + base + 16 * nt) = dvT[nt];
+      const f32x4 x = dkT[nt] * a.scale, y = dvT[nt];
+      *(u32x2*)((bf16*)a.dk + base + 16 * nt) = u32x2{pack2<bf16>(x[0], x[1]), pack2<bf16>(x[2], x[3])};
+      *(u32x2*)((bf16*)a.dv + base + 16 * nt) = u32x2{pack2<bf16>(y[0], y[1]), pack2<bf16>(y[2], y[3])};
     }
   }
 }
@@ -967,17 +975,26 @@ __global__ void __launch_bounds__(256) polar_bwd_prep_kernel(PolarPrepArgs a) {
 
 // Sum of the G consecutive query heads' shares of dk / dv (or, with G = 1, a copy) into
 // the output dtype: out[b, hk, r] = sum_g part[b, hk G + g, r], r over Tk * D elements,
-// four per thread.
-template <typename T>
-__global__ void __launch_bounds__(256) polar_bwd_group_sum_kernel(const float* __restrict__ part, T* __restrict__ out,
+// four per thread, accumulated in fp32 (shares fp32 or bf16).
+template <typename TI, typename T>
+__global__ void __launch_bounds__(256) polar_bwd_group_sum_kernel(const TI* __restrict__ part, T* __restrict__ out,
                                                                    int64_t rows4, int G) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // float4 index within (b, hk)
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // 4-element index within (b, hk)
   if (i >= rows4) return;
   const int64_t bhk = blockIdx.y;
-  const f32x4* src = (const f32x4*)part + bhk * G * rows4 + i;
-  f32x4 acc = src[0];
+  auto load4 = [&](int64_t j) -> f32x4 {
+    if constexpr (sizeof(TI) == 4) {
+      return ((const f32x4*)part)[j];
+    } else {
+      const u32x2 x = ((const u32x2*)part)[j];
+      const u32x4 y = {x[0], x[1], 0u, 0u};
+      return f32x4{elem16<TI>(y, 0), elem16<TI>(y, 1), elem16<TI>(y, 2), elem16<TI>(y, 3)};
+    }
+  };
+  const int64_t j0 = bhk * G * rows4 + i;
+  f32x4 acc = load4(j0);
   for (int g = 1; g < G; ++g) {
-    const f32x4 x = src[(int64_t)g * rows4];
+    const f32x4 x = load4(j0 + (int64_t)g * rows4);
     acc = f32x4{acc[0] + x[0], acc[1] + x[1], acc[2] + x[2], acc[3] + x[3]};
   }
   T* o = out + (bhk * rows4 + i) * 4;
@@ -1063,7 +1080,7 @@ extern "C" int atma_polar_attention_bwd(
     const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb, int64_t k_sh,
     int64_t k_st, const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, const void* gs,
     int64_t g_sb, int64_t g_sh, int64_t g_st, const float* gL, const float* gQ2, const float* M,
-    const float* temp, const float* n_keys, float* dq, float* dt, float* dk, float* dv, int64_t B,
+    const float* temp, const float* n_keys, void* dq, float* dt, void* dk, void* dv, int64_t B,
     int64_t Hq, int64_t Hkv, int64_t Tq, int64_t Tk, int64_t d, int dtype, int is_causal,
     int64_t window, void* stream) {
   using namespace atma;
@@ -1144,7 +1161,7 @@ extern "C" int atma_polar_attention_bwd_prep(
   }
 }
 
-extern "C" int atma_polar_bwd_group_sum(const float* part, void* out, int64_t n_groups, int64_t G,
+extern "C" int atma_polar_bwd_group_sum(const void* part, int part_dtype, void* out, int64_t n_groups, int64_t G,
                                         int64_t elems, int dtype, void* stream) {
   using namespace atma;
   if (n_groups < 0 || G <= 0 || elems < 0 || elems % 4)
@@ -1152,18 +1169,25 @@ extern "C" int atma_polar_bwd_group_sum(const float* part, void* out, int64_t n_
   if (n_groups == 0 || elems == 0) return ATMA_OK;
   if (n_groups > 65535 || elems / 4 > 0x7fffffffll * 256)
     return set_error(ATMA_ERR_INVALID, "polar_bwd_group_sum: sizes too large");
+  if (part_dtype != ATMA_F32 && part_dtype != ATMA_BF16)
+    return set_error(ATMA_ERR_INVALID, "polar_bwd_group_sum: shares are fp32 or bf16");
   if (!part || !out || (uintptr_t)part % 16)
     return set_error(ATMA_ERR_INVALID, "polar_bwd_group_sum: null or misaligned pointer");
   const int64_t rows4 = elems / 4;
   const dim3 grid((unsigned)((rows4 + 255) / 256), (unsigned)n_groups);
   hipStream_t s = (hipStream_t)stream;
-  switch (dtype) {
-    case ATMA_BF16: polar_bwd_group_sum_kernel<bf16><<<grid, dim3(256), 0, s>>>(part, (bf16*)out, rows4, (int)G); break;
-    case ATMA_F16: polar_bwd_group_sum_kernel<f16><<<grid, dim3(256), 0, s>>>(part, (f16*)out, rows4, (int)G); break;
-    case ATMA_F32: polar_bwd_group_sum_kernel<float><<<grid, dim3(256), 0, s>>>(part, (float*)out, rows4, (int)G); break;
-    default: return set_error(ATMA_ERR_INVALID, "polar_bwd_group_sum: unknown dtype %d", dtype);
-  }
-  return check_launch("polar_bwd_group_sum");
+  auto run = [&](auto ti) -> int {
+    using TI = decltype(ti);
+    const TI* p = (const TI*)part;
+    switch (dtype) {
+      case ATMA_BF16: polar_bwd_group_sum_kernel<TI, bf16><<<grid, dim3(256), 0, s>>>(p, (bf16*)out, rows4, (int)G); break;
+      case ATMA_F16: polar_bwd_group_sum_kernel<TI, f16><<<grid, dim3(256), 0, s>>>(p, (f16*)out, rows4, (int)G); break;
+      case ATMA_F32: polar_bwd_group_sum_kernel<TI, float><<<grid, dim3(256), 0, s>>>(p, (float*)out, rows4, (int)G); break;
+      default: return set_error(ATMA_ERR_INVALID, "polar_bwd_group_sum: unknown dtype %d", dtype);
+    }
+    return check_launch("polar_bwd_group_sum");
+  };
+  return part_dtype == ATMA_F32 ? run(float{}) : run(bf16{});
 }
 
 extern "C" size_t atma_polar_bwd_param_grads_workspace_bytes(int64_t H, int64_t d) {

@@ -123,9 +123,10 @@ int atma_polar_attention_packed_fwd(const void* q, int64_t q_st, int64_t q_sh, c
  * in dtype with strides (x_sb, x_sh, x_st, 1) (GQA resolved in-kernel: query head h
  * reads KV head h / (Hq / Hkv)); gL, gQ2, M: (B, Hq, Tq) fp32 contiguous (the
  * preamble's per-query cotangents and the forward's natural-log reference max);
- * temp: (Hq, Tq) fp32; n_keys: (Tq,) raw counts (the mask).  Outputs, fp32 contiguous,
- * every element written when Tk > 0: dq (B, Hq, Tq, d), dt (B, Hq, Tq) (= sum_j da * sig,
- * the real keys' share of dL/dtemp), dk, dv (B, Hq, Tk, d): each query head's share, so
+ * temp: (Hq, Tq) fp32; n_keys: (Tq,) raw counts (the mask).  Outputs, contiguous, every
+ * element written when Tk > 0: dq (B, Hq, Tq, d) in dtype, and fp32 dt (B, Hq, Tq) (= sum_j da * sig,
+ * the real keys' share of dL/dtemp), dk, dv (B, Hq, Tk, d) (fp32 for fp32 inputs, bf16 for
+ * 16-bit inputs): each query head's share, so
  * with Hkv < Hq the caller sums the Hq / Hkv consecutive heads of a group (one workgroup
  * per query head fills the GPU at causal T = 2,048; a deterministic sum, no atomics).
  * d = 64 or 128.
@@ -151,14 +152,15 @@ int atma_polar_attention_bwd_prep(const void* gc, const void* gm, const float* S
                                   float eps, void* stream);
 
 /*
- * Final step of the backward's dk / dv (and the dtype cast of dq), no reference
+ * Final step of the backward's dk / dv, no reference
  * counterpart (the reference's loops write per-KV-head fp32 gradients that autograd casts):
  * out[g0, r] = sum_{g < G} part[g0 * G + g, r] in dtype, for n_groups groups of G
- * consecutive slices of `elems` fp32 elements (elems % 4 == 0; part 16-byte aligned).
+ * consecutive slices of `elems` elements of part_dtype (ATMA_F32 or ATMA_BF16; elems % 4 == 0;
+ * part 16-byte aligned), summed in fp32.
  * With the (B, Hq, Tk, d) shares of atma_polar_attention_bwd: n_groups = B * Hkv,
  * G = Hq / Hkv, elems = Tk * d.  A fixed-order sum: deterministic.
  */
-int atma_polar_bwd_group_sum(const float* part, void* out, int64_t n_groups, int64_t G,
+int atma_polar_bwd_group_sum(const void* part, int part_dtype, void* out, int64_t n_groups, int64_t G,
                              int64_t elems, int dtype, void* stream);
 
 /*
@@ -181,8 +183,8 @@ int atma_polar_attention_bwd(const void* q, int64_t q_sb, int64_t q_sh, int64_t 
                              const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
                              const void* gs, int64_t g_sb, int64_t g_sh, int64_t g_st,
                              const float* gL, const float* gQ2, const float* M,
-                             const float* temp, const float* n_keys, float* dq, float* dt,
-                             float* dk, float* dv, int64_t B, int64_t Hq, int64_t Hkv,
+                             const float* temp, const float* n_keys, void* dq, float* dt,
+                             void* dk, void* dv, int64_t B, int64_t Hq, int64_t Hkv,
                              int64_t Tq, int64_t Tk, int64_t d, int dtype, int is_causal,
                              int64_t window, void* stream);
 

@@ -31,7 +31,7 @@ def lib():
 def test_library_exports_every_declared_symbol(lib):
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.atma_abi_version() == 1
+    assert lib.atma_abi_version() == 2
 
 
 def test_validation_rejects_without_launch(lib):
@@ -119,8 +119,8 @@ def test_validation_rejects_without_launch(lib):
     assert lib.atma_polar_attention_bwd_prep(*prep0, 2, 8, 0, 128, 1, 0, 0, 1e-6, null) == 0
     assert lib.atma_polar_attention_bwd_prep(*prep0, 2, 8, 16, 128, 1, 0, 0, 1e-6, null) == 1
     # backward group sum: elems must be a multiple of 4; nothing to do is a no-op
-    assert lib.atma_polar_bwd_group_sum(null, null, 2, 4, 6, 1, null) == 1
-    assert lib.atma_polar_bwd_group_sum(null, null, 0, 4, 8, 1, null) == 0
+    assert lib.atma_polar_bwd_group_sum(null, 0, null, 2, 4, 6, 1, null) == 1
+    assert lib.atma_polar_bwd_group_sum(null, 0, null, 0, 4, 8, 1, null) == 0
     # store_kvcache: unknown dtype
     assert lib.atma_store_kvcache(null, 0, null, 0, null, null, null, 1, 256, 8, 9, null) == 1
     # zero-size requests are no-ops
