@@ -175,6 +175,83 @@ def test_block_fp32_gradients_vs_fp64_oracle(dev, overlap):
     assert not bad, bad
 
 
+def _token_sum_scales(monkeypatch, sd, x, w):
+    """Per-head sums over tokens of |per-token contribution| to three gradients that
+    are token sums: the memory's write- and retention-gate biases (d/d logit summed over
+    (b, t)) and len_gain_raw (softplus'(len_gain) * sum_t d temp_t * ln n_t).  Obtained
+    by adding a zero tensor at each token to the logit / temperature in the fp64 oracle
+    and reading its gradient.  These sums cancel heavily (e.g. |sum| about 2.8 against
+    sum |.| about 300 for one head's write-gate bias at T=333), so 16-bit rounding of the
+    per-token terms is judged against the latter."""
+    import oracle.polar as OP
+    taps = {}
+    lin, tn = OB.linear, OP.polar_temp_null
+
+    def tap(name, y):
+        taps[name] = torch.zeros_like(y, requires_grad=True)
+        return y + taps[name]
+
+    def linear(xx, sdd, name):
+        y = lin(xx, sdd, name)
+        return tap(name, y) if name in ("mem.w_beta", "mem.w_gamma") else y
+
+    def temp_null(n, lg, nb, ns):
+        t, nu = tn(n, lg, nb, ns)
+        e = torch.zeros_like(t, requires_grad=True)
+        taps["temp"] = e
+        return t + e * torch.log(n.clamp_min(1.0))[None, :], nu
+
+    monkeypatch.setattr(OB, "linear", linear)
+    monkeypatch.setattr(OP, "polar_temp_null", temp_null)
+    out = OB.global_block(sd, x, H=H, Hkv=HKV, dk=DK)
+    names = ("mem.w_beta", "mem.w_gamma", "temp")
+    gb, gg, gt = torch.autograd.grad((out * w).sum(), [taps[n] for n in names])
+    monkeypatch.undo()
+    lg = sd["attn.len_gain_raw"].detach()
+    return {"attn.mem.w_beta.bias": gb.abs().sum((0, 1)), "attn.mem.w_gamma.bias": gg.abs().sum((0, 1)),
+            "attn.len_gain_raw": gt.abs().sum(1) * torch.sigmoid(lg)}
+
+
+@pytest.mark.parametrize("T", [200, 333])
+def test_block_bf16_gradients_vs_fp64_oracle(dev, monkeypatch, T):
+    """The 16-bit training route through the layer: the block in bfloat16 (its Polar
+    backward on the MFMA loops with bf16 key/value shares, the memory branch on the
+    chunked 16-bit gated-delta backward) against fp64 autograd through
+    ``oracle/block.global_block`` evaluated on the same bf16-rounded parameters and
+    input.  Per-tensor bar max|a-b| / max|b| <= 5e-2 (the reference's 16-bit backward
+    bar, kernel/test_polar_kernel.py:119-128); for the three gradients that are
+    cancelling token sums, max|a-b| <= 5e-3 * max_h sum_t |contribution| instead when
+    that is the looser."""
+    blk = _block(seed=3).to(torch.bfloat16)
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(2, T, DIM, generator=g).to(torch.bfloat16)
+    w = torch.randn(2, T, DIM, generator=g)
+    sd = {k: v.detach().double().clone().requires_grad_(True) for k, v in blk.state_dict().items()}
+    x64 = x.double().requires_grad_(True)
+    ref_out = OB.global_block(sd, x64, H=H, Hkv=HKV, dk=DK)
+    names = [n for n, _ in blk.named_parameters()]
+    ref = torch.autograd.grad((ref_out * w.double()).sum(), [x64] + [sd[n] for n in names])
+    scales = _token_sum_scales(monkeypatch, sd, x.double(), w.double())
+
+    print(f"bf16 block backward T={T}", flush=True)
+    blk = blk.to(dev)
+    xd = x.to(dev).requires_grad_(True)
+    out = blk(xd)
+    assert out.dtype == torch.bfloat16
+    got = torch.autograd.grad((out.float() * w.to(dev)).sum(), [xd] + [p for _, p in blk.named_parameters()])
+    assert rel_err(out.detach().float(), ref_out.detach()) <= 2e-2
+    bad = {}
+    for name, a, b in zip(["x"] + names, got, ref):
+        assert a.dtype == torch.bfloat16, name
+        e = rel_err(a.float(), b)
+        if e <= 5e-2:
+            continue
+        if name in scales and max_abs(a.float(), b) <= 5e-3 * scales[name].max().item():
+            continue
+        bad[name] = e
+    assert not bad, bad
+
+
 def _packed_maps(lengths, slots, dev):
     """The engine's tile map (one entry per 128-row query tile) and token map."""
     ts, tq, tl, st, en, sl, packed = [], [], [], [], [], [], 0
