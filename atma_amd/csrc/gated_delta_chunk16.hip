@@ -650,6 +650,322 @@ __global__ void __launch_bounds__(128, 1) gdn_scan16_kernel(GdnArgs a) {
   wait_vmcnt<0>();
 }
 
+// The scan with its output (seg_mode 0 and 2) on four waves: chain waves 0 and 1 run only
+// the recurrence of their 16 columns (K S -> X -> U -> S update), and output waves 2 and 3
+// compute the same columns' output rows and issue every copy.  A wave issues at most one
+// instruction per cycle slot of its SIMD, and with one wave per SIMD the chain's step time
+// is its instruction count; the output products, q reads, stores and copies move to the two
+// SIMDs the two-wave form leaves idle.  Per chunk c, between the top barrier B0 and the
+// middle barrier B1 the chain reads S_c's fragments from its registers and writes U_c's to
+// LDS; after B1 it updates S and writes S_{c+1}'s fragments.  The output wave reads S_c's
+// fragments before B1 (the chain overwrites them only after B1) and U_c's after B1 (the
+// chain overwrites them only after the next B0).
+template <typename T, int D>
+__global__ void __launch_bounds__(256, 1) gdn_scan16_pair_kernel(GdnArgs a) {
+  constexpr int C = kChunk, KS = D / 32, ST = D / 16;
+  constexpr int CPR = D / 8;                    // 16-byte chunks per k / q row
+  constexpr int KB = C * D, VB = C * 32;        // elements of one slot's k (q) rows, v slab
+  constexpr int RB = kGdn16RecBytes;            // bytes of one slot's record
+  constexpr int RPI = 64 / CPR;                 // k / q rows per copy instruction
+  constexpr int NKQ = 32 / RPI;                 // copy instructions per output wave for its 32 k (q) rows
+  constexpr int NREC = (RB / 1024 + 1) / 2;     // record blocks per output wave (wave 3 repeats its last)
+  constexpr int NDMA = 2 * NKQ + 2 + NREC;      // copies per output wave per chunk
+  static_assert(RB % 1024 == 0, "record of whole 1 KiB blocks");
+  __shared__ __attribute__((aligned(16))) T Ks[3 * KB];
+  __shared__ __attribute__((aligned(16))) T Qs[3 * KB];
+  __shared__ __attribute__((aligned(16))) T Vs[3 * VB];
+  __shared__ __attribute__((aligned(16))) char Rs[3 * RB];
+  __shared__ u32x4 SFs[2][KS][64];   // chain wave w: the state fragments at the current chunk's entry
+  __shared__ u32x4 UFs[2][2][64];    // chain wave w: U fragments of the current chunk
+
+  if (a.seg_mode != 2) gdn_signal_start(a);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool chain = wave < 2;
+  const int pw = wave & 1;           // column half: chain wave pw and output wave 2 + pw share it
+  const int g = lane >> 4, c16 = lane & 15;
+  const int bh = blockIdx.x, b = bh / a.H, h = bh % a.H, hk = h / a.G;
+  const int vw = 32 * blockIdx.y;    // the workgroup's 32 state columns
+  const int v0 = vw + 16 * pw;       // this wave pair's 16
+  const int seg = blockIdx.z;
+  const int c_begin = seg * a.seg_len, c_end = min(a.NC, c_begin + a.seg_len);
+
+  // ---- chain: state tile t, register i <-> row k = 32 (t/2) + 8g + 4 (t%2) + i, column v0 + c16
+  f32x4 S[ST];
+  u32x4 sf[KS];
+  if (chain) {
+#pragma unroll
+    for (int t = 0; t < ST; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kx = 32 * (t >> 1) + 8 * g + 4 * (t & 1) + i;
+        float x;
+        if (a.seg_mode == 0) x = a.s0 ? a.s0[((int64_t)bh * D + kx) * D + v0 + c16] : 0.f;
+        else x = a.seg_in[(((int64_t)bh * a.nseg + seg) * D + kx) * D + v0 + c16];
+        S[t][i] = x;
+      }
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      sf[s] = pack8<T>(S[2 * s], S[2 * s + 1]);
+      SFs[pw][s][lane] = sf[s];
+    }
+  }
+
+  // ---- lane parts of the LDS addresses (elements; tile and slot offsets are immediates),
+  // as in gdn_scan16_kernel
+  const int ksw = lds_swizzle<CPR>(c16);
+  int kAo[KS], qBo[KS], kTo[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    kAo[s] = c16 * D + 8 * ((4 * s + g) ^ ksw);
+    qBo[s] = c16 * D + 8 * ((4 * s + g) ^ rec_swizzle<CPR>(c16));
+    const int r0 = 4 * g + (c16 >> 2);
+    kTo[s] = r0 * D + 8 * ((4 * s + (c16 & 3)) ^ lds_swizzle<CPR>(r0));
+  }
+  const int vo = (4 * g + (c16 >> 2)) * 32 + 16 * pw + 4 * (c16 & 3);
+
+  // ---- copies (output waves): wave 2 + w copies k and q rows 32w .. 32w + 31, v slab rows
+  // 32w .. 32w + 31 and half of the record's 1 KiB blocks (wave 3 copies its last block
+  // twice when the count is odd).  Rows past T read as zeros.
+  const int cw = wave & 1;
+  const uint32_t kst2 = (uint32_t)a.k_st * 2u, qst2 = (uint32_t)a.q_st * 2u, vst2 = (uint32_t)a.v_st * 2u;
+  uint32_t kvo[NKQ], qvo[NKQ], vvo[2];
+#pragma unroll
+  for (int r = 0; r < NKQ; ++r) {
+    const int row = 32 * cw + RPI * r + lane / CPR, pc = lane % CPR;
+    kvo[r] = row * kst2 + 16u * (pc ^ lds_swizzle<CPR>(row));
+    qvo[r] = row * qst2 + 16u * (pc ^ rec_swizzle<CPR>(row));
+  }
+#pragma unroll
+  for (int r = 0; r < 2; ++r) vvo[r] = (32 * cw + 16 * r + lane / 4) * vst2 + 16u * (lane % 4);
+  const uint32_t rvo = 16u * lane;
+  const T* kb = (const T*)a.k + b * a.k_sb + hk * a.k_sh;
+  const T* qb = (const T*)a.q + b * a.q_sb + h * a.q_sh;
+  const T* vb = (const T*)a.v + b * a.v_sb + hk * a.v_sh + vw;
+  const char* rb0 = (const char*)a.ws + (int64_t)bh * a.NC * RB;
+  const int last = c_end - 1;
+  const uint32_t mk = __builtin_amdgcn_readfirstlane(lds_offset(Ks + 32 * cw * D));
+  const uint32_t mq = __builtin_amdgcn_readfirstlane(lds_offset(Qs + 32 * cw * D));
+  const uint32_t mv = __builtin_amdgcn_readfirstlane(lds_offset(Vs + 32 * cw * 32));
+  const uint32_t mr = __builtin_amdgcn_readfirstlane(lds_offset(Rs));
+  auto copy_chunk = [&](int j, auto slot_c) {
+    constexpr int sl = decltype(slot_c)::value;
+    const int rows = min(a.T - j * C, C);
+    const auto krs = buffer_rsrc(kb + (int64_t)j * C * a.k_st, (uint32_t)((rows - 1) * a.k_st + D) * 2u);
+    const auto qrs = buffer_rsrc(qb + (int64_t)j * C * a.q_st, (uint32_t)((rows - 1) * a.q_st + D) * 2u);
+    const auto vrs = buffer_rsrc(vb + (int64_t)j * C * a.v_st, (uint32_t)((rows - 1) * a.v_st + 32) * 2u);
+    const auto rrs = buffer_rsrc(rb0 + (int64_t)j * RB, RB);
+#pragma unroll
+    for (int r = 0; r < NKQ; ++r) {
+      dma_buf16_at(krs, kvo[r], 0, mk + (sl * KB + RPI * r * D) * 2);
+      dma_buf16_at(qrs, qvo[r], 0, mq + (sl * KB + RPI * r * D) * 2);
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) dma_buf16_at(vrs, vvo[r], 0, mv + (sl * VB + 16 * r * 32) * 2);
+#pragma unroll
+    for (int r = 0; r < NREC; ++r) {
+      const uint32_t blk = (uint32_t)min(NREC * cw + r, RB / 1024 - 1) * 1024u;
+      dma_buf16_at(rrs, rvo, blk, mr + sl * RB + blk);
+    }
+  };
+
+  const auto orsrc = buffer_rsrc((const T*)a.o + (int64_t)b * a.T * a.H * D, (uint32_t)((int64_t)a.T * a.H * D * 2));
+  const uint32_t oo = (uint32_t)((c16 * a.H + h) * D + v0 + 4 * g) * 2u;
+  const uint32_t otok = (uint32_t)a.H * D * 2u;
+  f32x4 o[4];
+
+  auto body = [&](int c, auto slot_c) {
+    constexpr int sl = decltype(slot_c)::value;
+    // B0: the output waves' copies of chunk c have landed (only chunk c + 1's and the
+    // previous chunk's stores may be in flight; loads complete in order), the chain's S_c
+    // fragments are written
+    wait_vmcnt<NDMA>();
+    __syncthreads();
+    const T* Kl = Ks + sl * KB;
+    const T* Ql = Qs + sl * KB;
+    const T* Vl = Vs + sl * VB;
+    const char* Rl = Rs + sl * RB;
+    const float* Fp = (const float*)(Rl + kGdn16F);
+    const u32x4* Tb = (const u32x4*)(Rl + kGdn16Tb);
+    const u32x4* Rb = (const u32x4*)(Rl + kGdn16Rb);
+    f32x4 ks[4];
+    u32x4 ukf[2], kT[2][ST];
+    if (chain) {
+      // (1) gC, then the k rows as A fragments of K S (tile p: row 16p + c16); LDS reads
+      // return in order, so the first product waits for gC and its own two fragments only
+      const float gC = Fp[192];
+      u32x4 kA[4][KS];
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int s = 0; s < KS; ++s) kA[p][s] = lds16(Kl + 16 * p * D + kAo[s]);
+      __builtin_amdgcn_sched_barrier(0);
+      // (2) K S (S_c as B fragments) with S <- gC S and the reads X and U need (v by
+      // transposing reads of the slab in the token slot order, geik, kf, T diag(beta))
+      // issued between the products
+#pragma unroll
+      for (int p = 0; p < 4; ++p) ks[p] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int p = 0; p < 4; ++p) ks[p] = mfma16x16x32<T>(kA[p][s], sf[s], ks[p]);
+#pragma unroll
+      for (int t = 0; t < ST; ++t) S[t] *= gC;
+      u32x2 vlo[2], vhi[2];
+      f32x4 wl[2], wh[2], kl[2], kh[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        vlo[j] = lds_read_tr16(Vl + 32 * j * 32 + vo);
+        vhi[j] = lds_read_tr16(Vl + (32 * j + 16) * 32 + vo);
+        wl[j] = *(const f32x4*)(Fp + 64 + 32 * j + 4 * g);
+        wh[j] = *(const f32x4*)(Fp + 64 + 32 * j + 16 + 4 * g);
+      }
+      u32x4 tb[6];
+#pragma unroll
+      for (int f = 0; f < 6; ++f) tb[f] = Tb[f * 64 + lane];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        kl[j] = *(const f32x4*)(Fp + 32 * j + 4 * g);
+        kh[j] = *(const f32x4*)(Fp + 32 * j + 16 + 4 * g);
+      }
+#pragma unroll
+      for (int i = 0; i < 4 * KS; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // a product
+        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // two decay multiplies
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // a read
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // (3) K^T's A fragments of the update by transposing reads, issued under X and U (for
+      // tile t, lane c16 supplies row r0 + c16 / 4 and the 4 columns 32 (t/2) + 8 (c16 % 4)
+      // + 4 (t%2) .., so lane r receives the state row of tile t)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int t = 0; t < ST; ++t) {
+          const T* pl = Kl + 32 * j * D + kTo[t >> 1] + 4 * (t & 1);
+          const u32x2 lo = lds_read_tr16(pl);
+          const u32x2 hi = lds_read_tr16(pl + 16 * D);
+          kT[j][t] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
+      // (4) X = V - geik K S as B fragments over token steps j
+      u32x4 xf[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        f32x4 xl, xh;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          xl[i] = elem16x2<T>(vlo[j], i) - wl[j][i] * ks[2 * j][i];
+          xh[i] = elem16x2<T>(vhi[j], i) - wh[j][i] * ks[2 * j + 1][i];
+        }
+        xf[j] = pack8<T>(xl, xh);
+      }
+      // (6) U = T diag(beta) X (tile P = tokens 16P + 4g + i), plain for the output wave and
+      // weighted by kf for the update
+      const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+      f32x4 U[4];
+      U[0] = mfma16x16x32<T>(tb[0], xf[0], z);
+      U[1] = mfma16x16x32<T>(tb[1], xf[0], z);
+      U[2] = mfma16x16x32<T>(tb[2], xf[0], z);
+      U[3] = mfma16x16x32<T>(tb[4], xf[0], z);
+      U[2] = mfma16x16x32<T>(tb[3], xf[1], U[2]);
+      U[3] = mfma16x16x32<T>(tb[5], xf[1], U[3]);
+#pragma unroll
+      for (int i = 0; i < 2 * ST; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 1);  // two transposing reads
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 1);  // X
+      }
+#pragma unroll
+      for (int i = 0; i < 6; ++i) __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        UFs[pw][j][lane] = pack8<T>(U[2 * j], U[2 * j + 1]);
+        ukf[j] = pack8<T>(U[2 * j] * kl[j], U[2 * j + 1] * kh[j]);
+      }
+    } else {
+      // chunk c + 2 goes to the slot chunk c - 1 used (every wave is past B0); past the last
+      // chunk the copies repeat it, so every step issues the same count
+      copy_chunk(min(c + 2, last), std::integral_constant<int, (sl + 2) % 3>{});
+      // q rows as B fragments of S^T Q^T (tile p': row 16p' + c16), S_c's fragments from the
+      // chain partner; O^T tile p' (rows = columns v0 + 4g + i, cols = tokens 16p' + c16)
+      u32x4 qB[4][KS];
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int s = 0; s < KS; ++s) qB[p][s] = lds16(Ql + 16 * p * D + qBo[s]);
+#pragma unroll
+      for (int s = 0; s < KS; ++s) sf[s] = SFs[pw][s][lane];
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) o[pp] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) o[pp] = mfma16x16x32<T>(sf[s], qB[pp][s], o[pp]);
+    }
+    // B1: U_c's fragments are written; every read of S_c's is done
+    __syncthreads();
+    if (chain) {
+      // (7) S += K^T diag(kf) U, then S_{c+1}'s fragments
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int t = 0; t < ST; ++t) S[t] = mfma16x16x32<T>(kT[j][t], ukf[j], S[t]);
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        sf[s] = pack8<T>(S[2 * s], S[2 * s + 1]);
+        SFs[pw][s][lane] = sf[s];
+      }
+    } else {
+      // output, second term: + U^T Rq^T, scaled first term by geqs of the token; 8-byte
+      // row pieces O[token][v0 + 4g ..] (the whole offset in the lane's voffset: only that
+      // part is range-checked, rows past T are dropped)
+      u32x4 uf[2], rq[6];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) uf[j] = UFs[pw][j][lane];
+#pragma unroll
+      for (int f = 0; f < 6; ++f) rq[f] = Rb[f * 64 + lane];
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        f32x4 x = o[pp] * Fp[128 + 16 * pp + c16];
+        if (pp < 2) {
+          x = mfma16x16x32<T>(uf[0], rq[pp], x);
+        } else {
+          x = mfma16x16x32<T>(uf[0], rq[2 * pp - 2], x);
+          x = mfma16x16x32<T>(uf[1], rq[2 * pp - 1], x);
+        }
+        const u32x2 pk = {pack2<T>(x[0], x[1]), pack2<T>(x[2], x[3])};
+        __builtin_amdgcn_raw_buffer_store_b64(pk, orsrc, oo + (uint32_t)(c * C + 16 * pp) * otok, 0, 0);
+      }
+    }
+  };
+
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  if (!chain) {
+    copy_chunk(c_begin, S0{});
+    copy_chunk(min(c_begin + 1, last), S1{});
+  }
+  for (int c = c_begin; c < c_end; c += 3) {
+    body(c, S0{});
+    if (c + 1 < c_end) body(c + 1, S1{});
+    if (c + 2 < c_end) body(c + 2, S2{});
+  }
+
+  if (chain && seg == a.nseg - 1 && a.s_out) {
+    float* sdst = a.s_out + (int64_t)bh * D * D;
+#pragma unroll
+    for (int t = 0; t < ST; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kx = 32 * (t >> 1) + 8 * g + 4 * (t & 1) + i;
+        sdst[kx * D + v0 + c16] = S[t][i];
+      }
+  }
+  // the copies issued past the last chunk land before the workgroup's LDS is released
+  wait_vmcnt<0>();
+}
+
 // Entry states of the segments from their summaries (fp32): seg_in[0] = s0 (or 0) and
 // seg_in[s] = M_{s-1} seg_in[s-1] + B_{s-1}, where summary s - 1 holds [B | M] row by row.
 // One workgroup per (sequence-head, 16 state columns); M is staged in LDS (rows padded
@@ -715,7 +1031,7 @@ static int launch16(const GdnArgs& a0, hipStream_t s) {
   gdn16_plan(BH, a.NC, D, a.nseg, a.seg_len);
   if (a.nseg == 1) {
     a.seg_mode = 0;
-    gdn_scan16_kernel<T, D, true><<<dim3((unsigned)BH, D / 32, 1), dim3(128), 0, s>>>(a);
+    gdn_scan16_pair_kernel<T, D><<<dim3((unsigned)BH, D / 32, 1), dim3(256), 0, s>>>(a);
     return check_launch("chunk_gated_delta_rule(scan16)");
   }
   // long sequences with few heads: segment summaries, their entry states, then the replays
@@ -729,7 +1045,7 @@ static int launch16(const GdnArgs& a0, hipStream_t s) {
   rc = check_launch("chunk_gated_delta_rule(combine16)");
   if (rc) return rc;
   a.seg_mode = 2;
-  gdn_scan16_kernel<T, D, true><<<dim3((unsigned)BH, D / 32, a.nseg), dim3(128), 0, s>>>(a);
+  gdn_scan16_pair_kernel<T, D><<<dim3((unsigned)BH, D / 32, a.nseg), dim3(256), 0, s>>>(a);
   return check_launch("chunk_gated_delta_rule(replay16)");
 }
 
