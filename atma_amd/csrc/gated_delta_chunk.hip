@@ -371,6 +371,8 @@ extern "C" int atma_chunk_gated_delta_rule(
                   v_st < dv))
     // the kernels copy a chunk's q / k / v rows through one buffer descriptor each
     return set_error(ATMA_ERR_UNSUPPORTED, "chunk_gated_delta_rule: q/k/v token stride out of range");
+  if (es == 2 && B * H * ((T + 63) / 64) >= (1ll << 31))  // the prep kernel indexes items in 32 bits
+    return set_error(ATMA_ERR_UNSUPPORTED, "chunk_gated_delta_rule: B*H*chunks too large");
   const size_t need = atma_chunk_gated_delta_workspace_bytes(B, T, H, dk, dv, chunk, dtype);
   if (!workspace || workspace_bytes < need)
     return set_error(ATMA_ERR_WORKSPACE, "chunk_gated_delta_rule: workspace %zu < %zu bytes",

@@ -47,6 +47,20 @@ __device__ __forceinline__ float elem16x2(const u32x2& x, int e) {
   return (float)__builtin_bit_cast(T, u);
 }
 
+// acc + x.lo^2 + x.hi^2 for a packed pair of 16-bit values (v_dot2_f32_bf16 / _f16).
+template <typename T>
+__device__ __forceinline__ float dot2_sq(uint32_t x, float acc) {
+  if constexpr (std::is_same_v<T, bf16>) {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    const v2 v = __builtin_bit_cast(v2, x);
+    return __builtin_amdgcn_fdot2_f32_bf16(v, v, acc, false);
+  } else {
+    typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+    const v2 v = __builtin_bit_cast(v2, x);
+    return __builtin_amdgcn_fdot2(v, v, acc, false);
+  }
+}
+
 // Eight floats (two accumulator tiles) -> one 16-byte MFMA fragment.
 template <typename T>
 __device__ __forceinline__ u32x4 pack8(const f32x4& lo, const f32x4& hi) {
@@ -70,23 +84,29 @@ __global__ void __launch_bounds__(256) gdn_prep16_kernel(GdnArgs a) {
   constexpr int C = kChunk, KS = D / 32;
   __shared__ __attribute__((aligned(16))) float Nb[4][4 * 256];  // per wave: N^T of the diagonal blocks
   __shared__ __attribute__((aligned(16))) float Mb[4][4 * 256];  // per wave: T^T of the diagonal blocks
-  __shared__ __attribute__((aligned(16))) float Tk[4][4][C];     // per wave: lg, beta, ik, iq of each token
+  __shared__ __attribute__((aligned(16))) float Tk[4][6][C];     // per wave: per-token factors (below)
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = lane >> 4, c16 = lane & 15;
-  const int64_t item = (int64_t)blockIdx.x * 4 + wave;
-  if (item >= (int64_t)a.B * a.H * a.NC) return;  // a whole wave; the kernel has no barrier
-  const int bh = (int)(item / a.NC), c = (int)(item % a.NC);
+  const uint32_t item = blockIdx.x * 4u + (uint32_t)wave;  // B H NC < 2^31 (the entry checks)
+  if (item >= (uint32_t)(a.B * a.H * a.NC)) return;          // a whole wave; the kernel has no barrier
+  const int bh = (int)(item / (uint32_t)a.NC), c = (int)(item % (uint32_t)a.NC);
   const int b = bh / a.H, h = bh % a.H;
   const int rows = min(a.T - c * C, C);
-  float* tlg = Tk[wave][0];
-  float* tbt = Tk[wave][1];
-  float* tik = Tk[wave][2];
-  float* tiq = Tk[wave][3];
+  float* tbt = Tk[wave][0];   // beta
+  float* tik = Tk[wave][1];   // 1 / |k| (1 without l2norm, 0 past T)
+  float* tiq = Tk[wave][2];   // scale / |q|
+  // exponents (base 2) that fold the row-norm, write-strength and decay factors of a scaled
+  // Gram entry into one exp2: aq = lg log2e + log2 iq, ak = lg log2e + log2(beta ik),
+  // bk = lg log2e - log2 ik, so Rq[p,s] = exp2(aq_p - bk_s) q_p.k_s and A[p,s] =
+  // exp2(ak_p - bk_s) k_p.k_s (a zero factor gives -inf / +inf, hence an exact 0)
+  float* taq = Tk[wave][3];
+  float* tak = Tk[wave][4];
+  float* tbk = Tk[wave][5];
   float* nb = Nb[wave];
   float* mb = Mb[wave];
-  char* rec = (char*)a.ws + item * kGdn16RecBytes;
+  char* rec = (char*)a.ws + (size_t)item * kGdn16RecBytes;
 
   // ---- k and q rows as MFMA fragments: lane (g, r) holds row 16p + r, columns 32s + 8g ..
   // (rows past T read as zeros)
@@ -116,10 +136,10 @@ __global__ void __launch_bounds__(256) gdn_prep16_kernel(GdnArgs a) {
     const float y = __shfl_up(lg, off, 64);
     if (lane >= off) lg += y;
   }
-  tlg[lane] = lg;
   tbt[lane] = bt;
 
-  // ---- row norms: partial sums over this lane's columns, then over the four lane groups
+  // ---- row norms: partial sums over this lane's columns (packed pairs, v_dot2), then over
+  // the four lane groups
   float nk[4], nq[4];
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
@@ -127,10 +147,9 @@ __global__ void __launch_bounds__(256) gdn_prep16_kernel(GdnArgs a) {
 #pragma unroll
     for (int s = 0; s < KS; ++s)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = elem16<T>(kf[p][s], e), y = elem16<T>(qf[p][s], e);
-        nk[p] = fmaf(x, x, nk[p]);
-        nq[p] = fmaf(y, y, nq[p]);
+      for (int e = 0; e < 4; ++e) {
+        nk[p] = dot2_sq<T>(kf[p][s][e], nk[p]);
+        nq[p] = dot2_sq<T>(qf[p][s][e], nq[p]);
       }
     nk[p] += __shfl_xor(nk[p], 16, 64);
     nq[p] += __shfl_xor(nq[p], 16, 64);
@@ -148,8 +167,12 @@ __global__ void __launch_bounds__(256) gdn_prep16_kernel(GdnArgs a) {
   }
   wave_sync();
 
-  // ---- per-token factors of the scan
+  // ---- per-token factors of the scan and the folded exponents
   {
+    const float l2 = lg * kLog2e, ik = tik[lane], iq = tiq[lane];
+    taq[lane] = l2 + __builtin_amdgcn_logf(iq);
+    tak[lane] = l2 + __builtin_amdgcn_logf(bt * ik);
+    tbk[lane] = l2 - __builtin_amdgcn_logf(ik);
     const float lgC = __shfl(lg, 63, 64);
     const float ge = __builtin_amdgcn_exp2f(lg * kLog2e);
     float* F = (float*)(rec + kGdn16F);
@@ -184,17 +207,14 @@ __global__ void __launch_bounds__(256) gdn_prep16_kernel(GdnArgs a) {
 #pragma unroll
     for (int P = 0; P < 4; ++P) {
       const int pt = 16 * P + c16;
-      const float lgp = tlg[pt], iqp = tiq[pt];
+      const float ap = taq[pt];
 #pragma unroll
       for (int S = 0; S <= P; ++S) {
-        const f32x4 lgs = *(const f32x4*)(tlg + 16 * S + 4 * g);
-        const f32x4 iks = *(const f32x4*)(tik + 16 * S + 4 * g);
+        const f32x4 bs = *(const f32x4*)(tbk + 16 * S + 4 * g);
         f32x4 v;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float dec = __builtin_amdgcn_exp2f((lgp - lgs[i]) * kLog2e);
-          v[i] = (16 * S + 4 * g + i <= pt) ? dec * iqp * iks[i] * gq[tri(S, P)][i] : 0.f;
-        }
+        for (int i = 0; i < 4; ++i)
+          v[i] = (16 * S + 4 * g + i <= pt) ? __builtin_amdgcn_exp2f(ap - bs[i]) * gq[tri(S, P)][i] : 0.f;
         rq[tri(S, P)] = v;
       }
     }
@@ -213,32 +233,24 @@ __global__ void __launch_bounds__(256) gdn_prep16_kernel(GdnArgs a) {
   f32x4 at[10];
 #pragma unroll
   for (int P = 1; P < 4; ++P) {
-    const int t = 16 * P + c16;
-    const float lgt = tlg[t], wt = tbt[t] * tik[t];
+    const float at_ = tak[16 * P + c16];
 #pragma unroll
     for (int k = 0; k < P; ++k) {
-      const f32x4 lgu = *(const f32x4*)(tlg + 16 * k + 4 * g);
-      const f32x4 iku = *(const f32x4*)(tik + 16 * k + 4 * g);
+      const f32x4 bu = *(const f32x4*)(tbk + 16 * k + 4 * g);
       f32x4 v;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        v[i] = wt * iku[i] * __builtin_amdgcn_exp2f((lgt - lgu[i]) * kLog2e) * gk[tri(k, P)][i];
+      for (int i = 0; i < 4; ++i) v[i] = __builtin_amdgcn_exp2f(at_ - bu[i]) * gk[tri(k, P)][i];
       at[tri(k, P)] = v;
     }
   }
 #pragma unroll
   for (int P = 0; P < 4; ++P) {
-    const int u = 16 * P + c16;
-    const float lgu = tlg[u], iku = tik[u];
-    const f32x4 lgr = *(const f32x4*)(tlg + 16 * P + 4 * g);
-    const f32x4 btr = *(const f32x4*)(tbt + 16 * P + 4 * g);
-    const f32x4 ikr = *(const f32x4*)(tik + 16 * P + 4 * g);
+    const float bu = tbk[16 * P + c16];
+    const f32x4 ar = *(const f32x4*)(tak + 16 * P + 4 * g);
     f32x4 v;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float dec = __builtin_amdgcn_exp2f((lgr[i] - lgu) * kLog2e);  // discarded above the diagonal
-      v[i] = (c16 < 4 * g + i) ? btr[i] * ikr[i] * iku * dec * gk[tri(P, P)][i] : 0.f;
-    }
+    for (int i = 0; i < 4; ++i)  // (the exponent is discarded above the diagonal)
+      v[i] = (c16 < 4 * g + i) ? __builtin_amdgcn_exp2f(ar[i] - bu) * gk[tri(P, P)][i] : 0.f;
     *(f32x4*)(nb + P * 256 + c16 * 16 + 4 * g) = v;  // N^T[c][4g + i] = N[4g + i][c]
   }
   wave_sync();
