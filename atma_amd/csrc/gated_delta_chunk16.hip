@@ -16,13 +16,15 @@
 //    levels of fp32 block products, then the record (T diag(beta) and Rq as MFMA
 //    fragments, per-token factors; 14 KiB, layout in gated_delta.h).
 //
-//  pass 2, gdn_scan16 -- one workgroup of two waves per (sequence, head, 32-column slab
-//    of the state); each wave owns 16 whole columns, and the columns of the recurrence
-//    are independent, so a chunk step needs no exchange between waves.  Per chunk a wave
-//    runs K S (16 MFMAs) -> X -> U = T diag(beta) X (6) -> S update (16) in registers, and
-//    the output O^T = S^T Q^T diag(geqs) + U^T Rq^T (22) beside the chain.  The k, q rows,
-//    the v slab and the record of chunk c + 2 stream into a third LDS slot (direct buffer
-//    copies) while chunk c computes; one workgroup barrier per chunk guards the slots.
+//  pass 2, gdn_scan16_pair -- one workgroup of four waves per (sequence, head, 32-column
+//    slab of the state).  The columns of the recurrence are independent: each of two chain
+//    waves owns 16 whole columns and runs K S (16 MFMAs) -> X -> U = T diag(beta) X (6) ->
+//    S update (16) in registers; each of two output waves computes the same columns'
+//    O^T = S^T Q^T diag(geqs) + U^T Rq^T (22) from the state and U fragments the chain hands
+//    over in LDS, and issues the copies: the k, q rows, the v slab and the record of chunk
+//    c + 2 stream into a third LDS slot (direct buffer copies) while chunk c computes.  Two
+//    workgroup barriers per chunk order the slots and the hand-over.  Segment summaries (no
+//    output) run the two-wave gdn_scan16 with the chain and the copies on the same waves.
 //
 // Fragment layouts (v_mfma_f32_16x16x32: A lane (g, r) holds row r, k = 8g + [0, 8); B lane
 // (g, c) holds column c, same k; accumulator lane (g, c) register i holds row 4g + i,
