@@ -1043,6 +1043,13 @@ static int launch16(const GdnArgs& a0, hipStream_t s) {
   int rc = check_launch("chunk_gated_delta_rule(prep16)");
   if (rc) return rc;
   gdn16_plan(BH, a.NC, D, a.nseg, a.seg_len);
+  // with a start flag the caller runs another kernel beside the recurrence (the overlapped
+  // prefill): the plain scan's few workgroups then run beside it, where the segment passes
+  // would take every CU first
+  if (a.start_flag) {
+    a.nseg = 1;
+    a.seg_len = a.NC;
+  }
   if (a.nseg == 1) {
     a.seg_mode = 0;
     gdn_scan16_pair_kernel<T, D><<<dim3((unsigned)BH, D / 32, 1), dim3(256), 0, s>>>(a);

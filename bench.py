@@ -140,11 +140,11 @@ def _time(torch, fn, steps, warmup):
 def bench_prefill(torch, dev, B, T, steps, warmup):
     w = Prefill(torch, dev, B, T)
     fp, fg = w.flops()
-    # about 20 ms of steps first, so every timed leg runs at the GPU's steady clocks;
+    # about 60 ms of steps first, so every timed leg runs at the GPU's steady clocks;
     # then the component legs, then the step in the layer's schedule: `warmup` untimed
     # steps and `steps` timed ones
     one = _time(torch, w.step, 1, 1)
-    _time(torch, w.step, max(1, int(20.0 / max(one, 1e-3))), 0)
+    _time(torch, w.step, max(1, int(60.0 / max(one, 1e-3))), 0)
     ms_polar = _time(torch, w.polar, steps, max(1, warmup // 2))
     ms_gdn = _time(torch, w.memory, steps, max(1, warmup // 2))
     ms_seq = _time(torch, w.step_sequential, steps, max(1, warmup // 2))

@@ -448,7 +448,9 @@ size_t atma_chunk_gated_delta_workspace_bytes(int64_t B, int64_t T, int64_t H, i
  * FLA counterpart: one launch fewer for TitansMemory).  chunk must be 64;
  * dk = dv = 128 or 64.  start_flag (nullable; no FLA counterpart): the recurrence
  * kernel's first workgroup stores start_epoch there as it starts, for
- * atma_wait_start_flag.
+ * atma_wait_start_flag; with a flag, 16-bit inputs take the unsegmented recurrence
+ * (one workgroup per sequence-head and 32 columns, to run beside the caller's other
+ * kernel), whose results can differ from the segmented one's in rounding.
  */
 int atma_chunk_gated_delta_rule(const void* q, int64_t q_sb, int64_t q_st, int64_t q_sh,
                                 const void* k, int64_t k_sb, int64_t k_st, int64_t k_sh,

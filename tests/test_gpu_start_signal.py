@@ -1,10 +1,14 @@
 """The recurrence start signal used by the overlapped prefill schedule: the gated-delta
 recurrence kernel raises it as it starts, the one-wave wait kernel returns on it or after
 its time limit (forced here from the host with a flag that is never raised), and the
-overlapped schedule gives the same bits as the sequential one."""
+overlapped schedule gives the same bits as the same kernels run back to back (with a start
+signal the recurrence is unsegmented, so against the sequential schedule's segmented
+recurrence the memory output agrees to rounding)."""
 
 import pytest
 import torch
+
+from helpers import rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -23,6 +27,8 @@ def test_wait_returns_on_the_flag_or_after_the_limit(dev):
     sig = StartSignal(dev)
     sig.arm()
     sig.flag.fill_(sig.epoch)
+    sig.wait(timeout_us=500_000)   # untimed: the first launch loads the library's code objects
+    torch.cuda.synchronize()
     assert _elapsed_ms(lambda: sig.wait(timeout_us=500_000)) < 50.0   # already raised
     sig.arm()                                                        # never raised
     t = _elapsed_ms(lambda: sig.wait(timeout_us=3_000))
@@ -86,10 +92,13 @@ def test_overlapped_schedule_is_bitwise_the_sequential_one(dev, B, T):
                                       scale=1.0, use_qk_l2norm_in_kernel=True, gate_bias=(3.9, 0.0),
                                       output_final_state=True, start_signal=sig)
 
-    c0, m0 = polar_attention_fwd(q, k, v, n, **p)
-    o0, s0 = mem()
     sig, side = StartSignal(dev), torch.cuda.Stream(device=dev)
     main = torch.cuda.current_stream()
+    c0, m0 = polar_attention_fwd(q, k, v, n, **p)
+    sig.arm()
+    o0, s0 = mem(sig)       # the overlapped schedule's plan, back to back (nobody waits)
+    o2, s2 = mem()          # the sequential schedule's (segmented when T is long)
+    assert rel_err(o2.float(), o0.float()) <= 1e-2 and rel_err(s2, s0) <= 1e-3
     for _ in range(3):
         sig.arm()
         side.wait_stream(main)
