@@ -14,10 +14,11 @@
 // gradient dS and dY; every other gradient is a product within one chunk, formed by the
 // caller from these (dV = diag(beta) dY, the rest batched over chunks).
 //
-// MI355X mapping: one workgroup of 4 waves per (sequence-head, 64 state columns), each
-// wave owning 16 columns (the recurrence never mixes V columns).  The chunk's shared
-// operands -- k rows, k^T, q^T, T (forward) or T^T (backward), Rq^T, 64 x 64 or 64 x d
-// bf16 tiles the caller lays out -- are staged in LDS with rows padded by 16 bytes (the
+// MI355X mapping: one workgroup of kChainWaves waves per (sequence-head, 16 kChainWaves
+// state columns), each wave owning 16 columns (the recurrence never mixes V columns).
+// The chunk's shared operands -- k rows, k^T, q^T, T (forward) or T^T (backward), Rq^T,
+// 64 x 64 or 64 x d bf16 tiles the caller lays out -- are staged in LDS with rows padded
+// by 16 bytes (the
 // 16-lane fragment reads then touch 16 distinct bank groups).  Products run on
 // v_mfma_f32_16x16x32 (fp32 accumulation); the state and every per-column intermediate
 // (Y, U, dU, dY) go through a per-wave transposed bf16 buffer ([column][k], 16 bytes per
@@ -55,48 +56,58 @@ struct Bwd16ChainArgs {
   int BH, NC;
 };
 
-// A contiguous 16-bit tile of N * 256 16-byte chunks: thread tid holds chunks tid + 256 j.
-template <int N>
+// A contiguous 16-bit tile of N * NTH 16-byte chunks: thread tid (of NTH) holds chunks
+// tid + NTH j.
+template <int N, int NTH = 256>
 __device__ __forceinline__ void tile_load(u32x4 (&r)[N], const void* src, int tid) {
   const u32x4* s = (const u32x4*)src;
 #pragma unroll
-  for (int j = 0; j < N; ++j) r[j] = s[tid + 256 * j];
+  for (int j = 0; j < N; ++j) r[j] = s[tid + NTH * j];
 }
 // ... into LDS rows of CPR chunks, padded to PITCH elements
-template <int N, int CPR, int PITCH, typename T>
+template <int N, int CPR, int PITCH, int NTH = 256, typename T>
 __device__ __forceinline__ void tile_store(T* dst, const u32x4 (&r)[N], int tid) {
 #pragma unroll
   for (int j = 0; j < N; ++j) {
-    const int i = tid + 256 * j;
+    const int i = tid + NTH * j;
     *(u32x4*)(dst + (i / CPR) * PITCH + 8 * (i % CPR)) = r[j];
   }
 }
 
+// Waves (16 state columns each) per workgroup of the chain kernel: two, so a configs[1]
+// shape (64 sequence-heads, d = 128) runs 256 workgroups, one per CU (the LDS of one
+// workgroup's tiles allows no second).
+constexpr int kChainWaves = 2;
+
 template <typename T, int D>
-__global__ void __launch_bounds__(256, 1) gdn_bwd16_chain_kernel(Bwd16ChainArgs a) {
+__global__ void __launch_bounds__(64 * kChainWaves, 1) gdn_bwd16_chain_kernel(Bwd16ChainArgs a) {
+  constexpr int NW = kChainWaves, NTH = 64 * NW, WC = 16 * NW;  // waves, threads, columns
   constexpr int C = 64, PD = D + 8, PC = C + 8;  // padded LDS pitches (elements)
   constexpr int KS = D / 32;                      // 32-wide k steps over D
   constexpr int DT = D / 16;                      // 16-row tiles over D
+  static_assert(D % WC == 0 && 4 * C % NTH == 0, "whole column slabs and factor rows");
   __shared__ __attribute__((aligned(16))) T Kr[C * PD];
   __shared__ __attribute__((aligned(16))) T Kt[D * PC];
   __shared__ __attribute__((aligned(16))) T Qt[D * PC];
   __shared__ __attribute__((aligned(16))) T Tm[C * PC];  // T in the forward chain, T^T in the backward
   __shared__ __attribute__((aligned(16))) T Rt[C * PC];
   __shared__ float Fs[4 * C];
-  __shared__ __attribute__((aligned(16))) T Sb[4][16 * PD];  // S^T / dS^T of the wave's columns
-  __shared__ __attribute__((aligned(16))) T X1[4][16 * PC];
-  __shared__ __attribute__((aligned(16))) T X2[4][16 * PC];
-  __shared__ __attribute__((aligned(16))) T XO[4][16 * PC];  // dO^T rows of the wave's columns
-  __shared__ __attribute__((aligned(16))) T XG[4][16 * PC];  // (Ga dO)^T rows
+  __shared__ __attribute__((aligned(16))) T Sb[NW][16 * PD];  // S^T / dS^T of the wave's columns
+  __shared__ __attribute__((aligned(16))) T X1[NW][16 * PC];
+  __shared__ __attribute__((aligned(16))) T X2[NW][16 * PC];
+  __shared__ __attribute__((aligned(16))) T XO[NW][16 * PC];  // dO^T rows of the wave's columns
+  __shared__ __attribute__((aligned(16))) T XG[NW][16 * PC];  // (Ga dO)^T rows
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, c16 = lane & 15;
-  const int bh = blockIdx.x / (D / 64);
-  const int v0 = 64 * (blockIdx.x % (D / 64)) + 16 * wave;  // the wave's first column
+  const int bh = blockIdx.x / (D / WC);
+  const int v0 = WC * (blockIdx.x % (D / WC)) + 16 * wave;  // the wave's first column
   const int col = v0 + c16;                                  // the lane's column (C layout)
 
-  constexpr int NT = D / 32;  // chunks per thread of a 64 x D or D x 64 tile
+  constexpr int NT = C * D / 8 / NTH;   // chunks per thread of a 64 x D or D x 64 tile
+  constexpr int NTM = C * C / 8 / NTH;  // ... of a 64 x 64 tile
+  constexpr int NF = 4 * C / NTH;       // factor entries per thread
   // the wave's 16 rows of a [D][64] tile: 2 chunks per lane
   auto rows16_load = [&](u32x4 (&r)[2], const void* src) {
     const u32x4* s = (const u32x4*)src;
@@ -131,14 +142,15 @@ __global__ void __launch_bounds__(256, 1) gdn_bwd16_chain_kernel(Bwd16ChainArgs 
       S[t][i] = a.s0 ? a.s0[((int64_t)bh * D + rows_of(t, i)) * D + col] : 0.f;
 
   // the next chunk's operands are loaded into registers while this one computes
-  u32x4 rk[NT], rkt[NT], rtm[2];
+  u32x4 rk[NT], rkt[NT], rtm[NTM];
   u32x2 rv[4];
-  float rf;
+  float rf[NF];
   auto fwd_load = [&](int64_t n) {
-    tile_load(rk, (const T*)a.kr + n * C * D, tid);
-    tile_load(rkt, (const T*)a.kt + n * D * C, tid);
-    tile_load(rtm, (const T*)a.tm + n * C * C, tid);
-    rf = a.f[n * kFRows * C + tid];
+    tile_load<NT, NTH>(rk, (const T*)a.kr + n * C * D, tid);
+    tile_load<NT, NTH>(rkt, (const T*)a.kt + n * D * C, tid);
+    tile_load<NTM, NTH>(rtm, (const T*)a.tm + n * C * C, tid);
+#pragma unroll
+    for (int j = 0; j < NF; ++j) rf[j] = a.f[n * kFRows * C + tid + NTH * j];
     const T* vrow = (const T*)a.vt + (n * D + col) * C;
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) rv[rt] = *(const u32x2*)(vrow + 16 * rt + 4 * g);
@@ -147,10 +159,11 @@ __global__ void __launch_bounds__(256, 1) gdn_bwd16_chain_kernel(Bwd16ChainArgs 
   for (int c = 0; c < a.NC; ++c) {
     const int64_t n = (int64_t)bh * a.NC + c;
     __syncthreads();  // every wave is done with the previous chunk's tiles
-    tile_store<NT, D / 8, PD>(Kr, rk, tid);
-    tile_store<NT, 8, PC>(Kt, rkt, tid);
-    tile_store<2, 8, PC>(Tm, rtm, tid);
-    Fs[tid] = rf;
+    tile_store<NT, D / 8, PD, NTH>(Kr, rk, tid);
+    tile_store<NT, 8, PC, NTH>(Kt, rkt, tid);
+    tile_store<NTM, 8, PC, NTH>(Tm, rtm, tid);
+#pragma unroll
+    for (int j = 0; j < NF; ++j) Fs[tid + NTH * j] = rf[j];
     f32x4 Vc[4];  // v of the lane's column, C layout (rows = tokens)
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
@@ -232,14 +245,15 @@ __global__ void __launch_bounds__(256, 1) gdn_bwd16_chain_kernel(Bwd16ChainArgs 
     for (int i = 0; i < 4; ++i)
       dS[t][i] = a.dst ? a.dst[((int64_t)bh * D + rows_of(t, i)) * D + col] : 0.f;
 
-  u32x4 rq[NT], rrt[2], ro[2], rgo[2];
+  u32x4 rq[NT], rrt[NTM], ro[2], rgo[2];
   auto bwd_load = [&](int64_t n) {
-    tile_load(rk, (const T*)a.kr + n * C * D, tid);
-    tile_load(rkt, (const T*)a.kt + n * D * C, tid);
-    tile_load(rq, (const T*)a.qt + n * D * C, tid);
-    tile_load(rtm, (const T*)a.tt + n * C * C, tid);
-    tile_load(rrt, (const T*)a.rt + n * C * C, tid);
-    rf = a.f[n * kFRows * C + tid];
+    tile_load<NT, NTH>(rk, (const T*)a.kr + n * C * D, tid);
+    tile_load<NT, NTH>(rkt, (const T*)a.kt + n * D * C, tid);
+    tile_load<NT, NTH>(rq, (const T*)a.qt + n * D * C, tid);
+    tile_load<NTM, NTH>(rtm, (const T*)a.tt + n * C * C, tid);
+    tile_load<NTM, NTH>(rrt, (const T*)a.rt + n * C * C, tid);
+#pragma unroll
+    for (int j = 0; j < NF; ++j) rf[j] = a.f[n * kFRows * C + tid + NTH * j];
     rows16_load(ro, (const T*)a.ot + (n * D + v0) * C);
     rows16_load(rgo, (const T*)a.got + (n * D + v0) * C);
   };
@@ -247,12 +261,13 @@ __global__ void __launch_bounds__(256, 1) gdn_bwd16_chain_kernel(Bwd16ChainArgs 
   for (int c = a.NC - 1; c >= 0; --c) {
     const int64_t n = (int64_t)bh * a.NC + c;
     __syncthreads();
-    tile_store<NT, D / 8, PD>(Kr, rk, tid);
-    tile_store<NT, 8, PC>(Kt, rkt, tid);
-    tile_store<NT, 8, PC>(Qt, rq, tid);
-    tile_store<2, 8, PC>(Tm, rtm, tid);
-    tile_store<2, 8, PC>(Rt, rrt, tid);
-    Fs[tid] = rf;
+    tile_store<NT, D / 8, PD, NTH>(Kr, rk, tid);
+    tile_store<NT, 8, PC, NTH>(Kt, rkt, tid);
+    tile_store<NT, 8, PC, NTH>(Qt, rq, tid);
+    tile_store<NTM, 8, PC, NTH>(Tm, rtm, tid);
+    tile_store<NTM, 8, PC, NTH>(Rt, rrt, tid);
+#pragma unroll
+    for (int j = 0; j < NF; ++j) Fs[tid + NTH * j] = rf[j];
     rows16_store(XO[wave], ro);
     rows16_store(XG[wave], rgo);
     if (c > 0) bwd_load(n - 1);
@@ -860,16 +875,17 @@ bool aligned16(std::initializer_list<const void*> ps) {
 
 }  // namespace
 
-#define ATMA_BWD16_DISPATCH(KERNEL, grid, stream, args)                                  \
-  do {                                                                                   \
-    if (dtype == ATMA_BF16) {                                                            \
-      if (d == 128) atma::KERNEL<atma::bf16, 128><<<grid, dim3(256), 0, stream>>>(args); \
-      else atma::KERNEL<atma::bf16, 64><<<grid, dim3(256), 0, stream>>>(args);           \
-    } else {                                                                             \
-      if (d == 128) atma::KERNEL<atma::f16, 128><<<grid, dim3(256), 0, stream>>>(args);  \
-      else atma::KERNEL<atma::f16, 64><<<grid, dim3(256), 0, stream>>>(args);            \
-    }                                                                                    \
+#define ATMA_BWD16_DISPATCH_NT(KERNEL, grid, nthreads, stream, args)                          \
+  do {                                                                                        \
+    if (dtype == ATMA_BF16) {                                                                 \
+      if (d == 128) atma::KERNEL<atma::bf16, 128><<<grid, dim3(nthreads), 0, stream>>>(args); \
+      else atma::KERNEL<atma::bf16, 64><<<grid, dim3(nthreads), 0, stream>>>(args);           \
+    } else {                                                                                  \
+      if (d == 128) atma::KERNEL<atma::f16, 128><<<grid, dim3(nthreads), 0, stream>>>(args);  \
+      else atma::KERNEL<atma::f16, 64><<<grid, dim3(nthreads), 0, stream>>>(args);            \
+    }                                                                                         \
   } while (0)
+#define ATMA_BWD16_DISPATCH(KERNEL, grid, stream, args) ATMA_BWD16_DISPATCH_NT(KERNEL, grid, 256, stream, args)
 
 extern "C" int atma_gated_delta_bwd16_prep(const void* q, const void* k, const void* v, const void* d_out,
                                            const float* g, const float* beta, void* kr, void* kt, void* qr,
@@ -909,12 +925,13 @@ extern "C" int atma_gated_delta_bwd16_chain(const void* kr, const void* kt, cons
     return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_chain: null pointer");
   if (!aligned16({kr, kt, qt, tm, tt, rt, vt, ot, got}))
     return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_chain: tiles must be 16-byte aligned");
-  if (BH * (d / 64) > 0x7fffffff || BH * NC > 0x7fffffff)
+  const int64_t slabs = d / (16 * kChainWaves);  // column slabs (workgroups) per sequence-head
+  if (BH * slabs > 0x7fffffff || BH * NC > 0x7fffffff)
     return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_chain: sizes too large");
   Bwd16ChainArgs a{kr, kt, qt, tm, tt, rt, vt, ot, got, f, s0, dst, s_entry, ds_end, u, dy, ds0,
                    (int)BH, (int)NC};
-  const dim3 grid((unsigned)(BH * (d / 64)));
-  ATMA_BWD16_DISPATCH(gdn_bwd16_chain_kernel, grid, (hipStream_t)stream, a);
+  const dim3 grid((unsigned)(BH * slabs));
+  ATMA_BWD16_DISPATCH_NT(gdn_bwd16_chain_kernel, grid, 64 * kChainWaves, (hipStream_t)stream, a);
   return check_launch("gated_delta_bwd16_chain");
 }
 
