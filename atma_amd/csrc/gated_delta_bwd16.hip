@@ -379,14 +379,24 @@ __device__ __forceinline__ float row8_sum(float x) {
 
 template <typename T, int D>
 __global__ void __launch_bounds__(256) gdn_bwd16_prep_kernel(Bwd16PrepArgs a) {
-  constexpr int C = 64, PD = D + 8, NP = 68, KS = D / 32;
+  constexpr int C = 64, PD = D + 8, PT = C + 8, KS = D / 32;
   constexpr int NV = D / 32;  // 16-byte row chunks per thread
   __shared__ __attribute__((aligned(16))) T Ks[C * PD];
   __shared__ __attribute__((aligned(16))) T Qs[C * PD];
   __shared__ __attribute__((aligned(16))) T Vs[C * PD];
   __shared__ __attribute__((aligned(16))) T Os[C * PD];
-  __shared__ __attribute__((aligned(16))) float Ns[C * NP];
+  // N = diag(beta) A in 16 x 16 blocks: the diagonal blocks as N^T (rows of 16 floats, the
+  // substitution's columns) and the six blocks below them in the transposed accumulator
+  // layout the block products take (register i of lane (g, c) of block (S, P), S < P:
+  // N[16P + c][16S + 4g + i]).  Only wave 0 reads them, in order, so the substitution's
+  // T^T diagonal blocks (Mb) overwrite the N^T ones it has consumed, and T, row-major 16-bit,
+  // overwrites all of it at the end (84 KiB in all would allow one workgroup per CU; 79 KiB
+  // allows two, so one's loads overlap the other's products)
+  __shared__ __attribute__((aligned(16))) float Nd[4 * 256 + 6 * 256];
   __shared__ float Lg[C], Bt[C], Gs[C];
+  float* Mb = Nd;  // T^T of the diagonal blocks
+  T* Tl = (T*)Nd;  // T, row-major, pitch PT
+  static_assert(C * PT * (int)sizeof(T) <= (int)sizeof(Nd), "T fits the N blocks' bytes");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -481,7 +491,8 @@ __global__ void __launch_bounds__(256) gdn_bwd16_prep_kernel(Bwd16PrepArgs a) {
   }
   __syncthreads();
 
-  // row block P = wave of K K^T and Q K^T: N and Rq^T
+  // row block P = wave of K K^T and Q K^T: Rq^T, the diagonal N block and, from the blocks
+  // right of the diagonal (Gram symmetry), the N blocks below it in the block products' layout
   {
     const int P = wave;
     u32x4 ka[KS], qa[KS];
@@ -499,65 +510,139 @@ __global__ void __launch_bounds__(256) gdn_bwd16_prep_kernel(Bwd16PrepArgs a) {
         kk = mfma16x16x32<T>(ka[s], kb, kk);
         qk = mfma16x16x32<T>(qa[s], kb, qk);
       }
+      // lane (g, c16) register i: token pair (16 P + 4g + i, 16 S + c16)
       const int sc = 16 * S + c16;
       const float lgs = Lg[sc];
       f32x4 rq;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int p = 16 * P + 4 * g + i;
-        const float e = sc <= p ? expf(Lg[p] - lgs) : 0.f;
-        Ns[p * NP + sc] = sc < p ? Bt[p] * e * kk[i] : 0.f;
-        rq[i] = e * qk[i];
+        rq[i] = sc <= p ? expf(Lg[p] - lgs) * qk[i] : 0.f;
       }
       *(u32x2*)((T*)a.rt + (n * C + sc) * C + 16 * P + 4 * g) = u32x2{pack2<T>(rq[0], rq[1]), pack2<T>(rq[2], rq[3])};
+      if (S == P) {  // N^T[c][4g + i] = N[16P + 4g + i][16P + c], strictly lower
+        f32x4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int p = 16 * P + 4 * g + i;
+          v[i] = c16 < 4 * g + i ? Bt[p] * expf(Lg[p] - lgs) * kk[i] : 0.f;
+        }
+        *(f32x4*)(Nd + P * 256 + c16 * 16 + 4 * g) = v;
+      } else if (S > P) {  // N[16S + c][16P + 4g + i] = beta_r e^(lg_r - lg_s) k_s . k_r
+        const int r = sc;
+        f32x4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = Bt[r] * expf(Lg[r] - Lg[16 * P + 4 * g + i]) * kk[i];
+        *(f32x4*)(Nd + 4 * 256 + tri(P, S - 1) * 256 + lane * 4) = v;
+      }
     }
   }
   __syncthreads();
 
   if (wave == 0) {
-    // T = (I + N)^-1: x[i] = T[i][j] for the lane's column j
-    float x[C];
+    // T = (I + N)^-1.  The diagonal blocks by forward substitution in fp32: lane (g, c) solves
+    // column c of block g, N^T rows read from LDS
+    {
+      const float* nt = Nd + g * 256;
+      float x[16];
 #pragma unroll
-    for (int i = 0; i < C; ++i) x[i] = i == lane ? 1.f : 0.f;
+      for (int r = 0; r < 16; ++r) x[r] = (r == c16) ? 1.f : 0.f;
 #pragma unroll
-    for (int i = 1; i < C; ++i) {
-      float acc = 0.f;
+      for (int j = 0; j < 15; ++j) {
+        float nv[16];
 #pragma unroll
-      for (int s4 = 0; s4 < (i + 3) / 4; ++s4) {
-        const f32x4 nv = *(const f32x4*)(Ns + i * NP + 4 * s4);  // N[i][s] = 0 for s >= i
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const f32x4 v = *(const f32x4*)(nt + j * 16 + 4 * q4);  // column j of N
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc = fmaf(nv[e], x[4 * s4 + e], acc);
+          for (int e = 0; e < 4; ++e) nv[4 * q4 + e] = v[e];
+        }
+#pragma unroll
+        for (int r = j + 1; r < 16; ++r) x[r] = fmaf(-nv[r], x[j], x[r]);
       }
-      x[i] -= acc;
+      float* mt = Mb + g * 256 + c16 * 16;  // T^T row c = column c of T
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) *(f32x4*)(mt + 4 * q4) = f32x4{x[4 * q4], x[4 * q4 + 1], x[4 * q4 + 2], x[4 * q4 + 3]};
     }
-    T* tmo = (T*)a.tm + n * C * C;
+    wave_sync();
+    f32x4 tpp[4], tppT[4], at[6];  // T_PP and T_PP^T in the accumulator layout
 #pragma unroll
-    for (int i = 0; i < C; ++i) tmo[i * C + lane] = from_f32<T>(x[i]);
-    T* tto = (T*)a.tt + (n * C + lane) * C;
+    for (int P = 0; P < 4; ++P) {
+      tpp[P] = *(const f32x4*)(Mb + P * 256 + c16 * 16 + 4 * g);
 #pragma unroll
-    for (int q = 0; q < 8; ++q)
-      *(u32x4*)(tto + 8 * q) = u32x4{pack2<T>(x[8 * q], x[8 * q + 1]), pack2<T>(x[8 * q + 2], x[8 * q + 3]),
-                                     pack2<T>(x[8 * q + 4], x[8 * q + 5]), pack2<T>(x[8 * q + 6], x[8 * q + 7])};
+      for (int i = 0; i < 4; ++i) tppT[P][i] = Mb[P * 256 + (4 * g + i) * 16 + c16];
+    }
+#pragma unroll
+    for (int k = 0; k < 6; ++k) at[k] = *(const f32x4*)(Nd + 4 * 256 + k * 256 + lane * 4);
+    // off-diagonal blocks, level L = P - S: T_PS = -T_PP Y_PS with Y_PS = sum_{k=S}^{P-1}
+    // N_Pk T_kS, and (T^T)_SP = -Y_PS^T T_PP^T (at(k, P) = block (k, P) of the layout above)
+    auto atb = [&](int k, int P) { return at[tri(k, P - 1)]; };
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+    const f32x4 y10 = blk_mul(atb(0, 1), tpp[0], z);
+    const f32x4 y21 = blk_mul(atb(1, 2), tpp[1], z);
+    const f32x4 y32 = blk_mul(atb(2, 3), tpp[2], z);
+    const f32x4 t10 = -blk_mul(tppT[1], y10, z);
+    const f32x4 t21 = -blk_mul(tppT[2], y21, z);
+    const f32x4 tt01 = -blk_mul(y10, tppT[1], z);
+    const f32x4 tt12 = -blk_mul(y21, tppT[2], z);
+    const f32x4 tt23 = -blk_mul(y32, tppT[3], z);
+    const f32x4 y20 = blk_mul(atb(1, 2), t10, blk_mul(atb(0, 2), tpp[0], z));
+    const f32x4 y31 = blk_mul(atb(2, 3), t21, blk_mul(atb(1, 3), tpp[1], z));
+    const f32x4 t20 = -blk_mul(tppT[2], y20, z);
+    const f32x4 tt02 = -blk_mul(y20, tppT[2], z);
+    const f32x4 tt13 = -blk_mul(y31, tppT[3], z);
+    const f32x4 y30 = blk_mul(atb(2, 3), t20, blk_mul(atb(1, 3), t10, blk_mul(atb(0, 3), tpp[0], z)));
+    const f32x4 tt03 = -blk_mul(y30, tppT[3], z);
+    // T row-major in 16 bits over the N blocks (every read of them is above): the T^T-form
+    // block (S, P) gives row 16P + c, columns 16S + 4g .. + 3 of T (zeros above the diagonal)
+    const f32x4 tb[4][4] = {{tppT[0], z, z, z}, {tt01, tppT[1], z, z}, {tt02, tt12, tppT[2], z},
+                            {tt03, tt13, tt23, tppT[3]}};
+#pragma unroll
+    for (int P = 0; P < 4; ++P)
+#pragma unroll
+      for (int S = 0; S < 4; ++S) {
+        const f32x4 v = tb[P][S];
+        *(u32x2*)(Tl + (16 * P + c16) * PT + 16 * S + 4 * g) = u32x2{pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
+      }
   } else {
-    // [D][64] tiles from the LDS rows: lane pairs (d, 8 tokens), d fastest
-    for (int i = tid - 64; i < 5 * D * 8; i += 192) {
-      const int tile = i / (D * 8), j = i % (D * 8);
-      const int d = j % D, ch = j / D;
+    // [D][64] tiles from the LDS rows by transposing reads: a 16-lane group reads 8 rows x 16
+    // columns (lane s: row r0 + s / 4 (+ 4), columns c0 + 4 (s % 4) ..), lane i then holds
+    // tokens r0 .. r0 + 7 of column c0 + i, one 16-byte chunk of row d = c0 + i of the tile
+    const int gi = (tid - 64) >> 4, sl = lane & 15;  // 12 groups of 16 lanes
+    const int rr = sl >> 2, cc = 4 * (sl & 3);
+    constexpr int UNITS = 5 * (D / 16) * 8;          // (tile, 16-column block, 8-row block)
+    for (int u = gi; u < UNITS; u += 12) {
+      const int tile = u / ((D / 16) * 8), rem = u % ((D / 16) * 8);
+      const int c0 = 16 * (rem / 8), r0 = 8 * (rem % 8);
       const T* src = tile == 0 ? Ks : tile == 1 ? Qs : tile == 2 ? Vs : Os;
-      uint32_t w[4];
-      if (tile < 4) {
+      const u32x2 lo = lds_read_tr16(src + (r0 + rr) * PD + c0 + cc);
+      const u32x2 hi = lds_read_tr16(src + (r0 + 4 + rr) * PD + c0 + cc);
+      u32x4 w = {lo[0], lo[1], hi[0], hi[1]};
+      if (tile == 4) {  // (diag(Ga) dO)^T
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          w[e] = (uint32_t)__builtin_bit_cast(uint16_t, src[(8 * ch + 2 * e) * PD + d]) |
-                 ((uint32_t)__builtin_bit_cast(uint16_t, src[(8 * ch + 2 * e + 1) * PD + d]) << 16);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          w[e] = pack2<T>(Gs[8 * ch + 2 * e] * to_f32(src[(8 * ch + 2 * e) * PD + d]),
-                          Gs[8 * ch + 2 * e + 1] * to_f32(src[(8 * ch + 2 * e + 1) * PD + d]));
+          w[e] = pack2<T>(Gs[r0 + 2 * e] * elem16<T>(w, 2 * e), Gs[r0 + 2 * e + 1] * elem16<T>(w, 2 * e + 1));
       }
       void* dst = tile == 0 ? a.kt : tile == 1 ? a.qt : tile == 2 ? a.vt : tile == 3 ? a.ot : a.got;
-      *(u32x4*)((T*)dst + (n * D + d) * C + 8 * ch) = u32x4{w[0], w[1], w[2], w[3]};
+      *(u32x4*)((T*)dst + (n * D + c0 + sl) * C + r0) = w;
+    }
+  }
+  __syncthreads();
+  // T and T^T out: 64 rows of 128 bytes each, two 16-byte chunks per thread
+  {
+    const int row = tid >> 2, ch = 2 * (tid & 3);  // ... chunks ch, ch + 1 of T's row
+    T* tmo = (T*)a.tm + (n * C + row) * C;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) *(u32x4*)(tmo + 8 * (ch + k)) = *(const u32x4*)(Tl + row * PT + 8 * (ch + k));
+    // T^T by transposing reads: group gi (16 lanes) takes 16-column block c0 and two 8-row
+    // blocks of T
+    const int gi = tid >> 4, sl = lane & 15, rr = sl >> 2, cc = 4 * (sl & 3);
+    const int c0 = 16 * (gi & 3);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int r0 = 8 * (2 * (gi >> 2) + k);
+      const u32x2 lo = lds_read_tr16(Tl + (r0 + rr) * PT + c0 + cc);
+      const u32x2 hi = lds_read_tr16(Tl + (r0 + 4 + rr) * PT + c0 + cc);
+      *(u32x4*)((T*)a.tt + (n * C + c0 + sl) * C + r0) = u32x4{lo[0], lo[1], hi[0], hi[1]};
     }
   }
 }

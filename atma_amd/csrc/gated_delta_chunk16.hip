@@ -69,18 +69,6 @@ __device__ __forceinline__ u32x4 pack8(const f32x4& lo, const f32x4& hi) {
   return u32x4{pack2<T>(lo[0], lo[1]), pack2<T>(lo[2], lo[3]), pack2<T>(hi[0], hi[1]), pack2<T>(hi[2], hi[3])};
 }
 
-// X Y of fp32 16 x 16 blocks on v_mfma_f32_16x16x4f32, with X entering transposed: xt and y
-// are in the accumulator layout (lane (g, c) register i = row 4g + i, column c), and step i
-// contracts k = 4g + i, so xt[i] is the A operand (X[c][4g + i]) and y[i] the B operand.
-__device__ __forceinline__ f32x4 blk_mul(const f32x4& xt, const f32x4& y, f32x4 acc) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xt[i], y[i], acc, 0, 0, 0);
-  return acc;
-}
-
-// Lower-triangle 16-token block pairs (k, P), k <= P, in the order (0,0) (0,1) (1,1) (0,2) ...
-__host__ __device__ constexpr int tri(int k, int P) { return P * (P + 1) / 2 + k; }
-
 template <typename T, int D>
 __global__ void __launch_bounds__(256) gdn_prep16_kernel(GdnArgs a) {
   constexpr int C = kChunk, KS = D / 32;
