@@ -352,10 +352,12 @@ __global__ void __launch_bounds__(64 * kChainWaves, 1) gdn_bwd16_chain_kernel(Bw
 // One workgroup per chunk-head item n (4 waves): the operand tiles of the chain and of the
 // chunk-local gradients.  The raw k, q rows are l2-normalised (q also scaled, as the
 // forward does: x / max(|x|, 1e-12)) and rounded to 16 bits once; wave P
-// forms row block P of K K^T and Q K^T on MFMA and from them N = diag(beta) A (fp32, LDS)
-// and Rq^T; then wave 0 inverts I + N by forward substitution (lane j solves column j of T,
-// 64 x 64 fully unrolled, N read as broadcast rows) while waves 1-3 write the transposed
-// tiles k^T, q^T, v^T, dO^T and (diag(Ga) dO)^T from the LDS rows.
+// forms row block P of K K^T and Q K^T on MFMA and from them Rq^T and the 16 x 16 blocks of
+// N = diag(beta) A (fp32, LDS); then wave 0 inverts I + N -- the four diagonal blocks by
+// forward substitution (lane (g, c) solves column c of block g), the blocks below them by
+// fp32 block products on v_mfma_f32_16x16x4f32 -- while waves 1-3 write the transposed
+// tiles k^T, q^T, v^T, dO^T and (diag(Ga) dO)^T from the LDS rows by transposing reads;
+// last, every wave writes T and T^T.
 struct Bwd16PrepArgs {
   const void* q;      // (B, T, H, D) 16-bit, raw
   const void* k;      // (B, T, H, D) 16-bit, raw
