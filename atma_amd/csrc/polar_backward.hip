@@ -451,11 +451,13 @@ __device__ __forceinline__ float bw_lane(float x, int l) {
 
 // dq, dt for 16-bit inputs: workgroup = (b * Hq + hq, 64-row query tile, last tile first)
 template <typename T, int D>
-__global__ void __launch_bounds__(256, 2) polar_bwd16_dq_kernel(PolarBwdArgs a) {
+__global__ void __launch_bounds__(256, 3) polar_bwd16_dq_kernel(PolarBwdArgs a) {
   constexpr int BM = 64, BN = 64, KS = D / 32, CPR = D / 8, NDMA = CPR / 4;
-  // double-buffered key blocks, filled by direct-to-LDS copies one block ahead
-  __shared__ __attribute__((aligned(16))) T Ks[2][BN * D];
-  __shared__ __attribute__((aligned(16))) T Vs[2][BN * D];
+  // one key block in LDS, filled by direct-to-LDS copies once every wave is done with the
+  // previous one: 32 KiB and at most 168 VGPRs give three workgroups per CU, whose copies
+  // and products overlap (a second LDS buffer would allow only two)
+  __shared__ __attribute__((aligned(16))) T Ks[BN * D];
+  __shared__ __attribute__((aligned(16))) T Vs[BN * D];
 
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -504,23 +506,20 @@ __global__ void __launch_bounds__(256, 2) polar_bwd16_dq_kernel(PolarBwdArgs a) 
     koff[k] = (uint32_t)((r * a.k_st + 8 * c) * 2);
     voff[k] = (uint32_t)((r * a.v_st + 8 * c) * 2);
   }
-  auto dma_block = [&](int k0, int buf) {
+  auto dma_block = [&](int k0) {
     const uint32_t kb = (uint32_t)((int64_t)k0 * a.k_st * 2), vb = (uint32_t)((int64_t)k0 * a.v_st * 2);
 #pragma unroll
     for (int k = 0; k < NDMA; ++k) {
-      dma_buf16(krs, koff[k] + kb, 0, &Ks[buf][(NDMA * wave + k) * 64 * 8]);
-      dma_buf16(vrs, voff[k] + vb, 0, &Vs[buf][(NDMA * wave + k) * 64 * 8]);
+      dma_buf16(krs, koff[k] + kb, 0, &Ks[(NDMA * wave + k) * 64 * 8]);
+      dma_buf16(vrs, voff[k] + vb, 0, &Vs[(NDMA * wave + k) * 64 * 8]);
     }
   };
-  if (lo < hi) dma_block(lo, 0);
-  int cur = 0;
+  if (lo < hi) dma_block(lo);
   for (int k0 = lo; k0 < hi; k0 += BN) {
     wait_vmcnt<0>();  // this wave's copies of block k0 (and every earlier load) are done
-    __syncthreads();  // ... and every wave's; buffer cur ^ 1 is no longer read
-    if (k0 + BN < hi) dma_block(k0 + BN, cur ^ 1);
-    const T* Kc = Ks[cur];
-    const T* Vc = Vs[cur];
-    cur ^= 1;
+    __syncthreads();  // ... and every wave's
+    const T* Kc = Ks;
+    const T* Vc = Vs;
     // S^T = K Q^T, dP^T = V gs^T: tile t holds keys k0 + 16 t + 4 g + i, query row
     f32x4 st[4], pt[4];
 #pragma unroll
@@ -580,6 +579,8 @@ __global__ void __launch_bounds__(256, 2) polar_bwd16_dq_kernel(PolarBwdArgs a) 
         dqT[nt + u] = mfma16x16x32<T>(ka[u][1], b1, dqT[nt + u]);
       }
     }
+    __syncthreads();  // every wave is done with the block's tiles
+    if (k0 + BN < hi) dma_block(k0 + BN);
   }
 
   dt += __shfl_xor(dt, 16, 64);
