@@ -840,6 +840,25 @@ struct PolarPrepArgs {
   float eps;
 };
 
+// The preamble's per-row scalar chain runs on every lane of the row's 16-lane group, so it
+// takes the hardware forms: exp2 / log2 (about 1 ulp) and reciprocals, instead of the
+// library's correctly rounded sequences, which were most of the kernel's instructions.
+__device__ __forceinline__ float pp_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+__device__ __forceinline__ float pp_log(float x) { return __builtin_amdgcn_logf(x) * kLn2; }
+__device__ __forceinline__ float pp_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+// log1p(y) for y >= 0: log(u) y / (u - 1) with u = 1 + y rounded, exact to rounding for small y
+__device__ __forceinline__ float pp_log1p(float y) {
+  const float u = 1.f + y;
+  return u == 1.f ? y : pp_log(u) * (y * pp_rcp(u - 1.f));
+}
+// softplus with torch's threshold (x > 20 -> x), as softplus()
+__device__ __forceinline__ float pp_softplus(float x) { return x > 20.f ? x : pp_log1p(pp_exp(x)); }
+// tanh(x) for x >= 0
+__device__ __forceinline__ float pp_tanh_pos(float x) {
+  const float e = pp_exp(-2.f * x);
+  return (1.f - e) * pp_rcp(1.f + e);
+}
+
 template <typename T, int D>
 __global__ void __launch_bounds__(256) polar_bwd_prep_kernel(PolarPrepArgs a) {
   // one query row per group of 16 lanes (E elements per lane): the row sums are DPP
@@ -856,10 +875,10 @@ __global__ void __launch_bounds__(256) polar_bwd_prep_kernel(PolarPrepArgs a) {
   float n = a.n_keys[ok ? t : 0];
   if (a.window > 0 && !a.preserve_length) n = fminf(n, (float)a.window);
   n = fmaxf(n, 1.f);
-  const float logn = logf(n), root = sqrtf(logf(n + 1.f));
-  const float temp = 1.f + softplus(a.len_gain_raw[h]) * logn;
-  const float nu = a.null_base[h] + softplus(a.null_slope_raw[h]) * root;
-  const float p_null = ok ? expf(temp * nu - a.M[row]) : 0.f;
+  const float logn = pp_log(n), root = sqrtf(pp_log(n + 1.f));
+  const float temp = 1.f + pp_softplus(a.len_gain_raw[h]) * logn;
+  const float nu = a.null_base[h] + pp_softplus(a.null_slope_raw[h]) * root;
+  const float p_null = ok ? pp_exp(temp * nu - a.M[row]) : 0.f;
   const float Lr = ok ? a.L[row] : 0.f, Q2r = ok ? a.Q2[row] : 0.f;
   const float gmr = (ok && a.gm) ? to_f32(((const T*)a.gm)[row]) : 0.f;
 
@@ -909,7 +928,7 @@ __global__ void __launch_bounds__(256) polar_bwd_prep_kernel(PolarPrepArgs a) {
   ss = row16_sum(ss);
   gcs = row16_sum(gcs);
   // gs = (gc - (gc.c) c) / |s|  with c = s / |s|:  (gc - (gc.s / |s|) s / |s|) / |s|
-  const float inv = 1.f / fmaxf(sqrtf(ss), a.eps);
+  const float inv = pp_rcp(fmaxf(sqrtf(ss), a.eps));
   const float gcc = gcs * inv;
   float g[E], gsv = 0.f;
 #pragma unroll
@@ -928,16 +947,17 @@ __global__ void __launch_bounds__(256) polar_bwd_prep_kernel(PolarPrepArgs a) {
   }
   gsv = row16_sum(gsv);
   // the magnitude path through m_eff = L^3 / (Q2 Z), Z = L + p_null
-  const float beta = softplus(a.mag_beta_raw[h]);
+  const float beta = pp_softplus(a.mag_beta_raw[h]);
   const float Z = Lr + p_null;
   const float Zc = fmaxf(Z, kTiny), Q2c = fmaxf(Q2r, kTiny);
-  const float me = (Lr * Lr / Q2c) * (Lr / Zc);
-  const float lm = log1pf(me);
-  const float mag = tanhf(beta * lm);
-  const float gme = gmr * beta * (1.f - mag * mag) / (1.f + me);
-  const float dme_dL = Lr > 0.f ? 3.f * me / Lr : 0.f;
-  const float dme_dQ2 = Q2r > kTiny ? -me / Q2c : 0.f;
-  const float dme_dZ = Z > kTiny ? -me / Zc : 0.f;
+  const float rQ2 = pp_rcp(Q2c), rZ = pp_rcp(Zc);
+  const float me = (Lr * Lr * rQ2) * (Lr * rZ);
+  const float lm = pp_log1p(me);
+  const float mag = pp_tanh_pos(beta * lm);
+  const float gme = gmr * beta * (1.f - mag * mag) * pp_rcp(1.f + me);
+  const float dme_dL = Lr > 0.f ? 3.f * me * pp_rcp(Lr) : 0.f;
+  const float dme_dQ2 = Q2r > kTiny ? -me * rQ2 : 0.f;
+  const float dme_dZ = Z > kTiny ? -me * rZ : 0.f;
   const float g_anull = (gsv + gme * dme_dZ) * p_null;
   if (ok && l16 == 0) {
     a.gL[row] = gme * (dme_dL + dme_dZ);
