@@ -379,6 +379,9 @@ __device__ __forceinline__ float row8_sum(float x) {
   return x + dpp_f32<0x141>(x);
 }
 
+// e^x on the hardware exp2 (about 1 ulp), for the prep's per-element decay factors
+__device__ __forceinline__ float exp_hw(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+
 template <typename T, int D>
 __global__ void __launch_bounds__(256) gdn_bwd16_prep_kernel(Bwd16PrepArgs a) {
   constexpr int C = 64, PD = D + 8, PT = C + 8, KS = D / 32;
@@ -438,9 +441,9 @@ __global__ void __launch_bounds__(256) gdn_bwd16_prep_kernel(Bwd16PrepArgs a) {
       // row norms: a row's D / 8 chunks sit in D / 8 consecutive lanes
       float sk = 0.f, sq = 0.f;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        sk = fmaf(elem16<T>(kx[j], e), elem16<T>(kx[j], e), sk);
-        sq = fmaf(elem16<T>(qx[j], e), elem16<T>(qx[j], e), sq);
+      for (int e = 0; e < 4; ++e) {  // packed pairs (v_dot2)
+        sk = dot2<T>(kx[j][e], kx[j][e], sk);
+        sq = dot2<T>(qx[j][e], qx[j][e], sq);
       }
       if constexpr (D == 128) {
         sk = row16_sum(sk);
@@ -451,13 +454,13 @@ __global__ void __launch_bounds__(256) gdn_bwd16_prep_kernel(Bwd16PrepArgs a) {
       }
       const float nk = sqrtf(sk), nq = sqrtf(sq);
       const bool ok = r < rows;
-      const float ik = !ok ? 0.f : a.l2norm ? 1.f / fmaxf(nk, 1e-12f) : 1.f;
-      const float iq = !ok ? 0.f : (a.l2norm ? 1.f / fmaxf(nq, 1e-12f) : 1.f) * a.scale;
+      const float ik = !ok ? 0.f : a.l2norm ? __builtin_amdgcn_rcpf(fmaxf(nk, 1e-12f)) : 1.f;
+      const float iq = !ok ? 0.f : (a.l2norm ? __builtin_amdgcn_rcpf(fmaxf(nq, 1e-12f)) : 1.f) * a.scale;
       if (ch == 0) {
         fo[5 * C + r] = iq;
         fo[6 * C + r] = ik;
-        fo[7 * C + r] = ok && a.l2norm && nq > 1e-12f ? 1.f / sq : 0.f;
-        fo[8 * C + r] = ok && a.l2norm && nk > 1e-12f ? 1.f / sk : 0.f;
+        fo[7 * C + r] = ok && a.l2norm && nq > 1e-12f ? __builtin_amdgcn_rcpf(sq) : 0.f;
+        fo[8 * C + r] = ok && a.l2norm && nk > 1e-12f ? __builtin_amdgcn_rcpf(sk) : 0.f;
       }
       u32x4 kp, qp;
 #pragma unroll
@@ -480,14 +483,14 @@ __global__ void __launch_bounds__(256) gdn_bwd16_prep_kernel(Bwd16PrepArgs a) {
         if (lane >= off) lg += y;
       }
       const float lgC = __shfl(lg, 63, 64);
-      const float ga = expf(lg);
+      const float ga = exp_hw(lg);
       Lg[lane] = lg;
       Bt[lane] = bt;
       Gs[lane] = ga;
       fo[lane] = ga;
-      fo[C + lane] = expf(lgC - lg);
+      fo[C + lane] = exp_hw(lgC - lg);
       fo[2 * C + lane] = bt;
-      fo[3 * C + lane] = expf(lgC);
+      fo[3 * C + lane] = exp_hw(lgC);
       fo[4 * C + lane] = lg;
     }
   }
@@ -519,7 +522,7 @@ __global__ void __launch_bounds__(256) gdn_bwd16_prep_kernel(Bwd16PrepArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int p = 16 * P + 4 * g + i;
-        rq[i] = sc <= p ? expf(Lg[p] - lgs) * qk[i] : 0.f;
+        rq[i] = sc <= p ? exp_hw(Lg[p] - lgs) * qk[i] : 0.f;
       }
       *(u32x2*)((T*)a.rt + (n * C + sc) * C + 16 * P + 4 * g) = u32x2{pack2<T>(rq[0], rq[1]), pack2<T>(rq[2], rq[3])};
       if (S == P) {  // N^T[c][4g + i] = N[16P + 4g + i][16P + c], strictly lower
@@ -527,14 +530,14 @@ __global__ void __launch_bounds__(256) gdn_bwd16_prep_kernel(Bwd16PrepArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int p = 16 * P + 4 * g + i;
-          v[i] = c16 < 4 * g + i ? Bt[p] * expf(Lg[p] - lgs) * kk[i] : 0.f;
+          v[i] = c16 < 4 * g + i ? Bt[p] * exp_hw(Lg[p] - lgs) * kk[i] : 0.f;
         }
         *(f32x4*)(Nd + P * 256 + c16 * 16 + 4 * g) = v;
       } else if (S > P) {  // N[16S + c][16P + 4g + i] = beta_r e^(lg_r - lg_s) k_s . k_r
         const int r = sc;
         f32x4 v;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = Bt[r] * expf(Lg[r] - Lg[16 * P + 4 * g + i]) * kk[i];
+        for (int i = 0; i < 4; ++i) v[i] = Bt[r] * exp_hw(Lg[r] - Lg[16 * P + 4 * g + i]) * kk[i];
         *(f32x4*)(Nd + 4 * 256 + tri(P, S - 1) * 256 + lane * 4) = v;
       }
     }
