@@ -729,6 +729,21 @@ __global__ void __launch_bounds__(256, 1) gdn_bwd16_local_kernel(Bwd16LocalArgs 
     qA[s] = *(const u32x4*)((const T*)a.qr + (n * C + ra) * D + 32 * s + 8 * g);
   }
   for (int i = tid; i < kFRows * C; i += 256) Fs[i] = a.f[n * kFRows * C + i];
+  // the raw k and q elements of the lane's dK / dQ tile entries (row 16 wave + 4g + i, column
+  // 16 t + c16), for the l2 norm's backward at the end: loaded now, so their latency passes
+  // under the products
+  T kraw16[DT][4], qraw16[DT][4];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int p = 16 * wave + 4 * g + i;
+      kraw16[t][i] = qraw16[t][i] = from_f32<T>(0.f);
+      if (p < rows) {
+        kraw16[t][i] = ((const T*)a.k)[base + p * rs + 16 * t + c16];
+        qraw16[t][i] = ((const T*)a.q)[base + p * rs + 16 * t + c16];
+      }
+    }
   tile_store<NSS, D / 8, PD>(SS, rss, tid);
   tile_store<NT, D / 8, PD>(Us, ru, tid);
   tile_store<NT, D / 8, PD>(Kr, rk, tid);
@@ -782,7 +797,7 @@ __global__ void __launch_bounds__(256, 1) gdn_bwd16_local_kernel(Bwd16LocalArgs 
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int p = 16 * wave + 4 * g + i;
-      const float e = sc <= p ? expf(Lgf[p] - lgs) : 0.f;
+      const float e = sc <= p ? exp_hw(Lgf[p] - lgs) : 0.f;
       const float A = sc < p ? e * kk[i] : 0.f;
       const float Rq = e * qk[i];
       const float dL = sc < p ? -yl[i] : 0.f;
@@ -886,11 +901,8 @@ __global__ void __launch_bounds__(256, 1) gdn_bwd16_local_kernel(Bwd16LocalArgs 
       rk3[i] = fmaf(kv, P3[t][i], rk3[i]);
       dKn[t][i] = dk[i] - Ga[p] * Bf[p] * P1[t][i] + Wf[p] * P3[t][i];
       dQs[t][i] = dq[i] + Ga[p] * P2[t][i];
-      kraw[t][i] = qraw[t][i] = 0.f;
-      if (p < rows) {
-        kraw[t][i] = to_f32(((const T*)a.k)[base + p * rs + d]);
-        qraw[t][i] = to_f32(((const T*)a.q)[base + p * rs + d]);
-      }
+      kraw[t][i] = to_f32(kraw16[t][i]);
+      qraw[t][i] = to_f32(qraw16[t][i]);
       xk[i] = fmaf(kraw[t][i], dKn[t][i], xk[i]);
       xq[i] = fmaf(qraw[t][i], dQs[t][i], xq[i]);
     }
