@@ -24,6 +24,7 @@
 // (Y, U, dU, dY) go through a per-wave transposed bf16 buffer ([column][k], 16 bytes per
 // lane per fragment) to become the B operand of the next product.
 #include <initializer_list>
+#include <type_traits>
 
 #include "common.h"
 
@@ -132,6 +133,20 @@ __global__ void __launch_bounds__(64 * kChainWaves, 1) gdn_bwd16_chain_kernel(Bw
     *(u32x2*)(buf + c16 * pitch + 16 * t + 4 * g) = pk;
   };
   auto rows_of = [&](int t, int i) { return 16 * t + 4 * g + i; };
+  // the wave's [16 columns][K] 16-bit tile (pitch P) out as K rows of a [K][D] output at
+  // columns v0 .. v0 + 15, by transposing reads: 16-byte stores of 8 columns of one row
+  // instead of one 2-byte store per element
+  auto store_cols = [&](const T* buf, int pitch, auto K_c, T* out) {
+    constexpr int K = decltype(K_c)::value;
+    const int q = lane >> 4, sl = lane & 15, rr = sl >> 2, cc = 4 * (sl & 3);
+#pragma unroll
+    for (int u = q; u < 2 * (K / 16); u += 4) {
+      const int r0 = 8 * (u & 1), c0 = 16 * (u >> 1);
+      const u32x2 lo = lds_read_tr16(buf + (r0 + rr) * pitch + c0 + cc);
+      const u32x2 hi = lds_read_tr16(buf + (r0 + 4 + rr) * pitch + c0 + cc);
+      *(u32x4*)(out + (int64_t)(c0 + sl) * D + v0 + r0) = u32x4{lo[0], lo[1], hi[0], hi[1]};
+    }
+  };
 
   // ---------------------------------------------------------------- forward chain
   f32x4 S[DT];
@@ -207,11 +222,11 @@ __global__ void __launch_bounds__(64 * kChainWaves, 1) gdn_bwd16_chain_kernel(Bw
 #pragma unroll
       for (int rt = 0; rt < 4; ++rt) U[rt] = mfma16x16x32<T>(frag(Tm, PC, 16 * rt, 32 * s), bf, U[rt]);
     }
-    T* uo = (T*)a.u + n * C * D;
+    // U out through the wave's X1 buffer (its Y^T operand reads are done: in order, one wave)
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) uo[rows_of(rt, i) * D + col] = from_f32<T>(U[rt][i]);
+    for (int rt = 0; rt < 4; ++rt) put_t(X1[wave], PC, rt, U[rt]);
+    wave_sync();
+    store_cols(X1[wave], PC, std::integral_constant<int, C>{}, (T*)a.u + n * C * D);
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       f32x4 x;
@@ -221,11 +236,7 @@ __global__ void __launch_bounds__(64 * kChainWaves, 1) gdn_bwd16_chain_kernel(Bw
     }
     wave_sync();
     // the entry state, then S <- Ga_C S + K^T diag(w) U
-    T* se = (T*)a.s_entry + n * D * D;
-#pragma unroll
-    for (int t = 0; t < DT; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) se[rows_of(t, i) * D + col] = from_f32<T>(S[t][i]);
+    store_cols(Sb[wave], PD, std::integral_constant<int, D>{}, (T*)a.s_entry + n * D * D);  // S^T of this step
     const float gC = Fs[3 * C];
 #pragma unroll
     for (int t = 0; t < DT; ++t) S[t] *= gC;
@@ -271,15 +282,11 @@ __global__ void __launch_bounds__(64 * kChainWaves, 1) gdn_bwd16_chain_kernel(Bw
     rows16_store(XO[wave], ro);
     rows16_store(XG[wave], rgo);
     if (c > 0) bwd_load(n - 1);
-    // the exit-state gradient of this chunk
-    T* de = (T*)a.ds_end + n * D * D;
-#pragma unroll
-    for (int t = 0; t < DT; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) de[rows_of(t, i) * D + col] = from_f32<T>(dS[t][i]);
 #pragma unroll
     for (int t = 0; t < DT; ++t) put_t(Sb[wave], PD, t, dS[t]);
     __syncthreads();
+    // the exit-state gradient of this chunk, from its 16-bit transpose
+    store_cols(Sb[wave], PD, std::integral_constant<int, D>{}, (T*)a.ds_end + n * D * D);
 
     // dU = diag(w) K dS + Rq^T dO
     f32x4 dU[4];
