@@ -15,8 +15,10 @@ follow the reference's module registration order, of:
 
 The layer routes are built from the pinned oracle functions (``polar_dense``,
 ``gated_delta_chunked``); the glue (linear layers, RMSNorm, depthwise conv, gating)
-is restated here and pinned in ``tests/test_oracle_block.py`` by causality, the
-zero-init identities the reference relies on, and prefill/decode consistency.
+is restated here and pinned against the reference's own modules by the golden tensors
+of ``tests/golden/block_glue.pt`` (``tests/test_oracle_golden.py``: fp64 bit for bit, fp32
+within 5e-6), and in ``tests/test_oracle_block.py`` by causality, the zero-init identities
+the reference relies on, and prefill/decode consistency.
 """
 
 import torch
@@ -35,14 +37,16 @@ def linear(x, sd, name):
     return F.linear(x, sd[name + ".weight"].to(x.dtype), None if b is None else b.to(x.dtype))
 
 
-def head_rms_norm(x, dk):
+def head_rms_norm(x, dk, native_eps=False):
     """Per-head ``F.rms_norm(x, (dk,))`` with torch's default epsilon of the model's
     compute dtype (``model/reference.py:136-137``, ``model/blocks.py:488``).  Left to
     itself torch uses ``finfo(x.dtype).eps``, so an fp64 oracle would compute a
     different function (eps 2.2e-16 instead of fp32's 1.2e-7), visible on rows whose
     readout is tiny (the memory's first token); the fp64 form therefore keeps fp32's
-    epsilon and differs from the fp32 model only by rounding."""
-    eps = torch.finfo(torch.float32).eps if x.dtype == torch.float64 else None
+    epsilon and differs from the fp32 model only by rounding.  ``native_eps=True`` keeps
+    torch's default instead: what the reference module computes when it is itself run
+    in fp64 (the golden fixtures)."""
+    eps = torch.finfo(torch.float32).eps if x.dtype == torch.float64 and not native_eps else None
     return F.rms_norm(x, (dk,), eps=eps)
 
 
@@ -53,7 +57,7 @@ def causal_depthwise(x_in, weight):
     return F.conv1d(F.pad(x_in, (K - 1, 0)), weight.to(x_in.dtype), groups=x_in.shape[1])
 
 
-def attention_qkv(sd, x, H, Hkv, dk):
+def attention_qkv(sd, x, H, Hkv, dk, native_eps=False):
     """Projections, RMSNorm, Canon conv (``model/reference.py:131-155``).
     Returns q (B,H,T,dk), k, v (B,Hkv,T,dk) unexpanded, gate (B,T,H*dk)."""
     B, T, _ = x.shape
@@ -61,8 +65,8 @@ def attention_qkv(sd, x, H, Hkv, dk):
     q, gate = torch.chunk(qg, 2, dim=-1)
     k = linear(x, sd, "k").view(B, T, Hkv, dk)
     v = linear(x, sd, "v").view(B, T, Hkv, dk)
-    q = head_rms_norm(q, dk)
-    k = head_rms_norm(k, dk)
+    q = head_rms_norm(q, dk, native_eps)
+    k = head_rms_norm(k, dk, native_eps)
     outs = []
     for t, name, h in ((q, "canon_q", H), (k, "canon_k", Hkv), (v, "canon_v", Hkv)):
         t_in = t.reshape(B, T, h * dk).transpose(1, 2)
@@ -95,10 +99,11 @@ def memory_branch(sd, x, q_t, k_t, v_t, S0=None, chunk=64):
     return out, S.transpose(-1, -2)
 
 
-def polar_attention(sd, x, *, H, Hkv, dk, window=None, mem=True):
-    """``PolarAttention.forward`` (``model/reference.py:127-195``), causal over x (B,T,dim)."""
+def polar_attention(sd, x, *, H, Hkv, dk, window=None, mem=True, native_eps=False):
+    """``PolarAttention.forward`` (``model/reference.py:127-195``), causal over x (B,T,dim).
+    ``native_eps``: see ``head_rms_norm``."""
     B, T, _ = x.shape
-    q, k, v, gate = attention_qkv(sd, x, H, Hkv, dk)
+    q, k, v, gate = attention_qkv(sd, x, H, Hkv, dk, native_eps)
     n_keys = torch.arange(1, T + 1, dtype=torch.float32)
     c, mag = polar_dense(q, k, v, n_keys, params=polar_params(sd), window=window)
     c_flat = c.transpose(1, 2).reshape(B, T, H * dk)
@@ -121,10 +126,10 @@ def mlp(sd, x, prefix="mlp"):
     return linear(gate * a.relu().square(), sd, prefix + ".proj")
 
 
-def global_block(sd, x, *, H, Hkv, dk, window=None, mem=True):
+def global_block(sd, x, *, H, Hkv, dk, window=None, mem=True, native_eps=False):
     """``Block.forward`` (``model/reference.py:226-229``) for an attention block; the
     mixer's parameters live under ``attn.``."""
     attn_sd = {k[5:]: t for k, t in sd.items() if k.startswith("attn.")}
     x = x + polar_attention(attn_sd, rms_norm_weighted(x, sd["norm1.weight"]), H=H, Hkv=Hkv, dk=dk,
-                            window=window, mem=mem)
+                            window=window, mem=mem, native_eps=native_eps)
     return x + mlp(sd, rms_norm_weighted(x, sd["norm2.weight"]))

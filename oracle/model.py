@@ -5,8 +5,10 @@ state dict with the reference's keys: token embedding, blocks in Local-Local-Glo
 order (``i % 4 == 2`` global, ``:245``), final RMSNorm, LM head, then the fp32 soft cap
 ``15 x / sqrt(x^2 + 225)`` (``:265-266``).  The LFM2 conv block restates
 ``LFM2Conv.forward`` (``model/reference.py:31-48``); the global block is
-``oracle/block.global_block``.  Pinned in ``tests/test_oracle_model.py`` (conv block ==
-an explicit per-token loop, causality, composition).
+``oracle/block.global_block``.  Pinned against the reference's ``LFM2Conv``, conv ``Block``
+and a 4-block ``ReferenceModel`` by the golden tensors of ``tests/golden/block_glue.pt``
+(``tests/test_oracle_golden.py``), and in ``tests/test_oracle_model.py`` (conv block == an
+explicit per-token loop, causality, composition).
 """
 
 import torch
