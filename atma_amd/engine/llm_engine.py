@@ -39,16 +39,19 @@ class LLMEngine:
         return seq
 
     def step(self):
-        seqs, is_prefill = self.scheduler.schedule()
-        if not seqs:
+        """Plan, run and account one batch.  Returns ``(finished, n)``: the requests that
+        finished in this step as ``(seq_id, completion token ids)``, and the tokens the step
+        fed -- positive for a prefill batch, negative (minus the batch size) for a decode
+        batch, 0 when idle (the reference's throughput accounting)."""
+        batch, is_prefill = self.scheduler.schedule()
+        if not batch:
             return [], 0
-        num_tokens = sum(s.num_scheduled_tokens for s in seqs) if is_prefill else -len(seqs)
-        token_ids = self.model_runner.run(seqs, is_prefill)
-        self.scheduler.postprocess(seqs, token_ids, is_prefill)
-        for seq in seqs:
-            if seq.is_finished and seq.seq_slot >= 0:
-                self.model_runner.free_seq_slot(seq)
-        return [(s.seq_id, s.completion_token_ids) for s in seqs if s.is_finished], num_tokens
+        fed = sum(s.num_scheduled_tokens for s in batch)
+        sampled = self.model_runner.run(batch, is_prefill)
+        done = self.scheduler.commit(batch, sampled)
+        for seq in done:
+            self.model_runner.free_seq_slot(seq)
+        return [(s.seq_id, s.completion_token_ids) for s in done], (fed if is_prefill else -fed)
 
     def is_finished(self):
         return self.scheduler.is_finished()

@@ -211,7 +211,7 @@ class ModelRunner:
             for pos in range(start, end):     # page = block_table[pos // page_size], row = pos % page_size
                 slot_mapping.append(seq.block_table[pos // self.block_size] * self.block_size + pos % self.block_size)
         seqlens = [cu_q[i + 1] - cu_q[i] for i in range(len(seqs))]
-        fresh = all(s.num_cached_tokens == 0 and s.num_scheduled_tokens == s.num_tokens for s in seqs)
+        fresh = all(s.num_cached_tokens == 0 and s.num_scheduled_tokens == len(s) for s in seqs)
         within = sum(seqlens) <= self.config.max_num_batched_tokens
         dense = len(seqs) > 1 and seqlens[0] > 0 and len(set(seqlens)) == 1 and fresh and within
         grouped = (len(seqs) > 1 and not dense and all(n > 0 for n in seqlens) and fresh and within
@@ -250,12 +250,14 @@ class ModelRunner:
         return self._to_dev(input_ids, torch.int64), self._to_dev(positions, torch.int64)
 
     def prepare_decode(self, seqs):
-        """One new token per sequence (``:451-480``): ``context_lens`` includes it, its cache
-        slot is the last page's next row."""
+        """One new token per sequence (``:451-480``): ``context_lens`` includes it, and its
+        cache slot is its position's row in its position's page (a sequence may hold pages
+        beyond its current length: they are reserved for its lifetime)."""
         input_ids = [s.last_token for s in seqs]
         positions = [len(s) - 1 for s in seqs]
         context_lens = [len(s) for s in seqs]
-        slot_mapping = [s.block_table[-1] * self.block_size + s.last_block_num_tokens - 1 for s in seqs]
+        bs = self.block_size
+        slot_mapping = [s.block_table[p // bs] * bs + p % bs for s, p in zip(seqs, positions)]
         set_context(False, slot_mapping=self._to_dev(slot_mapping, torch.int32),
                     context_lens=self._to_dev(context_lens, torch.int32),
                     block_tables=self.prepare_block_tables(seqs), conv_state_tables=self.conv_state_tables,

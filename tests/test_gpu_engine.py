@@ -36,10 +36,10 @@ def _model(dtype, seed=0):
     return hf, m, sd
 
 
-def _engine(hf, model, eager, max_num_seqs=4):
+def _engine(hf, model, eager, max_num_seqs=4, pages=64):
     from atma_amd.engine import Config, LLMEngine
     cfg = Config(kvcache_block_size=16, max_num_seqs=max_num_seqs, max_num_batched_tokens=4096,
-                 max_model_len=160, num_kvcache_blocks=64, enforce_eager=eager, hf_config=hf)
+                 max_model_len=160, num_kvcache_blocks=pages, enforce_eager=eager, hf_config=hf)
     return LLMEngine(cfg, model=model)
 
 
@@ -54,10 +54,8 @@ def _drive(engine, prompts, new_tokens):
         hist = [list(s.token_ids[:s.num_cached_tokens + s.num_scheduled_tokens]) for s in batch]
         toks = engine.model_runner.run(batch, is_prefill)
         records.append((is_prefill, hist, engine.model_runner.last_logits.float().cpu(), toks))
-        engine.scheduler.postprocess(batch, toks, is_prefill)
-        for s in batch:
-            if s.is_finished:
-                engine.model_runner.free_seq_slot(s)
+        for s in engine.scheduler.commit(batch, toks):
+            engine.model_runner.free_seq_slot(s)
     return seqs, records
 
 
@@ -140,3 +138,20 @@ def test_generate_reports_throughput(dev):
     assert m["prefill_tokens"] == 128 and m["decode_tokens"] == 4 * 7
     assert m["prefill_throughput"] > 0 and m["decode_throughput"] > 0
     engine.exit()
+
+
+def test_tight_page_pool_runs_requests_in_turn_with_the_same_tokens(dev):
+    """A pool that holds one request's lifetime pages at a time: the others wait queued,
+    then reuse the freed pages and state-table rows (zeroed on release).  Tokens equal an
+    unconstrained run's: no request sees another's conv tails or memory state."""
+    from atma_amd.engine import SamplingParams
+    hf, model, _ = _model(torch.bfloat16, seed=6)
+    prompts = _prompts([30, 45, 21], 7)
+    sp = SamplingParams(temperature=0.0, max_tokens=6, ignore_eos=True)
+    out = []
+    for pages in (64, 4):                        # 4 pages = 64 tokens: one request's 51 at most
+        engine = _engine(hf, model, eager=False, pages=pages)
+        res = engine.generate(prompts, sp)
+        out.append([r["token_ids"] for r in res])
+        engine.exit()
+    assert out[0] == out[1]
