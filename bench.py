@@ -102,9 +102,8 @@ class Prefill:
         return self.step_overlap() if self.overlap else self.step_sequential()
 
     def step_sequential(self):
-        """Both ops back to back on one stream."""
-        self.polar()
-        self.memory()
+        """Both ops back to back on one stream.  Returns (c, mag), (o, final state)."""
+        return self.polar(), self.memory()
 
     def step_overlap(self):
         """The memory branch on a second stream; Polar's launch waits (one-wave kernel) until
@@ -114,10 +113,13 @@ class Prefill:
         self.signal.arm()
         self.side.wait_stream(main)
         with torch.cuda.stream(self.side):
-            self.memory(self.signal)
+            mem = self.memory(self.signal)
         self.signal.wait()
-        self.polar()
+        out = self.polar()
         main.wait_stream(self.side)
+        for t in mem:                      # made on the side stream, read on this one
+            t.record_stream(main)
+        return out, mem
 
     def flops(self):
         return polar_flops(self.B, self.T), gdn_flops(self.B, self.T)

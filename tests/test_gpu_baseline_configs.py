@@ -165,8 +165,44 @@ def test_configs2_gated_delta_t262144_bf16(dev):
     assert rel_err(S, S_ref) <= 2e-2, rel_err(S, S_ref)
 
 
+def test_configs2_timed_step_t65536_overlapped(dev):
+    """The configs[2] step exactly as ``bench.py`` times it at T = 65,536, 8 / 2 heads: the
+    memory branch on the side stream with its recurrence unsegmented (start signal), Polar
+    launched once the recurrence has started.  Polar on sampled rows against the exact row
+    oracle; the memory output and final state against the fp32 FLA-contract oracle."""
+    bench = _bench()
+    _say("configs[2] timed step B=1 T=65536 8/2 d=128 bf16, overlapped schedule")
+    w = bench.Prefill(torch, dev, 1, 65536, seed=5)
+    assert w.overlap                         # the layer's schedule at this shape
+    (c, m), (o, S) = w.step_overlap()
+    (c2, m2), (o2, S2) = w.step_sequential() # the sequential schedule: segmented recurrence
+    torch.cuda.synchronize()
+    assert torch.equal(c, c2) and torch.equal(m, m2)
+    # the two schedules' recurrences differ in rounding only
+    assert rel_err(o2.float(), o.float()) <= 1e-2 and rel_err(S2, S) <= 1e-3, (rel_err(o2.float(), o.float()),
+                                                                               rel_err(S2, S))
+    del c2, m2, o2, S2
+    T = w.T
+    rows = torch.tensor([0, 1, 63, 127, 128, 4095, 30001, 65535 - 128, T - 2, T - 1])
+    c_rows, m_rows = c[:, :, rows.to(dev)].float().cpu(), m[:, :, rows.to(dev)].float().cpu()
+    o, S = o.float().cpu(), S.cpu()
+    q, k, v = w.q.float().cpu(), w.k.float().cpu(), w.v.float().cpu()
+    zg, zb = w.zg.cpu(), w.zb.cpu()
+    p = {a: b.float().cpu() for a, b in w.p.items()}
+    del w, c, m
+    n = torch.arange(1, T + 1, dtype=torch.float32)
+    c_ref, m_ref = OP.polar_online(q[:, :, rows], k, v, n[rows], params=p, k_block=8192)
+    assert rel_err(c_rows, c_ref) <= 2e-2, rel_err(c_rows, c_ref)
+    assert rel_err(m_rows, m_ref) <= 2e-2, rel_err(m_rows, m_ref)
+    kx, vx = (t.transpose(1, 2).repeat_interleave(HQ // HKV, 2) for t in (k, v))
+    o_ref, S_ref = OG.chunk_gated_delta_rule(q.transpose(1, 2), kx, vx, F.logsigmoid(zg + 3.9), torch.sigmoid(zb),
+                                             scale=1.0, output_final_state=True, use_qk_l2norm_in_kernel=True)
+    assert rel_err(o, o_ref) <= 2e-2, rel_err(o, o_ref)
+    assert rel_err(S, S_ref) <= 2e-2, rel_err(S, S_ref)
+
+
 # --------------------------------------------------------------------------- configs[3]
-def _bench_decode():
+def _bench():
     if str(ROOT) not in sys.path:
         sys.path.insert(0, str(ROOT))
     import bench
@@ -174,7 +210,7 @@ def _bench_decode():
 
 
 def test_configs3_graph_replay_equals_eager_and_oracle(dev):
-    bench = _bench_decode()
+    bench = _bench()
     _say("configs[3] decode step B=64 ctx~U[1024,32768]: graph replay vs eager vs oracle")
     eager = bench.Decode(torch, dev)
     graph = bench.Decode(torch, dev)        # same seed: identical pages, tables and inputs
