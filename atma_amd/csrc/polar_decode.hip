@@ -1246,7 +1246,8 @@ extern "C" int atma_global_decode_step(
 // No-allocation variant.  The split records live in a file-scope device array instead of
 // a caller workspace.  Each GPU holds its own copy of the array (at its own address) from
 // the library's load until the process ends; the host keeps that address per device,
-// looked up once with hipGetSymbolAddress on the entry point's first call on the device.
+// looked up once with hipGetSymbolAddress on the entry point's first call on the device
+// (which may be inside a stream capture: the lookup runs in relaxed capture mode).
 // Calls that overlap on one GPU share the array and race; nothing in it needs to start at
 // zero (every record the merge reads is written by the split pass of the same call).
 namespace atma {
@@ -1264,8 +1265,14 @@ int decode_scratch_ptr(void** out) {
     return set_error(ATMA_ERR_HIP, "polar_attention_decode_noalloc: no current device");
   std::lock_guard<std::mutex> lock(g_scratch_mutex);
   if (!g_scratch_ptr[dev]) {
+    // The first call may come while the caller's stream is being captured into a graph.
+    // The lookup is no stream work; relaxed capture mode lets it run there, and the
+    // thread's own mode is put back whatever the lookup returns.
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    const hipError_t em = hipThreadExchangeStreamCaptureMode(&mode);
     void* ptr = nullptr;
     hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(decode_scratch));
+    if (em == hipSuccess) hipThreadExchangeStreamCaptureMode(&mode);
     if (e != hipSuccess || !ptr)
       return set_error(ATMA_ERR_HIP, "polar_attention_decode_noalloc: hipGetSymbolAddress: %s",
                        hipGetErrorString(e));

@@ -3,7 +3,9 @@ no counterpart in the reference; for callers that cannot allocate: graph capture
 tight serving loops).  Called through the C ABI, its outputs equal the workspace entry
 point's (``polar_attention_decode``) bit for bit -- the same kernels run -- on two calls
 in a row, the second with a smaller input, so the fixed scratch array's leftover
-contents from the first call never leak into the second."""
+contents from the first call never leak into the second; and under HIP graph capture:
+the first call on the device made inside a capture (in a child process), and replays
+interleaved with other calls that reuse the array."""
 
 import pytest
 import torch
@@ -60,3 +62,37 @@ def test_noalloc_decode_equals_workspace_entry_point(dev):
         torch.cuda.synchronize()
         assert torch.equal(c, c_ref) and torch.equal(m, m_ref), i
         assert torch.isfinite(c.float()).all()
+
+
+def test_noalloc_decode_first_call_inside_graph_capture(dev):
+    """The entry point's first call on the device made under ``torch.cuda.graph`` capture
+    (a fresh child process, so no earlier call has looked the scratch address up), replayed
+    three times: every replay equals the workspace entry point bit for bit."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+    child = Path(__file__).resolve().parent / "noalloc_capture_child.py"
+    r = subprocess.run([sys.executable, "-u", str(child)], capture_output=True, text=True, timeout=110,
+                       env=dict(os.environ))
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0 and r.stdout.strip().endswith("OK")
+
+
+def test_noalloc_decode_replayed_from_a_graph_equals_eager(dev):
+    """Captured after earlier calls (the address already known): replays equal the workspace
+    entry point, with a different launch between replays reusing the same scratch array."""
+    from atma_amd.kernel import polar_attention_decode
+    q, kc, vc, bt, ctx, p = _case(dev, 16, 5000, 9)
+    c_ref, m_ref = polar_attention_decode(q, kc, vc, bt, ctx, **p)
+    _noalloc(q, kc, vc, bt, ctx, p)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        c, m = _noalloc(q, kc, vc, bt, ctx, p)
+    other = _case(dev, 5, 2000, 10)
+    for i in range(3):
+        _noalloc(*other)                         # overwrites the scratch records in between
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(c, c_ref) and torch.equal(m, m_ref), i
