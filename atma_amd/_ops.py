@@ -154,7 +154,7 @@ def polar_attention_bwd_op(q: Tensor, k: Tensor, v: Tensor, gs: Tensor, gL: Tens
     new = torch.empty if Tk > 0 else torch.zeros   # with no keys nothing is written
     dq = new((B, Hq, Tq, d), device=q.device, dtype=q.dtype)
     dt = new((B, Hq, Tq), **f)
-    share = torch.float32 if q.dtype == torch.float32 else torch.bfloat16
+    share = torch.bfloat16 if q.dtype == torch.bfloat16 else torch.float32   # fp16: fp32 shares
     dkv = new((2, B, Hq, Tk, d), device=q.device, dtype=share)   # each query head's share; the group sum follows
     dk, dv = dkv[0], dkv[1]   # the kernel's two outputs
     gL, gQ2, M, temp = (t.to(torch.float32).contiguous() for t in (gL, gQ2, M, temp))

@@ -1032,8 +1032,8 @@ extern "C" int atma_gated_delta_bwd16_chain(const void* kr, const void* kt, cons
   if (!kr || !kt || !qt || !tm || !tt || !rt || !vt || !ot || !got || !f || !s_entry || !ds_end || !u || !dy ||
       !ds0)
     return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_chain: null pointer");
-  if (!aligned16({kr, kt, qt, tm, tt, rt, vt, ot, got}))
-    return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_chain: tiles must be 16-byte aligned");
+  if (!aligned16({kr, kt, qt, tm, tt, rt, vt, ot, got, s_entry, ds_end, u, dy}))
+    return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_chain: tiles and outputs must be 16-byte aligned");
   const int64_t slabs = d / (16 * kChainWaves);  // column slabs (workgroups) per sequence-head
   if (BH * slabs > 0x7fffffff || BH * NC > 0x7fffffff)
     return set_error(ATMA_ERR_INVALID, "gated_delta_bwd16_chain: sizes too large");

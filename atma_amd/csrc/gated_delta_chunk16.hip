@@ -1009,7 +1009,11 @@ __global__ void __launch_bounds__(256) gdn_seg_combine_kernel(GdnArgs a) {
 
 // Segment count and length of a launch (nseg = 1: the plain scan); no segment is empty.
 // The plan assumes MI355X's 256 compute units rather than querying the device, so the
-// results of a given shape do not depend on the GPU (or partition) that computes them.
+// plan of a given shape and schedule does not depend on the GPU (or partition).  The
+// schedule does: a launch with a start flag (the overlapped prefill, which a caller picks
+// from the device's CU count and never under graph capture or autograd) takes the plain
+// scan, and the plain and segmented scans differ in rounding only (the segment entry
+// states are combined in fp32; agreement at 1e-2 of the output is tested at T = 65,536).
 static void gdn16_plan(int64_t BH, int NC, int D, int& nseg, int& seg_len) {
   nseg = gdn16_segments(BH, NC, D, 256);
   seg_len = (NC + nseg - 1) / nseg;

@@ -53,7 +53,7 @@ struct PolarBwdArgs {
   void* dq;             // (B, Hq, Tq, D) in the input dtype
   float* dt;            // (B, Hq, Tq)
   // (B, Hq, Tk, D): each query head's share, grouped heads summed by the caller; fp32 for
-  // fp32 inputs, bf16 for 16-bit inputs (BwShare<T>)
+  // fp32 and fp16 inputs, bf16 for bf16 inputs (BwShare<T>)
   void* dk;
   void* dv;
   int B, Hq, Hkv, Tq, Tk;
@@ -64,7 +64,7 @@ struct PolarBwdArgs {
 template <typename T>
 using BwFrag = std::conditional_t<sizeof(T) == 2, u32x4, float>;
 template <typename T>
-using BwShare = std::conditional_t<sizeof(T) == 2, bf16, float>;
+using BwShare = std::conditional_t<std::is_same_v<T, bf16>, bf16, float>;
 template <typename T>
 constexpr int kBwK = sizeof(T) == 2 ? 32 : 4;  // MFMA k depth
 template <typename T>
@@ -780,8 +780,13 @@ __global__ void __launch_bounds__(256, 2) polar_bwd16_dkdv_kernel(PolarBwdArgs a
 #pragma unroll
     for (int nt = 0; nt < D / 16; ++nt) {
       const f32x4 x = dkT[nt] * a.scale, y = dvT[nt];
-      *(u32x2*)((bf16*)a.dk + base + 16 * nt) = u32x2{pack2<bf16>(x[0], x[1]), pack2<bf16>(x[2], x[3])};
-      *(u32x2*)((bf16*)a.dv + base + 16 * nt) = u32x2{pack2<bf16>(y[0], y[1]), pack2<bf16>(y[2], y[3])};
+      if constexpr (std::is_same_v<BwShare<T>, float>) {
+        *(f32x4*)((float*)a.dk + base + 16 * nt) = x;
+        *(f32x4*)((float*)a.dv + base + 16 * nt) = y;
+      } else {
+        *(u32x2*)((bf16*)a.dk + base + 16 * nt) = u32x2{pack2<bf16>(x[0], x[1]), pack2<bf16>(x[2], x[3])};
+        *(u32x2*)((bf16*)a.dv + base + 16 * nt) = u32x2{pack2<bf16>(y[0], y[1]), pack2<bf16>(y[2], y[3])};
+      }
     }
   }
 }

@@ -125,8 +125,8 @@ int atma_polar_attention_packed_fwd(const void* q, int64_t q_st, int64_t q_sh, c
  * preamble's per-query cotangents and the forward's natural-log reference max);
  * temp: (Hq, Tq) fp32; n_keys: (Tq,) raw counts (the mask).  Outputs, contiguous, every
  * element written when Tk > 0: dq (B, Hq, Tq, d) in dtype, and fp32 dt (B, Hq, Tq) (= sum_j da * sig,
- * the real keys' share of dL/dtemp), dk, dv (B, Hq, Tk, d) (fp32 for fp32 inputs, bf16 for
- * 16-bit inputs): each query head's share, so
+ * the real keys' share of dL/dtemp), dk, dv (B, Hq, Tk, d) (fp32 for fp32 and fp16 inputs, bf16 for
+ * bf16 inputs): each query head's share, so
  * with Hkv < Hq the caller sums the Hq / Hkv consecutive heads of a group (one workgroup
  * per query head fills the GPU at causal T = 2,048; a deterministic sum, no atomics).
  * d = 64 or 128.
