@@ -953,10 +953,434 @@ __global__ void __launch_bounds__(256, 2) polar_fwd16_kernel(PolarFwdArgs args) 
   }
 }
 
+// 16-bit inputs, two query heads of one KV group per workgroup (G even): the ping-pong
+// schedule.  A workgroup of 8 waves owns one 128-row query tile of query heads 2p and
+// 2p + 1 of a KV group; waves 0-3 (group A) serve the first head and waves 4-7 (group B)
+// the second, 32 rows per wave, with the per-wave math of polar_fwd16_kernel.  The two
+// waves that share a SIMD (wave w and wave w + 4) are kept in opposite phases: a wave
+// alternates an MFMA phase -- O^T += V^T P^T for block j - 1, then S^T = K Q^T for block
+// j -- and a VALU phase -- the softmax of block j (exponentials, packing, sums, the rare
+// rescale) -- and group B runs one phase behind group A, with one workgroup barrier per
+// phase.  So while one wave of a SIMD issues its 32 MFMAs the other runs its softmax,
+// instead of the two drifting into step and leaving the matrix unit idle; the MFMA wave
+// holds a raised issue priority.  A wave issues VALU at about half its SIMD's rate on its
+// own (about 7.5 cycles per wave64 FMA, 16 per exp2), so the softmax phase (~1,200
+// cycles) and the MFMA phase (32 MFMAs, ~1,100 cycles) are about even.  Every wave runs
+// the same 2 * nblk + 2 phases (the first and last are idle for one group), so the
+// barrier counts match by construction.
+//
+// K and V tiles are double-buffered with different lifetimes: K(j) is read in phases
+// 2j (A) and 2j + 1 (B), V(j) in phases 2j + 2 and 2j + 3.  At phase 2m group B (then in
+// its softmax phase) copies K(m + 1) (into the K buffer K(m - 1) held) and V(m) (into the
+// buffer of V(m - 2)); both have two phases to land and are waited on at the end of phase
+// 2m + 1.  The two heads share every K / V tile, so a tile is copied once for 256 query
+// rows.  Each wave's arithmetic is polar_fwd16_kernel's, in the same order: the two
+// kernels give the same bits.
+template <typename T, int D>
+__global__ void __launch_bounds__(512, 1) polar_fwd16_pp_kernel(PolarFwdArgs args) {
+  constexpr int BM = 128, BN = 64, CPR = D / 8, NT = D / 32, QSTEPS = D / 16;
+  constexpr int RPI = 64 / CPR;  // rows per wave copy instruction (1 KB)
+  constexpr int TILE = BN * D;   // elements of one K or V tile
+  constexpr int NCP = 16 / RPI;  // copy instructions per wave and tile (16 rows per wave)
+  static_assert(RPI * NCP == 16, "a wave copies 16 rows");
+  __shared__ __attribute__((aligned(16))) T Ks[2 * TILE];
+  __shared__ __attribute__((aligned(16))) T Vs[2 * TILE];
+  __shared__ float s_bounds[4][2];
+  __shared__ float s_vnull[2][D];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2, wq = wave & 3;
+  const int ql = lane & 31, h = lane >> 5;
+
+  // ---- workgroup -> (query tile, b, head pair): tiles in order of decreasing length; the
+  // pairs of one KV group adjacent (and on one XCD when the remap applies)
+  const int G = args.Hq / args.Hkv, G2 = G / 2;
+  const int per_rank = args.B * args.Hkv * G2;
+  const int rank = blockIdx.x / per_rank;
+  int u = blockIdx.x % per_rank;
+  if (args.xcd_remap) {
+    const int x = u & 7, p = u >> 3;
+    u = (x + 8 * (p / G2)) * G2 + p % G2;
+  }
+  const int kvg = u / G2;  // b * Hkv + kv head
+  const int b = kvg / args.Hkv, hk = kvg % args.Hkv;
+  const int hq = hk * G + 2 * (u % G2) + grp;
+  const int q0 = (args.n_qtiles - 1 - rank) * BM;
+  const int Tq = args.Tq, Tk = args.Tk;
+
+  const int hq_u = __builtin_amdgcn_readfirstlane(hq);
+  const float lg_raw = args.len_gain_raw[hq_u], ns_raw = args.null_slope_raw[hq_u];
+  const float nb = args.null_base[hq_u], mb_raw = args.mag_beta_raw[hq_u];
+  const int qi = q0 + wq * 32 + ql;
+  const bool q_ok = qi < Tq;
+  const float n_ld = args.n_keys[min(qi, Tq - 1)];
+
+  const T* qp = (const T*)args.q + b * args.q_sb + hq * args.q_sh;
+  const T* kp = (const T*)args.k + b * args.k_sb + hk * args.k_sh;
+  const T* vp = (const T*)args.v + b * args.v_sb + hk * args.v_sh;
+
+  // ---- direct copies, issued by group B only (at even phases it is in its softmax
+  // phase, so the MFMA group's instruction stream carries no copies): wave w of the group
+  // copies rows 16 w .. 16 w + 15 of a tile, RPI rows per
+  // instruction, lane l at chunk position l % CPR of row row0 + l / CPR (the logical
+  // chunk the swizzle of that tile row stores there: the swizzle depends on the row
+  // modulo 16, so it is taken from the tile row, not from the row within the wave's 8).  Full blocks put the wave's row in the scalar offset; a partial last
+  // block puts the whole row offset into the range-checked per-lane offset.
+  // (the per-lane offsets are recomputed from a laundered lane index at each copy: a few
+  // VALU operations, where keeping them would hold registers through the whole loop)
+  const uint32_t kst2 = (uint32_t)args.k_st * 2u, vst2 = (uint32_t)args.v_st * 2u;
+  auto copy_tile = [&](const T* base, uint32_t st2, int blk, T* dst) __attribute__((always_inline)) {
+    const int rows = min(Tk - blk * BN, BN);
+    const auto rs = buffer_rsrc(base + (int64_t)blk * BN * (st2 / 2u), (uint32_t)(rows - 1) * st2 + 2u * D);
+    uint32_t ln = (uint32_t)lane;
+    asm volatile("" : "+v"(ln));
+    const uint32_t lr = ln / CPR;
+    if (rows == BN) {
+#pragma unroll
+      for (int r = 0; r < NCP; ++r) {
+        const uint32_t row0 = 16u * wq + RPI * r;
+        const uint32_t co = 16u * ((ln % CPR) ^ lds_swizzle<CPR>((int)(row0 + lr)));
+        dma_buf16(rs, lr * st2 + co, row0 * st2, dst + row0 * D);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < NCP; ++r) {
+        const uint32_t row0 = 16u * wq + RPI * r;
+        const uint32_t co = 16u * ((ln % CPR) ^ lds_swizzle<CPR>((int)(row0 + lr)));
+        dma_buf16(rs, (row0 + lr) * st2 + co, 0, dst + row0 * D);
+      }
+    }
+  };
+  auto swz = [](int r, int c) { return r * D + 8 * (c ^ lds_swizzle<CPR>(r)); };
+
+  // ---- prologue: the query operand, the null vector of the wave's head
+  u32x4 qreg16[QSTEPS];
+#pragma unroll
+  for (int s = 0; s < QSTEPS; ++s)
+    qreg16[s] = q_ok ? *(const u32x4*)(qp + (int64_t)qi * args.q_st + 16 * s + 8 * h)
+                     : u32x4{0, 0, 0, 0};
+  if (64 * wq < D)
+    dma_buf4(buffer_rsrc(args.v_null + (int64_t)hq * D, (uint32_t)D * 4u), 4u * (uint32_t)lane,
+             256u * (uint32_t)wq, s_vnull[grp] + 64 * wq);
+
+  const float n_raw = q_ok ? n_ld : 0.f;
+  float n_cal = n_raw;
+  if (args.window > 0 && !args.preserve_length) n_cal = fminf(n_cal, (float)args.window);
+  n_cal = fmaxf(n_cal, 1.f);
+  const float spg = softplus(lg_raw);
+  const float sps = softplus(ns_raw);
+  const float mbeta = softplus(mb_raw);
+  const float temp = 1.f + spg * logf(n_cal);
+  const float nullv = nb + sps * sqrtf(logf(n_cal + 1.f));
+  const float c1 = temp * kLog2e * (1.f / sqrtf((float)D));
+
+  // ---- key-loop bounds: both groups hold the same query rows, so group A's waves publish
+  {
+    float lo = q_ok ? n_raw : 3.0e38f, hi = q_ok ? n_raw : -1.f;
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    if (lane == 0 && grp == 0) {
+      s_bounds[wq][0] = lo;
+      s_bounds[wq][1] = hi;
+    }
+  }
+  __syncthreads();
+  const float w_nlo = s_bounds[wq][0], w_nhi = s_bounds[wq][1];
+  float g_nlo = s_bounds[0][0], g_nhi = s_bounds[0][1];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) {
+    g_nlo = fminf(g_nlo, s_bounds[w][0]);
+    g_nhi = fmaxf(g_nhi, s_bounds[w][1]);
+  }
+  int kend = 0, kbeg = 0;
+  if (g_nhi > 0.f) {
+    const float hiF = fminf(g_nhi, (float)Tk);
+    kend = (int)ceilf(hiF);
+    if (args.is_causal) kend = min(kend, min(q0 + BM, Tk));
+    if (args.window > 0) kbeg = max((int)floorf(g_nlo) - args.window, 0);
+    kbeg = (kbeg / BN) * BN;
+  }
+  const int nblk_beg = kbeg / BN, nblk_end = (kend + BN - 1) / BN;
+  const int nblk = nblk_end > nblk_beg ? nblk_end - nblk_beg : 0;
+  if (nblk > 0 && grp == 1) copy_tile(kp, kst2, nblk_beg, Ks);  // K(0) into K buffer 0
+
+#pragma unroll
+  for (int s = 0; s < QSTEPS; ++s) asm volatile("" ::"v"(qreg16[s]));
+
+  float m_run = kSentinel, l_part = 0.f, q2_part = 0.f;
+  f32x16 oacc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) oacc[t] = f32x16{};
+  f32x16 sacc[2] = {f32x16{}, f32x16{}};
+  u32x4 pb[4] = {};
+
+  const int arow = a_row_key(ql);
+  const int gq = lane >> 4, sl = lane & 15;
+  const int vkey = 8 * (gq >> 1) + (sl >> 2);
+  const int vcol = 16 * (gq & 1) + 4 * (sl & 3);
+
+  // MFMA phase of local block j: PV(j - 1) from V buffer (j - 1) % 2, then S(j) from K
+  // buffer j % 2.  JP = j % 2 is a compile-time constant, so every LDS operand address is
+  // a loop-invariant lane offset plus an immediate.
+  // MFMA phase of local block j: PV(j - 1) from V buffer (j - 1) % 2, then S(j) from K
+  // buffer j % 2.  JP = j % 2 is a compile-time constant, so every LDS operand address is
+  // a loop-invariant lane offset plus an immediate.  One wave per SIMD issues MFMAs in
+  // this phase, so its operand reads run ahead explicitly: V^T fragments three MFMAs
+  // ahead, K fragments two steps (four MFMAs) ahead.
+  auto mfma_phase = [&](int j, auto JP) __attribute__((always_inline)) {
+    constexpr int jp = decltype(JP)::value;
+    __builtin_amdgcn_s_setprio(1);  // the MFMA wave first when both waves of a SIMD can issue
+    if (j >= 1) {
+      const T* Vb = Vs + (jp ^ 1) * TILE;
+      auto vfrag = [&](int i) __attribute__((always_inline)) {
+        const int t = i % NT, ps = i / NT;
+        const int kr = 16 * ps + vkey, col = 32 * t + vcol;
+        const u32x2 lo = lds_read_tr16(Vb + swz(kr, col >> 3) + (col & 7));
+        const u32x2 hi = lds_read_tr16(Vb + swz(kr + 4, col >> 3) + (col & 7));
+        return u32x4{lo[0], lo[1], hi[0], hi[1]};
+      };
+      constexpr int NV = 4 * NT, VD = 3;
+      u32x4 vq[VD];
+#pragma unroll
+      for (int i = 0; i < VD; ++i) vq[i] = vfrag(i);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        oacc[i % NT] = mfma32<T>(vq[i % VD], pb[i / NT], oacc[i % NT]);
+        if (i + VD < NV) vq[i % VD] = vfrag(i + VD);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * VD, 0);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (i + VD < NV) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+    }
+    if (j < nblk) {
+      const T* Kb = Ks + jp * TILE;
+      u32x4 kf[2][2];
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        kf[st][0] = *(const u32x4*)(Kb + swz(arow, 2 * st + h));
+        kf[st][1] = *(const u32x4*)(Kb + swz(32 + arow, 2 * st + h));
+      }
+#pragma unroll
+      for (int st = 0; st < QSTEPS; ++st) {
+        sacc[0] = mfma32<T>(kf[st & 1][0], qreg16[st], st ? sacc[0] : f32x16{});
+        sacc[1] = mfma32<T>(kf[st & 1][1], qreg16[st], st ? sacc[1] : f32x16{});
+        if (st + 2 < QSTEPS) {
+          kf[st & 1][0] = *(const u32x4*)(Kb + swz(arow, 2 * (st + 2) + h));
+          kf[st & 1][1] = *(const u32x4*)(Kb + swz(32 + arow, 2 * (st + 2) + h));
+        }
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+      for (int st = 0; st < QSTEPS; ++st) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        if (st + 2 < QSTEPS) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
+  };
+
+  // VALU phase of local block j: mask (blocks crossing a row's valid range), the
+  // optimistic exponentials against the running max, the sums, and the rare rescale
+  constexpr float kSafe = __is_same(T, bf16) ? 1048576.f : 16384.f;
+  auto valu_phase = [&](int j) __attribute__((always_inline)) {
+    const int k0 = (nblk_beg + j) * BN;
+    const bool full = (k0 + BN <= (int)fminf(w_nlo, (float)Tk)) &&
+                      (args.window <= 0 || (float)k0 >= w_nhi - (float)args.window);
+    if (!full) {
+      const float tkf = (float)Tk;
+      const int key_hi = (int)ceilf(fminf(n_raw, tkf)) - k0;
+      const int key_lo =
+          args.window > 0 ? (int)ceilf(fminf(n_raw - (float)args.window, tkf)) - k0 : -(1 << 30);
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int key = st_key(jj, i, h);
+          sacc[jj][i] = ((key < key_hi) & (key >= key_lo)) ? sacc[jj][i] : -INFINITY;
+        }
+    }
+    float ls = 0.f, qs = 0.f;
+    auto exp_pack = [&]() __attribute__((always_inline)) {
+      const float neg_m = -m_run;
+      ls = qs = 0.f;
+#pragma unroll
+      for (int ps = 0; ps < 4; ++ps) {
+        const int jj = ps >> 1, base = 8 * (ps & 1);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[jj][base + 2 * w], c1, neg_m));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[jj][base + 2 * w + 1], c1, neg_m));
+          pb[ps][w] = pack2<T>(p0, p1);
+        }
+      }
+      const uint32_t one2 = pack2<T>(1.f, 1.f);
+#pragma unroll
+      for (int ps = 0; ps < 4; ++ps)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          ls = dot2<T>(pb[ps][w], one2, ls);
+          qs = dot2<T>(pb[ps][w], pb[ps][w], qs);
+        }
+    };
+    bool redo = j == 0;
+    if (!redo) {
+      exp_pack();
+      redo = __ballot(!(ls <= kSafe)) != 0;
+    }
+    if (redo) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[jj][i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = fmaxf(m_run, mx * c1);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      m_run = m_new;
+      l_part *= alpha;
+      q2_part *= alpha * alpha;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) oacc[t] *= alpha;
+      exp_pack();
+    }
+    l_part += ls;
+    q2_part += qs;
+  };
+
+  // ---- the phases.  Global phase p ends with a workgroup barrier for every wave, NP =
+  // 2 nblk + 2 of them.  Group A: MFMA(j) at p = 2j (j = 0 .. nblk), softmax(j) at 2j + 1;
+  // group B one phase later (idle at p = 0).  Copies K(m + 1), V(m) at every even p = 2m,
+  // waited on at the end of the odd phase that follows.  Each group runs its own straight
+  // loop over pairs of blocks, so buffer parities are compile-time constants.
+  auto copies = [&](int m, auto MP) __attribute__((always_inline)) {
+    constexpr int mp = decltype(MP)::value;  // m % 2
+    if (grp == 0) return;
+    if (m + 1 < nblk) copy_tile(kp, kst2, nblk_beg + m + 1, Ks + (mp ^ 1) * TILE);
+    if (m < nblk) copy_tile(vp, vst2, nblk_beg + m, Vs + mp * TILE);
+  };
+  using C0 = std::integral_constant<int, 0>;
+  using C1 = std::integral_constant<int, 1>;
+  if (nblk > 0) {
+    wait_vmcnt<0>();
+    lds_barrier();  // K(0) has landed for every wave
+    if (grp == 0) {
+      for (int j = 0;; j += 2) {
+        copies(j, C0{});            // p = 2j
+        mfma_phase(j, C0{});
+        lds_barrier();
+        if (j == nblk) break;
+        valu_phase(j);              // p = 2j + 1
+        wait_vmcnt<0>();
+        lds_barrier();
+        copies(j + 1, C1{});        // p = 2j + 2
+        mfma_phase(j + 1, C1{});
+        lds_barrier();
+        if (j + 1 == nblk) break;
+        valu_phase(j + 1);          // p = 2j + 3
+        wait_vmcnt<0>();
+        lds_barrier();
+      }
+      wait_vmcnt<0>();              // p = 2 nblk + 1: idle
+      lds_barrier();
+    } else {
+      copies(0, C0{});              // p = 0: idle
+      lds_barrier();
+      for (int j = 0;; j += 2) {
+        mfma_phase(j, C0{});        // p = 2j + 1
+        wait_vmcnt<0>();
+        lds_barrier();
+        if (j == nblk) break;
+        copies(j + 1, C1{});        // p = 2j + 2
+        valu_phase(j);
+        lds_barrier();
+        mfma_phase(j + 1, C1{});    // p = 2j + 3
+        wait_vmcnt<0>();
+        lds_barrier();
+        if (j + 1 == nblk) break;
+        copies(j + 2, C0{});        // p = 2j + 4
+        valu_phase(j + 1);
+        lds_barrier();
+      }
+    }
+  }
+  wait_vmcnt<0>();  // the null vector has landed (also with no key block) ...
+  __syncthreads();  // ... for every wave
+
+  // ---- fold the null sink, normalise, magnitude (as polar_fwd16_kernel)
+  float L = l_part + __shfl_xor(l_part, 32, 64);
+  float Q2 = q2_part + __shfl_xor(q2_part, 32, 64);
+  const float an2 = temp * nullv * kLog2e;
+  const float mn = fmaxf(m_run, an2);
+  const float al = exp2f(m_run - mn);
+  L *= al;
+  Q2 *= al * al;
+  const float pn = exp2f(an2 - mn);
+  const float Z = L + pn;
+  float ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int d = 32 * t + 8 * (i >> 2) + 4 * h + (i & 3);
+      const float s = oacc[t][i] * al + pn * s_vnull[grp][d];
+      oacc[t][i] = s;
+      ss += s * s;
+    }
+  }
+  ss += __shfl_xor(ss, 32, 64);
+  const float inv = 1.f / fmaxf(sqrtf(ss), args.eps);
+  const float n_eff = L * L / fmaxf(Q2, 1e-30f);
+  const float m_eff = n_eff * (L / fmaxf(Z, args.eps));
+  const float magv = tanhf(mbeta * log1pf(m_eff));
+
+  if (q_ok) {
+    const int64_t row = ((int64_t)b * args.Hq + hq) * args.Tq + qi;
+    T* cp = (T*)args.c + b * args.c_sb + hq * args.c_sh + qi * args.c_st;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d = 32 * t + 8 * g4 + 4 * h;
+        u32x2 pk = {pack2<T>(oacc[t][4 * g4] * inv, oacc[t][4 * g4 + 1] * inv),
+                    pack2<T>(oacc[t][4 * g4 + 2] * inv, oacc[t][4 * g4 + 3] * inv)};
+        *(u32x2*)(cp + d) = pk;
+      }
+    }
+    if (h == 0) {
+      ((T*)args.mag)[b * args.m_sb + hq * args.m_sh + qi * args.m_st] = (T)magv;
+      if (args.stat_m) args.stat_m[row] = mn * kLn2;
+      if (args.stat_l) args.stat_l[row] = L;
+      if (args.stat_q2) args.stat_q2[row] = Q2;
+    }
+    if (args.stat_s) {
+      float* sp = args.stat_s + row * D;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; ++g4) {
+          const int d = 32 * t + 8 * g4 + 4 * h;
+          f32x4 x = {oacc[t][4 * g4], oacc[t][4 * g4 + 1], oacc[t][4 * g4 + 2], oacc[t][4 * g4 + 3]};
+          *(f32x4*)(sp + d) = x;
+        }
+    }
+  }
+}
+
 template <typename T, int D>
 static int launch_fwd(PolarFwdArgs a, hipStream_t stream) {
   const int G = a.Hq / a.Hkv;
   if constexpr (sizeof(T) == 2) {
+    if (G % 2 == 0 && !a.tile_seq_start) {
+      // two query heads of a KV group per workgroup, the ping-pong schedule
+      const int64_t per_rank = (int64_t)a.B * a.Hkv * (G / 2);
+      a.xcd_remap = (per_rank % (8 * (G / 2)) == 0) ? 1 : 0;
+      polar_fwd16_pp_kernel<T, D><<<dim3((unsigned)(a.n_qtiles * per_rank)), dim3(512), 0, stream>>>(a);
+      return check_launch("polar_attention_fwd");
+    }
     // one query tile per workgroup
     const int64_t per_rank = (int64_t)a.B * a.Hq;
     a.xcd_remap = (per_rank % (8 * G) == 0) ? 1 : 0;
