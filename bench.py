@@ -1,24 +1,27 @@
 """Benchmark of ATMA's global-layer mixer on one MI355X.
 
-Default workload (the `value`): BASELINE.json configs[1] -- bf16 global-layer prefill,
-B=8, T=2048, 8 query / 2 KV heads, d=128: Polar attention forward (GQA in-kernel) plus
-the gated-delta chunked prefill (C=64, fp32 state from zero, memory gate / beta logits
-activated inside the prefill kernel's load as the layer does: logsigmoid(z + 3.9), sigmoid(z)).  One step = both ops over
-the resident batch in the global layer's schedule for the shape: back to back on one
-stream, or -- when the recurrence kernel's grid takes at most a quarter of the CUs, as
-at B=1, T=65,536 -- the memory branch on a second stream with Polar launched once the
-recurrence has started (both schedules are reported: ms_sequential, ms_overlap).
-value = (Polar + gated-delta algorithmic FLOPs) / step time.
+Default workload (the `value`): BASELINE.json configs[2] at T=65,536 -- the north-star
+long-context prefill, bf16, B=1, 8 query / 2 KV heads, d=128: Polar attention forward
+(GQA in-kernel) plus the gated-delta chunked prefill (C=64, fp32 state from zero, memory
+gate / beta logits activated inside the prefill kernel's load as the layer does:
+logsigmoid(z + 3.9), sigmoid(z)).  One step = both ops over the resident sequence in the
+global layer's schedule for the shape: back to back on one stream, or -- when the
+recurrence kernel's grid takes at most a quarter of the CUs, as at B=1, T=65,536 -- the
+memory branch on a second stream with Polar launched once the recurrence has started
+(both schedules are reported: ms_sequential, ms_overlap).
+value = (Polar + gated-delta algorithmic FLOPs) / step time; `roofline` is the Polar
+kernel alone at that shape (HIP events on its stream).
 
-Also reported in the same JSON line: configs[2] (B=1, T=65,536 and 262,144) and
-configs[3] (paged decode step: 64 sequences, ctx ~ U[1024, 32768], 256-token pages in
-a shuffled pool: the layer's fused decode route -- KV write + Polar decode + gated-delta
-step in two launches -- replayed as a HIP graph; the three separate calls timed beside
-it), each with its roofline fraction; configs[4] (the 378M model served through the
-paged engine, 32 x 2,048-token prompts -> 256 greedy tokens: prefill / decode tok/s and
-wall time); configs[0] (one global block in fp32 on the GPU); the training steps of the
-layer's two branches at the configs[1] shape (Polar and the gated-delta memory, forward +
-backward); plus the CPU oracle timed on this host (configs[1] sample and configs[0]).
+Also reported in the same JSON line: configs[1] (B=8, T=2,048, `breakdown_c2`),
+configs[2] at T=262,144 (`prefill_long`), configs[3] (paged decode step: 64 sequences,
+ctx ~ U[1024, 32768], 256-token pages in a shuffled pool: the layer's fused decode route
+-- KV write + Polar decode + gated-delta step in two launches -- replayed as a HIP
+graph; the three separate calls timed beside it), each with its roofline fraction;
+configs[4] (the 378M model served through the paged engine, 32 x 2,048-token prompts ->
+256 greedy tokens: prefill / decode tok/s and wall time); configs[0] (one global block
+in fp32 on the GPU); the training steps of the layer's two branches at the configs[1]
+shape (Polar and the gated-delta memory, forward + backward); plus the CPU oracle timed
+on this host (configs[2] extrapolated from a row / token sample, and configs[0] exact).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c1|c2|c3|c4|c5|ops|train|copy|cpu] [--no-cpu]
 """
@@ -475,47 +478,76 @@ def bench_c5(torch, dev, n_prompts=32, prompt_len=2048, new_tokens=256, seed=0):
             "prefill_tokens": m["prefill_tokens"], "decode_tokens": m["decode_tokens"]}
 
 
-def cpu_baseline(torch):
-    """The CPU oracle (oracle/: Polar streaming form + gated-delta chunked UT form, fp32)
-    on a bounded sample of configs[1]: one of the 8 sequences, full T = 2048, all heads;
-    plus configs[0] (the whole global block) as tokens/s."""
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def cpu_baseline(torch, T=65536, row_stride=256, gdn_tokens=8192):
+    """The CPU oracle (oracle/, fp32 torch on this host's cores) on the headline workload,
+    configs[2] (B=1, T=65,536, 8/2 heads, d=128), timed on a bounded sample and
+    EXTRAPOLATED to the full step (the full step would take tens of minutes on the CPU):
+
+    * Polar: the exact row oracle (oracle/polar.polar_rows, the streaming form) on the query
+      rows row_stride - 1, 2 row_stride - 1, ..., T - 1 of all 8 heads, each against all of
+      its causal keys; scaled by the causal (query, key) pairs of the full sequence,
+      T (T + 1) / 2, over the sampled rows' counts (the cost is linear in those pairs);
+    * gated delta: oracle chunk_gated_delta_rule (the chunked UT form) over the first
+      gdn_tokens tokens, scaled by T / gdn_tokens (the chunked scan is linear in T).
+
+    value = (Polar + gated-delta algorithmic FLOPs at T) / the extrapolated time.  Inputs are
+    seeded N(0, 1) like the GPU workload; median of up to 5 runs within about 20 s.  Also
+    reports configs[0] (one global block, exact, no extrapolation) under "c1"."""
     from oracle import gated_delta as OG
     from oracle import polar as OP
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
-    T = 2048
     q = torch.randn(1, HQ, T, D, generator=g)
     k = torch.randn(1, HKV, T, D, generator=g)
     v = torch.randn(1, HKV, T, D, generator=g)
-    zg, zb = torch.randn(1, T, HQ, generator=g), torch.randn(1, T, HQ, generator=g)
+    zg, zb = torch.randn(1, gdn_tokens, HQ, generator=g), torch.randn(1, gdn_tokens, HQ, generator=g)
     p = {n: t.cpu() for n, t in _params(torch, "cpu").items()}
     n = torch.arange(1, T + 1, dtype=torch.float32)
+    rows = torch.arange(row_stride - 1, T, row_stride)
+    pair_scale = (T * (T + 1) / 2) / float((rows + 1).sum())
+    tok_scale = T / gdn_tokens
+    qg = q[:, :, :gdn_tokens].transpose(1, 2)
+    kx = k[:, :, :gdn_tokens].repeat_interleave(HQ // HKV, 1).transpose(1, 2)
+    vx = v[:, :, :gdn_tokens].repeat_interleave(HQ // HKV, 1).transpose(1, 2)
+    gl, bt = torch.nn.functional.logsigmoid(zg + 3.9), torch.sigmoid(zb)
 
-    def run():
-        OP.polar_online(q, k, v, n, params=p, k_block=512)
-        kx, vx = k.repeat_interleave(4, 1), v.repeat_interleave(4, 1)
-        OG.chunk_gated_delta_rule(q.transpose(1, 2), kx.transpose(1, 2), vx.transpose(1, 2),
-                                  torch.nn.functional.logsigmoid(zg + 3.9), torch.sigmoid(zb),
-                                  scale=1.0, output_final_state=True, use_qk_l2norm_in_kernel=True)
+    def polar_sample():
+        with torch.no_grad():
+            OP.polar_rows(q, k, v, n, rows, params=p, k_block=4096)
 
-    sec, runs = _median_runs(run, 12.0)
+    def gdn_sample():
+        with torch.no_grad():
+            OG.chunk_gated_delta_rule(qg, kx, vx, gl, bt, scale=1.0, output_final_state=True,
+                                      use_qk_l2norm_in_kernel=True)
+
+    s_polar, r_polar = _median_runs(polar_sample, 10.0, min_runs=3, max_runs=5)
+    s_gdn, r_gdn = _median_runs(gdn_sample, 6.0, min_runs=3, max_runs=5)
+    sec = s_polar * pair_scale + s_gdn * tok_scale
     flops = polar_flops(1, T) + gdn_flops(1, T)
-    model = ""
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
     return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"configs[1] sequence 0 of 8 (B=1, T=2048, 8/2 heads, d=128), fp32 torch CPU, "
-                      f"median of {runs} runs = {sec:.3f} s",
-            "torch_threads": torch.get_num_threads(), "cpu_model": model,
+            "extrapolated": True,
+            "sample": (f"configs[2] B=1 T={T}, 8/2 heads, d=128, fp32 torch CPU oracle: Polar exact rows "
+                       f"every {row_stride} ({len(rows)} rows x 8 heads, all causal keys; median of "
+                       f"{r_polar} runs {s_polar:.3f} s) x {pair_scale:.1f} (causal pairs), plus the chunked "
+                       f"gated delta over the first {gdn_tokens} tokens (median of {r_gdn} runs {s_gdn:.3f} s) "
+                       f"x {tok_scale:.0f}; extrapolated step {sec:.1f} s"),
+            "ms_per_step_extrapolated": sec * 1e3, "polar_s_extrapolated": s_polar * pair_scale,
+            "gdn_s_extrapolated": s_gdn * tok_scale,
+            "torch_threads": torch.get_num_threads(), "cpu_model": _cpu_model(),
             "c1": dict(cpu_c1(torch), workload="configs[0]: one global block (Polar + gated-delta "
                                                 "memory + MLP), B=1, T=2048, hidden 1024, 8/2 heads, "
-                                                "d=128, fp32, params N(0,0.02) seed 0")}
+                                                "d=128, fp32, params N(0,0.02) seed 0 (exact, not extrapolated)")}
 
 
 def copy_calibration(torch, dev, steps):
@@ -529,10 +561,10 @@ def copy_calibration(torch, dev, steps):
     return {"bytes_read": n, "bytes_written": n, "ms": ms, "gbs": 2 * n / (ms * 1e-3) / 1e9}
 
 
-def _traffic():
+def _traffic(name):
     """HBM bytes per Polar prefill launch measured with rocprofv3 --pmc (FETCH_SIZE +
     WRITE_SIZE, scaled by a copy-kernel calibration), committed under profiles/."""
-    f = ROOT / "profiles" / "polar_prefill_c2_traffic.json"
+    f = ROOT / "profiles" / name
     try:
         return json.loads(f.read_text()).get("bytes_per_launch")
     except (OSError, ValueError):
@@ -569,17 +601,18 @@ def main(argv=None):
     if args.only == "cpu":
         print(json.dumps({"cpu_baseline": cpu_baseline(torch)}))
         return 0
-    if args.only in (None, "c2"):
-        c2 = bench_prefill(torch, dev, 8, 2048, args.steps, args.warmup)
-        print(f"# c2 prefill: {json.dumps(c2)}", file=sys.stderr, flush=True)
-        out["c2"] = c2
     if args.only in (None, "c3"):
-        c3 = [bench_prefill(torch, dev, 1, 65536, max(2, args.steps // 4), 1)]
+        # the headline: configs[2] at T = 65,536, `warmup` untimed and `steps` timed steps
+        c3 = [bench_prefill(torch, dev, 1, 65536, args.steps, args.warmup)]
         print(f"# c3 prefill T=65536: {json.dumps(c3[0])}", file=sys.stderr, flush=True)
         if not args.no_long:
             c3.append(bench_prefill(torch, dev, 1, 262144, 2, 1))
             print(f"# c3 prefill T=262144: {json.dumps(c3[1])}", file=sys.stderr, flush=True)
         out["c3"] = c3
+    if args.only in (None, "c2"):
+        c2 = bench_prefill(torch, dev, 8, 2048, args.steps, args.warmup)
+        print(f"# c2 prefill: {json.dumps(c2)}", file=sys.stderr, flush=True)
+        out["c2"] = c2
     if args.only in (None, "c4"):
         c4 = bench_decode(torch, dev, args.steps, args.warmup)
         print(f"# c4 decode: {json.dumps(c4)}", file=sys.stderr, flush=True)
@@ -606,37 +639,38 @@ def main(argv=None):
         print(json.dumps(out))
         return 0
 
-    c2 = out["c2"]
+    c3, c2 = out["c3"][0], out["c2"]
+    rnd = lambda d: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in d.items()}  # noqa: E731
     line = {
         "metric": METRIC,
-        "value": round(c2["tflops"], 3),
+        "value": round(c3["tflops"], 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(c2["ms_per_step"], 4),
+        "ms_per_step": round(c3["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) q/k/v and gate logits; Polar params at the reference priors)",
-        "config": {"workload": "configs[1]: global-layer prefill, Polar fwd + gated-delta chunked "
-                               "(C=64, fp32 state from 0)", "B": 8, "T": 2048, "q_heads": HQ,
-                   "kv_heads": HKV, "head_dim": D, "mfma_frac_of_bf16_peak": round(c2["mfma_frac"], 4)},
-        "roofline": {"bound": "mfma", "kernel": "polar_fwd16_kernel<bf16,128>",
-                     "achieved": round(c2["polar_tflops"], 2), "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(c2["polar_mfma_frac"], 4),
-                     "traffic": _traffic()},
-        "breakdown_c2": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c2.items()},
-        "prefill_long": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
-                         for r in out["c3"]],
-        "decode": [{k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
-                   for r in out["c4"]],
-        "inference_ops": {n: {k: (round(v, 4) if isinstance(v, float) else v) for k, v in r.items()}
-                          for n, r in out["ops"].items()},
-        "block_c1_gpu": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out["c1"].items()},
-        "serve_c5": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out["c5"].items()},
-        "train_c2": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in out["train"].items()},
+        "config": {"workload": "configs[2]: long-context single-sequence global-layer prefill, Polar fwd + "
+                               "gated-delta chunked (C=64, fp32 state from 0), B=1, T=65536, in the layer's "
+                               f"schedule ({c3['schedule']})", "B": 1, "T": 65536, "q_heads": HQ,
+                   "kv_heads": HKV, "head_dim": D, "mfma_frac_of_bf16_peak": round(c3["mfma_frac"], 4)},
+        "roofline": {"bound": "mfma", "kernel": "polar_fwd16_pp_kernel<bf16,128>",
+                     "achieved": round(c3["polar_tflops"], 2), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(c3["polar_mfma_frac"], 4),
+                     "traffic": _traffic("polar_prefill_c3_t65536_traffic.json"),
+                     "launch_ms": round(c3["polar_ms"], 4), "flops_per_launch": c3["polar_flops"]},
+        "breakdown_c3": rnd(c3),
+        "breakdown_c2": dict(rnd(c2), roofline_traffic=_traffic("polar_prefill_c2_traffic.json")),
+        "prefill_long": [rnd(r) for r in out["c3"][1:]],
+        "decode": [rnd(r) for r in out["c4"]],
+        "inference_ops": {n: rnd(r) for n, r in out["ops"].items()},
+        "block_c1_gpu": rnd(out["c1"]),
+        "serve_c5": rnd(out["c5"]),
+        "train_c2": rnd(out["train"]),
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(torch)
