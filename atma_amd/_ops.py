@@ -585,6 +585,30 @@ def _(logits):
     return torch.empty_like(logits)
 
 
+@torch.library.custom_op("atma_hip::linear_tokens", mutates_args=())
+def linear_tokens_op(x: Tensor, weight: Tensor, bias: Optional[Tensor]) -> Tensor:
+    """y = x weight^T (+ bias) for a few token rows (x (M, K), M <= 32): the decode
+    projection of the served model, weights streamed once (``atma_linear_tokens``)."""
+    _need_cuda(x, weight)
+    lib = _lib.load()
+    M, K = x.shape
+    N = weight.shape[0]
+    if x.stride(1) != 1 or weight.stride(1) != 1:
+        raise ValueError("linear_tokens: x and weight need unit inner stride")
+    out = torch.empty((M, N), device=x.device, dtype=x.dtype)
+    b = bias.contiguous() if bias is not None else None
+    rc = lib.atma_linear_tokens(x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
+                                None if b is None else b.data_ptr(), out.data_ptr(), out.stride(0),
+                                M, N, K, _lib.dtype_code(x.dtype), _lib.stream_handle(x.device))
+    _lib.check(rc, "linear_tokens")
+    return out
+
+
+@linear_tokens_op.register_fake
+def _(x, weight, bias):
+    return x.new_empty((x.shape[0], weight.shape[0]))
+
+
 @torch.library.custom_op("atma_hip::packed_causal_conv1d", mutates_args=("state_table",))
 def packed_causal_conv1d_op(x: Tensor, weight: Tensor, state_table: Tensor, token_seq_starts: Tensor,
                             token_seq_ends: Tensor, token_seq_slots: Tensor) -> Tensor:

@@ -20,7 +20,8 @@ from .. import _lib
 _lib.load()   # raises HipLibraryMissing (ImportError) when the library is absent
 
 from .conv import causal_conv1d_decode_step  # noqa: E402
-from .inference_ops import packed_causal_conv1d, softcap_logits, squared_relu_gate  # noqa: E402
+from .inference_ops import (linear_tokens, linear_tokens_supported, packed_causal_conv1d,  # noqa: E402
+                            softcap_logits, squared_relu_gate)
 from .gated_delta import (StartSignal, chunk_gated_delta_rule, gated_delta_decode_step,  # noqa: E402
                           gated_delta_gates, recurrence_pays_to_overlap)
 from .polar import (global_decode_step, global_decode_step_supported, polar_attention_decode,  # noqa: E402
@@ -43,6 +44,8 @@ __all__ = [
     "global_decode_step_supported",
     "gated_delta_decode_step",
     "chunk_gated_delta_rule",
+    "linear_tokens",
+    "linear_tokens_supported",
     "gated_delta_gates",
     "causal_conv1d_decode_step",
     "squared_relu_gate",

@@ -6,7 +6,8 @@ errors): ``squared_relu_gate`` (:123-135, the MLP activation of
 ``inference/models/atma.py:750-754``) and ``packed_causal_conv1d`` (:138-160, the grouped
 fresh prefill's depthwise convolutions, ``inference/models/atma.py:431-442, 648-652``).
 The prototype ``linear_head_rms`` (:163-189) is not part of the served path and is not
-provided.
+provided.  ``linear_tokens`` has no counterpart there: the served model's projection of a
+few token rows (one per decoding sequence), where the reference calls the vendor GEMM.
 """
 
 import torch
@@ -57,3 +58,26 @@ def packed_causal_conv1d(x, weight, state_table, token_seq_starts, token_seq_end
         raise ValueError("token maps must have one entry per token")
     weight = weight.to(dtype=x.dtype)
     return torch.ops.atma_hip.packed_causal_conv1d(x, weight, state_table, *maps)
+
+
+def linear_tokens_supported(rows, out_features, in_features, dtype):
+    """True for the shapes ``linear_tokens`` serves: 16-bit, at most 32 rows, out_features a
+    multiple of 16 and in_features 1024 or 2048 (the C ABI's ``atma_linear_tokens_supported``;
+    wider inputs read the activation rows from L2 once per output tile more than they read
+    weights, and the vendor GEMM serves them better)."""
+    return (dtype in (torch.bfloat16, torch.float16) and 1 <= rows <= 32 and out_features >= 16
+            and out_features % 16 == 0 and in_features in (1024, 2048))
+
+
+@torch.no_grad()
+def linear_tokens(x, weight, bias=None):
+    """``F.linear(x, weight, bias)`` for x (rows, in_features) with rows <= 32: the weights
+    are streamed once (one workgroup per 16 output features, 32 for wide outputs, K split
+    256 per wave, fp32 accumulation, one rounding).  Deterministic."""
+    if x.dim() != 2 or weight.dim() != 2 or weight.shape[1] != x.shape[1]:
+        raise ValueError("expected x [rows, in_features], weight [out_features, in_features]")
+    if not linear_tokens_supported(x.shape[0], weight.shape[0], x.shape[1], x.dtype):
+        raise ValueError(f"linear_tokens: unsupported shape {tuple(x.shape)} x {tuple(weight.shape)} {x.dtype}")
+    if weight.dtype != x.dtype or (bias is not None and bias.dtype != x.dtype):
+        raise ValueError("x, weight and bias must share a dtype")
+    return torch.ops.atma_hip.linear_tokens(x, weight, bias)

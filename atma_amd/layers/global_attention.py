@@ -41,7 +41,8 @@ from ..kernel import (StartSignal, causal_conv1d_decode_step, chunk_gated_delta_
                       gated_delta_decode_step, gated_delta_gates, global_decode_step, polar_attention,
                       polar_attention_decode, polar_attention_fwd, polar_attention_packed_fwd,
                       recurrence_pays_to_overlap)
-from ..kernel.inference_ops import packed_causal_conv1d, squared_relu_gate
+from ..kernel.inference_ops import (linear_tokens, linear_tokens_supported, packed_causal_conv1d,
+                                     squared_relu_gate)
 from .attention import store_kvcache
 
 # Polar structural priors (model/reference.py:17-20)
@@ -52,10 +53,21 @@ MAG_BETA_INIT = -1.5
 
 
 class Linear(nn.Linear):
-    """``F.linear`` with weights cast to the input dtype (``model/reference.py:22-28``)."""
+    """``F.linear`` with weights cast to the input dtype (``model/reference.py:22-28``).
+
+    Inference calls on a few token rows (a decode step: one row per sequence) at the shapes
+    ``linear_tokens`` serves run that HIP kernel, which streams the weights once; every
+    other call (training, prefill, other shapes) is ``F.linear``."""
 
     def forward(self, x):
-        return F.linear(x, self.weight.type_as(x), None if self.bias is None else self.bias.type_as(x))
+        w = self.weight.type_as(x)
+        b = None if self.bias is None else self.bias.type_as(x)
+        if x.is_cuda and not torch.is_grad_enabled() and x.dim() >= 1 and x.stride(-1) == 1:
+            K = x.shape[-1]
+            rows = x.numel() // K if K else 0
+            if linear_tokens_supported(rows, w.shape[0], K, x.dtype) and x.is_contiguous():
+                return linear_tokens(x.reshape(rows, K), w, b).view(*x.shape[:-1], w.shape[0])
+        return F.linear(x, w, b)
 
 
 class TitansMemory(nn.Module):

@@ -474,6 +474,21 @@ int atma_chunk_gated_delta_rule(const void* q, int64_t q_sb, int64_t q_st, int64
  */
 int atma_wait_start_flag(const int32_t* flag, int32_t epoch, int64_t timeout_us, void* stream);
 
+/*
+ * Projection of a few token rows, with no counterpart in the reference (whose nn.Linear
+ * calls the vendor GEMM, model/reference.py:22-28): y[m, n] = sum_k x[m, k] w[n, k]
+ * (+ bias[n]) for M <= 32 rows, in 16 bits with fp32 accumulation and one rounding.  It
+ * is the served model's decode projection (one token per sequence): the weights are
+ * streamed once at memory speed, where a library GEMM tile walks K serially.  x (M, K),
+ * w (N, K), y (M, N) row-major with row strides ldx, ldw, ldy (elements); bias (N,) or
+ * NULL; dtype ATMA_BF16 / ATMA_F16.  x / w rows 16-byte aligned, y rows 8-byte aligned.
+ * atma_linear_tokens_supported returns 1 for shapes the kernel serves (M <= 32,
+ * N % 16 == 0, K 1024 or 2048), 0 otherwise.  Deterministic (fixed summation order).
+ */
+int atma_linear_tokens_supported(int64_t M, int64_t N, int64_t K, int dtype);
+int atma_linear_tokens(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias, void* y,
+                       int64_t ldy, int64_t M, int64_t N, int64_t K, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -142,16 +142,25 @@ def test_generate_reports_throughput(dev):
 
 def test_tight_page_pool_runs_requests_in_turn_with_the_same_tokens(dev):
     """A pool that holds one request's lifetime pages at a time: the others wait queued,
-    then reuse the freed pages and state-table rows (zeroed on release).  Tokens equal an
-    unconstrained run's: no request sees another's conv tails or memory state."""
+    then reuse the freed pages and state-table rows (zeroed on release).  Each request's
+    tokens equal those of a fresh engine serving it alone (the same batch of one, the same
+    routes): no request sees another's KV pages, conv tails or memory state."""
     from atma_amd.engine import SamplingParams
     hf, model, _ = _model(torch.bfloat16, seed=6)
     prompts = _prompts([30, 45, 21], 7)
     sp = SamplingParams(temperature=0.0, max_tokens=6, ignore_eos=True)
-    out = []
-    for pages in (64, 4):                        # 4 pages = 64 tokens: one request's 51 at most
-        engine = _engine(hf, model, eager=False, pages=pages)
-        res = engine.generate(prompts, sp)
-        out.append([r["token_ids"] for r in res])
+    alone = []
+    for p in prompts:
+        engine = _engine(hf, model, eager=False, pages=64)
+        alone.append(engine.generate([p], sp)[0]["token_ids"])
         engine.exit()
-    assert out[0] == out[1]
+    engine = _engine(hf, model, eager=False, pages=4)   # 4 pages = 64 tokens: one request's 51 at most
+    seqs = [engine.add_request(p, sp) for p in prompts]
+    while not engine.is_finished():
+        batch, is_prefill = engine.scheduler.schedule()
+        assert len(batch) == 1                          # one request at a time
+        toks = engine.model_runner.run(batch, is_prefill)
+        for s in engine.scheduler.commit(batch, toks):
+            engine.model_runner.free_seq_slot(s)
+    engine.exit()
+    assert [s.completion_token_ids for s in seqs] == alone
