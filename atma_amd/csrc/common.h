@@ -32,6 +32,19 @@ __device__ __forceinline__ float to_f32(f16 x) { return (float)x; }
 template <typename T>
 __device__ __forceinline__ T from_f32(float x) { return (T)x; }
 
+__device__ __forceinline__ float round_bf16(float x) { return (float)(bf16)x; }
+
+// gate * relu(x)^2 in eager 16-bit order: the square rounded to bf16 for bf16 inputs
+// before the gate multiply (the output's rounding is the caller's).
+template <typename T>
+__device__ __forceinline__ float sq_relu_gate1(float x, float g) {
+#pragma clang fp contract(off)
+  const float pos = x < 0.f ? 0.f : x;  // NaN passes through, as torch's relu
+  float sq = pos * pos;
+  if constexpr (__is_same(T, bf16)) sq = round_bf16(sq);
+  return g * sq;
+}
+
 // softplus with torch's default threshold (x > 20 -> x).
 __device__ __forceinline__ float softplus(float x) {
   return x > 20.f ? x : log1pf(expf(x));

@@ -30,17 +30,7 @@
 
 namespace atma {
 
-__device__ __forceinline__ float round_bf16(float x) { return (float)(bf16)x; }
-
 // ------------------------------------------------------------------ squared_relu_gate
-template <typename T>
-__device__ __forceinline__ float sq_relu_gate1(float x, float g) {
-#pragma clang fp contract(off)
-  const float pos = x < 0.f ? 0.f : x;  // NaN passes through, as torch's relu
-  float sq = pos * pos;
-  if constexpr (std::is_same<T, bf16>::value) sq = round_bf16(sq);
-  return g * sq;
-}
 
 template <typename T, int VEC>
 __global__ void __launch_bounds__(256)

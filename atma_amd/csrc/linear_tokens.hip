@@ -8,12 +8,24 @@
 // (32 for wide outputs) and its waves split K, 256 per wave; every MFMA operand comes straight
 // from memory in the lane layout of v_mfma_f32_16x16x32 (A lane l: weight row l % 16,
 // k = 8 (l / 16) .. + 7, one 16-byte load; B lane l: token row l % 16, the same k), a wave
-// issues the loads
-// of all eight of its 32-wide K steps before its first product (one memory latency per
-// launch), weights with the non-temporal hint (read once per step) and the activation rows
-// through L2 (read by every workgroup).  The waves' partial sums are added in a fixed
-// order through LDS (deterministic), then the bias in fp32 and one rounding to the output
-// type.
+// issues the loads of all eight of its 32-wide K steps before its first product (one memory
+// latency per launch), weights with the non-temporal hint (read once per step) and the
+// activation rows through L2 (read by every workgroup).  The waves' partial sums are added
+// in a fixed order through LDS (deterministic).
+//
+// Two launch forms share the kernel:
+//  * segments: up to 8 weight matrices that read the same activations (the q / k / v /
+//    gate projections of one layer), each with its own bias and output rows; the launch's
+//    workgroups are laid over the segments' 16-feature tiles one after another, so the
+//    projections cost one launch.  Bias added in fp32, one rounding to the output type.
+//  * chunks: K split into chunks of 256-1024 across workgroups (blockIdx.y), chunk c with its
+//    own weight pointer, writing fp32 partial sums parts[c] (no bias, no rounding) for the
+//    consumer to add in chunk order (the residual RMSNorm).  That spreads a 4096-wide
+//    projection over 4x the workgroups, and lets two projections of different inputs whose
+//    outputs are summed (the global layer's output and memory projections) run as one.
+//    The activations can be formed as they load: gate * relu(a)^2 from the two halves of
+//    the MLP's first projection (squared_relu_gate's arithmetic), so the activation
+//    tensor is never written.
 //
 // No reference counterpart: the reference's nn.Linear calls the vendor GEMM
 // (model/reference.py:22-28); this is the engine's kernel for that call at decode shapes.
@@ -22,46 +34,120 @@
 
 namespace atma {
 
-struct LinTokArgs {
-  const void* x;  // (M, K), row stride ldx
-  int64_t ldx;
-  const void* w;  // (N, K), row stride ldw
-  int64_t ldw;
-  const void* bias;  // (N,) or null
-  void* y;           // (M, N), row stride ldy
-  int64_t ldy;
-  int M, N, K;
-};
-
 constexpr int kLinKPerWave = 256;  // K per wave: eight 32-wide steps, all loaded at once
 constexpr int kLinSteps = kLinKPerWave / 32;
-constexpr int kLinMaxWaves = 8;
+constexpr int kLinMaxSegs = 8;
+constexpr int kLinMaxChunks = 8;
+constexpr int kLinMaxWaves = 8;  // K per launch (segments) up to 2048, per chunk up to 1024
 
-// NW waves per workgroup (K = NW * 256); FT 16-feature tiles per workgroup, which share
-// each activation load (for wide outputs, where the activation rows would otherwise be
-// read from L2 once per 16 features)
-template <typename T, int NW, int FT>
+struct LinSeg {
+  const void* w;  // (n, K), row stride ldw
+  int64_t ldw;
+  const void* bias;  // (n,) or null
+  void* y;           // (M, n), row stride ldy
+  int64_t ldy;
+  int n;
+  int tile0;  // the segment's first tile in the launch
+};
+
+struct LinTokArgs {
+  const void* x;  // (M, *), row stride ldx
+  int64_t ldx;
+  int M;
+  // segments form
+  int n_segs;
+  LinSeg seg[kLinMaxSegs];
+  // chunks form: chunk c reads x columns [c K, c K + K) (with the gate transform: a there,
+  // gate at gate_off + c K) and weights cw[c] (N, K) with row stride cldw[c]
+  const void* cw[kLinMaxChunks];
+  int64_t cldw[kLinMaxChunks];
+  int64_t gate_off;
+  float* parts;  // (chunks, M, N) fp32
+  int N;
+};
+
+enum LinMode { kLinSegments = 0, kLinChunks = 1, kLinChunksSqReluGate = 2 };
+
+// 8 values gate * relu(a)^2, rounded to T, as one 16-byte MFMA operand
+template <typename T>
+__device__ __forceinline__ u32x4 sq_relu_gate8(const u32x4& a, const u32x4& g) {
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    o[e] = pack2<T>(sq_relu_gate1<T>(elem16<T>(a, 2 * e), elem16<T>(g, 2 * e)),
+                    sq_relu_gate1<T>(elem16<T>(a, 2 * e + 1), elem16<T>(g, 2 * e + 1)));
+  return o;
+}
+
+// NW waves per workgroup (K per launch or chunk = NW * 256, NW <= kLinMaxWaves); FT 16-feature tiles per
+// workgroup, which share each activation load
+template <typename T, int NW, int FT, int MODE>
 __global__ void __launch_bounds__(64 * NW) linear_tokens_kernel(LinTokArgs a) {
-  __shared__ f32x4 red[NW - 1][FT][2][64];
+  __shared__ f32x4 red[NW > 1 ? NW - 1 : 1][FT][2][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, g = lane >> 4;
-  const int f0 = blockIdx.x * 16 * FT;
+  const int tile = blockIdx.x;
+
+  // this workgroup's weights, feature range and activation columns (constant-index
+  // selects over the argument arrays, so they stay in scalar registers)
+  const void* wp = nullptr;
+  int64_t ldw = 0, xoff = 0;
+  int f0 = 0, n_lim = 0, seg = 0;
+  if constexpr (MODE == kLinSegments) {
+#pragma unroll
+    for (int s = 1; s < kLinMaxSegs; ++s)
+      if (s < a.n_segs && tile >= a.seg[s].tile0) seg = s;
+#pragma unroll
+    for (int s = 0; s < kLinMaxSegs; ++s)
+      if (s == seg) {
+        wp = a.seg[s].w;
+        ldw = a.seg[s].ldw;
+        n_lim = a.seg[s].n;
+        f0 = (tile - a.seg[s].tile0) * 16 * FT;
+      }
+  } else {
+    const int c = blockIdx.y;
+#pragma unroll
+    for (int s = 0; s < kLinMaxChunks; ++s)
+      if (s == c) {
+        wp = a.cw[s];
+        ldw = a.cldw[s];
+      }
+    n_lim = a.N;
+    f0 = tile * 16 * FT;
+    xoff = (int64_t)c * (NW * kLinKPerWave);
+  }
   const int k0 = wave * kLinKPerWave + 8 * g;
   const T* X = (const T*)a.x;
-  const T* W = (const T*)a.w;
+  const T* W = (const T*)wp;
   // token rows r and 16 + r (rows past M read row M - 1 and are zeroed: no divergent loads)
   const bool ok0 = r < a.M, ok1 = 16 + r < a.M;
-  const T* x0 = X + (int64_t)min(r, a.M - 1) * a.ldx + k0;
-  const T* x1 = X + (int64_t)min(16 + r, a.M - 1) * a.ldx + k0;
+  const T* x0 = X + (int64_t)min(r, a.M - 1) * a.ldx + xoff + k0;
+  const T* x1 = X + (int64_t)min(16 + r, a.M - 1) * a.ldx + xoff + k0;
 
   u32x4 wv[kLinSteps][FT], xv0[kLinSteps], xv1[kLinSteps];
 #pragma unroll
   for (int u = 0; u < kLinSteps; ++u) {
 #pragma unroll
-    for (int f = 0; f < FT; ++f)
-      wv[u][f] = __builtin_nontemporal_load((const u32x4*)(W + (int64_t)(f0 + 16 * f + r) * a.ldw + k0 + 32 * u));
+    for (int f = 0; f < FT; ++f) {
+      const int row = min(f0 + 16 * f + r, n_lim - 1);  // rows past the segment: discarded
+      wv[u][f] = __builtin_nontemporal_load((const u32x4*)(W + (int64_t)row * ldw + k0 + 32 * u));
+    }
     xv0[u] = *(const u32x4*)(x0 + 32 * u);
     xv1[u] = *(const u32x4*)(x1 + 32 * u);
+  }
+  if constexpr (MODE == kLinChunksSqReluGate) {
+    u32x4 gv0[kLinSteps], gv1[kLinSteps];
+#pragma unroll
+    for (int u = 0; u < kLinSteps; ++u) {
+      gv0[u] = *(const u32x4*)(x0 + a.gate_off + 32 * u);
+      gv1[u] = *(const u32x4*)(x1 + a.gate_off + 32 * u);
+    }
+#pragma unroll
+    for (int u = 0; u < kLinSteps; ++u) {
+      xv0[u] = sq_relu_gate8<T>(xv0[u], gv0[u]);
+      xv1[u] = sq_relu_gate8<T>(xv1[u], gv1[u]);
+    }
   }
   const u32x4 zero = {0u, 0u, 0u, 0u};
   f32x4 acc[FT][2];
@@ -77,60 +163,149 @@ __global__ void __launch_bounds__(64 * NW) linear_tokens_kernel(LinTokArgs a) {
     }
   }
 
-  if (wave > 0) {
+  if constexpr (NW > 1) {
+    if (wave > 0) {
 #pragma unroll
-    for (int f = 0; f < FT; ++f) {
-      red[wave - 1][f][0][lane] = acc[f][0];
-      red[wave - 1][f][1][lane] = acc[f][1];
+      for (int f = 0; f < FT; ++f) {
+        red[wave - 1][f][0][lane] = acc[f][0];
+        red[wave - 1][f][1][lane] = acc[f][1];
+      }
     }
+    __syncthreads();
+    if (wave > 0) return;
   }
-  __syncthreads();
-  if (wave > 0) return;
   // lane l holds features 4 (l / 16) + [0, 4) of tile f, token 16 t + l % 16
-  T* Y = (T*)a.y;
 #pragma unroll
   for (int f = 0; f < FT; ++f) {
-    const int n = f0 + 16 * f + 4 * g;
+    const int n = f0 + 16 * f + 4 * g;  // n_lim % 4 == 0: a lane's four features are all in or all out
+    if (n >= n_lim) continue;
     f32x4 bv = {0.f, 0.f, 0.f, 0.f};
-    if (a.bias) {
-      const T* bp = (const T*)a.bias + n;
-      bv = f32x4{to_f32(bp[0]), to_f32(bp[1]), to_f32(bp[2]), to_f32(bp[3])};
+    T* Y = nullptr;
+    int64_t ldy = 0;
+    if constexpr (MODE == kLinSegments) {
+#pragma unroll
+      for (int s = 0; s < kLinMaxSegs; ++s)
+        if (s == seg) {
+          Y = (T*)a.seg[s].y;
+          ldy = a.seg[s].ldy;
+          if (a.seg[s].bias) {
+            const T* bp = (const T*)a.seg[s].bias + n;
+            bv = f32x4{to_f32(bp[0]), to_f32(bp[1]), to_f32(bp[2]), to_f32(bp[3])};
+          }
+        }
     }
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       f32x4 v = acc[f][t];
 #pragma unroll
       for (int w = 0; w < NW - 1; ++w) v += red[w][f][t][lane];
-      v += bv;
       const int m = 16 * t + r;
-      if (m < a.M) {
+      if (m >= a.M) continue;
+      if constexpr (MODE == kLinSegments) {
+        v += bv;
         const u32x2 pk = {pack2<T>(v[0], v[1]), pack2<T>(v[2], v[3])};
-        *(u32x2*)(Y + (int64_t)m * a.ldy + n) = pk;
+        *(u32x2*)(Y + (int64_t)m * ldy + n) = pk;
+      } else {
+        *(f32x4*)(a.parts + ((int64_t)blockIdx.y * a.M + m) * a.N + n) = v;
       }
     }
   }
 }
 
+template <typename T, int NW>
+static void launch_segments(const LinTokArgs& a, int tiles, bool wide, hipStream_t s) {
+  const dim3 grid((unsigned)tiles);
+  if (wide) linear_tokens_kernel<T, NW, 2, kLinSegments><<<grid, dim3(64 * NW), 0, s>>>(a);
+  else linear_tokens_kernel<T, NW, 1, kLinSegments><<<grid, dim3(64 * NW), 0, s>>>(a);
+}
+
+template <typename T, int NW>
+static void launch_chunks(const LinTokArgs& a, int chunks, bool sq_relu_gate, hipStream_t s) {
+  const dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)chunks);
+  if (sq_relu_gate) linear_tokens_kernel<T, NW, 1, kLinChunksSqReluGate><<<grid, dim3(64 * NW), 0, s>>>(a);
+  else linear_tokens_kernel<T, NW, 1, kLinChunks><<<grid, dim3(64 * NW), 0, s>>>(a);
+}
+
 template <typename T>
-static void launch_linear_tokens(const LinTokArgs& a, hipStream_t s) {
-  const bool wide = a.N >= 4096 && a.N % 32 == 0;
-  const dim3 grid((unsigned)(a.N / (wide ? 32 : 16)));
-  if (a.K == 1024) {
-    if (wide) linear_tokens_kernel<T, 4, 2><<<grid, dim3(256), 0, s>>>(a);
-    else linear_tokens_kernel<T, 4, 1><<<grid, dim3(256), 0, s>>>(a);
-  } else {
-    if (wide) linear_tokens_kernel<T, 8, 2><<<grid, dim3(512), 0, s>>>(a);
-    else linear_tokens_kernel<T, 8, 1><<<grid, dim3(512), 0, s>>>(a);
+static void launch_segments_k(const LinTokArgs& a, int64_t K, int tiles, bool wide, hipStream_t s) {
+  switch (K) {
+    case 256: launch_segments<T, 1>(a, tiles, wide, s); break;
+    case 512: launch_segments<T, 2>(a, tiles, wide, s); break;
+    case 1024: launch_segments<T, 4>(a, tiles, wide, s); break;
+    default: launch_segments<T, 8>(a, tiles, wide, s); break;
   }
+}
+
+template <typename T>
+static void launch_chunks_k(const LinTokArgs& a, int64_t chunk_k, int chunks, bool sq, hipStream_t s) {
+  switch (chunk_k) {
+    case 256: launch_chunks<T, 1>(a, chunks, sq, s); break;
+    case 512: launch_chunks<T, 2>(a, chunks, sq, s); break;
+    default: launch_chunks<T, 4>(a, chunks, sq, s); break;
+  }
+}
+
+static bool lin_common_ok(int64_t M, int dtype) {
+  return (dtype == ATMA_BF16 || dtype == ATMA_F16) && M >= 1 && M <= 32;
+}
+static bool lin_k_ok(int64_t K, int max_waves) {
+  return K == 256 || K == 512 || K == 1024 || (max_waves >= 8 && K == 2048);
 }
 
 }  // namespace atma
 
 extern "C" int atma_linear_tokens_supported(int64_t M, int64_t N, int64_t K, int dtype) {
-  return (dtype == ATMA_BF16 || dtype == ATMA_F16) && M >= 1 && M <= 32 && N >= 16 && N % 16 == 0 &&
-                 (K == 1024 || K == 2048) && N <= (1 << 24)
+  return atma::lin_common_ok(M, dtype) && N >= 16 && N % 16 == 0 && atma::lin_k_ok(K, 8) && N <= (1 << 24)
              ? 1
              : 0;
+}
+
+extern "C" int atma_linear_tokens_multi(const void* x, int64_t ldx, int64_t M, int64_t K, int64_t n_segs,
+                                        const void* const* w, const int64_t* ldw, const void* const* bias,
+                                        void* const* y, const int64_t* ldy, const int64_t* n, int dtype,
+                                        void* stream) {
+  using namespace atma;
+  if (!lin_common_ok(M, dtype) || !lin_k_ok(K, kLinMaxWaves))
+    return set_error(ATMA_ERR_UNSUPPORTED,
+                     "linear_tokens: unsupported shape M=%lld K=%lld dtype=%d (16-bit, 1 <= M <= 32, K 256, 512, "
+                     "1024 or 2048)",
+                     (long long)M, (long long)K, dtype);
+  if (n_segs < 1 || n_segs > kLinMaxSegs)
+    return set_error(ATMA_ERR_INVALID, "linear_tokens: 1 to %d weight segments, got %lld", kLinMaxSegs,
+                     (long long)n_segs);
+  if (!x || !w || !ldw || !bias || !y || !ldy || !n) return set_error(ATMA_ERR_INVALID, "linear_tokens: null pointer");
+  if ((uintptr_t)x % 16 || ldx % 8 || ldx < K)
+    return set_error(ATMA_ERR_INVALID, "linear_tokens: x rows must be 16-byte aligned and at least K long");
+  LinTokArgs a{};
+  a.x = x;
+  a.ldx = ldx;
+  a.M = (int)M;
+  a.n_segs = (int)n_segs;
+  bool wide = true;
+  int64_t total = 0;
+  for (int s = 0; s < n_segs; ++s) {
+    if (!w[s] || !y[s]) return set_error(ATMA_ERR_INVALID, "linear_tokens: null pointer in segment %d", s);
+    if (n[s] < 4 || n[s] % 4 || n[s] > (1 << 24))
+      return set_error(ATMA_ERR_INVALID, "linear_tokens: segment %d has %lld features (a multiple of 4 needed)", s,
+                       (long long)n[s]);
+    if ((uintptr_t)w[s] % 16 || ldw[s] % 8 || ldw[s] < K || (uintptr_t)y[s] % 8 || ldy[s] % 4 || ldy[s] < n[s] ||
+        (bias[s] && (uintptr_t)bias[s] % 2))
+      return set_error(ATMA_ERR_INVALID,
+                       "linear_tokens: segment %d: weight rows must be 16-byte aligned, output rows 8-byte aligned", s);
+    wide = wide && n[s] % 32 == 0;
+    total += n[s];
+  }
+  wide = wide && total >= 4096;
+  int tiles = 0;
+  for (int s = 0; s < n_segs; ++s) {
+    const int per = wide ? 32 : 16;
+    a.seg[s] = LinSeg{w[s], ldw[s], bias[s], y[s], ldy[s], (int)n[s], tiles};
+    tiles += (int)((n[s] + per - 1) / per);
+  }
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == ATMA_BF16) launch_segments_k<bf16>(a, K, tiles, wide, st);
+  else launch_segments_k<f16>(a, K, tiles, wide, st);
+  return check_launch("linear_tokens");
 }
 
 extern "C" int atma_linear_tokens(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias,
@@ -140,16 +315,44 @@ extern "C" int atma_linear_tokens(const void* x, int64_t ldx, const void* w, int
   if (!atma_linear_tokens_supported(M, N, K, dtype))
     return set_error(ATMA_ERR_UNSUPPORTED,
                      "linear_tokens: unsupported shape M=%lld N=%lld K=%lld dtype=%d (16-bit, M <= 32, "
-                     "N %% 16 == 0, K 1024 or 2048)",
+                     "N %% 16 == 0, K 256, 512, 1024 or 2048)",
                      (long long)M, (long long)N, (long long)K, dtype);
   if (!x || !w || !y) return set_error(ATMA_ERR_INVALID, "linear_tokens: null pointer");
-  if (ldx < K || ldw < K || ldy < N) return set_error(ATMA_ERR_INVALID, "linear_tokens: row stride below row length");
-  if ((uintptr_t)x % 16 || (uintptr_t)w % 16 || (uintptr_t)y % 8 || ldx % 8 || ldw % 8 || ldy % 4 ||
-      (bias && (uintptr_t)bias % 2))
-    return set_error(ATMA_ERR_INVALID, "linear_tokens: x / w rows must be 16-byte aligned, y rows 8-byte aligned");
-  LinTokArgs a{x, ldx, w, ldw, bias, y, ldy, (int)M, (int)N, (int)K};
-  hipStream_t s = (hipStream_t)stream;
-  if (dtype == ATMA_BF16) launch_linear_tokens<bf16>(a, s);
-  else launch_linear_tokens<f16>(a, s);
-  return check_launch("linear_tokens");
+  if (ldy < N) return set_error(ATMA_ERR_INVALID, "linear_tokens: row stride below row length");
+  return atma_linear_tokens_multi(x, ldx, M, K, 1, &w, &ldw, &bias, &y, &ldy, &N, dtype, stream);
+}
+
+extern "C" int atma_linear_tokens_chunks(const void* x, int64_t ldx, int64_t M, int64_t chunk_k, int64_t n_chunks,
+                                         const void* const* w, const int64_t* ldw, int64_t N,
+                                         int64_t gate_off, float* parts, int dtype, void* stream) {
+  using namespace atma;
+  if (!lin_common_ok(M, dtype) || !lin_k_ok(chunk_k, 4) || n_chunks < 1 || n_chunks > kLinMaxChunks || N < 4 ||
+      N % 4 || N > (1 << 24))
+    return set_error(ATMA_ERR_UNSUPPORTED,
+                     "linear_tokens_chunks: unsupported shape M=%lld chunk_k=%lld chunks=%lld N=%lld dtype=%d "
+                     "(16-bit, 1 <= M <= 32, 1 to %d chunks of K 256, 512 or 1024, N %% 4 == 0)",
+                     (long long)M, (long long)chunk_k, (long long)n_chunks, (long long)N, dtype, kLinMaxChunks);
+  if (!x || !w || !ldw || !parts) return set_error(ATMA_ERR_INVALID, "linear_tokens_chunks: null pointer");
+  const int64_t width = n_chunks * chunk_k + gate_off;
+  if ((uintptr_t)x % 16 || ldx % 8 || ldx < width || gate_off < 0 || gate_off % 8 || (uintptr_t)parts % 16)
+    return set_error(ATMA_ERR_INVALID,
+                     "linear_tokens_chunks: x rows must be 16-byte aligned and hold every chunk (and gate); "
+                     "parts 16-byte aligned");
+  LinTokArgs a{};
+  a.x = x;
+  a.ldx = ldx;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.gate_off = gate_off;
+  a.parts = parts;
+  for (int c = 0; c < n_chunks; ++c) {
+    if (!w[c] || (uintptr_t)w[c] % 16 || ldw[c] % 8 || ldw[c] < chunk_k)
+      return set_error(ATMA_ERR_INVALID, "linear_tokens_chunks: chunk %d weight rows must be 16-byte aligned", c);
+    a.cw[c] = w[c];
+    a.cldw[c] = ldw[c];
+  }
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == ATMA_BF16) launch_chunks_k<bf16>(a, chunk_k, (int)n_chunks, gate_off > 0, st);
+  else launch_chunks_k<f16>(a, chunk_k, (int)n_chunks, gate_off > 0, st);
+  return check_launch("linear_tokens_chunks");
 }

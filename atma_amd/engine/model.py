@@ -21,8 +21,9 @@ import torch.nn.functional as F
 from torch import nn
 
 from ..kernel import causal_conv1d_decode_step, packed_causal_conv1d, softcap_logits
+from ..kernel.decode_fusions import lfm2_conv_step, residual_rms_norm_supported
 from ..layers.attention import Attention
-from ..layers.global_attention import MLP, GlobalLayerCache, Linear, PolarAttention, RMSNorm
+from ..layers.global_attention import MLP, GlobalLayerCache, Linear, PolarAttention, RMSNorm, decode_rows
 from .config import AtmaConfig
 from .context import get_context
 
@@ -45,12 +46,15 @@ class AtmaAttention(PolarAttention):
         return GlobalLayerCache(k_cache=self.attn.k_cache, v_cache=self.attn.v_cache, conv_q=t[f"attn_{i}_q"],
                                 conv_k=t[f"attn_{i}_k"], conv_v=t[f"attn_{i}_v"], mem_table=t.get(f"mem_{i}"))
 
-    def forward(self, x):
-        """x: (tokens, dim) -- the packed prefill tokens or one token per decoding sequence."""
+    def forward(self, x, defer=False):
+        """x: (tokens, dim) -- the packed prefill tokens or one token per decoding sequence.
+        ``defer``: a fused decode step may return its output projections unsummed
+        (``PartialSums``, finished by the next residual norm)."""
         ctx = get_context()
         cache = self._cache(ctx)
         if not ctx.is_prefill:
-            return self.decode(x, cache, ctx.seq_slots, ctx.block_tables, ctx.context_lens, ctx.slot_mapping)
+            return self.decode(x, cache, ctx.seq_slots, ctx.block_tables, ctx.context_lens, ctx.slot_mapping,
+                               defer=defer)
         if ctx.dense_prefill:
             B, T = ctx.dense_batch_size, ctx.dense_seq_len
             return self.prefill(x.view(B, T, -1), cache, ctx.seq_slots, ctx.slot_mapping).reshape(B * T, -1)
@@ -85,8 +89,12 @@ class AtmaLFM2Conv(nn.Module):
         self.out_proj = Linear(dim, dim)
         self.layer_idx = layer_idx
 
-    def forward(self, x):
+    def forward(self, x, defer=False):
         ctx = get_context()
+        if not ctx.is_prefill and decode_rows(x):
+            # one launch for b * x, the conv step and c * (.) (lfm2_conv_step)
+            table = ctx.conv_state_tables[f"conv_{self.layer_idx}_gated"]
+            return self.out_proj(lfm2_conv_step(self.in_proj(x), self.conv.weight.squeeze(1), ctx.seq_slots, table))
         b_gate, c_gate, x_proj = self.in_proj(x).chunk(3, dim=-1)
         xg = b_gate * x_proj
         w = self.conv.weight.squeeze(1)
@@ -140,6 +148,16 @@ class AtmaDecoderBlock(nn.Module):
         x = x + self.attn(self.norm1(x))
         return x + self.mlp(self.norm2(x))
 
+    def forward_stream(self, branch, residual):
+        """The same block over the residual stream: the previous block's branch output
+        and the stream before it go in, each add is fused with the norm after it
+        (``RMSNorm.add_norm``), and this block's MLP output comes out unadded -- the
+        additions are the eager block's, in the same dtype, so the stream's values are
+        unchanged.  Returns (mlp branch, stream)."""
+        h, residual = self.norm1.add_norm(branch, residual)
+        h, residual = self.norm2.add_norm(self.attn(h, defer=True), residual)
+        return self.mlp(h, defer=True), residual
+
 
 class Atma(nn.Module):
     """The served model (``Atma``, ``inference/models/atma.py:716-754``)."""
@@ -153,11 +171,18 @@ class Atma(nn.Module):
         self.proj = Linear(config.hidden_size, config.vocab_size)     # LM head, with bias
 
     def forward(self, input_ids, positions=None):
-        """Hidden states of every scheduled token (no positions: the model has none)."""
+        """Hidden states of every scheduled token (no positions: the model has none).
+        16-bit inference runs the blocks over the residual stream (``forward_stream``:
+        every residual add fused with the norm that follows it)."""
         x = self.embed(input_ids)
+        if torch.is_grad_enabled() or not residual_rms_norm_supported(x):
+            for block in self.blocks:
+                x = block(x)
+            return self.norm(x)
+        branch, residual = x, None
         for block in self.blocks:
-            x = block(x)
-        return self.norm(x)
+            branch, residual = block.forward_stream(branch, residual)
+        return self.norm.add_norm(branch, residual)[0]
 
     def compute_logits(self, hidden):
         """LM head + soft cap ``15 x / sqrt(x^2 + 225)`` (HIP ``softcap_logits``); at prefill

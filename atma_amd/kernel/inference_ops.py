@@ -62,11 +62,11 @@ def packed_causal_conv1d(x, weight, state_table, token_seq_starts, token_seq_end
 
 def linear_tokens_supported(rows, out_features, in_features, dtype):
     """True for the shapes ``linear_tokens`` serves: 16-bit, at most 32 rows, out_features a
-    multiple of 16 and in_features 1024 or 2048 (the C ABI's ``atma_linear_tokens_supported``;
-    wider inputs read the activation rows from L2 once per output tile more than they read
-    weights, and the vendor GEMM serves them better)."""
+    multiple of 16 and in_features 256, 512, 1024 or 2048 (the C ABI's
+    ``atma_linear_tokens_supported``: one wave per 256 inputs, at most eight per workgroup;
+    a wider input is split across workgroups by ``linear_tokens_chunks`` instead)."""
     return (dtype in (torch.bfloat16, torch.float16) and 1 <= rows <= 32 and out_features >= 16
-            and out_features % 16 == 0 and in_features in (1024, 2048))
+            and out_features % 16 == 0 and in_features in (256, 512, 1024, 2048))
 
 
 @torch.no_grad()

@@ -139,8 +139,14 @@ def global_decode_step_supported(q, k_cache, block_tables):
     """True when ``global_decode_step`` runs fused for these shapes: 16-bit caches whose
     pages hold whole 32-key units, head_dim 64 / 128, GQA groups of at most 16."""
     B, Hq, d = q.shape
-    return bool(_lib.load().atma_global_decode_step_supported(
-        B, Hq, k_cache.shape[2], block_tables.shape[1], k_cache.shape[1], d, _lib.dtype_code(q.dtype)))
+    return global_decode_step_supported_shape(B, Hq, k_cache.shape[2], block_tables.shape[1], k_cache.shape[1], d,
+                                              q.dtype)
+
+
+def global_decode_step_supported_shape(B, Hq, Hkv, max_pages, page_size, d, dtype):
+    """``global_decode_step_supported`` from the sizes alone."""
+    return bool(_lib.load().atma_global_decode_step_supported(B, Hq, Hkv, max_pages, page_size, d,
+                                                              _lib.dtype_code(dtype)))
 
 
 def global_decode_step(q, k_new, v_new, k_cache, v_cache, slot_mapping, block_tables, context_lens,

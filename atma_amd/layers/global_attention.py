@@ -41,9 +41,25 @@ from ..kernel import (StartSignal, causal_conv1d_decode_step, chunk_gated_delta_
                       gated_delta_decode_step, gated_delta_gates, global_decode_step, polar_attention,
                       polar_attention_decode, polar_attention_fwd, polar_attention_packed_fwd,
                       recurrence_pays_to_overlap)
+from ..kernel.decode_fusions import (PartialSums, chunk_width, global_decode_gate, global_decode_prep,
+                                     linear_tokens_chunks, linear_tokens_multi, linear_tokens_multi_supported,
+                                     residual_rms_norm, residual_rms_norm_supported)
 from ..kernel.inference_ops import (linear_tokens, linear_tokens_supported, packed_causal_conv1d,
                                      squared_relu_gate)
+from ..kernel.polar import global_decode_step_supported_shape
 from .attention import store_kvcache
+
+# torch's rms_norm without eps uses its compute type's epsilon: fp32's for 16-bit and fp32 rows
+F32_EPS = torch.finfo(torch.float32).eps
+
+
+def decode_rows(x):
+    """True for the decode step's activations: a few token rows (<= 32, one per
+    sequence) in 16 bits on the GPU, outside autograd -- the shapes the decode fusions
+    (linear_tokens and kernel/decode_fusions) serve."""
+    return (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and x.dim() == 2 and x.shape[0] <= 32
+            and x.is_contiguous() and not torch.is_grad_enabled())
+
 
 # Polar structural priors (model/reference.py:17-20)
 LEN_GAIN_INIT = -1.0
@@ -194,6 +210,17 @@ class PolarAttention(nn.Module):
     def polar_params(self):
         return dict(v_null=self.v_null, null_base=self.null_base, null_slope_raw=self.null_slope_raw,
                     len_gain_raw=self.len_gain_raw, mag_beta_raw=self.mag_beta_raw)
+
+    def polar_params_f32(self):
+        """``polar_params`` as the fp32 tensors the kernels read, converted once and kept
+        until a parameter changes (its version counter or storage), so that a decode step
+        -- and a graph captured from one -- does not convert them per call."""
+        ps = self.polar_params()
+        key = tuple((p.data_ptr(), p._version, p.dtype) for p in ps.values())
+        if getattr(self, "_pf32_key", None) != key:
+            self._pf32 = {n: p.detach().to(torch.float32).contiguous() for n, p in ps.items()}
+            self._pf32_key = key
+        return self._pf32
 
     def _project(self, x):
         """q/gate, k, v projections and per-head RMSNorm of q, k (``model/reference.py:131-139``).
@@ -434,11 +461,57 @@ class PolarAttention(nn.Module):
             out = out + r
         return out
 
-    def decode(self, x, cache: GlobalLayerCache, slots, block_tables, context_lens, slot_mapping):
+    def _decode_fusable(self, x, cache, block_tables):
+        H, Hkv, dk = self.num_heads, self.num_kv_heads, self.head_dim
+        m = self.mem
+        if m is None or not decode_rows(x) or dk not in (64, 128) or self.kernel_size > 16 \
+                or H * dk not in (256, 512, 1024):
+            return False
+        outs = [2 * H * dk, Hkv * dk, Hkv * dk, H * dk, H, H]
+        if not linear_tokens_multi_supported(x.shape[0], x.shape[1], outs, x.dtype):
+            return False
+        kc = cache.k_cache
+        return bool(kc.dtype == x.dtype and cache.conv_q.dtype == x.dtype and global_decode_step_supported_shape(
+            x.shape[0], H, kc.shape[2], block_tables.shape[1], kc.shape[1], dk, x.dtype))
+
+    def _decode_fused(self, x, cache, slots, block_tables, context_lens, slot_mapping):
+        """The decode step in seven launches: one projection launch for q|gate, k, v, the
+        memory gate and gate logits (``linear_tokens_multi``), the norms / Canon convs /
+        gates (``global_decode_prep``), the attention + KV write + memory step
+        (``global_decode_step``, two), the gated projection inputs
+        (``global_decode_gate``), and both output projections as fp32 partial sums
+        (``linear_tokens_chunks``), returned with their biases and ``mu_proj(mag)`` as a
+        ``PartialSums`` for the residual norm to add."""
+        H, Hkv, dk = self.num_heads, self.num_kv_heads, self.head_dim
+        m = self.mem
+        hd, kvd = H * dk, Hkv * dk
+        lin = (self.q, self.k, self.v, m.gate, m.w_gamma, m.w_beta)
+        y = linear_tokens_multi(x, [l.weight for l in lin], [l.bias for l in lin])
+        ck, cv = 2 * hd, 2 * hd + kvd
+        cm = cv + kvd
+        cg = cm + hd
+        taps = tuple(c.weight.squeeze(1) for c in (self.canon_q, self.canon_k, self.canon_v))
+        q, k, v, gamma, beta = global_decode_prep(y, H, Hkv, dk, (ck, cv, cg, cg + H), taps,
+                                                  (cache.conv_q, cache.conv_k, cache.conv_v), slots, F32_EPS,
+                                                  gate_bias=(m.gamma_bias, m.beta_bias))
+        c, mag, r = global_decode_step(q, k, v, cache.k_cache, cache.v_cache, slot_mapping, block_tables,
+                                       context_lens, gamma, beta, cache.mem_table, slots, window=self.window,
+                                       **self.polar_params_f32())
+        x2 = global_decode_gate(c, r, y, cm, F32_EPS)
+        parts = linear_tokens_chunks(x2, [self.proj.weight, m.proj.weight], hd)
+        return PartialSums(parts, [self.proj.bias, m.proj.bias, self.mu_proj.bias], mu_x=mag,
+                           mu_w=self.mu_proj.weight, dtype=x.dtype)
+
+    def decode(self, x, cache: GlobalLayerCache, slots, block_tables, context_lens, slot_mapping, defer=False):
         """One token per sequence (``inference/models/atma.py:546-618``).
 
         x: (B, dim); slots: (B,) int64 table rows; block_tables: (B, max_pages) int32;
-        context_lens: (B,) int32 including this token; slot_mapping: (B,) int32."""
+        context_lens: (B,) int32 including this token; slot_mapping: (B,) int32.
+        16-bit decode rows with the memory branch run fused (``_decode_fused``); ``defer``
+        then returns its ``PartialSums`` unsummed."""
+        if self._decode_fusable(x, cache, block_tables):
+            out = self._decode_fused(x, cache, slots, block_tables, context_lens, slot_mapping)
+            return out if defer else out.materialize()
         H, Hkv, dk = self.num_heads, self.num_kv_heads, self.head_dim
         Bn = x.shape[0]
         q, gate, k, v = self._project(x)
@@ -452,11 +525,11 @@ class PolarAttention(nn.Module):
             gamma, beta = self.mem.decode_gates(x)
             c, mag, r = global_decode_step(q, k, v, cache.k_cache, cache.v_cache, slot_mapping,
                                            block_tables, context_lens, gamma, beta, cache.mem_table,
-                                           slots, window=self.window, **self.polar_params())
+                                           slots, window=self.window, **self.polar_params_f32())
             return self._combine(c, mag, gate) + self.mem._out(x, r)
         store_kvcache(k, v, cache.k_cache, cache.v_cache, slot_mapping)
         c, mag = polar_attention_decode(q, cache.k_cache, cache.v_cache, block_tables, context_lens,
-                                        window=self.window, **self.polar_params())
+                                        window=self.window, **self.polar_params_f32())
         return self._combine(c, mag, gate)
 
 
@@ -471,6 +544,19 @@ class RMSNorm(nn.Module):
     def forward(self, x):
         return F.rms_norm(x, (x.size(-1),), weight=self.weight.type_as(x), eps=self.eps)
 
+    def add_norm(self, branch, residual):
+        """The pre-norm block's residual step: ``s = residual + branch`` (``residual`` None:
+        the branch starts the stream), returns ``(self(s), s)``.  On 16-bit GPU rows outside
+        autograd one HIP launch (``residual_rms_norm``), which also takes a branch still in
+        fp32 partial sums (``PartialSums``); otherwise the eager add and norm."""
+        w = self.weight.to(branch.dtype)
+        if not torch.is_grad_enabled() and residual_rms_norm_supported(w):
+            return residual_rms_norm(branch, residual, w, self.eps)
+        if isinstance(branch, PartialSums):
+            branch = branch.materialize()
+        s = branch if residual is None else residual + branch
+        return self(s), s
+
 
 class MLP(nn.Module):
     """Squared-ReLU gated MLP (``model/layers.py:19-31``)."""
@@ -480,7 +566,20 @@ class MLP(nn.Module):
         self.fc = Linear(dim, 8 * dim)
         self.proj = Linear(4 * dim, dim)
 
-    def forward(self, x):
+    def forward(self, x, defer=False):
+        """``defer`` (decode rows only): return the down projection as fp32 partial sums
+        (``PartialSums``) for the next ``RMSNorm.add_norm`` to finish -- the activation is
+        formed inside the projection's loads (``linear_tokens_chunks``), and the 4x-wide
+        projection spreads over 4x the workgroups."""
+        if defer and decode_rows(x):
+            dim, hidden = self.proj.weight.shape
+            ck = chunk_width(hidden)
+            if ck is not None and linear_tokens_supported(x.shape[0], self.fc.weight.shape[0], x.shape[1], x.dtype):
+                y = linear_tokens(x, self.fc.weight, self.fc.bias)
+                w = self.proj.weight
+                parts = linear_tokens_chunks(y, [w[:, c * ck:(c + 1) * ck] for c in range(hidden // ck)], ck,
+                                             sq_relu_gate=True)
+                return PartialSums(parts, [self.proj.bias], dtype=x.dtype)
         a, gate = torch.chunk(self.fc(x), 2, dim=-1)
         if x.is_cuda and not torch.is_grad_enabled():
             # InferenceMLP (inference/models/atma.py:87-96): the fused HIP activation,

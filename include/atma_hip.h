@@ -483,11 +483,89 @@ int atma_wait_start_flag(const int32_t* flag, int32_t epoch, int64_t timeout_us,
  * w (N, K), y (M, N) row-major with row strides ldx, ldw, ldy (elements); bias (N,) or
  * NULL; dtype ATMA_BF16 / ATMA_F16.  x / w rows 16-byte aligned, y rows 8-byte aligned.
  * atma_linear_tokens_supported returns 1 for shapes the kernel serves (M <= 32,
- * N % 16 == 0, K 1024 or 2048), 0 otherwise.  Deterministic (fixed summation order).
+ * N % 16 == 0, K 256, 512, 1024 or 2048), 0 otherwise.  Deterministic (fixed summation
+ * order).
  */
 int atma_linear_tokens_supported(int64_t M, int64_t N, int64_t K, int dtype);
 int atma_linear_tokens(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias, void* y,
                        int64_t ldy, int64_t M, int64_t N, int64_t K, int dtype, void* stream);
+
+/*
+ * The same projection for up to 8 weight matrices that read one x (no reference
+ * counterpart; the decode step's q / k / v / gate projections of a layer in one launch):
+ * for s < n_segs, y[s][m, n] = sum_k x[m, k] w[s][n, k] (+ bias[s][n]), n < n[s].
+ * Host arrays w, ldw, bias (entries may be NULL), y, ldy, n of n_segs entries; n[s] % 4
+ * == 0; K 256, 512, 1024 or 2048; alignment as atma_linear_tokens.
+ */
+int atma_linear_tokens_multi(const void* x, int64_t ldx, int64_t M, int64_t K, int64_t n_segs,
+                             const void* const* w, const int64_t* ldw, const void* const* bias, void* const* y,
+                             const int64_t* ldy, const int64_t* n, int dtype, void* stream);
+
+/*
+ * K split across workgroups, fp32 partial sums out (no reference counterpart; the decode
+ * step's 4096-wide MLP projection and the global layer's two output projections):
+ * parts[c][m][n] = sum_{k < chunk_k} X_c[m, k] w[c][n, k] for c < n_chunks (<= 8), where
+ * X_c[m, k] = x[m, c chunk_k + k] when gate_off == 0, and with gate_off > 0
+ * X_c[m, k] = gate * relu(a)^2 of a = x[m, c chunk_k + k], gate = x[m, gate_off +
+ * c chunk_k + k] (squared_relu_gate's arithmetic, rounded to 16 bits).  chunk_k 256, 512
+ * or 1024; parts (n_chunks, M, N) fp32 contiguous, 16-byte aligned; N % 4 == 0; no bias.
+ */
+int atma_linear_tokens_chunks(const void* x, int64_t ldx, int64_t M, int64_t chunk_k, int64_t n_chunks,
+                              const void* const* w, const int64_t* ldw, int64_t N, int64_t gate_off, float* parts,
+                              int dtype, void* stream);
+
+/*
+ * Residual add + RMSNorm of the pre-norm block (inference/models/atma.py:680-713, norm
+ * model/layers.py:6-16), no reference counterpart as one call: per row m,
+ *   br  = y[m]  or  round(sum_p parts[p][m] + sum_i bias[i] + mu_x[m] . mu_w^T)
+ *   s   = res ? round(res[m] + br) : br        (written to res_out when non-NULL)
+ *   out = round(s * rsqrt(mean(s^2) + eps) * weight)
+ * Exactly one of y / parts; parts (n_parts, M, D) fp32; up to 3 biases (D,); mu_x (M,
+ * mu_k) and mu_w (D, mu_k), mu_k <= 16 (the global layer's mu_proj(mag)); 16-bit rows,
+ * D % 8 == 0, D <= 4096, every row 16-byte aligned.
+ */
+int atma_residual_rms_norm(const void* y, int64_t ldy, const float* parts, int64_t n_parts, const void* const* bias,
+                           int64_t n_bias, const void* mu_x, int64_t ldmu, const void* mu_w, int64_t mu_k,
+                           const void* res, int64_t ldr, void* res_out, int64_t ldro, const void* weight, void* out,
+                           int64_t ldo, int64_t M, int64_t D, float eps, int dtype, void* stream);
+
+/*
+ * The LFM2 block's decode mixer (model/reference.py:31-48, inference/models/atma.py:
+ * 625-673) as one call: with b, c, x the three D-wide thirds of each bcx row (in_proj's
+ * output), out = c * conv(b * x), the depthwise conv of K taps (weight (D, K)) over the
+ * sequence's last K - 1 values of b * x held in state (S, D, K - 1) row slots[b], which
+ * is advanced in place.  Eager roundings: b * x, the conv, c * conv.  A slot outside
+ * [0, max_seqs) yields NaN outputs and leaves the table untouched.
+ */
+int atma_lfm2_conv_step(const void* bcx, int64_t ld, const void* weight, int64_t K, const int64_t* slots,
+                        void* state, int64_t s_ss, int64_t max_seqs, void* out, int64_t ldo, int64_t B, int64_t D,
+                        int dtype, void* stream);
+
+/*
+ * The global layer's decode inputs from one fused projection row y[b] (q and its output
+ * gate interleaved per head from column 0, k at ck, v at cv, gate logits at cg / cb;
+ * inference/models/atma.py:546-575 and model/blocks.py:426-490), no reference
+ * counterpart as one call: q, k = per-head rms_norm (eps), then q, k, v = x + conv(x),
+ * the Canon depthwise convs (taps wq / wk / wv (C, Kc)) over state tables tq / tk / tv
+ * (S, C, Kc - 1) row slots[b], advanced in place; gamma = exp(logsigmoid(z_g + g_bias)),
+ * beta = sigmoid(z_b + b_bias) fp32 (B, H) unless gamma and beta are NULL.  q (B, H, d),
+ * k, v (B, Hkv, d) contiguous; d 64 or 128; 16-bit.
+ */
+int atma_global_decode_prep(const void* y, int64_t ldy, int64_t ck, int64_t cv, int64_t cg, int64_t cb,
+                            const void* wq, const void* wk, const void* wv, int64_t Kc, void* tq, int64_t tq_ss,
+                            void* tk, int64_t tk_ss, void* tv, int64_t tv_ss, int64_t max_seqs, const int64_t* slots,
+                            void* q, void* k, void* v, float* gamma, float* beta, float eps, float g_bias,
+                            float b_bias, int64_t B, int64_t H, int64_t Hkv, int64_t d, int dtype, void* stream);
+
+/*
+ * The gated inputs of the global layer's output projections (inference/models/atma.py:
+ * 246-252, model/blocks.py:470-490), no reference counterpart as one call:
+ * x2[b, h d + e] = c[b, h, e] * sigmoid(y[b, 2 h d + d + e]) and, when r is non-NULL,
+ * x2[b, H d + h d + e] = round(rms_norm(r[b, h]) (eps mem_eps)) * sigmoid(y[b, cm + h d
+ * + e]), each sigmoid and product rounded to 16 bits.  c (B, H, d) 16-bit, r fp32.
+ */
+int atma_global_decode_gate(const void* c, const float* r, const void* y, int64_t ldy, int64_t cm, void* x2,
+                            int64_t ldx2, float mem_eps, int64_t B, int64_t H, int64_t d, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,237 @@
+"""The decode-step fusions (``kernel/decode_fusions.py``; no reference counterpart, each
+the one-launch form of a chain of the reference's decode ops) against the chains they
+replace, run in torch on the same 16-bit inputs:
+
+* ``linear_tokens_multi`` / ``linear_tokens_chunks`` against fp32 ``F.linear`` (fp32
+  accumulation: parts within 2e-5 relative of the fp64 product, 16-bit outputs within
+  1e-2, the ``linear_tokens`` bar), the chunks' fused activation against
+  ``squared_relu_gate`` (the same bf16 operand values);
+* ``residual_rms_norm``: the new stream equal to the eager bf16 add bit for bit (one
+  rounding of the same fp32 sum), a branch of partial sums + biases + low-rank term
+  within one bf16 ulp of its fp64 sum (one rounding), the normed row within one ulp of
+  ``F.rms_norm`` (the reciprocal square root's last bit);
+* ``lfm2_conv_step``: equal bit for bit to ``b * x`` -> ``causal_conv1d_decode_step`` ->
+  ``c * (.)``, state tables included;
+* ``global_decode_prep`` / ``global_decode_gate``: the head RMSNorm + Canon conv + gates
+  chain and the gated projection inputs within 1e-2 relative (a normed or sigmoid value
+  one bf16 ulp apart from torch's carries through a product), the un-normed v conv, the
+  gates and the v table bit for bit, the normed tables within one ulp.
+"""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from tests.helpers import rel_err
+
+pytestmark = pytest.mark.gpu
+
+BF = torch.bfloat16
+
+
+def _g(dev, seed):
+    return torch.Generator(device=dev).manual_seed(seed)
+
+
+def _ulps(a, b):
+    """max |a - b| in units of b's bf16 spacing (2^(e-7) for |b| in [2^e, 2^(e+1)))."""
+    a, b = a.double(), b.double()
+    spacing = torch.exp2(torch.floor(torch.log2(b.abs().clamp_min(1e-30))) - 7)
+    return ((a - b).abs() / spacing).max().item()
+
+
+# --------------------------------------------------------------------------- projections
+@pytest.mark.parametrize("K", [256, 512, 1024, 2048])
+@pytest.mark.parametrize("M", [1, 7, 32])
+def test_linear_tokens_multi_segments_vs_fp32(dev, M, K):
+    from atma_amd.kernel.decode_fusions import linear_tokens_multi
+    g = _g(dev, M * 13 + K)
+    ns = [2048, 256, 256, 1024, 8, 4, 36]
+    x = torch.randn(M, K, device=dev, generator=g).to(BF)
+    ws = [(torch.randn(n, K, device=dev, generator=g) * 0.03).to(BF) for n in ns]
+    bs = [(torch.randn(n, device=dev, generator=g) * 0.1).to(BF) if i != 2 else None for i, n in enumerate(ns)]
+    y = linear_tokens_multi(x, ws, bs)
+    assert y.shape == (M, sum(ns))
+    off = 0
+    for w, b, n in zip(ws, bs, ns):
+        ref = F.linear(x.float(), w.float(), None if b is None else b.float())
+        assert rel_err(y[:, off:off + n], ref) <= 1e-2, (n, rel_err(y[:, off:off + n], ref))
+        off += n
+    assert torch.equal(y, linear_tokens_multi(x, ws, bs))
+
+
+def test_linear_tokens_multi_wide_segments(dev):
+    """Every segment a multiple of 32 and 4096+ outputs in all: 32 features per workgroup."""
+    from atma_amd.kernel.decode_fusions import linear_tokens_multi
+    g = _g(dev, 5)
+    x = torch.randn(32, 1024, device=dev, generator=g).half()
+    ws = [(torch.randn(n, 1024, device=dev, generator=g) * 0.03).half() for n in (4096, 1056)]
+    y = linear_tokens_multi(x, ws, [None, None])
+    assert rel_err(y[:, :4096], x.float() @ ws[0].float().t()) <= 1e-2
+    assert rel_err(y[:, 4096:], x.float() @ ws[1].float().t()) <= 1e-2
+
+
+@pytest.mark.parametrize("chunk_k,C", [(1024, 4), (256, 4), (512, 2), (1024, 1), (256, 8)])
+@pytest.mark.parametrize("M", [3, 32])
+def test_linear_tokens_chunks_vs_fp64(dev, M, chunk_k, C):
+    from atma_amd.kernel.decode_fusions import linear_tokens_chunks
+    g = _g(dev, M + chunk_k + C)
+    N = 1024
+    x = torch.randn(M, C * chunk_k + 64, device=dev, generator=g).to(BF)
+    w = (torch.randn(N, C * chunk_k, device=dev, generator=g) * 0.03).to(BF)
+    parts = linear_tokens_chunks(x, [w[:, c * chunk_k:(c + 1) * chunk_k] for c in range(C)], chunk_k)
+    assert parts.shape == (C, M, N) and parts.dtype == torch.float32
+    for c in range(C):
+        sl = slice(c * chunk_k, (c + 1) * chunk_k)
+        ref = x[:, sl].double() @ w[:, sl].double().t()
+        assert rel_err(parts[c], ref) <= 2e-5
+
+
+@pytest.mark.parametrize("M", [1, 32])
+def test_linear_tokens_chunks_squared_relu_gate(dev, M):
+    """The MLP's down projection with the activation formed on load equals
+    ``squared_relu_gate`` then the chunked product (same bf16 operands)."""
+    from atma_amd.kernel import squared_relu_gate
+    from atma_amd.kernel.decode_fusions import linear_tokens_chunks
+    g = _g(dev, 40 + M)
+    dim, hidden = 1024, 4096
+    y = torch.randn(M, 2 * hidden, device=dev, generator=g).to(BF)
+    w = (torch.randn(dim, hidden, device=dev, generator=g) * 0.02).to(BF)
+    parts = linear_tokens_chunks(y, [w[:, c * 1024:(c + 1) * 1024] for c in range(4)], 1024, sq_relu_gate=True)
+    h = squared_relu_gate(y[:, :hidden], y[:, hidden:])
+    ref = h.double() @ w.double().t()
+    assert rel_err(parts.sum(0), ref) <= 2e-5
+    eager = (y[:, hidden:] * y[:, :hidden].relu().square())
+    assert torch.equal(h, eager)
+
+
+def test_linear_tokens_chunks_rejects(dev):
+    from atma_amd.kernel.decode_fusions import linear_tokens_chunks
+    x = torch.randn(4, 2048, device=dev).to(BF)
+    w = torch.randn(64, 2048, device=dev).to(BF)
+    with pytest.raises(ValueError):
+        linear_tokens_chunks(x, [w[:, :2048]], 2048)        # chunk wider than 1024
+    with pytest.raises(ValueError):
+        linear_tokens_chunks(x, [w[:, :1024]] * 3, 1024)     # x holds 2 chunks, not 3
+    with pytest.raises(ValueError):
+        linear_tokens_chunks(torch.randn(33, 1024, device=dev).to(BF), [w[:, :1024]], 1024)
+
+
+# --------------------------------------------------------------------------- residual stream
+@pytest.mark.parametrize("D", [256, 1024, 2048, 4096])
+@pytest.mark.parametrize("M", [1, 5, 32, 300])
+def test_residual_rms_norm_tensor_branch(dev, M, D):
+    from atma_amd.kernel.decode_fusions import residual_rms_norm
+    g = _g(dev, M * 3 + D)
+    res = torch.randn(M, D, device=dev, generator=g).to(BF)
+    br = torch.randn(M, D, device=dev, generator=g).to(BF)
+    w = (1 + 0.1 * torch.randn(D, device=dev, generator=g)).to(BF)
+    out, s = residual_rms_norm(br, res, w, 1e-6)
+    eager_s = res + br
+    assert torch.equal(s, eager_s)
+    ref = F.rms_norm(eager_s.float(), (D,), w.float(), 1e-6)
+    assert _ulps(out, ref) <= 1.0
+    out0, s0 = residual_rms_norm(br, None, w, 1e-6)         # the stream starts with the branch
+    assert s0 is br and _ulps(out0, F.rms_norm(br.float(), (D,), w.float(), 1e-6)) <= 1.0
+
+
+@pytest.mark.parametrize("with_res", [True, False])
+@pytest.mark.parametrize("M", [1, 32])
+def test_residual_rms_norm_partial_sums(dev, M, with_res):
+    from atma_amd.kernel.decode_fusions import PartialSums, residual_rms_norm
+    g = _g(dev, 77 + M)
+    D, P, H = 1024, 2, 8
+    parts = torch.randn(P, M, D, device=dev, generator=g)
+    biases = [(torch.randn(D, device=dev, generator=g) * 0.1).to(BF) for _ in range(3)]
+    mag = torch.rand(M, H, device=dev, generator=g).to(BF)
+    mu_w = (torch.randn(D, H, device=dev, generator=g) * 0.3).to(BF)
+    res = torch.randn(M, D, device=dev, generator=g).to(BF) if with_res else None
+    w = (1 + 0.1 * torch.randn(D, device=dev, generator=g)).to(BF)
+    ps = PartialSums(parts, biases, mu_x=mag, mu_w=mu_w, dtype=BF)
+    out, s = residual_rms_norm(ps, res, w, 1e-6)
+    br64 = parts.double().sum(0) + sum(b.double() for b in biases) + mag.double() @ mu_w.double().t()
+    if with_res:                                           # the eager add of the rounded branch
+        assert _ulps(s, res + ps.materialize()) <= 1.0
+    else:                                                  # the branch itself: one rounding
+        assert _ulps(s, br64) <= 1.0
+    assert _ulps(out, F.rms_norm(s.float(), (D,), w.float(), 1e-6)) <= 1.0
+
+
+# --------------------------------------------------------------------------- mixers
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("K", [3, 4, 1])
+def test_lfm2_conv_step_equals_eager_chain(dev, dtype, K):
+    from atma_amd.kernel import causal_conv1d_decode_step
+    from atma_amd.kernel.decode_fusions import lfm2_conv_step
+    g = _g(dev, K)
+    B, D, S = 9, 1024, 12
+    bcx = torch.randn(B, 3 * D, device=dev, generator=g).to(dtype)
+    w = (torch.randn(D, K, device=dev, generator=g) * 0.5).to(dtype)
+    table = torch.randn(S, D, max(K - 1, 1), device=dev, generator=g).to(dtype)[:, :, :K - 1].contiguous()
+    slots = torch.tensor([3, 0, 11, 5, 7, 1, 2, 4, 6], device=dev)
+    t_fused, t_eager = table.clone(), table.clone()
+    out = lfm2_conv_step(bcx, w, slots, t_fused)
+    b, c, x = bcx.chunk(3, dim=-1)
+    ref = c * causal_conv1d_decode_step(b * x, w, slots, t_eager)
+    assert torch.equal(out, ref)
+    assert torch.equal(t_fused, t_eager)
+
+
+def _prep_inputs(dev, B=6, H=8, Hkv=2, d=128, Kc=4, S=10, seed=0):
+    g = _g(dev, seed)
+    hd, kvd = H * d, Hkv * d
+    W = 2 * hd + 2 * kvd + hd + 2 * H
+    y = torch.randn(B, W, device=dev, generator=g).to(BF)
+    taps = [(torch.randn(C, Kc, device=dev, generator=g) * 0.4).to(BF) for C in (hd, kvd, kvd)]
+    tables = [torch.randn(S, C, Kc - 1, device=dev, generator=g).to(BF) for C in (hd, kvd, kvd)]
+    slots = torch.randperm(S, device=dev, generator=g)[:B]
+    return y, taps, tables, slots
+
+
+@pytest.mark.parametrize("d,H,Hkv", [(128, 8, 2), (64, 4, 1)])
+def test_global_decode_prep_vs_eager_chain(dev, d, H, Hkv):
+    from atma_amd.kernel import causal_conv1d_decode_step, gated_delta_gates
+    from atma_amd.kernel.decode_fusions import global_decode_prep
+    y, taps, tables, slots = _prep_inputs(dev, H=H, Hkv=Hkv, d=d, seed=d + H)
+    B = y.shape[0]
+    hd, kvd = H * d, Hkv * d
+    ck, cv = 2 * hd, 2 * hd + kvd
+    cm = cv + kvd
+    cg = cm + hd
+    mine = [t.clone() for t in tables]
+    q, k, v, gamma, beta = global_decode_prep(y, H, Hkv, d, (ck, cv, cg, cg + H), taps, mine, slots,
+                                              torch.finfo(torch.float32).eps, gate_bias=(3.9, 0.0))
+    eager = [t.clone() for t in tables]
+    qg = y[:, :2 * hd].reshape(B, H, 2 * d)
+    qn = F.rms_norm(qg[..., :d], (d,))
+    kn = F.rms_norm(y[:, ck:cv].reshape(B, Hkv, d), (d,))
+    rq = causal_conv1d_decode_step(qn.reshape(B, hd), taps[0], slots, eager[0], residual=True)
+    rk = causal_conv1d_decode_step(kn.reshape(B, kvd), taps[1], slots, eager[1], residual=True)
+    rv = causal_conv1d_decode_step(y[:, cv:cm].contiguous(), taps[2], slots, eager[2], residual=True)
+    ga, be = gated_delta_gates(y[:, cg:cg + H].float(), y[:, cg + H:cg + 2 * H].float(), 3.9, 0.0,
+                               decay_as_prob=True)
+    assert rel_err(q.reshape(B, hd), rq) <= 1e-2 and rel_err(k.reshape(B, kvd), rk) <= 1e-2
+    assert torch.equal(v.reshape(B, kvd), rv)
+    assert torch.equal(gamma, ga) and torch.equal(beta, be)
+    # the tables hold the normed inputs: equal where the norm rounded alike
+    assert torch.equal(mine[2], eager[2])
+    assert _ulps(mine[0], eager[0]) <= 1.0 and _ulps(mine[1], eager[1]) <= 1.0
+
+
+def test_global_decode_gate_vs_eager(dev):
+    from atma_amd.kernel.decode_fusions import global_decode_gate
+    g = _g(dev, 9)
+    B, H, d = 7, 8, 128
+    hd = H * d
+    y = torch.randn(B, 4 * hd, device=dev, generator=g).to(BF)
+    cm = 3 * hd
+    c = torch.randn(B, H, d, device=dev, generator=g).to(BF)
+    r = torch.randn(B, H, d, device=dev, generator=g) * 1e-2
+    x2 = global_decode_gate(c, r, y, cm, torch.finfo(torch.float32).eps)
+    gate = y[:, :2 * hd].reshape(B, H, 2 * d)[..., d:].reshape(B, hd)
+    ref1 = c.reshape(B, hd) * torch.sigmoid(gate)
+    ref2 = F.rms_norm(r, (d,)).reshape(B, hd).to(BF) * torch.sigmoid(y[:, cm:cm + hd])
+    assert rel_err(x2[:, :hd], ref1) <= 1e-2
+    assert rel_err(x2[:, hd:], ref2) <= 1e-2
+    only = global_decode_gate(c, None, y, cm, 0.0)
+    assert only.shape == (B, hd) and torch.equal(only, x2[:, :hd])

@@ -56,7 +56,7 @@ def test_linear_tokens_rejects_unsupported(dev):
     with pytest.raises(ValueError):
         linear_tokens(x, w)                        # 33 rows
     with pytest.raises(ValueError):
-        linear_tokens(x[:4, :1000], w[:, :1000])   # K not 1024 / 2048
+        linear_tokens(x[:4, :1000], w[:, :1000])   # K not 256 / 512 / 1024 / 2048
     with pytest.raises(ValueError):
         linear_tokens(torch.randn(4, 4096, device=dev).bfloat16(), torch.randn(64, 4096, device=dev).bfloat16())
 
