@@ -63,6 +63,7 @@ SIGNATURES = {
     "atma_gated_delta_bwd16_local": (_i32, [_p] * 18 + [_i64] * 4 + [_i32, _p]),
     "atma_squared_relu_gate": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i32, _p]),
     "atma_softcap_logits": (_i32, [_p, _p, _i64, _i32, _p]),
+    "atma_softcap_argmax": (_i32, [_p, _i64, _p, _i64, _p, _i64, _i64, _i32, _p]),
     "atma_linear_tokens_supported": (_i32, [_i64, _i64, _i64, _i32]),
     "atma_linear_tokens": (_i32, [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),
     "atma_linear_tokens_multi": (_i32, [_p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _i32, _p]),

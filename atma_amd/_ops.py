@@ -609,6 +609,24 @@ def _(x, weight, bias):
     return x.new_empty((x.shape[0], weight.shape[0]))
 
 
+@torch.library.custom_op("atma_hip::softcap_argmax", mutates_args=())
+def softcap_argmax_op(logits: Tensor) -> List[Tensor]:
+    _need_cuda(logits)
+    rows, V = logits.shape
+    out = torch.empty((rows, V), device=logits.device, dtype=logits.dtype)
+    ids = torch.empty((rows,), device=logits.device, dtype=torch.int64)
+    rc = _lib.load().atma_softcap_argmax(logits.data_ptr(), logits.stride(0), out.data_ptr(), out.stride(0),
+                                         ids.data_ptr(), rows, V, _lib.dtype_code(logits.dtype),
+                                         _lib.stream_handle(logits.device))
+    _lib.check(rc, "softcap_argmax")
+    return [out, ids]
+
+
+@softcap_argmax_op.register_fake
+def _(logits):
+    return [logits.new_empty(logits.shape), logits.new_empty((logits.shape[0],), dtype=torch.int64)]
+
+
 @torch.library.custom_op("atma_hip::packed_causal_conv1d", mutates_args=("state_table",))
 def packed_causal_conv1d_op(x: Tensor, weight: Tensor, state_table: Tensor, token_seq_starts: Tensor,
                             token_seq_ends: Tensor, token_seq_slots: Tensor) -> Tensor:

@@ -6,7 +6,7 @@
 //    adds every branch to the stream and normalises the sum for the next branch, so the add
 //    and the norm read and write the row once together.  The branch is a 16-bit tensor or
 //    fp32 partial sums (linear_tokens' chunks form) plus biases and a low-rank term (the
-//    global layer's mu_proj(mag), H <= 16 inputs), added in fp32 and rounded once.
+//    global layer's mu_proj(mag), 4, 8 or 16 inputs), added in fp32 and rounded once.
 //  * lfm2_conv_step: the LFM2 block's gated conv for one token, c * conv(b * x)
 //    (model/reference.py:31-48, inference/models/atma.py:625-673) from the rows of its
 //    in_proj output, state table advanced in place.
@@ -27,20 +27,6 @@ namespace atma {
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
 
 template <typename T>
-__device__ __forceinline__ void load8(const T* p, float* v) {
-  const u32x4 u = *(const u32x4*)p;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] = elem16<T>(u, e);
-}
-__device__ __forceinline__ void load8(const float* p, float* v) {
-  const f32x4 a = *(const f32x4*)p, b = *(const f32x4*)(p + 4);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    v[e] = a[e];
-    v[4 + e] = b[e];
-  }
-}
-template <typename T>
 __device__ __forceinline__ void store8(T* p, const float* v) {
   u32x4 u;
 #pragma unroll
@@ -52,7 +38,6 @@ __device__ __forceinline__ float rnd(float x) { return to_f32(from_f32<T>(x)); }
 
 // ------------------------------------------------------------------ residual_rms_norm
 constexpr int kResMaxBias = 3;
-constexpr int kResMaxMu = 16;
 
 struct ResNormArgs {
   const void* y;  // branch (M, D) in T, row stride ldy; or null: the branch is `parts`
@@ -76,51 +61,83 @@ struct ResNormArgs {
   int M, D;
 };
 
-// one wave per row, P passes of 512 columns (8 per lane)
-template <typename T, int P>
+constexpr int kResMaxParts = 8;
+
+template <typename T>
+__device__ __forceinline__ void unpack8(const u32x4& u, float* v) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = elem16<T>(u, e);
+}
+__device__ __forceinline__ f32x4 ld4(const float* p) { return *(const f32x4*)p; }
+
+// One wave per row, P passes of 512 columns (8 per lane).  A pass issues every load it
+// needs (branch or partial sums, biases, low-rank weights, residual, gain) before its
+// first arithmetic, so a row costs one memory round trip per pass.  MU: the low-rank
+// term's width (0: none), a template so that its weights index registers statically.
+template <typename T, int P, int MU>
 __global__ void __launch_bounds__(256) residual_rms_norm_kernel(ResNormArgs a) {
   const int lane = threadIdx.x & 63;
   const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (m >= a.M) return;
-  float s[P][8];
-  float sq = 0.f;
-  float mu[kResMaxMu];
-  if (a.mu_x) {
+  float mu[MU > 0 ? MU : 1];
+  if constexpr (MU > 0) {
     const T* mx = (const T*)a.mu_x + (int64_t)m * a.ldmu;
 #pragma unroll
-    for (int h = 0; h < kResMaxMu; ++h) mu[h] = h < a.mu_k ? to_f32(mx[h]) : 0.f;
+    for (int h = 0; h < MU; ++h) mu[h] = to_f32(mx[h]);
   }
+  float s[P][8];
+  u32x4 wv[P];
+  float sq = 0.f;
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int c = (p * 64 + lane) * 8;
-    if (c >= a.D) continue;
+    const bool in = c < a.D;
+    const int cc = in ? c : 0;  // lanes past the row read column 0 and drop it
+    wv[p] = *(const u32x4*)((const T*)a.w + cc);
+    u32x4 rv = {0u, 0u, 0u, 0u};
+    if (a.res) rv = *(const u32x4*)((const T*)a.res + (int64_t)m * a.ldr + cc);
     float br[8];
     if (a.y) {
-      load8((const T*)a.y + (int64_t)m * a.ldy + c, br);
+      unpack8<T>(*(const u32x4*)((const T*)a.y + (int64_t)m * a.ldy + cc), br);
     } else {
-      load8(a.parts + (int64_t)m * a.D + c, br);
-      for (int q = 1; q < a.n_parts; ++q) {
-        float t[8];
-        load8(a.parts + ((int64_t)q * a.M + m) * a.D + c, t);
+      f32x4 pv[kResMaxParts][2];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) br[e] += t[e];
+      for (int q = 0; q < kResMaxParts; ++q)
+        if (q < a.n_parts) {
+          const float* pp = a.parts + ((int64_t)q * a.M + m) * a.D + cc;
+          pv[q][0] = ld4(pp);
+          pv[q][1] = ld4(pp + 4);
+        }
+      u32x4 bv[kResMaxBias];
+#pragma unroll
+      for (int b = 0; b < kResMaxBias; ++b)
+        if (b < a.n_bias) bv[b] = *(const u32x4*)((const T*)a.bias[b] + cc);
+      u32x4 mwv[MU > 0 ? MU : 1];
+      if constexpr (MU > 0) {
+        // rows cc .. cc + 7 of mu_w (D, MU): 8 MU contiguous values, MU 16-byte vectors
+#pragma unroll
+        for (int i = 0; i < MU; ++i) mwv[i] = *(const u32x4*)((const T*)a.mu_w + (int64_t)cc * MU + 8 * i);
       }
 #pragma unroll
-      for (int b = 0; b < kResMaxBias; ++b) {
-        if (b >= a.n_bias) break;
-        float t[8];
-        load8((const T*)a.bias[b] + c, t);
+      for (int e = 0; e < 8; ++e) br[e] = pv[0][e >> 2][e & 3];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) br[e] += t[e];
-      }
-      if (a.mu_x) {
-        const T* mw = (const T*)a.mu_w + (int64_t)c * a.mu_k;
+      for (int q = 1; q < kResMaxParts; ++q)
+        if (q < a.n_parts) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) br[e] += pv[q][e >> 2][e & 3];
+        }
+#pragma unroll
+      for (int b = 0; b < kResMaxBias; ++b)
+        if (b < a.n_bias) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) br[e] += elem16<T>(bv[b], e);
+        }
+      if constexpr (MU > 0) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           float acc = 0.f;
 #pragma unroll
-          for (int h = 0; h < kResMaxMu; ++h)
-            if (h < a.mu_k) acc += mu[h] * to_f32(mw[e * a.mu_k + h]);
+          for (int h = 0; h < MU; ++h) acc += mu[h] * elem16<T>(mwv[(e * MU + h) >> 3], (e * MU + h) & 7);
           br[e] += acc;
         }
       }
@@ -129,14 +146,19 @@ __global__ void __launch_bounds__(256) residual_rms_norm_kernel(ResNormArgs a) {
     }
     if (a.res) {
       float x[8];
-      load8((const T*)a.res + (int64_t)m * a.ldr + c, x);
+      unpack8<T>(rv, x);
 #pragma unroll
       for (int e = 0; e < 8; ++e) s[p][e] = rnd<T>(x[e] + br[e]);
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) s[p][e] = br[e];
     }
-    if (a.res_out) store8((T*)a.res_out + (int64_t)m * a.ldro + c, s[p]);
+    if (!in) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s[p][e] = 0.f;
+    } else if (a.res_out) {
+      store8((T*)a.res_out + (int64_t)m * a.ldro + c, s[p]);
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) sq += s[p][e] * s[p][e];
   }
@@ -145,21 +167,31 @@ __global__ void __launch_bounds__(256) residual_rms_norm_kernel(ResNormArgs a) {
   for (int p = 0; p < P; ++p) {
     const int c = (p * 64 + lane) * 8;
     if (c >= a.D) continue;
-    float wv[8], o[8];
-    load8((const T*)a.w + c, wv);
+    float w8[8], o[8];
+    unpack8<T>(wv[p], w8);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = (s[p][e] * rstd) * wv[e];
+    for (int e = 0; e < 8; ++e) o[e] = (s[p][e] * rstd) * w8[e];
     store8((T*)a.out + (int64_t)m * a.ldo + c, o);
   }
 }
 
+template <typename T, int MU>
+static void launch_res_norm_mu(const ResNormArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)((a.M + 3) / 4)), block(256);
+  if (a.D <= 512) residual_rms_norm_kernel<T, 1, MU><<<grid, block, 0, s>>>(a);
+  else if (a.D <= 1024) residual_rms_norm_kernel<T, 2, MU><<<grid, block, 0, s>>>(a);
+  else if (a.D <= 2048) residual_rms_norm_kernel<T, 4, MU><<<grid, block, 0, s>>>(a);
+  else residual_rms_norm_kernel<T, 8, MU><<<grid, block, 0, s>>>(a);
+}
+
 template <typename T>
 static void launch_res_norm(const ResNormArgs& a, hipStream_t s) {
-  const dim3 grid((unsigned)((a.M + 3) / 4)), block(256);
-  if (a.D <= 512) residual_rms_norm_kernel<T, 1><<<grid, block, 0, s>>>(a);
-  else if (a.D <= 1024) residual_rms_norm_kernel<T, 2><<<grid, block, 0, s>>>(a);
-  else if (a.D <= 2048) residual_rms_norm_kernel<T, 4><<<grid, block, 0, s>>>(a);
-  else residual_rms_norm_kernel<T, 8><<<grid, block, 0, s>>>(a);
+  switch (a.mu_x ? a.mu_k : 0) {
+    case 4: launch_res_norm_mu<T, 4>(a, s); break;
+    case 8: launch_res_norm_mu<T, 8>(a, s); break;
+    case 16: launch_res_norm_mu<T, 16>(a, s); break;
+    default: launch_res_norm_mu<T, 0>(a, s); break;
+  }
 }
 
 // ------------------------------------------------------------------ lfm2_conv_step
@@ -336,11 +368,12 @@ extern "C" int atma_residual_rms_norm(const void* y, int64_t ldy, const float* p
   if (M == 0) return ATMA_OK;
   if (!weight || !out || (!y && !parts) || (y && parts))
     return set_error(ATMA_ERR_INVALID, "residual_rms_norm: need weight, out and exactly one of y / parts");
-  if (parts && (n_parts < 1 || n_bias < 0 || n_bias > kResMaxBias || (n_bias && !bias)))
-    return set_error(ATMA_ERR_INVALID, "residual_rms_norm: 1 or more parts and at most %d biases", kResMaxBias);
-  if (mu_x && (!parts || !mu_w || mu_k < 1 || mu_k > kResMaxMu || ldmu < mu_k))
-    return set_error(ATMA_ERR_INVALID, "residual_rms_norm: the low-rank term needs parts, mu_w and 1 <= k <= %d",
-                     kResMaxMu);
+  if (parts && (n_parts < 1 || n_parts > kResMaxParts || n_bias < 0 || n_bias > kResMaxBias || (n_bias && !bias)))
+    return set_error(ATMA_ERR_INVALID, "residual_rms_norm: 1 to %d parts and at most %d biases", kResMaxParts,
+                     kResMaxBias);
+  if (mu_x && (!parts || !mu_w || (mu_k != 4 && mu_k != 8 && mu_k != 16) || ldmu < mu_k || ((uintptr_t)mu_w & 15)))
+    return set_error(ATMA_ERR_INVALID,
+                     "residual_rms_norm: the low-rank term needs parts and a 16-byte aligned mu_w of width 4, 8 or 16");
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   if ((y && (!al16(y) || ldy % 8 || ldy < D)) || (parts && !al16(parts)) || (res && (!al16(res) || ldr % 8 || ldr < D)) ||
       (res_out && (!al16(res_out) || ldro % 8 || ldro < D)) || !al16(weight) || !al16(out) || ldo % 8 || ldo < D)

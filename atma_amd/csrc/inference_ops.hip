@@ -96,6 +96,65 @@ __global__ void __launch_bounds__(256) softcap_kernel(const T* __restrict__ x, T
   }
 }
 
+// ------------------------------------------------------------------ softcap_argmax
+// The decode step's soft cap and greedy pick in one pass over a row of logits: out =
+// softcap(x) (softcap_logits' arithmetic) and the index of its largest value as
+// torch.argmax over those 16-bit values returns it -- the first index among equal values,
+// NaN above every number.  One workgroup of 512 threads per row.
+__device__ __forceinline__ bool argmax_before(float v, int i, float bv, int bi) {
+  const bool vn = v != v, bn = bv != bv;
+  if (vn || bn) return vn && (!bn || i < bi);
+  return v > bv || (v == bv && i < bi);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(512)
+softcap_argmax_kernel(const T* __restrict__ x, int64_t ldx, T* __restrict__ out, int64_t ldo,
+                      int64_t* __restrict__ idx, int V, int vec) {
+  const T* xr = x + (int64_t)blockIdx.x * ldx;
+  T* orow = out + (int64_t)blockIdx.x * ldo;
+  float best = -__builtin_inff();
+  int bi = 0x7fffffff;
+  const int nv = vec ? V / 8 : 0;  // 16-byte vectors when every row is 16-byte aligned
+  for (int i = threadIdx.x; i < nv; i += 512) {
+    const u32x4 u = *(const u32x4*)(xr + 8 * i);
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float y0 = to_f32(from_f32<T>(softcap1<T>(elem16<T>(u, 2 * e))));
+      const float y1 = to_f32(from_f32<T>(softcap1<T>(elem16<T>(u, 2 * e + 1))));
+      o[e] = pack2<T>(y0, y1);
+      if (argmax_before(y0, 8 * i + 2 * e, best, bi)) best = y0, bi = 8 * i + 2 * e;
+      if (argmax_before(y1, 8 * i + 2 * e + 1, best, bi)) best = y1, bi = 8 * i + 2 * e + 1;
+    }
+    *(u32x4*)(orow + 8 * i) = o;
+  }
+  for (int i = 8 * nv + threadIdx.x; i < V; i += 512) {
+    const float y = to_f32(from_f32<T>(softcap1<T>(to_f32(xr[i]))));
+    orow[i] = from_f32<T>(y);
+    if (argmax_before(y, i, best, bi)) best = y, bi = i;
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(best, m, 64);
+    const int oi = __shfl_xor(bi, m, 64);
+    if (argmax_before(ov, oi, best, bi)) best = ov, bi = oi;
+  }
+  __shared__ float sv[8];
+  __shared__ int si[8];
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sv[wave] = best;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 8; ++w)
+      if (argmax_before(sv[w], si[w], best, bi)) best = sv[w], bi = si[w];
+    idx[blockIdx.x] = bi;
+  }
+}
+
 // ------------------------------------------------------------------ packed_causal_conv1d
 constexpr int kConvStrip = 32;  // tokens per lane strip
 constexpr int kConvMaxK = 8;
@@ -319,6 +378,26 @@ extern "C" int atma_softcap_logits(const void* logits, void* out, int64_t n, int
     case ATMA_F16: return launch_softcap<f16>(logits, out, n, s);
     default: return set_error(ATMA_ERR_INVALID, "softcap_logits: unknown dtype %d", dtype);
   }
+}
+
+extern "C" int atma_softcap_argmax(const void* logits, int64_t ldx, void* out, int64_t ldo, int64_t* idx,
+                                   int64_t rows, int64_t V, int dtype, void* stream) {
+  using namespace atma;
+  if (dtype != ATMA_BF16 && dtype != ATMA_F16)
+    return set_error(ATMA_ERR_UNSUPPORTED, "softcap_argmax: 16-bit logits only (dtype %d)", dtype);
+  if (rows < 0 || V < 1 || V > 0x7fffffff || rows > 0x7fffffff || ldx < V || ldo < V)
+    return set_error(ATMA_ERR_INVALID, "softcap_argmax: bad sizes");
+  if (rows == 0) return ATMA_OK;
+  if (!logits || !out || !idx) return set_error(ATMA_ERR_INVALID, "softcap_argmax: null pointer");
+  const int vec = !((uintptr_t)logits % 16 || (uintptr_t)out % 16 || ldx % 8 || ldo % 8);
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == ATMA_BF16)
+    softcap_argmax_kernel<bf16><<<dim3((unsigned)rows), dim3(512), 0, s>>>((const bf16*)logits, ldx, (bf16*)out, ldo,
+                                                                         idx, (int)V, vec);
+  else
+    softcap_argmax_kernel<f16><<<dim3((unsigned)rows), dim3(512), 0, s>>>((const f16*)logits, ldx, (f16*)out, ldo,
+                                                                        idx, (int)V, vec);
+  return check_launch("softcap_argmax");
 }
 
 extern "C" int atma_packed_causal_conv1d(const void* x, int64_t x_st, int64_t x_sc, const void* weight,

@@ -20,7 +20,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from ..kernel import causal_conv1d_decode_step, packed_causal_conv1d, softcap_logits
+from ..kernel import causal_conv1d_decode_step, packed_causal_conv1d, softcap_argmax, softcap_logits
 from ..kernel.decode_fusions import lfm2_conv_step, residual_rms_norm_supported
 from ..layers.attention import Attention
 from ..layers.global_attention import MLP, GlobalLayerCache, Linear, PolarAttention, RMSNorm, decode_rows
@@ -191,6 +191,15 @@ class Atma(nn.Module):
         if ctx.is_prefill and ctx.cu_seqlens_q is not None:
             hidden = hidden[ctx.cu_seqlens_q[1:].long() - 1]
         return softcap_logits(self.proj(hidden))
+
+    def decode_head(self, hidden):
+        """Logits of one token per decoding sequence and, for 16-bit models, their greedy
+        ids from the same pass over the logits (``softcap_argmax``); graph capturable.
+        Returns (logits, ids or None)."""
+        logits = self.proj(hidden)
+        if logits.dtype in (torch.bfloat16, torch.float16):
+            return softcap_argmax(logits)
+        return softcap_logits(logits), None
 
     def init_weights(self, std=0.02, seed=0):
         """Every parameter N(0, std) from ``seed`` (the random-init convention of the

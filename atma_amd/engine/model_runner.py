@@ -64,7 +64,7 @@ class ModelRunner:
         self._zero_state_tables()
 
     def exit(self):
-        for name in ("graphs", "graph_pool", "graph_vars"):
+        for name in ("graphs", "graph_out", "graph_pool", "graph_vars"):
             if hasattr(self, name):
                 delattr(self, name)
         torch.cuda.synchronize(self.device)
@@ -146,23 +146,43 @@ class ModelRunner:
                 self.free_seq_slot(s)
         torch.cuda.synchronize(self.device)
 
+    def _decode_stage(self, max_bs, max_blocks):
+        """One buffer for every decode-step input the graphs read: token ids and table
+        rows (int64), cache slots, context lengths and block tables (int32).  Each step
+        fills a pinned host copy (two, used in turn) and sends it with one H2D copy."""
+        n64, n32 = 2 * max_bs, 2 * max_bs + max_bs * max_blocks
+        nbytes = 8 * n64 + 4 * n32
+        dev = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        hosts = [torch.empty(nbytes, dtype=torch.uint8).pin_memory() for _ in range(2)]
+
+        def views(buf):
+            i64 = buf[:8 * n64].view(torch.int64)
+            i32 = buf[8 * n64:].view(torch.int32)
+            return dict(input_ids=i64[:max_bs], seq_slots=i64[max_bs:], slot_mapping=i32[:max_bs],
+                        context_lens=i32[max_bs:2 * max_bs],
+                        block_tables=i32[2 * max_bs:].view(max_bs, max_blocks))
+        self._stage_dev, self._stage_hosts = dev, hosts
+        self._stage_np = [{k: v.numpy() for k, v in views(h).items()} for h in hosts]
+        self._stage_flip = 0
+        return views(dev)
+
     @torch.inference_mode()
     def capture_cudagraph(self):
-        """The decode forward captured once per batch-size bucket (``:254-310``)."""
-        hf, cfg = self.config.hf_config, self.config
+        """The decode forward captured once per batch-size bucket (``:254-310``), LM head
+        included; 16-bit models also take the greedy ids inside the graph
+        (``Atma.decode_head``)."""
+        cfg = self.config
         max_bs = cfg.max_num_seqs
         max_blocks = (cfg.max_model_len + self.block_size - 1) // self.block_size
-        dev = self.device
-        gv = dict(input_ids=torch.zeros(max_bs, dtype=torch.int64, device=dev),
-                  positions=torch.zeros(max_bs, dtype=torch.int64, device=dev),
-                  slot_mapping=torch.full((max_bs,), -1, dtype=torch.int32, device=dev),
-                  context_lens=torch.zeros(max_bs, dtype=torch.int32, device=dev),
-                  block_tables=torch.zeros(max_bs, max_blocks, dtype=torch.int32, device=dev),
-                  seq_slots=torch.full((max_bs,), self.pad_slot, dtype=torch.int64, device=dev),
-                  outputs=torch.zeros(max_bs, hf.hidden_size, device=dev, dtype=hf.dtype))
+        gv = self._decode_stage(max_bs, max_blocks)
+        gv["slot_mapping"].fill_(-1)
+        gv["context_lens"].zero_()
+        gv["block_tables"].zero_()
+        gv["input_ids"].zero_()
+        gv["seq_slots"].fill_(self.pad_slot)
         self.graph_bs = sorted({b for b in [1, 2, 4, 8] + list(range(16, max_bs + 1, 16)) + [max_bs]
                                 if b <= max_bs})
-        self.graphs, self.graph_pool = {}, None
+        self.graphs, self.graph_out, self.graph_pool = {}, {}, None
         # two execs per bucket, replayed in turn: a graph exec relaunched right behind
         # itself waits for its previous launch to retire, two alternating ones do not
         self.graph_flip = 0
@@ -170,19 +190,53 @@ class ModelRunner:
             set_context(False, slot_mapping=gv["slot_mapping"][:bs], context_lens=gv["context_lens"][:bs],
                         block_tables=gv["block_tables"][:bs], seq_slots=gv["seq_slots"][:bs],
                         conv_state_tables=self.conv_state_tables)
-            gv["outputs"][:bs] = self.model(gv["input_ids"][:bs], gv["positions"][:bs])   # warm-up
-            pair = []
+            self.model.decode_head(self.model(gv["input_ids"][:bs]))                 # warm-up
+            pair, outs = [], []
             for _ in range(2):
                 graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(graph, self.graph_pool):
-                    gv["outputs"][:bs] = self.model(gv["input_ids"][:bs], gv["positions"][:bs])
+                    out = self.model.decode_head(self.model(gv["input_ids"][:bs]))
                 if self.graph_pool is None:
                     self.graph_pool = graph.pool()
                 pair.append(graph)
-            self.graphs[bs] = pair
-            torch.cuda.synchronize(dev)
+                outs.append(out)
+            self.graphs[bs], self.graph_out[bs] = pair, outs
+            torch.cuda.synchronize(self.device)
             reset_context()
         self.graph_vars = gv
+
+    def _uses_graph(self, bs):
+        return not self.enforce_eager and hasattr(self, "graphs") and bs <= self.config.max_num_seqs
+
+    def _run_decode_graph(self, seqs):
+        """Replay the smallest captured bucket that fits: the step's inputs go in one H2D
+        copy of the staging buffer (rows past the batch: token 0, slot -1, length 0, the
+        tables' spare row), the graph runs the model and the LM head.  Returns (logits
+        (bs, V), greedy ids (bs,) or None)."""
+        bs = len(seqs)
+        bucket = next(b for b in self.graph_bs if b >= bs)
+        k = self._stage_flip
+        self._stage_flip ^= 1
+        h = self._stage_np[k]
+        page = self.block_size
+        h["input_ids"][:bs] = [s.last_token for s in seqs]
+        h["input_ids"][bs:] = 0
+        h["seq_slots"][:bs] = [s.seq_slot for s in seqs]
+        h["seq_slots"][bs:] = self.pad_slot
+        h["context_lens"][:bs] = [len(s) for s in seqs]
+        h["context_lens"][bs:] = 0
+        h["slot_mapping"][:bs] = [s.block_table[(len(s) - 1) // page] * page + (len(s) - 1) % page for s in seqs]
+        h["slot_mapping"][bs:] = -1
+        bt = h["block_tables"]
+        bt[:bucket] = 0
+        for i, s in enumerate(seqs):
+            bt[i, :len(s.block_table)] = s.block_table
+        self._stage_dev.copy_(self._stage_hosts[k], non_blocking=True)
+        g = self.graph_flip
+        self.graph_flip ^= 1
+        self.graphs[bucket][g].replay()
+        logits, ids = self.graph_out[bucket][g]
+        return logits[:bs], (None if ids is None else ids[:bs])
 
     # ------------------------------------------------------------------ inputs
     def _to_dev(self, values, dtype):
@@ -267,40 +321,27 @@ class ModelRunner:
     # ------------------------------------------------------------------ forward
     @torch.inference_mode()
     def run_model(self, input_ids, positions, is_prefill):
-        """Prefill eager; decode by replaying the smallest captured bucket that fits (``:491-513``)."""
-        bs = input_ids.size(0)
-        if is_prefill or self.enforce_eager or not hasattr(self, "graphs") or bs > self.config.max_num_seqs:
-            return self.model.compute_logits(self.model(input_ids, positions))
-        ctx = get_context()
-        graph = self.graphs[next(b for b in self.graph_bs if b >= bs)][self.graph_flip]
-        self.graph_flip ^= 1
-        gv = self.graph_vars
-        gv["input_ids"][:bs] = input_ids
-        gv["positions"][:bs] = positions
-        gv["slot_mapping"].fill_(-1)
-        gv["slot_mapping"][:bs] = ctx.slot_mapping
-        gv["context_lens"].zero_()
-        gv["context_lens"][:bs] = ctx.context_lens
-        n_blocks = ctx.block_tables.size(1)
-        gv["block_tables"][:bs, :n_blocks] = ctx.block_tables
-        gv["block_tables"][:bs, n_blocks:].zero_()
-        gv["seq_slots"].fill_(self.pad_slot)
-        gv["seq_slots"][:bs] = ctx.seq_slots
-        graph.replay()
-        return self.model.compute_logits(gv["outputs"][:bs])
+        """The model and its LM head, eager (prefill, or decode without graphs)."""
+        return self.model.compute_logits(self.model(input_ids, positions))
 
     @torch.inference_mode()
     def run(self, seqs, is_prefill):
         """Schedule-step entry (``:520-533``): slots for new sequences, inputs, forward,
         sampling; returns one token id per sequence.  ``last_logits`` keeps the step's
-        logits (one row per sequence)."""
+        logits (one row per sequence; after a graph replay, valid until the next step)."""
         for seq in seqs:
             if seq.seq_slot < 0:
                 self.alloc_seq_slot(seq)
-        input_ids, positions = self.prepare_prefill(seqs) if is_prefill else self.prepare_decode(seqs)
         temps = [s.temperature for s in seqs]
-        logits = self.run_model(input_ids, positions, is_prefill)
+        greedy = all(t == 0 for t in temps)
+        ids = None
+        if not is_prefill and self._uses_graph(len(seqs)):
+            logits, ids = self._run_decode_graph(seqs)
+        else:
+            input_ids, positions = self.prepare_prefill(seqs) if is_prefill else self.prepare_decode(seqs)
+            logits = self.run_model(input_ids, positions, is_prefill)
         self.last_logits = logits
-        tok = self.sampler(logits, self._to_dev(temps, torch.float32), all_greedy=all(t == 0 for t in temps))
+        if ids is None or not greedy:
+            ids = self.sampler(logits, self._to_dev(temps, torch.float32), all_greedy=greedy)
         reset_context()
-        return tok.tolist()
+        return ids.tolist()

@@ -21,7 +21,7 @@ _lib.load()   # raises HipLibraryMissing (ImportError) when the library is absen
 
 from .conv import causal_conv1d_decode_step  # noqa: E402
 from .inference_ops import (linear_tokens, linear_tokens_supported, packed_causal_conv1d,  # noqa: E402
-                            softcap_logits, squared_relu_gate)
+                            softcap_argmax, softcap_logits, squared_relu_gate)
 from .gated_delta import (StartSignal, chunk_gated_delta_rule, gated_delta_decode_step,  # noqa: E402
                           gated_delta_gates, recurrence_pays_to_overlap)
 from .polar import (global_decode_step, global_decode_step_supported, polar_attention_decode,  # noqa: E402
@@ -50,5 +50,6 @@ __all__ = [
     "causal_conv1d_decode_step",
     "squared_relu_gate",
     "softcap_logits",
+    "softcap_argmax",
     "packed_causal_conv1d",
 ]

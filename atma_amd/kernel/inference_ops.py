@@ -4,7 +4,8 @@ Mirrors ``kernel/inference_ops_triton.py`` of the reference (same names, argumen
 errors): ``squared_relu_gate`` (:123-135, the MLP activation of
 ``inference/models/atma.py:87-96``), ``softcap_logits`` (:214-223, the output soft cap of
 ``inference/models/atma.py:750-754``) and ``packed_causal_conv1d`` (:138-160, the grouped
-fresh prefill's depthwise convolutions, ``inference/models/atma.py:431-442, 648-652``).
+fresh prefill's depthwise convolutions, ``inference/models/atma.py:431-442, 648-652``);
+``softcap_argmax`` is the soft cap fused with the greedy sampler's argmax.
 The prototype ``linear_head_rms`` (:163-189) is not part of the served path and is not
 provided.  ``linear_tokens`` has no counterpart there: the served model's projection of a
 few token rows (one per decoding sequence), where the reference calls the vendor GEMM.
@@ -32,6 +33,19 @@ def squared_relu_gate(x, gate):
 def softcap_logits(logits):
     """Fuse the elementwise 15*x/sqrt(x^2+225) output soft cap (any shape, logits' dtype)."""
     return torch.ops.atma_hip.softcap_logits(logits)
+
+
+@torch.no_grad()
+def softcap_argmax(logits):
+    """``capped = softcap_logits(logits)`` and ``capped.float().argmax(-1)`` in one launch
+    (one workgroup per row): the decode step's soft cap and greedy pick.  logits (rows,
+    V) 16-bit.  Returns (capped (rows, V), ids (rows,) int64).
+    No counterpart in the reference's op set (its sampler takes the argmax in torch)."""
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("expected logits [rows, vocab] with unit inner stride")
+    if logits.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("softcap_argmax takes 16-bit logits")
+    return torch.ops.atma_hip.softcap_argmax(logits)
 
 
 @torch.no_grad()

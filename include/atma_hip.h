@@ -475,6 +475,17 @@ int atma_chunk_gated_delta_rule(const void* q, int64_t q_sb, int64_t q_st, int64
 int atma_wait_start_flag(const int32_t* flag, int32_t epoch, int64_t timeout_us, void* stream);
 
 /*
+ * The decode step's soft cap and greedy pick in one pass (softcap_logits, then the
+ * sampler's argmax for temperature-0 rows, inference/layers/sampler.py:5-10; no
+ * reference counterpart as one call): per row, out = 15 x / sqrt(x^2 + 225) with
+ * atma_softcap_logits' roundings (out may equal logits), and idx[row] = the index of the
+ * largest out value, the first among equals, NaN above every number (torch.argmax).
+ * 16-bit rows (16-byte vectors when every row is 16-byte aligned); one workgroup per row.
+ */
+int atma_softcap_argmax(const void* logits, int64_t ldx, void* out, int64_t ldo, int64_t* idx, int64_t rows,
+                        int64_t V, int dtype, void* stream);
+
+/*
  * Projection of a few token rows, with no counterpart in the reference (whose nn.Linear
  * calls the vendor GEMM, model/reference.py:22-28): y[m, n] = sum_k x[m, k] w[n, k]
  * (+ bias[n]) for M <= 32 rows, in 16 bits with fp32 accumulation and one rounding.  It
@@ -521,7 +532,7 @@ int atma_linear_tokens_chunks(const void* x, int64_t ldx, int64_t M, int64_t chu
  *   s   = res ? round(res[m] + br) : br        (written to res_out when non-NULL)
  *   out = round(s * rsqrt(mean(s^2) + eps) * weight)
  * Exactly one of y / parts; parts (n_parts, M, D) fp32; up to 3 biases (D,); mu_x (M,
- * mu_k) and mu_w (D, mu_k), mu_k <= 16 (the global layer's mu_proj(mag)); 16-bit rows,
+ * mu_k) and mu_w (D, mu_k), mu_k 4, 8 or 16 (the global layer's mu_proj(mag)); 16-bit rows,
  * D % 8 == 0, D <= 4096, every row 16-byte aligned.
  */
 int atma_residual_rms_norm(const void* y, int64_t ldy, const float* parts, int64_t n_parts, const void* const* bias,

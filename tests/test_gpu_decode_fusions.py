@@ -235,3 +235,33 @@ def test_global_decode_gate_vs_eager(dev):
     assert rel_err(x2[:, hd:], ref2) <= 1e-2
     only = global_decode_gate(c, None, y, cm, 0.0)
     assert only.shape == (B, hd) and torch.equal(only, x2[:, :hd])
+
+
+@pytest.mark.parametrize("H", [4, 16])
+def test_residual_rms_norm_low_rank_widths(dev, H):
+    from atma_amd.kernel.decode_fusions import PartialSums, residual_rms_norm
+    g = _g(dev, 300 + H)
+    M, D = 5, 256
+    parts = torch.randn(4, M, D, device=dev, generator=g)
+    mag = torch.rand(M, H, device=dev, generator=g).to(BF)
+    mu_w = (torch.randn(D, H, device=dev, generator=g) * 0.3).to(BF)
+    w = torch.ones(D, device=dev).to(BF)
+    out, s = residual_rms_norm(PartialSums(parts, [], mu_x=mag, mu_w=mu_w, dtype=BF), None, w, 1e-6)
+    br64 = parts.double().sum(0) + mag.double() @ mu_w.double().t()
+    assert _ulps(s, br64) <= 1.0
+
+
+@pytest.mark.parametrize("V", [50304, 1000, 77])
+def test_softcap_argmax_equals_softcap_then_argmax(dev, V):
+    from atma_amd.kernel import softcap_argmax, softcap_logits
+    g = _g(dev, V)
+    rows = 32
+    x = (torch.randn(rows, V, device=dev, generator=g) * 20).to(BF)
+    x[3, 10] = x[3, 500 % V] = 1e4                       # equal after the cap: the first index wins
+    x[5] = -float("inf")
+    x[6, V // 2] = float("nan")                           # NaN ranks above every number
+    capped, ids = softcap_argmax(x)
+    ref = softcap_logits(x)
+    assert torch.equal(capped.view(torch.int16), ref.view(torch.int16))   # bitwise (NaN rows included)
+    assert torch.equal(ids, ref.float().argmax(-1))
+    assert ids[3].item() == min(10, 500 % V) and ids[5].item() == 0 and ids[6].item() == V // 2
