@@ -18,14 +18,15 @@
 //    gate projections of one layer), each with its own bias and output rows; the launch's
 //    workgroups are laid over the segments' 16-feature tiles one after another, so the
 //    projections cost one launch.  Bias added in fp32, one rounding to the output type.
+//  * gated: the MLP's first projection with its activation, h[m, n] = gate * relu(a)^2
+//    of a = (x W^T + b)[m, n], gate = (x W^T + b)[m, H + n] (each rounded to the output
+//    type first, then squared_relu_gate's arithmetic): a workgroup computes the a and
+//    gate tiles of the same 16 features, so the 2H-wide projection is never written.
 //  * chunks: K split into chunks of 256-1024 across workgroups (blockIdx.y), chunk c with its
 //    own weight pointer, writing fp32 partial sums parts[c] (no bias, no rounding) for the
 //    consumer to add in chunk order (the residual RMSNorm).  That spreads a 4096-wide
 //    projection over 4x the workgroups, and lets two projections of different inputs whose
 //    outputs are summed (the global layer's output and memory projections) run as one.
-//    The activations can be formed as they load: gate * relu(a)^2 from the two halves of
-//    the MLP's first projection (squared_relu_gate's arithmetic), so the activation
-//    tensor is never written.
 //
 // No reference counterpart: the reference's nn.Linear calls the vendor GEMM
 // (model/reference.py:22-28); this is the engine's kernel for that call at decode shapes.
@@ -57,27 +58,16 @@ struct LinTokArgs {
   // segments form
   int n_segs;
   LinSeg seg[kLinMaxSegs];
-  // chunks form: chunk c reads x columns [c K, c K + K) (with the gate transform: a there,
-  // gate at gate_off + c K) and weights cw[c] (N, K) with row stride cldw[c]
+  // chunks form: chunk c reads x columns [c K, c K + K) and weights cw[c] (N, K) with row
+  // stride cldw[c]
   const void* cw[kLinMaxChunks];
   int64_t cldw[kLinMaxChunks];
-  int64_t gate_off;
   float* parts;  // (chunks, M, N) fp32
   int N;
 };
 
-enum LinMode { kLinSegments = 0, kLinChunks = 1, kLinChunksSqReluGate = 2 };
-
-// 8 values gate * relu(a)^2, rounded to T, as one 16-byte MFMA operand
-template <typename T>
-__device__ __forceinline__ u32x4 sq_relu_gate8(const u32x4& a, const u32x4& g) {
-  u32x4 o;
-#pragma unroll
-  for (int e = 0; e < 4; ++e)
-    o[e] = pack2<T>(sq_relu_gate1<T>(elem16<T>(a, 2 * e), elem16<T>(g, 2 * e)),
-                    sq_relu_gate1<T>(elem16<T>(a, 2 * e + 1), elem16<T>(g, 2 * e + 1)));
-  return o;
-}
+// kLinGated uses segment 0: its n is H, its weight has 2H rows (a, then gate), its output H
+enum LinMode { kLinSegments = 0, kLinChunks = 1, kLinGated = 2 };
 
 // NW waves per workgroup (K per launch or chunk = NW * 256, NW <= kLinMaxWaves); FT 16-feature tiles per
 // workgroup, which share each activation load
@@ -105,6 +95,12 @@ __global__ void __launch_bounds__(64 * NW) linear_tokens_kernel(LinTokArgs a) {
         n_lim = a.seg[s].n;
         f0 = (tile - a.seg[s].tile0) * 16 * FT;
       }
+  } else if constexpr (MODE == kLinGated) {
+    static_assert(FT == 2, "the gated form pairs an a tile with its gate tile");
+    wp = a.seg[0].w;
+    ldw = a.seg[0].ldw;
+    n_lim = a.seg[0].n;
+    f0 = tile * 16;
   } else {
     const int c = blockIdx.y;
 #pragma unroll
@@ -130,24 +126,13 @@ __global__ void __launch_bounds__(64 * NW) linear_tokens_kernel(LinTokArgs a) {
   for (int u = 0; u < kLinSteps; ++u) {
 #pragma unroll
     for (int f = 0; f < FT; ++f) {
-      const int row = min(f0 + 16 * f + r, n_lim - 1);  // rows past the segment: discarded
+      // rows past the segment are clamped and discarded; the gated form's second tile is
+      // the gate rows of the same features
+      const int row = MODE == kLinGated ? f * n_lim + f0 + r : min(f0 + 16 * f + r, n_lim - 1);
       wv[u][f] = __builtin_nontemporal_load((const u32x4*)(W + (int64_t)row * ldw + k0 + 32 * u));
     }
     xv0[u] = *(const u32x4*)(x0 + 32 * u);
     xv1[u] = *(const u32x4*)(x1 + 32 * u);
-  }
-  if constexpr (MODE == kLinChunksSqReluGate) {
-    u32x4 gv0[kLinSteps], gv1[kLinSteps];
-#pragma unroll
-    for (int u = 0; u < kLinSteps; ++u) {
-      gv0[u] = *(const u32x4*)(x0 + a.gate_off + 32 * u);
-      gv1[u] = *(const u32x4*)(x1 + a.gate_off + 32 * u);
-    }
-#pragma unroll
-    for (int u = 0; u < kLinSteps; ++u) {
-      xv0[u] = sq_relu_gate8<T>(xv0[u], gv0[u]);
-      xv1[u] = sq_relu_gate8<T>(xv1[u], gv1[u]);
-    }
   }
   const u32x4 zero = {0u, 0u, 0u, 0u};
   f32x4 acc[FT][2];
@@ -175,6 +160,34 @@ __global__ void __launch_bounds__(64 * NW) linear_tokens_kernel(LinTokArgs a) {
     if (wave > 0) return;
   }
   // lane l holds features 4 (l / 16) + [0, 4) of tile f, token 16 t + l % 16
+  auto reduced = [&](int f, int t) {
+    f32x4 v = acc[f][t];
+#pragma unroll
+    for (int w = 0; w < NW - 1; ++w) v += red[w][f][t][lane];
+    return v;
+  };
+  auto bias4 = [&](const void* b, int n) {
+    if (!b) return f32x4{0.f, 0.f, 0.f, 0.f};
+    const T* bp = (const T*)b + n;
+    return f32x4{to_f32(bp[0]), to_f32(bp[1]), to_f32(bp[2]), to_f32(bp[3])};
+  };
+  if constexpr (MODE == kLinGated) {
+    const int n = f0 + 4 * g;
+    const f32x4 ba = bias4(a.seg[0].bias, n), bg = bias4(a.seg[0].bias, n_lim + n);
+    T* Y = (T*)a.seg[0].y;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const f32x4 va = reduced(0, t) + ba, vg = reduced(1, t) + bg;
+      const int m = 16 * t + r;
+      if (m >= a.M) continue;
+      float h[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) h[e] = sq_relu_gate1<T>(to_f32(from_f32<T>(va[e])), to_f32(from_f32<T>(vg[e])));
+      const u32x2 pk = {pack2<T>(h[0], h[1]), pack2<T>(h[2], h[3])};
+      *(u32x2*)(Y + (int64_t)m * a.seg[0].ldy + n) = pk;
+    }
+    return;
+  }
 #pragma unroll
   for (int f = 0; f < FT; ++f) {
     const int n = f0 + 16 * f + 4 * g;  // n_lim % 4 == 0: a lane's four features are all in or all out
@@ -188,17 +201,12 @@ __global__ void __launch_bounds__(64 * NW) linear_tokens_kernel(LinTokArgs a) {
         if (s == seg) {
           Y = (T*)a.seg[s].y;
           ldy = a.seg[s].ldy;
-          if (a.seg[s].bias) {
-            const T* bp = (const T*)a.seg[s].bias + n;
-            bv = f32x4{to_f32(bp[0]), to_f32(bp[1]), to_f32(bp[2]), to_f32(bp[3])};
-          }
+          bv = bias4(a.seg[s].bias, n);
         }
     }
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      f32x4 v = acc[f][t];
-#pragma unroll
-      for (int w = 0; w < NW - 1; ++w) v += red[w][f][t][lane];
+      f32x4 v = reduced(f, t);
       const int m = 16 * t + r;
       if (m >= a.M) continue;
       if constexpr (MODE == kLinSegments) {
@@ -220,10 +228,14 @@ static void launch_segments(const LinTokArgs& a, int tiles, bool wide, hipStream
 }
 
 template <typename T, int NW>
-static void launch_chunks(const LinTokArgs& a, int chunks, bool sq_relu_gate, hipStream_t s) {
+static void launch_chunks(const LinTokArgs& a, int chunks, hipStream_t s) {
   const dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)chunks);
-  if (sq_relu_gate) linear_tokens_kernel<T, NW, 1, kLinChunksSqReluGate><<<grid, dim3(64 * NW), 0, s>>>(a);
-  else linear_tokens_kernel<T, NW, 1, kLinChunks><<<grid, dim3(64 * NW), 0, s>>>(a);
+  linear_tokens_kernel<T, NW, 1, kLinChunks><<<grid, dim3(64 * NW), 0, s>>>(a);
+}
+
+template <typename T, int NW>
+static void launch_gated(const LinTokArgs& a, hipStream_t s) {
+  linear_tokens_kernel<T, NW, 2, kLinGated><<<dim3((unsigned)(a.seg[0].n / 16)), dim3(64 * NW), 0, s>>>(a);
 }
 
 template <typename T>
@@ -237,11 +249,21 @@ static void launch_segments_k(const LinTokArgs& a, int64_t K, int tiles, bool wi
 }
 
 template <typename T>
-static void launch_chunks_k(const LinTokArgs& a, int64_t chunk_k, int chunks, bool sq, hipStream_t s) {
+static void launch_chunks_k(const LinTokArgs& a, int64_t chunk_k, int chunks, hipStream_t s) {
   switch (chunk_k) {
-    case 256: launch_chunks<T, 1>(a, chunks, sq, s); break;
-    case 512: launch_chunks<T, 2>(a, chunks, sq, s); break;
-    default: launch_chunks<T, 4>(a, chunks, sq, s); break;
+    case 256: launch_chunks<T, 1>(a, chunks, s); break;
+    case 512: launch_chunks<T, 2>(a, chunks, s); break;
+    default: launch_chunks<T, 4>(a, chunks, s); break;
+  }
+}
+
+template <typename T>
+static void launch_gated_k(const LinTokArgs& a, int64_t K, hipStream_t s) {
+  switch (K) {
+    case 256: launch_gated<T, 1>(a, s); break;
+    case 512: launch_gated<T, 2>(a, s); break;
+    case 1024: launch_gated<T, 4>(a, s); break;
+    default: launch_gated<T, 8>(a, s); break;
   }
 }
 
@@ -322,9 +344,35 @@ extern "C" int atma_linear_tokens(const void* x, int64_t ldx, const void* w, int
   return atma_linear_tokens_multi(x, ldx, M, K, 1, &w, &ldw, &bias, &y, &ldy, &N, dtype, stream);
 }
 
+extern "C" int atma_linear_tokens_gated(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias,
+                                        void* y, int64_t ldy, int64_t M, int64_t H, int64_t K, int dtype,
+                                        void* stream) {
+  using namespace atma;
+  if (!lin_common_ok(M, dtype) || !lin_k_ok(K, kLinMaxWaves) || H < 16 || H % 16 || H > (1 << 23))
+    return set_error(ATMA_ERR_UNSUPPORTED,
+                     "linear_tokens_gated: unsupported shape M=%lld H=%lld K=%lld dtype=%d (16-bit, 1 <= M <= 32, "
+                     "H %% 16 == 0, K 256, 512, 1024 or 2048)",
+                     (long long)M, (long long)H, (long long)K, dtype);
+  if (!x || !w || !y) return set_error(ATMA_ERR_INVALID, "linear_tokens_gated: null pointer");
+  if ((uintptr_t)x % 16 || ldx % 8 || ldx < K || (uintptr_t)w % 16 || ldw % 8 || ldw < K || (uintptr_t)y % 8 ||
+      ldy % 4 || ldy < H || (bias && (uintptr_t)bias % 2))
+    return set_error(ATMA_ERR_INVALID,
+                     "linear_tokens_gated: x / w rows must be 16-byte aligned and y rows 8-byte aligned");
+  LinTokArgs a{};
+  a.x = x;
+  a.ldx = ldx;
+  a.M = (int)M;
+  a.n_segs = 1;
+  a.seg[0] = LinSeg{w, ldw, bias, y, ldy, (int)H, 0};
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == ATMA_BF16) launch_gated_k<bf16>(a, K, st);
+  else launch_gated_k<f16>(a, K, st);
+  return check_launch("linear_tokens_gated");
+}
+
 extern "C" int atma_linear_tokens_chunks(const void* x, int64_t ldx, int64_t M, int64_t chunk_k, int64_t n_chunks,
-                                         const void* const* w, const int64_t* ldw, int64_t N,
-                                         int64_t gate_off, float* parts, int dtype, void* stream) {
+                                         const void* const* w, const int64_t* ldw, int64_t N, float* parts,
+                                         int dtype, void* stream) {
   using namespace atma;
   if (!lin_common_ok(M, dtype) || !lin_k_ok(chunk_k, 4) || n_chunks < 1 || n_chunks > kLinMaxChunks || N < 4 ||
       N % 4 || N > (1 << 24))
@@ -333,17 +381,14 @@ extern "C" int atma_linear_tokens_chunks(const void* x, int64_t ldx, int64_t M, 
                      "(16-bit, 1 <= M <= 32, 1 to %d chunks of K 256, 512 or 1024, N %% 4 == 0)",
                      (long long)M, (long long)chunk_k, (long long)n_chunks, (long long)N, dtype, kLinMaxChunks);
   if (!x || !w || !ldw || !parts) return set_error(ATMA_ERR_INVALID, "linear_tokens_chunks: null pointer");
-  const int64_t width = n_chunks * chunk_k + gate_off;
-  if ((uintptr_t)x % 16 || ldx % 8 || ldx < width || gate_off < 0 || gate_off % 8 || (uintptr_t)parts % 16)
+  if ((uintptr_t)x % 16 || ldx % 8 || ldx < n_chunks * chunk_k || (uintptr_t)parts % 16)
     return set_error(ATMA_ERR_INVALID,
-                     "linear_tokens_chunks: x rows must be 16-byte aligned and hold every chunk (and gate); "
-                     "parts 16-byte aligned");
+                     "linear_tokens_chunks: x rows must be 16-byte aligned and hold every chunk; parts 16-byte aligned");
   LinTokArgs a{};
   a.x = x;
   a.ldx = ldx;
   a.M = (int)M;
   a.N = (int)N;
-  a.gate_off = gate_off;
   a.parts = parts;
   for (int c = 0; c < n_chunks; ++c) {
     if (!w[c] || (uintptr_t)w[c] % 16 || ldw[c] % 8 || ldw[c] < chunk_k)
@@ -352,7 +397,7 @@ extern "C" int atma_linear_tokens_chunks(const void* x, int64_t ldx, int64_t M, 
     a.cldw[c] = ldw[c];
   }
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == ATMA_BF16) launch_chunks_k<bf16>(a, chunk_k, (int)n_chunks, gate_off > 0, st);
-  else launch_chunks_k<f16>(a, chunk_k, (int)n_chunks, gate_off > 0, st);
+  if (dtype == ATMA_BF16) launch_chunks_k<bf16>(a, chunk_k, (int)n_chunks, st);
+  else launch_chunks_k<f16>(a, chunk_k, (int)n_chunks, st);
   return check_launch("linear_tokens_chunks");
 }

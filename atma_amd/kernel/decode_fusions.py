@@ -3,7 +3,8 @@
 A decode step pushes one token per sequence through every block; at 32 sequences each
 kernel moves a few hundred KB, and a launch costs more than its memory traffic.  These
 entry points replace chains of small launches with one each (C ABI
-``atma_linear_tokens_multi``, ``atma_linear_tokens_chunks``, ``atma_residual_rms_norm``,
+``atma_linear_tokens_multi``, ``atma_linear_tokens_gated``, ``atma_linear_tokens_chunks``,
+``atma_residual_rms_norm``,
 ``atma_lfm2_conv_step``, ``atma_global_decode_prep``, ``atma_global_decode_gate``).
 None has a reference counterpart: they are the engine's own compositions of the
 reference's decode arithmetic (``inference/models/atma.py:546-713``), with its eager
@@ -112,19 +113,40 @@ def chunk_width(in_features):
 
 
 @torch.no_grad()
-def linear_tokens_chunks(x, weights, chunk_k, sq_relu_gate=False):
+def linear_tokens_gated(x, weight, bias=None):
+    """The MLP's first projection with its activation: ``a, gate = F.linear(x, weight,
+    bias).chunk(2, -1)`` then ``squared_relu_gate(a, gate)`` in one launch, the 2H-wide
+    projection never written.  x (M, K), M <= 32, K in {256, 512, 1024, 2048}; weight
+    (2H, K), H % 16 == 0.  Returns (M, H) in x's dtype, equal to that chain wherever the
+    projections round alike."""
+    _rows(x, "x")
+    _rows(weight, "weight")
+    M, K = x.shape
+    H = weight.shape[0] // 2
+    if x.dtype not in _DT or not 1 <= M <= 32 or K not in (256, 512, 1024, 2048) or weight.shape != (2 * H, K) \
+            or H % 16 or weight.dtype != x.dtype or (bias is not None and (bias.shape != (2 * H,) or bias.dtype != x.dtype)):
+        raise ValueError(f"linear_tokens_gated: unsupported x {tuple(x.shape)} {x.dtype}, weight {tuple(weight.shape)}")
+    _contig_cuda(x, weight)
+    b = None if bias is None else bias.contiguous()
+    y = torch.empty((M, H), device=x.device, dtype=x.dtype)
+    rc = _lib.load().atma_linear_tokens_gated(x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
+                                              _lib.ptr(b), y.data_ptr(), y.stride(0), M, H, K,
+                                              _lib.dtype_code(x.dtype), _lib.stream_handle(x.device))
+    _lib.check(rc, "linear_tokens_gated")
+    return y
+
+
+@torch.no_grad()
+def linear_tokens_chunks(x, weights, chunk_k):
     """fp32 partial products ``parts[c] = X_c @ weights[c].T`` (C, M, N) where X_c is
-    columns [c chunk_k, (c + 1) chunk_k) of x -- or, with ``sq_relu_gate``, of
-    ``gate * relu(a)^2`` with a = x[:, :W], gate = x[:, W:], W = C chunk_k (the MLP's
-    activation, formed as it loads).  weights[c]: (N, chunk_k) with unit inner stride
-    (slices of one weight matrix are fine).  No bias: the consumer adds it."""
+    columns [c chunk_k, (c + 1) chunk_k) of x.  weights[c]: (N, chunk_k) with unit inner
+    stride (slices of one weight matrix are fine).  No bias: the consumer adds it."""
     _rows(x, "x")
     M = x.shape[0]
     C = len(weights)
     N = weights[0].shape[0]
-    width = C * chunk_k * (2 if sq_relu_gate else 1)
     if x.dtype not in _DT or not 1 <= M <= 32 or chunk_k not in (256, 512, 1024) or not 1 <= C <= 8 \
-            or N % 4 or x.shape[1] < width:
+            or N % 4 or x.shape[1] < C * chunk_k:
         raise ValueError(f"linear_tokens_chunks: unsupported x {tuple(x.shape)} {x.dtype}, {C} chunks of "
                          f"{chunk_k} -> {N}")
     for w in weights:
@@ -136,8 +158,8 @@ def linear_tokens_chunks(x, weights, chunk_k, sq_relu_gate=False):
     _w, pw = _addr(ctypes.c_void_p, [w.data_ptr() for w in weights])
     _lw, plw = _addr(ctypes.c_int64, [w.stride(0) for w in weights])
     rc = _lib.load().atma_linear_tokens_chunks(x.data_ptr(), x.stride(0), M, chunk_k, C, pw, plw, N,
-                                               C * chunk_k if sq_relu_gate else 0, parts.data_ptr(),
-                                               _lib.dtype_code(x.dtype), _lib.stream_handle(x.device))
+                                               parts.data_ptr(), _lib.dtype_code(x.dtype),
+                                               _lib.stream_handle(x.device))
     _lib.check(rc, "linear_tokens_chunks")
     return parts
 

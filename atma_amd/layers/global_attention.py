@@ -42,7 +42,8 @@ from ..kernel import (StartSignal, causal_conv1d_decode_step, chunk_gated_delta_
                       polar_attention_decode, polar_attention_fwd, polar_attention_packed_fwd,
                       recurrence_pays_to_overlap)
 from ..kernel.decode_fusions import (PartialSums, chunk_width, global_decode_gate, global_decode_prep,
-                                     linear_tokens_chunks, linear_tokens_multi, linear_tokens_multi_supported,
+                                     linear_tokens_chunks, linear_tokens_gated, linear_tokens_multi,
+                                     linear_tokens_multi_supported,
                                      residual_rms_norm, residual_rms_norm_supported)
 from ..kernel.inference_ops import (linear_tokens, linear_tokens_supported, packed_causal_conv1d,
                                      squared_relu_gate)
@@ -567,18 +568,17 @@ class MLP(nn.Module):
         self.proj = Linear(4 * dim, dim)
 
     def forward(self, x, defer=False):
-        """``defer`` (decode rows only): return the down projection as fp32 partial sums
-        (``PartialSums``) for the next ``RMSNorm.add_norm`` to finish -- the activation is
-        formed inside the projection's loads (``linear_tokens_chunks``), and the 4x-wide
-        projection spreads over 4x the workgroups."""
+        """``defer`` (decode rows only): the activation is formed in the first projection's
+        epilogue (``linear_tokens_gated``) and the down projection returned as fp32 partial
+        sums (``PartialSums``, K split over 4x the workgroups) for the next
+        ``RMSNorm.add_norm`` to finish."""
         if defer and decode_rows(x):
             dim, hidden = self.proj.weight.shape
             ck = chunk_width(hidden)
             if ck is not None and linear_tokens_supported(x.shape[0], self.fc.weight.shape[0], x.shape[1], x.dtype):
-                y = linear_tokens(x, self.fc.weight, self.fc.bias)
+                h = linear_tokens_gated(x, self.fc.weight, self.fc.bias)
                 w = self.proj.weight
-                parts = linear_tokens_chunks(y, [w[:, c * ck:(c + 1) * ck] for c in range(hidden // ck)], ck,
-                                             sq_relu_gate=True)
+                parts = linear_tokens_chunks(h, [w[:, c * ck:(c + 1) * ck] for c in range(hidden // ck)], ck)
                 return PartialSums(parts, [self.proj.bias], dtype=x.dtype)
         a, gate = torch.chunk(self.fc(x), 2, dim=-1)
         if x.is_cuda and not torch.is_grad_enabled():

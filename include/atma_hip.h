@@ -513,17 +513,25 @@ int atma_linear_tokens_multi(const void* x, int64_t ldx, int64_t M, int64_t K, i
                              const int64_t* ldy, const int64_t* n, int dtype, void* stream);
 
 /*
+ * The MLP's first projection with its activation (model/layers.py:19-31; no reference
+ * counterpart as one call): with w (2H, K) -- the a rows, then the gate rows -- and bias
+ * (2H,) or NULL, y[m, n] = gate * relu(a)^2 for a = round(x[m] . w[n] + bias[n]),
+ * gate = round(x[m] . w[H + n] + bias[H + n]), n < H, in squared_relu_gate's arithmetic.
+ * H % 16 == 0; K, M and alignment as atma_linear_tokens.
+ */
+int atma_linear_tokens_gated(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias, void* y,
+                             int64_t ldy, int64_t M, int64_t H, int64_t K, int dtype, void* stream);
+
+/*
  * K split across workgroups, fp32 partial sums out (no reference counterpart; the decode
  * step's 4096-wide MLP projection and the global layer's two output projections):
- * parts[c][m][n] = sum_{k < chunk_k} X_c[m, k] w[c][n, k] for c < n_chunks (<= 8), where
- * X_c[m, k] = x[m, c chunk_k + k] when gate_off == 0, and with gate_off > 0
- * X_c[m, k] = gate * relu(a)^2 of a = x[m, c chunk_k + k], gate = x[m, gate_off +
- * c chunk_k + k] (squared_relu_gate's arithmetic, rounded to 16 bits).  chunk_k 256, 512
- * or 1024; parts (n_chunks, M, N) fp32 contiguous, 16-byte aligned; N % 4 == 0; no bias.
+ * parts[c][m][n] = sum_{k < chunk_k} x[m, c chunk_k + k] w[c][n, k] for c < n_chunks
+ * (<= 8).  chunk_k 256, 512 or 1024; parts (n_chunks, M, N) fp32 contiguous, 16-byte
+ * aligned; N % 4 == 0; no bias.
  */
 int atma_linear_tokens_chunks(const void* x, int64_t ldx, int64_t M, int64_t chunk_k, int64_t n_chunks,
-                              const void* const* w, const int64_t* ldw, int64_t N, int64_t gate_off, float* parts,
-                              int dtype, void* stream);
+                              const void* const* w, const int64_t* ldw, int64_t N, float* parts, int dtype,
+                              void* stream);
 
 /*
  * Residual add + RMSNorm of the pre-norm block (inference/models/atma.py:680-713, norm

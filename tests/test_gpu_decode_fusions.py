@@ -4,8 +4,8 @@ replace, run in torch on the same 16-bit inputs:
 
 * ``linear_tokens_multi`` / ``linear_tokens_chunks`` against fp32 ``F.linear`` (fp32
   accumulation: parts within 2e-5 relative of the fp64 product, 16-bit outputs within
-  1e-2, the ``linear_tokens`` bar), the chunks' fused activation against
-  ``squared_relu_gate`` (the same bf16 operand values);
+  1e-2, the ``linear_tokens`` bar); ``linear_tokens_gated`` bit for bit against
+  ``linear_tokens`` then ``squared_relu_gate`` (the same products and roundings);
 * ``residual_rms_norm``: the new stream equal to the eager bf16 add bit for bit (one
   rounding of the same fp32 sum), a branch of partial sums + biases + low-rank term
   within one bf16 ulp of its fp64 sum (one rounding), the normed row within one ulp of
@@ -87,22 +87,26 @@ def test_linear_tokens_chunks_vs_fp64(dev, M, chunk_k, C):
         assert rel_err(parts[c], ref) <= 2e-5
 
 
+@pytest.mark.parametrize("K", [256, 1024, 2048])
 @pytest.mark.parametrize("M", [1, 32])
-def test_linear_tokens_chunks_squared_relu_gate(dev, M):
-    """The MLP's down projection with the activation formed on load equals
-    ``squared_relu_gate`` then the chunked product (same bf16 operands)."""
-    from atma_amd.kernel import squared_relu_gate
-    from atma_amd.kernel.decode_fusions import linear_tokens_chunks
-    g = _g(dev, 40 + M)
-    dim, hidden = 1024, 4096
-    y = torch.randn(M, 2 * hidden, device=dev, generator=g).to(BF)
-    w = (torch.randn(dim, hidden, device=dev, generator=g) * 0.02).to(BF)
-    parts = linear_tokens_chunks(y, [w[:, c * 1024:(c + 1) * 1024] for c in range(4)], 1024, sq_relu_gate=True)
-    h = squared_relu_gate(y[:, :hidden], y[:, hidden:])
-    ref = h.double() @ w.double().t()
-    assert rel_err(parts.sum(0), ref) <= 2e-5
-    eager = (y[:, hidden:] * y[:, :hidden].relu().square())
-    assert torch.equal(h, eager)
+def test_linear_tokens_gated_equals_projection_then_activation(dev, M, K):
+    """The MLP's first projection with the activation in its epilogue equals
+    ``linear_tokens`` (same products, same rounding) followed by ``squared_relu_gate``."""
+    from atma_amd.kernel import linear_tokens, squared_relu_gate
+    from atma_amd.kernel.decode_fusions import linear_tokens_gated
+    g = _g(dev, 40 + M + K)
+    H = 4096 if K == 1024 else 1024
+    x = torch.randn(M, K, device=dev, generator=g).to(BF)
+    w = (torch.randn(2 * H, K, device=dev, generator=g) * 0.03).to(BF)
+    b = (torch.randn(2 * H, device=dev, generator=g) * 0.1).to(BF)
+    h = linear_tokens_gated(x, w, b)
+    y = F.linear(x.float(), w.float(), b.float())
+    ref = squared_relu_gate(y[:, :H].to(BF), y[:, H:].to(BF))
+    assert rel_err(h, ref) <= 1e-2
+    yk = linear_tokens(x, w, b)
+    assert torch.equal(h, squared_relu_gate(yk[:, :H], yk[:, H:]))     # bitwise, same products
+    eager = yk[:, H:] * yk[:, :H].relu().square()
+    assert torch.equal(squared_relu_gate(yk[:, :H], yk[:, H:]), eager)
 
 
 def test_linear_tokens_chunks_rejects(dev):
