@@ -448,7 +448,10 @@ def bench_c5(torch, dev, n_prompts=32, prompt_len=2048, new_tokens=256, seed=0):
     prompts prefill as one dense batch; decode replays the captured HIP graph.  Prefill and
     decode tok/s are the engine's own (HIP events around each step, as the reference's
     LLMEngine.generate); wall_s is the whole timed generate.  A short untimed generate on
-    the same prompts runs first (kernel and library warm-up at the full prefill shape)."""
+    the same prompts runs first (kernel and library warm-up at the full prefill shape).
+    decode_ms_per_step is the served step (host scheduling, input staging, the graph, the
+    token sync); decode_graph_ms the graph alone; decode_hbm_frac each over 8 TB/s for the
+    step's algorithmic bytes (``_c5_decode_bytes`` at the run's mean context)."""
     from atma_amd.engine import AtmaConfig, Config, LLMEngine, SamplingParams
     pages = (prompt_len + new_tokens + 255) // 256
     cfg = Config(kvcache_block_size=256, max_num_seqs=n_prompts, max_num_batched_tokens=n_prompts * prompt_len,
@@ -466,16 +469,47 @@ def bench_c5(torch, dev, n_prompts=32, prompt_len=2048, new_tokens=256, seed=0):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     m = engine.last_metrics
-    n_params = sum(p.numel() for p in engine.model_runner.model.parameters())
+    mr = engine.model_runner
+    n_params = sum(p.numel() for p in mr.model.parameters())
     assert all(len(r["token_ids"]) == new_tokens for r in res)
+    # the device time of one decode step alone: the bucket-32 graph (model, LM head,
+    # greedy pick) replayed back to back on the last step's inputs (every request has
+    # finished: the replays write only into freed pages and table rows)
+    graph = mr.graphs[n_prompts][0]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    graph.replay()
+    e0.record()
+    for _ in range(20):
+        graph.replay()
+    e1.record()
+    e1.synchronize()
+    graph_ms = e0.elapsed_time(e1) / 20
     engine.exit()
     del engine
     torch.cuda.empty_cache()
+    step_ms = m["decode_time"] * 1e3 / max(1, m["decode_tokens"] // n_prompts)
+    step_bytes = _c5_decode_bytes(cfg.hf_config, n_params, n_prompts, prompt_len + (new_tokens + 1) / 2)
     return {"model_params": n_params, "requests": n_prompts, "prompt_len": prompt_len, "new_tokens": new_tokens,
             "prefill_tok_s": m["prefill_throughput"], "decode_tok_s": m["decode_throughput"],
-            "prefill_ms": m["prefill_time"] * 1e3, "decode_ms_per_step": m["decode_time"] * 1e3 /
-            max(1, m["decode_tokens"] // n_prompts), "wall_s": wall, "init_s": t_init,
+            "prefill_ms": m["prefill_time"] * 1e3, "decode_ms_per_step": step_ms,
+            "decode_graph_ms": graph_ms, "decode_bytes_per_step": step_bytes,
+            "decode_hbm_frac": step_bytes / (step_ms * 1e-3) / 8e12,
+            "decode_graph_hbm_frac": step_bytes / (graph_ms * 1e-3) / 8e12,
+            "wall_s": wall, "init_s": t_init,
             "prefill_tokens": m["prefill_tokens"], "decode_tokens": m["decode_tokens"]}
+
+
+def _c5_decode_bytes(hf, n_params, n_seqs, avg_context):
+    """Algorithmic HBM bytes of one decode step of the served model: every weight but the
+    embedding table once (16-bit), each sequence's KV cache over its context once in every
+    global layer, and the memory state read and written (fp32) -- the conv tails, token
+    rows and activations are below 0.1% of it and left out."""
+    item = 2
+    n_global = sum(hf.is_attention_layer(i) for i in range(hf.num_hidden_layers))
+    weights = (n_params - hf.vocab_size * hf.hidden_size) * item
+    kv = n_seqs * avg_context * hf.num_key_value_heads * hf.head_dim * 2 * item * n_global
+    mem = n_seqs * hf.num_attention_heads * hf.head_dim * hf.head_dim * 4 * 2 * n_global if hf.mem_enabled else 0
+    return int(weights + kv + mem)
 
 
 def _cpu_model():
