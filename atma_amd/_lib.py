@@ -76,6 +76,11 @@ SIGNATURES = {
                                        _p, _i64, _i64, _p, _p, _p, _p, _p, _p, _f32, _f32, _f32, _i64, _i64,
                                        _i64, _i64, _i32, _p]),
     "atma_global_decode_gate": (_i32, [_p, _p, _p, _i64, _i64, _p, _i64, _f32, _i64, _i64, _i64, _i32, _p]),
+    "atma_head_rms_norm": (_i32, [_p, _i64, _i64, _p, _i64, _i64, _i64, _f32, _i32, _p]),
+    "atma_global_gate": (_i32, [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i32, _p, _i64, _p, _i64,
+                                _p, _i64, _i64, _i64, _i64, _f32, _i32, _p]),
+    "atma_lfm2_conv_packed": (_i32, [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _i64, _p, _p, _p, _i64, _i64,
+                                     _i32, _p]),
     "atma_packed_causal_conv1d": (_i32, [
         _p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _i64, _i64, _i64,
         _i32, _i32, _p]),

@@ -13,9 +13,8 @@
 //  * global_decode_prep: the global layer's per-head RMSNorm of q and k, Canon residual
 //    convs of q / k / v (inference/models/atma.py:546-575) and the memory gates
 //    (model/blocks.py:426-490) from one row of its fused input projection.
-//  * global_decode_gate: the two gated inputs of the global layer's output projections,
-//    c * sigmoid(gate) (inference/models/atma.py:246-252) and
-//    RMSNorm(r) * sigmoid(mem_gate) (model/blocks.py:470-490).
+//  (the gated inputs of the global layer's output projections, global_decode_gate, are
+//  layer_fusions.hip's global_gate at one token per sequence)
 //
 // All are latency-bound at decode sizes (a few KB per row); a row is one wave (64 lanes,
 // 8 contiguous 16-bit values per lane per pass), reductions stay inside the wave.
@@ -23,8 +22,6 @@
 #include "gated_delta.h"
 
 namespace atma {
-
-__device__ __forceinline__ float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
 
 template <typename T>
 __device__ __forceinline__ void store8(T* p, const float* v) {
@@ -79,11 +76,12 @@ __global__ void __launch_bounds__(256) residual_rms_norm_kernel(ResNormArgs a) {
   const int lane = threadIdx.x & 63;
   const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (m >= a.M) return;
-  float mu[MU > 0 ? MU : 1];
+  // the low-rank term's inputs of this row as packed 16-bit pairs (v_dot2 operands)
+  uint32_t mu2[MU > 0 ? MU / 2 : 1];
   if constexpr (MU > 0) {
-    const T* mx = (const T*)a.mu_x + (int64_t)m * a.ldmu;
+    const uint32_t* mx = (const uint32_t*)((const T*)a.mu_x + (int64_t)m * a.ldmu);
 #pragma unroll
-    for (int h = 0; h < MU; ++h) mu[h] = to_f32(mx[h]);
+    for (int i = 0; i < MU / 2; ++i) mu2[i] = mx[i];
   }
   float s[P][8];
   u32x4 wv[P];
@@ -97,27 +95,31 @@ __global__ void __launch_bounds__(256) residual_rms_norm_kernel(ResNormArgs a) {
     u32x4 rv = {0u, 0u, 0u, 0u};
     if (a.res) rv = *(const u32x4*)((const T*)a.res + (int64_t)m * a.ldr + cc);
     float br[8];
-    if (a.y) {
-      unpack8<T>(*(const u32x4*)((const T*)a.y + (int64_t)m * a.ldy + cc), br);
-    } else {
-      f32x4 pv[kResMaxParts][2];
+    // the branch: a 16-bit tensor or the fp32 partial sums, plus the biases and the
+    // low-rank term (fp32), rounded once whenever anything was added in fp32
+    u32x4 yv = {0u, 0u, 0u, 0u};
+    if (a.y) yv = *(const u32x4*)((const T*)a.y + (int64_t)m * a.ldy + cc);
+    f32x4 pv[kResMaxParts][2];
 #pragma unroll
-      for (int q = 0; q < kResMaxParts; ++q)
-        if (q < a.n_parts) {
-          const float* pp = a.parts + ((int64_t)q * a.M + m) * a.D + cc;
-          pv[q][0] = ld4(pp);
-          pv[q][1] = ld4(pp + 4);
-        }
-      u32x4 bv[kResMaxBias];
-#pragma unroll
-      for (int b = 0; b < kResMaxBias; ++b)
-        if (b < a.n_bias) bv[b] = *(const u32x4*)((const T*)a.bias[b] + cc);
-      u32x4 mwv[MU > 0 ? MU : 1];
-      if constexpr (MU > 0) {
-        // rows cc .. cc + 7 of mu_w (D, MU): 8 MU contiguous values, MU 16-byte vectors
-#pragma unroll
-        for (int i = 0; i < MU; ++i) mwv[i] = *(const u32x4*)((const T*)a.mu_w + (int64_t)cc * MU + 8 * i);
+    for (int q = 0; q < kResMaxParts; ++q)
+      if (q < a.n_parts) {
+        const float* pp = a.parts + ((int64_t)q * a.M + m) * a.D + cc;
+        pv[q][0] = ld4(pp);
+        pv[q][1] = ld4(pp + 4);
       }
+    u32x4 bv[kResMaxBias];
+#pragma unroll
+    for (int b = 0; b < kResMaxBias; ++b)
+      if (b < a.n_bias) bv[b] = *(const u32x4*)((const T*)a.bias[b] + cc);
+    u32x4 mwv[MU > 0 ? MU : 1];
+    if constexpr (MU > 0) {
+      // rows cc .. cc + 7 of mu_w (D, MU): 8 MU contiguous values, MU 16-byte vectors
+#pragma unroll
+      for (int i = 0; i < MU; ++i) mwv[i] = *(const u32x4*)((const T*)a.mu_w + (int64_t)cc * MU + 8 * i);
+    }
+    if (a.y) {
+      unpack8<T>(yv, br);
+    } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) br[e] = pv[0][e >> 2][e & 3];
 #pragma unroll
@@ -126,21 +128,27 @@ __global__ void __launch_bounds__(256) residual_rms_norm_kernel(ResNormArgs a) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) br[e] += pv[q][e >> 2][e & 3];
         }
+    }
 #pragma unroll
-      for (int b = 0; b < kResMaxBias; ++b)
-        if (b < a.n_bias) {
+    for (int b = 0; b < kResMaxBias; ++b)
+      if (b < a.n_bias) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) br[e] += elem16<T>(bv[b], e);
-        }
-      if constexpr (MU > 0) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float acc = 0.f;
-#pragma unroll
-          for (int h = 0; h < MU; ++h) acc += mu[h] * elem16<T>(mwv[(e * MU + h) >> 3], (e * MU + h) & 7);
-          br[e] += acc;
-        }
+        for (int e = 0; e < 8; ++e) br[e] += elem16<T>(bv[b], e);
       }
+    if constexpr (MU > 0) {
+      // element e's MU weights are words e MU / 2 .. e MU / 2 + MU / 2 - 1 of the block
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < MU / 2; ++i) {
+          const int wd = e * (MU / 2) + i;
+          acc = dot2<T>(mwv[wd >> 2][wd & 3], mu2[i], acc);
+        }
+        br[e] += acc;
+      }
+    }
+    if (!a.y || a.n_bias > 0 || MU > 0) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) br[e] = rnd<T>(br[e]);
     }
@@ -307,49 +315,6 @@ __global__ void __launch_bounds__(64) global_decode_prep_kernel(GlobalPrepArgs a
   }
 }
 
-// ------------------------------------------------------------------ global_decode_gate
-struct GlobalGateArgs {
-  const void* c;  // (B, H, d) T
-  const float* r;  // (B, H, d) fp32 memory readout, or null (no memory branch)
-  const void* y;   // fused projection rows: the output gate of head h at h 2 d + d, the memory gate at cm + h d
-  int64_t ldy, cm;
-  void* x2;  // (B, ldx2): c * sigmoid(gate) at column h d, RMSNorm(r) * sigmoid(mem_gate) at H d + h d
-  int64_t ldx2;
-  float mem_eps;
-  int B, H, d;
-};
-
-template <typename T, int CPL>
-__global__ void __launch_bounds__(64) global_decode_gate_kernel(GlobalGateArgs a) {
-  const int lane = threadIdx.x;
-  const int b = blockIdx.x, h = blockIdx.y;
-  const T* row = (const T*)a.y + (int64_t)b * a.ldy;
-  const T* c = (const T*)a.c + ((int64_t)b * a.H + h) * a.d;
-  T* x2 = (T*)a.x2 + (int64_t)b * a.ldx2;
-#pragma unroll
-  for (int i = 0; i < CPL; ++i) {
-    const int e = i * 64 + lane;
-    const float sg = rnd<T>(sigmoid_f(to_f32(row[(int64_t)h * 2 * a.d + a.d + e])));
-    x2[h * a.d + e] = from_f32<T>(to_f32(c[e]) * sg);
-  }
-  if (!a.r) return;
-  const float* r = a.r + ((int64_t)b * a.H + h) * a.d;
-  float rv[CPL];
-  float ss = 0.f;
-#pragma unroll
-  for (int i = 0; i < CPL; ++i) {
-    rv[i] = r[i * 64 + lane];
-    ss += rv[i] * rv[i];
-  }
-  const float rstd = rsqrtf(wave_sum(ss) / (float)a.d + a.mem_eps);
-#pragma unroll
-  for (int i = 0; i < CPL; ++i) {
-    const int e = i * 64 + lane;
-    const float sg = rnd<T>(sigmoid_f(to_f32(row[a.cm + (int64_t)h * a.d + e])));
-    x2[(int64_t)a.H * a.d + h * a.d + e] = from_f32<T>(rnd<T>(rv[i] * rstd) * sg);
-  }
-}
-
 }  // namespace atma
 
 // ---------------------------------------------------------------------------- C ABI
@@ -368,12 +333,13 @@ extern "C" int atma_residual_rms_norm(const void* y, int64_t ldy, const float* p
   if (M == 0) return ATMA_OK;
   if (!weight || !out || (!y && !parts) || (y && parts))
     return set_error(ATMA_ERR_INVALID, "residual_rms_norm: need weight, out and exactly one of y / parts");
-  if (parts && (n_parts < 1 || n_parts > kResMaxParts || n_bias < 0 || n_bias > kResMaxBias || (n_bias && !bias)))
+  if ((parts && (n_parts < 1 || n_parts > kResMaxParts)) || n_bias < 0 || n_bias > kResMaxBias || (n_bias && !bias))
     return set_error(ATMA_ERR_INVALID, "residual_rms_norm: 1 to %d parts and at most %d biases", kResMaxParts,
                      kResMaxBias);
-  if (mu_x && (!parts || !mu_w || (mu_k != 4 && mu_k != 8 && mu_k != 16) || ldmu < mu_k || ((uintptr_t)mu_w & 15)))
-    return set_error(ATMA_ERR_INVALID,
-                     "residual_rms_norm: the low-rank term needs parts and a 16-byte aligned mu_w of width 4, 8 or 16");
+  if (mu_x && (!mu_w || (mu_k != 4 && mu_k != 8 && mu_k != 16) || ldmu < mu_k || ldmu % 2 || ((uintptr_t)mu_x & 3) ||
+               ((uintptr_t)mu_w & 15)))
+    return set_error(ATMA_ERR_INVALID, "residual_rms_norm: the low-rank term needs a 16-byte aligned mu_w of width 4, 8 "
+                     "or 16");
   auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
   if ((y && (!al16(y) || ldy % 8 || ldy < D)) || (parts && !al16(parts)) || (res && (!al16(res) || ldr % 8 || ldr < D)) ||
       (res_out && (!al16(res_out) || ldro % 8 || ldro < D)) || !al16(weight) || !al16(out) || ldo % 8 || ldo < D)
@@ -383,7 +349,7 @@ extern "C" int atma_residual_rms_norm(const void* y, int64_t ldy, const float* p
   a.ldy = ldy;
   a.parts = parts;
   a.n_parts = parts ? (int)n_parts : 0;
-  a.n_bias = parts ? (int)n_bias : 0;
+  a.n_bias = (int)n_bias;
   for (int i = 0; i < a.n_bias; ++i) {
     if (!bias[i] || !al16(bias[i])) return set_error(ATMA_ERR_INVALID, "residual_rms_norm: bias %d null or unaligned", i);
     a.bias[i] = bias[i];
@@ -460,28 +426,4 @@ extern "C" int atma_global_decode_prep(const void* y, int64_t ldy, int64_t ck, i
     else global_decode_prep_kernel<f16, 1><<<grid, dim3(64), 0, s>>>(a);
   }
   return check_launch("global_decode_prep");
-}
-
-extern "C" int atma_global_decode_gate(const void* c, const float* r, const void* y, int64_t ldy, int64_t cm,
-                                       void* x2, int64_t ldx2, float mem_eps, int64_t B, int64_t H, int64_t d,
-                                       int dtype, void* stream) {
-  if (dtype != ATMA_BF16 && dtype != ATMA_F16)
-    return set_error(ATMA_ERR_UNSUPPORTED, "global_decode_gate: 16-bit only (dtype %d)", dtype);
-  if (B < 0 || H < 1 || (d != 64 && d != 128) || B > 0x7fffffff || H > 64)
-    return set_error(ATMA_ERR_INVALID, "global_decode_gate: bad sizes (d 64 or 128)");
-  if (B == 0) return ATMA_OK;
-  if (!c || !y || !x2) return set_error(ATMA_ERR_INVALID, "global_decode_gate: null pointer");
-  if (ldy < 2 * H * d || (r && (cm < 0 || cm + H * d > ldy)) || ldx2 < (r ? 2 : 1) * H * d)
-    return set_error(ATMA_ERR_INVALID, "global_decode_gate: column offsets outside the rows");
-  GlobalGateArgs a{c, r, y, ldy, cm, x2, ldx2, mem_eps, (int)B, (int)H, (int)d};
-  const dim3 grid((unsigned)B, (unsigned)H);
-  hipStream_t s = (hipStream_t)stream;
-  if (dtype == ATMA_BF16) {
-    if (d == 128) global_decode_gate_kernel<bf16, 2><<<grid, dim3(64), 0, s>>>(a);
-    else global_decode_gate_kernel<bf16, 1><<<grid, dim3(64), 0, s>>>(a);
-  } else {
-    if (d == 128) global_decode_gate_kernel<f16, 2><<<grid, dim3(64), 0, s>>>(a);
-    else global_decode_gate_kernel<f16, 1><<<grid, dim3(64), 0, s>>>(a);
-  }
-  return check_launch("global_decode_gate");
 }

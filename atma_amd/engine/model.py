@@ -21,7 +21,8 @@ import torch.nn.functional as F
 from torch import nn
 
 from ..kernel import causal_conv1d_decode_step, packed_causal_conv1d, softcap_argmax, softcap_logits
-from ..kernel.decode_fusions import lfm2_conv_step, residual_rms_norm_supported
+from ..kernel.decode_fusions import PartialSums, lfm2_conv_step, residual_rms_norm_supported
+from ..kernel.layer_fusions import lfm2_conv_packed
 from ..layers.attention import Attention
 from ..layers.global_attention import MLP, GlobalLayerCache, Linear, PolarAttention, RMSNorm, decode_rows
 from .config import AtmaConfig
@@ -57,12 +58,13 @@ class AtmaAttention(PolarAttention):
                                defer=defer)
         if ctx.dense_prefill:
             B, T = ctx.dense_batch_size, ctx.dense_seq_len
-            return self.prefill(x.view(B, T, -1), cache, ctx.seq_slots, ctx.slot_mapping).reshape(B * T, -1)
+            out = self.prefill(x.view(B, T, -1), cache, ctx.seq_slots, ctx.slot_mapping, defer=defer)
+            return out if isinstance(out, PartialSums) else out.reshape(B * T, -1)
         if ctx.grouped_polar_prefill:
             return self.prefill_packed(
                 x, cache, ctx.seqlens_q, ctx.seq_slots, ctx.slot_mapping,
                 (ctx.polar_tile_seq_starts, ctx.polar_tile_q_starts, ctx.polar_tile_seq_lens),
-                (ctx.token_seq_starts, ctx.token_seq_ends, ctx.token_seq_slots))
+                (ctx.token_seq_starts, ctx.token_seq_ends, ctx.token_seq_slots), defer=defer)
         outs, start = [], 0
         for i, n in enumerate(ctx.seqlens_q):
             seq = ctx.seqs[i]
@@ -91,14 +93,18 @@ class AtmaLFM2Conv(nn.Module):
 
     def forward(self, x, defer=False):
         ctx = get_context()
+        table = ctx.conv_state_tables[f"conv_{self.layer_idx}_gated"]
         if not ctx.is_prefill and decode_rows(x):
             # one launch for b * x, the conv step and c * (.) (lfm2_conv_step)
-            table = ctx.conv_state_tables[f"conv_{self.layer_idx}_gated"]
             return self.out_proj(lfm2_conv_step(self.in_proj(x), self.conv.weight.squeeze(1), ctx.seq_slots, table))
+        if (ctx.is_prefill and ctx.token_seq_starts is not None and x.is_cuda and not torch.is_grad_enabled()
+                and x.dtype in (torch.bfloat16, torch.float16) and x.shape[-1] % 8 == 0 and self.kernel_size in (3, 4)):
+            # fresh prompts: b * x, the packed conv and c * (.) in one launch (lfm2_conv_packed)
+            return self.out_proj(lfm2_conv_packed(self.in_proj(x), self.conv.weight.squeeze(1), table,
+                                                  ctx.token_seq_starts, ctx.token_seq_ends, ctx.token_seq_slots))
         b_gate, c_gate, x_proj = self.in_proj(x).chunk(3, dim=-1)
         xg = b_gate * x_proj
         w = self.conv.weight.squeeze(1)
-        table = ctx.conv_state_tables[f"conv_{self.layer_idx}_gated"]
         if not ctx.is_prefill:
             xc = causal_conv1d_decode_step(xg, w, ctx.seq_slots, table)
         elif ctx.token_seq_starts is not None:        # fresh prompts: one packed launch, tails written

@@ -42,23 +42,26 @@ def _contig_cuda(*ts):
 
 
 class PartialSums:
-    """A projection's output not yet summed: fp32 ``parts`` (P, M, N) from
-    ``linear_tokens_chunks``, plus ``biases`` (each (N,)) and an optional low-rank term
-    ``mu_x @ mu_w.T`` (mu_x (M, k), mu_w (N, k), k <= 16).  ``residual_rms_norm`` adds it
-    to the residual stream in the same launch; ``materialize`` is the same sum in torch
-    (fp32, one rounding)."""
+    """A projection output not yet summed: a 16-bit ``base`` (M, N) or fp32 ``parts``
+    (P, M, N) from ``linear_tokens_chunks``, plus ``biases`` (each (N,)) and an optional
+    low-rank term ``mu_x @ mu_w.T`` (mu_x (M, k), mu_w (N, k), k 4, 8 or 16).
+    ``residual_rms_norm`` adds it to the residual stream in the same launch (fp32, one
+    rounding); ``materialize`` is the same sum in torch."""
 
-    __slots__ = ("parts", "biases", "mu_x", "mu_w", "dtype")
+    __slots__ = ("parts", "base", "biases", "mu_x", "mu_w", "dtype")
 
-    def __init__(self, parts, biases=(), mu_x=None, mu_w=None, dtype=torch.bfloat16):
-        self.parts, self.biases, self.mu_x, self.mu_w, self.dtype = parts, tuple(biases), mu_x, mu_w, dtype
+    def __init__(self, parts, biases=(), mu_x=None, mu_w=None, dtype=torch.bfloat16, base=None):
+        if (parts is None) == (base is None):
+            raise ValueError("PartialSums takes exactly one of parts / base")
+        self.parts, self.base, self.biases, self.mu_x, self.mu_w = parts, base, tuple(biases), mu_x, mu_w
+        self.dtype = dtype
 
     @property
     def shape(self):
-        return self.parts.shape[1:]
+        return self.parts.shape[1:] if self.parts is not None else self.base.shape
 
     def materialize(self):
-        s = self.parts.sum(0)
+        s = self.parts.sum(0) if self.parts is not None else self.base.float()
         for b in self.biases:
             s = s + b.float()
         if self.mu_x is not None:
@@ -177,11 +180,13 @@ def residual_rms_norm(branch, residual, weight, eps):
     ``branch``: (M, D) tensor or ``PartialSums`` (summed in fp32 with its biases and
     low-rank term, rounded once); ``residual`` None starts the stream with the branch.
     Returns (normed (M, D), stream (M, D))."""
-    parts = branch.parts if isinstance(branch, PartialSums) else None
+    ps = branch if isinstance(branch, PartialSums) else None
+    parts = ps.parts if ps is not None else None
+    y = branch if ps is None else ps.base
     dtype = branch.dtype
-    if parts is None:
-        _rows(branch, "branch")
-    M, D = (parts.shape[1], parts.shape[2]) if parts is not None else branch.shape
+    if y is not None:
+        _rows(y, "branch")
+    M, D = (parts.shape[1], parts.shape[2]) if parts is not None else y.shape
     if dtype not in _DT or D % 8 or not 8 <= D <= 4096 or weight.shape != (D,) or weight.dtype != dtype:
         raise ValueError(f"residual_rms_norm: unsupported rows of {D} {dtype}")
     if residual is not None:
@@ -189,30 +194,22 @@ def residual_rms_norm(branch, residual, weight, eps):
         if residual.shape != (M, D) or residual.dtype != dtype:
             raise ValueError("residual_rms_norm: residual must match the branch")
     out = torch.empty((M, D), device=weight.device, dtype=dtype)
-    new_res = branch if (residual is None and parts is None) else torch.empty_like(out)
-    lib = _lib.load()
-    if parts is not None:
-        if not parts.is_contiguous() or parts.dtype != torch.float32:
-            raise ValueError("residual_rms_norm: parts must be contiguous fp32 (P, M, D)")
-        biases = [b.contiguous() for b in branch.biases]
-        _b, pb = _addr(ctypes.c_void_p, [b.data_ptr() for b in biases] or [None])
-        mu_x, mu_w = branch.mu_x, branch.mu_w
-        if mu_x is not None:
-            _rows(mu_x, "mu_x")
-            mu_w = mu_w.contiguous()
-        rc = lib.atma_residual_rms_norm(
-            None, 0, parts.data_ptr(), parts.shape[0], pb, len(biases),
-            None if mu_x is None else mu_x.data_ptr(), 0 if mu_x is None else mu_x.stride(0),
-            None if mu_w is None else mu_w.data_ptr(), 0 if mu_x is None else mu_x.shape[1],
-            _lib.ptr(residual), 0 if residual is None else residual.stride(0), new_res.data_ptr(), new_res.stride(0),
-            weight.data_ptr(), out.data_ptr(), out.stride(0), M, D, float(eps), _lib.dtype_code(dtype),
-            _lib.stream_handle(weight.device))
-    else:
-        rc = lib.atma_residual_rms_norm(
-            branch.data_ptr(), branch.stride(0), None, 0, None, 0, None, 0, None, 0,
-            _lib.ptr(residual), 0 if residual is None else residual.stride(0),
-            None if residual is None else new_res.data_ptr(), new_res.stride(0), weight.data_ptr(),
-            out.data_ptr(), out.stride(0), M, D, float(eps), _lib.dtype_code(dtype), _lib.stream_handle(weight.device))
+    new_res = branch if (residual is None and ps is None) else torch.empty_like(out)
+    if parts is not None and (not parts.is_contiguous() or parts.dtype != torch.float32):
+        raise ValueError("residual_rms_norm: parts must be contiguous fp32 (P, M, D)")
+    biases = [b.contiguous() for b in ps.biases] if ps is not None else []
+    _b, pb = _addr(ctypes.c_void_p, [b.data_ptr() for b in biases] or [None])
+    mu_x = ps.mu_x if ps is not None else None
+    mu_w = None
+    if mu_x is not None:
+        _rows(mu_x, "mu_x")
+        mu_w = ps.mu_w.contiguous()
+    rc = _lib.load().atma_residual_rms_norm(
+        _lib.ptr(y), 0 if y is None else y.stride(0), _lib.ptr(parts), 0 if parts is None else parts.shape[0],
+        pb, len(biases), _lib.ptr(mu_x), 0 if mu_x is None else mu_x.stride(0), _lib.ptr(mu_w),
+        0 if mu_x is None else mu_x.shape[1], _lib.ptr(residual), 0 if residual is None else residual.stride(0),
+        None if new_res is branch else new_res.data_ptr(), new_res.stride(0), weight.data_ptr(),
+        out.data_ptr(), out.stride(0), M, D, float(eps), _lib.dtype_code(dtype), _lib.stream_handle(weight.device))
     _lib.check(rc, "residual_rms_norm")
     return out, new_res
 

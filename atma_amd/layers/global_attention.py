@@ -47,6 +47,7 @@ from ..kernel.decode_fusions import (PartialSums, chunk_width, global_decode_gat
                                      residual_rms_norm, residual_rms_norm_supported)
 from ..kernel.inference_ops import (linear_tokens, linear_tokens_supported, packed_causal_conv1d,
                                      squared_relu_gate)
+from ..kernel.layer_fusions import global_gate, head_rms_norm
 from ..kernel.polar import global_decode_step_supported_shape
 from .attention import store_kvcache
 
@@ -121,14 +122,16 @@ class TitansMemory(nn.Module):
         ``[K, V]`` (B, H, dk, dv) fp32 or None.  ``start_signal``: raised as the recurrence
         kernel starts (the overlapped prefill schedule).  Returns (out (B, T, dim), final
         state or None) -- ``_mem_prefill_dense`` (``inference/models/atma.py:305-339``)."""
-        zg, zb = self.raw_logits(x)   # activations applied inside the prefill's load
-        r, S = chunk_gated_delta_rule(q, k, v, zg, zb, scale=1.0,
-                                      initial_state=initial_state,
-                                      output_final_state=output_final_state,
-                                      use_qk_l2norm_in_kernel=True,
-                                      gate_bias=(self.gamma_bias, self.beta_bias),
-                                      start_signal=start_signal)
+        r, S = self.readout(x, q, k, v, initial_state, output_final_state, start_signal)
         return self._out(x, r), S
+
+    def readout(self, x, q, k, v, initial_state=None, output_final_state=False, start_signal=None):
+        """The recurrence alone: (r (B, T, H, dk) fp32 readout before its norm and gate,
+        final state or None) -- what ``forward`` feeds ``_out``."""
+        zg, zb = self.raw_logits(x)   # activations applied inside the prefill's load
+        return chunk_gated_delta_rule(q, k, v, zg, zb, scale=1.0, initial_state=initial_state,
+                                      output_final_state=output_final_state, use_qk_l2norm_in_kernel=True,
+                                      gate_bias=(self.gamma_bias, self.beta_bias), start_signal=start_signal)
 
     def decode_gates(self, x):
         """(gamma, beta) of one decode step: retention sigmoid(w_gamma x + gamma_bias) and
@@ -223,15 +226,25 @@ class PolarAttention(nn.Module):
             self._pf32_key = key
         return self._pf32
 
+    def _glue_fusable(self, x):
+        """16-bit GPU inference with the memory branch: the per-head glue runs as the
+        layer-fusion kernels (``head_rms_norm``, ``global_gate``)."""
+        return (x.is_cuda and x.dtype in (torch.bfloat16, torch.float16) and not torch.is_grad_enabled()
+                and self.head_dim in (64, 128) and self.mem is not None)
+
     def _project(self, x):
         """q/gate, k, v projections and per-head RMSNorm of q, k (``model/reference.py:131-139``).
-        x: (..., dim) -> q (..., H, dk), gate (..., H*dk), k, v (..., Hkv, dk)."""
+        x: (..., dim) -> q (..., H, dk), gate (..., H, dk) (a view of the q|gate projection),
+        k, v (..., Hkv, dk).  16-bit inference normalises q and k in one pass each, reading
+        q in place (``head_rms_norm``; torch's default eps of the compute type, fp32's)."""
         lead = x.shape[:-1]
         H, Hkv, dk = self.num_heads, self.num_kv_heads, self.head_dim
         q, gate = torch.chunk(self.q(x).view(*lead, H, 2 * dk), 2, dim=-1)
         k = self.k(x).view(*lead, Hkv, dk)
         v = self.v(x).view(*lead, Hkv, dk)
-        return F.rms_norm(q, (dk,)), gate.reshape(*lead, H * dk), F.rms_norm(k, (dk,)), v
+        if self._glue_fusable(x):
+            return head_rms_norm(q, F32_EPS), gate, head_rms_norm(k, F32_EPS), v
+        return F.rms_norm(q, (dk,)), gate, F.rms_norm(k, (dk,)), v
 
     @staticmethod
     def _conv_prefill(t, conv, tails=None, slots=None, continuing=False):
@@ -276,10 +289,24 @@ class PolarAttention(nn.Module):
 
     def _combine(self, c, mag, gate):
         """``proj(c * sigmoid(gate)) + mu_proj(mag)`` (``inference/models/atma.py:246-252``).
-        c: (..., H, dk), mag: (..., H), gate: (..., H*dk)."""
+        c, gate: (..., H, dk), mag: (..., H)."""
         lead = c.shape[:-2]
-        c_flat = c.reshape(*lead, self.num_heads * self.head_dim)
-        return self.proj(c_flat * torch.sigmoid(gate)) + self.mu_proj(mag.to(c.dtype))
+        gated = (c * torch.sigmoid(gate)).reshape(*lead, self.num_heads * self.head_dim)
+        return self.proj(gated) + self.mu_proj(mag.to(c.dtype))
+
+    def _fused_out(self, x, c, mag, gate, r):
+        """The layer's output for 16-bit inference rows, unsummed: ``global_gate`` forms both
+        projection inputs in one pass, one GEMM and one GEMM-accumulate give
+        ``proj(xa) + mem.proj(xm)`` without biases, and the biases and ``mu_proj(mag)`` ride
+        along as a ``PartialSums`` for the residual norm (or ``materialize``).
+        x (rows, dim); c (B, T, H, dk) view with rows = B T; mag (rows, H); gate (rows, H, dk)
+        view; r (rows, H, dk) fp32."""
+        m = self.mem
+        xa, xm = global_gate(c, gate, r, m.gate(x), F32_EPS)
+        y = F.linear(xa, self.proj.weight.type_as(xa)).addmm_(xm, m.proj.weight.type_as(xm).t())
+        return PartialSums(None, [self.proj.bias.type_as(y), m.proj.bias.type_as(y), self.mu_proj.bias.type_as(y)],
+                           mu_x=mag.contiguous().to(y.dtype), mu_w=self.mu_proj.weight.type_as(y), dtype=y.dtype,
+                           base=y)
 
     def _side_stream(self, device):
         s = self._side.get(device)
@@ -337,10 +364,13 @@ class PolarAttention(nn.Module):
         v = self._conv_prefill(v.reshape(B, T, Hkv * dk), self.canon_v).view(B, T, Hkv, dk)
         return self._attend_prefill(x, q, gate, k, v, None, None)
 
-    def _attend_prefill(self, x, q, gate, k, v, S0, final_sink):
+    def _attend_prefill(self, x, q, gate, k, v, S0, final_sink, defer=False):
+        """``defer`` (16-bit inference): return the output as a ``PartialSums`` over B T rows."""
         B, T = q.shape[:2]
+        H, dk = self.num_heads, self.head_dim
         n_keys = torch.arange(1, T + 1, device=x.device, dtype=torch.float32)
         qh, kh, vh = (t.transpose(1, 2) for t in (q, k, v))   # (B, heads, T, dk) views
+        fused = self._glue_fusable(x)
 
         # under autograd the differentiable op (HIP forward with saved statistics, HIP
         # backward loops); otherwise the forward-only kernel
@@ -348,20 +378,27 @@ class PolarAttention(nn.Module):
 
         def polar():
             c, mag = attend(qh, kh, vh, n_keys, is_causal=True, window=self.window, **self.polar_params())
+            if fused:
+                return c, mag
             return self._combine(c.transpose(1, 2), mag.transpose(1, 2), gate)
 
         def memory(signal):
-            return self.mem(x, q, k, v, initial_state=S0, output_final_state=final_sink is not None,
-                            start_signal=signal)
+            fn = self.mem.readout if fused else self.mem
+            return fn(x, q, k, v, initial_state=S0, output_final_state=final_sink is not None, start_signal=signal)
 
         out, m = self._with_memory(polar, memory, (x, q, k, v))
+        if m is not None and final_sink is not None:
+            final_sink(m[1])
+        if fused:
+            c, mag = out
+            res = self._fused_out(x.reshape(B * T, -1), c.transpose(1, 2), mag.transpose(1, 2).reshape(B * T, H),
+                                  gate.reshape(B * T, H, dk), m[0].reshape(B * T, H, dk))
+            return res if defer else res.materialize().view(B, T, -1)
         if m is not None:
             out = out + m[0]
-            if final_sink is not None:
-                final_sink(m[1])
         return out
 
-    def prefill(self, x, cache: GlobalLayerCache, slots, slot_mapping):
+    def prefill(self, x, cache: GlobalLayerCache, slots, slot_mapping, defer=False):
         """Dense fresh prefill of B equal-length sequences (``inference/models/atma.py:397-437``).
 
         x: (B, T, dim); slots: (B,) int64 rows of the conv / memory tables;
@@ -380,9 +417,10 @@ class PolarAttention(nn.Module):
         def sink(S):
             cache.mem_table[slots] = S
 
-        return self._attend_prefill(x, q, gate, k, v, S0, sink)
+        return self._attend_prefill(x, q, gate, k, v, S0, sink, defer)
 
-    def prefill_packed(self, x, cache: GlobalLayerCache, seq_lens, slots, slot_mapping, tile_maps, token_maps):
+    def prefill_packed(self, x, cache: GlobalLayerCache, seq_lens, slots, slot_mapping, tile_maps, token_maps,
+                       defer=False):
         """Grouped fresh prefill of ragged prompts packed along tokens
         (``inference/models/atma.py:431-507``): the Canon convs as one packed launch each
         (tails written per sequence), the K/V rows to the pages, ONE tile-mapped Polar
@@ -403,6 +441,18 @@ class PolarAttention(nn.Module):
             total, Hkv, dk)
         store_kvcache(k, v, cache.k_cache, cache.v_cache, slot_mapping)
         c, mag = polar_attention_packed_fwd(q, k, v, *tile_maps, window=self.window, **self.polar_params())
+        if self._glue_fusable(x):
+            rs, start = [], 0
+            for i, n in enumerate(int(t) for t in seq_lens):
+                sl = slots[i:i + 1]
+                seg = slice(start, start + n)
+                r, S = self.mem.readout(x[seg][None], q[seg][None], k[seg][None], v[seg][None],
+                                        initial_state=cache.mem_table[sl], output_final_state=True)
+                cache.mem_table[sl] = S
+                rs.append(r[0])
+                start += n
+            res = self._fused_out(x, c.view(1, total, H, dk), mag, gate, torch.cat(rs, 0))
+            return res if defer else res.materialize()
         out = self._combine(c, mag, gate)
         if self.mem is not None:
             parts, start = [], 0

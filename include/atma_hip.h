@@ -536,7 +536,8 @@ int atma_linear_tokens_chunks(const void* x, int64_t ldx, int64_t M, int64_t chu
 /*
  * Residual add + RMSNorm of the pre-norm block (inference/models/atma.py:680-713, norm
  * model/layers.py:6-16), no reference counterpart as one call: per row m,
- *   br  = y[m]  or  round(sum_p parts[p][m] + sum_i bias[i] + mu_x[m] . mu_w^T)
+ *   br  = round(y[m] or sum_p parts[p][m], + sum_i bias[i] + mu_x[m] . mu_w^T)  (y[m] itself when
+ *         y comes with no bias and no low-rank term)
  *   s   = res ? round(res[m] + br) : br        (written to res_out when non-NULL)
  *   out = round(s * rsqrt(mean(s^2) + eps) * weight)
  * Exactly one of y / parts; parts (n_parts, M, D) fp32; up to 3 biases (D,); mu_x (M,
@@ -577,14 +578,46 @@ int atma_global_decode_prep(const void* y, int64_t ldy, int64_t ck, int64_t cv, 
                             float b_bias, int64_t B, int64_t H, int64_t Hkv, int64_t d, int dtype, void* stream);
 
 /*
- * The gated inputs of the global layer's output projections (inference/models/atma.py:
- * 246-252, model/blocks.py:470-490), no reference counterpart as one call:
- * x2[b, h d + e] = c[b, h, e] * sigmoid(y[b, 2 h d + d + e]) and, when r is non-NULL,
- * x2[b, H d + h d + e] = round(rms_norm(r[b, h]) (eps mem_eps)) * sigmoid(y[b, cm + h d
- * + e]), each sigmoid and product rounded to 16 bits.  c (B, H, d) 16-bit, r fp32.
+ * Per-head RMSNorm of a strided view (no reference counterpart as one call; the global
+ * layer's q / k norms, model/reference.py:136-137): out[m, h, :] = x[m, h, :] *
+ * rsqrt(mean(x[m, h, :]^2) + eps), element (m, h, e) of x at m ldr + h ldh + e, out
+ * (rows, H, d) contiguous.  d 64 or 128; 16-bit; 16-byte aligned heads.
  */
+int atma_head_rms_norm(const void* x, int64_t ldr, int64_t ldh, void* out, int64_t rows, int64_t H, int64_t d,
+                       float eps, int dtype, void* stream);
+
+/*
+ * The gated inputs of the global layer's output projections (inference/models/atma.py:
+ * 246-252, model/blocks.py:470-490), no reference counterpart as one call.  Row m = b T + t:
+ *   xa[m, h d + e] = c[b, t, h, e] * sigmoid(gate[m, h, e])
+ *   xm[m, h d + e] = round(rms_norm(r[m, h, :])[e] (eps mem_eps)) * sigmoid(mgate[m, h d + e])
+ * with c at b c_sb + t c_st + h c_sh + e (Polar's head-major output, or one row per sequence),
+ * gate at m g_sr + h g_sh + e, r at m r_sr + h d + e (r_dtype ATMA_F32 or dtype), mgate at m mg_sr + h d + e; each
+ * sigmoid and product rounded to 16 bits.  r NULL: no memory branch (xm, mgate unused).
+ * d 64 or 128; every head-row 16-byte aligned.  atma_global_decode_gate is the decode
+ * form: c (B, H, d) contiguous, the output gate of head h at y[b, 2 h d + d ..], the memory
+ * gate at y[b, cm + h d ..], x2 = [xa | xm] per row.
+ */
+int atma_global_gate(const void* c, int64_t c_sb, int64_t c_st, int64_t c_sh, int64_t T, const void* gate,
+                     int64_t g_sr, int64_t g_sh, const void* r, int64_t r_sr, int r_dtype, const void* mgate, int64_t mg_sr,
+                     void* xa, int64_t a_sr, void* xm, int64_t m_sr, int64_t rows, int64_t H, int64_t d,
+                     float mem_eps, int dtype, void* stream);
 int atma_global_decode_gate(const void* c, const float* r, const void* y, int64_t ldy, int64_t cm, void* x2,
                             int64_t ldx2, float mem_eps, int64_t B, int64_t H, int64_t d, int dtype, void* stream);
+
+/*
+ * The LFM2 block's fresh-prefill mixer input over packed ragged sequences
+ * (model/reference.py:31-48, inference/models/atma.py:625-673 with packed_causal_conv1d
+ * :138-160), no reference counterpart as one call: with b, c, x the three D-wide thirds of
+ * each bcx row, out[t] = c * conv(b * x)[t], the depthwise causal conv of K taps (weight
+ * (D, K)) over each token's own sequence (token maps as atma_packed_causal_conv1d), and each
+ * sequence's last K - 1 values of b * x (zero before its start) written to its row of state
+ * (S, D, K - 1).  Eager roundings: b * x, the conv, c * conv.  K 3 or 4; 16-bit; D % 8 == 0.
+ */
+int atma_lfm2_conv_packed(const void* bcx, int64_t ld, const void* weight, int64_t K, void* out, int64_t ldo,
+                          void* state, int64_t s_ss, int64_t num_slots, const int32_t* token_seq_starts,
+                          const int32_t* token_seq_ends, const int32_t* token_seq_slots, int64_t total, int64_t D,
+                          int dtype, void* stream);
 
 #ifdef __cplusplus
 }
