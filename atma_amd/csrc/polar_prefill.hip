@@ -1027,28 +1027,36 @@ __global__ void __launch_bounds__(512, 1) polar_fwd16_pp_kernel(PolarFwdArgs arg
   // chunk the swizzle of that tile row stores there: the swizzle depends on the row
   // modulo 16, so it is taken from the tile row, not from the row within the wave's 8).  Full blocks put the wave's row in the scalar offset; a partial last
   // block puts the whole row offset into the range-checked per-lane offset.
-  // (the per-lane offsets are recomputed from a laundered lane index at each copy: a few
-  // VALU operations, where keeping them would hold registers through the whole loop)
+  // (the per-lane offsets are recomputed from a laundered lane index at each tile, where
+  // keeping them would hold registers through the whole loop.  Instruction r covers tile
+  // rows row0 .. row0 + RPI - 1 with row0 a multiple of RPI, and for these widths the
+  // swizzle splits as f(row0 + lr) = f(lr) ^ f(row0): the lane's chunk position lc ^ f(lr)
+  // is computed once per tile and each instruction XORs in the wave-uniform f(row0).)
+  // One buffer descriptor per tensor slice, built once: the range ends at the last key row,
+  // so rows past Tk (only ever addressed through the range-checked per-lane offset of a
+  // partial last block) read as zeros; a full block puts its offset in the scalar offset.
   const uint32_t kst2 = (uint32_t)args.k_st * 2u, vst2 = (uint32_t)args.v_st * 2u;
-  auto copy_tile = [&](const T* base, uint32_t st2, int blk, T* dst) __attribute__((always_inline)) {
-    const int rows = min(Tk - blk * BN, BN);
-    const auto rs = buffer_rsrc(base + (int64_t)blk * BN * (st2 / 2u), (uint32_t)(rows - 1) * st2 + 2u * D);
+  const auto krs = buffer_rsrc(kp, Tk > 0 ? (uint32_t)(Tk - 1) * kst2 + 2u * D : 0u);
+  const auto vrs = buffer_rsrc(vp, Tk > 0 ? (uint32_t)(Tk - 1) * vst2 + 2u * D : 0u);
+  auto copy_tile = [&](__amdgpu_buffer_rsrc_t rs, uint32_t st2, int blk, T* dst) __attribute__((always_inline)) {
+    const uint32_t boff = (uint32_t)blk * (uint32_t)BN * st2;
     uint32_t ln = (uint32_t)lane;
     asm volatile("" : "+v"(ln));
-    const uint32_t lr = ln / CPR;
-    if (rows == BN) {
+    const uint32_t lr = (ln / CPR) % RPI, lc = ln % CPR;
+    const uint32_t cl = lc ^ (uint32_t)lds_swizzle<CPR>((int)lr);  // chunk position, lane part
+    const uint32_t ro = lr * st2;                                   // row offset, lane part
+    if (blk * BN + BN <= Tk) {
 #pragma unroll
       for (int r = 0; r < NCP; ++r) {
         const uint32_t row0 = 16u * wq + RPI * r;
-        const uint32_t co = 16u * ((ln % CPR) ^ lds_swizzle<CPR>((int)(row0 + lr)));
-        dma_buf16(rs, lr * st2 + co, row0 * st2, dst + row0 * D);
+        dma_buf16(rs, ro + 16u * (cl ^ (uint32_t)lds_swizzle<CPR>((int)row0)), boff + row0 * st2, dst + row0 * D);
       }
     } else {
 #pragma unroll
       for (int r = 0; r < NCP; ++r) {
         const uint32_t row0 = 16u * wq + RPI * r;
-        const uint32_t co = 16u * ((ln % CPR) ^ lds_swizzle<CPR>((int)(row0 + lr)));
-        dma_buf16(rs, (row0 + lr) * st2 + co, 0, dst + row0 * D);
+        dma_buf16(rs, boff + ro + row0 * st2 + 16u * (cl ^ (uint32_t)lds_swizzle<CPR>((int)row0)), 0,
+                  dst + row0 * D);
       }
     }
   };
@@ -1101,9 +1109,13 @@ __global__ void __launch_bounds__(512, 1) polar_fwd16_pp_kernel(PolarFwdArgs arg
     if (args.window > 0) kbeg = max((int)floorf(g_nlo) - args.window, 0);
     kbeg = (kbeg / BN) * BN;
   }
-  const int nblk_beg = kbeg / BN, nblk_end = (kend + BN - 1) / BN;
+  // the bounds are uniform (read from LDS by every lane): made scalar here, so every copy's
+  // block offset is scalar arithmetic -- a vector-computed scalar offset would reach the
+  // inline-asm copies through v_readfirstlane, whose SGPR write the copy may read stale
+  const int nblk_beg = __builtin_amdgcn_readfirstlane(kbeg / BN);
+  const int nblk_end = __builtin_amdgcn_readfirstlane((kend + BN - 1) / BN);
   const int nblk = nblk_end > nblk_beg ? nblk_end - nblk_beg : 0;
-  if (nblk > 0 && grp == 1) copy_tile(kp, kst2, nblk_beg, Ks);  // K(0) into K buffer 0
+  if (nblk > 0 && grp == 1) copy_tile(krs, kst2, nblk_beg, Ks);  // K(0) into K buffer 0
 
 #pragma unroll
   for (int s = 0; s < QSTEPS; ++s) asm volatile("" ::"v"(qreg16[s]));
@@ -1259,8 +1271,8 @@ __global__ void __launch_bounds__(512, 1) polar_fwd16_pp_kernel(PolarFwdArgs arg
   auto copies = [&](int m, auto MP) __attribute__((always_inline)) {
     constexpr int mp = decltype(MP)::value;  // m % 2
     if (grp == 0) return;
-    if (m + 1 < nblk) copy_tile(kp, kst2, nblk_beg + m + 1, Ks + (mp ^ 1) * TILE);
-    if (m < nblk) copy_tile(vp, vst2, nblk_beg + m, Vs + mp * TILE);
+    if (m + 1 < nblk) copy_tile(krs, kst2, nblk_beg + m + 1, Ks + (mp ^ 1) * TILE);
+    if (m < nblk) copy_tile(vrs, vst2, nblk_beg + m, Vs + mp * TILE);
   };
   using C0 = std::integral_constant<int, 0>;
   using C1 = std::integral_constant<int, 1>;
@@ -1374,7 +1386,9 @@ template <typename T, int D>
 static int launch_fwd(PolarFwdArgs a, hipStream_t stream) {
   const int G = a.Hq / a.Hkv;
   if constexpr (sizeof(T) == 2) {
-    if (G % 2 == 0 && !a.tile_seq_start) {
+    // the ping-pong kernel addresses a (b, KV head) slice of k / v through one 32-bit buffer range
+    const bool slices32 = (int64_t)a.Tk * a.k_st * 2 < (1ll << 32) && (int64_t)a.Tk * a.v_st * 2 < (1ll << 32);
+    if (G % 2 == 0 && !a.tile_seq_start && slices32) {
       // two query heads of a KV group per workgroup, the ping-pong schedule
       const int64_t per_rank = (int64_t)a.B * a.Hkv * (G / 2);
       a.xcd_remap = (per_rank % (8 * (G / 2)) == 0) ? 1 : 0;
