@@ -127,6 +127,65 @@ def test_validation_rejects_without_launch(lib):
     assert lib.atma_store_kvcache(null, 0, null, 0, null, null, null, 0, 256, 8, 1, null) == 0
 
 
+def test_fusion_entry_points_validate_without_launch(lib):
+    """The served path's projections and fusions reject bad requests before any launch
+    (ATMA_ERR_INVALID = 1, ATMA_ERR_UNSUPPORTED = 2) and treat empty requests as no-ops."""
+    null, BF16, F32 = None, 1, 0
+    buf = ctypes.create_string_buffer(64)
+    ptr = ctypes.cast(buf, ctypes.c_void_p)
+    ptrs = (ctypes.c_void_p * 9)(*([ptr.value] * 9))
+    lds = (ctypes.c_int64 * 9)(*([1024] * 9))
+    ns = (ctypes.c_int64 * 9)(*([64] * 9))
+    # residual + RMSNorm: D outside [8, 4096] or not a multiple of 8; both y and parts; 16-bit only
+    assert lib.atma_residual_rms_norm(null, 0, null, 0, null, 0, null, 0, null, 0, null, 0, null, 0,
+                                      null, null, 0, 4, 8192, 1e-6, BF16, null) == 1
+    assert lib.atma_residual_rms_norm(ptr, 64, buf, 1, null, 0, null, 0, null, 0, null, 0, null, 0,
+                                      ptr, ptr, 64, 4, 64, 1e-6, BF16, null) == 1
+    assert lib.atma_residual_rms_norm(null, 0, null, 0, null, 0, null, 0, null, 0, null, 0, null, 0,
+                                      null, null, 0, 4, 64, 1e-6, F32, null) == 2
+    assert lib.atma_residual_rms_norm(null, 0, null, 0, null, 0, null, 0, null, 0, null, 0, null, 0,
+                                      null, null, 0, 0, 64, 1e-6, BF16, null) == 0
+    # token-row projections: at most 32 rows, K of 256 .. 2048, 1 to 8 weight segments
+    assert lib.atma_linear_tokens_multi(ptr, 1024, 33, 1024, 1, ptrs, lds, ptrs, ptrs, lds, ns, BF16, null) == 2
+    assert lib.atma_linear_tokens_multi(ptr, 1024, 4, 1000, 1, ptrs, lds, ptrs, ptrs, lds, ns, BF16, null) == 2
+    assert lib.atma_linear_tokens_multi(ptr, 1024, 4, 1024, 9, ptrs, lds, ptrs, ptrs, lds, ns, BF16, null) == 1
+    assert lib.atma_linear_tokens_multi(null, 1024, 4, 1024, 1, ptrs, lds, ptrs, ptrs, lds, ns, BF16, null) == 1
+    assert lib.atma_linear_tokens_gated(ptr, 1024, ptr, 1024, null, ptr, 1024, 4, 40, 1024, BF16, null) == 2
+    assert lib.atma_linear_tokens_chunks(ptr, 4096, 4, 1024, 9, ptrs, lds, 64, buf, BF16, null) == 2
+    assert lib.atma_linear_tokens_chunks(ptr, 2048, 4, 1024, 4, ptrs, lds, 64, buf, BF16, null) == 1
+    # LFM2 conv step: kernel size 1 .. 16; no rows is a no-op
+    assert lib.atma_lfm2_conv_step(null, 0, null, 17, null, null, 0, 0, null, 0, 1, 8, BF16, null) == 1
+    assert lib.atma_lfm2_conv_step(null, 24, null, 3, null, null, 0, 0, null, 8, 0, 8, BF16, null) == 0
+    # global decode inputs: head dim 64 or 128; heads in groups
+    assert lib.atma_global_decode_prep(null, 0, 0, 0, 0, 0, null, null, null, 4, null, 0, null, 0, null, 0,
+                                       0, null, null, null, null, null, null, 1e-6, 0.0, 0.0,
+                                       1, 8, 2, 96, BF16, null) == 1
+    assert lib.atma_global_decode_prep(null, 0, 0, 0, 0, 0, null, null, null, 4, null, 0, null, 0, null, 0,
+                                       0, null, null, null, null, null, null, 1e-6, 0.0, 0.0,
+                                       1, 8, 3, 128, BF16, null) == 1
+    # per-head RMSNorm: head dim 64 or 128; overlapping heads
+    assert lib.atma_head_rms_norm(null, 0, 0, null, 4, 8, 96, 1e-6, BF16, null) == 1
+    assert lib.atma_head_rms_norm(ptr, 256, 128, ptr, 4, 8, 128, 1e-6, BF16, null) == 1
+    assert lib.atma_head_rms_norm(null, 0, 0, null, 0, 8, 128, 1e-6, BF16, null) == 0
+    # gated projection inputs: rows a multiple of T; r of another 16-bit dtype
+    assert lib.atma_global_gate(null, 0, 0, 0, 3, null, 0, 0, null, 0, F32, null, 0, null, 0, null, 0,
+                                4, 8, 128, 1e-6, BF16, null) == 1
+    assert lib.atma_global_gate(ptr, 0, 0, 0, 4, ptr, 0, 0, ptr, 0, 2, ptr, 0, ptr, 0, ptr, 0,
+                                4, 8, 128, 1e-6, BF16, null) == 1
+    assert lib.atma_global_decode_gate(null, null, null, 0, 0, null, 0, 1e-6, 1, 8, 96, BF16, null) == 1
+    # packed LFM2 prefill conv: kernel sizes 3 and 4 only; D a multiple of 8
+    assert lib.atma_lfm2_conv_packed(null, 0, null, 5, null, 0, null, 0, 0, null, null, null, 4, 64,
+                                     BF16, null) == 2
+    assert lib.atma_lfm2_conv_packed(null, 0, null, 3, null, 0, null, 0, 0, null, null, null, 4, 60,
+                                     BF16, null) == 1
+    assert lib.atma_lfm2_conv_packed(null, 0, null, 3, null, 0, null, 0, 0, null, null, null, 0, 64,
+                                     BF16, null) == 0
+    # softcap + greedy pick: 16-bit logits; rows shorter than V
+    assert lib.atma_softcap_argmax(null, 0, null, 0, null, 2, 100, F32, null) == 2
+    assert lib.atma_softcap_argmax(null, 50, null, 100, null, 2, 100, BF16, null) == 1
+    assert lib.atma_softcap_argmax(null, 100, null, 100, null, 0, 100, BF16, null) == 0
+
+
 def test_python_wrappers_validate_like_the_reference():
     from atma_amd.kernel import polar_attention_fwd
     p = dict(v_null=torch.zeros(2, 128), null_base=torch.zeros(2), null_slope_raw=torch.zeros(2),
