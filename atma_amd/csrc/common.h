@@ -133,9 +133,14 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) { return (uint32_t
 // bytes land at lds_wave_base + 16*i.  Issued through inline asm so the compiler does
 // not serialise later LDS reads behind it; completion is tracked by vmcnt, so the
 // caller waits with s_waitcnt vmcnt(N) and a barrier before reading the data.
+// The compiler inserts no wait states around inline asm, so each copy below starts with
+// the one a GFX9 LDS DMA needs after the scalar write of m0 that precedes it (s_nop 0).
+// Its other scalar operands (descriptor, scalar offset) must not come from a VALU write
+// (v_readfirstlane, v_readlane) in the five wait states before it; the callers keep them
+// in SALU arithmetic, and a CPU test checks the generated code for both rules.
 __device__ __forceinline__ void dma_load16(const void* gptr, const void* lds_wave_base) {
   const uint32_t off = lds_offset(lds_wave_base);
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gptr),
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr),
                "{m0}"(__builtin_amdgcn_readfirstlane(off))
                : "memory");
 }
@@ -147,7 +152,7 @@ __device__ __forceinline__ void dma_load16(const void* gptr, const void* lds_wav
 __device__ __forceinline__ void dma_buf16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
                                           const void* lds_wave_base) {
   const uint32_t off = lds_offset(lds_wave_base);
-  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff),
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff),
                "{m0}"(__builtin_amdgcn_readfirstlane(off))
                : "memory");
 }
@@ -156,7 +161,7 @@ __device__ __forceinline__ void dma_buf16(__amdgpu_buffer_rsrc_t r, uint32_t vof
 // callers that keep their LDS bases in scalar registers).
 __device__ __forceinline__ void dma_buf16_at(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
                                              uint32_t lds_byte_offset) {
-  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff),
+  asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff),
                "{m0}"(__builtin_amdgcn_readfirstlane(lds_byte_offset))
                : "memory");
 }
@@ -165,7 +170,7 @@ __device__ __forceinline__ void dma_buf16_at(__amdgpu_buffer_rsrc_t r, uint32_t 
 __device__ __forceinline__ void dma_buf4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
                                          const void* lds_wave_base) {
   const uint32_t off = lds_offset(lds_wave_base);
-  asm volatile("buffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff),
+  asm volatile("s_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff),
                "{m0}"(__builtin_amdgcn_readfirstlane(off))
                : "memory");
 }
