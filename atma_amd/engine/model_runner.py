@@ -164,6 +164,7 @@ class ModelRunner:
                         block_tables=i32[2 * max_bs:].view(max_bs, max_blocks))
         self._stage_dev, self._stage_hosts = dev, hosts
         self._stage_np = [{k: v.numpy() for k, v in views(h).items()} for h in hosts]
+        self._stage_key = [None, None]   # the batch whose table rows and slots each host copy holds
         self._stage_flip = 0
         return views(dev)
 
@@ -220,18 +221,25 @@ class ModelRunner:
         self._stage_flip ^= 1
         h = self._stage_np[k]
         page = self.block_size
-        h["input_ids"][:bs] = [s.last_token for s in seqs]
-        h["input_ids"][bs:] = 0
-        h["seq_slots"][:bs] = [s.seq_slot for s in seqs]
-        h["seq_slots"][bs:] = self.pad_slot
-        h["context_lens"][:bs] = [len(s) for s in seqs]
-        h["context_lens"][bs:] = 0
-        h["slot_mapping"][:bs] = [s.block_table[(len(s) - 1) // page] * page + (len(s) - 1) % page for s in seqs]
-        h["slot_mapping"][bs:] = -1
         bt = h["block_tables"]
-        bt[:bucket] = 0
-        for i, s in enumerate(seqs):
-            bt[i, :len(s.block_table)] = s.block_table
+        # table rows and state slots change only with the batch (a request's pages are reserved
+        # for its lifetime), so a host copy keeps them while it serves the same batch
+        key = (bucket, tuple((s.seq_id, s.seq_slot, len(s.block_table)) for s in seqs))
+        if self._stage_key[k] != key:
+            h["seq_slots"][:bs] = [s.seq_slot for s in seqs]
+            h["seq_slots"][bs:] = self.pad_slot
+            h["input_ids"][bs:] = 0
+            h["context_lens"][bs:] = 0
+            h["slot_mapping"][bs:] = -1
+            bt[:bucket] = 0
+            for i, s in enumerate(seqs):
+                bt[i, :len(s.block_table)] = s.block_table
+            self._stage_key[k] = key
+        lens = np.fromiter((len(s) for s in seqs), dtype=np.int64, count=bs)
+        h["input_ids"][:bs] = [s.last_token for s in seqs]
+        h["context_lens"][:bs] = lens
+        pos = lens - 1        # the new token's cache slot: its position's row in its position's page
+        h["slot_mapping"][:bs] = bt[np.arange(bs), pos // page] * page + pos % page
         self._stage_dev.copy_(self._stage_hosts[k], non_blocking=True)
         g = self.graph_flip
         self.graph_flip ^= 1

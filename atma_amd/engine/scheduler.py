@@ -94,7 +94,7 @@ class Scheduler:
                 continue
             seq.token_ids.append(int(tok))
             hit_eos = not seq.params.ignore_eos and tok == self.eos
-            if hit_eos or len(seq.completion_token_ids) >= seq.params.max_tokens:
+            if hit_eos or len(seq.token_ids) - seq.prompt_len >= seq.params.max_tokens:
                 seq.phase = Phase.DONE
                 self.pool.give_back(seq)
                 finished.append(seq)
