@@ -68,6 +68,8 @@ SIGNATURES = {
     "atma_linear_tokens": (_i32, [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),
     "atma_linear_tokens_multi": (_i32, [_p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _i32, _p]),
     "atma_linear_tokens_gated": (_i32, [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),
+    "atma_linear_tokens_conv": (_i32, [_p, _i64, _p, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _p, _i64, _i64, _i64,
+                                       _i64, _i32, _p]),
     "atma_linear_tokens_chunks": (_i32, [_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _i32, _p]),
     "atma_residual_rms_norm": (_i32, [_p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _p, _i64,
                                       _p, _p, _i64, _i64, _i64, _f32, _i32, _p]),

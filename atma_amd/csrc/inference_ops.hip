@@ -100,12 +100,16 @@ __global__ void __launch_bounds__(256) softcap_kernel(const T* __restrict__ x, T
 // The decode step's soft cap and greedy pick in one pass over a row of logits: out =
 // softcap(x) (softcap_logits' arithmetic) and the index of its largest value as
 // torch.argmax over those 16-bit values returns it -- the first index among equal values,
-// NaN above every number.  One workgroup of 512 threads per row.
+// NaN above every number.  One workgroup of 512 threads per row; a thread issues the loads
+// of up to kPickVecs 16-byte vectors before it converts any (one memory latency for a row
+// of up to 512 * kPickVecs * 8 values, 65,536: the served vocabulary is 50,304).
 __device__ __forceinline__ bool argmax_before(float v, int i, float bv, int bi) {
   const bool vn = v != v, bn = bv != bv;
   if (vn || bn) return vn && (!bn || i < bi);
   return v > bv || (v == bv && i < bi);
 }
+
+constexpr int kPickVecs = 16;
 
 template <typename T>
 __global__ void __launch_bounds__(512)
@@ -116,18 +120,30 @@ softcap_argmax_kernel(const T* __restrict__ x, int64_t ldx, T* __restrict__ out,
   float best = -__builtin_inff();
   int bi = 0x7fffffff;
   const int nv = vec ? V / 8 : 0;  // 16-byte vectors when every row is 16-byte aligned
-  for (int i = threadIdx.x; i < nv; i += 512) {
-    const u32x4 u = *(const u32x4*)(xr + 8 * i);
-    u32x4 o;
+  // argmax_before is a strict total order on (value, index), so the pick does not depend on
+  // the order in which a thread visits its vectors
+  for (int i0 = threadIdx.x; i0 < nv; i0 += 512 * kPickVecs) {
+    u32x4 u[kPickVecs];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float y0 = to_f32(from_f32<T>(softcap1<T>(elem16<T>(u, 2 * e))));
-      const float y1 = to_f32(from_f32<T>(softcap1<T>(elem16<T>(u, 2 * e + 1))));
-      o[e] = pack2<T>(y0, y1);
-      if (argmax_before(y0, 8 * i + 2 * e, best, bi)) best = y0, bi = 8 * i + 2 * e;
-      if (argmax_before(y1, 8 * i + 2 * e + 1, best, bi)) best = y1, bi = 8 * i + 2 * e + 1;
+    for (int j = 0; j < kPickVecs; ++j)  // past the row: a repeat of its last vector, unused
+      u[j] = *(const u32x4*)(xr + 8 * min(i0 + 512 * j, nv - 1));
+#pragma unroll
+    for (int j = 0; j < kPickVecs; ++j) {
+      // every vector is converted (so no load is moved next to a conditional use); only
+      // those inside the row are stored and compared
+      const int i = i0 + 512 * j;
+      const bool in = i < nv;
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float y0 = to_f32(from_f32<T>(softcap1<T>(elem16<T>(u[j], 2 * e))));
+        const float y1 = to_f32(from_f32<T>(softcap1<T>(elem16<T>(u[j], 2 * e + 1))));
+        o[e] = pack2<T>(y0, y1);
+        if (in && argmax_before(y0, 8 * i + 2 * e, best, bi)) best = y0, bi = 8 * i + 2 * e;
+        if (in && argmax_before(y1, 8 * i + 2 * e + 1, best, bi)) best = y1, bi = 8 * i + 2 * e + 1;
+      }
+      if (in) *(u32x4*)(orow + 8 * i) = o;
     }
-    *(u32x4*)(orow + 8 * i) = o;
   }
   for (int i = 8 * nv + threadIdx.x; i < V; i += 512) {
     const float y = to_f32(from_f32<T>(softcap1<T>(to_f32(xr[i]))));

@@ -22,6 +22,11 @@
 //    of a = (x W^T + b)[m, n], gate = (x W^T + b)[m, H + n] (each rounded to the output
 //    type first, then squared_relu_gate's arithmetic): a workgroup computes the a and
 //    gate tiles of the same 16 features, so the 2H-wide projection is never written.
+//  * conv: the LFM2 block's in_proj with its gated conv step, h = c * conv(b * x) for
+//    b, c, x = (x W^T + bias).chunk(3) (each rounded to the output type, then
+//    lfm2_conv_step's arithmetic, the channel's conv state advanced in place; 2 to 4 taps): a
+//    workgroup computes the b, c and x tiles of the same 16 channels, so the 3H-wide
+//    projection is never written and the conv step costs no launch of its own.
 //  * chunks: K split into chunks of 256-1024 across workgroups (blockIdx.y), chunk c with its
 //    own weight pointer, writing fp32 partial sums parts[c] (no bias, no rounding) for the
 //    consumer to add in chunk order (the residual RMSNorm).  That spreads a 4096-wide
@@ -64,14 +69,21 @@ struct LinTokArgs {
   int64_t cldw[kLinMaxChunks];
   float* parts;  // (chunks, M, N) fp32
   int N;
+  // conv form: depthwise taps (n, ktaps) and the state table (max_seqs, n, ktaps - 1) rows slots[m]
+  const void* taps;
+  int ktaps;
+  const int64_t* slots;
+  void* state;
+  int64_t s_ss, max_seqs;
 };
 
-// kLinGated uses segment 0: its n is H, its weight has 2H rows (a, then gate), its output H
-enum LinMode { kLinSegments = 0, kLinChunks = 1, kLinGated = 2 };
+// kLinGated and kLinConv use segment 0: its n is H, its weight has 2H rows (a, then gate) or
+// 3H rows (b, c, x), its output H
+enum LinMode { kLinSegments = 0, kLinChunks = 1, kLinGated = 2, kLinConv = 3 };
 
 // NW waves per workgroup (K per launch or chunk = NW * 256, NW <= kLinMaxWaves); FT 16-feature tiles per
-// workgroup, which share each activation load
-template <typename T, int NW, int FT, int MODE>
+// workgroup, which share each activation load; KT the conv form's taps (2 to 4)
+template <typename T, int NW, int FT, int MODE, int KT = 0>
 __global__ void __launch_bounds__(64 * NW) linear_tokens_kernel(LinTokArgs a) {
   __shared__ f32x4 red[NW > 1 ? NW - 1 : 1][FT][2][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -95,8 +107,9 @@ __global__ void __launch_bounds__(64 * NW) linear_tokens_kernel(LinTokArgs a) {
         n_lim = a.seg[s].n;
         f0 = (tile - a.seg[s].tile0) * 16 * FT;
       }
-  } else if constexpr (MODE == kLinGated) {
-    static_assert(FT == 2, "the gated form pairs an a tile with its gate tile");
+  } else if constexpr (MODE == kLinGated || MODE == kLinConv) {
+    static_assert(MODE == kLinGated ? FT == 2 : FT == 3,
+                  "the gated form pairs an a tile with its gate tile, the conv form takes b, c and x tiles");
     wp = a.seg[0].w;
     ldw = a.seg[0].ldw;
     n_lim = a.seg[0].n;
@@ -126,13 +139,35 @@ __global__ void __launch_bounds__(64 * NW) linear_tokens_kernel(LinTokArgs a) {
   for (int u = 0; u < kLinSteps; ++u) {
 #pragma unroll
     for (int f = 0; f < FT; ++f) {
-      // rows past the segment are clamped and discarded; the gated form's second tile is
-      // the gate rows of the same features
-      const int row = MODE == kLinGated ? f * n_lim + f0 + r : min(f0 + 16 * f + r, n_lim - 1);
+      // rows past the segment are clamped and discarded; the gated and conv forms' tile f
+      // is block f (a / gate, or b / c / x) of the same features
+      const int row = MODE == kLinGated || MODE == kLinConv ? f * n_lim + f0 + r : min(f0 + 16 * f + r, n_lim - 1);
       wv[u][f] = __builtin_nontemporal_load((const u32x4*)(W + (int64_t)row * ldw + k0 + 32 * u));
     }
     xv0[u] = *(const u32x4*)(x0 + 32 * u);
     xv1[u] = *(const u32x4*)(x1 + 32 * u);
+  }
+  // conv form: the epilogue's small operands (biases, taps, the tokens' state slots) go out
+  // behind the projection's loads, unconditionally (a missing bias reads x and is not used;
+  // rows past M read row M - 1), so no wait of the epilogue stands alone
+  constexpr int KS = KT > 1 ? KT - 1 : 1;
+  T cbias[3][4], ctap[4][KT > 0 ? KT : 1];
+  int64_t cslot[2];
+  if constexpr (MODE == kLinConv) {
+    static_assert(KT >= 2 && KT <= 4, "the conv form takes 2 to 4 taps");
+    const int n = f0 + 4 * g;
+    const T* bsrc = a.seg[0].bias ? (const T*)a.seg[0].bias : X;
+    const int bstep = a.seg[0].bias ? 1 : 0;
+#pragma unroll
+    for (int f = 0; f < 3; ++f)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) cbias[f][e] = bsrc[bstep * (f * n_lim + n + e)];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int j = 0; j < KT; ++j) ctap[e][j] = ((const T*)a.taps)[(int64_t)(n + e) * KT + j];
+    cslot[0] = a.slots[min(r, a.M - 1)];
+    cslot[1] = a.slots[min(16 + r, a.M - 1)];
   }
   const u32x4 zero = {0u, 0u, 0u, 0u};
   f32x4 acc[FT][2];
@@ -145,6 +180,21 @@ __global__ void __launch_bounds__(64 * NW) linear_tokens_kernel(LinTokArgs a) {
     for (int f = 0; f < FT; ++f) {
       acc[f][0] = mfma16x16x32<T>(wv[u][f], b0, acc[f][0]);
       acc[f][1] = mfma16x16x32<T>(wv[u][f], b1, acc[f][1]);
+    }
+  }
+  // conv form: the state rows of the tokens' channels, read before the partial sums meet
+  // (a token without a state row reads row 0 and discards it)
+  T cold[2][4][KS];
+  if constexpr (MODE == kLinConv) {
+    const int n = f0 + 4 * g;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int64_t slot = cslot[t] >= 0 && cslot[t] < a.max_seqs ? cslot[t] : 0;
+      const T* st = (const T*)a.state + slot * a.s_ss + (int64_t)n * KS;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int j = 0; j < KS; ++j) cold[t][e][j] = st[e * KS + j];
     }
   }
 
@@ -185,6 +235,58 @@ __global__ void __launch_bounds__(64 * NW) linear_tokens_kernel(LinTokArgs a) {
       for (int e = 0; e < 4; ++e) h[e] = sq_relu_gate1<T>(to_f32(from_f32<T>(va[e])), to_f32(from_f32<T>(vg[e])));
       const u32x2 pk = {pack2<T>(h[0], h[1]), pack2<T>(h[2], h[3])};
       *(u32x2*)(Y + (int64_t)m * a.seg[0].ldy + n) = pk;
+    }
+    return;
+  }
+  if constexpr (MODE == kLinConv) {
+    const int n = f0 + 4 * g;
+    T* Y = (T*)a.seg[0].y;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      f32x4 v[3];
+#pragma unroll
+      for (int f = 0; f < 3; ++f) {
+        v[f] = reduced(f, t);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[f][e] += a.seg[0].bias ? to_f32(cbias[f][e]) : 0.f;
+      }
+      const int m = 16 * t + r;
+      if (m >= a.M) continue;
+      T* Ym = Y + (int64_t)m * a.seg[0].ldy + n;
+      if (cslot[t] < 0 || cslot[t] >= a.max_seqs) {  // no state row: the output says so
+        // (the scalar conversion's NaN, as lfm2_conv_step writes it)
+        const uint32_t nb = __builtin_bit_cast(uint16_t, from_f32<T>(__builtin_nanf("")));
+        *(u32x2*)Ym = u32x2{nb | nb << 16, nb | nb << 16};
+        continue;
+      }
+      T* st = (T*)a.state + cslot[t] * a.s_ss + (int64_t)n * KS;
+      float h[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // lfm2_conv_step on the rounded projections b, c, x: newest tap first, then the
+        // state's inputs oldest first; the state shifts and takes the new input
+        const float bx = to_f32(from_f32<T>(to_f32(from_f32<T>(v[0][e])) * to_f32(from_f32<T>(v[2][e]))));
+        // fused multiply-adds in lfm2_conv_step's order (written out: unrolled, the first
+        // product could otherwise be the one fused)
+        float acc = bx * to_f32(ctap[e][KT - 1]);
+#pragma unroll
+        for (int j = 0; j < KS; ++j) {
+          acc = __builtin_fmaf(to_f32(cold[t][e][j]), to_f32(ctap[e][j]), acc);
+          if (j > 0) st[e * KS + j - 1] = cold[t][e][j];
+        }
+        st[e * KS + KS - 1] = from_f32<T>(bx);
+        // the sum is rounded to fp32 and then to T, as in lfm2_conv_step: kept as an fp32
+        // register, the last multiply-add cannot fold into a mixed-precision one that rounds
+        // to T directly (v_fma_mixlo: one rounding instead of two, which moves ties)
+        asm volatile("" : "+v"(acc));
+        h[e] = to_f32(from_f32<T>(v[1][e])) * to_f32(from_f32<T>(acc));
+      }
+      // scalar conversions, as lfm2_conv_step rounds (the packed conversion can differ from
+      // them on fp16 subnormals)
+      uint32_t hb[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) hb[e] = __builtin_bit_cast(uint16_t, from_f32<T>(h[e]));
+      *(u32x2*)Ym = u32x2{hb[0] | hb[1] << 16, hb[2] | hb[3] << 16};
     }
     return;
   }
@@ -236,6 +338,26 @@ static void launch_chunks(const LinTokArgs& a, int chunks, hipStream_t s) {
 template <typename T, int NW>
 static void launch_gated(const LinTokArgs& a, hipStream_t s) {
   linear_tokens_kernel<T, NW, 2, kLinGated><<<dim3((unsigned)(a.seg[0].n / 16)), dim3(64 * NW), 0, s>>>(a);
+}
+
+template <typename T, int NW>
+static void launch_conv(const LinTokArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)(a.seg[0].n / 16)), block(64 * NW);
+  switch (a.ktaps) {
+    case 2: linear_tokens_kernel<T, NW, 3, kLinConv, 2><<<grid, block, 0, s>>>(a); break;
+    case 3: linear_tokens_kernel<T, NW, 3, kLinConv, 3><<<grid, block, 0, s>>>(a); break;
+    default: linear_tokens_kernel<T, NW, 3, kLinConv, 4><<<grid, block, 0, s>>>(a); break;
+  }
+}
+
+template <typename T>
+static void launch_conv_k(const LinTokArgs& a, int64_t K, hipStream_t s) {
+  switch (K) {
+    case 256: launch_conv<T, 1>(a, s); break;
+    case 512: launch_conv<T, 2>(a, s); break;
+    case 1024: launch_conv<T, 4>(a, s); break;
+    default: launch_conv<T, 8>(a, s); break;
+  }
 }
 
 template <typename T>
@@ -368,6 +490,43 @@ extern "C" int atma_linear_tokens_gated(const void* x, int64_t ldx, const void* 
   if (dtype == ATMA_BF16) launch_gated_k<bf16>(a, K, st);
   else launch_gated_k<f16>(a, K, st);
   return check_launch("linear_tokens_gated");
+}
+
+extern "C" int atma_linear_tokens_conv(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias,
+                                       const void* taps, int64_t ktaps, const int64_t* slots, void* state,
+                                       int64_t s_ss, int64_t max_seqs, void* y, int64_t ldy, int64_t M, int64_t H,
+                                       int64_t K, int dtype, void* stream) {
+  using namespace atma;
+  if (!lin_common_ok(M, dtype) || !lin_k_ok(K, kLinMaxWaves) || H < 16 || H % 16 || H > (1 << 22) || ktaps < 2 ||
+      ktaps > 4)
+    return set_error(ATMA_ERR_UNSUPPORTED,
+                     "linear_tokens_conv: unsupported shape M=%lld H=%lld K=%lld taps=%lld dtype=%d (16-bit, "
+                     "1 <= M <= 32, H %% 16 == 0, K 256, 512, 1024 or 2048, 2 to 4 taps)",
+                     (long long)M, (long long)H, (long long)K, (long long)ktaps, dtype);
+  if (!x || !w || !taps || !y || !slots || !state)
+    return set_error(ATMA_ERR_INVALID, "linear_tokens_conv: null pointer");
+  if ((uintptr_t)x % 16 || ldx % 8 || ldx < K || (uintptr_t)w % 16 || ldw % 8 || ldw < K || (uintptr_t)y % 8 ||
+      ldy % 4 || ldy < H || (bias && (uintptr_t)bias % 2) || (uintptr_t)taps % 2 || (uintptr_t)state % 2 ||
+      max_seqs < 1 || s_ss < H * (ktaps - 1))
+    return set_error(ATMA_ERR_INVALID,
+                     "linear_tokens_conv: x / w rows must be 16-byte aligned, y rows 8-byte aligned, state rows "
+                     "(H, taps - 1)");
+  LinTokArgs a{};
+  a.x = x;
+  a.ldx = ldx;
+  a.M = (int)M;
+  a.n_segs = 1;
+  a.seg[0] = LinSeg{w, ldw, bias, y, ldy, (int)H, 0};
+  a.taps = taps;
+  a.ktaps = (int)ktaps;
+  a.slots = slots;
+  a.state = state;
+  a.s_ss = s_ss;
+  a.max_seqs = max_seqs;
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == ATMA_BF16) launch_conv_k<bf16>(a, K, st);
+  else launch_conv_k<f16>(a, K, st);
+  return check_launch("linear_tokens_conv");
 }
 
 extern "C" int atma_linear_tokens_chunks(const void* x, int64_t ldx, int64_t M, int64_t chunk_k, int64_t n_chunks,

@@ -21,7 +21,8 @@ import torch.nn.functional as F
 from torch import nn
 
 from ..kernel import causal_conv1d_decode_step, packed_causal_conv1d, softcap_argmax, softcap_logits
-from ..kernel.decode_fusions import PartialSums, lfm2_conv_step, residual_rms_norm_supported
+from ..kernel.decode_fusions import (PartialSums, lfm2_conv_step, linear_tokens_conv, linear_tokens_conv_supported,
+                                     residual_rms_norm_supported)
 from ..kernel.layer_fusions import lfm2_conv_packed
 from ..layers.attention import Attention
 from ..layers.global_attention import MLP, GlobalLayerCache, Linear, PolarAttention, RMSNorm, decode_rows
@@ -95,8 +96,13 @@ class AtmaLFM2Conv(nn.Module):
         ctx = get_context()
         table = ctx.conv_state_tables[f"conv_{self.layer_idx}_gated"]
         if not ctx.is_prefill and decode_rows(x):
+            taps = self.conv.weight.squeeze(1)
+            w = self.in_proj.weight
+            if x.is_contiguous() and w.dtype == x.dtype and linear_tokens_conv_supported(x, w, taps):
+                # in_proj, b * x, the conv step and c * (.) in one launch (linear_tokens_conv)
+                return self.out_proj(linear_tokens_conv(x, w, self.in_proj.bias, taps, ctx.seq_slots, table))
             # one launch for b * x, the conv step and c * (.) (lfm2_conv_step)
-            return self.out_proj(lfm2_conv_step(self.in_proj(x), self.conv.weight.squeeze(1), ctx.seq_slots, table))
+            return self.out_proj(lfm2_conv_step(self.in_proj(x), taps, ctx.seq_slots, table))
         if (ctx.is_prefill and ctx.token_seq_starts is not None and x.is_cuda and not torch.is_grad_enabled()
                 and x.dtype in (torch.bfloat16, torch.float16) and x.shape[-1] % 8 == 0 and self.kernel_size in (3, 4)):
             # fresh prompts: b * x, the packed conv and c * (.) in one launch (lfm2_conv_packed)
@@ -198,13 +204,13 @@ class Atma(nn.Module):
             hidden = hidden[ctx.cu_seqlens_q[1:].long() - 1]
         return softcap_logits(self.proj(hidden))
 
-    def decode_head(self, hidden):
+    def decode_head(self, hidden, ids_out=None):
         """Logits of one token per decoding sequence and, for 16-bit models, their greedy
-        ids from the same pass over the logits (``softcap_argmax``); graph capturable.
-        Returns (logits, ids or None)."""
+        ids from the same pass over the logits (``softcap_argmax``, into ``ids_out`` when
+        given); graph capturable.  Returns (logits, ids or None)."""
         logits = self.proj(hidden)
         if logits.dtype in (torch.bfloat16, torch.float16):
-            return softcap_argmax(logits)
+            return softcap_argmax(logits, ids_out)
         return softcap_logits(logits), None
 
     def init_weights(self, std=0.02, seed=0):

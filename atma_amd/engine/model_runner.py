@@ -120,12 +120,26 @@ class ModelRunner:
 
     def free_seq_slot(self, seq: Sequence):
         """Release a sequence's table rows, zeroed for the next owner (``:205-211``)."""
-        if seq.seq_slot < 0:
+        self.free_seq_slots([seq])
+
+    def free_seq_slots(self, seqs):
+        """``free_seq_slot`` for several sequences at once: one zeroing launch per state table
+        for all their rows (a batch that finishes together, 32 requests x 28 tables, would
+        otherwise make 896 launches)."""
+        slots = [s.seq_slot for s in seqs if s.seq_slot >= 0]
+        if not slots:
             return
-        for t in self.conv_state_tables.values():
-            t[seq.seq_slot].zero_()
-        self._free_slots.append(seq.seq_slot)
-        seq.seq_slot = -1
+        if len(slots) == 1:
+            for t in self.conv_state_tables.values():
+                t[slots[0]].zero_()
+        else:
+            idx = torch.tensor(slots, dtype=torch.int64).to(self.device)
+            for t in self.conv_state_tables.values():
+                t.index_fill_(0, idx, 0)
+        for s in seqs:
+            if s.seq_slot >= 0:
+                self._free_slots.append(s.seq_slot)
+                s.seq_slot = -1
 
     # ------------------------------------------------------------------ warm-up / graphs
     def warmup_model(self):
@@ -166,13 +180,19 @@ class ModelRunner:
         self._stage_np = [{k: v.numpy() for k, v in views(h).items()} for h in hosts]
         self._stage_key = [None, None]   # the batch whose table rows and slots each host copy holds
         self._stage_flip = 0
+        self._stage_ids_bytes = 8 * max_bs  # the token ids lead the buffer
+        # greedy ids of a launched step come back through these (pinned, used in turn)
+        self._ids_host = [torch.empty(max_bs, dtype=torch.int64).pin_memory() for _ in range(2)]
+        self._ids_done = [torch.cuda.Event(), torch.cuda.Event()]
+        self._ids_flip = 0
         return views(dev)
 
     @torch.inference_mode()
     def capture_cudagraph(self):
         """The decode forward captured once per batch-size bucket (``:254-310``), LM head
         included; 16-bit models also take the greedy ids inside the graph
-        (``Atma.decode_head``)."""
+        (``Atma.decode_head``), written over the step's own input ids: a step that feeds the
+        same batch again finds its tokens in place (``launch_decode``)."""
         cfg = self.config
         max_bs = cfg.max_num_seqs
         max_blocks = (cfg.max_model_len + self.block_size - 1) // self.block_size
@@ -192,12 +212,13 @@ class ModelRunner:
             set_context(False, slot_mapping=gv["slot_mapping"][:bs], context_lens=gv["context_lens"][:bs],
                         block_tables=gv["block_tables"][:bs], seq_slots=gv["seq_slots"][:bs],
                         conv_state_tables=self.conv_state_tables)
-            self.model.decode_head(self.model(gv["input_ids"][:bs]))                 # warm-up
+            ids_out = gv["input_ids"][:bs]
+            self.model.decode_head(self.model(gv["input_ids"][:bs]), ids_out)    # warm-up
             pair, outs = [], []
             for _ in range(2):
                 graph = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(graph, self.graph_pool):
-                    out = self.model.decode_head(self.model(gv["input_ids"][:bs]))
+                    out = self.model.decode_head(self.model(gv["input_ids"][:bs]), ids_out)
                 if self.graph_pool is None:
                     self.graph_pool = graph.pool()
                 pair.append(graph)
@@ -210,11 +231,48 @@ class ModelRunner:
     def _uses_graph(self, bs):
         return not self.enforce_eager and hasattr(self, "graphs") and bs <= self.config.max_num_seqs
 
-    def _run_decode_graph(self, seqs):
-        """Replay the smallest captured bucket that fits: the step's inputs go in one H2D
-        copy of the staging buffer (rows past the batch: token 0, slot -1, length 0, the
-        tables' spare row), the graph runs the model and the LM head.  Returns (logits
-        (bs, V), greedy ids (bs,) or None)."""
+    def can_pipeline(self, seqs):
+        """True when decode steps of this batch can be launched ahead of reading back the
+        previous step's tokens: captured graphs that take the greedy ids themselves (16-bit
+        models), every request greedy, the batch within the largest bucket."""
+        return (self._uses_graph(len(seqs)) and self.graph_out[self.graph_bs[-1]][0][1] is not None
+                and all(s.temperature == 0 for s in seqs))
+
+    @torch.inference_mode()
+    def launch_decode(self, seqs, ahead):
+        """Enqueue one decode step of ``seqs`` without waiting for it; ``collect`` returns its
+        tokens.  ahead 0: every request's newest token is known on the host.  ahead 1: the
+        step right after a launched, not yet collected step of the same batch in the same
+        order -- its input tokens are that step's greedy ids, already in place on the device
+        (the graph writes them over its input ids), and each request is one token longer
+        than its host record.  The step's ids are copied back into pinned memory behind the
+        graph."""
+        bs = len(seqs)
+        bucket = self._stage(seqs, ahead)
+        off = self._stage_ids_bytes if ahead else 0
+        self._stage_dev[off:].copy_(self._stage_hosts[self._stage_flip ^ 1][off:], non_blocking=True)
+        g = self.graph_flip
+        self.graph_flip ^= 1
+        self.graphs[bucket][g].replay()
+        logits, ids = self.graph_out[bucket][g]
+        host, done = self._ids_host[self._ids_flip], self._ids_done[self._ids_flip]
+        self._ids_flip ^= 1
+        host[:bs].copy_(ids[:bs], non_blocking=True)
+        done.record()
+        self.last_logits = logits[:bs]
+        return done, host, bs
+
+    @staticmethod
+    def collect(launch):
+        """The token ids of a ``launch_decode`` step (waits for it)."""
+        done, host, bs = launch
+        done.synchronize()
+        return host[:bs].tolist()
+
+    def _stage(self, seqs, ahead=0):
+        """Fill the next pinned staging copy for a decode step of ``seqs`` whose requests are
+        ``ahead`` tokens longer than their host records (rows past the batch: token 0, slot
+        -1, length 0, the padding table row); returns the graph bucket."""
         bs = len(seqs)
         bucket = next(b for b in self.graph_bs if b >= bs)
         k = self._stage_flip
@@ -235,12 +293,22 @@ class ModelRunner:
             for i, s in enumerate(seqs):
                 bt[i, :len(s.block_table)] = s.block_table
             self._stage_key[k] = key
-        lens = np.fromiter((len(s) for s in seqs), dtype=np.int64, count=bs)
-        h["input_ids"][:bs] = [s.last_token for s in seqs]
+        lens = np.fromiter((len(s) for s in seqs), dtype=np.int64, count=bs) + ahead
+        if not ahead:
+            h["input_ids"][:bs] = [s.last_token for s in seqs]
         h["context_lens"][:bs] = lens
         pos = lens - 1        # the new token's cache slot: its position's row in its position's page
         h["slot_mapping"][:bs] = bt[np.arange(bs), pos // page] * page + pos % page
-        self._stage_dev.copy_(self._stage_hosts[k], non_blocking=True)
+        return bucket
+
+    def _run_decode_graph(self, seqs):
+        """Replay the smallest captured bucket that fits: the step's inputs go in one H2D
+        copy of the staging buffer (rows past the batch: token 0, slot -1, length 0, the
+        tables' spare row), the graph runs the model and the LM head.  Returns (logits
+        (bs, V), greedy ids (bs,) or None)."""
+        bs = len(seqs)
+        bucket = self._stage(seqs)
+        self._stage_dev.copy_(self._stage_hosts[self._stage_flip ^ 1], non_blocking=True)
         g = self.graph_flip
         self.graph_flip ^= 1
         self.graphs[bucket][g].replay()

@@ -88,6 +88,8 @@ class Scheduler:
         """Record one step's sampled tokens; returns the requests that finished."""
         finished = []
         for seq, tok in zip(batch, token_ids):
+            if seq.phase is Phase.DONE:          # finished while a later step was in flight
+                continue
             seq.num_cached_tokens += seq.num_scheduled_tokens
             seq.num_scheduled_tokens = 0
             if not seq.prompt_done:

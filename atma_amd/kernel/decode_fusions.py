@@ -3,7 +3,8 @@
 A decode step pushes one token per sequence through every block; at 32 sequences each
 kernel moves a few hundred KB, and a launch costs more than its memory traffic.  These
 entry points replace chains of small launches with one each (C ABI
-``atma_linear_tokens_multi``, ``atma_linear_tokens_gated``, ``atma_linear_tokens_chunks``,
+``atma_linear_tokens_multi``, ``atma_linear_tokens_gated``, ``atma_linear_tokens_conv``,
+``atma_linear_tokens_chunks``,
 ``atma_residual_rms_norm``,
 ``atma_lfm2_conv_step``, ``atma_global_decode_prep``, ``atma_global_decode_gate``).
 None has a reference counterpart: they are the engine's own compositions of the
@@ -136,6 +137,43 @@ def linear_tokens_gated(x, weight, bias=None):
                                               _lib.ptr(b), y.data_ptr(), y.stride(0), M, H, K,
                                               _lib.dtype_code(x.dtype), _lib.stream_handle(x.device))
     _lib.check(rc, "linear_tokens_gated")
+    return y
+
+
+def linear_tokens_conv_supported(x, weight, taps):
+    M, K = x.shape if x.dim() == 2 else (0, 0)
+    H = taps.shape[0]
+    return (x.dtype in _DT and 1 <= M <= 32 and K in (256, 512, 1024, 2048) and H % 16 == 0 and H >= 16
+            and weight.shape == (3 * H, K) and 2 <= taps.shape[1] <= 4)
+
+
+@torch.no_grad()
+def linear_tokens_conv(x, weight, bias, taps, slots, state_table):
+    """The LFM2 block's in_proj and decode mixer in one launch: ``lfm2_conv_step(F.linear(x,
+    weight, bias), taps, slots, state_table)``, bit for bit, the 3H-wide projection never
+    written.  x (M, K), M <= 32, K in {256, 512, 1024, 2048}; weight (3H, K) -- b, c, x
+    rows; bias (3H,) or None; taps (H, Kt) contiguous, 2 <= Kt <= 4; state_table (max_seqs,
+    H, Kt - 1) contiguous, rows ``slots`` advanced in place.  Returns (M, H) in x's dtype."""
+    _rows(x, "x")
+    _rows(weight, "weight")
+    M, K = x.shape
+    H, Kt = taps.shape
+    if not linear_tokens_conv_supported(x, weight, taps) or weight.dtype != x.dtype or taps.dtype != x.dtype \
+            or not taps.is_contiguous() or (bias is not None and (bias.shape != (3 * H,) or bias.dtype != x.dtype)):
+        raise ValueError(f"linear_tokens_conv: unsupported x {tuple(x.shape)} {x.dtype}, weight "
+                         f"{tuple(weight.shape)}, taps {tuple(taps.shape)}")
+    if state_table.shape[1:] != (H, Kt - 1) or state_table.dtype != x.dtype or not state_table.is_contiguous():
+        raise ValueError(f"linear_tokens_conv: state_table must be contiguous (max_seqs, {H}, {Kt - 1}) in x's dtype")
+    _contig_cuda(x, weight, taps, state_table)
+    b = None if bias is None else bias.contiguous()
+    slots = slots.to(device=x.device, dtype=torch.int64).reshape(M).contiguous()
+    y = torch.empty((M, H), device=x.device, dtype=x.dtype)
+    rc = _lib.load().atma_linear_tokens_conv(x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0),
+                                             _lib.ptr(b), taps.data_ptr(), Kt, slots.data_ptr(),
+                                             state_table.data_ptr(), state_table.stride(0), state_table.shape[0],
+                                             y.data_ptr(), y.stride(0), M, H, K, _lib.dtype_code(x.dtype),
+                                             _lib.stream_handle(x.device))
+    _lib.check(rc, "linear_tokens_conv")
     return y
 
 

@@ -13,6 +13,7 @@ few token rows (one per decoding sequence), where the reference calls the vendor
 
 import torch
 
+from .. import _lib
 from .. import _ops  # noqa: F401  (registers torch.ops.atma_hip.*)
 
 
@@ -36,16 +37,30 @@ def softcap_logits(logits):
 
 
 @torch.no_grad()
-def softcap_argmax(logits):
+def softcap_argmax(logits, ids_out=None):
     """``capped = softcap_logits(logits)`` and ``capped.float().argmax(-1)`` in one launch
     (one workgroup per row): the decode step's soft cap and greedy pick.  logits (rows,
-    V) 16-bit.  Returns (capped (rows, V), ids (rows,) int64).
+    V) 16-bit.  Returns (capped (rows, V), ids (rows,) int64); with ``ids_out`` (a
+    contiguous int64 (rows,) tensor, inference only) the ids are written there.
     No counterpart in the reference's op set (its sampler takes the argmax in torch)."""
     if logits.dim() != 2 or logits.stride(1) != 1:
         raise ValueError("expected logits [rows, vocab] with unit inner stride")
     if logits.dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("softcap_argmax takes 16-bit logits")
-    return torch.ops.atma_hip.softcap_argmax(logits)
+    if ids_out is None:
+        return torch.ops.atma_hip.softcap_argmax(logits)
+    rows, V = logits.shape
+    if ids_out.shape != (rows,) or ids_out.dtype != torch.int64 or not ids_out.is_contiguous() \
+            or ids_out.device != logits.device:
+        raise ValueError(f"ids_out must be a contiguous int64 ({rows},) tensor on the logits' device")
+    if not logits.is_cuda:
+        raise RuntimeError("softcap_argmax requires a GPU (HIP)")
+    out = torch.empty((rows, V), device=logits.device, dtype=logits.dtype)
+    rc = _lib.load().atma_softcap_argmax(logits.data_ptr(), logits.stride(0), out.data_ptr(), out.stride(0),
+                                         ids_out.data_ptr(), rows, V, _lib.dtype_code(logits.dtype),
+                                         _lib.stream_handle(logits.device))
+    _lib.check(rc, "softcap_argmax")
+    return out, ids_out
 
 
 @torch.no_grad()

@@ -523,6 +523,22 @@ int atma_linear_tokens_gated(const void* x, int64_t ldx, const void* w, int64_t 
                              int64_t ldy, int64_t M, int64_t H, int64_t K, int dtype, void* stream);
 
 /*
+ * The LFM2 block's in_proj and decode mixer in one call (model/reference.py:31-48,
+ * inference/models/atma.py:625-673; no reference counterpart as one call): with w (3H, K)
+ * -- the b rows, the c rows, the x rows -- and bias (3H,) or NULL, b, c, x of row m are
+ * round(x[m] . w[n] + bias[n]) for the three blocks, and y[m, n] = c * conv(b * x) in
+ * atma_lfm2_conv_step's arithmetic: taps (H, ktaps), state (max_seqs, H, ktaps - 1) with
+ * row stride s_ss, row slots[m], advanced in place (a slot outside [0, max_seqs) yields NaN
+ * outputs and leaves the table untouched).  Equal to atma_linear_tokens then
+ * atma_lfm2_conv_step, bit for bit.  H % 16 == 0, 2 <= ktaps <= 4, max_seqs >= 1; K, M and
+ * alignment as atma_linear_tokens.
+ */
+int atma_linear_tokens_conv(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias,
+                            const void* taps, int64_t ktaps, const int64_t* slots, void* state, int64_t s_ss,
+                            int64_t max_seqs, void* y, int64_t ldy, int64_t M, int64_t H, int64_t K, int dtype,
+                            void* stream);
+
+/*
  * K split across workgroups, fp32 partial sums out (no reference counterpart; the decode
  * step's 4096-wide MLP projection and the global layer's two output projections):
  * parts[c][m][n] = sum_{k < chunk_k} x[m, c chunk_k + k] w[c][n, k] for c < n_chunks

@@ -151,6 +151,15 @@ def test_fusion_entry_points_validate_without_launch(lib):
     assert lib.atma_linear_tokens_multi(ptr, 1024, 4, 1024, 9, ptrs, lds, ptrs, ptrs, lds, ns, BF16, null) == 1
     assert lib.atma_linear_tokens_multi(null, 1024, 4, 1024, 1, ptrs, lds, ptrs, ptrs, lds, ns, BF16, null) == 1
     assert lib.atma_linear_tokens_gated(ptr, 1024, ptr, 1024, null, ptr, 1024, 4, 40, 1024, BF16, null) == 2
+    # in_proj + conv step: H a multiple of 16, 1 .. 16 taps, a state table when taps > 1
+    assert lib.atma_linear_tokens_conv(ptr, 1024, ptr, 1024, null, ptr, 3, ptr, ptr, 2048, 4, ptr, 1024,
+                                       4, 40, 1024, BF16, null) == 2
+    assert lib.atma_linear_tokens_conv(ptr, 1024, ptr, 1024, null, ptr, 17, ptr, ptr, 2048, 4, ptr, 1024,
+                                       4, 1024, 1024, BF16, null) == 2
+    assert lib.atma_linear_tokens_conv(ptr, 1024, ptr, 1024, null, ptr, 3, null, null, 2048, 4, ptr, 1024,
+                                       4, 1024, 1024, BF16, null) == 1
+    assert lib.atma_linear_tokens_conv(ptr, 1024, ptr, 1024, null, ptr, 3, ptr, ptr, 1000, 4, ptr, 1024,
+                                       4, 1024, 1024, BF16, null) == 1
     assert lib.atma_linear_tokens_chunks(ptr, 4096, 4, 1024, 9, ptrs, lds, 64, buf, BF16, null) == 2
     assert lib.atma_linear_tokens_chunks(ptr, 2048, 4, 1024, 4, ptrs, lds, 64, buf, BF16, null) == 1
     # LFM2 conv step: kernel size 1 .. 16; no rows is a no-op

@@ -11,7 +11,9 @@ replace, run in torch on the same 16-bit inputs:
   within one bf16 ulp of its fp64 sum (one rounding), the normed row within one ulp of
   ``F.rms_norm`` (the reciprocal square root's last bit);
 * ``lfm2_conv_step``: equal bit for bit to ``b * x`` -> ``causal_conv1d_decode_step`` ->
-  ``c * (.)``, state tables included;
+  ``c * (.)``, state tables included; ``linear_tokens_conv`` bit for bit to
+  ``linear_tokens`` then ``lfm2_conv_step`` (state tables included, a row without a state
+  slot NaN and its table untouched);
 * ``global_decode_prep`` / ``global_decode_gate``: the head RMSNorm + Canon conv + gates
   chain and the gated projection inputs within 1e-2 relative (a normed or sigmoid value
   one bf16 ulp apart from torch's carries through a product), the un-normed v conv, the
@@ -181,6 +183,55 @@ def test_lfm2_conv_step_equals_eager_chain(dev, dtype, K):
     assert torch.equal(t_fused, t_eager)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,K,Kt", [(32, 1024, 3), (7, 512, 4), (1, 2048, 3), (12, 256, 2)])
+def test_linear_tokens_conv_equals_projection_then_conv_step(dev, dtype, M, K, Kt):
+    from atma_amd.kernel import linear_tokens
+    from atma_amd.kernel.decode_fusions import lfm2_conv_step, linear_tokens_conv
+    g = _g(dev, M + K + Kt)
+    H, S = 1024, 40
+    x = torch.randn(M, K, device=dev, generator=g).to(dtype)
+    w = (torch.randn(3 * H, K, device=dev, generator=g) * K ** -0.5).to(dtype)
+    bias = (torch.randn(3 * H, device=dev, generator=g) * 0.1).to(dtype)
+    taps = (torch.randn(H, Kt, device=dev, generator=g) * 0.5).to(dtype)
+    table = torch.randn(S, H, Kt - 1, device=dev, generator=g).to(dtype)
+    slots = torch.randperm(S - 1, device=dev, generator=g)[:M]
+    if M > 1:
+        slots[M // 2] = S                                  # no state row: NaN, table untouched
+    t_fused, t_chain = table.clone(), table.clone()
+    out = linear_tokens_conv(x, w, bias, taps, slots, t_fused)
+    ref = lfm2_conv_step(linear_tokens(x, w, bias), taps, slots, t_chain)
+    nan = torch.isnan(ref)
+    assert torch.equal(torch.isnan(out), nan)
+    diff = (out.view(torch.int16) != ref.view(torch.int16)) & ~nan
+    if diff.any():
+        i, j = diff.nonzero()[0].tolist()
+        raise AssertionError(f"{int(diff.sum())} outputs differ, first at {(i, j)}: {out[i, j].item()!r} against "
+                             f"{ref[i, j].item()!r}")
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16))     # NaN rows with the same bits
+    assert torch.equal(t_fused, t_chain)
+    if M > 1:
+        assert nan[M // 2].all()
+    assert torch.equal(t_fused[S - 1], table[S - 1])          # a row no token names
+
+
+def test_linear_tokens_conv_rejects(dev):
+    from atma_amd.kernel.decode_fusions import linear_tokens_conv
+    x = torch.zeros(4, 1024, device=dev, dtype=BF)
+    w = torch.zeros(3 * 1024, 1024, device=dev, dtype=BF)
+    taps = torch.zeros(1024, 3, device=dev, dtype=BF)
+    table = torch.zeros(4, 1024, 2, device=dev, dtype=BF)
+    slots = torch.arange(4, device=dev)
+    with pytest.raises(ValueError):
+        linear_tokens_conv(torch.zeros(33, 1024, device=dev, dtype=BF), w, None, taps, torch.arange(33), table)
+    with pytest.raises(ValueError):
+        linear_tokens_conv(x, w[:3000], None, taps[:1000], slots, table)
+    with pytest.raises(ValueError):
+        linear_tokens_conv(x, w, None, taps, slots, table[:, :, :1])
+    with pytest.raises(ValueError):                       # one tap: the two-launch chain serves it
+        linear_tokens_conv(x, w, None, taps[:, :1].contiguous(), slots, table[:, :, :0])
+
+
 def _prep_inputs(dev, B=6, H=8, Hkv=2, d=128, Kc=4, S=10, seed=0):
     g = _g(dev, seed)
     hd, kvd = H * d, Hkv * d
@@ -255,7 +306,7 @@ def test_residual_rms_norm_low_rank_widths(dev, H):
     assert _ulps(s, br64) <= 1.0
 
 
-@pytest.mark.parametrize("V", [50304, 1000, 77])
+@pytest.mark.parametrize("V", [50304, 1000, 77, 131080, 200000])
 def test_softcap_argmax_equals_softcap_then_argmax(dev, V):
     from atma_amd.kernel import softcap_argmax, softcap_logits
     g = _g(dev, V)

@@ -127,6 +127,40 @@ def test_engine_graph_replay_equals_eager(dev):
     assert len(log_e) == len(log_g) and all(torch.equal(a, b) for a, b in zip(log_e, log_g))
 
 
+def test_pipelined_generate_equals_stepping(dev):
+    """``generate``'s pipelined decode (each step launched before the previous step's tokens
+    are read back, its input ids left on the device by that step's graph) == the same
+    requests stepped one synchronous step at a time, token for token: ragged token limits
+    end runs early, and an end-of-sequence id met mid-run drops the step launched behind it."""
+    from atma_amd.engine import Config, LLMEngine, SamplingParams
+    hf, model, _ = _model(torch.bfloat16, seed=5)
+    prompts = _prompts([23, 50, 9, 31], 4)
+    limits = (9, 5, 12, 12)
+
+    def run(eos, pipelined):
+        cfg = Config(kvcache_block_size=16, max_num_seqs=4, max_num_batched_tokens=4096, max_model_len=160,
+                     num_kvcache_blocks=64, enforce_eager=False, hf_config=hf, eos=eos)
+        engine = LLMEngine(cfg, model=model)
+        sps = [SamplingParams(temperature=0.0, max_tokens=m, ignore_eos=False) for m in limits]
+        if pipelined:
+            out = [r["token_ids"] for r in engine.generate(prompts, sps)]
+        else:
+            seqs = [engine.add_request(p, sp) for p, sp in zip(prompts, sps)]
+            while not engine.is_finished():
+                engine.step()
+            out = [s.completion_token_ids for s in seqs]
+        engine.exit()
+        return out
+
+    free = run(-1, False)                    # no end-of-sequence id
+    assert run(-1, True) == free
+    assert [len(t) for t in free] == list(limits)
+    eos = free[2][6]                         # request 2 meets it at its 7th token, mid-run
+    stepped = run(eos, False)
+    assert len(stepped[2]) <= 7 and stepped[2][-1] == eos
+    assert run(eos, True) == stepped
+
+
 def test_generate_reports_throughput(dev):
     hf, model, _ = _model(torch.bfloat16, seed=4)
     engine = _engine(hf, model, eager=False)
