@@ -102,7 +102,11 @@ __global__ void __launch_bounds__(256) softcap_kernel(const T* __restrict__ x, T
 // torch.argmax over those 16-bit values returns it -- the first index among equal values,
 // NaN above every number.  One workgroup of 512 threads per row; a thread issues the loads
 // of up to kPickVecs 16-byte vectors before it converts any (one memory latency for a row
-// of up to 512 * kPickVecs * 8 values, 65,536: the served vocabulary is 50,304).
+// of up to 512 * kPickVecs * 8 values, 65,536: the served vocabulary is 50,304).  The cap
+// (a correctly rounded square root and division per value) is the costly part, and one
+// workgroup per row puts a 32-row decode step on 32 CUs: contiguous rows are therefore
+// capped by the elementwise softcap kernel over the whole grid first, and this kernel then
+// only picks (CAPPED: x holds the capped values, nothing is written but idx).
 __device__ __forceinline__ bool argmax_before(float v, int i, float bv, int bi) {
   const bool vn = v != v, bn = bv != bv;
   if (vn || bn) return vn && (!bn || i < bi);
@@ -111,7 +115,7 @@ __device__ __forceinline__ bool argmax_before(float v, int i, float bv, int bi) 
 
 constexpr int kPickVecs = 16;
 
-template <typename T>
+template <typename T, bool CAPPED>
 __global__ void __launch_bounds__(512)
 softcap_argmax_kernel(const T* __restrict__ x, int64_t ldx, T* __restrict__ out, int64_t ldo,
                       int64_t* __restrict__ idx, int V, int vec) {
@@ -136,18 +140,24 @@ softcap_argmax_kernel(const T* __restrict__ x, int64_t ldx, T* __restrict__ out,
       u32x4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float y0 = to_f32(from_f32<T>(softcap1<T>(elem16<T>(u[j], 2 * e))));
-        const float y1 = to_f32(from_f32<T>(softcap1<T>(elem16<T>(u[j], 2 * e + 1))));
-        o[e] = pack2<T>(y0, y1);
+        float y0 = elem16<T>(u[j], 2 * e), y1 = elem16<T>(u[j], 2 * e + 1);
+        if constexpr (!CAPPED) {
+          y0 = to_f32(from_f32<T>(softcap1<T>(y0)));
+          y1 = to_f32(from_f32<T>(softcap1<T>(y1)));
+          o[e] = pack2<T>(y0, y1);
+        }
         if (in && argmax_before(y0, 8 * i + 2 * e, best, bi)) best = y0, bi = 8 * i + 2 * e;
         if (in && argmax_before(y1, 8 * i + 2 * e + 1, best, bi)) best = y1, bi = 8 * i + 2 * e + 1;
       }
-      if (in) *(u32x4*)(orow + 8 * i) = o;
+      if (!CAPPED && in) *(u32x4*)(orow + 8 * i) = o;
     }
   }
   for (int i = 8 * nv + threadIdx.x; i < V; i += 512) {
-    const float y = to_f32(from_f32<T>(softcap1<T>(to_f32(xr[i]))));
-    orow[i] = from_f32<T>(y);
+    float y = to_f32(xr[i]);
+    if constexpr (!CAPPED) {
+      y = to_f32(from_f32<T>(softcap1<T>(y)));
+      orow[i] = from_f32<T>(y);
+    }
     if (argmax_before(y, i, best, bi)) best = y, bi = i;
   }
 #pragma unroll
@@ -407,12 +417,23 @@ extern "C" int atma_softcap_argmax(const void* logits, int64_t ldx, void* out, i
   if (!logits || !out || !idx) return set_error(ATMA_ERR_INVALID, "softcap_argmax: null pointer");
   const int vec = !((uintptr_t)logits % 16 || (uintptr_t)out % 16 || ldx % 8 || ldo % 8);
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == ATMA_BF16)
-    softcap_argmax_kernel<bf16><<<dim3((unsigned)rows), dim3(512), 0, s>>>((const bf16*)logits, ldx, (bf16*)out, ldo,
-                                                                         idx, (int)V, vec);
-  else
-    softcap_argmax_kernel<f16><<<dim3((unsigned)rows), dim3(512), 0, s>>>((const f16*)logits, ldx, (f16*)out, ldo,
-                                                                        idx, (int)V, vec);
+  const dim3 grid((unsigned)rows), block(512);
+  if (ldx == V && ldo == V && rows * V >= (1 << 16)) {
+    // contiguous rows: cap them over the whole grid, then pick from the capped values
+    const int rc = dtype == ATMA_BF16 ? launch_softcap<bf16>(logits, out, rows * V, s)
+                                      : launch_softcap<f16>(logits, out, rows * V, s);
+    if (rc != ATMA_OK) return rc;
+    if (dtype == ATMA_BF16)
+      softcap_argmax_kernel<bf16, true><<<grid, block, 0, s>>>((const bf16*)out, ldo, nullptr, 0, idx, (int)V, vec);
+    else
+      softcap_argmax_kernel<f16, true><<<grid, block, 0, s>>>((const f16*)out, ldo, nullptr, 0, idx, (int)V, vec);
+  } else if (dtype == ATMA_BF16) {
+    softcap_argmax_kernel<bf16, false><<<grid, block, 0, s>>>((const bf16*)logits, ldx, (bf16*)out, ldo, idx, (int)V,
+                                                              vec);
+  } else {
+    softcap_argmax_kernel<f16, false><<<grid, block, 0, s>>>((const f16*)logits, ldx, (f16*)out, ldo, idx, (int)V,
+                                                             vec);
+  }
   return check_launch("softcap_argmax");
 }
 
