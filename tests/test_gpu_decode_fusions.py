@@ -306,6 +306,29 @@ def test_residual_rms_norm_low_rank_widths(dev, H):
     assert _ulps(s, br64) <= 1.0
 
 
+@pytest.mark.parametrize("H", [4, 8, 16])
+def test_residual_rms_norm_low_rank_many_rows(dev, H):
+    """The prefill's form (a 16-bit base, two biases, the low-rank term, a residual) over many
+    rows equals the same rows in a few-row call bit for bit (whose roundings the tests above
+    pin), and the new stream is within 1e-2 of its fp64 sum."""
+    from atma_amd.kernel.decode_fusions import PartialSums, residual_rms_norm
+    g = _g(dev, 400 + H)
+    M, D = 8195, 1024
+    base = torch.randn(M, D, device=dev, generator=g).to(BF)
+    b1, b2 = [(torch.randn(D, device=dev, generator=g) * 0.1).to(BF) for _ in range(2)]
+    mag = torch.rand(M, H, device=dev, generator=g).to(BF)
+    mu_w = (torch.randn(D, H, device=dev, generator=g) * 0.3).to(BF)
+    res = torch.randn(M, D, device=dev, generator=g).to(BF)
+    w = (1 + 0.1 * torch.randn(D, device=dev, generator=g)).to(BF)
+    out, s = residual_rms_norm(PartialSums(None, [b1, b2], mu_x=mag, mu_w=mu_w, dtype=BF, base=base), res, w, 1e-6)
+    few = slice(M - 7, M)
+    out7, s7 = residual_rms_norm(PartialSums(None, [b1, b2], mu_x=mag[few].contiguous(), mu_w=mu_w, dtype=BF,
+                                             base=base[few].contiguous()), res[few].contiguous(), w, 1e-6)
+    assert torch.equal(out[few], out7) and torch.equal(s[few], s7)
+    s64 = base.double() + b1.double() + b2.double() + mag.double() @ mu_w.double().t() + res.double()
+    assert rel_err(s, s64) <= 1e-2
+
+
 @pytest.mark.parametrize("V", [50304, 1000, 77, 131080, 200000])
 def test_softcap_argmax_equals_softcap_then_argmax(dev, V):
     from atma_amd.kernel import softcap_argmax, softcap_logits
