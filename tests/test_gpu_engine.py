@@ -161,6 +161,32 @@ def test_pipelined_generate_equals_stepping(dev):
     assert run(eos, True) == stepped
 
 
+def test_pipelined_generate_with_queued_requests(dev):
+    """Seven requests on four state rows: each pipelined run ends where a request finishes,
+    the queued ones are admitted and prefilled, and decoding resumes in a new run -- the
+    tokens equal stepping one synchronous step at a time."""
+    from atma_amd.engine import Config, LLMEngine, SamplingParams
+    hf, model, _ = _model(torch.bfloat16, seed=6)
+    prompts = _prompts([23, 50, 9, 31, 12, 40, 17], 7)
+    limits = (6, 3, 9, 4, 5, 8, 2)
+    outs = []
+    for pipelined in (False, True):
+        cfg = Config(kvcache_block_size=16, max_num_seqs=4, max_num_batched_tokens=4096, max_model_len=160,
+                     num_kvcache_blocks=64, enforce_eager=False, hf_config=hf)
+        engine = LLMEngine(cfg, model=model)
+        sps = [SamplingParams(temperature=0.0, max_tokens=m, ignore_eos=True) for m in limits]
+        if pipelined:
+            outs.append([r["token_ids"] for r in engine.generate(prompts, sps)])
+        else:
+            seqs = [engine.add_request(p, sp) for p, sp in zip(prompts, sps)]
+            while not engine.is_finished():
+                engine.step()
+            outs.append([s.completion_token_ids for s in seqs])
+        engine.exit()
+    assert outs[0] == outs[1]
+    assert [len(t) for t in outs[0]] == list(limits)
+
+
 def test_generate_reports_throughput(dev):
     hf, model, _ = _model(torch.bfloat16, seed=4)
     engine = _engine(hf, model, eager=False)
