@@ -68,6 +68,7 @@ SIGNATURES = {
     "atma_linear_tokens": (_i32, [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),
     "atma_linear_tokens_multi": (_i32, [_p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _i32, _p]),
     "atma_linear_tokens_gated": (_i32, [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),
+    "atma_linear_gated": (_i32, [_p, _i64, _p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i32, _p]),
     "atma_linear_tokens_conv": (_i32, [_p, _i64, _p, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _p, _i64, _i64, _i64,
                                        _i64, _i32, _p]),
     "atma_linear_tokens_chunks": (_i32, [_p, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _i32, _p]),

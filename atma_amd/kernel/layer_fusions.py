@@ -1,5 +1,6 @@
-"""Per-head glue of the global layer and the LFM2 prefill conv, backed by libatma_hip.so
-(C ABI ``atma_head_rms_norm``, ``atma_global_gate``, ``atma_lfm2_conv_packed``).
+"""Per-head glue of the global layer, the LFM2 prefill conv and the MLP's gated first
+projection over many rows, backed by libatma_hip.so (C ABI ``atma_head_rms_norm``,
+``atma_global_gate``, ``atma_lfm2_conv_packed``, ``atma_linear_gated``).
 
 No reference counterparts: each is one launch for a chain of the reference's eager ops on
 the served path (``model/reference.py:31-48,131-139``, ``model/blocks.py:470-490``,
@@ -93,3 +94,34 @@ def lfm2_conv_packed(bcx, weight, state_table, token_seq_starts, token_seq_ends,
                                            _lib.dtype_code(bcx.dtype), _lib.stream_handle(bcx.device))
     _lib.check(rc, "lfm2_conv_packed")
     return out
+
+
+def linear_gated_supported(rows, in_features, out_features, dtype):
+    """Shapes ``linear_gated`` serves: 16-bit, K a multiple of 128, 2H rows with H a multiple
+    of 128, at least 4,096 rows (fewer rows take the weight-streaming decode kernels)."""
+    return (dtype in _DT and rows >= 4096 and in_features >= 128 and in_features % 128 == 0
+            and out_features % 256 == 0 and out_features >= 256)
+
+
+@torch.no_grad()
+def linear_gated(x, weight, bias=None):
+    """The MLP's first projection with its activation for many rows: ``a, gate =
+    F.linear(x, weight, bias).chunk(2, -1)`` then ``squared_relu_gate(a, gate)`` in one kernel
+    that never writes the 2H-wide projection.  x (M, K) with unit inner stride; weight (2H, K);
+    bias (2H,) or None.  Equal to that chain up to the products' summation order (each
+    projection value is one fp32 sum rounded once, as the vendor GEMM's)."""
+    _gpu16(x, weight)
+    if x.dim() != 2 or x.stride(1) != 1 or weight.dim() != 2 or weight.stride(1) != 1:
+        raise ValueError("linear_gated: x (M, K) and weight (2H, K) with unit inner strides")
+    M, K = x.shape
+    H = weight.shape[0] // 2
+    if weight.shape != (2 * H, K) or weight.dtype != x.dtype or (bias is not None and (
+            bias.shape != (2 * H,) or bias.dtype != x.dtype)):
+        raise ValueError(f"linear_gated: weight (2H, {K}) and bias (2H,) in x's dtype")
+    b = None if bias is None else bias.contiguous()
+    y = torch.empty((M, H), device=x.device, dtype=x.dtype)
+    rc = _lib.load().atma_linear_gated(x.data_ptr(), x.stride(0), weight.data_ptr(), weight.stride(0), _lib.ptr(b),
+                                       y.data_ptr(), y.stride(0), M, H, K, _lib.dtype_code(x.dtype),
+                                       _lib.stream_handle(x.device))
+    _lib.check(rc, "linear_gated")
+    return y

@@ -47,7 +47,7 @@ from ..kernel.decode_fusions import (PartialSums, chunk_width, global_decode_gat
                                      residual_rms_norm, residual_rms_norm_supported)
 from ..kernel.inference_ops import (linear_tokens, linear_tokens_supported, packed_causal_conv1d,
                                      squared_relu_gate)
-from ..kernel.layer_fusions import global_gate, head_rms_norm
+from ..kernel.layer_fusions import global_gate, head_rms_norm, linear_gated, linear_gated_supported
 from ..kernel.polar import global_decode_step_supported_shape
 from .attention import store_kvcache
 
@@ -630,6 +630,13 @@ class MLP(nn.Module):
                 w = self.proj.weight
                 parts = linear_tokens_chunks(h, [w[:, c * ck:(c + 1) * ck] for c in range(hidden // ck)], ck)
                 return PartialSums(parts, [self.proj.bias], dtype=x.dtype)
+        if x.is_cuda and not torch.is_grad_enabled() and x.is_contiguous() and self.fc.weight.dtype == x.dtype:
+            rows, K = x.numel() // x.shape[-1], x.shape[-1]
+            if linear_gated_supported(rows, K, self.fc.weight.shape[0], x.dtype):
+                # many rows (a prefill): the projection and its activation in one MFMA kernel
+                # that never writes the 8 dim-wide projection (linear_gated)
+                h = linear_gated(x.view(rows, K), self.fc.weight, self.fc.bias)
+                return self.proj(h.view(*x.shape[:-1], -1))
         a, gate = torch.chunk(self.fc(x), 2, dim=-1)
         if x.is_cuda and not torch.is_grad_enabled():
             # InferenceMLP (inference/models/atma.py:87-96): the fused HIP activation,

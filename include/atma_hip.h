@@ -523,6 +523,20 @@ int atma_linear_tokens_gated(const void* x, int64_t ldx, const void* w, int64_t 
                              int64_t ldy, int64_t M, int64_t H, int64_t K, int dtype, void* stream);
 
 /*
+ * The MLP's first projection with its activation over many token rows (model/layers.py:19-31,
+ * inference/models/atma.py:87-96; no reference counterpart as one call): with w (2H, K) -- the
+ * a rows, then the gate rows -- and bias (2H,) or NULL, y[m, n] = gate * relu(a)^2 for
+ * a = round(x[m] . w[n] + bias[n]), gate = round(x[m] . w[H + n] + bias[H + n]), n < H, in
+ * squared_relu_gate's arithmetic; each projection value is one fp32 sum rounded once (the
+ * products' order is the kernel's).  The served prefill's MFMA GEMM: the 2H-wide projection
+ * is never written.  x (M, K), w, y (M, H) row-major with row strides ldx, ldw, ldy; rows
+ * 16-byte aligned, bias 4-byte aligned; H a multiple of 128, K of 128; x and w each under
+ * 4 GiB.
+ */
+int atma_linear_gated(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias, void* y,
+                      int64_t ldy, int64_t M, int64_t H, int64_t K, int dtype, void* stream);
+
+/*
  * The LFM2 block's in_proj and decode mixer in one call (model/reference.py:31-48,
  * inference/models/atma.py:625-673; no reference counterpart as one call): with w (3H, K)
  * -- the b rows, the c rows, the x rows -- and bias (3H,) or NULL, b, c, x of row m are

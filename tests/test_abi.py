@@ -151,6 +151,12 @@ def test_fusion_entry_points_validate_without_launch(lib):
     assert lib.atma_linear_tokens_multi(ptr, 1024, 4, 1024, 9, ptrs, lds, ptrs, ptrs, lds, ns, BF16, null) == 1
     assert lib.atma_linear_tokens_multi(null, 1024, 4, 1024, 1, ptrs, lds, ptrs, ptrs, lds, ns, BF16, null) == 1
     assert lib.atma_linear_tokens_gated(ptr, 1024, ptr, 1024, null, ptr, 1024, 4, 40, 1024, BF16, null) == 2
+    # gated MLP projection over many rows: H and K multiples of 128; no rows is a no-op
+    assert lib.atma_linear_gated(ptr, 1024, ptr, 1024, null, ptr, 4096, 64, 4000, 1024, BF16, null) == 2
+    assert lib.atma_linear_gated(ptr, 1024, ptr, 1024, null, ptr, 4096, 64, 4096, 1000, BF16, null) == 2
+    assert lib.atma_linear_gated(ptr, 1024, ptr, 1024, null, ptr, 4096, 64, 4096, 1024, F32, null) == 2
+    assert lib.atma_linear_gated(null, 1024, ptr, 1024, null, ptr, 4096, 64, 4096, 1024, BF16, null) == 1
+    assert lib.atma_linear_gated(null, 0, null, 0, null, null, 0, 0, 4096, 1024, BF16, null) == 0
     # in_proj + conv step: H a multiple of 16, 1 .. 16 taps, a state table when taps > 1
     assert lib.atma_linear_tokens_conv(ptr, 1024, ptr, 1024, null, ptr, 3, ptr, ptr, 2048, 4, ptr, 1024,
                                        4, 40, 1024, BF16, null) == 2

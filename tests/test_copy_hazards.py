@@ -19,7 +19,7 @@ from pathlib import Path
 
 from atma_amd import _build
 
-SOURCES = ["polar_prefill.hip", "gated_delta_chunk16.hip", "polar_backward.hip"]
+SOURCES = ["polar_prefill.hip", "gated_delta_chunk16.hip", "polar_backward.hip", "gemm_gated.hip"]
 COPIES = ("buffer_load_dwordx4", "buffer_load_dword", "global_load_lds_dwordx4")
 # VALU instructions that write an SGPR: the destination, or the carry-out in the second slot
 VALU_SGPR_FIRST = re.compile(r"^(v_readfirstlane_b32|v_readlane_b32|v_cmpx?_\w+_e64|v_div_scale_\w+)$")
