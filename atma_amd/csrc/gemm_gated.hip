@@ -14,8 +14,9 @@
 // the x tile (256 x 64) and the weight tile (256 x 64) of a step go straight from memory
 // into LDS with buffer_load ... lds (rows past M read as zeros), double-buffered, the copies
 // of step k + 1 issued right after the one barrier of step k.  Rows are 128 bytes (8
-// chunks of 16); chunk c of row r sits at chunk position c ^ f(r), so the MFMA operand
-// reads (16 bytes of 32 consecutive rows at one chunk) are conflict-free.  The grid is
+// chunks of 16); chunk c of row r sits at chunk position c ^ f(r), f(r) = (r / 2) mod 8
+// (gg_swizzle), so the MFMA operand reads (16 bytes of 32 consecutive rows at one chunk)
+// are conflict-free: each 16-lane group of a ds_read_b128 covers all 64 banks.  The grid is
 // persistent (one workgroup per CU): the next tile's first copies fly during the current
 // tile's epilogue.
 //
@@ -46,6 +47,10 @@ __device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, c
 constexpr int kGgBM = 256;       // token rows per workgroup
 constexpr int kGgBF = 128;       // output features per workgroup (256 weight rows)
 constexpr int kGgBK = 64;        // K per step
+
+// Chunk position offset of row r in the 128-byte-row tiles: rows r and r + 2 are 256 bytes
+// apart (the same banks), so 16 consecutive rows need 8 distinct offsets per row parity.
+__device__ __forceinline__ int gg_swizzle(int r) { return (r >> 1) & 7; }
 
 struct GatedArgs {
   const void* x;  // (M, K) row stride ldx
@@ -89,17 +94,19 @@ __global__ void __launch_bounds__(512, 1) linear_gated_kernel(GatedArgs a) {
   if (!gated_tile(a, xcd, u, m0, f0)) return;
 
   // ---- copies: wave w moves rows 32 w .. + 31 of both tiles, 8 rows per instruction; lane l
-  // writes row (l / 8), chunk position l % 8, i.e. logical chunk (l % 8) ^ f(l / 8); rows
+  // writes row (l / 8), chunk position l % 8, i.e. logical chunk (l % 8) ^ f(row); rows
   // past M land past the buffer's end (zeros)
   const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.x, (uint32_t)((int64_t)a.M * a.ldx * sizeof(T)));
   const __amdgpu_buffer_rsrc_t wr = buffer_rsrc(a.w, (uint32_t)((int64_t)2 * a.H * a.ldw * sizeof(T)));
+  // copy i writes tile rows 8 i + crow (mod 16: the wave's rows start at a multiple of 32)
   const int crow = lane >> 3;
-  const uint32_t cchunk = 16u * (uint32_t)((lane & 7) ^ lds_swizzle<8>(crow));
+  const uint32_t cchunk[2] = {16u * (uint32_t)((lane & 7) ^ gg_swizzle(crow)),
+                              16u * (uint32_t)((lane & 7) ^ gg_swizzle(8 + crow))};
   uint32_t xv0, wv0;
   auto aim = [&](int tm0, int tf0) {  // the copy offsets of tile (tm0, tf0)
-    xv0 = (uint32_t)((int64_t)(tm0 + 32 * wave + crow) * a.ldx * sizeof(T)) + cchunk;
+    xv0 = (uint32_t)((int64_t)(tm0 + 32 * wave + crow) * a.ldx * sizeof(T));
     const int wrow0 = (wave < 4 ? tf0 : a.H + tf0 - 128) + 32 * wave + crow;
-    wv0 = (uint32_t)((int64_t)wrow0 * a.ldw * sizeof(T)) + cchunk;
+    wv0 = (uint32_t)((int64_t)wrow0 * a.ldw * sizeof(T));
   };
   const uint32_t xstep8 = (uint32_t)(8 * a.ldx * sizeof(T)), wstep8 = (uint32_t)(8 * a.ldw * sizeof(T));
   const uint32_t dst0 = lds_offset(&lds[0][0][0]) + (uint32_t)(32 * wave * kGgBK * sizeof(T));
@@ -110,13 +117,13 @@ __global__ void __launch_bounds__(512, 1) linear_gated_kernel(GatedArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t d = dst0 + S * 2 * kTileBytes + i * (8 * kGgBK * sizeof(T));
-      dma_buf16_at(xr, xv0 + i * xstep8 + kofs, 0u, d);
-      dma_buf16_at(wr, wv0 + i * wstep8 + kofs, 0u, d + kTileBytes);
+      dma_buf16_at(xr, xv0 + i * xstep8 + kofs + cchunk[i & 1], 0u, d);
+      dma_buf16_at(wr, wv0 + i * wstep8 + kofs + cchunk[i & 1], 0u, d + kTileBytes);
     }
   };
 
   // ---- operand reads: 16 bytes of row (tile row + l32), logical chunk 2 s + h
-  const int sw = lds_swizzle<8>(l32 & 7);
+  const int sw = gg_swizzle(l32 & 15);
   uint32_t chk[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) chk[s] = 16u * (uint32_t)((2 * s + h) ^ sw);
