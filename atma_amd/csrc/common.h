@@ -200,11 +200,13 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
 }
 
 // Chunk swizzle of row-major 16-bit tiles in LDS (rows of CPR 16-byte chunks): logical
-// 16-byte chunk c of row r is stored at chunk position c ^ f(r).  f is a bijection on
-// r mod CPR, so row reads (one chunk of 16 different rows per 16 lanes) hit 16 distinct
-// chunk positions, and f(r) >> 2 differs across any 4 consecutive rows 4k .. 4k + 3, so
-// transposing reads (4 rows x 4 adjacent chunks per 32 lanes) hit 16 distinct positions
-// too.
+// 16-byte chunk c of row r is stored at chunk position c ^ f(r).  With 256-byte rows
+// (CPR 16) f is a bijection on r mod 16, so row reads (one chunk of 16 different rows per
+// 16 lanes) hit 16 distinct bank groups, and f(r) >> 2 differs across any 4 consecutive
+// rows 4k .. 4k + 3, so transposing reads (4 rows x 4 adjacent chunks per 32 lanes) hit 16
+// distinct positions too.  With 128-byte rows (CPR 8) rows r and r + 2 share banks and f
+// takes 8 values, so 16-row reads pair up two ways (the d = 64 tiles; gemm_gated.hip uses
+// its own f for such rows).
 template <int CPR>
 __device__ __forceinline__ int lds_swizzle(int r) {
   if constexpr (CPR == 16) return 4 * (r & 3) + ((r >> 2) & 3);
