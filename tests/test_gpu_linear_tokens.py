@@ -13,7 +13,8 @@ from tests.helpers import rel_err
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(1024, 1024), (3072, 1024), (8192, 1024), (1024, 2048), (256, 1024), (2048, 1024), (4112, 1024)]
+SHAPES = [(1024, 1024), (3072, 1024), (8192, 1024), (1024, 2048), (256, 1024), (2048, 1024), (4112, 1024),
+          (50304, 1024), (32768, 512)]
 
 
 def _ref(x, w, b):
@@ -33,6 +34,20 @@ def test_linear_tokens_vs_fp32(dev, M, N, K):
     assert rel_err(y, _ref(x, w, b)) <= 1e-2
     y2 = linear_tokens(x, w, b)
     assert torch.equal(y, y2)                      # deterministic
+
+
+def test_linear_tokens_tile_width_does_not_change_results(dev):
+    """The LM head's 50,304 outputs (32 features per workgroup) and the same rows as a
+    narrower projection (the first 4,112 outputs: 16 per workgroup) give the same bits -- the
+    per-feature sums do not depend on the tile width or the grid."""
+    from atma_amd.kernel import linear_tokens
+    g = torch.Generator(device=dev).manual_seed(11)
+    x = torch.randn(32, 1024, device=dev, generator=g).bfloat16()
+    w = (torch.randn(50304, 1024, device=dev, generator=g) * 0.02).bfloat16()
+    b = (torch.randn(50304, device=dev, generator=g) * 0.02).bfloat16()
+    full = linear_tokens(x, w, b)
+    assert torch.equal(full[:, :4096], linear_tokens(x, w[:4096], b[:4096]))
+    assert torch.equal(full[:, :4112], linear_tokens(x, w[:4112], b[:4112]))
 
 
 def test_linear_tokens_fp16_strided_no_bias(dev):
