@@ -3,9 +3,9 @@
 The reference imports every kernel module inside ``try/except Exception`` and, on
 failure, sets the op to ``None`` and its flag to False, then takes its eager path
 (``inference/models/atma.py:31-80``).  Here the ops package raises ``ImportError``
-when libatma_hip.so cannot be loaded, so that guard works unchanged with the
-one-line module swap shown in INTEGRATION.md; with the library present, every
-reference-named module exports the reference's names and flag."""
+when libatma_hip.so cannot be loaded, so that guard works unchanged when the reference's
+kernel imports are pointed at the ``atma_amd.kernel`` modules of the same names; with the
+library present, every reference-named module exports the reference's names and flag."""
 
 import subprocess
 import sys
