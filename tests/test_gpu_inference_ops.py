@@ -108,6 +108,35 @@ def test_packed_conv_strided_input_and_bad_slot(dev):
     assert torch.equal(t_dev.cpu(), ref_table) and torch.equal(t_dev[0].cpu(), table[0])
 
 
+@pytest.mark.parametrize("layout", ["contiguous", "transposed", "misaligned"])
+def test_packed_conv_weight_layouts(dev, layout):
+    """The taps of a contiguous, 16-byte aligned weight are read as whole 16-byte words; a
+    transposed view and one whose storage starts 2 bytes in take the strided gather. All
+    three equal the oracle bitwise."""
+    from atma_amd.kernel import packed_causal_conv1d
+    g = torch.Generator().manual_seed(11)
+    lengths, C, K = [300, 1, 95, 40], 1024, 4
+    x = torch.randn(sum(lengths), C, generator=g).to(torch.bfloat16)
+    w = torch.randn(C, K, generator=g).to(torch.bfloat16)
+    if layout == "contiguous":
+        w_dev = w.to(dev)
+    elif layout == "transposed":
+        w_dev = w.t().contiguous().to(dev).t()                # strides (1, C)
+    else:
+        buf = torch.zeros(C * K + 1, dtype=torch.bfloat16, device=dev)
+        buf[1:] = w.reshape(-1).to(dev)
+        w_dev = buf[1:].view(C, K)                            # contiguous, 2 bytes off alignment
+        assert w_dev.data_ptr() % 16 != 0
+    table = torch.randn(6, C, K - 1, generator=g).to(torch.bfloat16)
+    maps = _maps(lengths, [4, 0, 2, 5])
+    t_dev = table.to(dev)
+    out = packed_causal_conv1d(x.to(dev), w_dev, t_dev, *[m.to(dev) for m in maps])
+    ref_table = table.clone()
+    ref = OI.packed_causal_conv1d(x, w, ref_table, *maps)
+    assert torch.equal(out.cpu(), ref)
+    assert torch.equal(t_dev.cpu(), ref_table)
+
+
 def test_reference_errors():
     from atma_amd.kernel import packed_causal_conv1d
     x = torch.zeros(4, 8)
