@@ -56,6 +56,54 @@ squared_relu_gate_kernel(const T* __restrict__ x, int64_t x_s0, int64_t x_s1, co
   }
 }
 
+// Rows of at least 256 vectors: blockIdx.y walks the rows, each lane owns two 16-byte vectors
+// of a row and issues all four loads before any arithmetic (no per-element index division).
+// NT: non-temporal loads and stores, for streams larger than the GPU's last-level cache
+// (1.61 GB at 65,536 x 4,096 bf16: 265 against 308 us for the flat loop).
+constexpr int kSqRowVecs = 2;
+
+template <typename T, bool NT>
+__global__ void __launch_bounds__(256)
+squared_relu_gate_rows_kernel(const T* __restrict__ x, int64_t x_s0, const T* __restrict__ gate, int64_t g_s0,
+                              T* __restrict__ out, int64_t rows, int64_t width) {
+  constexpr int V = 16 / (int)sizeof(T);
+  typedef T tv __attribute__((ext_vector_type(V)));
+  const int64_t c0 = ((int64_t)blockIdx.x * 256 * kSqRowVecs + threadIdx.x) * V;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    u32x4 xv[kSqRowVecs], gv[kSqRowVecs];
+#pragma unroll
+    for (int u = 0; u < kSqRowVecs; ++u) {
+      const int64_t c = c0 + (int64_t)u * 256 * V;
+      if (c < width) {
+        const u32x4* px = (const u32x4*)(x + r * x_s0 + c);
+        const u32x4* pg = (const u32x4*)(gate + r * g_s0 + c);
+        if constexpr (NT) {
+          xv[u] = __builtin_nontemporal_load(px);
+          gv[u] = __builtin_nontemporal_load(pg);
+        } else {
+          xv[u] = *px;
+          gv[u] = *pg;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kSqRowVecs; ++u) {
+      const int64_t c = c0 + (int64_t)u * 256 * V;
+      if (c < width) {
+        const tv a = __builtin_bit_cast(tv, xv[u]), b = __builtin_bit_cast(tv, gv[u]);
+        tv o;
+#pragma unroll
+        for (int e = 0; e < V; ++e) o[e] = from_f32<T>(sq_relu_gate1<T>(to_f32(a[e]), to_f32(b[e])));
+        u32x4* po = (u32x4*)(out + r * width + c);
+        if constexpr (NT)
+          __builtin_nontemporal_store(__builtin_bit_cast(u32x4, o), po);
+        else
+          *po = __builtin_bit_cast(u32x4, o);
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ softcap_logits
 template <typename T>
 __device__ __forceinline__ float softcap1(float x) {
@@ -294,6 +342,9 @@ packed_causal_conv1d_kernel(const T* __restrict__ x, int64_t x_st, int64_t x_sc,
   }
 }
 
+// streams beyond the MI355X's 256 MiB last-level cache take non-temporal accesses
+constexpr int64_t kSqStreamBytes = 256ll << 20;
+
 static unsigned elementwise_grid(int64_t n) {
   const int64_t blocks = (n + 255) / 256;
   return (unsigned)std::max<int64_t>(1, std::min<int64_t>(blocks, 256 * 64));
@@ -306,7 +357,16 @@ static int launch_sq(const void* x, int64_t x_s0, int64_t x_s1, const void* g, i
   const bool vec = x_s1 == 1 && g_s1 == 1 && width % V == 0 && (uintptr_t)x % 16 == 0 &&
                    (uintptr_t)g % 16 == 0 && (uintptr_t)out % 16 == 0 && (x_s0 * sizeof(T)) % 16 == 0 &&
                    (g_s0 * sizeof(T)) % 16 == 0;
-  if (vec)
+  if (vec && width / V >= 256) {
+    const dim3 grid((unsigned)((width / V + 256 * kSqRowVecs - 1) / (256 * kSqRowVecs)),
+                    (unsigned)std::min<int64_t>(rows, 8192));
+    if (3 * rows * width * (int64_t)sizeof(T) > kSqStreamBytes)
+      squared_relu_gate_rows_kernel<T, true><<<grid, 256, 0, s>>>((const T*)x, x_s0, (const T*)g, g_s0, (T*)out,
+                                                                 rows, width);
+    else
+      squared_relu_gate_rows_kernel<T, false><<<grid, 256, 0, s>>>((const T*)x, x_s0, (const T*)g, g_s0, (T*)out,
+                                                                  rows, width);
+  } else if (vec)
     squared_relu_gate_kernel<T, V><<<elementwise_grid(rows * width / V), 256, 0, s>>>(
         (const T*)x, x_s0, x_s1, (const T*)g, g_s0, g_s1, (T*)out, rows, width);
   else

@@ -22,7 +22,7 @@ def _eq(a, b):
 
 @pytest.mark.parametrize("dtype", DT)
 @pytest.mark.parametrize("shape,halves", [((32, 1024), True), ((7, 257), False), ((64, 4096), False),
-                                          ((5, 514), True)])
+                                          ((5, 514), True), ((9, 4112), True)])
 def test_squared_relu_gate_bitwise(dev, dtype, shape, halves):
     from atma_amd.kernel import squared_relu_gate
     g = torch.Generator().manual_seed(shape[1])
@@ -40,6 +40,21 @@ def test_squared_relu_gate_bitwise(dev, dtype, shape, halves):
     assert _eq(out, OI.squared_relu_gate(x, gate))
     if dtype == torch.bfloat16:      # the reference test's own expected form
         assert _eq(out, gate * x.relu().square())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_squared_relu_gate_stream_bitwise(dev, dtype):
+    """Rows of at least 256 vectors run one row per workgroup row; an operand stream beyond
+    256 MiB (here 270 MB) takes non-temporal loads and stores. Bitwise equal to the oracle."""
+    from atma_amd.kernel import squared_relu_gate
+    g = torch.Generator().manual_seed(5)
+    packed = torch.randn(11000, 8192, generator=g).to(dtype)
+    packed[3, :4] = torch.tensor([float("nan"), float("inf"), -0.0, -float("inf")]).to(dtype)
+    x, gate = packed.chunk(2, dim=-1)
+    xd, gd = packed.to(dev).chunk(2, dim=-1)
+    assert 3 * x.numel() * x.element_size() > 256 << 20
+    out = squared_relu_gate(xd, gd)
+    assert _eq(out, OI.squared_relu_gate(x, gate))
 
 
 @pytest.mark.parametrize("dtype", DT)
