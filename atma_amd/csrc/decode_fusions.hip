@@ -67,129 +67,163 @@ __device__ __forceinline__ void unpack8(const u32x4& u, float* v) {
 }
 __device__ __forceinline__ f32x4 ld4(const float* p) { return *(const f32x4*)p; }
 
-// One wave per row, P passes of 512 columns (8 per lane).  A pass issues every load it
-// needs (branch or partial sums, biases, low-rank weights, residual, gain) before its
-// first arithmetic, so a row costs one memory round trip per pass.  MU: the low-rank
-// term's width (0: none), a template so that its weights index registers statically.
-template <typename T, int P, int MU>
+// One wave per RPW consecutive rows, P passes of 512 columns (8 per lane).  The gain and the
+// low-rank weights of a lane's columns are loaded once for the wave's rows (at RPW = 1 and
+// MU = 8 every row re-read its lanes' share of mu_w: the whole 16 KB weight per row, twice
+// the row's own HBM bytes).  A pass issues every load it needs (branch or partial sums,
+// biases, residual) before its first arithmetic, so a row costs one memory round trip per
+// pass.  MU: the low-rank term's width (0: none), a template so that its weights index
+// registers statically.
+template <typename T, int P, int MU, int RPW, bool PARTS>
 __global__ void __launch_bounds__(256) residual_rms_norm_kernel(ResNormArgs a) {
   const int lane = threadIdx.x & 63;
-  const int m = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (m >= a.M) return;
-  // the low-rank term's inputs of this row as packed 16-bit pairs (v_dot2 operands)
-  uint32_t mu2[MU > 0 ? MU / 2 : 1];
-  if constexpr (MU > 0) {
-    const uint32_t* mx = (const uint32_t*)((const T*)a.mu_x + (int64_t)m * a.ldmu);
-#pragma unroll
-    for (int i = 0; i < MU / 2; ++i) mu2[i] = mx[i];
-  }
-  float s[P][8];
+  const int m0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+  if (m0 >= a.M) return;
   u32x4 wv[P];
-  float sq = 0.f;
+  u32x4 mwv[P][MU > 0 ? MU : 1];
 #pragma unroll
   for (int p = 0; p < P; ++p) {
     const int c = (p * 64 + lane) * 8;
-    const bool in = c < a.D;
-    const int cc = in ? c : 0;  // lanes past the row read column 0 and drop it
+    const int cc = c < a.D ? c : 0;  // lanes past the row read column 0 and drop it
     wv[p] = *(const u32x4*)((const T*)a.w + cc);
-    u32x4 rv = {0u, 0u, 0u, 0u};
-    if (a.res) rv = *(const u32x4*)((const T*)a.res + (int64_t)m * a.ldr + cc);
-    float br[8];
-    // the branch: a 16-bit tensor or the fp32 partial sums, plus the biases and the
-    // low-rank term (fp32), rounded once whenever anything was added in fp32
-    u32x4 yv = {0u, 0u, 0u, 0u};
-    if (a.y) yv = *(const u32x4*)((const T*)a.y + (int64_t)m * a.ldy + cc);
-    f32x4 pv[kResMaxParts][2];
-#pragma unroll
-    for (int q = 0; q < kResMaxParts; ++q)
-      if (q < a.n_parts) {
-        const float* pp = a.parts + ((int64_t)q * a.M + m) * a.D + cc;
-        pv[q][0] = ld4(pp);
-        pv[q][1] = ld4(pp + 4);
-      }
-    u32x4 bv[kResMaxBias];
-#pragma unroll
-    for (int b = 0; b < kResMaxBias; ++b)
-      if (b < a.n_bias) bv[b] = *(const u32x4*)((const T*)a.bias[b] + cc);
-    u32x4 mwv[MU > 0 ? MU : 1];
     if constexpr (MU > 0) {
       // rows cc .. cc + 7 of mu_w (D, MU): 8 MU contiguous values, MU 16-byte vectors
 #pragma unroll
-      for (int i = 0; i < MU; ++i) mwv[i] = *(const u32x4*)((const T*)a.mu_w + (int64_t)cc * MU + 8 * i);
+      for (int i = 0; i < MU; ++i) mwv[p][i] = *(const u32x4*)((const T*)a.mu_w + (int64_t)cc * MU + 8 * i);
     }
-    if (a.y) {
-      unpack8<T>(yv, br);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) br[e] = pv[0][e >> 2][e & 3];
-#pragma unroll
-      for (int q = 1; q < kResMaxParts; ++q)
-        if (q < a.n_parts) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) br[e] += pv[q][e >> 2][e & 3];
-        }
-    }
-#pragma unroll
-    for (int b = 0; b < kResMaxBias; ++b)
-      if (b < a.n_bias) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) br[e] += elem16<T>(bv[b], e);
-      }
-    if constexpr (MU > 0) {
-      // element e's MU weights are words e MU / 2 .. e MU / 2 + MU / 2 - 1 of the block
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float acc = 0.f;
-#pragma unroll
-        for (int i = 0; i < MU / 2; ++i) {
-          const int wd = e * (MU / 2) + i;
-          acc = dot2<T>(mwv[wd >> 2][wd & 3], mu2[i], acc);
-        }
-        br[e] += acc;
-      }
-    }
-    if (!a.y || a.n_bias > 0 || MU > 0) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) br[e] = rnd<T>(br[e]);
-    }
-    if (a.res) {
-      float x[8];
-      unpack8<T>(rv, x);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s[p][e] = rnd<T>(x[e] + br[e]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s[p][e] = br[e];
-    }
-    if (!in) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s[p][e] = 0.f;
-    } else if (a.res_out) {
-      store8((T*)a.res_out + (int64_t)m * a.ldro + c, s[p]);
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) sq += s[p][e] * s[p][e];
   }
-  const float rstd = rsqrtf(wave_sum(sq) / (float)a.D + a.eps);
+  for (int k = 0; k < RPW; ++k) {
+    const int m = m0 + k;
+    if (m >= a.M) break;
+    // the low-rank term's inputs of this row as packed 16-bit pairs (v_dot2 operands)
+    uint32_t mu2[MU > 0 ? MU / 2 : 1];
+    if constexpr (MU > 0) {
+      const uint32_t* mx = (const uint32_t*)((const T*)a.mu_x + (int64_t)m * a.ldmu);
 #pragma unroll
-  for (int p = 0; p < P; ++p) {
-    const int c = (p * 64 + lane) * 8;
-    if (c >= a.D) continue;
-    float w8[8], o[8];
-    unpack8<T>(wv[p], w8);
+      for (int i = 0; i < MU / 2; ++i) mu2[i] = mx[i];
+    }
+    float s[P][8];
+    float sq = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = (s[p][e] * rstd) * w8[e];
-    store8((T*)a.out + (int64_t)m * a.ldo + c, o);
+    for (int p = 0; p < P; ++p) {
+      const int c = (p * 64 + lane) * 8;
+      const bool in = c < a.D;
+      const int cc = in ? c : 0;  // lanes past the row read column 0 and drop it
+      u32x4 rv = {0u, 0u, 0u, 0u};
+      if (a.res) rv = *(const u32x4*)((const T*)a.res + (int64_t)m * a.ldr + cc);
+      float br[8];
+      // the branch: a 16-bit tensor or the fp32 partial sums, plus the biases and the
+      // low-rank term (fp32), rounded once whenever anything was added in fp32
+      // (PARTS: the branch is the partial sums; a template, so that the 16-bit form holds no
+      // registers for them)
+      u32x4 yv = {0u, 0u, 0u, 0u};
+      if constexpr (!PARTS) yv = *(const u32x4*)((const T*)a.y + (int64_t)m * a.ldy + cc);
+      f32x4 pv[PARTS ? kResMaxParts : 1][2];
+      if constexpr (PARTS) {
+#pragma unroll
+        for (int q = 0; q < kResMaxParts; ++q)
+          if (q < a.n_parts) {
+            const float* pp = a.parts + ((int64_t)q * a.M + m) * a.D + cc;
+            pv[q][0] = ld4(pp);
+            pv[q][1] = ld4(pp + 4);
+          }
+      }
+      u32x4 bv[kResMaxBias];
+#pragma unroll
+      for (int b = 0; b < kResMaxBias; ++b)
+        if (b < a.n_bias) bv[b] = *(const u32x4*)((const T*)a.bias[b] + cc);
+      if constexpr (!PARTS) {
+        unpack8<T>(yv, br);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) br[e] = pv[0][e >> 2][e & 3];
+#pragma unroll
+        for (int q = 1; q < kResMaxParts; ++q)
+          if (q < a.n_parts) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) br[e] += pv[q][e >> 2][e & 3];
+          }
+      }
+#pragma unroll
+      for (int b = 0; b < kResMaxBias; ++b)
+        if (b < a.n_bias) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) br[e] += elem16<T>(bv[b], e);
+        }
+      if constexpr (MU > 0) {
+        // element e's MU weights are words e MU / 2 .. e MU / 2 + MU / 2 - 1 of the block
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < MU / 2; ++i) {
+            const int wd = e * (MU / 2) + i;
+            acc = dot2<T>(mwv[p][wd >> 2][wd & 3], mu2[i], acc);
+          }
+          br[e] += acc;
+        }
+      }
+      if (PARTS || a.n_bias > 0 || MU > 0) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) br[e] = rnd<T>(br[e]);
+      }
+      if (a.res) {
+        float x[8];
+        unpack8<T>(rv, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s[p][e] = rnd<T>(x[e] + br[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s[p][e] = br[e];
+      }
+      if (!in) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s[p][e] = 0.f;
+      } else if (a.res_out) {
+        store8((T*)a.res_out + (int64_t)m * a.ldro + c, s[p]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sq += s[p][e] * s[p][e];
+    }
+    const float rstd = rsqrtf(wave_sum(sq) / (float)a.D + a.eps);
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int c = (p * 64 + lane) * 8;
+      if (c >= a.D) continue;
+      float w8[8], o[8];
+      unpack8<T>(wv[p], w8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (s[p][e] * rstd) * w8[e];
+      store8((T*)a.out + (int64_t)m * a.ldo + c, o);
+    }
   }
 }
 
+template <typename T, int MU, int RPW, bool PARTS>
+static void launch_res_norm_form(const ResNormArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)((a.M + 4 * RPW - 1) / (4 * RPW))), block(256);
+  if (a.D <= 512) residual_rms_norm_kernel<T, 1, MU, RPW, PARTS><<<grid, block, 0, s>>>(a);
+  else if (a.D <= 1024) residual_rms_norm_kernel<T, 2, MU, RPW, PARTS><<<grid, block, 0, s>>>(a);
+  else if (a.D <= 2048) residual_rms_norm_kernel<T, 4, MU, RPW, PARTS><<<grid, block, 0, s>>>(a);
+  else residual_rms_norm_kernel<T, 8, MU, RPW, PARTS><<<grid, block, 0, s>>>(a);
+}
+
+template <typename T, int MU, int RPW>
+static void launch_res_norm_rows(const ResNormArgs& a, hipStream_t s) {
+  if (a.y) launch_res_norm_form<T, MU, RPW, false>(a, s);
+  else launch_res_norm_form<T, MU, RPW, true>(a, s);
+}
+
+// the low-rank form over many rows shares its weights across 8 rows per wave; few rows (the
+// decode step) keep one row per wave, so no wave walks rows in sequence
+constexpr int kResShareRows = 8192;
+
 template <typename T, int MU>
 static void launch_res_norm_mu(const ResNormArgs& a, hipStream_t s) {
-  const dim3 grid((unsigned)((a.M + 3) / 4)), block(256);
-  if (a.D <= 512) residual_rms_norm_kernel<T, 1, MU><<<grid, block, 0, s>>>(a);
-  else if (a.D <= 1024) residual_rms_norm_kernel<T, 2, MU><<<grid, block, 0, s>>>(a);
-  else if (a.D <= 2048) residual_rms_norm_kernel<T, 4, MU><<<grid, block, 0, s>>>(a);
-  else residual_rms_norm_kernel<T, 8, MU><<<grid, block, 0, s>>>(a);
+  if constexpr (MU > 0) {
+    if (a.M >= kResShareRows) return launch_res_norm_rows<T, MU, 8>(a, s);
+  }
+  launch_res_norm_rows<T, MU, 1>(a, s);
 }
 
 template <typename T>
